@@ -1,0 +1,292 @@
+"""gpeed_amd - MI355X (gfx950) IQ3_XXS dequantize-and-multiply path.
+
+Python host layer over the C ABI in include/gpeed_iq3.h (libgpeed_iq3.so,
+built in-tree by ``gpeed_amd.build``). Device memory and streams come from
+PyTorch; every computation runs in the HIP library. There is no CPU fallback:
+if the library is missing or no GPU is visible, the calls raise.
+
+The WeightStore class mirrors the reference's WeightStore::matvec_quant /
+matmul_quant contract (cpp/core/include/glm5/weights.h:41-48): same argument
+meaning (tensor name, first row, in_dim, out_dim), same errors (missing
+tensor, row not block aligned) raised as RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgpeed_iq3.so")
+
+GPEED_OK = 0
+ERRORS = {
+    -1: "invalid argument",
+    -2: "element count not a multiple of block size",
+    -3: "row not block aligned",
+    -4: "dtype not implemented on the GPU path",
+    -5: "HIP error",
+    -6: "T16 operand off a 16-row tile boundary",
+    -7: "workspace missing or too small",
+    -8: "no HIP device",
+}
+DTYPE_IQ3_XXS = 18
+QK = 256
+BLOCK_BYTES = 98
+
+_lib = None
+
+
+class GpeedError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{msg} (status {code}: {ERRORS.get(code, 'unknown')})")
+        self.code = code
+
+
+def lib():
+    """The loaded libgpeed_iq3.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run gpeed_amd.build.build() first")
+        L = C.CDLL(LIB_PATH)
+        vp, u64, i64, i32, sz = C.c_void_p, C.c_uint64, C.c_int64, C.c_int, C.c_size_t
+        sig = {
+            "gpeed_device_count": ([], i32),
+            "gpeed_device_name": ([i32, C.c_char_p, sz], i32),
+            "gpeed_add_f32": ([vp, vp, vp, i32], i32),
+            "gpeed_init": ([], i32),
+            "gpeed_last_error": ([], C.c_char_p),
+            "gpeed_iq3xxs_row_bytes": ([i64], sz),
+            "gpeed_iq3xxs_t16_bytes": ([u64, i64], sz),
+            "gpeed_dequantize": ([i32, vp, vp, u64, vp], i32),
+            "gpeed_t16_sign_table": ([vp, sz], i32),
+            "gpeed_t16_aux_word": ([C.c_uint32], C.c_uint32),
+            "gpeed_iq3xxs_tile": ([vp, u64, i64, vp, vp], i32),
+            "gpeed_iq3xxs_untile": ([vp, u64, i64, vp, vp], i32),
+            "gpeed_iq3xxs_matvec_ws_bytes": ([i64], sz),
+            "gpeed_iq3xxs_matvec": ([vp, u64, u64, i32, i32, vp, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_matvec_raw": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
+            "gpeed_iq3xxs_act_bytes": ([i64], sz),
+            "gpeed_iq3xxs_prep_act": ([vp, i64, vp, sz, vp], i32),
+            "gpeed_iq3xxs_prep_swiglu": ([vp, vp, i64, C.c_float, vp, sz, vp], i32),
+            "gpeed_iq3xxs_matvec_act": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
+        }
+        for name, (args, res) in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def _check(rc: int, what: str):
+    if rc != GPEED_OK:
+        msg = lib().gpeed_last_error().decode(errors="replace")
+        raise GpeedError(rc, f"{what}: {msg}")
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _stream(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _ptr(t) -> C.c_void_p:
+    return C.c_void_p(t.data_ptr())
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("gpeed_amd operates on device tensors (tensor.is_cuda is False)")
+        if not t.is_contiguous():
+            raise ValueError("gpeed_amd expects contiguous tensors")
+
+
+def init():
+    _check(lib().gpeed_init(), "gpeed_init")
+
+
+def device_count() -> int:
+    return lib().gpeed_device_count()
+
+
+def device_name(index: int = 0) -> str:
+    buf = C.create_string_buffer(256)
+    _check(lib().gpeed_device_name(index, buf, 256), "gpeed_device_name")
+    return buf.value.decode()
+
+
+def add_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Host-array a + b through the device (the reference's cuda_add smoke test)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty_like(a)
+    _check(lib().gpeed_add_f32(a.ctypes.data, b.ctypes.data, out.ctypes.data, a.size), "gpeed_add_f32")
+    return out
+
+
+def row_bytes(in_dim: int) -> int:
+    return lib().gpeed_iq3xxs_row_bytes(in_dim)
+
+
+def t16_bytes(n_rows: int, in_dim: int) -> int:
+    return lib().gpeed_iq3xxs_t16_bytes(n_rows, in_dim)
+
+
+def dequantize(raw, n: int, out=None, dtype: int = DTYPE_IQ3_XXS, stream=None):
+    """fp32 [n] from GGUF bytes on the device (bit-exact with quant.cpp:186-210)."""
+    torch = _torch()
+    _require_cuda(raw)
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=raw.device)
+    _check(lib().gpeed_dequantize(dtype, _ptr(raw), _ptr(out), n, _stream(stream)), "dequantize")
+    return out
+
+
+def tile(raw, n_rows: int, in_dim: int, out=None, stream=None):
+    """T16 copy of [n_rows, in_dim] GGUF rows held on the device."""
+    torch = _torch()
+    _require_cuda(raw)
+    if out is None:
+        out = torch.empty(t16_bytes(n_rows, in_dim), dtype=torch.uint8, device=raw.device)
+    _check(lib().gpeed_iq3xxs_tile(_ptr(raw), n_rows, in_dim, _ptr(out), _stream(stream)), "tile")
+    return out
+
+
+def untile(t16, n_rows: int, in_dim: int, out=None, stream=None):
+    torch = _torch()
+    _require_cuda(t16)
+    if out is None:
+        out = torch.empty(n_rows * row_bytes(in_dim), dtype=torch.uint8, device=t16.device)
+    _check(lib().gpeed_iq3xxs_untile(_ptr(t16), n_rows, in_dim, _ptr(out), _stream(stream)), "untile")
+    return out
+
+
+def matvec_workspace(in_dim: int, device="cuda"):
+    torch = _torch()
+    return torch.empty(lib().gpeed_iq3xxs_matvec_ws_bytes(in_dim), dtype=torch.uint8, device=device)
+
+
+def matvec(w_t16, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None, ws=None, stream=None):
+    """dst = W[row0:row0+out_dim] @ x from a T16 tensor (batch 1, fp32)."""
+    torch = _torch()
+    _require_cuda(w_t16, x)
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = matvec_workspace(in_dim, x.device)
+    _check(lib().gpeed_iq3xxs_matvec(_ptr(w_t16), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out),
+                                     _ptr(ws), ws.numel(), _stream(stream)), "matvec")
+    return out
+
+
+def act_buffer(in_dim: int, device="cuda"):
+    """Device buffer for one prepared activation (fp16 hi/lo operand + scale)."""
+    torch = _torch()
+    return torch.empty(lib().gpeed_iq3xxs_act_bytes(in_dim), dtype=torch.uint8, device=device)
+
+
+def prep_act(x, act, stream=None):
+    _require_cuda(x, act)
+    _check(lib().gpeed_iq3xxs_prep_act(_ptr(x), x.numel(), _ptr(act), act.numel(), _stream(stream)), "prep_act")
+    return act
+
+
+def prep_swiglu(g, u, act, limit: float = 10.0, stream=None):
+    _require_cuda(g, u, act)
+    _check(lib().gpeed_iq3xxs_prep_swiglu(_ptr(g), _ptr(u), g.numel(), limit, _ptr(act), act.numel(),
+                                          _stream(stream)), "prep_swiglu")
+    return act
+
+
+def matvec_act(w_t16, n_rows: int, row0: int, in_dim: int, out_dim: int, act, out=None, stream=None):
+    torch = _torch()
+    _require_cuda(w_t16, act)
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.float32, device=act.device)
+    _check(lib().gpeed_iq3xxs_matvec_act(_ptr(w_t16), n_rows, row0, in_dim, out_dim, _ptr(act), _ptr(out),
+                                         _stream(stream)), "matvec_act")
+    return out
+
+
+def matvec_raw(w, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None, stream=None):
+    """dst = W[row0:row0+out_dim] @ x straight from GGUF rows on the device."""
+    torch = _torch()
+    _require_cuda(w, x)
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    _check(lib().gpeed_iq3xxs_matvec_raw(_ptr(w), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out),
+                                         _stream(stream)), "matvec_raw")
+    return out
+
+
+class WeightStore:
+    """Device-resident IQ3_XXS tensors behind the reference's matvec_quant contract.
+
+    ``add(name, payload, in_dim, n_rows)`` uploads GGUF rows once and keeps
+    their T16 copy in HBM (the role of pin_nonexpert, weights.cpp:70-84).
+    ``matvec_quant`` follows weights.cpp:167-203: ``dst[j] = sum_i
+    W[row0+j][i] * x[i]`` for ``j < out_dim``; host numpy arrays in, host
+    numpy out (synchronous, like the reference), or device tensors in and out.
+    """
+
+    def __init__(self, device="cuda"):
+        self.device = device
+        self.tensors = {}
+        self._ws = {}
+
+    def add(self, name: str, payload, in_dim: int, n_rows: int):
+        torch = _torch()
+        if in_dim % QK:
+            raise RuntimeError(f"weights: row not block aligned for {name}")
+        if isinstance(payload, np.ndarray):
+            raw = torch.from_numpy(np.ascontiguousarray(payload).reshape(-1).view(np.uint8)).to(self.device)
+        else:
+            raw = payload.reshape(-1)
+        t16 = tile(raw, n_rows, in_dim)
+        self.tensors[name] = (t16, in_dim, n_rows)
+        return t16
+
+    def has(self, name: str) -> bool:
+        return name in self.tensors
+
+    def _get(self, name: str, in_dim: int):
+        if name not in self.tensors:
+            raise RuntimeError(f"weights: missing tensor {name}")
+        if in_dim % QK:
+            raise RuntimeError(f"weights: row not block aligned for {name}")
+        return self.tensors[name]
+
+    def _workspace(self, in_dim: int):
+        ws = self._ws.get(in_dim)
+        if ws is None:
+            ws = self._ws[in_dim] = matvec_workspace(in_dim, self.device)
+        return ws
+
+    def matvec_quant(self, name: str, row0: int, in_dim: int, out_dim: int, x, dst=None):
+        torch = _torch()
+        t16, _, n_rows = self._get(name, in_dim)
+        host = isinstance(x, np.ndarray)
+        if out_dim <= 0:
+            return dst
+        xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(self.device) if host else x
+        yd = matvec(t16, n_rows, row0, in_dim, out_dim, xd, ws=self._workspace(in_dim))
+        if host:
+            y = yd.cpu().numpy()
+            if dst is not None:
+                dst[:out_dim] = y
+                return dst
+            return y
+        if dst is not None:
+            dst.copy_(yd)
+            return dst
+        return yd

@@ -1,0 +1,263 @@
+// C ABI (include/gpeed_iq3.h) over the gfx950 kernels.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/gpeed_iq3.h"
+#include "iq3_common.h"
+#include "iq3_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(GPEED_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_init_mu;
+void* g_sign_table[kMaxDevices] = {};
+
+// Per-device 64 KiB signed lookup table (uploaded once, kept until exit).
+int device_tables(const void** sign_table) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(GPEED_ERR_INVALID, "device index out of range");
+    if (!g_sign_table[dev]) {
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        if (!g_sign_table[dev]) {
+            std::vector<uint16_t> host(gpeed::kSignTableBytes / 2);
+            gpeed::build_sign_table(host.data());
+            void* p = nullptr;
+            e = hipMalloc(&p, gpeed::kSignTableBytes);
+            if (e != hipSuccess) return hip_fail(e, "hipMalloc(sign table)");
+            e = hipMemcpy(p, host.data(), gpeed::kSignTableBytes, hipMemcpyHostToDevice);
+            if (e != hipSuccess) {
+                (void)hipFree(p);
+                return hip_fail(e, "hipMemcpy(sign table)");
+            }
+            g_sign_table[dev] = p;
+        }
+    }
+    *sign_table = g_sign_table[dev];
+    return GPEED_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* gpeed_last_error(void) { return g_err.c_str(); }
+
+int gpeed_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int gpeed_device_name(int index, char* buf, size_t len) {
+    if (!buf || len == 0) return fail(GPEED_ERR_INVALID, "gpeed_device_name: empty buffer");
+    hipDeviceProp_t prop;
+    const char* name = "<none>";
+    if (hipGetDeviceProperties(&prop, index) == hipSuccess) name = prop.name;
+    std::snprintf(buf, len, "%s", name);
+    return GPEED_OK;
+}
+
+int gpeed_add_f32(const float* a, const float* b, float* dst, int n) {
+    if (n <= 0) return GPEED_OK;
+    if (!a || !b || !dst) return fail(GPEED_ERR_INVALID, "gpeed_add_f32: null pointer");
+    float *da = nullptr, *db = nullptr, *dd = nullptr;
+    const size_t bytes = (size_t)n * sizeof(float);
+    hipError_t e = hipMalloc(&da, bytes);
+    if (e == hipSuccess) e = hipMalloc(&db, bytes);
+    if (e == hipSuccess) e = hipMalloc(&dd, bytes);
+    if (e == hipSuccess) e = hipMemcpy(da, a, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(db, b, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = gpeed::launch_add(da, db, dd, n, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(dst, dd, bytes, hipMemcpyDeviceToHost);
+    (void)hipFree(da);
+    (void)hipFree(db);
+    (void)hipFree(dd);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "gpeed_add_f32");
+}
+
+int gpeed_init(void) {
+    if (gpeed_device_count() <= 0) return fail(GPEED_ERR_NO_DEVICE, "no HIP device");
+    const void* t = nullptr;
+    return device_tables(&t);
+}
+
+size_t gpeed_iq3xxs_row_bytes(int64_t in_dim) {
+    if (in_dim <= 0 || in_dim % gpeed::kQK) return 0;
+    return gpeed::iq3_row_bytes(in_dim);
+}
+
+size_t gpeed_iq3xxs_t16_bytes(uint64_t n_rows, int64_t in_dim) {
+    if (in_dim <= 0 || in_dim % gpeed::kQK) return 0;
+    return gpeed::t16_bytes(n_rows, in_dim);
+}
+
+int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_stream_t stream) {
+    if (dtype != GPEED_DTYPE_IQ3_XXS)
+        return fail(GPEED_ERR_UNIMPLEMENTED, "dequantize: dtype not handled on the GPU path");
+    if (n % gpeed::kQK)
+        return fail(GPEED_ERR_NOT_MULTIPLE, "dequantize: element count not a multiple of block size");
+    if (n == 0) return GPEED_OK;
+    if (!src || !dst) return fail(GPEED_ERR_INVALID, "dequantize: null pointer");
+    if (!aligned(src, 2) || !aligned(dst, 16))
+        return fail(GPEED_ERR_INVALID, "dequantize: src must be 2-byte and dst 16-byte aligned");
+    hipError_t e = gpeed::launch_dequant_raw(static_cast<const uint8_t*>(src), dst, n,
+                                             static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "dequantize launch");
+}
+
+int gpeed_t16_sign_table(uint16_t* out, size_t n) {
+    if (!out || n < (size_t)gpeed::kSignTableBytes / 2)
+        return fail(GPEED_ERR_INVALID, "t16_sign_table: buffer smaller than 32768 entries");
+    gpeed::build_sign_table(out);
+    return GPEED_OK;
+}
+
+uint32_t gpeed_t16_aux_word(uint32_t gguf_aux) { return gpeed::aux_to_t16(gguf_aux); }
+
+static int check_tile_args(const void* a, const void* b, int64_t in_dim, const char* who) {
+    if (in_dim <= 0 || in_dim % gpeed::kQK)
+        return fail(GPEED_ERR_UNALIGNED_ROW, std::string(who) + ": row not block aligned");
+    if (in_dim / gpeed::kQK > (1 << 24)) return fail(GPEED_ERR_INVALID, std::string(who) + ": in_dim too large");
+    if (!a || !b) return fail(GPEED_ERR_INVALID, std::string(who) + ": null pointer");
+    return GPEED_OK;
+}
+
+int gpeed_iq3xxs_tile(const void* raw, uint64_t n_rows, int64_t in_dim, void* t16,
+                      gpeed_stream_t stream) {
+    if (n_rows == 0) return GPEED_OK;
+    int rc = check_tile_args(raw, t16, in_dim, "tile");
+    if (rc) return rc;
+    if (!aligned(raw, 2) || !aligned(t16, 16))
+        return fail(GPEED_ERR_INVALID, "tile: raw must be 2-byte and t16 16-byte aligned");
+    hipError_t e = gpeed::launch_tile(static_cast<const uint8_t*>(raw), n_rows, (int)in_dim,
+                                      static_cast<uint8_t*>(t16), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "tile launch");
+}
+
+int gpeed_iq3xxs_untile(const void* t16, uint64_t n_rows, int64_t in_dim, void* raw,
+                        gpeed_stream_t stream) {
+    if (n_rows == 0) return GPEED_OK;
+    int rc = check_tile_args(t16, raw, in_dim, "untile");
+    if (rc) return rc;
+    if (!aligned(raw, 2) || !aligned(t16, 16))
+        return fail(GPEED_ERR_INVALID, "untile: raw must be 2-byte and t16 16-byte aligned");
+    hipError_t e = gpeed::launch_untile(static_cast<const uint8_t*>(t16), n_rows, (int)in_dim,
+                                        static_cast<uint8_t*>(raw), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "untile launch");
+}
+
+size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim) {
+    if (in_dim <= 0 || in_dim % gpeed::kQK) return 0;
+    return gpeed::prep_x_bytes(1, (int)in_dim);
+}
+
+static int check_mv_args(const void* w, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                         const float* x, float* dst, const char* who) {
+    if (in_dim <= 0 || in_dim % gpeed::kQK)
+        return fail(GPEED_ERR_UNALIGNED_ROW, std::string(who) + ": row not block aligned");
+    if (!w || !x || !dst) return fail(GPEED_ERR_INVALID, std::string(who) + ": null pointer");
+    if (row0 > n_rows || (uint64_t)out_dim > n_rows - row0)
+        return fail(GPEED_ERR_INVALID, std::string(who) + ": rows out of range");
+    return GPEED_OK;
+}
+
+size_t gpeed_iq3xxs_act_bytes(int64_t in_dim) { return gpeed_iq3xxs_matvec_ws_bytes(in_dim); }
+
+static int check_act(const void* act, size_t act_bytes, int64_t in_dim, const char* who) {
+    if (in_dim <= 0 || in_dim % gpeed::kQK)
+        return fail(GPEED_ERR_UNALIGNED_ROW, std::string(who) + ": row not block aligned");
+    if (in_dim > (1 << 30)) return fail(GPEED_ERR_INVALID, std::string(who) + ": in_dim too large");
+    if (!act || act_bytes < gpeed::prep_x_bytes(1, (int)in_dim) || !aligned(act, 16))
+        return fail(GPEED_ERR_WORKSPACE,
+                    std::string(who) + ": activation buffer missing, misaligned or too small");
+    return GPEED_OK;
+}
+
+static float* act_scale(void* act, int64_t in_dim) {
+    return reinterpret_cast<float*>(static_cast<uint8_t*>(act) + (size_t)in_dim * 4);
+}
+
+int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, void* act, size_t act_bytes,
+                          gpeed_stream_t stream) {
+    int rc = check_act(act, act_bytes, in_dim, "prep_act");
+    if (rc) return rc;
+    if (!x) return fail(GPEED_ERR_INVALID, "prep_act: null pointer");
+    hipError_t e = gpeed::launch_prep_x(x, 1, (int)in_dim, static_cast<uint32_t*>(act),
+                                        act_scale(act, in_dim), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "prep_act launch");
+}
+
+int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, float limit, void* act,
+                             size_t act_bytes, gpeed_stream_t stream) {
+    int rc = check_act(act, act_bytes, n, "prep_swiglu");
+    if (rc) return rc;
+    if (!g || !u) return fail(GPEED_ERR_INVALID, "prep_swiglu: null pointer");
+    hipError_t e = gpeed::launch_prep_swiglu(g, u, limit, 1, (int)n, static_cast<uint32_t*>(act),
+                                             act_scale(act, n), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "prep_swiglu launch");
+}
+
+int gpeed_iq3xxs_matvec_act(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim,
+                            int out_dim, const void* act, float* dst, gpeed_stream_t stream) {
+    if (out_dim <= 0) return GPEED_OK;
+    const float dummy = 0.0f;
+    int rc = check_mv_args(w_t16, n_rows, row0, in_dim, out_dim, &dummy, dst, "matvec");
+    if (rc) return rc;
+    if (!act || !aligned(act, 16)) return fail(GPEED_ERR_WORKSPACE, "matvec: activation missing or misaligned");
+    if (row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "matvec: row0 must be a multiple of 16 on the T16 layout");
+    if (!aligned(w_t16, 16)) return fail(GPEED_ERR_INVALID, "matvec: T16 weights must be 16-byte aligned");
+    const void* tbl = nullptr;
+    rc = device_tables(&tbl);
+    if (rc) return rc;
+    hipError_t e = gpeed::launch_matvec_t16(static_cast<const uint8_t*>(w_t16), in_dim, row0, out_dim,
+                                            static_cast<const uint32_t*>(act),
+                                            act_scale(const_cast<void*>(act), in_dim), dst, tbl,
+                                            static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec launch");
+}
+
+int gpeed_iq3xxs_matvec(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                        const float* x, float* dst, void* ws, size_t ws_bytes,
+                        gpeed_stream_t stream) {
+    if (out_dim <= 0) return GPEED_OK;
+    int rc = check_mv_args(w_t16, n_rows, row0, in_dim, out_dim, x, dst, "matvec");
+    if (rc) return rc;
+    if (row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "matvec: row0 must be a multiple of 16 on the T16 layout");
+    rc = gpeed_iq3xxs_prep_act(x, in_dim, ws, ws_bytes, stream);
+    if (rc) return rc;
+    return gpeed_iq3xxs_matvec_act(w_t16, n_rows, row0, in_dim, out_dim, ws, dst, stream);
+}
+
+int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,
+                            int out_dim, const float* x, float* dst, gpeed_stream_t stream) {
+    if (out_dim <= 0) return GPEED_OK;
+    int rc = check_mv_args(w_gguf, n_rows, row0, in_dim, out_dim, x, dst, "matvec_raw");
+    if (rc) return rc;
+    if (!aligned(w_gguf, 2) || !aligned(x, 16))
+        return fail(GPEED_ERR_INVALID, "matvec_raw: w must be 2-byte and x 16-byte aligned");
+    hipError_t e = gpeed::launch_matvec_raw(static_cast<const uint8_t*>(w_gguf), in_dim, row0, out_dim,
+                                            x, dst, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec_raw launch");
+}
+
+}  // extern "C"

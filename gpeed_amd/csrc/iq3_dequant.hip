@@ -1,0 +1,157 @@
+// IQ3_XXS dequantization and layout conversion kernels (gfx950).
+#include "iq3_common.h"
+#include "iq3_kernels.h"
+
+namespace gpeed {
+
+namespace {
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+// 2-byte aligned little-endian u32 (GGUF blocks are 98 bytes, so the words
+// inside them are only 2-byte aligned).
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {
+    return ld_u16(p) | (ld_u16(p + 2) << 16);
+}
+
+// One thread per 8-weight group (2 grid indices, one sign index). Mirrors
+// blk_iq3_xxs (quant.cpp:186-210) operation for operation; every product is
+// exact in fp32, so the result is bit-identical to the CPU decode.
+__global__ __launch_bounds__(256) void k_dequant_raw(const uint8_t* __restrict__ src,
+                                                     float* __restrict__ dst,
+                                                     unsigned long long n_groups) {
+    __shared__ uint32_t grid[256];
+    grid[threadIdx.x] = kIq3xxsGrid[threadIdx.x];
+    __syncthreads();
+    const unsigned long long gi = (unsigned long long)blockIdx.x * 256 + threadIdx.x;
+    if (gi >= n_groups) return;
+    const unsigned long long b = gi >> 5;
+    const int ib = (int)(gi >> 2) & 7;
+    const int l = (int)gi & 3;
+    const uint8_t* blk = src + b * kBlockBytes;
+    const float d = f16_bits_to_f32(ld_u16(blk));
+    const uint32_t aux = ld_u32_a2(blk + 66 + 4 * ib);
+    const uint32_t qq = ld_u16(blk + 2 + 8 * ib + 2 * l);
+    const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+    const uint32_t s7 = (aux >> (7 * l)) & 127u;
+    const uint32_t sg = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+    const uint32_t g1 = grid[qq & 255u];
+    const uint32_t g2 = grid[qq >> 8];
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        y[j] = db * (float)((g1 >> (8 * j)) & 255u) * (((sg >> j) & 1u) ? -1.0f : 1.0f);
+        y[j + 4] = db * (float)((g2 >> (8 * j)) & 255u) * (((sg >> (j + 4)) & 1u) ? -1.0f : 1.0f);
+    }
+    float4* out = reinterpret_cast<float4*>(dst + gi * 8);
+    out[0] = make_float4(y[0], y[1], y[2], y[3]);
+    out[1] = make_float4(y[4], y[5], y[6], y[7]);
+}
+
+// One thread per 12-byte unit (tile, block, lane L, half j); threads with
+// L < 16 and j == 0 also move the row's fp16 d. Rows past n_rows (padding of
+// the last tile) are written as zeros.
+__global__ __launch_bounds__(256) void k_tile(const uint8_t* __restrict__ raw,
+                                              unsigned long long n_rows, int nb,
+                                              uint8_t* __restrict__ t16,
+                                              unsigned long long n_units) {
+    const unsigned long long u = (unsigned long long)blockIdx.x * 256 + threadIdx.x;
+    if (u >= n_units) return;
+    const int jl = (int)(u & 127);  // j*64 + L
+    const unsigned long long rec = u >> 7;
+    const int b = (int)(rec % (unsigned long long)nb);
+    const unsigned long long t = rec / (unsigned long long)nb;
+    const int j = jl >> 6, L = jl & 63, n = L & 15, g = L >> 4;
+    const int ib = 4 * j + g;
+    const unsigned long long row = t * kTileRows + n;
+    const size_t rb = (size_t)nb * kBlockBytes;
+    uint8_t* dst_rec = t16 + rec * kRecordBytes;
+    uint32_t* unit = reinterpret_cast<uint32_t*>(dst_rec + j * kUnitHalfBytes + L * 12);
+    if (row >= n_rows) {
+        unit[0] = 0; unit[1] = 0; unit[2] = 0;
+        if (j == 0 && g == 0) *reinterpret_cast<uint16_t*>(dst_rec + 2 * kUnitHalfBytes + 2 * n) = 0;
+        return;
+    }
+    const uint8_t* blk = raw + row * rb + (size_t)b * kBlockBytes;
+    unit[0] = ld_u32_a2(blk + 2 + 8 * ib);
+    unit[1] = ld_u32_a2(blk + 2 + 8 * ib + 4);
+    unit[2] = aux_to_t16_dev(ld_u32_a2(blk + 66 + 4 * ib));
+    if (j == 0 && g == 0)
+        *reinterpret_cast<uint16_t*>(dst_rec + 2 * kUnitHalfBytes + 2 * n) = (uint16_t)ld_u16(blk);
+}
+
+__global__ __launch_bounds__(256) void k_untile(const uint8_t* __restrict__ t16,
+                                                unsigned long long n_rows, int nb,
+                                                uint8_t* __restrict__ raw,
+                                                unsigned long long n_units) {
+    const unsigned long long u = (unsigned long long)blockIdx.x * 256 + threadIdx.x;
+    if (u >= n_units) return;
+    const int jl = (int)(u & 127);
+    const unsigned long long rec = u >> 7;
+    const int b = (int)(rec % (unsigned long long)nb);
+    const unsigned long long t = rec / (unsigned long long)nb;
+    const int j = jl >> 6, L = jl & 63, n = L & 15, g = L >> 4;
+    const int ib = 4 * j + g;
+    const unsigned long long row = t * kTileRows + n;
+    if (row >= n_rows) return;
+    const size_t rb = (size_t)nb * kBlockBytes;
+    const uint8_t* src_rec = t16 + rec * kRecordBytes;
+    const uint32_t* unit = reinterpret_cast<const uint32_t*>(src_rec + j * kUnitHalfBytes + L * 12);
+    uint16_t* blk = reinterpret_cast<uint16_t*>(raw + row * rb + (size_t)b * kBlockBytes);
+    const uint32_t q0 = unit[0], q1 = unit[1], a = t16_to_aux_dev(unit[2]);
+    // 16-bit stores: the fields are 2-byte aligned inside the 98-byte block
+    uint16_t* qs = blk + 1 + 4 * ib;
+    qs[0] = (uint16_t)q0; qs[1] = (uint16_t)(q0 >> 16);
+    qs[2] = (uint16_t)q1; qs[3] = (uint16_t)(q1 >> 16);
+    uint16_t* aw = blk + 33 + 2 * ib;
+    aw[0] = (uint16_t)a; aw[1] = (uint16_t)(a >> 16);
+    if (j == 0 && g == 0)
+        blk[0] = *reinterpret_cast<const uint16_t*>(src_rec + 2 * kUnitHalfBytes + 2 * n);
+}
+
+__global__ __launch_bounds__(256) void k_add(const float* __restrict__ a, const float* __restrict__ b,
+                                             float* __restrict__ d, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) d[i] = a[i] + b[i];
+}
+
+}  // namespace
+
+hipError_t launch_dequant_raw(const uint8_t* src, float* dst, unsigned long long n, hipStream_t s) {
+    const unsigned long long groups = n / 8;
+    if (groups == 0) return hipSuccess;
+    const unsigned long long grid = (groups + 255) / 256;
+    hipLaunchKernelGGL(k_dequant_raw, dim3((unsigned)grid), dim3(256), 0, s, src, dst, groups);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile(const uint8_t* raw, unsigned long long n_rows, int in_dim, uint8_t* t16,
+                       hipStream_t s) {
+    const int nb = in_dim / kQK;
+    const unsigned long long tiles = (n_rows + kTileRows - 1) / kTileRows;
+    const unsigned long long units = tiles * (unsigned long long)nb * 128ull;
+    if (units == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_tile, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, raw, n_rows, nb,
+                       t16, units);
+    return hipGetLastError();
+}
+
+hipError_t launch_untile(const uint8_t* t16, unsigned long long n_rows, int in_dim, uint8_t* raw,
+                         hipStream_t s) {
+    const int nb = in_dim / kQK;
+    const unsigned long long tiles = (n_rows + kTileRows - 1) / kTileRows;
+    const unsigned long long units = tiles * (unsigned long long)nb * 128ull;
+    if (units == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_untile, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, t16, n_rows,
+                       nb, raw, units);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const float* a, const float* b, float* dst, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add, dim3((n + 255) / 256), dim3(256), 0, s, a, b, dst, n);
+    return hipGetLastError();
+}
+
+}  // namespace gpeed

@@ -1,0 +1,118 @@
+/* gpeed_iq3.h - C ABI of the MI355X (gfx950) IQ3_XXS dequantize-and-multiply path.
+ *
+ * Plain C: device pointers, sizes and a stream handle (a hipStream_t passed
+ * as void*; NULL = the default stream). No entry point throws or allocates
+ * device memory on the compute path; each returns GPEED_OK or a negative
+ * status (the C++ host layer turns these back into the reference's
+ * std::runtime_error behaviour). Compute entry points are asynchronous on
+ * `stream` unless stated otherwise.
+ *
+ * Citations name the reference interface each entry point replaces, with
+ * paths relative to the reference repository root.
+ */
+#ifndef GPEED_IQ3_H
+#define GPEED_IQ3_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* gpeed_stream_t;
+
+#define GPEED_OK 0
+#define GPEED_ERR_INVALID (-1)        /* null pointer, negative size, bounds */
+#define GPEED_ERR_NOT_MULTIPLE (-2)   /* n % 256 != 0            (quant.cpp:523-524) */
+#define GPEED_ERR_UNALIGNED_ROW (-3)  /* in_dim % 256 != 0       (weights.cpp:93-94, 173-174) */
+#define GPEED_ERR_UNIMPLEMENTED (-4)  /* dtype not on this path  (quant.cpp:553-554); caller falls back */
+#define GPEED_ERR_HIP (-5)            /* a HIP runtime call failed (see gpeed_last_error) */
+#define GPEED_ERR_LAYOUT (-6)         /* T16 operand addressed off a 16-row tile boundary */
+#define GPEED_ERR_WORKSPACE (-7)      /* workspace missing or too small */
+#define GPEED_ERR_NO_DEVICE (-8)      /* no HIP device visible */
+
+#define GPEED_DTYPE_IQ3_XXS 18        /* common.h:27 */
+
+/* ---- device query / smoke (replaces kernels.h:7-11) --------------------- */
+
+/* cuda_device_count (kernels.h:7, device_info.cu:12-16): 0 when none. */
+int gpeed_device_count(void);
+/* cuda_device_name (kernels.h:8, device_info.cu:18-22): writes the device
+ * name (or "<none>") into buf, NUL-terminated. */
+int gpeed_device_name(int index, char* buf, size_t len);
+/* cuda_add (kernels.h:11, device_info.cu:24-38): dst = a + b for HOST
+ * arrays; synchronous, stages through device memory like the reference. */
+int gpeed_add_f32(const float* a, const float* b, float* dst, int n);
+
+/* Uploads the per-device lookup tables for the current device. Called
+ * implicitly by the compute entry points; call it once up front to keep the
+ * one-time allocation out of timed or captured regions. */
+int gpeed_init(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char* gpeed_last_error(void);
+
+/* ---- geometry (replaces quant.cpp:52-126 for IQ3_XXS) ------------------- */
+
+/* dtype_row_bytes(IQ3_XXS, in_dim) (quant.cpp:119-126): 0 if in_dim % 256. */
+size_t gpeed_iq3xxs_row_bytes(int64_t in_dim);
+/* Bytes of the T16 (tiled) copy of an [n_rows, in_dim] IQ3_XXS tensor: the
+ * GGUF size rounded up to whole 16-row tiles. */
+size_t gpeed_iq3xxs_t16_bytes(uint64_t n_rows, int64_t in_dim);
+
+/* ---- dequantize (replaces quant.h:18-22, quant.cpp:565-573) ------------- */
+
+/* dequantize(DType, src, dst, n) for dtype == IQ3_XXS: dst[0..n) fp32 from the
+ * GGUF bytes at src (device pointers; dst 16-byte aligned). Bit-exact with
+ * the reference. Other dtypes return GPEED_ERR_UNIMPLEMENTED. */
+int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_stream_t stream);
+
+/* ---- weight residency (replaces weights.cpp:62-84 pin_nonexpert/payload) */
+
+/* Host-only layout introspection (no device use; no reference counterpart):
+ * the 64 KiB signed lookup table the kernels keep in LDS (32768 fp16 bit
+ * patterns; returns GPEED_ERR_INVALID if n < 32768), and the T16 sign/scale
+ * word made from a GGUF aux word. Lets CPU tests model the GPU decode. */
+int gpeed_t16_sign_table(uint16_t* out, size_t n);
+uint32_t gpeed_t16_aux_word(uint32_t gguf_aux);
+
+/* GGUF rows -> T16 copy (same bytes per weight) / back. */
+int gpeed_iq3xxs_tile(const void* raw, uint64_t n_rows, int64_t in_dim, void* t16,
+                      gpeed_stream_t stream);
+int gpeed_iq3xxs_untile(const void* t16, uint64_t n_rows, int64_t in_dim, void* raw,
+                        gpeed_stream_t stream);
+
+/* ---- batch-1 matvec (replaces WeightStore::matvec_quant, weights.h:41-42,
+ *      weights.cpp:167-203) ---------------------------------------------- */
+
+/* Workspace bytes gpeed_iq3xxs_matvec needs for an in_dim activation. */
+size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim);
+/* dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim, from the T16 copy of a
+ * tensor with n_rows rows. row0 % 16 == 0. x, dst: fp32 device arrays. */
+int gpeed_iq3xxs_matvec(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                        const float* x, float* dst, void* ws, size_t ws_bytes,
+                        gpeed_stream_t stream);
+/* The two halves of gpeed_iq3xxs_matvec, for callers that reuse one
+ * activation across several tensors (gate and up of model.cpp:681-682) or
+ * fuse the SwiGLU epilogue into the next product's input
+ * (model.cpp:683-689): a "prepared activation" is the fp16 hi/lo MFMA
+ * operand of one fp32 vector plus its power-of-two scale, in a caller-owned
+ * device buffer of gpeed_iq3xxs_act_bytes(in_dim) bytes (16-byte aligned). */
+size_t gpeed_iq3xxs_act_bytes(int64_t in_dim);
+int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, void* act, size_t act_bytes,
+                          gpeed_stream_t stream);
+/* act <- silu(min(g,limit)) * clamp(u,-limit,limit) over n = in_dim elements
+ * (model.cpp:683-688 with swiglu_limit, model_config.h:70). */
+int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, float limit, void* act,
+                             size_t act_bytes, gpeed_stream_t stream);
+int gpeed_iq3xxs_matvec_act(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim,
+                            int out_dim, const void* act, float* dst, gpeed_stream_t stream);
+
+/* Same product straight from GGUF rows (no tiling; any row0). */
+int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,
+                            int out_dim, const float* x, float* dst, gpeed_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

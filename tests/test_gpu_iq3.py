@@ -1,0 +1,234 @@
+"""GPU parity tests for the IQ3_XXS path, through the C ABI (gpeed_amd -> libgpeed_iq3.so).
+
+Bars: dequantized weights and layout conversions bit-exact; products within
+1e-3 of the oracle under rel_err (conftest.rel_err, the north-star gate) and,
+as a tighter design check, within 2e-5 -- the MFMA path multiplies exactly
+(fp16 q*(2s+1) times fp16 hi/lo activation halves), so only fp32
+accumulation order separates it from the CPU. Dropping the low activation
+half would still pass 1e-3 (it costs ~3e-4), so the tight bound is what
+catches it.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import gpeed_amd as G
+import oracle
+from gpeed_amd import synth
+from conftest import ROOT, rel_err
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(ROOT, "tests", "golden")
+TOL = 1e-3
+TIGHT = 2e-5
+
+
+def dev(a, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def same_bits_or_nan(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    nan = np.isnan(a) | np.isnan(b)
+    return bool(np.array_equal(np.isnan(a), np.isnan(b))
+                and np.array_equal(a[~nan].view(np.uint32), b[~nan].view(np.uint32)))
+
+
+# ------------------------------------------------------------------ dequant / layout
+
+@pytest.mark.parametrize("name", ["selftest_block", "edge_blocks"])
+def test_dequant_golden(gpu, name):
+    z = np.load(os.path.join(GOLD, name + ".npz"))
+    n = z["raw"].size // 98 * 256
+    out = G.dequantize(dev(z["raw"].reshape(-1), gpu), n)
+    assert same_bits_or_nan(host(out), z["deq"])
+
+
+def test_dequant_random_vs_oracle(gpu):
+    raw = synth.iq3xxs_blocks(41, 0, 3000)
+    out = G.dequantize(dev(raw.reshape(-1), gpu), 3000 * 256)
+    assert same_bits_or_nan(host(out), oracle.dequantize(raw, 3000 * 256))
+
+
+def test_dequant_errors(gpu):
+    import torch
+
+    raw = torch.zeros(98, dtype=torch.uint8, device=gpu)
+    with pytest.raises(G.GpeedError) as e:
+        G.dequantize(raw, 255)
+    assert e.value.code == -2
+    with pytest.raises(G.GpeedError) as e:
+        G.dequantize(raw, 256, dtype=12)
+    assert e.value.code == -4
+
+
+@pytest.mark.parametrize("n_rows,in_dim", [(16, 256), (17, 768), (64, 4096), (45, 2048)])
+def test_tile_roundtrip(gpu, n_rows, in_dim):
+    raw = synth.iq3xxs_matrix(42, n_rows, n_rows, in_dim)
+    t16 = G.tile(dev(raw.reshape(-1), gpu), n_rows, in_dim)
+    assert t16.numel() == ((n_rows + 15) // 16) * 16 * in_dim // 256 * 98
+    back = host(G.untile(t16, n_rows, in_dim))
+    assert np.array_equal(back, raw.reshape(-1))
+
+
+def test_tile_record_layout(gpu):
+    """One record checked field by field against the layout definition."""
+    n_rows, in_dim = 16, 512
+    raw = synth.iq3xxs_matrix(43, 0, n_rows, in_dim)
+    t16 = host(G.tile(dev(raw.reshape(-1), gpu), n_rows, in_dim))
+    L = G.lib()
+    rec = t16[1568:2 * 1568]  # tile 0, block 1
+    for j in range(2):
+        for lane in range(64):
+            n, g = lane % 16, lane // 16
+            ib = 4 * j + g
+            blk = raw[n, 98:196]
+            unit = rec[j * 768 + lane * 12: j * 768 + lane * 12 + 12]
+            assert np.array_equal(unit[:8], blk[2 + 8 * ib: 10 + 8 * ib])
+            aux = int(np.frombuffer(blk[66 + 4 * ib: 70 + 4 * ib].tobytes(), "<u4")[0])
+            assert int(np.frombuffer(unit[8:].tobytes(), "<u4")[0]) == L.gpeed_t16_aux_word(aux)
+    for n in range(16):
+        assert np.array_equal(rec[1536 + 2 * n: 1538 + 2 * n], raw[n, 98:100])
+
+
+# ------------------------------------------------------------------ matvec
+
+def run_matvec(gpu, w, n_rows, in_dim, row0, out_dim, x):
+    t16 = G.tile(dev(w.reshape(-1), gpu), n_rows, in_dim)
+    return host(G.matvec(t16, n_rows, row0, in_dim, out_dim, dev(x, gpu)))
+
+
+def test_matvec_golden(gpu):
+    z = np.load(os.path.join(GOLD, "matvec.npz"))
+    y = run_matvec(gpu, z["w"], 48, 1024, 16, 32, z["x"])
+    e = rel_err(y, z["y_row16"])
+    assert e < TIGHT, e
+
+
+@pytest.mark.parametrize("n_rows,in_dim,row0,out_dim", [
+    (4096, 4096, 0, 4096),    # single IQ3_XXS GEMV, 4096 x 4096
+    (64, 256, 16, 48),        # one block per row
+    (35, 768, 0, 35),         # 3 blocks per row, partial last tile
+    (80, 1280, 32, 40),       # 5 blocks, row0 inside the tensor, partial tile
+    (16, 2048, 0, 16),
+])
+def test_matvec_shapes(gpu, n_rows, in_dim, row0, out_dim):
+    w = synth.iq3xxs_matrix(50, n_rows, n_rows, in_dim)
+    x = synth.normal(50, 1000 + in_dim, in_dim)
+    y = run_matvec(gpu, w, n_rows, in_dim, row0, out_dim, x)
+    ref = oracle.matvec(w, row0, in_dim, out_dim, x)
+    e = rel_err(y, ref)
+    assert e < TIGHT, e
+
+
+@pytest.mark.parametrize("scale", [1e-6, 3e4, 1.0])
+def test_matvec_activation_range(gpu, scale):
+    n_rows, in_dim = 64, 2048
+    w = synth.iq3xxs_matrix(51, 0, n_rows, in_dim)
+    x = synth.normal(51, 1, in_dim) * np.float32(scale)
+    x[::97] *= np.float32(50.0)  # outliers
+    y = run_matvec(gpu, w, n_rows, in_dim, 0, n_rows, x)
+    e = rel_err(y, oracle.matvec(w, 0, in_dim, n_rows, x))
+    assert e < TIGHT, e
+
+
+def test_matvec_zero_activation(gpu):
+    w = synth.iq3xxs_matrix(52, 0, 32, 512)
+    y = run_matvec(gpu, w, 32, 512, 0, 32, np.zeros(512, np.float32))
+    assert np.all(y == 0)
+
+
+@pytest.mark.parametrize("n_rows,in_dim", [(12288, 6144), (6144, 12288)])
+def test_matvec_dense_mlp_shapes(gpu, n_rows, in_dim):
+    """Gate/up 12288 x 6144 and down 6144 x 12288 at full size."""
+    w = synth.iq3xxs_matrix(53, n_rows, n_rows, in_dim)
+    x = synth.normal(53, 7, in_dim)
+    y = run_matvec(gpu, w, n_rows, in_dim, 0, n_rows, x)
+    ref = oracle.matvec(w, 0, in_dim, n_rows, x)
+    e = rel_err(y, ref)
+    assert e < TOL and e < TIGHT, e
+
+
+def test_matvec_raw(gpu):
+    n_rows, in_dim = 70, 1536
+    w = synth.iq3xxs_matrix(54, 0, n_rows, in_dim)
+    x = synth.normal(54, 1, in_dim)
+    y = host(G.matvec_raw(dev(w.reshape(-1), gpu), n_rows, 3, in_dim, 60, dev(x, gpu)))
+    e = rel_err(y, oracle.matvec(w, 3, in_dim, 60, x))
+    assert e < TIGHT, e
+
+
+def test_matvec_errors(gpu):
+    import torch
+
+    w = synth.iq3xxs_matrix(55, 0, 32, 512)
+    t16 = G.tile(dev(w.reshape(-1), gpu), 32, 512)
+    x = torch.zeros(512, device=gpu)
+    with pytest.raises(G.GpeedError) as e:
+        G.matvec(t16, 32, 8, 512, 16, x)
+    assert e.value.code == -6
+    with pytest.raises(G.GpeedError) as e:
+        G.matvec(t16, 32, 16, 512, 32, x)
+    assert e.value.code == -1
+    with pytest.raises(G.GpeedError) as e:
+        G.matvec(t16, 32, 0, 500, 16, x)
+    assert e.value.code == -3
+    with pytest.raises(G.GpeedError) as e:
+        G.matvec(t16, 32, 0, 512, 16, x, ws=torch.empty(16, dtype=torch.uint8, device=gpu))
+    assert e.value.code == -7
+    # out_dim <= 0 returns without touching dst (weights.cpp:88 semantics)
+    G.matvec(t16, 32, 0, 512, 0, x, out=torch.empty(1, device=gpu))
+
+
+def test_dense_mlp_step(gpu):
+    """dense_mlp (model.cpp:677-690): gate/up share one prepared activation,
+    SwiGLU fused into the down projection's activation prep."""
+    import torch
+
+    H, I = 1024, 2048
+    wg = synth.iq3xxs_matrix(56, 0, I, H)
+    wu = synth.iq3xxs_matrix(56, 1, I, H)
+    wd = synth.iq3xxs_matrix(56, 2, H, I)
+    x = synth.normal(56, 9, H) * np.float32(4.0)
+    tg, tu, td = (G.tile(dev(a.reshape(-1), gpu), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I)))
+    act = G.act_buffer(H, gpu)
+    G.prep_act(dev(x, gpu), act)
+    g = G.matvec_act(tg, I, 0, H, I, act)
+    u = G.matvec_act(tu, I, 0, H, I, act)
+    act2 = G.act_buffer(I, gpu)
+    G.prep_swiglu(g, u, act2, 10.0)
+    y = host(G.matvec_act(td, H, 0, I, H, act2))
+    ref = oracle.dense_mlp(wg, wu, wd, H, I, x[None, :], 10.0)[0]
+    e = rel_err(y, ref)
+    assert e < TOL, e
+    assert e < 1e-4, e  # silu via the device expf differs by ulps from glibc's
+    torch.cuda.synchronize()
+
+
+def test_weight_store_mirror(gpu):
+    w = synth.iq3xxs_matrix(57, 0, 64, 512)
+    ws = G.WeightStore(device=gpu)
+    ws.add("blk.0.ffn_up.weight", w, 512, 64)
+    x = synth.normal(57, 1, 512)
+    y = ws.matvec_quant("blk.0.ffn_up.weight", 16, 512, 32, x)
+    assert rel_err(y, oracle.matvec(w, 16, 512, 32, x)) < TIGHT
+    with pytest.raises(RuntimeError, match="missing tensor"):
+        ws.matvec_quant("nope", 0, 512, 16, x)
+    with pytest.raises(RuntimeError, match="not block aligned"):
+        ws.matvec_quant("blk.0.ffn_up.weight", 0, 500, 16, x)
+
+
+def test_device_smoke(gpu):
+    assert G.device_count() >= 1
+    assert G.device_name(0) not in ("", "<none>")
+    a = synth.normal(58, 0, 1000)
+    b = synth.normal(58, 1, 1000)
+    assert np.array_equal(G.add_f32(a, b), a + b)
