@@ -11,10 +11,10 @@ the 256 MB Infinity Cache, `--copies` distinct copies of the three tensors
 (default 8, 694 MB) are rotated step by step.
 
 value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
-roofline = the matvec kernel (k_matvec_t16): algorithmic bytes per launch
-(packed W + activation operand + output) / its mean duration, timed with
-HIP events on the launch stream around every matvec launch of the timed
-steps, against 8 TB/s HBM.
+roofline = the matvec kernel (k_matvec_t16, launched once for gate+up and
+once for down per step): algorithmic bytes of its launches (packed W +
+prepared activation + outputs) / their summed duration, each launch timed
+with HIP events on the launch stream during the timed steps, against 8 TB/s.
 cpu_baseline = the reference's own CPU path (oracle/_ref: WeightStore::
 matvec_quant compiled from the reference sources, single-threaded as the
 reference builds on Linux) on one full step of the same workload; the
@@ -140,25 +140,23 @@ def main():
     y = torch.empty(H, device=dev)
     stream = torch.cuda.current_stream()
 
+    def timed_launch(ev, kind, fn):
+        if ev is None:
+            fn()
+            return
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        ev.append((kind, a, b))
+
     def step(c, ev=None):
         tg, tu, td = copies[c]
         G.prep_act(xd, act)
-        for w_t, dst, a, rows, k in ((tg, g, act, I, H), (tu, u, act, I, H)):
-            if ev is not None:
-                ev[0].append(torch.cuda.Event(enable_timing=True))
-                ev[0][-1].record(stream)
-            G.matvec_act(w_t, rows, 0, k, rows, a, out=dst)
-            if ev is not None:
-                ev[1].append(torch.cuda.Event(enable_timing=True))
-                ev[1][-1].record(stream)
+        timed_launch(ev, "gate+up", lambda: G.matvec2_act(tg, tu, I, 0, H, I, act, out_a=g, out_b=u))
         G.prep_swiglu(g, u, act2, SWIGLU_LIMIT)
-        if ev is not None:
-            ev[0].append(torch.cuda.Event(enable_timing=True))
-            ev[0][-1].record(stream)
-        G.matvec_act(td, H, 0, I, H, act2, out=y)
-        if ev is not None:
-            ev[1].append(torch.cuda.Event(enable_timing=True))
-            ev[1][-1].record(stream)
+        timed_launch(ev, "down", lambda: G.matvec_act(td, H, 0, I, H, act2, out=y))
 
     log("warmup")
     for i in range(args.warmup):
@@ -169,7 +167,7 @@ def main():
     y_gpu = y.cpu().numpy().copy()
 
     log("timed")
-    ev = ([], [])
+    ev = []
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -179,11 +177,21 @@ def main():
     t1.record(stream)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
-    launch_ms = [a.elapsed_time(b) for a, b in zip(*ev)]
-    mean_launch = statistics.fmean(launch_ms)
-    per_launch_bytes = W_BYTES // 3 + H * 4 + I * 4  # packed W + activation operand + output
-    achieved = per_launch_bytes / (mean_launch * 1e-3) / 1e9
+    # k_matvec_t16 launches: bytes = packed W + prepared activation + outputs
+    act_bytes = {"gate+up": G.lib().gpeed_iq3xxs_act_bytes(H), "down": G.lib().gpeed_iq3xxs_act_bytes(I)}
+    launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + act_bytes["gate+up"] + 2 * I * 4,
+                    "down": W_BYTES // 3 + act_bytes["down"] + H * 4}
+    per_kind = {}
+    for kind, a, b in ev:
+        per_kind.setdefault(kind, []).append(a.elapsed_time(b))
+    tot_ms = sum(sum(v) for v in per_kind.values())
+    tot_bytes = sum(launch_bytes[k] * len(v) for k, v in per_kind.items())
+    achieved = tot_bytes / (tot_ms * 1e-3) / 1e9
     value = W_BYTES / (ms * 1e-3) / 1e9
+    kinds = {k: {"mean_us": round(statistics.fmean(v) * 1e3, 3), "launches": len(v),
+                 "algorithmic_bytes": launch_bytes[k],
+                 "GBps": round(launch_bytes[k] / (statistics.fmean(v) * 1e-3) / 1e9, 1)}
+             for k, v in per_kind.items()}
 
     rec = {
         "metric": METRIC,
@@ -204,8 +212,7 @@ def main():
                    "packed_weight_bytes_per_step": W_BYTES, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_matvec_t16", "mean_launch_us": round(mean_launch * 1e3, 3),
-                     "launches": len(launch_ms), "algorithmic_bytes_per_launch": per_launch_bytes},
+                     "kernel": "k_matvec_t16", "launch_kinds": kinds},
     }
     if not args.no_cpu:
         log("cpu baseline")

@@ -61,7 +61,7 @@ def lib():
             "gpeed_iq3xxs_row_bytes": ([i64], sz),
             "gpeed_iq3xxs_t16_bytes": ([u64, i64], sz),
             "gpeed_dequantize": ([i32, vp, vp, u64, vp], i32),
-            "gpeed_t16_sign_table": ([vp, sz], i32),
+            "gpeed_t16_grid_table": ([vp, sz], i32),
             "gpeed_t16_aux_word": ([C.c_uint32], C.c_uint32),
             "gpeed_iq3xxs_tile": ([vp, u64, i64, vp, vp], i32),
             "gpeed_iq3xxs_untile": ([vp, u64, i64, vp, vp], i32),
@@ -72,6 +72,7 @@ def lib():
             "gpeed_iq3xxs_prep_act": ([vp, i64, vp, sz, vp], i32),
             "gpeed_iq3xxs_prep_swiglu": ([vp, vp, i64, C.c_float, vp, sz, vp], i32),
             "gpeed_iq3xxs_matvec_act": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
+            "gpeed_iq3xxs_matvec2_act": ([vp, vp, u64, u64, i32, i32, vp, vp, vp, vp], i32),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -216,6 +217,20 @@ def matvec_act(w_t16, n_rows: int, row0: int, in_dim: int, out_dim: int, act, ou
     _check(lib().gpeed_iq3xxs_matvec_act(_ptr(w_t16), n_rows, row0, in_dim, out_dim, _ptr(act), _ptr(out),
                                          _stream(stream)), "matvec_act")
     return out
+
+
+def matvec2_act(w_a, w_b, n_rows: int, row0: int, in_dim: int, out_dim: int, act, out_a=None, out_b=None,
+                stream=None):
+    """Two same-shape T16 tensors against one prepared activation, one launch."""
+    torch = _torch()
+    _require_cuda(w_a, w_b, act)
+    if out_a is None:
+        out_a = torch.empty(out_dim, dtype=torch.float32, device=act.device)
+    if out_b is None:
+        out_b = torch.empty(out_dim, dtype=torch.float32, device=act.device)
+    _check(lib().gpeed_iq3xxs_matvec2_act(_ptr(w_a), _ptr(w_b), n_rows, row0, in_dim, out_dim, _ptr(act),
+                                          _ptr(out_a), _ptr(out_b), _stream(stream)), "matvec2_act")
+    return out_a, out_b
 
 
 def matvec_raw(w, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None, stream=None):

@@ -24,31 +24,40 @@ int hip_fail(hipError_t e, const char* what) {
 
 constexpr int kMaxDevices = 64;
 std::mutex g_init_mu;
-void* g_sign_table[kMaxDevices] = {};
+struct DeviceState {
+    void* grid_table = nullptr;  // 64 KiB replicated grid table
+    int num_cus = 0;
+};
+DeviceState g_dev[kMaxDevices];
 
-// Per-device 64 KiB signed lookup table (uploaded once, kept until exit).
-int device_tables(const void** sign_table) {
+// Per-device state, made once (hipMalloc + upload) and kept until exit.
+int device_state(const DeviceState** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     if (dev < 0 || dev >= kMaxDevices) return fail(GPEED_ERR_INVALID, "device index out of range");
-    if (!g_sign_table[dev]) {
+    DeviceState& st = g_dev[dev];
+    if (!__atomic_load_n(&st.grid_table, __ATOMIC_ACQUIRE)) {
         std::lock_guard<std::mutex> lk(g_init_mu);
-        if (!g_sign_table[dev]) {
-            std::vector<uint16_t> host(gpeed::kSignTableBytes / 2);
-            gpeed::build_sign_table(host.data());
+        if (!st.grid_table) {
+            int cus = 0;
+            e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+            std::vector<uint16_t> host(gpeed::kGridTableBytes / 2);
+            gpeed::build_grid_table(host.data());
             void* p = nullptr;
-            e = hipMalloc(&p, gpeed::kSignTableBytes);
-            if (e != hipSuccess) return hip_fail(e, "hipMalloc(sign table)");
-            e = hipMemcpy(p, host.data(), gpeed::kSignTableBytes, hipMemcpyHostToDevice);
+            e = hipMalloc(&p, gpeed::kGridTableBytes);
+            if (e != hipSuccess) return hip_fail(e, "hipMalloc(grid table)");
+            e = hipMemcpy(p, host.data(), gpeed::kGridTableBytes, hipMemcpyHostToDevice);
             if (e != hipSuccess) {
                 (void)hipFree(p);
-                return hip_fail(e, "hipMemcpy(sign table)");
+                return hip_fail(e, "hipMemcpy(grid table)");
             }
-            g_sign_table[dev] = p;
+            st.num_cus = cus;
+            __atomic_store_n(&st.grid_table, p, __ATOMIC_RELEASE);
         }
     }
-    *sign_table = g_sign_table[dev];
+    *out = &st;
     return GPEED_OK;
 }
 
@@ -95,8 +104,8 @@ int gpeed_add_f32(const float* a, const float* b, float* dst, int n) {
 
 int gpeed_init(void) {
     if (gpeed_device_count() <= 0) return fail(GPEED_ERR_NO_DEVICE, "no HIP device");
-    const void* t = nullptr;
-    return device_tables(&t);
+    const DeviceState* st = nullptr;
+    return device_state(&st);
 }
 
 size_t gpeed_iq3xxs_row_bytes(int64_t in_dim) {
@@ -123,10 +132,10 @@ int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_s
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "dequantize launch");
 }
 
-int gpeed_t16_sign_table(uint16_t* out, size_t n) {
-    if (!out || n < (size_t)gpeed::kSignTableBytes / 2)
-        return fail(GPEED_ERR_INVALID, "t16_sign_table: buffer smaller than 32768 entries");
-    gpeed::build_sign_table(out);
+int gpeed_t16_grid_table(uint16_t* out, size_t n) {
+    if (!out || n < (size_t)gpeed::kGridTableBytes / 2)
+        return fail(GPEED_ERR_INVALID, "t16_grid_table: buffer smaller than 32768 entries");
+    gpeed::build_grid_table(out);
     return GPEED_OK;
 }
 
@@ -164,13 +173,15 @@ int gpeed_iq3xxs_untile(const void* t16, uint64_t n_rows, int64_t in_dim, void* 
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "untile launch");
 }
 
-size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim) {
-    if (in_dim <= 0 || in_dim % gpeed::kQK) return 0;
-    return gpeed::prep_x_bytes(1, (int)in_dim);
+size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim) { return gpeed_iq3xxs_act_bytes(in_dim); }
+
+size_t gpeed_iq3xxs_act_bytes(int64_t in_dim) {
+    if (in_dim <= 0 || in_dim % gpeed::kQK || in_dim > (1 << 30)) return 0;
+    return gpeed::act_bytes((int)in_dim);
 }
 
 static int check_mv_args(const void* w, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
-                         const float* x, float* dst, const char* who) {
+                         const void* x, float* dst, const char* who) {
     if (in_dim <= 0 || in_dim % gpeed::kQK)
         return fail(GPEED_ERR_UNALIGNED_ROW, std::string(who) + ": row not block aligned");
     if (!w || !x || !dst) return fail(GPEED_ERR_INVALID, std::string(who) + ": null pointer");
@@ -179,29 +190,23 @@ static int check_mv_args(const void* w, uint64_t n_rows, uint64_t row0, int in_d
     return GPEED_OK;
 }
 
-size_t gpeed_iq3xxs_act_bytes(int64_t in_dim) { return gpeed_iq3xxs_matvec_ws_bytes(in_dim); }
-
 static int check_act(const void* act, size_t act_bytes, int64_t in_dim, const char* who) {
     if (in_dim <= 0 || in_dim % gpeed::kQK)
         return fail(GPEED_ERR_UNALIGNED_ROW, std::string(who) + ": row not block aligned");
     if (in_dim > (1 << 30)) return fail(GPEED_ERR_INVALID, std::string(who) + ": in_dim too large");
-    if (!act || act_bytes < gpeed::prep_x_bytes(1, (int)in_dim) || !aligned(act, 16))
+    if (!act || act_bytes < gpeed::act_bytes((int)in_dim) || !aligned(act, 16))
         return fail(GPEED_ERR_WORKSPACE,
                     std::string(who) + ": activation buffer missing, misaligned or too small");
     return GPEED_OK;
-}
-
-static float* act_scale(void* act, int64_t in_dim) {
-    return reinterpret_cast<float*>(static_cast<uint8_t*>(act) + (size_t)in_dim * 4);
 }
 
 int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, void* act, size_t act_bytes,
                           gpeed_stream_t stream) {
     int rc = check_act(act, act_bytes, in_dim, "prep_act");
     if (rc) return rc;
-    if (!x) return fail(GPEED_ERR_INVALID, "prep_act: null pointer");
-    hipError_t e = gpeed::launch_prep_x(x, 1, (int)in_dim, static_cast<uint32_t*>(act),
-                                        act_scale(act, in_dim), static_cast<hipStream_t>(stream));
+    if (!x || !aligned(x, 16)) return fail(GPEED_ERR_INVALID, "prep_act: x null or not 16-byte aligned");
+    hipError_t e = gpeed::launch_prep_act(x, (int)in_dim, static_cast<uint8_t*>(act),
+                                          static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "prep_act launch");
 }
 
@@ -209,30 +214,50 @@ int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, float li
                              size_t act_bytes, gpeed_stream_t stream) {
     int rc = check_act(act, act_bytes, n, "prep_swiglu");
     if (rc) return rc;
-    if (!g || !u) return fail(GPEED_ERR_INVALID, "prep_swiglu: null pointer");
-    hipError_t e = gpeed::launch_prep_swiglu(g, u, limit, 1, (int)n, static_cast<uint32_t*>(act),
-                                             act_scale(act, n), static_cast<hipStream_t>(stream));
+    if (!g || !u || !aligned(g, 16) || !aligned(u, 16))
+        return fail(GPEED_ERR_INVALID, "prep_swiglu: g/u null or not 16-byte aligned");
+    hipError_t e = gpeed::launch_prep_swiglu(g, u, limit, (int)n, static_cast<uint8_t*>(act),
+                                             static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "prep_swiglu launch");
+}
+
+static int matvec_act_n(const void* const* w, float* const* dst, int n_tensors, uint64_t n_rows,
+                        uint64_t row0, int in_dim, int out_dim, const void* act,
+                        gpeed_stream_t stream) {
+    if (out_dim <= 0) return GPEED_OK;
+    for (int i = 0; i < n_tensors; ++i) {
+        int rc = check_mv_args(w[i], n_rows, row0, in_dim, out_dim, act, dst[i], "matvec");
+        if (rc) return rc;
+        if (!aligned(w[i], 16)) return fail(GPEED_ERR_INVALID, "matvec: T16 weights must be 16-byte aligned");
+    }
+    if (!aligned(act, 16)) return fail(GPEED_ERR_WORKSPACE, "matvec: activation misaligned");
+    if (row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "matvec: row0 must be a multiple of 16 on the T16 layout");
+    const DeviceState* st = nullptr;
+    int rc = device_state(&st);
+    if (rc) return rc;
+    const uint8_t* wp[2] = {static_cast<const uint8_t*>(w[0]),
+                            static_cast<const uint8_t*>(w[n_tensors > 1 ? 1 : 0])};
+    float* yp[2] = {dst[0], dst[n_tensors > 1 ? 1 : 0]};
+    hipError_t e = gpeed::launch_matvec_t16(wp, yp, n_tensors, in_dim, row0, out_dim,
+                                            static_cast<const uint8_t*>(act), st->grid_table,
+                                            st->num_cus, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec launch");
 }
 
 int gpeed_iq3xxs_matvec_act(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim,
                             int out_dim, const void* act, float* dst, gpeed_stream_t stream) {
-    if (out_dim <= 0) return GPEED_OK;
-    const float dummy = 0.0f;
-    int rc = check_mv_args(w_t16, n_rows, row0, in_dim, out_dim, &dummy, dst, "matvec");
-    if (rc) return rc;
-    if (!act || !aligned(act, 16)) return fail(GPEED_ERR_WORKSPACE, "matvec: activation missing or misaligned");
-    if (row0 % gpeed::kTileRows)
-        return fail(GPEED_ERR_LAYOUT, "matvec: row0 must be a multiple of 16 on the T16 layout");
-    if (!aligned(w_t16, 16)) return fail(GPEED_ERR_INVALID, "matvec: T16 weights must be 16-byte aligned");
-    const void* tbl = nullptr;
-    rc = device_tables(&tbl);
-    if (rc) return rc;
-    hipError_t e = gpeed::launch_matvec_t16(static_cast<const uint8_t*>(w_t16), in_dim, row0, out_dim,
-                                            static_cast<const uint32_t*>(act),
-                                            act_scale(const_cast<void*>(act), in_dim), dst, tbl,
-                                            static_cast<hipStream_t>(stream));
-    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec launch");
+    const void* w[1] = {w_t16};
+    float* d[1] = {dst};
+    return matvec_act_n(w, d, 1, n_rows, row0, in_dim, out_dim, act, stream);
+}
+
+int gpeed_iq3xxs_matvec2_act(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0,
+                             int in_dim, int out_dim, const void* act, float* dst_a, float* dst_b,
+                             gpeed_stream_t stream) {
+    const void* w[2] = {w_a, w_b};
+    float* d[2] = {dst_a, dst_b};
+    return matvec_act_n(w, d, 2, n_rows, row0, in_dim, out_dim, act, stream);
 }
 
 int gpeed_iq3xxs_matvec(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,

@@ -15,18 +15,19 @@ hipError_t launch_tile(const uint8_t* raw, unsigned long long n_rows, int in_dim
                        hipStream_t s);
 hipError_t launch_untile(const uint8_t* t16, unsigned long long n_rows, int in_dim, uint8_t* raw,
                          hipStream_t s);
-// fp32 activations [n_tok][in_dim] -> fp16 hi/lo A-operand layout with a
-// power-of-two scale per token (xscale[t] = 2^-e_t).
-hipError_t launch_prep_x(const float* x, int n_tok, int in_dim, uint32_t* x16, float* xscale,
-                         hipStream_t s);
-size_t prep_x_bytes(int n_tok, int in_dim);
-// Same layout for h = silu(min(g,lim)) * clamp(u,-lim,lim) (SwiGLU epilogue).
-hipError_t launch_prep_swiglu(const float* g, const float* u, float lim, int n_tok, int in_dim,
-                              uint32_t* x16, float* xscale, hipStream_t s);
-// y[j] = sum_k W[row0+j][k] x[k] from the T16 payload (one token).
-hipError_t launch_matvec_t16(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
-                             const uint32_t* x16, const float* xscale, float* y,
-                             const void* sign_table, hipStream_t s);
+// Prepared activation ("act"): for each 256-element block, the fp16 hi/lo
+// MFMA A operand of the block scaled by a power of two (1 KiB), then one fp32
+// unscale per block. act_bytes() is its size, rounded to 256 bytes.
+size_t act_bytes(int in_dim);
+hipError_t launch_prep_act(const float* x, int in_dim, uint8_t* act, hipStream_t s);
+// Same for h = silu(min(g,lim)) * clamp(u,-lim,lim) (SwiGLU epilogue).
+hipError_t launch_prep_swiglu(const float* g, const float* u, float lim, int in_dim, uint8_t* act,
+                              hipStream_t s);
+// y_i[j] = sum_k W_i[row0+j][k] x[k] over the T16 payloads of n_tensors
+// (1 or 2) same-shape tensors sharing one prepared activation.
+hipError_t launch_matvec_t16(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
+                             unsigned long long row0, int out_dim, const uint8_t* act,
+                             const void* grid_table, int num_cus, hipStream_t s);
 // Same product straight from GGUF rows (VALU decode, no repacking).
 hipError_t launch_matvec_raw(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
                              const float* x, float* y, hipStream_t s);

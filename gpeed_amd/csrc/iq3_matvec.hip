@@ -1,13 +1,20 @@
 // IQ3_XXS decode matvec kernels (gfx950).
 //
-// k_matvec_t16: batch-1 y = W x over the T16 layout. Each wavefront streams
-// records of one 16-row tile with 12-byte coalesced loads, turns every
-// 8-weight group into an fp16 B operand with two LDS lookups (signed grid
-// values) scaled by the exact small integer (2s+1), and feeds
-// v_mfma_f32_16x16x32_f16. The activation is carried as two fp16 rows
-// (x = hi + lo after a power-of-two scaling), so products are exact and the
-// only rounding is fp32 accumulation. The block scale d/4 is applied once per
-// 256-weight block to the MFMA accumulator.
+// k_matvec_t16: batch-1 y = W x over the T16 layout, persistent: one
+// 1024-thread workgroup per CU keeps the 64 KiB signed grid table and the
+// prepared activation in LDS and walks groups of up to kMvMaxR 16-row tiles.
+// The (tile, block) records of a group are split evenly over its 16
+// wavefronts; each streams its records with 12-byte coalesced loads through
+// a kMvPF-deep register ring and meets the others in LDS per tile.
+//
+// Per record (16 rows x 256 weights) a wavefront issues 8
+// v_mfma_f32_16x16x32_f16. Lane n+16g owns sub-block 4j+g of row n: its two
+// LDS lookups per 8-weight group give the signed grid values as fp16, the
+// A operand carries the activation as two fp16 rows (hi, lo) placed in rows
+// 4g and 4g+1, so accumulator rows 4g/4g+1 of lane n+16g hold exactly that
+// sub-block's partial sum and the lane applies its own scale
+// d*(0.5+s)*0.5 (times the activation block's power-of-two unscale) to it.
+// All products are exact; only fp32 accumulation order differs from the CPU.
 #include "iq3_common.h"
 #include "iq3_kernels.h"
 
@@ -15,162 +22,307 @@ namespace gpeed {
 
 namespace {
 
-constexpr int kMatvecWaves = 4;
+constexpr int kMvMaxR = 8;         // tiles per group
+constexpr int kMvMaxStageNb = 64;  // activations up to 16384 elements live in LDS
+constexpr int kZeroBytes = 1024;
 
-// Half index of activation element k in the M=1 A-operand layout
-// [block][j][l][g][hl][8]: the 16 bytes lane (16g + hl) loads for MFMA (j, l).
-__device__ __forceinline__ size_t x16_index_m1(int k, int hl) {
-    const int blk = k >> 8, ib = (k >> 5) & 7, j = ib >> 2, g = ib & 3, l = (k >> 3) & 3, r = k & 7;
-    return ((((size_t)(blk * 2 + j) * 4 + l) * 4 + g) * 2 + hl) * 8 + r;
+// Half index of element kk (0..255) of a block in the activation layout
+// [j][l][g][hl][8]: the 16 bytes lane (m = 4g + hl, group g) feeds MFMA (j, l).
+__device__ __forceinline__ int act_half_index(int kk, int hl) {
+    const int ib = kk >> 5, j = ib >> 2, g = ib & 3, l = (kk >> 3) & 3, r = kk & 7;
+    return (((j * 4 + l) * 4 + g) * 2 + hl) * 8 + r;
 }
 
-// One workgroup per token: max|v| -> power-of-two scale -> fp16 hi/lo split
-// into the A-operand layout. MODE 0: v = x. MODE 1: v = SwiGLU with clamp,
-// silu(min(g,lim)) * clamp(u,-lim,lim) (model.cpp:683-688,
-// model_batch.cpp:245-253), with g = x and u = x2.
+// One wavefront per 256-element block: max|v| -> power-of-two scale ->
+// fp16 hi/lo split. MODE 0: v = x. MODE 1: v = silu(min(g,lim)) *
+// clamp(u,-lim,lim) (model.cpp:683-688, model_batch.cpp:245-253), g = x, u = x2.
 template <int MODE>
-__global__ __launch_bounds__(256) void k_prep_x(const float* __restrict__ x,
-                                                const float* __restrict__ x2, float lim,
-                                                int in_dim, _Float16* __restrict__ x16,
-                                                float* __restrict__ xscale) {
-    __shared__ float red[256];
-    const int t = blockIdx.x;
-    const float* xt = x + (size_t)t * in_dim;
-    const float* ut = MODE == 1 ? x2 + (size_t)t * in_dim : nullptr;
-    auto value = [&](int k) -> float {
-        if (MODE == 0) return xt[k];
-        const float gi = fminf(xt[k], lim);
-        const float ui = fminf(fmaxf(ut[k], -lim), lim);
-        return (gi / (1.0f + expf(-gi))) * ui;
-    };
-    float m = 0.0f;
-    for (int k = threadIdx.x; k < in_dim; k += 256) m = fmaxf(m, fabsf(value(k)));
-    red[threadIdx.x] = m;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (threadIdx.x < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
-        __syncthreads();
+__global__ __launch_bounds__(256) void k_prep_act(const float* __restrict__ x,
+                                                  const float* __restrict__ x2, float lim, int nb,
+                                                  _Float16* __restrict__ x16,
+                                                  float* __restrict__ xsc) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + wave;
+    if (b >= nb) return;
+    const float4 v = *reinterpret_cast<const float4*>(x + (size_t)b * 256 + 4 * lane);
+    float e[4] = {v.x, v.y, v.z, v.w};
+    if (MODE == 1) {
+        const float4 u = *reinterpret_cast<const float4*>(x2 + (size_t)b * 256 + 4 * lane);
+        const float us[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float gi = fminf(e[c], lim);
+            const float ui = fminf(fmaxf(us[c], -lim), lim);
+            e[c] = (gi / (1.0f + expf(-gi))) * ui;
+        }
     }
-    m = red[0];
-    int e = 0;
+    float m = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    int sc = 0;
     if (m > 0.0f && m < __builtin_inff()) {
         int ex;
         (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
-        e = 14 - ex;           // scaled max in [2^13, 2^14)
-        e = e > 120 ? 120 : (e < -120 ? -120 : e);
+        sc = 14 - ex;          // scaled max in [2^13, 2^14)
+        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
     }
-    _Float16* out = x16 + (size_t)t * ((size_t)in_dim * 2);
-    for (int k = threadIdx.x; k < in_dim; k += 256) {
-        const float xs = ldexpf(value(k), e);
-        const _Float16 hi = (_Float16)xs;
-        const _Float16 lo = (_Float16)(xs - (float)hi);
-        out[x16_index_m1(k, 0)] = hi;
-        out[x16_index_m1(k, 1)] = lo;
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float xs = ldexpf(e[c], sc);
+        hi[c] = (_Float16)xs;
+        lo[c] = (_Float16)(xs - (float)hi[c]);
     }
-    if (threadIdx.x == 0) xscale[t] = ldexpf(1.0f, -e);
+    _Float16* out = x16 + (size_t)b * 512 + act_half_index(4 * lane, 0);
+    *reinterpret_cast<u32x2_t*>(out) = __builtin_bit_cast(u32x2_t, hi);
+    *reinterpret_cast<u32x2_t*>(out + 8) = __builtin_bit_cast(u32x2_t, lo);
+    if (lane == 0) xsc[b] = ldexpf(1.0f, -sc);
 }
 
 __device__ __forceinline__ u32x2_t lds_lookup(const uint8_t* tbl, uint32_t addr) {
     return *reinterpret_cast<const u32x2_t*>(tbl + addr);
 }
 
-__device__ __forceinline__ uint32_t pk_mul_f16(uint32_t v, half2_t f) {
-    half2_t h = __builtin_bit_cast(half2_t, v);
-    return __builtin_bit_cast(uint32_t, h * f);
-}
-
-// B operand of group l of a unit (q0, q1 = grid index words, cb1/cb2 = code
-// bytes of the four groups), scaled by f = (2s+1).
+// B operand of group L of a unit: two lookups of 4 unsigned fp16 grid values
+// (the lane's own replica of the table, so no bank conflicts) and the eight
+// signs inserted on the fp16 sign bits with v_bfi_b32. lb = (lane & 31) << 3.
 template <int L>
 __device__ __forceinline__ half8_t decode_group(const uint8_t* tbl, uint32_t q0, uint32_t q1,
-                                                uint32_t cb1, uint32_t cb2, half2_t f) {
+                                                uint32_t lb, uint32_t sw) {
     const uint32_t q = (L < 2) ? q0 : q1;
     constexpr uint32_t p1 = (2 * L) & 3, p2 = p1 + 1;
-    constexpr uint32_t sel1 = 0x0C0C0000u | ((4u + p1) << 8) | (uint32_t)L;
-    constexpr uint32_t sel2 = 0x0C0C0000u | ((4u + p2) << 8) | (uint32_t)L;
-    const uint32_t a1 = __builtin_amdgcn_perm(q, cb1, sel1);
-    const uint32_t a2 = __builtin_amdgcn_perm(q, cb2, sel2);
-    const u32x2_t v1 = lds_lookup(tbl, a1);
-    const u32x2_t v2 = lds_lookup(tbl, a2);
-    u32x4_t r;
-    r.x = pk_mul_f16(v1.x, f);
-    r.y = pk_mul_f16(v1.y, f);
-    r.z = pk_mul_f16(v2.x, f);
-    r.w = pk_mul_f16(v2.y, f);
+    constexpr uint32_t sel1 = 0x0C0C0000u | ((4u + p1) << 8);
+    constexpr uint32_t sel2 = 0x0C0C0000u | ((4u + p2) << 8);
+    const u32x2_t g1 = lds_lookup(tbl, __builtin_amdgcn_perm(q, lb, sel1));
+    const u32x2_t g2 = lds_lookup(tbl, __builtin_amdgcn_perm(q, lb, sel2));
+    const u32x4_t r = {((sw << (0 + L)) & 0x80008000u) | g1.x,
+                       ((sw << (4 + L)) & 0x80008000u) | g1.y,
+                       ((sw << (8 + L)) & 0x80008000u) | g2.x,
+                       ((sw << (12 + L)) & 0x80008000u) | g2.y};
     return __builtin_bit_cast(half8_t, r);
 }
 
-struct Unit {
-    uint32_t q0, q1, a;
+// 7 dwords per lane per record: two 12-byte units and the row's fp16 d.
+struct Rec {
+    uint32_t u[7];
 };
 
-__device__ __forceinline__ Unit load_unit(const uint8_t* p) {
-    const uint32_t* u = reinterpret_cast<const uint32_t*>(p);
-    return Unit{u[0], u[1], u[2]};
+__device__ __forceinline__ void load_rec(Rec& r, const uint8_t* rec, uint32_t lane, uint32_t n) {
+    // uniform record base + 32-bit unsigned lane offset: SGPR-based addressing
+    const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rec + lane * 12u);
+    const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rec + kUnitHalfBytes + lane * 12u);
+    r.u[0] = p0[0];
+    r.u[1] = p0[1];
+    r.u[2] = p0[2];
+    r.u[3] = p1[0];
+    r.u[4] = p1[1];
+    r.u[5] = p1[2];
+    r.u[6] = *reinterpret_cast<const uint16_t*>(rec + 2 * kUnitHalfBytes + 2u * n);
 }
 
-// Accumulates the 4 MFMAs of one unit into acc.
-__device__ __forceinline__ float4_t unit_mfma(const uint8_t* tbl, const Unit& u, const half8_t* A,
-                                              float4_t acc) {
-    const uint32_t cb1 = (u.a << 3) & 0x78787878u;
-    const uint32_t cb2 = (u.a & 0x78787878u) | 0x80808080u;
-    const uint32_t s = t16_scale(u.a);
-    const _Float16 fs = (_Float16)(float)(2u * s + 1u);
-    const half2_t f = {fs, fs};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], decode_group<0>(tbl, u.q0, u.q1, cb1, cb2, f), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], decode_group<1>(tbl, u.q0, u.q1, cb1, cb2, f), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], decode_group<2>(tbl, u.q0, u.q1, cb1, cb2, f), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], decode_group<3>(tbl, u.q0, u.q1, cb1, cb2, f), acc, 0, 0, 0);
+// A operands of one unit (4 MFMAs). Only lanes 4g and 4g+1 of lane group g
+// carry data. From LDS every lane reads (idle lanes from a 1 KiB zero region,
+// a same-address broadcast), so no branch and no register zeroing; from
+// global memory the idle lanes skip the load.
+template <bool STAGE>
+__device__ __forceinline__ void load_a4(half8_t (&A)[4], const uint8_t* a_lds, const half8_t* a_g,
+                                        bool a_lane) {
+    if (STAGE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A[i] = *reinterpret_cast<const half8_t*>(a_lds + i * 128);
+    } else if (a_lane) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A[i] = a_g[i * 8];
+    } else {
+        const half8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A[i] = z;
+    }
+}
+
+// One record: 2 units x 4 chained MFMAs; acc += db * (hi + lo partial).
+// a_lds / a_g point at this lane's A bytes of the record's block.
+template <bool STAGE>
+__device__ __forceinline__ float record_dot(const uint8_t* tbl, const Rec& r, uint32_t lb,
+                                            const uint8_t* a_lds, const half8_t* a_g, bool a_lane,
+                                            float d4, float acc) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t q0 = r.u[3 * j], q1 = r.u[3 * j + 1], w = r.u[3 * j + 2];
+        const uint32_t sw = t16_full_signs(w);
+        const float db = (float)(2u * ((w >> 16) & 15u) + 1u) * d4;
+        half8_t A[4];
+        load_a4<STAGE>(A, a_lds + j * 512, a_g + j * 32, a_lane);
+        float4_t D = {0.0f, 0.0f, 0.0f, 0.0f};
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], decode_group<0>(tbl, q0, q1, lb, sw), D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], decode_group<1>(tbl, q0, q1, lb, sw), D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[2], decode_group<2>(tbl, q0, q1, lb, sw), D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[3], decode_group<3>(tbl, q0, q1, lb, sw), D, 0, 0, 0);
+        acc = fmaf(db, D[0] + D[1], acc);
+    }
     return acc;
 }
 
-// Workgroup = kMatvecWaves wavefronts sharing one 16-row tile; wave w takes
-// a contiguous range of blocks along K; partial row sums meet in LDS.
-__global__ __launch_bounds__(kMatvecWaves * 64) void k_matvec_t16(
-    const uint8_t* __restrict__ w, int nb, long long tile0, int out_dim,
-    const half8_t* __restrict__ x16, const float* __restrict__ xscale, float* __restrict__ y,
-    const u32x4_t* __restrict__ sign_table) {
-    __shared__ __attribute__((aligned(16))) uint8_t tbl[kSignTableBytes];
-    __shared__ float red[kMatvecWaves][16];
+struct MvArgs {
+    const uint8_t* w[2];  // T16 records of the first requested tile, per tensor
+    float* y[2];
+    int n_tensors;
+    int nb;
+    int n_tiles;  // tiles per tensor
+    int out_dim;
+    const uint8_t* act;  // x16 [nb][1024 B] then xscale [nb]
+    const u32x4_t* table;
+};
+
+// Workgroup barrier that orders LDS only: outstanding global loads (the
+// record ring) stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <bool STAGE, int WAVES, int PF>
+__global__ __launch_bounds__(WAVES * 64) void k_matvec_t16(MvArgs args) {
+    constexpr int kThreads = WAVES * 64;
+    // One LDS arena so the table sits at address 0 and lookup addresses need
+    // no base: [grid table 64 KiB][activation nb KiB][zeros 1 KiB][unscales][partials]
+    constexpr int kXsBytes = STAGE ? kMvMaxStageNb * 1024 : 0;
+    constexpr int kZeroOff = kGridTableBytes + kXsBytes;
+    constexpr int kXscOff = kZeroOff + (STAGE ? kZeroBytes : 0);
+    constexpr int kRedOff = kXscOff + kMvMaxStageNb * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kRedOff + kMvMaxR * WAVES * 16 * 4];
+    uint8_t* const tbl = lds;
+    uint8_t* const xs = lds + kGridTableBytes;
+    float* const xsc = reinterpret_cast<float*>(lds + kXscOff);
+    float(*const red)[WAVES][16] = reinterpret_cast<float(*)[WAVES][16]>(lds + kRedOff);
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int n = lane & 15, g = lane >> 4;
-    const long long t = tile0 + blockIdx.x;
-    const int b0 = (nb * wave) / kMatvecWaves, b1 = (nb * (wave + 1)) / kMatvecWaves;
+    // wave-uniform: keeps the record ranges and loop control in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t lane = tid & 63;
+    const uint32_t n = lane & 15, g = lane >> 4;
+    const int nb = args.nb;
+    const bool a_lane = (n >> 1) == 2 * g;  // rows 4g (hi) and 4g+1 (lo) of the A operand
+    const int a_lane_off = g * 32 + (n & 1) * 16;
+    const uint32_t lb = (lane & 31u) << 3;  // this lane's replica of the grid table
+    const uint8_t* act = args.act;
+    const float* xsc_g = reinterpret_cast<const float*>(act + (size_t)nb * 1024);
 
-    for (int i = tid; i < kSignTableBytes / 16; i += kMatvecWaves * 64)
-        reinterpret_cast<u32x4_t*>(tbl)[i] = sign_table[i];
-    __syncthreads();
-
-    const bool a_lane = n < 2;  // rows 0 (hi) and 1 (lo) of the A operand
-    const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-    float acc = 0.0f;
-    const uint8_t* rec = w + ((size_t)t * nb + b0) * kRecordBytes;
-    for (int b = b0; b < b1; ++b, rec += kRecordBytes) {
-        const Unit u0 = load_unit(rec + lane * 12);
-        const Unit u1 = load_unit(rec + kUnitHalfBytes + lane * 12);
-        const uint32_t dh = *reinterpret_cast<const uint16_t*>(rec + 2 * kUnitHalfBytes + 2 * n);
-        half8_t A0[4], A1[4];
-        const half8_t* xb = x16 + (size_t)b * 64 + g * 2 + n;
+    // Table (and staged activation) loads go out first so the LDS writes
+    // that need them do not also wait for the record ring issued after them.
+    constexpr int kTblPerThread = kGridTableBytes / 16 / kThreads;
+    u32x4_t tv[kTblPerThread];
 #pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            A0[l] = a_lane ? xb[(0 * 4 + l) * 8] : zero8;
-            A1[l] = a_lane ? xb[(1 * 4 + l) * 8] : zero8;
-        }
-        float4_t D = {0.0f, 0.0f, 0.0f, 0.0f};
-        D = unit_mfma(tbl, u0, A0, D);
-        D = unit_mfma(tbl, u1, A1, D);
-        const float d4 = f16_bits_to_f32(dh) * 0.25f;
-        acc += d4 * (D[0] + D[1]);
+    for (int i = 0; i < kTblPerThread; ++i) tv[i] = args.table[tid + i * kThreads];
+    constexpr int kXPerThread = STAGE ? (kMvMaxStageNb * 64 + kThreads - 1) / kThreads : 1;
+    u32x4_t xv[kXPerThread];
+    const int nchunk = nb * 64;
+    if (STAGE) {
+        const u32x4_t* src = reinterpret_cast<const u32x4_t*>(act);
+#pragma unroll
+        for (int i = 0; i < kXPerThread; ++i) xv[i] = src[min(tid + i * kThreads, nchunk - 1)];
     }
-    if (g == 0) red[wave][n] = acc;
-    __syncthreads();
-    if (wave == 0 && g == 0) {
-        float s = 0.0f;
+    float xsc_v = 0.0f;
+    if (STAGE && tid < nb) xsc_v = xsc_g[tid];
+
+    // Tiles are dealt round-robin over the grid (tile' = blockIdx + k*G, tile'
+    // counting the tensors' tiles in order) and, inside a workgroup, records
+    // round-robin over its wavefronts, so at any moment the whole GPU reads
+    // one contiguous window of the weights rather than one chunk per CU.
+    const int T_all = args.n_tiles * args.n_tensors;
+    const int G = gridDim.x;
+    const int my_tiles = (T_all - (int)blockIdx.x + G - 1) / G;
+    bool first = true;
+    for (int k0 = 0; k0 < my_tiles; k0 += kMvMaxR) {
+        const int nt = min(kMvMaxR, my_tiles - k0);
+        const int P = nt * nb;
+        auto rec_ptr = [&](int p) -> const uint8_t* {
+            const int kt = p / nb;
+            const int tp = (int)blockIdx.x + (k0 + kt) * G;
+            const int ten = tp >= args.n_tiles ? 1 : 0;
+            const int t = tp - ten * args.n_tiles;
+            return args.w[ten] + ((size_t)t * nb + (p - kt * nb)) * kRecordBytes;
+        };
+
+        // Ring loads are unconditional: past the wave's records they re-read
+        // the round's last record (valid, cache-resident), so no load waits
+        // on a branch.
+        Rec buf[PF];
 #pragma unroll
-        for (int v = 0; v < kMatvecWaves; ++v) s += red[v][n];
-        const int row = (int)blockIdx.x * 16 + n;
-        if (row < out_dim) y[row] = s * xscale[0];
+        for (int s = 0; s < PF; ++s) load_rec(buf[s], rec_ptr(min(wave + s * WAVES, P - 1)), lane, n);
+
+        if (first) {
+#pragma unroll
+            for (int i = 0; i < kTblPerThread; ++i) reinterpret_cast<u32x4_t*>(tbl)[tid + i * kThreads] = tv[i];
+            if (STAGE) {
+#pragma unroll
+                for (int i = 0; i < kXPerThread; ++i)
+                    if (tid + i * kThreads < nchunk) reinterpret_cast<u32x4_t*>(xs)[tid + i * kThreads] = xv[i];
+                if (tid < nb) xsc[tid] = xsc_v;
+                if (tid < kZeroBytes / 16) {
+                    const u32x4_t z = {0u, 0u, 0u, 0u};
+                    reinterpret_cast<u32x4_t*>(lds + kZeroOff)[tid] = z;
+                }
+            }
+            for (int i = tid; i < kMvMaxR * WAVES * 16; i += kThreads) (&red[0][0][0])[i] = 0.0f;
+            first = false;
+            lds_barrier();
+        }
+
+        int tl = wave / nb, b = wave - (wave / nb) * nb;  // (tile, block) of record p
+        float acc = 0.0f;
+        for (int i = 0; wave + i * WAVES < P; i += PF) {
+#pragma unroll
+            for (int s = 0; s < PF; ++s) {
+                const int p = wave + (i + s) * WAVES;
+                if (p < P) {
+                    const float xsb = STAGE ? xsc[b] : xsc_g[b];
+                    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)buf[s].u[6]);
+                    const float d4 = d * 0.25f * xsb;
+                    acc = record_dot<STAGE>(tbl, buf[s], lb, a_lane ? xs + b * 1024 + a_lane_off : lds + kZeroOff,
+                                            reinterpret_cast<const half8_t*>(act + (size_t)b * 1024 + a_lane_off),
+                                            a_lane, d4, acc);
+                    // refill unconditionally (clamped like the prologue) so the
+                    // slot has one live copy
+                    load_rec(buf[s], rec_ptr(min(p + PF * WAVES, P - 1)), lane, n);
+                    // keep records from interleaving: the ring, not the
+                    // scheduler, provides the overlap, and registers stay at
+                    // ring + one record's temporaries
+                    __builtin_amdgcn_sched_barrier(0);
+                    // next record of this wave: flush the partial on a tile change
+                    int nb_ = b + WAVES, ntl = tl;
+                    while (nb_ >= nb) {
+                        nb_ -= nb;
+                        ++ntl;
+                    }
+                    if (ntl != tl || p + WAVES >= P) {
+                        float v = acc + __shfl_xor(acc, 16);
+                        v += __shfl_xor(v, 32);
+                        if (g == 0) red[tl][wave][n] = v;
+                        acc = 0.0f;
+                    }
+                    tl = ntl;
+                    b = nb_;
+                }
+            }
+        }
+        lds_barrier();
+        // sum the wavefront partials in a fixed order; the reader re-zeroes
+        // its slots for the next round
+        if (tid < nt * 16) {
+            const int tt = tid >> 4, nn = tid & 15;
+            float sum = 0.0f;
+#pragma unroll
+            for (int v = 0; v < WAVES; ++v) {
+                sum += red[tt][v][nn];
+                red[tt][v][nn] = 0.0f;
+            }
+            const int tp = (int)blockIdx.x + (k0 + tt) * G;
+            const int ten = tp >= args.n_tiles ? 1 : 0;
+            const int row = (tp - ten * args.n_tiles) * 16 + nn;
+            if (row < args.out_dim) args.y[ten][row] = sum;
+        }
+        lds_barrier();
     }
 }
 
@@ -222,34 +374,71 @@ __global__ __launch_bounds__(256) void k_matvec_raw(const uint8_t* __restrict__ 
 
 }  // namespace
 
-size_t prep_x_bytes(int n_tok, int in_dim) {
-    return (size_t)n_tok * (size_t)in_dim * 4 + 256;
+size_t act_bytes(int in_dim) {
+    // fp16 hi/lo operand (4 bytes per element) + one fp32 unscale per block,
+    // rounded up to 256 bytes
+    const size_t b = (size_t)in_dim * 4 + (size_t)(in_dim / kQK) * 4;
+    return (b + 255) / 256 * 256;
 }
 
-hipError_t launch_prep_x(const float* x, int n_tok, int in_dim, uint32_t* x16, float* xscale,
-                         hipStream_t s) {
-    hipLaunchKernelGGL(k_prep_x<0>, dim3(n_tok), dim3(256), 0, s, x, nullptr, 0.0f, in_dim,
-                       reinterpret_cast<_Float16*>(x16), xscale);
-    return hipGetLastError();
-}
-
-hipError_t launch_prep_swiglu(const float* g, const float* u, float lim, int n_tok, int in_dim,
-                              uint32_t* x16, float* xscale, hipStream_t s) {
-    hipLaunchKernelGGL(k_prep_x<1>, dim3(n_tok), dim3(256), 0, s, g, u, lim, in_dim,
-                       reinterpret_cast<_Float16*>(x16), xscale);
-    return hipGetLastError();
-}
-
-hipError_t launch_matvec_t16(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
-                             const uint32_t* x16, const float* xscale, float* y,
-                             const void* sign_table, hipStream_t s) {
+hipError_t launch_prep_act(const float* x, int in_dim, uint8_t* act, hipStream_t s) {
     const int nb = in_dim / kQK;
-    const int tiles = (out_dim + kTileRows - 1) / kTileRows;
-    hipLaunchKernelGGL(k_matvec_t16, dim3(tiles), dim3(kMatvecWaves * 64), 0, s, w, nb,
-                       (long long)(row0 / kTileRows), out_dim,
-                       reinterpret_cast<const half8_t*>(x16), xscale, y,
-                       reinterpret_cast<const u32x4_t*>(sign_table));
+    hipLaunchKernelGGL(k_prep_act<0>, dim3((nb + 3) / 4), dim3(256), 0, s, x, nullptr, 0.0f, nb,
+                       reinterpret_cast<_Float16*>(act), reinterpret_cast<float*>(act + (size_t)in_dim * 4));
     return hipGetLastError();
+}
+
+hipError_t launch_prep_swiglu(const float* g, const float* u, float lim, int in_dim, uint8_t* act,
+                              hipStream_t s) {
+    const int nb = in_dim / kQK;
+    hipLaunchKernelGGL(k_prep_act<1>, dim3((nb + 3) / 4), dim3(256), 0, s, g, u, lim, nb,
+                       reinterpret_cast<_Float16*>(act), reinterpret_cast<float*>(act + (size_t)in_dim * 4));
+    return hipGetLastError();
+}
+
+// Launch configuration: activation staged in LDS (K <= 16384), 16 wavefronts
+// per workgroup, 8-record ring, one workgroup per CU.
+#ifndef MV_STAGE
+#define MV_STAGE 1
+#endif
+#ifndef MV_WAVES
+#define MV_WAVES 16
+#endif
+#ifndef MV_PF
+#define MV_PF 8
+#endif
+#ifndef MV_WG_PER_CU
+#define MV_WG_PER_CU 1
+#endif
+
+template <bool STAGE, int WAVES, int PF>
+static hipError_t launch_cfg(const MvArgs& a, int slots, hipStream_t s) {
+    const int total = a.n_tiles * a.n_tensors;
+    const int grid = total < slots ? total : slots;
+    hipLaunchKernelGGL((k_matvec_t16<STAGE, WAVES, PF>), dim3(grid), dim3(WAVES * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_t16(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
+                             unsigned long long row0, int out_dim, const uint8_t* act,
+                             const void* grid_table, int num_cus, hipStream_t s) {
+    MvArgs a;
+    a.nb = in_dim / kQK;
+    const size_t skip = (size_t)(row0 / kTileRows) * a.nb * kRecordBytes;
+    for (int i = 0; i < 2; ++i) {
+        const int k = i < n_tensors ? i : 0;
+        a.w[i] = w[k] + skip;
+        a.y[i] = y[k];
+    }
+    a.n_tensors = n_tensors;
+    a.n_tiles = (out_dim + kTileRows - 1) / kTileRows;
+    a.out_dim = out_dim;
+    a.act = act;
+    a.table = reinterpret_cast<const u32x4_t*>(grid_table);
+    const int cus = num_cus > 0 ? num_cus : 256;
+    if (MV_STAGE && a.nb <= kMvMaxStageNb)
+        return launch_cfg<(MV_STAGE != 0), MV_WAVES, MV_PF>(a, cus * MV_WG_PER_CU, s);
+    return launch_cfg<false, MV_WAVES, MV_PF>(a, cus * MV_WG_PER_CU, s);
 }
 
 hipError_t launch_matvec_raw(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,

@@ -70,10 +70,10 @@ int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_s
 /* ---- weight residency (replaces weights.cpp:62-84 pin_nonexpert/payload) */
 
 /* Host-only layout introspection (no device use; no reference counterpart):
- * the 64 KiB signed lookup table the kernels keep in LDS (32768 fp16 bit
+ * the 64 KiB replicated grid table the kernels keep in LDS (32768 fp16 bit
  * patterns; returns GPEED_ERR_INVALID if n < 32768), and the T16 sign/scale
  * word made from a GGUF aux word. Lets CPU tests model the GPU decode. */
-int gpeed_t16_sign_table(uint16_t* out, size_t n);
+int gpeed_t16_grid_table(uint16_t* out, size_t n);
 uint32_t gpeed_t16_aux_word(uint32_t gguf_aux);
 
 /* GGUF rows -> T16 copy (same bytes per weight) / back. */
@@ -107,6 +107,11 @@ int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, float li
                              size_t act_bytes, gpeed_stream_t stream);
 int gpeed_iq3xxs_matvec_act(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim,
                             int out_dim, const void* act, float* dst, gpeed_stream_t stream);
+/* Two same-shape tensors against one prepared activation in one launch
+ * (gate and up of model.cpp:681-682, or of the shared expert at 747-748). */
+int gpeed_iq3xxs_matvec2_act(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0,
+                             int in_dim, int out_dim, const void* act, float* dst_a, float* dst_b,
+                             gpeed_stream_t stream);
 
 /* Same product straight from GGUF rows (no tiling; any row0). */
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,

@@ -3,9 +3,9 @@
 * libgpeed_iq3.so loads and exports every entry point include/gpeed_iq3.h declares;
 * host-only geometry and layout helpers answer correctly;
 * a numpy model of the GPU decode (T16 unit -> perm addresses -> the library's
-  own 64 KiB LDS table -> (2s+1) -> d/4) reproduces the oracle's dequantized
-  weights bit for bit, so the layout and table are right before any kernel
-  runs.
+  own 64 KiB replicated LDS table -> sign bits from the T16 word -> (2s+1)d/4)
+  reproduces the oracle's dequantized weights bit for bit, so the layout and
+  table are right before any kernel runs.
 """
 import ctypes as C
 import os
@@ -47,15 +47,14 @@ def test_geometry():
 
 
 def aux_t16_model(aux):
-    """T16 sign/scale word, restated from the layout definition."""
-    out = 0
+    """T16 sign/scale word, restated bit by bit from the layout definition:
+    sign j (< 7) of group l at bit 15-k (j even) or 31-k (j odd), k = 4(j//2)+l;
+    the scale nibble at bits 16..19."""
+    out = ((aux >> 28) & 15) << 16
     for l in range(4):
-        s7 = (aux >> (7 * l)) & 127
-        s = [(s7 >> i) & 1 for i in range(7)]
-        t3 = s[0] ^ s[1] ^ s[2] ^ s[3]
-        b = s[0] | s[1] << 1 | s[2] << 2 | t3 << 3 | s[4] << 4 | s[5] << 5 | s[6] << 6
-        b |= ((aux >> (28 + l)) & 1) << 7
-        out |= b << (8 * l)
+        for j in range(7):
+            k = 4 * (j // 2) + l
+            out |= ((aux >> (7 * l + j)) & 1) << (31 - k if j & 1 else 15 - k)
     return out
 
 
@@ -66,15 +65,52 @@ def test_aux_word_matches_model():
         assert L.gpeed_t16_aux_word(w) == aux_t16_model(w), hex(w)
 
 
+def test_aux_word_is_a_bijection_on_used_bits():
+    """Every one of the 32 aux bits lands on a distinct T16 bit."""
+    L = gpeed_amd.lib()
+    seen = 0
+    for b in range(32):
+        t = L.gpeed_t16_aux_word(1 << b)
+        assert t and (t & (t - 1)) == 0, b
+        assert not (seen & t), b
+        seen |= t
+    assert seen == 0xFFFFFFFF
+
+
 @pytest.fixture(scope="module")
-def sign_table():
+def grid_table():
     t = np.empty(32768, np.uint16)
-    assert gpeed_amd.lib().gpeed_t16_sign_table(t.ctypes.data, t.size) == 0
-    assert gpeed_amd.lib().gpeed_t16_sign_table(t.ctypes.data, 100) != 0
-    return t.view(np.float16)
+    assert gpeed_amd.lib().gpeed_t16_grid_table(t.ctypes.data, t.size) == 0
+    assert gpeed_amd.lib().gpeed_t16_grid_table(t.ctypes.data, 100) != 0
+    return t
 
 
-def test_decode_model_matches_oracle(sign_table):
+def full_signs_model(w):
+    """The kernel's sign word: implied 8th signs (even parity per group) folded
+    in over the scale nibble with three xor-folds (t16_full_signs)."""
+    m = w & 0xFFF0FFFF
+    t = m ^ (m >> 16)
+    t ^= t >> 8
+    t ^= t >> 4
+    return m | ((t & 15) << 16)
+
+
+def test_grid_table_replicas_conflict_free(grid_table):
+    """Each lane's 8-byte entry for any index sits in its own bank pair among
+    the 32 lanes of an LDS pass (64 banks x 4 B)."""
+    for idx in (0, 1, 77, 255):
+        banks = [(((idx << 8) | (lane << 3)) // 4) % 64 for lane in range(32)]
+        assert len(set(banks)) == 32
+        ref = grid_table[(idx << 8) // 2: (idx << 8) // 2 + 4]
+        for lane in range(32):
+            a = ((idx << 8) | (lane << 3)) // 2
+            assert np.array_equal(grid_table[a: a + 4], ref)
+    assert not (grid_table & 0x8000).any()  # unsigned entries
+
+
+def test_decode_model_matches_oracle(grid_table):
+    """T16 unit -> v_perm addresses -> replicated table -> sign insertion ->
+    db = (2s+1) * d/4: bit-exact with the oracle's dequantized weights."""
     L = gpeed_amd.lib()
     blocks = synth.iq3xxs_blocks(5, 0, 48)
     want = oracle.dequantize(blocks, 48 * 256).reshape(48, 256)
@@ -83,20 +119,22 @@ def test_decode_model_matches_oracle(sign_table):
         aux = np.frombuffer(raw[66:98].tobytes(), "<u4")
         got = np.empty(256, np.float32)
         for ib in range(8):
-            a = L.gpeed_t16_aux_word(int(aux[ib]))
+            lane = (7 * bi + 13 * ib) % 64
+            lb = (lane & 31) << 3
+            w = L.gpeed_t16_aux_word(int(aux[ib]))
+            sw = full_signs_model(w)
+            s = (w >> 16) & 15
+            db = np.float32(2 * s + 1) * (d * np.float32(0.25))
             q = raw[2 + 8 * ib: 10 + 8 * ib]
-            cb1 = (a << 3) & 0x78787878
-            cb2 = (a & 0x78787878) | 0x80808080
-            s = sum(((a >> (8 * l + 7)) & 1) << l for l in range(4))
-            assert s == int(aux[ib]) >> 28
-            f = np.float16(2 * s + 1)
             for l in range(4):
-                a1 = (int(q[2 * l]) << 8) | ((cb1 >> (8 * l)) & 255)
-                a2 = (int(q[2 * l + 1]) << 8) | ((cb2 >> (8 * l)) & 255)
-                v = np.concatenate([sign_table[a1 // 2: a1 // 2 + 4], sign_table[a2 // 2: a2 // 2 + 4]])
-                vf = (v * f).astype(np.float16)  # exact: |q*(2s+1)| <= 1922
-                assert np.array_equal(vf.astype(np.float64), v.astype(np.float64) * (2 * s + 1))
-                got[32 * ib + 8 * l: 32 * ib + 8 * l + 8] = vf.astype(np.float32) * (d * np.float32(0.25))
+                h = np.empty(8, np.uint16)
+                for half in range(2):
+                    a = ((int(q[2 * l + half]) << 8) | lb) // 2
+                    h[4 * half: 4 * half + 4] = grid_table[a: a + 4]
+                for e in range(8):
+                    k = 4 * (e // 2) + l
+                    h[e] |= ((sw >> (31 - k if e & 1 else 15 - k)) & 1) << 15
+                got[32 * ib + 8 * l: 32 * ib + 8 * l + 8] = h.view(np.float16).astype(np.float32) * db
         assert np.array_equal(got.view(np.uint32), want[bi].view(np.uint32)), bi
 
 

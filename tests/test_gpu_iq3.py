@@ -140,6 +140,31 @@ def test_matvec_activation_range(gpu, scale):
     assert e < TIGHT, e
 
 
+@pytest.mark.parametrize("n_rows,in_dim,row0,out_dim", [
+    (48, 20480, 16, 32),      # 80 blocks: activation read from global memory
+    (33000, 256, 0, 33000),   # 2063 tiles: more groups than workgroups, groups loop
+])
+def test_matvec_large_k_and_many_tiles(gpu, n_rows, in_dim, row0, out_dim):
+    w = synth.iq3xxs_matrix(59, 0, n_rows, in_dim)
+    x = synth.normal(59, 1, in_dim)
+    y = run_matvec(gpu, w, n_rows, in_dim, row0, out_dim, x)
+    e = rel_err(y, oracle.matvec(w, row0, in_dim, out_dim, x))
+    assert e < TIGHT, e
+
+
+def test_matvec2_shared_activation(gpu):
+    n_rows, in_dim = 200, 1536
+    wa = synth.iq3xxs_matrix(60, 0, n_rows, in_dim)
+    wb = synth.iq3xxs_matrix(60, 1, n_rows, in_dim)
+    x = synth.normal(60, 2, in_dim)
+    ta = G.tile(dev(wa.reshape(-1), gpu), n_rows, in_dim)
+    tb = G.tile(dev(wb.reshape(-1), gpu), n_rows, in_dim)
+    act = G.prep_act(dev(x, gpu), G.act_buffer(in_dim, gpu))
+    ya, yb = G.matvec2_act(ta, tb, n_rows, 16, in_dim, 180, act)
+    assert rel_err(host(ya), oracle.matvec(wa, 16, in_dim, 180, x)) < TIGHT
+    assert rel_err(host(yb), oracle.matvec(wb, 16, in_dim, 180, x)) < TIGHT
+
+
 def test_matvec_zero_activation(gpu):
     w = synth.iq3xxs_matrix(52, 0, 32, 512)
     y = run_matvec(gpu, w, 32, 512, 0, 32, np.zeros(512, np.float32))
@@ -201,8 +226,9 @@ def test_dense_mlp_step(gpu):
     tg, tu, td = (G.tile(dev(a.reshape(-1), gpu), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I)))
     act = G.act_buffer(H, gpu)
     G.prep_act(dev(x, gpu), act)
-    g = G.matvec_act(tg, I, 0, H, I, act)
-    u = G.matvec_act(tu, I, 0, H, I, act)
+    g, u = G.matvec2_act(tg, tu, I, 0, H, I, act)
+    assert rel_err(host(g), oracle.matvec(wg, 0, H, I, x)) < TIGHT
+    assert rel_err(host(u), oracle.matvec(wu, 0, H, I, x)) < TIGHT
     act2 = G.act_buffer(I, gpu)
     G.prep_swiglu(g, u, act2, 10.0)
     y = host(G.matvec_act(td, H, 0, I, H, act2))
