@@ -11,7 +11,7 @@ the 256 MB Infinity Cache, `--copies` distinct copies of the three tensors
 (default 8, 694 MB) are rotated step by step.
 
 value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
-roofline = the matvec kernel (k_matvec_t16, launched once for gate+up and
+roofline = the GEMV kernel (k_gemv_t64, launched once for gate+up and
 once for down per step): algorithmic bytes of its launches (packed W +
 prepared activation + outputs) / their summed duration, each launch timed
 with HIP events on the launch stream during the timed steps, against 8 TB/s.
@@ -133,11 +133,13 @@ def main():
     base = [G.tile(torch.from_numpy(a.reshape(-1)).to(dev), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I))]
     copies = [base] + [[t.clone() for t in base] for _ in range(args.copies - 1)]
     xd = torch.from_numpy(x).to(dev)
-    act = G.act_buffer(H, dev)
-    act2 = G.act_buffer(I, dev)
-    g = torch.empty(I, device=dev)
-    u = torch.empty(I, device=dev)
-    y = torch.empty(H, device=dev)
+    act = G.act_buffer(H, 1, dev)
+    act2 = G.act_buffer(I, 1, dev)
+    ws_gu = G.gemv_workspace(H, I, 1, 2, dev)
+    ws_d = G.gemv_workspace(I, H, 1, 1, dev)
+    g = torch.empty(1, I, device=dev)
+    u = torch.empty(1, I, device=dev)
+    y = torch.empty(1, H, device=dev)
     stream = torch.cuda.current_stream()
 
     def timed_launch(ev, kind, fn):
@@ -154,9 +156,9 @@ def main():
     def step(c, ev=None):
         tg, tu, td = copies[c]
         G.prep_act(xd, act)
-        timed_launch(ev, "gate+up", lambda: G.matvec2_act(tg, tu, I, 0, H, I, act, out_a=g, out_b=u))
+        timed_launch(ev, "gate+up", lambda: G.gemv2_act(tg, tu, I, 0, H, I, act, 1, out_a=g, out_b=u, ws=ws_gu))
         G.prep_swiglu(g, u, act2, SWIGLU_LIMIT)
-        timed_launch(ev, "down", lambda: G.matvec_act(td, H, 0, I, H, act2, out=y))
+        timed_launch(ev, "down", lambda: G.gemv_act(td, H, 0, I, H, act2, 1, out=y, ws=ws_d))
 
     log("warmup")
     for i in range(args.warmup):
@@ -164,7 +166,7 @@ def main():
     torch.cuda.synchronize()
     step(0)
     torch.cuda.synchronize()
-    y_gpu = y.cpu().numpy().copy()
+    y_gpu = y.cpu().numpy()[0].copy()
 
     log("timed")
     ev = []
@@ -177,8 +179,8 @@ def main():
     t1.record(stream)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
-    # k_matvec_t16 launches: bytes = packed W + prepared activation + outputs
-    act_bytes = {"gate+up": G.lib().gpeed_iq3xxs_act_bytes(H), "down": G.lib().gpeed_iq3xxs_act_bytes(I)}
+    # k_gemv_t64 launches: bytes = packed W + prepared activation + outputs
+    act_bytes = {"gate+up": G.lib().gpeed_iq3xxs_act_bytes(H, 1), "down": G.lib().gpeed_iq3xxs_act_bytes(I, 1)}
     launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + act_bytes["gate+up"] + 2 * I * 4,
                     "down": W_BYTES // 3 + act_bytes["down"] + H * 4}
     per_kind = {}
@@ -212,7 +214,7 @@ def main():
                    "packed_weight_bytes_per_step": W_BYTES, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_matvec_t16", "launch_kinds": kinds},
+                     "kernel": "k_gemv_t64", "launch_kinds": kinds},
     }
     if not args.no_cpu:
         log("cpu baseline")

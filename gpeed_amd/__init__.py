@@ -27,7 +27,7 @@ ERRORS = {
     -3: "row not block aligned",
     -4: "dtype not implemented on the GPU path",
     -5: "HIP error",
-    -6: "T16 operand off a 16-row tile boundary",
+    -6: "T64 operand off a 64-row tile boundary",
     -7: "workspace missing or too small",
     -8: "no HIP device",
 }
@@ -59,20 +59,23 @@ def lib():
             "gpeed_init": ([], i32),
             "gpeed_last_error": ([], C.c_char_p),
             "gpeed_iq3xxs_row_bytes": ([i64], sz),
-            "gpeed_iq3xxs_t16_bytes": ([u64, i64], sz),
+            "gpeed_iq3xxs_t64_bytes": ([u64, i64], sz),
             "gpeed_dequantize": ([i32, vp, vp, u64, vp], i32),
-            "gpeed_t16_grid_table": ([vp, sz], i32),
-            "gpeed_t16_aux_word": ([C.c_uint32], C.c_uint32),
+            "gpeed_t64_grid_table": ([vp, sz], i32),
+            "gpeed_t64_aux_word": ([C.c_uint32], C.c_uint32),
             "gpeed_iq3xxs_tile": ([vp, u64, i64, vp, vp], i32),
             "gpeed_iq3xxs_untile": ([vp, u64, i64, vp, vp], i32),
-            "gpeed_iq3xxs_matvec_ws_bytes": ([i64], sz),
+            "gpeed_iq3xxs_matvec_ws_bytes": ([i64, i64], sz),
+            "gpeed_iq3xxs_matmul_ws_bytes": ([i64, i64, i32], sz),
             "gpeed_iq3xxs_matvec": ([vp, u64, u64, i32, i32, vp, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_matmul": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_matvec_raw": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
-            "gpeed_iq3xxs_act_bytes": ([i64], sz),
-            "gpeed_iq3xxs_prep_act": ([vp, i64, vp, sz, vp], i32),
-            "gpeed_iq3xxs_prep_swiglu": ([vp, vp, i64, C.c_float, vp, sz, vp], i32),
-            "gpeed_iq3xxs_matvec_act": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
-            "gpeed_iq3xxs_matvec2_act": ([vp, vp, u64, u64, i32, i32, vp, vp, vp, vp], i32),
+            "gpeed_iq3xxs_act_bytes": ([i64, i32], sz),
+            "gpeed_iq3xxs_prep_act": ([vp, i64, i32, vp, sz, vp], i32),
+            "gpeed_iq3xxs_prep_swiglu": ([vp, vp, i64, i32, C.c_float, vp, sz, vp], i32),
+            "gpeed_iq3xxs_gemv_ws_bytes": ([i32, i64, i64, i32], sz),
+            "gpeed_iq3xxs_gemv_act": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_gemv2_act": ([vp, vp, u64, u64, i32, i32, vp, i32, vp, vp, vp, sz, vp], i32),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -139,8 +142,8 @@ def row_bytes(in_dim: int) -> int:
     return lib().gpeed_iq3xxs_row_bytes(in_dim)
 
 
-def t16_bytes(n_rows: int, in_dim: int) -> int:
-    return lib().gpeed_iq3xxs_t16_bytes(n_rows, in_dim)
+def t64_bytes(n_rows: int, in_dim: int) -> int:
+    return lib().gpeed_iq3xxs_t64_bytes(n_rows, in_dim)
 
 
 def dequantize(raw, n: int, out=None, dtype: int = DTYPE_IQ3_XXS, stream=None):
@@ -154,82 +157,123 @@ def dequantize(raw, n: int, out=None, dtype: int = DTYPE_IQ3_XXS, stream=None):
 
 
 def tile(raw, n_rows: int, in_dim: int, out=None, stream=None):
-    """T16 copy of [n_rows, in_dim] GGUF rows held on the device."""
+    """T64 copy of [n_rows, in_dim] GGUF rows held on the device."""
     torch = _torch()
     _require_cuda(raw)
     if out is None:
-        out = torch.empty(t16_bytes(n_rows, in_dim), dtype=torch.uint8, device=raw.device)
+        out = torch.empty(t64_bytes(n_rows, in_dim), dtype=torch.uint8, device=raw.device)
     _check(lib().gpeed_iq3xxs_tile(_ptr(raw), n_rows, in_dim, _ptr(out), _stream(stream)), "tile")
     return out
 
 
-def untile(t16, n_rows: int, in_dim: int, out=None, stream=None):
+def untile(t64, n_rows: int, in_dim: int, out=None, stream=None):
     torch = _torch()
-    _require_cuda(t16)
+    _require_cuda(t64)
     if out is None:
-        out = torch.empty(n_rows * row_bytes(in_dim), dtype=torch.uint8, device=t16.device)
-    _check(lib().gpeed_iq3xxs_untile(_ptr(t16), n_rows, in_dim, _ptr(out), _stream(stream)), "untile")
+        out = torch.empty(n_rows * row_bytes(in_dim), dtype=torch.uint8, device=t64.device)
+    _check(lib().gpeed_iq3xxs_untile(_ptr(t64), n_rows, in_dim, _ptr(out), _stream(stream)), "untile")
     return out
 
 
-def matvec_workspace(in_dim: int, device="cuda"):
+def _zeros(nbytes: int, device):
+    """Zero-filled device buffer; a size the library rejects (0) still gets a
+    small buffer so that the call itself reports why."""
     torch = _torch()
-    return torch.empty(lib().gpeed_iq3xxs_matvec_ws_bytes(in_dim), dtype=torch.uint8, device=device)
+    return torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
-def matvec(w_t16, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None, ws=None, stream=None):
-    """dst = W[row0:row0+out_dim] @ x from a T16 tensor (batch 1, fp32)."""
+def matmul_workspace(in_dim: int, out_dim: int, n_tok: int = 1, device="cuda"):
+    """Zero-filled workspace for matvec / matmul (reusable, one per stream)."""
+    return _zeros(lib().gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, n_tok), device)
+
+
+def matvec_workspace(in_dim: int, out_dim: int, device="cuda"):
+    return matmul_workspace(in_dim, out_dim, 1, device)
+
+
+def matvec(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None, ws=None, stream=None):
+    """dst = W[row0:row0+out_dim] @ x from a T64 tensor (batch 1, fp32)."""
     torch = _torch()
-    _require_cuda(w_t16, x)
+    _require_cuda(w_t64, x)
     if out is None:
         out = torch.empty(out_dim, dtype=torch.float32, device=x.device)
     if ws is None:
-        ws = matvec_workspace(in_dim, x.device)
-    _check(lib().gpeed_iq3xxs_matvec(_ptr(w_t16), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out),
+        ws = matvec_workspace(in_dim, out_dim, x.device)
+    _check(lib().gpeed_iq3xxs_matvec(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out),
                                      _ptr(ws), ws.numel(), _stream(stream)), "matvec")
     return out
 
 
-def act_buffer(in_dim: int, device="cuda"):
-    """Device buffer for one prepared activation (fp16 hi/lo operand + scale)."""
+def matmul(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None, ws=None, stream=None):
+    """Y[t] = W[row0:row0+out_dim] @ X[t] for X [n_tok, in_dim] fp32; Y [n_tok, out_dim]."""
     torch = _torch()
-    return torch.empty(lib().gpeed_iq3xxs_act_bytes(in_dim), dtype=torch.uint8, device=device)
+    _require_cuda(w_t64, X)
+    n_tok = X.shape[0] if X.dim() == 2 else 1
+    if out is None:
+        out = torch.empty(n_tok, out_dim, dtype=torch.float32, device=X.device)
+    if ws is None:
+        ws = matmul_workspace(in_dim, out_dim, n_tok, X.device)
+    _check(lib().gpeed_iq3xxs_matmul(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(X), n_tok, _ptr(out),
+                                     _ptr(ws), ws.numel(), _stream(stream)), "matmul")
+    return out
+
+
+def act_buffer(in_dim: int, n_tok: int = 1, device="cuda"):
+    """Device buffer for n_tok prepared activations (fp16 hi/lo operand + scales)."""
+    torch = _torch()
+    return torch.empty(lib().gpeed_iq3xxs_act_bytes(in_dim, n_tok), dtype=torch.uint8, device=device)
+
+
+def gemv_workspace(in_dim: int, out_dim: int, n_tok: int = 1, n_tensors: int = 1, device="cuda"):
+    """Zero-filled GEMV workspace (shared-tile partials and tickets), one per stream."""
+    return _zeros(lib().gpeed_iq3xxs_gemv_ws_bytes(n_tensors, in_dim, out_dim, n_tok), device)
 
 
 def prep_act(x, act, stream=None):
+    """Prepare x ([in_dim] or [n_tok, in_dim], fp32) into act."""
     _require_cuda(x, act)
-    _check(lib().gpeed_iq3xxs_prep_act(_ptr(x), x.numel(), _ptr(act), act.numel(), _stream(stream)), "prep_act")
+    n_tok = x.shape[0] if x.dim() == 2 else 1
+    _check(lib().gpeed_iq3xxs_prep_act(_ptr(x), x.shape[-1], n_tok, _ptr(act), act.numel(), _stream(stream)),
+           "prep_act")
     return act
 
 
 def prep_swiglu(g, u, act, limit: float = 10.0, stream=None):
     _require_cuda(g, u, act)
-    _check(lib().gpeed_iq3xxs_prep_swiglu(_ptr(g), _ptr(u), g.numel(), limit, _ptr(act), act.numel(),
+    n_tok = g.shape[0] if g.dim() == 2 else 1
+    _check(lib().gpeed_iq3xxs_prep_swiglu(_ptr(g), _ptr(u), g.shape[-1], n_tok, limit, _ptr(act), act.numel(),
                                           _stream(stream)), "prep_swiglu")
     return act
 
 
-def matvec_act(w_t16, n_rows: int, row0: int, in_dim: int, out_dim: int, act, out=None, stream=None):
+def gemv_act(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, act, n_tok: int = 1, out=None,
+             ws=None, stream=None):
+    """dst[t] = W[row0:row0+out_dim] @ x_t for the n_tok prepared vectors in act."""
     torch = _torch()
-    _require_cuda(w_t16, act)
+    _require_cuda(w_t64, act)
     if out is None:
-        out = torch.empty(out_dim, dtype=torch.float32, device=act.device)
-    _check(lib().gpeed_iq3xxs_matvec_act(_ptr(w_t16), n_rows, row0, in_dim, out_dim, _ptr(act), _ptr(out),
-                                         _stream(stream)), "matvec_act")
+        out = torch.empty(n_tok, out_dim, dtype=torch.float32, device=act.device)
+    if ws is None:
+        ws = gemv_workspace(in_dim, out_dim, n_tok, 1, act.device)
+    _check(lib().gpeed_iq3xxs_gemv_act(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(act), n_tok, _ptr(out),
+                                       _ptr(ws), ws.numel(), _stream(stream)), "gemv_act")
     return out
 
 
-def matvec2_act(w_a, w_b, n_rows: int, row0: int, in_dim: int, out_dim: int, act, out_a=None, out_b=None,
-                stream=None):
-    """Two same-shape T16 tensors against one prepared activation, one launch."""
+def gemv2_act(w_a, w_b, n_rows: int, row0: int, in_dim: int, out_dim: int, act, n_tok: int = 1, out_a=None,
+              out_b=None, ws=None, stream=None):
+    """Two same-shape T64 tensors against one prepared activation, one launch."""
     torch = _torch()
     _require_cuda(w_a, w_b, act)
     if out_a is None:
-        out_a = torch.empty(out_dim, dtype=torch.float32, device=act.device)
+        out_a = torch.empty(n_tok, out_dim, dtype=torch.float32, device=act.device)
     if out_b is None:
-        out_b = torch.empty(out_dim, dtype=torch.float32, device=act.device)
-    _check(lib().gpeed_iq3xxs_matvec2_act(_ptr(w_a), _ptr(w_b), n_rows, row0, in_dim, out_dim, _ptr(act),
-                                          _ptr(out_a), _ptr(out_b), _stream(stream)), "matvec2_act")
+        out_b = torch.empty(n_tok, out_dim, dtype=torch.float32, device=act.device)
+    if ws is None:
+        ws = gemv_workspace(in_dim, out_dim, n_tok, 2, act.device)
+    _check(lib().gpeed_iq3xxs_gemv2_act(_ptr(w_a), _ptr(w_b), n_rows, row0, in_dim, out_dim, _ptr(act), n_tok,
+                                        _ptr(out_a), _ptr(out_b), _ptr(ws), ws.numel(), _stream(stream)),
+           "gemv2_act")
     return out_a, out_b
 
 
@@ -248,10 +292,12 @@ class WeightStore:
     """Device-resident IQ3_XXS tensors behind the reference's matvec_quant contract.
 
     ``add(name, payload, in_dim, n_rows)`` uploads GGUF rows once and keeps
-    their T16 copy in HBM (the role of pin_nonexpert, weights.cpp:70-84).
+    their T64 copy in HBM (the role of pin_nonexpert, weights.cpp:70-84).
     ``matvec_quant`` follows weights.cpp:167-203: ``dst[j] = sum_i
-    W[row0+j][i] * x[i]`` for ``j < out_dim``; host numpy arrays in, host
-    numpy out (synchronous, like the reference), or device tensors in and out.
+    W[row0+j][i] * x[i]`` for ``j < out_dim``; ``matmul_quant`` follows
+    weights.cpp:86-165 (``Y[t][j]`` for ``t < n_tok``, nothing done when
+    ``n_tok <= 0`` or ``out_dim <= 0``). Host numpy arrays in, host numpy out
+    (synchronous, like the reference), or device tensors in and out.
     """
 
     def __init__(self, device="cuda"):
@@ -267,9 +313,9 @@ class WeightStore:
             raw = torch.from_numpy(np.ascontiguousarray(payload).reshape(-1).view(np.uint8)).to(self.device)
         else:
             raw = payload.reshape(-1)
-        t16 = tile(raw, n_rows, in_dim)
-        self.tensors[name] = (t16, in_dim, n_rows)
-        return t16
+        t64 = tile(raw, n_rows, in_dim)
+        self.tensors[name] = (t64, in_dim, n_rows)
+        return t64
 
     def has(self, name: str) -> bool:
         return name in self.tensors
@@ -281,20 +327,21 @@ class WeightStore:
             raise RuntimeError(f"weights: row not block aligned for {name}")
         return self.tensors[name]
 
-    def _workspace(self, in_dim: int):
-        ws = self._ws.get(in_dim)
+    def _workspace(self, in_dim: int, out_dim: int, n_tok: int):
+        key = (in_dim, out_dim, min(n_tok, 8))
+        ws = self._ws.get(key)
         if ws is None:
-            ws = self._ws[in_dim] = matvec_workspace(in_dim, self.device)
+            ws = self._ws[key] = matmul_workspace(in_dim, out_dim, n_tok, self.device)
         return ws
 
     def matvec_quant(self, name: str, row0: int, in_dim: int, out_dim: int, x, dst=None):
         torch = _torch()
-        t16, _, n_rows = self._get(name, in_dim)
+        t64, _, n_rows = self._get(name, in_dim)
         host = isinstance(x, np.ndarray)
         if out_dim <= 0:
             return dst
         xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(self.device) if host else x
-        yd = matvec(t16, n_rows, row0, in_dim, out_dim, xd, ws=self._workspace(in_dim))
+        yd = matvec(t64, n_rows, row0, in_dim, out_dim, xd, ws=self._workspace(in_dim, out_dim, 1))
         if host:
             y = yd.cpu().numpy()
             if dst is not None:
@@ -305,3 +352,23 @@ class WeightStore:
             dst.copy_(yd)
             return dst
         return yd
+
+    def matmul_quant(self, name: str, row0: int, in_dim: int, out_dim: int, X, n_tok: int, Y=None):
+        torch = _torch()
+        t64, _, n_rows = self._get(name, in_dim)
+        if n_tok <= 0 or out_dim <= 0:
+            return Y
+        host = isinstance(X, np.ndarray)
+        Xd = torch.from_numpy(np.ascontiguousarray(X, np.float32).reshape(n_tok, in_dim)).to(self.device) \
+            if host else X.reshape(n_tok, in_dim)
+        Yd = matmul(t64, n_rows, row0, in_dim, out_dim, Xd, ws=self._workspace(in_dim, out_dim, n_tok))
+        if host:
+            y = Yd.cpu().numpy()
+            if Y is not None:
+                Y.reshape(n_tok, out_dim)[:] = y
+                return Y
+            return y
+        if Y is not None:
+            Y.copy_(Yd.reshape(Y.shape))
+            return Y
+        return Yd

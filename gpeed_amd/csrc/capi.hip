@@ -25,36 +25,24 @@ int hip_fail(hipError_t e, const char* what) {
 constexpr int kMaxDevices = 64;
 std::mutex g_init_mu;
 struct DeviceState {
-    void* grid_table = nullptr;  // 64 KiB replicated grid table
-    int num_cus = 0;
+    int num_cus = 0;  // set once, read without the lock afterwards
 };
 DeviceState g_dev[kMaxDevices];
 
-// Per-device state, made once (hipMalloc + upload) and kept until exit.
+// Per-device launch parameters, read once per device.
 int device_state(const DeviceState** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     if (dev < 0 || dev >= kMaxDevices) return fail(GPEED_ERR_INVALID, "device index out of range");
     DeviceState& st = g_dev[dev];
-    if (!__atomic_load_n(&st.grid_table, __ATOMIC_ACQUIRE)) {
+    if (!__atomic_load_n(&st.num_cus, __ATOMIC_ACQUIRE)) {
         std::lock_guard<std::mutex> lk(g_init_mu);
-        if (!st.grid_table) {
+        if (!st.num_cus) {
             int cus = 0;
             e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
             if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
-            std::vector<uint16_t> host(gpeed::kGridTableBytes / 2);
-            gpeed::build_grid_table(host.data());
-            void* p = nullptr;
-            e = hipMalloc(&p, gpeed::kGridTableBytes);
-            if (e != hipSuccess) return hip_fail(e, "hipMalloc(grid table)");
-            e = hipMemcpy(p, host.data(), gpeed::kGridTableBytes, hipMemcpyHostToDevice);
-            if (e != hipSuccess) {
-                (void)hipFree(p);
-                return hip_fail(e, "hipMemcpy(grid table)");
-            }
-            st.num_cus = cus;
-            __atomic_store_n(&st.grid_table, p, __ATOMIC_RELEASE);
+            __atomic_store_n(&st.num_cus, cus > 0 ? cus : 1, __ATOMIC_RELEASE);
         }
     }
     *out = &st;
@@ -113,9 +101,9 @@ size_t gpeed_iq3xxs_row_bytes(int64_t in_dim) {
     return gpeed::iq3_row_bytes(in_dim);
 }
 
-size_t gpeed_iq3xxs_t16_bytes(uint64_t n_rows, int64_t in_dim) {
+size_t gpeed_iq3xxs_t64_bytes(uint64_t n_rows, int64_t in_dim) {
     if (in_dim <= 0 || in_dim % gpeed::kQK) return 0;
-    return gpeed::t16_bytes(n_rows, in_dim);
+    return gpeed::t64_bytes(n_rows, in_dim);
 }
 
 int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_stream_t stream) {
@@ -132,14 +120,14 @@ int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_s
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "dequantize launch");
 }
 
-int gpeed_t16_grid_table(uint16_t* out, size_t n) {
+int gpeed_t64_grid_table(uint16_t* out, size_t n) {
     if (!out || n < (size_t)gpeed::kGridTableBytes / 2)
-        return fail(GPEED_ERR_INVALID, "t16_grid_table: buffer smaller than 32768 entries");
+        return fail(GPEED_ERR_INVALID, "t64_grid_table: buffer smaller than 32768 entries");
     gpeed::build_grid_table(out);
     return GPEED_OK;
 }
 
-uint32_t gpeed_t16_aux_word(uint32_t gguf_aux) { return gpeed::aux_to_t16(gguf_aux); }
+uint32_t gpeed_t64_aux_word(uint32_t gguf_aux) { return gpeed::aux_to_t64(gguf_aux); }
 
 static int check_tile_args(const void* a, const void* b, int64_t in_dim, const char* who) {
     if (in_dim <= 0 || in_dim % gpeed::kQK)
@@ -149,128 +137,174 @@ static int check_tile_args(const void* a, const void* b, int64_t in_dim, const c
     return GPEED_OK;
 }
 
-int gpeed_iq3xxs_tile(const void* raw, uint64_t n_rows, int64_t in_dim, void* t16,
+int gpeed_iq3xxs_tile(const void* raw, uint64_t n_rows, int64_t in_dim, void* t64,
                       gpeed_stream_t stream) {
     if (n_rows == 0) return GPEED_OK;
-    int rc = check_tile_args(raw, t16, in_dim, "tile");
+    int rc = check_tile_args(raw, t64, in_dim, "tile");
     if (rc) return rc;
-    if (!aligned(raw, 2) || !aligned(t16, 16))
-        return fail(GPEED_ERR_INVALID, "tile: raw must be 2-byte and t16 16-byte aligned");
+    if (!aligned(raw, 2) || !aligned(t64, 16))
+        return fail(GPEED_ERR_INVALID, "tile: raw must be 2-byte and t64 16-byte aligned");
     hipError_t e = gpeed::launch_tile(static_cast<const uint8_t*>(raw), n_rows, (int)in_dim,
-                                      static_cast<uint8_t*>(t16), static_cast<hipStream_t>(stream));
+                                      static_cast<uint8_t*>(t64), static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "tile launch");
 }
 
-int gpeed_iq3xxs_untile(const void* t16, uint64_t n_rows, int64_t in_dim, void* raw,
+int gpeed_iq3xxs_untile(const void* t64, uint64_t n_rows, int64_t in_dim, void* raw,
                         gpeed_stream_t stream) {
     if (n_rows == 0) return GPEED_OK;
-    int rc = check_tile_args(t16, raw, in_dim, "untile");
+    int rc = check_tile_args(t64, raw, in_dim, "untile");
     if (rc) return rc;
-    if (!aligned(raw, 2) || !aligned(t16, 16))
-        return fail(GPEED_ERR_INVALID, "untile: raw must be 2-byte and t16 16-byte aligned");
-    hipError_t e = gpeed::launch_untile(static_cast<const uint8_t*>(t16), n_rows, (int)in_dim,
+    if (!aligned(raw, 2) || !aligned(t64, 16))
+        return fail(GPEED_ERR_INVALID, "untile: raw must be 2-byte and t64 16-byte aligned");
+    hipError_t e = gpeed::launch_untile(static_cast<const uint8_t*>(t64), n_rows, (int)in_dim,
                                         static_cast<uint8_t*>(raw), static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "untile launch");
 }
 
-size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim) { return gpeed_iq3xxs_act_bytes(in_dim); }
+static bool dims_ok(int64_t in_dim) { return in_dim > 0 && in_dim % gpeed::kQK == 0 && in_dim <= (1 << 28); }
+static size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+constexpr int kMaxTok = 8;
 
-size_t gpeed_iq3xxs_act_bytes(int64_t in_dim) {
-    if (in_dim <= 0 || in_dim % gpeed::kQK || in_dim > (1 << 30)) return 0;
-    return gpeed::act_bytes((int)in_dim);
+size_t gpeed_iq3xxs_act_bytes(int64_t in_dim, int n_tok) {
+    if (!dims_ok(in_dim) || n_tok < 1 || n_tok > kMaxTok) return 0;
+    return gpeed::act_bytes((int)in_dim, n_tok);
+}
+
+size_t gpeed_iq3xxs_gemv_ws_bytes(int n_tensors, int64_t in_dim, int64_t out_dim, int n_tok) {
+    if (!dims_ok(in_dim) || out_dim <= 0 || out_dim > (1 << 30) || n_tensors < 1 || n_tensors > 2 ||
+        n_tok < 1 || n_tok > kMaxTok)
+        return 0;
+    return gpeed::gemv_ws_bytes(n_tensors, (int)in_dim, (int)out_dim, n_tok);
+}
+
+size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok) {
+    if (n_tok < 1) return 0;
+    const int nt = n_tok < kMaxTok ? n_tok : kMaxTok;
+    const size_t a = gpeed_iq3xxs_act_bytes(in_dim, nt), w = gpeed_iq3xxs_gemv_ws_bytes(1, in_dim, out_dim, nt);
+    if (!a || !w) return 0;
+    return align256(a) + w;
+}
+
+size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim, int64_t out_dim) {
+    return gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, 1);
 }
 
 static int check_mv_args(const void* w, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
-                         const void* x, float* dst, const char* who) {
+                         const void* x, const float* dst, const char* who) {
     if (in_dim <= 0 || in_dim % gpeed::kQK)
         return fail(GPEED_ERR_UNALIGNED_ROW, std::string(who) + ": row not block aligned");
+    if (!dims_ok(in_dim) || out_dim > (1 << 30)) return fail(GPEED_ERR_INVALID, std::string(who) + ": size too large");
     if (!w || !x || !dst) return fail(GPEED_ERR_INVALID, std::string(who) + ": null pointer");
     if (row0 > n_rows || (uint64_t)out_dim > n_rows - row0)
         return fail(GPEED_ERR_INVALID, std::string(who) + ": rows out of range");
     return GPEED_OK;
 }
 
-static int check_act(const void* act, size_t act_bytes, int64_t in_dim, const char* who) {
+static int check_act(const void* act, size_t act_bytes, int64_t in_dim, int n_tok, const char* who) {
     if (in_dim <= 0 || in_dim % gpeed::kQK)
         return fail(GPEED_ERR_UNALIGNED_ROW, std::string(who) + ": row not block aligned");
-    if (in_dim > (1 << 30)) return fail(GPEED_ERR_INVALID, std::string(who) + ": in_dim too large");
-    if (!act || act_bytes < gpeed::act_bytes((int)in_dim) || !aligned(act, 16))
+    if (!dims_ok(in_dim)) return fail(GPEED_ERR_INVALID, std::string(who) + ": in_dim too large");
+    if (n_tok < 1 || n_tok > kMaxTok) return fail(GPEED_ERR_INVALID, std::string(who) + ": n_tok outside 1..8");
+    if (!act || act_bytes < gpeed::act_bytes((int)in_dim, n_tok) || !aligned(act, 16))
         return fail(GPEED_ERR_WORKSPACE,
                     std::string(who) + ": activation buffer missing, misaligned or too small");
     return GPEED_OK;
 }
 
-int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, void* act, size_t act_bytes,
+int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, int n_tok, void* act, size_t act_bytes,
                           gpeed_stream_t stream) {
-    int rc = check_act(act, act_bytes, in_dim, "prep_act");
+    int rc = check_act(act, act_bytes, in_dim, n_tok, "prep_act");
     if (rc) return rc;
     if (!x || !aligned(x, 16)) return fail(GPEED_ERR_INVALID, "prep_act: x null or not 16-byte aligned");
-    hipError_t e = gpeed::launch_prep_act(x, (int)in_dim, static_cast<uint8_t*>(act),
+    hipError_t e = gpeed::launch_prep_act(x, (int)in_dim, n_tok, static_cast<uint8_t*>(act),
                                           static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "prep_act launch");
 }
 
-int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, float limit, void* act,
+int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, int n_tok, float limit, void* act,
                              size_t act_bytes, gpeed_stream_t stream) {
-    int rc = check_act(act, act_bytes, n, "prep_swiglu");
+    int rc = check_act(act, act_bytes, n, n_tok, "prep_swiglu");
     if (rc) return rc;
     if (!g || !u || !aligned(g, 16) || !aligned(u, 16))
         return fail(GPEED_ERR_INVALID, "prep_swiglu: g/u null or not 16-byte aligned");
-    hipError_t e = gpeed::launch_prep_swiglu(g, u, limit, (int)n, static_cast<uint8_t*>(act),
+    hipError_t e = gpeed::launch_prep_swiglu(g, u, limit, (int)n, n_tok, static_cast<uint8_t*>(act),
                                              static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "prep_swiglu launch");
 }
 
-static int matvec_act_n(const void* const* w, float* const* dst, int n_tensors, uint64_t n_rows,
-                        uint64_t row0, int in_dim, int out_dim, const void* act,
-                        gpeed_stream_t stream) {
+static int gemv_n(const void* const* w, float* const* dst, int n_tensors, uint64_t n_rows, uint64_t row0,
+                  int in_dim, int out_dim, const void* act, int n_tok, void* ws, size_t ws_bytes,
+                  gpeed_stream_t stream) {
     if (out_dim <= 0) return GPEED_OK;
     for (int i = 0; i < n_tensors; ++i) {
-        int rc = check_mv_args(w[i], n_rows, row0, in_dim, out_dim, act, dst[i], "matvec");
+        int rc = check_mv_args(w[i], n_rows, row0, in_dim, out_dim, act, dst[i], "gemv");
         if (rc) return rc;
-        if (!aligned(w[i], 16)) return fail(GPEED_ERR_INVALID, "matvec: T16 weights must be 16-byte aligned");
+        if (!aligned(w[i], 16)) return fail(GPEED_ERR_INVALID, "gemv: T64 weights must be 16-byte aligned");
     }
-    if (!aligned(act, 16)) return fail(GPEED_ERR_WORKSPACE, "matvec: activation misaligned");
+    if (n_tok < 1 || n_tok > kMaxTok) return fail(GPEED_ERR_INVALID, "gemv: n_tok outside 1..8");
+    if (!aligned(act, 16)) return fail(GPEED_ERR_WORKSPACE, "gemv: activation misaligned");
     if (row0 % gpeed::kTileRows)
-        return fail(GPEED_ERR_LAYOUT, "matvec: row0 must be a multiple of 16 on the T16 layout");
+        return fail(GPEED_ERR_LAYOUT, "gemv: row0 must be a multiple of 64 on the T64 layout");
+    if (!ws || !aligned(ws, 16) || ws_bytes < gpeed::gemv_ws_bytes(n_tensors, in_dim, out_dim, n_tok))
+        return fail(GPEED_ERR_WORKSPACE, "gemv: workspace missing, misaligned or too small");
     const DeviceState* st = nullptr;
     int rc = device_state(&st);
     if (rc) return rc;
     const uint8_t* wp[2] = {static_cast<const uint8_t*>(w[0]),
                             static_cast<const uint8_t*>(w[n_tensors > 1 ? 1 : 0])};
     float* yp[2] = {dst[0], dst[n_tensors > 1 ? 1 : 0]};
-    hipError_t e = gpeed::launch_matvec_t16(wp, yp, n_tensors, in_dim, row0, out_dim,
-                                            static_cast<const uint8_t*>(act), st->grid_table,
-                                            st->num_cus, static_cast<hipStream_t>(stream));
-    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec launch");
+    hipError_t e = gpeed::launch_gemv_t64(wp, yp, n_tensors, in_dim, row0, out_dim, n_tok,
+                                          static_cast<const uint8_t*>(act), static_cast<uint8_t*>(ws),
+                                          st->num_cus, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemv launch");
 }
 
-int gpeed_iq3xxs_matvec_act(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim,
-                            int out_dim, const void* act, float* dst, gpeed_stream_t stream) {
-    const void* w[1] = {w_t16};
+int gpeed_iq3xxs_gemv_act(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                          const void* act, int n_tok, float* dst, void* ws, size_t ws_bytes,
+                          gpeed_stream_t stream) {
+    const void* w[1] = {w_t64};
     float* d[1] = {dst};
-    return matvec_act_n(w, d, 1, n_rows, row0, in_dim, out_dim, act, stream);
+    return gemv_n(w, d, 1, n_rows, row0, in_dim, out_dim, act, n_tok, ws, ws_bytes, stream);
 }
 
-int gpeed_iq3xxs_matvec2_act(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0,
-                             int in_dim, int out_dim, const void* act, float* dst_a, float* dst_b,
-                             gpeed_stream_t stream) {
+int gpeed_iq3xxs_gemv2_act(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0,
+                           int in_dim, int out_dim, const void* act, int n_tok, float* dst_a,
+                           float* dst_b, void* ws, size_t ws_bytes, gpeed_stream_t stream) {
     const void* w[2] = {w_a, w_b};
     float* d[2] = {dst_a, dst_b};
-    return matvec_act_n(w, d, 2, n_rows, row0, in_dim, out_dim, act, stream);
+    return gemv_n(w, d, 2, n_rows, row0, in_dim, out_dim, act, n_tok, ws, ws_bytes, stream);
 }
 
-int gpeed_iq3xxs_matvec(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
-                        const float* x, float* dst, void* ws, size_t ws_bytes,
+int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                        const float* X, int n_tok, float* Y, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream) {
-    if (out_dim <= 0) return GPEED_OK;
-    int rc = check_mv_args(w_t16, n_rows, row0, in_dim, out_dim, x, dst, "matvec");
+    if (n_tok <= 0 || out_dim <= 0) return GPEED_OK;  // weights.cpp:88
+    int rc = check_mv_args(w_t64, n_rows, row0, in_dim, out_dim, X, Y, "matmul");
     if (rc) return rc;
     if (row0 % gpeed::kTileRows)
-        return fail(GPEED_ERR_LAYOUT, "matvec: row0 must be a multiple of 16 on the T16 layout");
-    rc = gpeed_iq3xxs_prep_act(x, in_dim, ws, ws_bytes, stream);
-    if (rc) return rc;
-    return gpeed_iq3xxs_matvec_act(w_t16, n_rows, row0, in_dim, out_dim, ws, dst, stream);
+        return fail(GPEED_ERR_LAYOUT, "matmul: row0 must be a multiple of 64 on the T64 layout");
+    const size_t need = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, n_tok);
+    if (!ws || !aligned(ws, 256) || ws_bytes < need)
+        return fail(GPEED_ERR_WORKSPACE, "matmul: workspace missing, misaligned or too small");
+    const int nt_max = n_tok < kMaxTok ? n_tok : kMaxTok;
+    const size_t a_bytes = align256(gpeed::act_bytes(in_dim, nt_max));
+    uint8_t* act = static_cast<uint8_t*>(ws);
+    uint8_t* gws = act + a_bytes;
+    for (int t0 = 0; t0 < n_tok; t0 += kMaxTok) {
+        const int nt = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
+        rc = gpeed_iq3xxs_prep_act(X + (size_t)t0 * in_dim, in_dim, nt, act, a_bytes, stream);
+        if (rc) return rc;
+        rc = gpeed_iq3xxs_gemv_act(w_t64, n_rows, row0, in_dim, out_dim, act, nt, Y + (size_t)t0 * out_dim,
+                                   gws, ws_bytes - a_bytes, stream);
+        if (rc) return rc;
+    }
+    return GPEED_OK;
+}
+
+int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                        const float* x, float* dst, void* ws, size_t ws_bytes,
+                        gpeed_stream_t stream) {
+    return gpeed_iq3xxs_matmul(w_t64, n_rows, row0, in_dim, out_dim, x, 1, dst, ws, ws_bytes, stream);
 }
 
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,

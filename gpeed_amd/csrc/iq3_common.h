@@ -8,30 +8,29 @@
 //   w[32ib + 8l + j] = d*(0.5+s)*0.5 * grid(qs[8ib+2l+j/4])[j%4] * sign_j
 //   with signs = sign index | parity << 7 (8 signs of even parity).
 //
-// Tiled layout "T16" (what the matvec / matmul kernels stream). It is a
-// byte-for-byte bijection of the GGUF payload and the same size (98 bytes per
-// 256 weights; a trailing partial tile of rows is padded to 16 rows):
-//   rows are grouped in tiles of 16; the record of (tile t, block b) is 1568 B
-//   at byte offset (t*nb + b)*1568, nb = in_dim/256;
-//   record = [unit j=0: 64 x 12 B][unit j=1: 64 x 12 B][d: 16 x fp16]
-//   12-byte unit at index L = n + 16g (row n of the tile, g = 0..3) of half j
-//   belongs to sub-block ib = 4j+g of row n:
-//     word0 = qs[8ib..8ib+3], word1 = qs[8ib+4..8ib+7] (bytes unchanged)
-//     word2 = W, the sign/scale word, bit-sliced for the decode:
-//        the signs of elements (2d, 2d+1) of group l sit at bits
-//        15-k and 31-k with k = 4d + l, so (W << k) puts them on the fp16
-//        sign bits of one packed pair; the position of element 7 (implied:
-//        parity of the other seven) holds the scale instead, i.e. bits
-//        16..19 = s.
-// Lane L = n + 16g of a wavefront loads unit L of each half, which is exactly
-// the B operand it feeds to v_mfma_f32_16x16x32_f16 (column n, k-slots of
-// lane group g), so a record is consumed with fully coalesced 12-byte loads
-// and no cross-lane traffic.
+// Tiled layout "T64" (what the GEMV kernels stream). It is a byte-for-byte
+// bijection of the GGUF payload and the same size (98 bytes per 256 weights;
+// a trailing partial tile of rows is padded to 64 rows with zero bytes):
+//   rows are grouped in tiles of 64; the record of (tile t, block b) is
+//   6272 B at byte offset (t*nb + b)*6272, nb = in_dim/256;
+//   record = [unit u=0..5: 64 lanes x 16 B][d: 64 x fp16]
+//   lane n (row n of the tile) owns a 24-dword sequence spread over the six
+//   units (dwords 4u..4u+3 in unit u, at byte u*1024 + 16n). Sub-block ib
+//   of the row sits at dwords 3ib..3ib+2:
+//     q0 = qs[8ib..8ib+3], q1 = qs[8ib+4..8ib+7] (bytes unchanged)
+//     W  = the sign/scale word. The 8 elements 8l..8l+7 of group l form four
+//          pairs (elements 2c, 2c+1 for c = 0..3); pair c of group l owns
+//          bits a and a+16 with a = 4c + l (lower element at bit a). So
+//          rotr(W, a + 17) puts a pair's two signs on the fp16 sign bits of
+//          a packed pair. Bits 28..31 (the implied eighth sign of each group)
+//          hold the scale s instead, bit 28+l = bit l of s.
+// A wavefront loads one record with six fully coalesced 16-byte loads and a
+// 2-byte load; lane n then holds all 256 weights of row n for block b.
 //
-// Grid table (64 KiB, built by build_grid_table, kept in LDS): the 256
-// codebook entries as 4 unsigned fp16 each, replicated 32 times so that lane
-// L reads its own copy at byte (idx << 8) | ((L & 31) << 3): within every
-// 16-lane LDS pass the lanes hit 16 distinct bank pairs whatever the indices.
+// Grid table (64 KiB, built in LDS by every GEMV workgroup): the 256 codebook
+// entries as 4 unsigned fp16 each, replicated 32 times so that lane L reads
+// its own copy at byte (idx << 8) | ((L & 31) << 3): within every 32-lane
+// LDS pass the lanes hit 32 distinct bank pairs whatever the indices.
 #pragma once
 
 #include <cstddef>
@@ -43,14 +42,15 @@ namespace gpeed {
 
 constexpr int kQK = 256;
 constexpr int kBlockBytes = 98;
-constexpr int kTileRows = 16;
-constexpr int kRecordBytes = kTileRows * kBlockBytes;  // 1568
-constexpr int kUnitHalfBytes = 64 * 12;                // 768
+constexpr int kTileRows = 64;
+constexpr int kRecordBytes = kTileRows * kBlockBytes;  // 6272
+constexpr int kUnitBytes = 64 * 16;                    // 1024
+constexpr int kRecordDOffset = 6 * kUnitBytes;         // 6144
 constexpr int kGridTableBytes = 65536;
 constexpr int kGridReplicas = 32;
 
 inline size_t iq3_row_bytes(long long in_dim) { return (size_t)(in_dim / kQK) * kBlockBytes; }
-inline size_t t16_bytes(unsigned long long n_rows, long long in_dim) {
+inline size_t t64_bytes(unsigned long long n_rows, long long in_dim) {
     const unsigned long long tiles = (n_rows + kTileRows - 1) / kTileRows;
     return (size_t)tiles * (size_t)(in_dim / kQK) * kRecordBytes;
 }
@@ -72,17 +72,29 @@ inline void build_grid_table(uint16_t* out) {
                     host_f16_of_small_uint((kIq3xxsGrid[idx] >> (8 * j)) & 255u);
 }
 
-// T16 sign/scale word from a GGUF aux word (see the layout above).
-inline uint32_t aux_to_t16(uint32_t aux) {
-    uint32_t w = ((aux >> 28) & 15u) << 16;
-    for (int l = 0; l < 4; ++l) {
-        const uint32_t s7 = (aux >> (7 * l)) & 127u;
-        for (int j = 0; j < 7; ++j) {
-            const int d = j >> 1, k = 4 * d + l;
-            w |= ((s7 >> j) & 1u) << ((j & 1) ? 31 - k : 15 - k);
-        }
-    }
+// Bit of the T64 sign word that holds the sign of element e (0..31) of a
+// sub-block (e = 8l + j).
+constexpr int t64_sign_bit(int e) {
+    return 4 * ((e & 7) >> 1) + (e >> 3) + 16 * (e & 1);
+}
+
+// T64 sign/scale word from a GGUF aux word (see the layout above).
+__host__ __device__ inline uint32_t aux_to_t64(uint32_t aux) {
+    uint32_t w = (aux >> 28) << 28;
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+#pragma unroll
+        for (int j = 0; j < 7; ++j) w |= ((aux >> (7 * l + j)) & 1u) << t64_sign_bit(8 * l + j);
     return w;
+}
+
+__host__ __device__ inline uint32_t t64_to_aux(uint32_t w) {
+    uint32_t aux = (w >> 28) << 28;
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+#pragma unroll
+        for (int j = 0; j < 7; ++j) aux |= ((w >> t64_sign_bit(8 * l + j)) & 1u) << (7 * l + j);
+    return aux;
 }
 
 }  // namespace gpeed
@@ -92,50 +104,21 @@ inline uint32_t aux_to_t16(uint32_t aux) {
 
 namespace gpeed {
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t aux_to_t16_dev(uint32_t aux) {
-    uint32_t w = ((aux >> 28) & 15u) << 16;
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-        const uint32_t s7 = (aux >> (7 * l)) & 127u;
-#pragma unroll
-        for (int j = 0; j < 7; ++j) {
-            const int d = j >> 1, k = 4 * d + l;
-            w |= ((s7 >> j) & 1u) << ((j & 1) ? 31 - k : 15 - k);
-        }
-    }
-    return w;
-}
-
-__device__ __forceinline__ uint32_t t16_to_aux_dev(uint32_t w) {
-    uint32_t aux = ((w >> 16) & 15u) << 28;
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-#pragma unroll
-        for (int j = 0; j < 7; ++j) {
-            const int d = j >> 1, k = 4 * d + l;
-            aux |= ((w >> ((j & 1) ? 31 - k : 15 - k)) & 1u) << (7 * l + j);
-        }
-    }
-    return aux;
-}
-
-// The T16 sign word with the four implied signs (element 7 of each group,
+// The T64 sign word with the four implied signs (element 7 of each group,
 // the parity of the other seven) written over the scale nibble. Group l's
-// bits are exactly the positions = 3-l (mod 4), so three xor-folds give all
-// four parities at once, in bits 3-l.
-__device__ __forceinline__ uint32_t t16_full_signs(uint32_t w) {
-    const uint32_t m = w & 0xFFF0FFFFu;
+// bits are exactly the positions = l (mod 4), so three xor-folds give all
+// four parities at once, in bits 0..3.
+__device__ __forceinline__ uint32_t t64_full_signs(uint32_t w) {
+    const uint32_t m = w & 0x0FFFFFFFu;
     uint32_t t = m ^ (m >> 16);
     t ^= t >> 8;
     t ^= t >> 4;
-    return m | ((t & 15u) << 16);
+    return m | (t << 28);
 }
 
 // fp16 bit pattern -> fp32, integer-only (exact for every pattern, NaN

@@ -49,65 +49,72 @@ __global__ __launch_bounds__(256) void k_dequant_raw(const uint8_t* __restrict__
     out[1] = make_float4(y[4], y[5], y[6], y[7]);
 }
 
-// One thread per 12-byte unit (tile, block, lane L, half j); threads with
-// L < 16 and j == 0 also move the row's fp16 d. Rows past n_rows (padding of
-// the last tile) are written as zeros.
+// One thread per (record, lane): lane n of record (tile t, block b) takes
+// row 64t+n's block b (24 dwords + d, T64 order). Rows past n_rows (padding
+// of the last tile) are written as zeros.
 __global__ __launch_bounds__(256) void k_tile(const uint8_t* __restrict__ raw,
                                               unsigned long long n_rows, int nb,
-                                              uint8_t* __restrict__ t16,
-                                              unsigned long long n_units) {
+                                              uint8_t* __restrict__ t64,
+                                              unsigned long long n_items) {
     const unsigned long long u = (unsigned long long)blockIdx.x * 256 + threadIdx.x;
-    if (u >= n_units) return;
-    const int jl = (int)(u & 127);  // j*64 + L
-    const unsigned long long rec = u >> 7;
+    if (u >= n_items) return;
+    const int n = (int)(u & 63);
+    const unsigned long long rec = u >> 6;
     const int b = (int)(rec % (unsigned long long)nb);
     const unsigned long long t = rec / (unsigned long long)nb;
-    const int j = jl >> 6, L = jl & 63, n = L & 15, g = L >> 4;
-    const int ib = 4 * j + g;
     const unsigned long long row = t * kTileRows + n;
-    const size_t rb = (size_t)nb * kBlockBytes;
-    uint8_t* dst_rec = t16 + rec * kRecordBytes;
-    uint32_t* unit = reinterpret_cast<uint32_t*>(dst_rec + j * kUnitHalfBytes + L * 12);
-    if (row >= n_rows) {
-        unit[0] = 0; unit[1] = 0; unit[2] = 0;
-        if (j == 0 && g == 0) *reinterpret_cast<uint16_t*>(dst_rec + 2 * kUnitHalfBytes + 2 * n) = 0;
-        return;
+    uint8_t* dst = t64 + rec * kRecordBytes;
+    uint32_t seq[24];
+    uint32_t d = 0;
+    if (row < n_rows) {
+        const uint8_t* blk = raw + row * ((size_t)nb * kBlockBytes) + (size_t)b * kBlockBytes;
+#pragma unroll
+        for (int ib = 0; ib < 8; ++ib) {
+            seq[3 * ib] = ld_u32_a2(blk + 2 + 8 * ib);
+            seq[3 * ib + 1] = ld_u32_a2(blk + 2 + 8 * ib + 4);
+            seq[3 * ib + 2] = aux_to_t64(ld_u32_a2(blk + 66 + 4 * ib));
+        }
+        d = ld_u16(blk);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 24; ++i) seq[i] = 0;
     }
-    const uint8_t* blk = raw + row * rb + (size_t)b * kBlockBytes;
-    unit[0] = ld_u32_a2(blk + 2 + 8 * ib);
-    unit[1] = ld_u32_a2(blk + 2 + 8 * ib + 4);
-    unit[2] = aux_to_t16_dev(ld_u32_a2(blk + 66 + 4 * ib));
-    if (j == 0 && g == 0)
-        *reinterpret_cast<uint16_t*>(dst_rec + 2 * kUnitHalfBytes + 2 * n) = (uint16_t)ld_u16(blk);
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+        *reinterpret_cast<uint4*>(dst + i * kUnitBytes + n * 16) =
+            make_uint4(seq[4 * i], seq[4 * i + 1], seq[4 * i + 2], seq[4 * i + 3]);
+    *reinterpret_cast<uint16_t*>(dst + kRecordDOffset + n * 2) = (uint16_t)d;
 }
 
-__global__ __launch_bounds__(256) void k_untile(const uint8_t* __restrict__ t16,
+__global__ __launch_bounds__(256) void k_untile(const uint8_t* __restrict__ t64,
                                                 unsigned long long n_rows, int nb,
                                                 uint8_t* __restrict__ raw,
-                                                unsigned long long n_units) {
+                                                unsigned long long n_items) {
     const unsigned long long u = (unsigned long long)blockIdx.x * 256 + threadIdx.x;
-    if (u >= n_units) return;
-    const int jl = (int)(u & 127);
-    const unsigned long long rec = u >> 7;
+    if (u >= n_items) return;
+    const int n = (int)(u & 63);
+    const unsigned long long rec = u >> 6;
     const int b = (int)(rec % (unsigned long long)nb);
     const unsigned long long t = rec / (unsigned long long)nb;
-    const int j = jl >> 6, L = jl & 63, n = L & 15, g = L >> 4;
-    const int ib = 4 * j + g;
     const unsigned long long row = t * kTileRows + n;
     if (row >= n_rows) return;
-    const size_t rb = (size_t)nb * kBlockBytes;
-    const uint8_t* src_rec = t16 + rec * kRecordBytes;
-    const uint32_t* unit = reinterpret_cast<const uint32_t*>(src_rec + j * kUnitHalfBytes + L * 12);
-    uint16_t* blk = reinterpret_cast<uint16_t*>(raw + row * rb + (size_t)b * kBlockBytes);
-    const uint32_t q0 = unit[0], q1 = unit[1], a = t16_to_aux_dev(unit[2]);
+    const uint8_t* src = t64 + rec * kRecordBytes;
+    uint32_t seq[24];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src + i * kUnitBytes + n * 16);
+        seq[4 * i] = v.x; seq[4 * i + 1] = v.y; seq[4 * i + 2] = v.z; seq[4 * i + 3] = v.w;
+    }
     // 16-bit stores: the fields are 2-byte aligned inside the 98-byte block
-    uint16_t* qs = blk + 1 + 4 * ib;
-    qs[0] = (uint16_t)q0; qs[1] = (uint16_t)(q0 >> 16);
-    qs[2] = (uint16_t)q1; qs[3] = (uint16_t)(q1 >> 16);
-    uint16_t* aw = blk + 33 + 2 * ib;
-    aw[0] = (uint16_t)a; aw[1] = (uint16_t)(a >> 16);
-    if (j == 0 && g == 0)
-        blk[0] = *reinterpret_cast<const uint16_t*>(src_rec + 2 * kUnitHalfBytes + 2 * n);
+    uint16_t* blk = reinterpret_cast<uint16_t*>(raw + row * ((size_t)nb * kBlockBytes) + (size_t)b * kBlockBytes);
+    blk[0] = *reinterpret_cast<const uint16_t*>(src + kRecordDOffset + n * 2);
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint32_t q0 = seq[3 * ib], q1 = seq[3 * ib + 1], a = t64_to_aux(seq[3 * ib + 2]);
+        blk[1 + 4 * ib] = (uint16_t)q0; blk[2 + 4 * ib] = (uint16_t)(q0 >> 16);
+        blk[3 + 4 * ib] = (uint16_t)q1; blk[4 + 4 * ib] = (uint16_t)(q1 >> 16);
+        blk[33 + 2 * ib] = (uint16_t)a; blk[34 + 2 * ib] = (uint16_t)(a >> 16);
+    }
 }
 
 __global__ __launch_bounds__(256) void k_add(const float* __restrict__ a, const float* __restrict__ b,
@@ -126,25 +133,25 @@ hipError_t launch_dequant_raw(const uint8_t* src, float* dst, unsigned long long
     return hipGetLastError();
 }
 
-hipError_t launch_tile(const uint8_t* raw, unsigned long long n_rows, int in_dim, uint8_t* t16,
+hipError_t launch_tile(const uint8_t* raw, unsigned long long n_rows, int in_dim, uint8_t* t64,
                        hipStream_t s) {
     const int nb = in_dim / kQK;
     const unsigned long long tiles = (n_rows + kTileRows - 1) / kTileRows;
-    const unsigned long long units = tiles * (unsigned long long)nb * 128ull;
-    if (units == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_tile, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, raw, n_rows, nb,
-                       t16, units);
+    const unsigned long long items = tiles * (unsigned long long)nb * 64ull;
+    if (items == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_tile, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, raw, n_rows, nb,
+                       t64, items);
     return hipGetLastError();
 }
 
-hipError_t launch_untile(const uint8_t* t16, unsigned long long n_rows, int in_dim, uint8_t* raw,
+hipError_t launch_untile(const uint8_t* t64, unsigned long long n_rows, int in_dim, uint8_t* raw,
                          hipStream_t s) {
     const int nb = in_dim / kQK;
     const unsigned long long tiles = (n_rows + kTileRows - 1) / kTileRows;
-    const unsigned long long units = tiles * (unsigned long long)nb * 128ull;
-    if (units == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_untile, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, t16, n_rows,
-                       nb, raw, units);
+    const unsigned long long items = tiles * (unsigned long long)nb * 64ull;
+    if (items == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_untile, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, t64, n_rows,
+                       nb, raw, items);
     return hipGetLastError();
 }
 

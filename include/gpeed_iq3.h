@@ -28,7 +28,7 @@ typedef void* gpeed_stream_t;
 #define GPEED_ERR_UNALIGNED_ROW (-3)  /* in_dim % 256 != 0       (weights.cpp:93-94, 173-174) */
 #define GPEED_ERR_UNIMPLEMENTED (-4)  /* dtype not on this path  (quant.cpp:553-554); caller falls back */
 #define GPEED_ERR_HIP (-5)            /* a HIP runtime call failed (see gpeed_last_error) */
-#define GPEED_ERR_LAYOUT (-6)         /* T16 operand addressed off a 16-row tile boundary */
+#define GPEED_ERR_LAYOUT (-6)         /* T64 operand addressed off a 64-row tile boundary */
 #define GPEED_ERR_WORKSPACE (-7)      /* workspace missing or too small */
 #define GPEED_ERR_NO_DEVICE (-8)      /* no HIP device visible */
 
@@ -45,9 +45,9 @@ int gpeed_device_name(int index, char* buf, size_t len);
  * arrays; synchronous, stages through device memory like the reference. */
 int gpeed_add_f32(const float* a, const float* b, float* dst, int n);
 
-/* Uploads the per-device lookup tables for the current device. Called
- * implicitly by the compute entry points; call it once up front to keep the
- * one-time allocation out of timed or captured regions. */
+/* Reads the device attributes the launches are sized by (CU count) for the
+ * current device. Called implicitly by the compute entry points; call it
+ * once up front to keep the one-time query out of timed regions. */
 int gpeed_init(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* gpeed_last_error(void);
@@ -56,9 +56,9 @@ const char* gpeed_last_error(void);
 
 /* dtype_row_bytes(IQ3_XXS, in_dim) (quant.cpp:119-126): 0 if in_dim % 256. */
 size_t gpeed_iq3xxs_row_bytes(int64_t in_dim);
-/* Bytes of the T16 (tiled) copy of an [n_rows, in_dim] IQ3_XXS tensor: the
- * GGUF size rounded up to whole 16-row tiles. */
-size_t gpeed_iq3xxs_t16_bytes(uint64_t n_rows, int64_t in_dim);
+/* Bytes of the T64 (tiled) copy of an [n_rows, in_dim] IQ3_XXS tensor: the
+ * GGUF size rounded up to whole 64-row tiles. */
+size_t gpeed_iq3xxs_t64_bytes(uint64_t n_rows, int64_t in_dim);
 
 /* ---- dequantize (replaces quant.h:18-22, quant.cpp:565-573) ------------- */
 
@@ -70,50 +70,74 @@ int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_s
 /* ---- weight residency (replaces weights.cpp:62-84 pin_nonexpert/payload) */
 
 /* Host-only layout introspection (no device use; no reference counterpart):
- * the 64 KiB replicated grid table the kernels keep in LDS (32768 fp16 bit
- * patterns; returns GPEED_ERR_INVALID if n < 32768), and the T16 sign/scale
- * word made from a GGUF aux word. Lets CPU tests model the GPU decode. */
-int gpeed_t16_grid_table(uint16_t* out, size_t n);
-uint32_t gpeed_t16_aux_word(uint32_t gguf_aux);
+ * the 64 KiB replicated grid table the GEMV kernels build in LDS (32768 fp16
+ * bit patterns; returns GPEED_ERR_INVALID if n < 32768), and the T64
+ * sign/scale word made from a GGUF aux word. Lets CPU tests model the GPU
+ * decode. */
+int gpeed_t64_grid_table(uint16_t* out, size_t n);
+uint32_t gpeed_t64_aux_word(uint32_t gguf_aux);
 
-/* GGUF rows -> T16 copy (same bytes per weight) / back. */
-int gpeed_iq3xxs_tile(const void* raw, uint64_t n_rows, int64_t in_dim, void* t16,
+/* GGUF rows -> T64 copy (same bytes per weight, 64-row tiles) / back.
+ * Done once at load time, in place of pinning the GGUF payload. */
+int gpeed_iq3xxs_tile(const void* raw, uint64_t n_rows, int64_t in_dim, void* t64,
                       gpeed_stream_t stream);
-int gpeed_iq3xxs_untile(const void* t16, uint64_t n_rows, int64_t in_dim, void* raw,
+int gpeed_iq3xxs_untile(const void* t64, uint64_t n_rows, int64_t in_dim, void* raw,
                         gpeed_stream_t stream);
 
-/* ---- batch-1 matvec (replaces WeightStore::matvec_quant, weights.h:41-42,
- *      weights.cpp:167-203) ---------------------------------------------- */
+/* ---- products (replace WeightStore::matvec_quant, weights.h:41-42,
+ *      weights.cpp:167-203, and matmul_quant, weights.h:47-48,
+ *      weights.cpp:86-165) ----------------------------------------------- */
 
-/* Workspace bytes gpeed_iq3xxs_matvec needs for an in_dim activation. */
-size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim);
-/* dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim, from the T16 copy of a
- * tensor with n_rows rows. row0 % 16 == 0. x, dst: fp32 device arrays. */
-int gpeed_iq3xxs_matvec(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+/* Workspace bytes of gpeed_iq3xxs_matvec / gpeed_iq3xxs_matmul for n_tok
+ * vectors (n_tok = 1 for matvec). The workspace must be zero-filled once
+ * before its first use; calls leave it ready for the next one. One
+ * workspace per stream: calls that run concurrently must not share one. */
+size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim, int64_t out_dim);
+size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok);
+/* dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim, from the T64 copy of a
+ * tensor with n_rows rows. row0 % 64 == 0. x, dst: fp32 device arrays. */
+int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* x, float* dst, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream);
-/* The two halves of gpeed_iq3xxs_matvec, for callers that reuse one
- * activation across several tensors (gate and up of model.cpp:681-682) or
- * fuse the SwiGLU epilogue into the next product's input
- * (model.cpp:683-689): a "prepared activation" is the fp16 hi/lo MFMA
- * operand of one fp32 vector plus its power-of-two scale, in a caller-owned
- * device buffer of gpeed_iq3xxs_act_bytes(in_dim) bytes (16-byte aligned). */
-size_t gpeed_iq3xxs_act_bytes(int64_t in_dim);
-int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, void* act, size_t act_bytes,
-                          gpeed_stream_t stream);
-/* act <- silu(min(g,limit)) * clamp(u,-limit,limit) over n = in_dim elements
- * (model.cpp:683-688 with swiglu_limit, model_config.h:70). */
-int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, float limit, void* act,
-                             size_t act_bytes, gpeed_stream_t stream);
-int gpeed_iq3xxs_matvec_act(const void* w_t16, uint64_t n_rows, uint64_t row0, int in_dim,
-                            int out_dim, const void* act, float* dst, gpeed_stream_t stream);
-/* Two same-shape tensors against one prepared activation in one launch
- * (gate and up of model.cpp:681-682, or of the shared expert at 747-748). */
-int gpeed_iq3xxs_matvec2_act(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0,
-                             int in_dim, int out_dim, const void* act, float* dst_a, float* dst_b,
-                             gpeed_stream_t stream);
+/* Y[t][j] = sum_i W[row0+j][i] * X[t][i] for t < n_tok (X [n_tok][in_dim],
+ * Y [n_tok][out_dim], fp32, row-major). Row t of Y is the matvec of X[t]
+ * (weights.cpp:86-165 makes the same promise). */
+int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                        const float* X, int n_tok, float* Y, void* ws, size_t ws_bytes,
+                        gpeed_stream_t stream);
 
-/* Same product straight from GGUF rows (no tiling; any row0). */
+/* The two halves of the products, for callers that reuse one activation
+ * across several tensors (gate and up of model.cpp:681-682) or fuse the
+ * SwiGLU epilogue into the next product's input (model.cpp:683-689). A
+ * "prepared activation" holds 1..8 fp32 vectors as the fp16 hi/lo MFMA
+ * operand plus a power-of-two scale per 256 elements, in a caller-owned
+ * device buffer of gpeed_iq3xxs_act_bytes(in_dim, n_tok) bytes (16-byte
+ * aligned). The GEMV workspace (gpeed_iq3xxs_gemv_ws_bytes, zero-filled
+ * once, one per stream) holds the partial sums of row tiles that two
+ * workgroups share. */
+size_t gpeed_iq3xxs_act_bytes(int64_t in_dim, int n_tok);
+int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, int n_tok, void* act, size_t act_bytes,
+                          gpeed_stream_t stream);
+/* act <- silu(min(g,limit)) * clamp(u,-limit,limit) over n_tok vectors of
+ * n = in_dim elements (model.cpp:683-688, model_batch.cpp:245-253 with
+ * swiglu_limit, model_config.h:70). */
+int gpeed_iq3xxs_prep_swiglu(const float* g, const float* u, int64_t n, int n_tok, float limit,
+                             void* act, size_t act_bytes, gpeed_stream_t stream);
+size_t gpeed_iq3xxs_gemv_ws_bytes(int n_tensors, int64_t in_dim, int64_t out_dim, int n_tok);
+/* dst[t][j] = sum_i W[row0+j][i] * x_t[i] for the n_tok (1..8) prepared
+ * vectors; dst is [n_tok][out_dim]. */
+int gpeed_iq3xxs_gemv_act(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                          const void* act, int n_tok, float* dst, void* ws, size_t ws_bytes,
+                          gpeed_stream_t stream);
+/* Two same-shape tensors against one prepared activation in one launch
+ * (gate and up of model.cpp:681-682, or of the shared expert at 747-748);
+ * ws sized for n_tensors = 2. */
+int gpeed_iq3xxs_gemv2_act(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0,
+                           int in_dim, int out_dim, const void* act, int n_tok, float* dst_a,
+                           float* dst_b, void* ws, size_t ws_bytes, gpeed_stream_t stream);
+
+/* Same product as gpeed_iq3xxs_matvec straight from GGUF rows (no tiling;
+ * any row0), one wavefront per row. */
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,
                             int out_dim, const float* x, float* dst, gpeed_stream_t stream);
 

@@ -2,10 +2,10 @@
 
 * libgpeed_iq3.so loads and exports every entry point include/gpeed_iq3.h declares;
 * host-only geometry and layout helpers answer correctly;
-* a numpy model of the GPU decode (T16 unit -> perm addresses -> the library's
-  own 64 KiB replicated LDS table -> sign bits from the T16 word -> (2s+1)d/4)
-  reproduces the oracle's dequantized weights bit for bit, so the layout and
-  table are right before any kernel runs.
+* a numpy model of the GPU decode (T64 lane data -> perm addresses -> the
+  library's 64 KiB replicated LDS table -> sign bits from the T64 word ->
+  (2s+1) d/4) reproduces the oracle's dequantized weights bit for bit, so the
+  layout and table are right before any kernel runs.
 """
 import ctypes as C
 import os
@@ -41,58 +41,59 @@ def test_geometry():
     assert L.gpeed_iq3xxs_row_bytes(4096) == 16 * 98
     assert L.gpeed_iq3xxs_row_bytes(12288) == 4704
     assert L.gpeed_iq3xxs_row_bytes(100) == 0
-    assert L.gpeed_iq3xxs_t16_bytes(6144, 12288) == 6144 * 4704
-    assert L.gpeed_iq3xxs_t16_bytes(17, 256) == 32 * 98
-    assert L.gpeed_iq3xxs_t16_bytes(1, 200) == 0
+    assert L.gpeed_iq3xxs_t64_bytes(6144, 12288) == 6144 * 4704
+    assert L.gpeed_iq3xxs_t64_bytes(17, 256) == 64 * 98
+    assert L.gpeed_iq3xxs_t64_bytes(1, 200) == 0
 
 
-def aux_t16_model(aux):
-    """T16 sign/scale word, restated bit by bit from the layout definition:
-    sign j (< 7) of group l at bit 15-k (j even) or 31-k (j odd), k = 4(j//2)+l;
-    the scale nibble at bits 16..19."""
-    out = ((aux >> 28) & 15) << 16
+def sign_bit(e):
+    """T64 bit of the sign of element e = 8l + j of a sub-block, restated from
+    the layout definition: pair c = j // 2 of group l owns bits a = 4c + l
+    (lower element) and a + 16 (upper element)."""
+    l, j = divmod(e, 8)
+    return 4 * (j // 2) + l + 16 * (j & 1)
+
+
+def aux_t64_model(aux):
+    out = (aux >> 28) << 28
     for l in range(4):
         for j in range(7):
-            k = 4 * (j // 2) + l
-            out |= ((aux >> (7 * l + j)) & 1) << (31 - k if j & 1 else 15 - k)
+            out |= ((aux >> (7 * l + j)) & 1) << sign_bit(8 * l + j)
     return out
+
+
+def test_sign_bits_layout():
+    """The 32 element signs use 32 distinct bits; the implied ones (j = 7)
+    sit on the scale nibble; group l uses the bits = l (mod 4)."""
+    bits = [sign_bit(e) for e in range(32)]
+    assert sorted(bits) == list(range(32))
+    assert [sign_bit(8 * l + 7) for l in range(4)] == [28, 29, 30, 31]
+    assert all(sign_bit(e) % 4 == e // 8 for e in range(32))
 
 
 def test_aux_word_matches_model():
     L = gpeed_amd.lib()
     words = synth.u64(3, 0, 4000) & np.uint64(0xFFFFFFFF)
     for w in [0, 0xFFFFFFFF, 0x80000000, 0x0FFFFFFF] + [int(v) for v in words]:
-        assert L.gpeed_t16_aux_word(w) == aux_t16_model(w), hex(w)
-
-
-def test_aux_word_is_a_bijection_on_used_bits():
-    """Every one of the 32 aux bits lands on a distinct T16 bit."""
-    L = gpeed_amd.lib()
-    seen = 0
-    for b in range(32):
-        t = L.gpeed_t16_aux_word(1 << b)
-        assert t and (t & (t - 1)) == 0, b
-        assert not (seen & t), b
-        seen |= t
-    assert seen == 0xFFFFFFFF
+        assert L.gpeed_t64_aux_word(w) == aux_t64_model(w), hex(w)
 
 
 @pytest.fixture(scope="module")
 def grid_table():
     t = np.empty(32768, np.uint16)
-    assert gpeed_amd.lib().gpeed_t16_grid_table(t.ctypes.data, t.size) == 0
-    assert gpeed_amd.lib().gpeed_t16_grid_table(t.ctypes.data, 100) != 0
+    assert gpeed_amd.lib().gpeed_t64_grid_table(t.ctypes.data, t.size) == 0
+    assert gpeed_amd.lib().gpeed_t64_grid_table(t.ctypes.data, 100) != 0
     return t
 
 
 def full_signs_model(w):
-    """The kernel's sign word: implied 8th signs (even parity per group) folded
-    in over the scale nibble with three xor-folds (t16_full_signs)."""
-    m = w & 0xFFF0FFFF
+    """The kernel's sign word: implied eighth signs (even parity per group)
+    folded in over the scale nibble with three xor-folds (t64_full_signs)."""
+    m = w & 0x0FFFFFFF
     t = m ^ (m >> 16)
     t ^= t >> 8
     t ^= t >> 4
-    return m | ((t & 15) << 16)
+    return (m | (t << 28)) & 0xFFFFFFFF
 
 
 def test_grid_table_replicas_conflict_free(grid_table):
@@ -108,9 +109,15 @@ def test_grid_table_replicas_conflict_free(grid_table):
     assert not (grid_table & 0x8000).any()  # unsigned entries
 
 
+def rotr(w, r):
+    r &= 31
+    return ((w >> r) | (w << (32 - r))) & 0xFFFFFFFF if r else w
+
+
 def test_decode_model_matches_oracle(grid_table):
-    """T16 unit -> v_perm addresses -> replicated table -> sign insertion ->
-    db = (2s+1) * d/4: bit-exact with the oracle's dequantized weights."""
+    """T64 lane data -> v_perm addresses -> replicated table -> sign bits by
+    rotate-and-mask (rotr(W, a+17) & 0x80008000) -> (2s+1) * d/4: bit-exact
+    with the oracle's dequantized weights."""
     L = gpeed_amd.lib()
     blocks = synth.iq3xxs_blocks(5, 0, 48)
     want = oracle.dequantize(blocks, 48 * 256).reshape(48, 256)
@@ -118,23 +125,23 @@ def test_decode_model_matches_oracle(grid_table):
         d = np.float32(np.frombuffer(raw[0:2].tobytes(), np.float16)[0])
         aux = np.frombuffer(raw[66:98].tobytes(), "<u4")
         got = np.empty(256, np.float32)
+        lane = (7 * bi) % 64
+        lb = (lane & 31) << 3
         for ib in range(8):
-            lane = (7 * bi + 13 * ib) % 64
-            lb = (lane & 31) << 3
-            w = L.gpeed_t16_aux_word(int(aux[ib]))
+            w = L.gpeed_t64_aux_word(int(aux[ib]))
             sw = full_signs_model(w)
-            s = (w >> 16) & 15
-            db = np.float32(2 * s + 1) * (d * np.float32(0.25))
+            sc = np.float32((w >> 27) | 1)
             q = raw[2 + 8 * ib: 10 + 8 * ib]
-            for l in range(4):
-                h = np.empty(8, np.uint16)
-                for half in range(2):
-                    a = ((int(q[2 * l + half]) << 8) | lb) // 2
-                    h[4 * half: 4 * half + 4] = grid_table[a: a + 4]
-                for e in range(8):
-                    k = 4 * (e // 2) + l
-                    h[e] |= ((sw >> (31 - k if e & 1 else 15 - k)) & 1) << 15
-                got[32 * ib + 8 * l: 32 * ib + 8 * l + 8] = h.view(np.float16).astype(np.float32) * db
+            for m in range(8):  # one MFMA: grid index q[m], elements 4m..4m+3
+                l, h = m >> 1, m & 1
+                a = ((int(q[m]) << 8) | lb) // 2
+                v = grid_table[a: a + 4].copy()
+                for p in range(2):
+                    bits = rotr(sw, 4 * (2 * h + p) + l + 17) & 0x80008000
+                    v[2 * p] |= (bits >> 0) & 0x8000
+                    v[2 * p + 1] |= (bits >> 16) & 0x8000
+                got[32 * ib + 4 * m: 32 * ib + 4 * m + 4] = v.view(np.float16).astype(np.float32) * sc
+        got *= d * np.float32(0.25)
         assert np.array_equal(got.view(np.uint32), want[bi].view(np.uint32)), bi
 
 

@@ -3,10 +3,10 @@
 Bars: dequantized weights and layout conversions bit-exact; products within
 1e-3 of the oracle under rel_err (conftest.rel_err, the north-star gate) and,
 as a tighter design check, within 2e-5 -- the MFMA path multiplies exactly
-(fp16 q*(2s+1) times fp16 hi/lo activation halves), so only fp32
-accumulation order separates it from the CPU. Dropping the low activation
-half would still pass 1e-3 (it costs ~3e-4), so the tight bound is what
-catches it.
+(fp16 signed grid values times fp16 hi/lo activation halves, then the exact
+(2s+1) and d/4 scales), so only fp32 accumulation order separates it from the
+CPU. Dropping the low activation half would still pass 1e-3 (it costs
+~3e-4), so the tight bound is what catches it.
 """
 import os
 
@@ -70,54 +70,62 @@ def test_dequant_errors(gpu):
     assert e.value.code == -4
 
 
-@pytest.mark.parametrize("n_rows,in_dim", [(16, 256), (17, 768), (64, 4096), (45, 2048)])
+@pytest.mark.parametrize("n_rows,in_dim", [(64, 256), (65, 768), (130, 4096), (45, 2048)])
 def test_tile_roundtrip(gpu, n_rows, in_dim):
     raw = synth.iq3xxs_matrix(42, n_rows, n_rows, in_dim)
-    t16 = G.tile(dev(raw.reshape(-1), gpu), n_rows, in_dim)
-    assert t16.numel() == ((n_rows + 15) // 16) * 16 * in_dim // 256 * 98
-    back = host(G.untile(t16, n_rows, in_dim))
+    t64 = G.tile(dev(raw.reshape(-1), gpu), n_rows, in_dim)
+    assert t64.numel() == ((n_rows + 63) // 64) * 64 * in_dim // 256 * 98
+    back = host(G.untile(t64, n_rows, in_dim))
     assert np.array_equal(back, raw.reshape(-1))
 
 
 def test_tile_record_layout(gpu):
-    """One record checked field by field against the layout definition."""
-    n_rows, in_dim = 16, 512
+    """One record checked field by field against the layout definition;
+    padding rows of the partial tile are zero bytes."""
+    n_rows, in_dim = 50, 512
     raw = synth.iq3xxs_matrix(43, 0, n_rows, in_dim)
-    t16 = host(G.tile(dev(raw.reshape(-1), gpu), n_rows, in_dim))
+    t64 = host(G.tile(dev(raw.reshape(-1), gpu), n_rows, in_dim))
     L = G.lib()
-    rec = t16[1568:2 * 1568]  # tile 0, block 1
-    for j in range(2):
-        for lane in range(64):
-            n, g = lane % 16, lane // 16
-            ib = 4 * j + g
-            blk = raw[n, 98:196]
-            unit = rec[j * 768 + lane * 12: j * 768 + lane * 12 + 12]
-            assert np.array_equal(unit[:8], blk[2 + 8 * ib: 10 + 8 * ib])
+    rec = t64[6272:2 * 6272]  # tile 0, block 1
+    for n in range(64):
+        seq = np.concatenate([rec[u * 1024 + 16 * n: u * 1024 + 16 * n + 16] for u in range(6)]).view("<u4")
+        d = rec[6144 + 2 * n: 6146 + 2 * n]
+        if n >= n_rows:
+            assert not seq.any() and not d.any()
+            continue
+        blk = raw[n, 98:196]
+        assert np.array_equal(d, blk[0:2])
+        for ib in range(8):
+            assert seq[3 * ib: 3 * ib + 2].tobytes() == blk[2 + 8 * ib: 10 + 8 * ib].tobytes()
             aux = int(np.frombuffer(blk[66 + 4 * ib: 70 + 4 * ib].tobytes(), "<u4")[0])
-            assert int(np.frombuffer(unit[8:].tobytes(), "<u4")[0]) == L.gpeed_t16_aux_word(aux)
-    for n in range(16):
-        assert np.array_equal(rec[1536 + 2 * n: 1538 + 2 * n], raw[n, 98:100])
+            assert int(seq[3 * ib + 2]) == L.gpeed_t64_aux_word(aux)
 
 
-# ------------------------------------------------------------------ matvec
+# ------------------------------------------------------------------ GEMV
 
 def run_matvec(gpu, w, n_rows, in_dim, row0, out_dim, x):
-    t16 = G.tile(dev(w.reshape(-1), gpu), n_rows, in_dim)
-    return host(G.matvec(t16, n_rows, row0, in_dim, out_dim, dev(x, gpu)))
+    t64 = G.tile(dev(w.reshape(-1), gpu), n_rows, in_dim)
+    return host(G.matvec(t64, n_rows, row0, in_dim, out_dim, dev(x, gpu)))
 
 
 def test_matvec_golden(gpu):
+    """Fixture written by the reference's own WeightStore (oracle/_ref)."""
     z = np.load(os.path.join(GOLD, "matvec.npz"))
-    y = run_matvec(gpu, z["w"], 48, 1024, 16, 32, z["x"])
-    e = rel_err(y, z["y_row16"])
+    y = run_matvec(gpu, z["w"], 48, 1024, 0, 48, z["x"])
+    e = rel_err(y[16:48], z["y_row16"])
+    assert e < TIGHT, e
+    t64 = G.tile(dev(z["w"].reshape(-1), gpu), 48, 1024)
+    Y = host(G.matmul(t64, 48, 0, 1024, 48, dev(z["X"], gpu)))
+    e = rel_err(Y[:, 8:40], z["Y_row8"])
     assert e < TIGHT, e
 
 
 @pytest.mark.parametrize("n_rows,in_dim,row0,out_dim", [
     (4096, 4096, 0, 4096),    # single IQ3_XXS GEMV, 4096 x 4096
-    (64, 256, 16, 48),        # one block per row
+    (64, 256, 0, 64),         # one block per row
     (35, 768, 0, 35),         # 3 blocks per row, partial last tile
-    (80, 1280, 32, 40),       # 5 blocks, row0 inside the tensor, partial tile
+    (200, 1280, 64, 100),     # row0 inside the tensor, partial tile
+    (300, 512, 128, 172),     # ends on the tensor's partial last tile
     (16, 2048, 0, 16),
 ])
 def test_matvec_shapes(gpu, n_rows, in_dim, row0, out_dim):
@@ -141,10 +149,11 @@ def test_matvec_activation_range(gpu, scale):
 
 
 @pytest.mark.parametrize("n_rows,in_dim,row0,out_dim", [
-    (48, 20480, 16, 32),      # 80 blocks: activation read from global memory
-    (33000, 256, 0, 33000),   # 2063 tiles: more groups than workgroups, groups loop
+    (128, 20480, 64, 64),     # 80 blocks per row, one tile cut into many chunks
+    (128, 12288, 0, 128),     # 96 records over 96 workgroups: 48 partials per tile
+    (33000, 256, 0, 33000),   # 516 one-block tiles, several tiles per chunk
 ])
-def test_matvec_large_k_and_many_tiles(gpu, n_rows, in_dim, row0, out_dim):
+def test_matvec_split_and_many_tiles(gpu, n_rows, in_dim, row0, out_dim):
     w = synth.iq3xxs_matrix(59, 0, n_rows, in_dim)
     x = synth.normal(59, 1, in_dim)
     y = run_matvec(gpu, w, n_rows, in_dim, row0, out_dim, x)
@@ -152,22 +161,58 @@ def test_matvec_large_k_and_many_tiles(gpu, n_rows, in_dim, row0, out_dim):
     assert e < TIGHT, e
 
 
-def test_matvec2_shared_activation(gpu):
+def test_gemv_deterministic_and_workspace_reset(gpu):
+    """Shared tiles are summed in chunk order (bitwise repeatable) and every
+    launch leaves the workspace tickets at zero."""
+    import torch
+
+    n_rows, in_dim = 6144, 12288
+    w = synth.iq3xxs_matrix(61, 0, n_rows, in_dim)
+    t64 = G.tile(dev(w.reshape(-1), gpu), n_rows, in_dim)
+    x = synth.normal(61, 1, in_dim)
+    act = G.prep_act(dev(x, gpu), G.act_buffer(in_dim, 1, gpu))
+    ws = G.gemv_workspace(in_dim, n_rows, 1, 1, gpu)
+    ys = [host(G.gemv_act(t64, n_rows, 0, in_dim, n_rows, act, 1, ws=ws)) for _ in range(3)]
+    assert all(np.array_equal(ys[0].view(np.uint32), y.view(np.uint32)) for y in ys[1:])
+    torch.cuda.synchronize()
+    n_tiles = n_rows // 64
+    assert not host(ws[:4 * n_tiles]).any()
+    assert rel_err(ys[0][0], oracle.matvec(w, 0, in_dim, n_rows, x)) < TIGHT
+
+
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 4, 5, 6, 7, 8, 11])
+def test_matmul_tokens(gpu, n_tok):
+    """matmul_quant (weights.cpp:86-165): Y[t] = W X[t]; row t equals the
+    token's own matvec up to accumulation order."""
+    n_rows, in_dim = 200, 1536
+    w = synth.iq3xxs_matrix(62, n_tok, n_rows, in_dim)
+    X = np.stack([synth.normal(62, 100 + t, in_dim) * np.float32(1 + t) for t in range(n_tok)])
+    t64 = G.tile(dev(w.reshape(-1), gpu), n_rows, in_dim)
+    Y = host(G.matmul(t64, n_rows, 64, in_dim, 136, dev(X, gpu)))
+    ref = oracle.matmul(w, 64, in_dim, 136, X)
+    for t in range(n_tok):
+        e = rel_err(Y[t], ref[t])
+        assert e < TIGHT, (t, e)
+
+
+def test_gemv2_shared_activation(gpu):
     n_rows, in_dim = 200, 1536
     wa = synth.iq3xxs_matrix(60, 0, n_rows, in_dim)
     wb = synth.iq3xxs_matrix(60, 1, n_rows, in_dim)
-    x = synth.normal(60, 2, in_dim)
+    X = np.stack([synth.normal(60, 2, in_dim), synth.normal(60, 3, in_dim)])
     ta = G.tile(dev(wa.reshape(-1), gpu), n_rows, in_dim)
     tb = G.tile(dev(wb.reshape(-1), gpu), n_rows, in_dim)
-    act = G.prep_act(dev(x, gpu), G.act_buffer(in_dim, gpu))
-    ya, yb = G.matvec2_act(ta, tb, n_rows, 16, in_dim, 180, act)
-    assert rel_err(host(ya), oracle.matvec(wa, 16, in_dim, 180, x)) < TIGHT
-    assert rel_err(host(yb), oracle.matvec(wb, 16, in_dim, 180, x)) < TIGHT
+    act = G.prep_act(dev(X, gpu), G.act_buffer(in_dim, 2, gpu))
+    ya, yb = G.gemv2_act(ta, tb, n_rows, 64, in_dim, 136, act, 2)
+    ra, rb = oracle.matmul(wa, 64, in_dim, 136, X), oracle.matmul(wb, 64, in_dim, 136, X)
+    for t in range(2):
+        assert rel_err(host(ya)[t], ra[t]) < TIGHT
+        assert rel_err(host(yb)[t], rb[t]) < TIGHT
 
 
 def test_matvec_zero_activation(gpu):
-    w = synth.iq3xxs_matrix(52, 0, 32, 512)
-    y = run_matvec(gpu, w, 32, 512, 0, 32, np.zeros(512, np.float32))
+    w = synth.iq3xxs_matrix(52, 0, 64, 512)
+    y = run_matvec(gpu, w, 64, 512, 0, 64, np.zeros(512, np.float32))
     assert np.all(y == 0)
 
 
@@ -194,58 +239,71 @@ def test_matvec_raw(gpu):
 def test_matvec_errors(gpu):
     import torch
 
-    w = synth.iq3xxs_matrix(55, 0, 32, 512)
-    t16 = G.tile(dev(w.reshape(-1), gpu), 32, 512)
+    w = synth.iq3xxs_matrix(55, 0, 128, 512)
+    t64 = G.tile(dev(w.reshape(-1), gpu), 128, 512)
     x = torch.zeros(512, device=gpu)
     with pytest.raises(G.GpeedError) as e:
-        G.matvec(t16, 32, 8, 512, 16, x)
+        G.matvec(t64, 128, 16, 512, 16, x)
     assert e.value.code == -6
     with pytest.raises(G.GpeedError) as e:
-        G.matvec(t16, 32, 16, 512, 32, x)
+        G.matvec(t64, 128, 64, 512, 65, x)
     assert e.value.code == -1
     with pytest.raises(G.GpeedError) as e:
-        G.matvec(t16, 32, 0, 500, 16, x)
+        G.matvec(t64, 128, 0, 500, 16, x)
     assert e.value.code == -3
     with pytest.raises(G.GpeedError) as e:
-        G.matvec(t16, 32, 0, 512, 16, x, ws=torch.empty(16, dtype=torch.uint8, device=gpu))
+        G.matvec(t64, 128, 0, 512, 16, x, ws=torch.zeros(256, dtype=torch.uint8, device=gpu))
     assert e.value.code == -7
-    # out_dim <= 0 returns without touching dst (weights.cpp:88 semantics)
-    G.matvec(t16, 32, 0, 512, 0, x, out=torch.empty(1, device=gpu))
+    act = G.act_buffer(512, 8, gpu)
+    with pytest.raises(G.GpeedError) as e:
+        G.gemv_act(t64, 128, 0, 512, 64, act, 9, ws=torch.zeros(1 << 20, dtype=torch.uint8, device=gpu))
+    assert e.value.code == -1
+    # out_dim <= 0 / n_tok <= 0 return without touching dst (weights.cpp:88)
+    G.matvec(t64, 128, 0, 512, 0, x, out=torch.empty(1, device=gpu))
 
 
-def test_dense_mlp_step(gpu):
-    """dense_mlp (model.cpp:677-690): gate/up share one prepared activation,
-    SwiGLU fused into the down projection's activation prep."""
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_dense_mlp_step(gpu, n_tok):
+    """dense_mlp / dense_mlp_batch (model.cpp:677-690, model_batch.cpp:145-163):
+    gate/up share one prepared activation, SwiGLU fused into the down
+    projection's activation prep."""
     import torch
 
     H, I = 1024, 2048
     wg = synth.iq3xxs_matrix(56, 0, I, H)
     wu = synth.iq3xxs_matrix(56, 1, I, H)
     wd = synth.iq3xxs_matrix(56, 2, H, I)
-    x = synth.normal(56, 9, H) * np.float32(4.0)
+    X = np.stack([synth.normal(56, 9 + t, H) * np.float32(4.0) for t in range(n_tok)])
     tg, tu, td = (G.tile(dev(a.reshape(-1), gpu), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I)))
-    act = G.act_buffer(H, gpu)
-    G.prep_act(dev(x, gpu), act)
-    g, u = G.matvec2_act(tg, tu, I, 0, H, I, act)
-    assert rel_err(host(g), oracle.matvec(wg, 0, H, I, x)) < TIGHT
-    assert rel_err(host(u), oracle.matvec(wu, 0, H, I, x)) < TIGHT
-    act2 = G.act_buffer(I, gpu)
+    act = G.act_buffer(H, n_tok, gpu)
+    G.prep_act(dev(X, gpu), act)
+    g, u = G.gemv2_act(tg, tu, I, 0, H, I, act, n_tok)
+    for t in range(n_tok):
+        assert rel_err(host(g)[t], oracle.matvec(wg, 0, H, I, X[t])) < TIGHT
+        assert rel_err(host(u)[t], oracle.matvec(wu, 0, H, I, X[t])) < TIGHT
+    act2 = G.act_buffer(I, n_tok, gpu)
     G.prep_swiglu(g, u, act2, 10.0)
-    y = host(G.matvec_act(td, H, 0, I, H, act2))
-    ref = oracle.dense_mlp(wg, wu, wd, H, I, x[None, :], 10.0)[0]
-    e = rel_err(y, ref)
-    assert e < TOL, e
-    assert e < 1e-4, e  # silu via the device expf differs by ulps from glibc's
+    y = host(G.gemv_act(td, H, 0, I, H, act2, n_tok))
+    ref = oracle.dense_mlp(wg, wu, wd, H, I, X, 10.0)
+    for t in range(n_tok):
+        e = rel_err(y[t], ref[t])
+        assert e < TOL, e
+        assert e < 1e-4, e  # silu via the device expf differs by ulps from glibc's
     torch.cuda.synchronize()
 
 
 def test_weight_store_mirror(gpu):
-    w = synth.iq3xxs_matrix(57, 0, 64, 512)
+    w = synth.iq3xxs_matrix(57, 0, 128, 512)
     ws = G.WeightStore(device=gpu)
-    ws.add("blk.0.ffn_up.weight", w, 512, 64)
+    ws.add("blk.0.ffn_up.weight", w, 512, 128)
     x = synth.normal(57, 1, 512)
-    y = ws.matvec_quant("blk.0.ffn_up.weight", 16, 512, 32, x)
-    assert rel_err(y, oracle.matvec(w, 16, 512, 32, x)) < TIGHT
+    y = ws.matvec_quant("blk.0.ffn_up.weight", 64, 512, 32, x)
+    assert rel_err(y, oracle.matvec(w, 64, 512, 32, x)) < TIGHT
+    X = np.stack([synth.normal(57, 2 + t, 512) for t in range(5)])
+    Y = ws.matmul_quant("blk.0.ffn_up.weight", 0, 512, 100, X, 5)
+    ref = oracle.matmul(w, 0, 512, 100, X)
+    assert max(rel_err(Y[t], ref[t]) for t in range(5)) < TIGHT
+    assert ws.matmul_quant("blk.0.ffn_up.weight", 0, 512, 100, X, 0) is None
     with pytest.raises(RuntimeError, match="missing tensor"):
         ws.matvec_quant("nope", 0, 512, 16, x)
     with pytest.raises(RuntimeError, match="not block aligned"):
