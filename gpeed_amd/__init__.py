@@ -76,6 +76,11 @@ def lib():
             "gpeed_iq3xxs_gemv_ws_bytes": ([i32, i64, i64, i32], sz),
             "gpeed_iq3xxs_gemv_act": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv2_act": ([vp, vp, u64, u64, i32, i32, vp, i32, vp, vp, vp, sz, vp], i32),
+            "gpeed_moe_route_ws_bytes": ([i32, i32, i32], sz),
+            "gpeed_moe_route": ([vp, i32, i32, i32, i32, vp, C.c_float, i32, vp, vp, vp, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_moe_ws_bytes": ([i32, i32, i32, i32, i32], sz),
+            "gpeed_iq3xxs_moe_experts": ([vp, vp, vp, i32, i32, i32, vp, i32, i32, vp, vp, vp, C.c_float, vp, vp,
+                                          sz, vp], i32),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -285,6 +290,45 @@ def matvec_raw(w, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None
         out = torch.empty(out_dim, dtype=torch.float32, device=x.device)
     _check(lib().gpeed_iq3xxs_matvec_raw(_ptr(w), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out),
                                          _stream(stream)), "matvec_raw")
+    return out
+
+
+def moe_route(logits, top_k: int, mode: int = 1, bias=None, routed_scale: float = 1.0, norm_topk: bool = True,
+              ws=None, stream=None):
+    """Router top-k and stable expert buckets on the device (model_batch.cpp:178-219).
+
+    logits: [n_tok, n_exp] fp32 device tensor. Returns (eptr [n_exp+1],
+    tok [n_tok*top_k], wt [n_tok*top_k], sel [n_tok, top_k]) device tensors.
+    """
+    torch = _torch()
+    _require_cuda(logits)
+    T, E = logits.shape
+    dev_ = logits.device
+    eptr = torch.empty(E + 1, dtype=torch.int32, device=dev_)
+    tok = torch.empty(T * top_k, dtype=torch.int32, device=dev_)
+    wt = torch.empty(T * top_k, dtype=torch.float32, device=dev_)
+    sel = torch.empty(T, top_k, dtype=torch.int32, device=dev_)
+    if ws is None:
+        ws = _zeros(lib().gpeed_moe_route_ws_bytes(T, E, top_k), dev_)
+    b = C.c_void_p(0) if bias is None else _ptr(bias)
+    _check(lib().gpeed_moe_route(_ptr(logits), T, E, top_k, mode, b, routed_scale, int(norm_topk), _ptr(eptr),
+                                 _ptr(tok), _ptr(wt), _ptr(sel), _ptr(ws), ws.numel(), _stream(stream)), "moe_route")
+    return eptr, tok, wt, sel
+
+
+def moe_experts(w_gate, w_up, w_down, n_exp: int, hidden: int, inter: int, X, top_k: int, eptr, tok, wt,
+                swiglu_limit: float = 10.0, out=None, ws=None, stream=None):
+    """Routed experts (model_batch.cpp:221-262) over T64 expert tensors; Y [n_tok, hidden]."""
+    torch = _torch()
+    _require_cuda(w_gate, w_up, w_down, X, eptr, tok, wt)
+    T = X.shape[0]
+    if out is None:
+        out = torch.empty(T, hidden, dtype=torch.float32, device=X.device)
+    if ws is None:
+        ws = _zeros(lib().gpeed_iq3xxs_moe_ws_bytes(T, n_exp, top_k, hidden, inter), X.device)
+    _check(lib().gpeed_iq3xxs_moe_experts(_ptr(w_gate), _ptr(w_up), _ptr(w_down), n_exp, hidden, inter, _ptr(X), T,
+                                          top_k, _ptr(eptr), _ptr(tok), _ptr(wt), swiglu_limit, _ptr(out), _ptr(ws),
+                                          ws.numel(), _stream(stream)), "moe_experts")
     return out
 
 

@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libgpeed_iq3.so")
-SOURCES = ["capi.hip", "iq3_dequant.hip", "iq3_gemv.hip"]
+SOURCES = ["capi.hip", "iq3_dequant.hip", "iq3_gemv.hip", "iq3_moe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",

@@ -307,6 +307,61 @@ int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
     return gpeed_iq3xxs_matmul(w_t64, n_rows, row0, in_dim, out_dim, x, 1, dst, ws, ws_bytes, stream);
 }
 
+size_t gpeed_moe_route_ws_bytes(int n_tok, int n_exp, int top_k) {
+    if (n_tok < 1 || n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp) return 0;
+    return gpeed::moe_route_ws_bytes(n_tok, top_k);
+}
+
+int gpeed_moe_route(const float* logits, int n_tok, int n_exp, int top_k, int mode, const float* bias,
+                    float routed_scale, int norm_topk, int* eptr, int* tok, float* wt, int* sel, void* ws,
+                    size_t ws_bytes, gpeed_stream_t stream) {
+    if (n_tok <= 0) return GPEED_OK;
+    if (n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp)
+        return fail(GPEED_ERR_UNIMPLEMENTED, "moe_route: needs 1 <= top_k <= min(32, n_exp), n_exp <= 1024");
+    if (mode != 0 && mode != 1) return fail(GPEED_ERR_INVALID, "moe_route: mode must be 0 (sigmoid) or 1 (softmax)");
+    if ((int64_t)n_tok * top_k > (1 << 24)) return fail(GPEED_ERR_INVALID, "moe_route: too many assignments");
+    if (!logits || !eptr || !tok || !wt) return fail(GPEED_ERR_INVALID, "moe_route: null pointer");
+    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::moe_route_ws_bytes(n_tok, top_k))
+        return fail(GPEED_ERR_WORKSPACE, "moe_route: workspace missing, misaligned or too small");
+    hipError_t e = gpeed::launch_moe_route(logits, n_tok, n_exp, top_k, mode, bias, routed_scale, norm_topk, eptr,
+                                           tok, wt, sel, static_cast<uint8_t*>(ws),
+                                           static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "moe_route launch");
+}
+
+size_t gpeed_iq3xxs_moe_ws_bytes(int n_tok, int n_exp, int top_k, int hidden, int inter) {
+    if (n_tok < 1 || n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp) return 0;
+    if (!dims_ok(hidden) || !dims_ok(inter)) return 0;
+    return gpeed::moe_ws_bytes(n_tok, n_exp, top_k, hidden, inter);
+}
+
+int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w_down, int n_exp, int hidden,
+                             int inter, const float* X, int n_tok, int top_k, const int* eptr, const int* tok,
+                             const float* wt, float swiglu_limit, float* Y, void* ws, size_t ws_bytes,
+                             gpeed_stream_t stream) {
+    if (n_tok <= 0) return GPEED_OK;
+    if (hidden <= 0 || hidden % gpeed::kQK || inter <= 0 || inter % gpeed::kQK)
+        return fail(GPEED_ERR_UNALIGNED_ROW, "moe_experts: row not block aligned");
+    if (!dims_ok(hidden) || !dims_ok(inter)) return fail(GPEED_ERR_INVALID, "moe_experts: size too large");
+    if (n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp)
+        return fail(GPEED_ERR_UNIMPLEMENTED, "moe_experts: needs 1 <= top_k <= min(32, n_exp), n_exp <= 1024");
+    if ((int64_t)n_tok * top_k > (1 << 24)) return fail(GPEED_ERR_INVALID, "moe_experts: too many assignments");
+    if (!w_gate || !w_up || !w_down || !X || !eptr || !tok || !wt || !Y)
+        return fail(GPEED_ERR_INVALID, "moe_experts: null pointer");
+    if (!aligned(w_gate, 16) || !aligned(w_up, 16) || !aligned(w_down, 16) || !aligned(X, 16) || !aligned(Y, 16))
+        return fail(GPEED_ERR_INVALID, "moe_experts: weights, X and Y must be 16-byte aligned");
+    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::moe_ws_bytes(n_tok, n_exp, top_k, hidden, inter))
+        return fail(GPEED_ERR_WORKSPACE, "moe_experts: workspace missing, misaligned or too small");
+    const DeviceState* st = nullptr;
+    int rc = device_state(&st);
+    if (rc) return rc;
+    hipError_t e = gpeed::launch_moe_experts(
+        static_cast<const uint8_t*>(w_gate), static_cast<const uint8_t*>(w_up), static_cast<const uint8_t*>(w_down),
+        n_exp, hidden, inter, X, n_tok, top_k, eptr, tok, wt, swiglu_limit, Y, static_cast<uint8_t*>(ws),
+        st->num_cus, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "moe_experts launch");
+}
+
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,
                             int out_dim, const float* x, float* dst, gpeed_stream_t stream) {
     if (out_dim <= 0) return GPEED_OK;

@@ -25,9 +25,8 @@
 // (2s+1), and by d/4 times the activation block's power-of-two unscale once
 // per block. Products are exact in fp32; only the accumulation order differs
 // from the CPU path.
-#include <type_traits>
-
 #include "iq3_common.h"
+#include "iq3_gemv_core.h"
 #include "iq3_kernels.h"
 
 namespace gpeed {
@@ -135,93 +134,12 @@ struct GemvArgs {
 };
 
 template <int NT>
-struct Rec {
-    u32x4_t u[6];
-    uint32_t d;
-    u32x2_t a[GemvCfg<NT>::kPairs][4];
-};
-
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-template <int NT>
-__device__ __forceinline__ void load_rec(Rec<NT>& r, const GemvArgs& g, int rec, uint32_t lane) {
+__device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g, int rec, uint32_t lane) {
     const int per_tensor = g.n_tiles * g.nb;
     const int ten = rec >= per_tensor ? 1 : 0;
     const int rl = rec - ten * per_tensor;
-    const uint8_t* base = g.w[ten] + (size_t)rl * kRecordBytes;
-#pragma unroll
-    for (int i = 0; i < 6; ++i)
-        r.u[i] = *reinterpret_cast<const u32x4_t*>(base + i * kUnitBytes + lane * 16u);
-    r.d = *reinterpret_cast<const uint16_t*>(base + kRecordDOffset + lane * 2u);
     const int b = rl - (rl / g.nb) * g.nb;
-    const uint8_t* ab = g.act + (size_t)b * NT * 1024;
-#pragma unroll
-    for (int p = 0; p < GemvCfg<NT>::kPairs; ++p) {
-        const bool half = (NT & 1) && p == NT / 2;
-        if (!half) {
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-                r.a[p][a] = *reinterpret_cast<const u32x2_t*>(ab + p * 2048 + a * 512 + lane * 8u);
-        } else {
-            // rows 2, 3 of a single-token pair are never read back
-            const uint32_t off = ((lane >> 2) * 2 + (lane & 1)) * 8u;
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-                r.a[p][a] = *reinterpret_cast<const u32x2_t*>(ab + p * 2048 + a * 256 + off);
-        }
-    }
-}
-
-// Compile-time loop (the MFMA broadcast block ABID is an instruction field).
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<I + 1, N>(f);
-    }
-}
-
-// One record: lane n's 256 weights of row n against NT activation blocks;
-// blk[t] += (2s+1) * partial, per sub-block.
-template <int NT>
-__device__ __forceinline__ void record_dot(const uint8_t* tbl, const Rec<NT>& r, uint32_t lb,
-                                           float (&blk)[NT]) {
-    constexpr int NP = GemvCfg<NT>::kPairs;
-    const uint32_t* dw = reinterpret_cast<const uint32_t*>(&r.u[0]);
-    static_for<0, 8>([&](auto ibc) {
-        constexpr int ib = decltype(ibc)::value;
-        const uint32_t q0 = dw[3 * ib], q1 = dw[3 * ib + 1], w = dw[3 * ib + 2];
-        const uint32_t sw = t64_full_signs(w);
-        const float sc = (float)((w >> 27) | 1u);  // 2s+1
-        float4_t D[NP];
-#pragma unroll
-        for (int p = 0; p < NP; ++p) D[p] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        static_for<0, 8>([&](auto mc) {
-            constexpr int m = decltype(mc)::value;
-            const uint32_t q = m < 4 ? q0 : q1;
-            constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
-            const uint32_t addr = __builtin_amdgcn_perm(q, lb, sel);  // (idx << 8) | lb
-            const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
-            constexpr int l = m >> 1, h = m & 1;
-            constexpr int a0 = 4 * (2 * h) + l, a1 = 4 * (2 * h + 1) + l;  // sign-bit pairs
-            const uint32_t bx = (__builtin_amdgcn_alignbit(sw, sw, (a0 + 17) & 31) & 0x80008000u) | g.x;
-            const uint32_t by = (__builtin_amdgcn_alignbit(sw, sw, (a1 + 17) & 31) & 0x80008000u) | g.y;
-            const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
-#pragma unroll
-            for (int p = 0; p < NP; ++p)
-                D[p] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, r.a[p][ib >> 1]), B, D[p],
-                                                          4, 8 * (ib & 1) + m, 0);
-        });
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            blk[2 * p] = fmaf(sc, D[p][0] + D[p][1], blk[2 * p]);
-            if (2 * p + 1 < NT) blk[2 * p + 1] = fmaf(sc, D[p][2] + D[p][3], blk[2 * p + 1]);
-        }
-    });
+    load_record<(NT + 1) / 2>(r, g.w[ten] + (size_t)rl * kRecordBytes, g.act + (size_t)b * NT * 1024, lane, NT);
 }
 
 template <int NT>
@@ -229,6 +147,7 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
     constexpr int W = GemvCfg<NT>::kWaves;
     constexpr int PF = GemvCfg<NT>::kPF;
     constexpr int S = GemvCfg<NT>::kSlots;
+    constexpr int NP = GemvCfg<NT>::kPairs;
     constexpr int kThreads = W * 64;
     __shared__ __attribute__((aligned(16))) uint8_t tbl[kGridTableBytes];
     __shared__ float red[S][W][NT][64];
@@ -246,29 +165,12 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
 
     // The codebook words go out first, then the records; the table is built
     // while the records are in flight (the loads complete in issue order).
-    constexpr int kGridPer = (1024 + kThreads - 1) / kThreads;
-    uint32_t gv[kGridPer];
-#pragma unroll
-    for (int i = 0; i < kGridPer; ++i) gv[i] = kIq3xxsGrid[((tid + i * kThreads) >> 2) & 255];
-    Rec<NT> ring[PF];
+    GridWords<kThreads> gw;
+    grid_words<kThreads>(gw, tid);
+    Rec<NP> ring[PF];
 #pragma unroll
     for (int s = 0; s < PF; ++s) load_rec<NT>(ring[s], g, min(c0 + wave + s * W, c1 - 1), lane);
-
-#pragma unroll
-    for (int i = 0; i < kGridPer; ++i) {
-        const int it = tid + i * kThreads;
-        if (it < 1024) {
-            const int idx = it >> 2, q4 = it & 3;
-            const uint32_t v = gv[i];
-            const uint32_t h01 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)(v & 255u)) |
-                                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)((v >> 8) & 255u)) << 16);
-            const uint32_t h23 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)((v >> 16) & 255u)) |
-                                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)(v >> 24)) << 16);
-            u32x4_t* dst = reinterpret_cast<u32x4_t*>(tbl + (idx << 8) + q4 * 64);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dst[j] = u32x4_t{h01, h23, h01, h23};
-        }
-    }
+    grid_table_store<kThreads>(tbl, gw, tid);
     for (int i = tid; i < S * W * NT * 64; i += kThreads) (&red[0][0][0][0])[i] = 0.0f;
     lds_barrier();
 
@@ -298,10 +200,10 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
                 cur_slot = slot;
             }
             if (valid) {
-                float blk[NT];
+                float blk[2 * NP];
 #pragma unroll
-                for (int t = 0; t < NT; ++t) blk[t] = 0.0f;
-                record_dot<NT>(tbl, ring[s], lb, blk);
+                for (int t = 0; t < 2 * NP; ++t) blk[t] = 0.0f;
+                record_dot<NP>(tbl, ring[s], lb, blk);
                 const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)ring[s].d) * 0.25f;
                 const float* xs = g.xsc + (size_t)b * NT;
 #pragma unroll

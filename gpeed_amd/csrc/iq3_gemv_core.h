@@ -1,0 +1,140 @@
+// Device building blocks shared by the GEMV kernels over the T64 layout:
+// the LDS grid table, one record's loads (weights + activation images) and
+// its decode-and-multiply with v_mfma_f32_4x4x4_16b_f16.
+#pragma once
+
+#include <type_traits>
+
+#include "iq3_common.h"
+
+namespace gpeed {
+
+// Compile-time loop (the MFMA broadcast block ABID is an instruction field).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// Workgroup barrier that orders LDS only: outstanding global loads (the
+// record ring) stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The replicated grid table, built by a workgroup of kThreads threads: the
+// codebook words are fetched first (grid_words), the LDS writes done later
+// (grid_table_store) so that loads issued in between stay in flight.
+template <int kThreads>
+struct GridWords {
+    static constexpr int kPer = (1024 + kThreads - 1) / kThreads;
+    uint32_t v[kPer];
+};
+
+template <int kThreads>
+__device__ __forceinline__ void grid_words(GridWords<kThreads>& gw, int tid) {
+#pragma unroll
+    for (int i = 0; i < GridWords<kThreads>::kPer; ++i)
+        gw.v[i] = kIq3xxsGrid[((tid + i * kThreads) >> 2) & 255];
+}
+
+__device__ __forceinline__ uint32_t f16_pair_of_bytes(uint32_t lo, uint32_t hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)hi) << 16);
+}
+
+// Entry idx, replica r at byte (idx << 8) | (r << 3): 4 unsigned fp16.
+template <int kThreads>
+__device__ __forceinline__ void grid_table_store(uint8_t* tbl, const GridWords<kThreads>& gw, int tid) {
+#pragma unroll
+    for (int i = 0; i < GridWords<kThreads>::kPer; ++i) {
+        const int it = tid + i * kThreads;
+        if (it < 1024) {
+            const int idx = it >> 2, q4 = it & 3;
+            const uint32_t v = gw.v[i];
+            const uint32_t h01 = f16_pair_of_bytes(v & 255u, (v >> 8) & 255u);
+            const uint32_t h23 = f16_pair_of_bytes((v >> 16) & 255u, v >> 24);
+            u32x4_t* dst = reinterpret_cast<u32x4_t*>(tbl + (idx << 8) + q4 * 64);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[j] = u32x4_t{h01, h23, h01, h23};
+        }
+    }
+}
+
+// One record as a lane holds it: its row's 24 dwords and d, and the NP
+// activation register images (token pairs) of the record's block.
+template <int NP>
+struct Rec {
+    u32x4_t u[6];
+    uint32_t d;
+    u32x2_t a[NP][4];
+};
+
+// rec: the record; ab: its block's prepared activation (n_tok vectors,
+// 2*NP - 1 <= n_tok <= 2*NP). The loads do not depend on a branch, so the
+// compiler can wait for one ring slot at a time.
+template <int NP>
+__device__ __forceinline__ void load_record(Rec<NP>& r, const uint8_t* rec, const uint8_t* ab,
+                                            uint32_t lane, int n_tok) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+        r.u[i] = *reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u);
+    r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
+    // a last pair holding one token stores rows 0, 1 only (256-byte images);
+    // rows 2, 3 then read a duplicate and are never used
+    const uint32_t off_half = ((lane >> 2) * 2 + (lane & 1)) * 8u;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const bool half = (p == NP - 1) && (n_tok & 1);
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const uint32_t off = half ? a * 256u + off_half : a * 512u + lane * 8u;
+            r.a[p][a] = *reinterpret_cast<const u32x2_t*>(ab + p * 2048 + off);
+        }
+    }
+}
+
+// One record: lane n's 256 weights of row n against the NP token pairs;
+// blk[t] += (2s+1) * partial, per sub-block (blk[2p+1] of a single-token
+// last pair is meaningless).
+template <int NP>
+__device__ __forceinline__ void record_dot(const uint8_t* tbl, const Rec<NP>& r, uint32_t lb,
+                                           float (&blk)[2 * NP]) {
+    const uint32_t* dw = reinterpret_cast<const uint32_t*>(&r.u[0]);
+    static_for<0, 8>([&](auto ibc) {
+        constexpr int ib = decltype(ibc)::value;
+        const uint32_t q0 = dw[3 * ib], q1 = dw[3 * ib + 1], w = dw[3 * ib + 2];
+        const uint32_t sw = t64_full_signs(w);
+        const float sc = (float)((w >> 27) | 1u);  // 2s+1
+        float4_t D[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) D[p] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        static_for<0, 8>([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            const uint32_t q = m < 4 ? q0 : q1;
+            constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
+            const uint32_t addr = __builtin_amdgcn_perm(q, lb, sel);  // (idx << 8) | lb
+            const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
+            constexpr int l = m >> 1, h = m & 1;
+            constexpr int a0 = 4 * (2 * h) + l, a1 = 4 * (2 * h + 1) + l;  // sign-bit pairs
+            const uint32_t bx = (__builtin_amdgcn_alignbit(sw, sw, (a0 + 17) & 31) & 0x80008000u) | g.x;
+            const uint32_t by = (__builtin_amdgcn_alignbit(sw, sw, (a1 + 17) & 31) & 0x80008000u) | g.y;
+            const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                D[p] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, r.a[p][ib >> 1]), B, D[p],
+                                                          4, 8 * (ib & 1) + m, 0);
+        });
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            blk[2 * p] = fmaf(sc, D[p][0] + D[p][1], blk[2 * p]);
+            blk[2 * p + 1] = fmaf(sc, D[p][2] + D[p][3], blk[2 * p + 1]);
+        }
+    });
+}
+
+}  // namespace gpeed

@@ -50,4 +50,20 @@ hipError_t launch_matvec_raw(const uint8_t* w, int in_dim, unsigned long long ro
                              const float* x, float* y, hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, float* dst, int n, hipStream_t s);
 
+// Router (model_batch.cpp:178-219) on the device: top-k per token of
+// logits [T][E], then the stable expert buckets eptr[E+1], tok[T*K],
+// wt[T*K] (and the per-token ranked choices sel[T*K] if sel != null).
+// ws: moe_route_ws_bytes(T, K) bytes of scratch.
+size_t moe_route_ws_bytes(int T, int K);
+hipError_t launch_moe_route(const float* logits, int T, int E, int K, int mode, const float* bias,
+                            float routed_scale, int norm_topk, int* eptr, int* tok, float* wt, int* sel,
+                            uint8_t* ws, hipStream_t s);
+// Routed experts (model_batch.cpp:221-262): gate/up/down of every touched
+// expert over its bucket of tokens, SwiGLU between, weighted combine into
+// Y [T][H] (overwritten). ws: moe_ws_bytes(...) bytes of scratch.
+size_t moe_ws_bytes(int T, int E, int K, int H, int I);
+hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int E, int H,
+                              int I, const float* X, int T, int K, const int* eptr, const int* tok,
+                              const float* wt, float lim, float* Y, uint8_t* ws, int num_cus, hipStream_t s);
+
 }  // namespace gpeed

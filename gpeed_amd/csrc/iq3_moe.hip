@@ -1,0 +1,512 @@
+// Routed-expert (MoE) path on the GPU (gfx950), model_batch.cpp:165-262.
+//
+// k_moe_route    router top-k per token, expert histogram, exclusive scan and
+//                a stable scatter of the (token, k) assignments into expert
+//                buckets: eptr / tok / wt exactly as the CPU builds them.
+// k_moe_plan     expert buckets -> work segments of at most 8 tokens, the
+//                segment of every bucket slot, each token's slots in expert
+//                order; zeroes the work counters.
+// k_prep_grouped gathers each slot's activation (MODE 0: X[tok], MODE 1:
+//                SwiGLU of the gate/up rows) into its segment's prepared
+//                activation.
+// k_gemv_grouped ragged grouped GEMV: a wavefront takes (segment, tensor,
+//                tile) items from an atomic counter and streams the tile's
+//                records over the whole row (no partial sums leave it).
+// k_moe_combine  Y[t] = sum over the token's slots, in expert order, of
+//                wt * down row (one fma per term, like axpy_f32).
+#include <climits>
+
+#include "iq3_common.h"
+#include "iq3_gemv_core.h"
+#include "iq3_kernels.h"
+
+namespace gpeed {
+
+namespace {
+
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopK = 32;
+constexpr int kSegTok = 8;
+
+// ---------------------------------------------------------------------------
+// Router
+
+// (key, id) rank order: larger key first, equal keys lower id first.
+__device__ __forceinline__ bool ranks_before(float ka, int a, float kb, int b) {
+    return ka > kb || (ka == kb && a < b);
+}
+
+__global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ logits, int T, int E, int K,
+                                                    int mode, const float* __restrict__ bias,
+                                                    float routed_scale, int norm_topk, int* __restrict__ eptr,
+                                                    int* __restrict__ tok, float* __restrict__ wt,
+                                                    int* __restrict__ sel, int* __restrict__ asg_e,
+                                                    float* __restrict__ asg_w) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int cursor[kMaxExperts];
+    __shared__ int chunk_e[1024];
+    __shared__ float rank_score[16][kMaxTopK];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+    __syncthreads();
+
+    // 1. top-k per token (one wavefront per token); lane l holds experts l + 64j
+    constexpr int J = kMaxExperts / 64;
+    for (int t = wave; t < T; t += 16) {
+        float key[J], sc[J];
+        unsigned taken = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int e = lane + 64 * j;
+            key[j] = -__builtin_inff();
+            sc[j] = 0.0f;
+            if (e < E) {
+                const float l = logits[(size_t)t * E + e];
+                if (mode == 0) {
+                    sc[j] = 1.0f / (1.0f + expf(-l));
+                    key[j] = sc[j] + (bias ? bias[e] : 0.0f);
+                } else {
+                    sc[j] = l;
+                    key[j] = l;
+                }
+                // a NaN key ranks last (it still ranks, so every pick is an expert)
+                if (__builtin_isnan(key[j])) key[j] = -__builtin_inff();
+            }
+        }
+        for (int k = 0; k < K; ++k) {
+            float bk = -__builtin_inff(), bs = 0.0f;
+            int be = INT_MAX;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int e = lane + 64 * j;
+                if (e < E && !((taken >> j) & 1u) && ranks_before(key[j], e, bk, be)) {
+                    bk = key[j];
+                    be = e;
+                    bs = sc[j];
+                }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ok = __shfl_xor(bk, off);
+                const int oe = __shfl_xor(be, off);
+                const float os = __shfl_xor(bs, off);
+                if (ranks_before(ok, oe, bk, be)) {
+                    bk = ok;
+                    be = oe;
+                    bs = os;
+                }
+            }
+            if ((be & 63) == lane) taken |= 1u << (be >> 6);
+            if (lane == 0) {
+                rank_score[wave][k] = bs;
+                asg_e[(size_t)t * K + k] = be;
+                if (sel) sel[(size_t)t * K + k] = be;
+                atomicAdd(&cnt[be], 1);
+            }
+        }
+        if (lane == 0) {
+            // combine weights, summed in rank order (model_batch.cpp:195-200)
+            if (mode == 0) {
+                float denom = 1e-20f;
+                for (int k = 0; k < K; ++k) denom += rank_score[wave][k];
+                const float inv = norm_topk ? routed_scale / denom : routed_scale;
+                for (int k = 0; k < K; ++k) asg_w[(size_t)t * K + k] = rank_score[wave][k] * inv;
+            } else {
+                const float lmax = rank_score[wave][0];
+                float denom = 0.0f;
+                for (int k = 0; k < K; ++k) denom += expf(rank_score[wave][k] - lmax);
+                for (int k = 0; k < K; ++k) asg_w[(size_t)t * K + k] = expf(rank_score[wave][k] - lmax) / denom;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. exclusive scan of the expert counts (model_batch.cpp:205-209)
+    {
+        int run = 0;
+        if (tid == 0) {
+            for (int e = 0; e < E; ++e) {
+                const int c = cnt[e];
+                cursor[e] = run;
+                eptr[e] = run;
+                run += c;
+            }
+            eptr[E] = run;
+        }
+    }
+    __syncthreads();
+
+    // 3. stable scatter by expert (model_batch.cpp:211-219): assignment a
+    // goes to its expert's cursor plus the number of earlier assignments of
+    // that expert, found per chunk of 1024 by comparison.
+    const int N = T * K;
+    for (int c0 = 0; c0 < N; c0 += 1024) {
+        const int a = c0 + tid;
+        const int ea = a < N ? asg_e[a] : -1;
+        chunk_e[tid] = ea;
+        __syncthreads();
+        if (a < N) {
+            int rank = 0;
+            for (int j = 0; j < tid; ++j) rank += chunk_e[j] == ea;
+            const int p = cursor[ea] + rank;
+            tok[p] = a / K;
+            wt[p] = asg_w[a];
+        }
+        __syncthreads();
+        if (a < N) atomicAdd(&cursor[ea], 1);
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Work plan of the grouped products
+
+struct MoePlan {
+    int* n_seg;      // [1]
+    int* seg_e;      // [S]
+    int* seg_p0;     // [S]
+    int* seg_n;      // [S]
+    int* seg_of;     // [N] segment of bucket slot p
+    int* idx_of;     // [N] token index of slot p inside its segment
+    int* pos;        // [T][K] slots of token t, in expert order
+    uint32_t* ctr;   // [2] work counters (gate/up, down)
+};
+
+__global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr, const int* __restrict__ tok,
+                                                   int T, int E, int K, MoePlan pl) {
+    __shared__ int ep[kMaxExperts + 1];
+    __shared__ int sstart[kMaxExperts + 1];
+    const int tid = threadIdx.x;
+    for (int e = tid; e <= E; e += 1024) ep[e] = eptr[e];
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int e = 0; e < E; ++e) {
+            sstart[e] = run;
+            run += (ep[e + 1] - ep[e] + kSegTok - 1) / kSegTok;
+        }
+        sstart[E] = run;
+        *pl.n_seg = run;
+        // the grouped GEMVs take work from these with device-scope atomics
+        __hip_atomic_store(pl.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pl.ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 1024) {
+        const int g = ep[e + 1] - ep[e];
+        for (int j = 0; j * kSegTok < g; ++j) {
+            const int s = sstart[e] + j;
+            pl.seg_e[s] = e;
+            pl.seg_p0[s] = ep[e] + j * kSegTok;
+            pl.seg_n[s] = min(kSegTok, g - j * kSegTok);
+        }
+    }
+    const int N = ep[E];
+    for (int p = tid; p < N; p += 1024) {
+        int lo = 0, hi = E;  // largest e with ep[e] <= p
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (ep[mid] <= p) lo = mid; else hi = mid;
+        }
+        while (lo < E - 1 && ep[lo + 1] <= p) ++lo;  // skip empty buckets
+        const int r = p - ep[lo];
+        pl.seg_of[p] = sstart[lo] + r / kSegTok;
+        pl.idx_of[p] = r % kSegTok;
+    }
+    // each token's slots in bucket order = expert order
+    for (int t = tid; t < T; t += 1024) {
+        int c = 0;
+        for (int p = 0; p < N && c < K; ++p)
+            if (tok[p] == t) pl.pos[(size_t)t * K + c++] = p;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Activation gather / SwiGLU into per-segment prepared activations
+
+__device__ __forceinline__ size_t act_off(int n_tok, int b, int t, int a, int beta, int hl) {
+    const int p = t >> 1;
+    const bool half_pair = (n_tok & 1) && (p == (n_tok >> 1));
+    const size_t base = (size_t)b * n_tok * 1024 + (size_t)p * 2048;
+    if (half_pair) return base + a * 256 + (2 * beta + hl) * 8;
+    return base + a * 512 + (4 * beta + 2 * (t & 1) + hl) * 8;
+}
+
+// One wavefront per (slot p, block b). MODE 0: v = X[tok[p]]; MODE 1:
+// v = silu(min(G[p],lim)) * clamp(U[p],-lim,lim).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_prep_grouped(const float* __restrict__ X, const float* __restrict__ U,
+                                                      const int* __restrict__ tok, const int* __restrict__ eptr,
+                                                      int E, int nb, float lim, MoePlan pl,
+                                                      uint8_t* __restrict__ act, size_t seg_stride) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + wave;
+    const int N = eptr[E];
+    if (item >= N * nb) return;
+    const int p = item / nb, b = item - p * nb;
+    const size_t row = MODE == 0 ? (size_t)tok[p] : (size_t)p;
+    const size_t src = row * nb * 256 + (size_t)b * 256 + 4 * lane;
+    const float4 v = *reinterpret_cast<const float4*>(X + src);
+    float e[4] = {v.x, v.y, v.z, v.w};
+    if (MODE == 1) {
+        const float4 u = *reinterpret_cast<const float4*>(U + src);
+        const float us[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float gi = fminf(e[c], lim);
+            const float ui = fminf(fmaxf(us[c], -lim), lim);
+            e[c] = (gi / (1.0f + expf(-gi))) * ui;
+        }
+    }
+    float m = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    int sc = 0;
+    if (m > 0.0f && m < __builtin_inff()) {
+        int ex;
+        (void)frexpf(m, &ex);
+        sc = 14 - ex;
+        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
+    }
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float xs = ldexpf(e[c], sc);
+        hi[c] = (_Float16)xs;
+        lo[c] = (_Float16)(xs - (float)hi[c]);
+    }
+    const int s = pl.seg_of[p], t = pl.idx_of[p], n = pl.seg_n[s];
+    uint8_t* base = act + (size_t)s * seg_stride;
+    const int a = lane >> 4, beta = lane & 15;
+    *reinterpret_cast<u32x2_t*>(base + act_off(n, b, t, a, beta, 0)) = __builtin_bit_cast(u32x2_t, hi);
+    *reinterpret_cast<u32x2_t*>(base + act_off(n, b, t, a, beta, 1)) = __builtin_bit_cast(u32x2_t, lo);
+    if (lane == 0) reinterpret_cast<float*>(base + (size_t)nb * n * 1024)[(size_t)b * n + t] = ldexpf(1.0f, -sc);
+}
+
+// ---------------------------------------------------------------------------
+// Ragged grouped GEMV
+
+struct GroupedArgs {
+    const uint8_t* w[2];      // T64 tensors holding every expert's rows
+    float* y[2];              // [N][rows_per_expert] per tensor, bucket order
+    const uint8_t* act;       // per-segment prepared activations
+    size_t seg_stride;
+    int n_tensors;
+    int nb;                   // blocks per row
+    int tiles;                // 64-row tiles per expert
+    int rows;                 // rows per expert (= output width)
+    MoePlan pl;
+    int ctr_index;
+};
+
+// One (segment, tensor, tile) item: the wavefront walks the tile's nb
+// records through a 2-deep ring and writes the 64 rows x n tokens result.
+template <int NP>
+__device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, uint32_t lane, const uint8_t* rec0,
+                                             const uint8_t* act, int n, int nb, float* y, int rows, int row0) {
+    constexpr int PF = 2;
+    const float* xsc = reinterpret_cast<const float*>(act + (size_t)nb * n * 1024);
+    Rec<NP> ring[PF];
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+        const int b = min(s, nb - 1);
+        load_record<NP>(ring[s], rec0 + (size_t)b * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
+    }
+    float acc[2 * NP];
+#pragma unroll
+    for (int t = 0; t < 2 * NP; ++t) acc[t] = 0.0f;
+    for (int k0 = 0; k0 < nb; k0 += PF) {
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+            const int k = k0 + s;
+            if (k < nb) {
+                float blk[2 * NP];
+#pragma unroll
+                for (int t = 0; t < 2 * NP; ++t) blk[t] = 0.0f;
+                record_dot<NP>(tbl, ring[s], lb, blk);
+                const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)ring[s].d) * 0.25f;
+#pragma unroll
+                for (int t = 0; t < 2 * NP; ++t)
+                    if (t < n) acc[t] = fmaf(d4 * xsc[(size_t)k * n + t], blk[t], acc[t]);
+            }
+            const int b = min(k + PF, nb - 1);
+            load_record<NP>(ring[s], rec0 + (size_t)b * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2 * NP; ++t)
+        if (t < n) y[(size_t)t * rows + row0 + lane] = acc[t];
+}
+
+constexpr int kGroupedThreads = 256;
+
+__global__ __launch_bounds__(kGroupedThreads, 2) void k_gemv_grouped(GroupedArgs g) {
+    __shared__ __attribute__((aligned(16))) uint8_t tbl[kGridTableBytes];
+    const int tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t lb = (lane & 31u) << 3;
+    GridWords<kGroupedThreads> gw;
+    grid_words<kGroupedThreads>(gw, tid);
+    grid_table_store<kGroupedThreads>(tbl, gw, tid);
+    lds_barrier();
+    const int per_seg = g.n_tensors * g.tiles;
+    const int n_items = *g.pl.n_seg * per_seg;
+    while (true) {
+        uint32_t item = 0;
+        if (lane == 0)
+            item = __hip_atomic_fetch_add(g.pl.ctr + g.ctr_index, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        item = __builtin_amdgcn_readfirstlane(__shfl(item, 0));
+        if (item >= (uint32_t)n_items) break;
+        const int s = item / per_seg;
+        const int rem = item - s * per_seg;
+        const int ten = rem / g.tiles, tile = rem - ten * g.tiles;
+        const int e = g.pl.seg_e[s], p0 = g.pl.seg_p0[s], n = g.pl.seg_n[s];
+        const uint8_t* rec0 = g.w[ten] + ((size_t)e * g.tiles + tile) * g.nb * kRecordBytes;
+        const uint8_t* act = g.act + (size_t)s * g.seg_stride;
+        float* y = g.y[ten] + (size_t)p0 * g.rows;
+        switch ((n + 1) >> 1) {
+            case 1: grouped_tile<1>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
+            case 2: grouped_tile<2>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
+            case 3: grouped_tile<3>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
+            default: grouped_tile<4>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weighted combine (model_batch.cpp:257-261): Y[t] = sum_k wt * D[slot],
+// slots in expert order, one fma per term.
+__global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ D, const float* __restrict__ wt,
+                                                     const int* __restrict__ pos, int T, int K, int H,
+                                                     float* __restrict__ Y) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t n4 = (size_t)T * H / 4;
+    if (i >= n4) return;
+    const int t = (int)(i * 4 / H);
+    const int h = (int)(i * 4 - (size_t)t * H);
+    float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k = 0; k < K; ++k) {
+        const int p = pos[(size_t)t * K + k];
+        const float w = wt[p];
+        const float4 d = *reinterpret_cast<const float4*>(D + (size_t)p * H + h);
+        y.x = fmaf(w, d.x, y.x);
+        y.y = fmaf(w, d.y, y.y);
+        y.z = fmaf(w, d.z, y.z);
+        y.w = fmaf(w, d.w, y.w);
+    }
+    *reinterpret_cast<float4*>(Y + (size_t)t * H + h) = y;
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+struct MoeLayout {
+    size_t plan_off[8];
+    size_t act1, g, u, act2, d, total;
+    size_t stride1, stride2;
+    int seg_max;
+};
+
+MoeLayout moe_layout(int T, int E, int K, int H, int I) {
+    MoeLayout L{};
+    const size_t N = (size_t)T * K;
+    L.seg_max = (int)((N + (size_t)(kSegTok - 1) * E) / kSegTok + 1);
+    size_t off = 0;
+    const size_t sizes[8] = {256, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max,
+                             4 * N, 4 * N, 4 * N, 256};
+    for (int i = 0; i < 8; ++i) {
+        L.plan_off[i] = off;
+        off += align256(sizes[i]);
+    }
+    L.stride1 = align256((size_t)(H / kQK) * kSegTok * (1024 + 4));
+    L.stride2 = align256((size_t)(I / kQK) * kSegTok * (1024 + 4));
+    L.act1 = off; off += L.stride1 * L.seg_max;
+    L.g = off; off += align256(N * I * 4);
+    L.u = off; off += align256(N * I * 4);
+    L.act2 = off; off += L.stride2 * L.seg_max;
+    L.d = off; off += align256(N * H * 4);
+    L.total = off;
+    return L;
+}
+
+MoePlan plan_ptrs(uint8_t* ws, const MoeLayout& L) {
+    MoePlan p;
+    p.n_seg = reinterpret_cast<int*>(ws + L.plan_off[0]);
+    p.ctr = reinterpret_cast<uint32_t*>(ws + L.plan_off[7]);
+    p.seg_e = reinterpret_cast<int*>(ws + L.plan_off[1]);
+    p.seg_p0 = reinterpret_cast<int*>(ws + L.plan_off[2]);
+    p.seg_n = reinterpret_cast<int*>(ws + L.plan_off[3]);
+    p.seg_of = reinterpret_cast<int*>(ws + L.plan_off[4]);
+    p.idx_of = reinterpret_cast<int*>(ws + L.plan_off[5]);
+    p.pos = reinterpret_cast<int*>(ws + L.plan_off[6]);
+    return p;
+}
+
+}  // namespace
+
+size_t moe_route_ws_bytes(int T, int K) { return 2 * align256((size_t)T * K * 4); }
+
+hipError_t launch_moe_route(const float* logits, int T, int E, int K, int mode, const float* bias,
+                            float routed_scale, int norm_topk, int* eptr, int* tok, float* wt, int* sel,
+                            uint8_t* ws, hipStream_t s) {
+    int* asg_e = reinterpret_cast<int*>(ws);
+    float* asg_w = reinterpret_cast<float*>(ws + align256((size_t)T * K * 4));
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale,
+                       norm_topk, eptr, tok, wt, sel, asg_e, asg_w);
+    return hipGetLastError();
+}
+
+size_t moe_ws_bytes(int T, int E, int K, int H, int I) { return moe_layout(T, E, K, H, I).total; }
+
+hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int E, int H,
+                              int I, const float* X, int T, int K, const int* eptr, const int* tok,
+                              const float* wt, float lim, float* Y, uint8_t* ws, int num_cus, hipStream_t s) {
+    const MoeLayout L = moe_layout(T, E, K, H, I);
+    const MoePlan pl = plan_ptrs(ws, L);
+    const int N = T * K;
+    const int nbH = H / kQK, nbI = I / kQK;
+    float* G = reinterpret_cast<float*>(ws + L.g);
+    float* U = reinterpret_cast<float*>(ws + L.u);
+    float* D = reinterpret_cast<float*>(ws + L.d);
+    hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(1024), 0, s, eptr, tok, T, E, K, pl);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_prep_grouped<0>, dim3((N * nbH + 3) / 4), dim3(256), 0, s, X, nullptr, tok, eptr, E,
+                       nbH, 0.0f, pl, ws + L.act1, L.stride1);
+    const int grid = (num_cus > 0 ? num_cus : 256) * 2;
+    GroupedArgs ga{};
+    ga.w[0] = w_gate;
+    ga.w[1] = w_up;
+    ga.y[0] = G;
+    ga.y[1] = U;
+    ga.act = ws + L.act1;
+    ga.seg_stride = L.stride1;
+    ga.n_tensors = 2;
+    ga.nb = nbH;
+    ga.tiles = I / kTileRows;
+    ga.rows = I;
+    ga.pl = pl;
+    ga.ctr_index = 0;
+    hipLaunchKernelGGL(k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, ga);
+    hipLaunchKernelGGL(k_prep_grouped<1>, dim3((N * nbI + 3) / 4), dim3(256), 0, s, G, U, tok, eptr, E, nbI,
+                       lim, pl, ws + L.act2, L.stride2);
+    GroupedArgs gd = ga;
+    gd.w[0] = w_down;
+    gd.w[1] = w_down;
+    gd.y[0] = D;
+    gd.y[1] = D;
+    gd.act = ws + L.act2;
+    gd.seg_stride = L.stride2;
+    gd.n_tensors = 1;
+    gd.nb = nbI;
+    gd.tiles = H / kTileRows;
+    gd.rows = H;
+    gd.ctr_index = 1;
+    hipLaunchKernelGGL(k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, gd);
+    const size_t n4 = (size_t)T * H / 4;
+    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, D, wt, pl.pos, T, K, H,
+                       Y);
+    return hipGetLastError();
+}
+
+}  // namespace gpeed

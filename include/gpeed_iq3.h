@@ -136,6 +136,38 @@ int gpeed_iq3xxs_gemv2_act(const void* w_a, const void* w_b, uint64_t n_rows, ui
                            int in_dim, int out_dim, const void* act, int n_tok, float* dst_a,
                            float* dst_b, void* ws, size_t ws_bytes, gpeed_stream_t stream);
 
+/* ---- routed experts (replace Model::moe_batch steps 1-3,
+ *      model_batch.cpp:165-262) ------------------------------------------ */
+
+/* Router on the device: per token t < n_tok the top_k of logits[t][0..n_exp)
+ * (mode 0: the reference router, score = sigmoid(logit), ranked by score +
+ * bias[e] (bias may be NULL), weight = score * routed_scale / (1e-20 + sum
+ * of the top-k scores) if norm_topk else score * routed_scale,
+ * model_batch.cpp:186-203; mode 1: ranked by logit, weight = softmax over
+ * the top_k); equal keys rank the lower expert id first. Then the stable
+ * bucket sort of the (token, k) assignments by expert (model_batch.cpp:
+ * 205-219): eptr[n_exp+1] offsets, tok[n_tok*top_k] token of each bucket
+ * slot, wt[...] its weight; sel[n_tok*top_k] (optional, may be NULL) the
+ * ranked experts per token. All device arrays; integers equal the CPU's.
+ * n_exp <= 1024, top_k <= 32. ws: gpeed_moe_route_ws_bytes bytes. */
+size_t gpeed_moe_route_ws_bytes(int n_tok, int n_exp, int top_k);
+int gpeed_moe_route(const float* logits, int n_tok, int n_exp, int top_k, int mode, const float* bias,
+                    float routed_scale, int norm_topk, int* eptr, int* tok, float* wt, int* sel, void* ws,
+                    size_t ws_bytes, gpeed_stream_t stream);
+/* Routed experts for n_tok tokens X [n_tok][hidden]: for every expert e with
+ * tokens, gate/up = rows e*inter.. of w_gate / w_up (T64 copies of
+ * [n_exp*inter, hidden] tensors, ffn_gate_exps / ffn_up_exps), SwiGLU with
+ * swiglu_limit, down = rows e*hidden.. of w_down ([n_exp*hidden, inter],
+ * ffn_down_exps); Y[t] = sum over the token's experts, in expert order, of
+ * wt * down (Y overwritten; the shared expert is not included). hidden and
+ * inter are multiples of 256. eptr/tok/wt as gpeed_moe_route makes them.
+ * ws: gpeed_iq3xxs_moe_ws_bytes bytes (no zero-fill needed). */
+size_t gpeed_iq3xxs_moe_ws_bytes(int n_tok, int n_exp, int top_k, int hidden, int inter);
+int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w_down, int n_exp, int hidden,
+                             int inter, const float* X, int n_tok, int top_k, const int* eptr, const int* tok,
+                             const float* wt, float swiglu_limit, float* Y, void* ws, size_t ws_bytes,
+                             gpeed_stream_t stream);
+
 /* Same product as gpeed_iq3xxs_matvec straight from GGUF rows (no tiling;
  * any row0), one wavefront per row. */
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,
