@@ -1,24 +1,29 @@
 #!/usr/bin/env python3
-"""IQ3_XXS decode benchmark on one MI355X.
+"""IQ3_XXS dequantize-and-multiply benchmark on one MI355X.
 
-Workload: the dense-layer decode step at batch 1 (dense_mlp, model.cpp:677-690)
-with IQ3_XXS weights gate/up 12288x6144 (K=6144) and down 6144x12288
-(K=12288): prepare x, gate and up matvecs sharing the prepared activation,
-SwiGLU fused into the down projection's activation prep, down matvec.
-Weights are synthetic (seeded, the block distribution of gpeed_amd.synth),
-x ~ N(0,1) fp32, resident in HBM before timing. To measure HBM rather than
-the 256 MB Infinity Cache, `--copies` distinct copies of the three tensors
-(default 8, 694 MB) are rotated step by step.
+Headline workload (value / metric): the dense-layer decode step at batch 1
+(dense_mlp, model.cpp:677-690) with IQ3_XXS weights gate/up 12288x6144
+(K=6144) and down 6144x12288 (K=12288): prepare x, one launch for gate and
+up sharing the prepared activation, SwiGLU fused into the down projection's
+activation prep, down. Weights are synthetic (seeded, the block distribution
+of gpeed_amd.synth), x ~ N(0,1) fp32, resident in HBM before timing. To
+measure HBM rather than the 256 MB Infinity Cache, `--copies` distinct
+copies of the three tensors (default 8, 694 MB) are rotated step by step.
 
 value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
-roofline = the GEMV kernel (k_gemv_t64, launched once for gate+up and
-once for down per step): algorithmic bytes of its launches (packed W +
-prepared activation + outputs) / their summed duration, each launch timed
-with HIP events on the launch stream during the timed steps, against 8 TB/s.
+roofline = the GEMV kernel (k_gemv_t64: one gate+up launch and one down
+launch per step): algorithmic bytes of a gate+up + down launch pair (packed
+W + prepared activation + outputs) / the pair's duration, timed with HIP
+events on the launch stream around replays of a HIP graph holding only
+those launches (all copies in turn, so still HBM-bound).
 cpu_baseline = the reference's own CPU path (oracle/_ref: WeightStore::
 matvec_quant compiled from the reference sources, single-threaded as the
 reference builds on Linux) on one full step of the same workload; the
 oracle's C restatement stands in if oracle/_ref was not built.
+
+Secondary line items (same JSON object, key "extra"): the routed-expert
+decode batch (64 experts of gate/up 2048x6144 and down 6144x2048, 32
+tokens, softmax top-8: GB/s over the packed bytes of the touched experts).
 """
 from __future__ import annotations
 
@@ -103,6 +108,62 @@ def cpu_baseline(wg, wu, wd, x):
     return out, y_ref
 
 
+def moe_decode(torch, G, synth, dev, steps, warmup):
+    """Routed-expert decode batch: route + grouped gate/up + SwiGLU + grouped down + combine."""
+    E, T, K, HM, IM = 64, 32, 8, 6144, 2048
+    log("moe: generating 64 experts")
+    tens = []
+    for i, (r, c) in enumerate(((E * IM, HM), (E * IM, HM), (E * HM, IM))):
+        raw = torch.from_numpy(synth.iq3xxs_matrix(2025, i, r, c).reshape(-1)).to(dev)
+        tens.append(G.tile(raw, r, c))
+        del raw
+    X = torch.from_numpy(synth.normal(2025, 10, T * HM).reshape(T, HM)).to(dev)
+    logits = torch.from_numpy(synth.normal(2025, 11, T * E).reshape(T, E)).to(dev)
+    ws_r = torch.zeros(G.lib().gpeed_moe_route_ws_bytes(T, E, K), dtype=torch.uint8, device=dev)
+    ws_e = torch.zeros(G.lib().gpeed_iq3xxs_moe_ws_bytes(T, E, K, HM, IM), dtype=torch.uint8, device=dev)
+    Y = torch.empty(T, HM, device=dev)
+
+    def step():
+        eptr, tok, wt, _ = G.moe_route(logits, K, 1, ws=ws_r)
+        G.moe_experts(tens[0], tens[1], tens[2], E, HM, IM, X, K, eptr, tok, wt, SWIGLU_LIMIT, out=Y, ws=ws_e)
+        return eptr
+
+    for _ in range(warmup):
+        eptr = step()
+    torch.cuda.synchronize()
+    counts = np.diff(eptr.cpu().numpy())
+    touched = int((counts > 0).sum())
+    blk_bytes = IM * HM // 256 * 98  # one expert's gate (or up, or down) tensor
+    moe_bytes = touched * 3 * blk_bytes
+    G.prof_start(4 * steps + 8)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    d = G.prof_read(G.PROF_GROUPED).astype(np.float64)  # launch order: gate+up, down, ...
+    gu, dn = d[0::2], d[1::2]
+    n_asg = T * K
+    gu_bytes = touched * 2 * blk_bytes + n_asg * (HM // 256) * 1028 + 2 * n_asg * IM * 4
+    dn_bytes = touched * blk_bytes + n_asg * (IM // 256) * 1028 + n_asg * HM * 4
+    k_ms = float(gu.mean() + dn.mean())
+    return {
+        "workload": "routed-expert decode batch: 64 experts x (gate/up 2048x6144 + down 6144x2048) IQ3_XXS, "
+                    "32 tokens, softmax top-8, router + grouped GEMVs + combine on the GPU",
+        "touched_experts": touched, "packed_bytes_per_step": moe_bytes,
+        "ms_per_step": round(ms, 4), "GBps": round(moe_bytes / (ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(moe_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "grouped_gemv": {"kernel": "k_gemv_grouped", "gate_up_us": round(float(gu.mean()) * 1e3, 2),
+                         "down_us": round(float(dn.mean()) * 1e3, 2),
+                         "algorithmic_bytes": gu_bytes + dn_bytes,
+                         "GBps": round((gu_bytes + dn_bytes) / (k_ms * 1e-3) / 1e9, 1),
+                         "frac": round((gu_bytes + dn_bytes) / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,6 +171,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the multi-GPU "
@@ -140,25 +202,13 @@ def main():
     g = torch.empty(1, I, device=dev)
     u = torch.empty(1, I, device=dev)
     y = torch.empty(1, H, device=dev)
-    stream = torch.cuda.current_stream()
 
-    def timed_launch(ev, kind, fn):
-        if ev is None:
-            fn()
-            return
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        fn()
-        b.record(stream)
-        ev.append((kind, a, b))
-
-    def step(c, ev=None):
+    def step(c):
         tg, tu, td = copies[c]
         G.prep_act(xd, act)
-        timed_launch(ev, "gate+up", lambda: G.gemv2_act(tg, tu, I, 0, H, I, act, 1, out_a=g, out_b=u, ws=ws_gu))
+        G.gemv2_act(tg, tu, I, 0, H, I, act, 1, out_a=g, out_b=u, ws=ws_gu)
         G.prep_swiglu(g, u, act2, SWIGLU_LIMIT)
-        timed_launch(ev, "down", lambda: G.gemv_act(td, H, 0, I, H, act2, 1, out=y, ws=ws_d))
+        G.gemv_act(td, H, 0, I, H, act2, 1, out=y, ws=ws_d)
 
     log("warmup")
     for i in range(args.warmup):
@@ -169,30 +219,58 @@ def main():
     y_gpu = y.cpu().numpy()[0].copy()
 
     log("timed")
-    ev = []
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t0.record(stream)
+    t0.record()
     for i in range(args.steps):
-        step(i % args.copies, ev)
-    t1.record(stream)
+        step(i % args.copies)
+    t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
+    value = W_BYTES / (ms * 1e-3) / 1e9
+
+    # Kernel timing: the GEMV launches of the step alone (gate+up, down for
+    # every copy in turn, activations already prepared), captured in one HIP
+    # graph so that consecutive launches leave no host gaps; one event pair
+    # on the launch stream brackets the replays. Per-launch duration =
+    # elapsed / launches (inter-launch gaps included, so it errs low).
+    log("kernel timing")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for c in range(args.copies):
+                tg, tu, td = copies[c]
+                G.gemv2_act(tg, tu, I, 0, H, I, act, 1, out_a=g, out_b=u, ws=ws_gu)
+                G.gemv_act(td, H, 0, I, H, act2, 1, out=y, ws=ws_d)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    reps = max(4, args.steps // args.copies)
+    graph.replay()
+    torch.cuda.synchronize()
+    k0 = torch.cuda.Event(enable_timing=True)
+    k1 = torch.cuda.Event(enable_timing=True)
+    k0.record()
+    for _ in range(reps):
+        graph.replay()
+    k1.record()
+    torch.cuda.synchronize()
+    pair_ms = k0.elapsed_time(k1) / (reps * args.copies)  # one gate+up + one down launch
+    # dispatch-stamped events split the pair per kind (they add a little each)
+    G.prof_start(2 * 64 + 8)
+    for i in range(64):
+        step(i % args.copies)
+    dur = G.prof_read(G.PROF_GEMV).astype(np.float64)  # launch order: gate+up, down, ...
+    per_kind = {"gate+up": dur[0::2], "down": dur[1::2]}
     # k_gemv_t64 launches: bytes = packed W + prepared activation + outputs
     act_bytes = {"gate+up": G.lib().gpeed_iq3xxs_act_bytes(H, 1), "down": G.lib().gpeed_iq3xxs_act_bytes(I, 1)}
     launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + act_bytes["gate+up"] + 2 * I * 4,
                     "down": W_BYTES // 3 + act_bytes["down"] + H * 4}
-    per_kind = {}
-    for kind, a, b in ev:
-        per_kind.setdefault(kind, []).append(a.elapsed_time(b))
-    tot_ms = sum(sum(v) for v in per_kind.values())
-    tot_bytes = sum(launch_bytes[k] * len(v) for k, v in per_kind.items())
-    achieved = tot_bytes / (tot_ms * 1e-3) / 1e9
-    value = W_BYTES / (ms * 1e-3) / 1e9
-    kinds = {k: {"mean_us": round(statistics.fmean(v) * 1e3, 3), "launches": len(v),
-                 "algorithmic_bytes": launch_bytes[k],
-                 "GBps": round(launch_bytes[k] / (statistics.fmean(v) * 1e-3) / 1e9, 1)}
+    pair_bytes = launch_bytes["gate+up"] + launch_bytes["down"]
+    achieved = pair_bytes / (pair_ms * 1e-3) / 1e9
+    kinds = {k: {"dispatch_event_us": round(float(v.mean()) * 1e3, 3), "algorithmic_bytes": launch_bytes[k]}
              for k, v in per_kind.items()}
 
     rec = {
@@ -206,16 +284,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "iq3_xxs weights, fp32 activations; f16 MFMA on exact operands, f32 accumulate",
+        "dtype": "iq3_xxs",
         "data": "synthetic (seeded IQ3_XXS blocks, x ~ N(0,1)); weights resident in HBM, "
                 f"{args.copies} rotated copies ({args.copies * W_BYTES / 1e6:.0f} MB)",
         "config": {"workload": "dense-layer decode at batch 1: IQ3_XXS gate/up 12288x6144, "
-                               "down 6144x12288 (prep, 2 matvec, SwiGLU-prep, matvec)",
-                   "packed_weight_bytes_per_step": W_BYTES, "batch": 1},
+                               "down 6144x12288 (prep, gate+up GEMV, SwiGLU-prep, down GEMV)",
+                   "packed_weight_bytes_per_step": W_BYTES, "batch": 1,
+                   "arithmetic": "iq3_xxs weights decoded to exact fp16, fp32 activations as fp16 hi+lo, "
+                                 "f16 MFMA with fp32 accumulation"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv_t64", "launch_kinds": kinds},
+                     "kernel": "k_gemv_t64", "avg_launch_us": round(pair_ms * 1e3 / 2, 3),
+                     "pair_us": round(pair_ms * 1e3, 3), "pair_algorithmic_bytes": pair_bytes,
+                     "launch_kinds": kinds},
     }
+    if not args.no_extra:
+        del copies, base
+        torch.cuda.empty_cache()
+        rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(10, args.steps // 10), 3)}
     if not args.no_cpu:
         log("cpu baseline")
         cb, y_ref = cpu_baseline(wg, wu, wd, x)

@@ -76,6 +76,8 @@ def lib():
             "gpeed_iq3xxs_gemv_ws_bytes": ([i32, i64, i64, i32], sz),
             "gpeed_iq3xxs_gemv_act": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv2_act": ([vp, vp, u64, u64, i32, i32, vp, i32, vp, vp, vp, sz, vp], i32),
+            "gpeed_prof_start": ([i32], i32),
+            "gpeed_prof_read": ([i32, vp, i32, vp], i32),
             "gpeed_moe_route_ws_bytes": ([i32, i32, i32], sz),
             "gpeed_moe_route": ([vp, i32, i32, i32, i32, vp, C.c_float, i32, vp, vp, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_moe_ws_bytes": ([i32, i32, i32, i32, i32], sz),
@@ -122,6 +124,23 @@ def _require_cuda(*ts):
 
 def init():
     _check(lib().gpeed_init(), "gpeed_init")
+
+
+PROF_GEMV, PROF_GROUPED, PROF_GEMM = 0, 1, 2
+
+
+def prof_start(max_launches: int = 4096):
+    """Time every following hot-kernel launch (kernel execution only)."""
+    _check(lib().gpeed_prof_start(max_launches), "prof_start")
+
+
+def prof_read(kind: int) -> np.ndarray:
+    """Stop timing; per-launch durations (ms) of one kernel kind, launch order."""
+    n = C.c_int(0)
+    _check(lib().gpeed_prof_read(kind, None, 0, C.byref(n)), "prof_read")
+    out = np.zeros(max(n.value, 1), np.float32)
+    _check(lib().gpeed_prof_read(kind, out.ctypes.data, n.value, C.byref(n)), "prof_read")
+    return out[:n.value]
 
 
 def device_count() -> int:

@@ -13,6 +13,9 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libgpeed_iq3.so")
+HOST_LIB = os.path.join(HERE, "libgpeed_glm5.so")
+ROOT = os.path.dirname(HERE)
+HOST_CHECK = os.path.join(ROOT, "tests", "cpp", "host_check")
 SOURCES = ["capi.hip", "iq3_dequant.hip", "iq3_gemv.hip", "iq3_moe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -48,7 +51,24 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)
+    build_host()
     return LIB
+
+
+def build_host() -> str:
+    """C++ host layer with the reference's signatures (glm5 namespace) over the
+    C ABI, and the small driver the GPU tests run it through. Plain g++: the
+    host layer needs no HIP header."""
+    cxx = os.environ.get("CXX", "g++")
+    tmp = HOST_LIB + ".tmp"
+    _run([cxx, "-std=c++17", "-O2", "-Wall", "-fPIC", "-shared", os.path.join(HERE, "host", "glm5_gpu.cpp"),
+          "-o", tmp, "-L" + HERE, "-lgpeed_iq3", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, HOST_LIB)
+    tmp = HOST_CHECK + ".tmp"
+    _run([cxx, "-std=c++17", "-O2", "-Wall", os.path.join(ROOT, "tests", "cpp", "host_check.cpp"), "-o", tmp,
+          "-L" + HERE, "-lgpeed_glm5", "-lgpeed_iq3", "-Wl,-rpath,$ORIGIN/../../gpeed_amd"])
+    os.replace(tmp, HOST_CHECK)
+    return HOST_LIB
 
 
 if __name__ == "__main__":

@@ -51,11 +51,117 @@ int device_state(const DeviceState** out) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Launch timing pool (see iq3_prof.h). One pool per process, guarded by a
+// mutex; events are created on the device current at gpeed_prof_start.
+struct ProfPool {
+    std::mutex mu;
+    bool on = false;
+    std::vector<hipEvent_t> start, stop;
+    std::vector<int> kind;
+    size_t used = 0;
+};
+ProfPool g_prof;
+
 }  // namespace
+
+namespace gpeed {
+bool prof_slot(int kind, hipEvent_t* a, hipEvent_t* b) {
+    std::lock_guard<std::mutex> lk(g_prof.mu);
+    if (!g_prof.on || g_prof.used >= g_prof.start.size()) return false;
+    const size_t i = g_prof.used++;
+    g_prof.kind[i] = kind;
+    *a = g_prof.start[i];
+    *b = g_prof.stop[i];
+    return true;
+}
+}  // namespace gpeed
 
 extern "C" {
 
 const char* gpeed_last_error(void) { return g_err.c_str(); }
+
+int gpeed_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(GPEED_ERR_INVALID, "malloc: null out pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return GPEED_OK;
+    hipError_t e = hipMalloc(ptr, bytes);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "hipMalloc");
+}
+
+int gpeed_free(void* ptr) {
+    if (!ptr) return GPEED_OK;
+    hipError_t e = hipFree(ptr);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "hipFree");
+}
+
+int gpeed_memcpy(void* dst, const void* src, size_t bytes, int kind) {
+    if (bytes == 0) return GPEED_OK;
+    if (!dst || !src) return fail(GPEED_ERR_INVALID, "memcpy: null pointer");
+    hipMemcpyKind k;
+    switch (kind) {
+        case 1: k = hipMemcpyHostToDevice; break;
+        case 2: k = hipMemcpyDeviceToHost; break;
+        case 3: k = hipMemcpyDeviceToDevice; break;
+        default: return fail(GPEED_ERR_INVALID, "memcpy: kind must be 1, 2 or 3");
+    }
+    hipError_t e = hipMemcpy(dst, src, bytes, k);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "hipMemcpy");
+}
+
+int gpeed_zero(void* ptr, size_t bytes, gpeed_stream_t stream) {
+    if (bytes == 0) return GPEED_OK;
+    if (!ptr) return fail(GPEED_ERR_INVALID, "zero: null pointer");
+    hipError_t e = hipMemsetAsync(ptr, 0, bytes, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "hipMemsetAsync");
+}
+
+int gpeed_stream_sync(gpeed_stream_t stream) {
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int gpeed_prof_start(int max_launches) {
+    if (max_launches < 1 || max_launches > (1 << 20)) return fail(GPEED_ERR_INVALID, "prof_start: bad pool size");
+    std::lock_guard<std::mutex> lk(g_prof.mu);
+    for (size_t i = 0; i < g_prof.start.size(); ++i) {
+        (void)hipEventDestroy(g_prof.start[i]);
+        (void)hipEventDestroy(g_prof.stop[i]);
+    }
+    g_prof.start.assign(max_launches, nullptr);
+    g_prof.stop.assign(max_launches, nullptr);
+    g_prof.kind.assign(max_launches, -1);
+    for (int i = 0; i < max_launches; ++i) {
+        hipError_t e = hipEventCreate(&g_prof.start[i]);
+        if (e == hipSuccess) e = hipEventCreate(&g_prof.stop[i]);
+        if (e != hipSuccess) {
+            g_prof.start.resize(i);
+            g_prof.stop.resize(i);
+            g_prof.kind.resize(i);
+            return hip_fail(e, "prof_start: hipEventCreate");
+        }
+    }
+    g_prof.used = 0;
+    g_prof.on = true;
+    return GPEED_OK;
+}
+
+int gpeed_prof_read(int kind, float* durations_ms, int max_n, int* n) {
+    if (!n) return fail(GPEED_ERR_INVALID, "prof_read: null count");
+    std::lock_guard<std::mutex> lk(g_prof.mu);
+    g_prof.on = false;
+    int c = 0;
+    for (size_t i = 0; i < g_prof.used; ++i) {
+        if (g_prof.kind[i] != kind) continue;
+        hipError_t e = hipEventSynchronize(g_prof.stop[i]);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, g_prof.start[i], g_prof.stop[i]);
+        if (e != hipSuccess) return hip_fail(e, "prof_read");
+        if (durations_ms && c < max_n) durations_ms[c] = ms;
+        ++c;
+    }
+    *n = c;
+    return GPEED_OK;
+}
 
 int gpeed_device_count(void) {
     int n = 0;

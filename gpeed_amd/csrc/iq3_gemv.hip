@@ -28,6 +28,7 @@
 #include "iq3_common.h"
 #include "iq3_gemv_core.h"
 #include "iq3_kernels.h"
+#include "iq3_prof.h"
 
 namespace gpeed {
 
@@ -331,8 +332,7 @@ template <int NT>
 hipError_t launch_gemv_nt(const GemvPlan& plan, GemvArgs a, hipStream_t s) {
     a.chunk = plan.chunk;
     a.max_parts = plan.max_parts;
-    hipLaunchKernelGGL((k_gemv_t64<NT>), dim3(plan.grid), dim3(GemvCfg<NT>::kWaves * 64), 0, s, a);
-    return hipGetLastError();
+    return launch_timed(kProfGemv, k_gemv_t64<NT>, dim3(plan.grid), dim3(GemvCfg<NT>::kWaves * 64), 0, s, a);
 }
 
 }  // namespace

@@ -19,6 +19,7 @@
 #include "iq3_common.h"
 #include "iq3_gemv_core.h"
 #include "iq3_kernels.h"
+#include "iq3_prof.h"
 
 namespace gpeed {
 
@@ -487,7 +488,8 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     ga.rows = I;
     ga.pl = pl;
     ga.ctr_index = 0;
-    hipLaunchKernelGGL(k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, ga);
+    e = launch_timed(kProfGrouped, k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, ga);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_prep_grouped<1>, dim3((N * nbI + 3) / 4), dim3(256), 0, s, G, U, tok, eptr, E, nbI,
                        lim, pl, ws + L.act2, L.stride2);
     GroupedArgs gd = ga;
@@ -502,7 +504,8 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     gd.tiles = H / kTileRows;
     gd.rows = H;
     gd.ctr_index = 1;
-    hipLaunchKernelGGL(k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, gd);
+    e = launch_timed(kProfGrouped, k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, gd);
+    if (e != hipSuccess) return e;
     const size_t n4 = (size_t)T * H / 4;
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, D, wt, pl.pos, T, K, H,
                        Y);

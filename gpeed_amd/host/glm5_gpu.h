@@ -1,0 +1,88 @@
+// C++ host layer over the gpeed C ABI, with the reference's call signatures.
+//
+// * glm5::cuda_device_count / cuda_device_name / cuda_add keep the kernel
+//   slot of cpp/kernels/include/glm5/kernels.h:7-11 (device_info.cu) and run
+//   on the HIP device.
+// * glm5::gpu::WeightStore keeps WeightStore::matvec_quant / matmul_quant
+//   (cpp/core/include/glm5/weights.h:41-48, weights.cpp:86-203): same
+//   arguments, host fp32 arrays in and out, synchronous, the same
+//   std::runtime_error messages ("weights: missing tensor <name>",
+//   "weights: row not block aligned for <name>"). Tensors are uploaded once
+//   (add) and kept in HBM in the T64 layout.
+// * WeightStore::moe_experts runs steps 1-3 of Model::moe_batch
+//   (model_batch.cpp:165-262) from the router logits on the device.
+//
+// No HIP header is needed by users of this file; it links against
+// libgpeed_iq3.so (include/gpeed_iq3.h).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <map>
+#include <tuple>
+#include <unordered_map>
+
+namespace glm5 {
+
+int cuda_device_count();
+std::string cuda_device_name(int index);
+// dst[i] = a[i] + b[i] over host arrays, computed on the device.
+void cuda_add(const float* a, const float* b, float* dst, int n);
+
+namespace gpu {
+
+class WeightStore {
+public:
+    WeightStore();
+    ~WeightStore();
+    WeightStore(const WeightStore&) = delete;
+    WeightStore& operator=(const WeightStore&) = delete;
+
+    // Uploads n_rows GGUF IQ3_XXS rows of in_dim weights (host bytes) and
+    // keeps their T64 copy in HBM (the role of pin_nonexpert,
+    // weights.cpp:70-84). Replaces a tensor of the same name.
+    void add(const std::string& name, const void* gguf_rows, uint64_t n_rows, int in_dim);
+    bool has(const std::string& name) const { return tensors_.count(name) != 0; }
+    size_t resident_bytes() const { return resident_bytes_; }
+
+    // dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim (weights.cpp:167-203).
+    void matvec_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* x,
+                      float* dst);
+    // Y[t][j] = sum_i W[row0+j][i] * X[t][i], t < n_tok (weights.cpp:86-165).
+    void matmul_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* X,
+                      int n_tok, float* Y);
+
+    // Model::moe_batch steps 1-3: router top_k over logits [n_tok][n_exp]
+    // (mode 0: sigmoid + bias with routed_scale / norm_topk as the reference;
+    // mode 1: softmax over the top_k), expert buckets, per-expert gate/up
+    // (rows e*inter of gate/up), SwiGLU(limit), down (rows e*hidden), and
+    // Y[t] = sum of the weighted expert outputs (overwritten).
+    void moe_experts(const std::string& gate, const std::string& up, const std::string& down, int n_exp,
+                     int hidden, int inter, const float* X, int n_tok, const float* logits, int top_k, int mode,
+                     const float* bias, float routed_scale, bool norm_topk, float swiglu_limit, float* Y);
+
+private:
+    struct Tensor {
+        void* t64 = nullptr;
+        uint64_t n_rows = 0;
+        int in_dim = 0;
+        size_t bytes = 0;
+    };
+    struct Buffer {
+        void* p = nullptr;
+        size_t bytes = 0;
+    };
+    const Tensor& get(const std::string& name, int in_dim) const;
+    void* scratch(Buffer& b, size_t bytes, bool zero);
+
+    std::unordered_map<std::string, Tensor> tensors_;
+    size_t resident_bytes_ = 0;
+    // GEMV workspaces are zero-filled once per (in_dim, out_dim, tokens)
+    // shape and then kept: each launch leaves its tickets at zero.
+    std::map<std::tuple<int, int, int>, Buffer> ws_;
+    Buffer x_, y_, route_ws_, moe_ws_, logits_, bias_, eptr_, tok_, wt_;
+};
+
+}  // namespace gpu
+}  // namespace glm5

@@ -52,6 +52,26 @@ int gpeed_init(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* gpeed_last_error(void);
 
+/* Device memory and copies for callers without HIP headers (the C++ host
+ * layer; no reference counterpart: the reference keeps weights in host RAM,
+ * weights.cpp:62-84). gpeed_memcpy kind: 1 host->device, 2 device->host,
+ * 3 device->device; synchronous. gpeed_zero: device memset to 0 on stream. */
+int gpeed_malloc(void** ptr, size_t bytes);
+int gpeed_free(void* ptr);
+int gpeed_memcpy(void* dst, const void* src, size_t bytes, int kind);
+int gpeed_zero(void* ptr, size_t bytes, gpeed_stream_t stream);
+int gpeed_stream_sync(gpeed_stream_t stream);
+
+/* Launch timing for benchmarks (no reference counterpart): gpeed_prof_start
+ * makes a pool of max_launches event pairs and times every following launch
+ * of the hot kernels with events stamped by the dispatch itself (kernel
+ * execution only); gpeed_prof_read stops timing, waits, and returns the
+ * durations of the timed launches of one kind (0 = GEMV k_gemv_t64,
+ * 1 = grouped GEMV, 2 = prefill GEMM) in launch order (up to max_n of them;
+ * *n = how many there were). */
+int gpeed_prof_start(int max_launches);
+int gpeed_prof_read(int kind, float* durations_ms, int max_n, int* n);
+
 /* ---- geometry (replaces quant.cpp:52-126 for IQ3_XXS) ------------------- */
 
 /* dtype_row_bytes(IQ3_XXS, in_dim) (quant.cpp:119-126): 0 if in_dim % 256. */
@@ -89,9 +109,10 @@ int gpeed_iq3xxs_untile(const void* t64, uint64_t n_rows, int64_t in_dim, void* 
  *      weights.cpp:86-165) ----------------------------------------------- */
 
 /* Workspace bytes of gpeed_iq3xxs_matvec / gpeed_iq3xxs_matmul for n_tok
- * vectors (n_tok = 1 for matvec). The workspace must be zero-filled once
- * before its first use; calls leave it ready for the next one. One
- * workspace per stream: calls that run concurrently must not share one. */
+ * vectors (n_tok = 1 for matvec). The workspace must be zero-filled before
+ * its first use with a given (in_dim, out_dim, min(n_tok, 8)); calls leave it
+ * ready for the next call of that shape. One workspace per stream: calls
+ * that run concurrently must not share one. */
 size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim, int64_t out_dim);
 size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok);
 /* dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim, from the T64 copy of a
@@ -112,9 +133,9 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
  * "prepared activation" holds 1..8 fp32 vectors as the fp16 hi/lo MFMA
  * operand plus a power-of-two scale per 256 elements, in a caller-owned
  * device buffer of gpeed_iq3xxs_act_bytes(in_dim, n_tok) bytes (16-byte
- * aligned). The GEMV workspace (gpeed_iq3xxs_gemv_ws_bytes, zero-filled
- * once, one per stream) holds the partial sums of row tiles that two
- * workgroups share. */
+ * aligned). The GEMV workspace (gpeed_iq3xxs_gemv_ws_bytes; zero-filled
+ * before its first use with a given shape, one per stream) holds the
+ * tickets and partial sums of row tiles that workgroups share. */
 size_t gpeed_iq3xxs_act_bytes(int64_t in_dim, int n_tok);
 int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, int n_tok, void* act, size_t act_bytes,
                           gpeed_stream_t stream);

@@ -36,6 +36,25 @@ def test_header_symbols_exported():
         assert hasattr(L, n), n
 
 
+def test_host_layer_exports_reference_signatures():
+    """libgpeed_glm5.so (C++ host layer) exports the reference's kernel-slot
+    functions (kernels.h:7-11) and the WeightStore product methods
+    (weights.h:41-48) under the glm5 namespace."""
+    import subprocess
+
+    lib = os.path.join(ROOT, "gpeed_amd", "libgpeed_glm5.so")
+    syms = subprocess.run(["nm", "-D", "--defined-only", "-C", lib], stdout=subprocess.PIPE, text=True,
+                          check=True).stdout
+    for want in ["glm5::cuda_device_count()", "glm5::cuda_device_name[abi:cxx11](int)",
+                 "glm5::cuda_add(float const*, float const*, float*, int)",
+                 "glm5::gpu::WeightStore::matvec_quant(std::__cxx11::basic_string<char, std::char_traits<char>, "
+                 "std::allocator<char> > const&, unsigned long, int, int, float const*, float*)",
+                 "glm5::gpu::WeightStore::matmul_quant(std::__cxx11::basic_string<char, std::char_traits<char>, "
+                 "std::allocator<char> > const&, unsigned long, int, int, float const*, int, float*)"]:
+        assert want in syms, want
+    assert os.access(os.path.join(ROOT, "tests", "cpp", "host_check"), os.X_OK)
+
+
 def test_geometry():
     L = gpeed_amd.lib()
     assert L.gpeed_iq3xxs_row_bytes(4096) == 16 * 98

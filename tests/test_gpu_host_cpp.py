@@ -1,0 +1,66 @@
+"""GPU tests of the C++ host layer (gpeed_amd/host/glm5_gpu.{h,cpp}): the
+reference's call signatures -- glm5::cuda_device_count / cuda_device_name /
+cuda_add (kernels.h:7-11) and WeightStore::matvec_quant / matmul_quant
+(weights.h:41-48) plus the moe_batch expert step -- driven through
+tests/cpp/host_check with host arrays, checked against the oracle."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from gpeed_amd import synth
+from conftest import ROOT, rel_err
+
+pytestmark = pytest.mark.gpu
+EXE = os.path.join(ROOT, "tests", "cpp", "host_check")
+TIGHT = 2e-5
+
+
+def run(*args):
+    r = subprocess.run([EXE, *map(str, args)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                       timeout=240)
+    assert r.returncode == 0, r.stdout
+    return r.stdout
+
+
+def test_kernels_parity_set(gpu):
+    out = run("kernels")
+    assert "add=ok" in out and "devices=" in out and "name=<none>" not in out
+
+
+def test_errors_match_reference(gpu):
+    assert "missing=1 unaligned=1 zero=1" in run("errors")
+
+
+@pytest.mark.parametrize("n_rows,in_dim,row0,out_dim,n_tok", [(200, 1536, 64, 136, 3), (6144, 12288, 0, 6144, 1),
+                                                             (300, 512, 0, 300, 11)])
+def test_matvec_matmul_quant(gpu, tmp_path, n_rows, in_dim, row0, out_dim, n_tok):
+    w = synth.iq3xxs_matrix(80, n_tok, n_rows, in_dim)
+    X = synth.normal(80, 1, n_tok * in_dim).reshape(n_tok, in_dim)
+    w.tofile(tmp_path / "w.bin")
+    X.tofile(tmp_path / "x.bin")
+    run("matmul", tmp_path, n_rows, in_dim, row0, out_dim, n_tok)
+    y = np.fromfile(tmp_path / "y.bin", np.float32)
+    Y = np.fromfile(tmp_path / "Y.bin", np.float32).reshape(n_tok, out_dim)
+    assert rel_err(y, oracle.matvec(w, row0, in_dim, out_dim, X[0])) < TIGHT
+    ref = oracle.matmul(w, row0, in_dim, out_dim, X)
+    assert max(rel_err(Y[t], ref[t]) for t in range(n_tok)) < TIGHT
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_moe_experts(gpu, tmp_path, mode):
+    E, H, I, T, K = 16, 1024, 512, 12, 4
+    wg = synth.iq3xxs_matrix(81, 0, E * I, H)
+    wu = synth.iq3xxs_matrix(81, 1, E * I, H)
+    wd = synth.iq3xxs_matrix(81, 2, E * H, I)
+    X = synth.normal(81, 3, T * H).reshape(T, H)
+    logits = synth.normal(81, 4, T * E).reshape(T, E)
+    for name, a in (("gate", wg), ("up", wu), ("down", wd), ("x", X), ("logits", logits)):
+        a.tofile(tmp_path / f"{name}.bin")
+    run("moe", tmp_path, E, H, I, T, K, mode)
+    Y = np.fromfile(tmp_path / "Y.bin", np.float32).reshape(T, H)
+    eptr, tok, wt, _ = oracle.moe_route(logits, K, mode, routed_scale=2.5 if mode == 0 else 1.0)
+    ref = oracle.moe_experts(wg, wu, wd, H, I, X, eptr, tok, wt, 10.0)
+    assert max(rel_err(Y[t], ref[t]) for t in range(T)) < TIGHT

@@ -310,6 +310,39 @@ def test_weight_store_mirror(gpu):
         ws.matvec_quant("blk.0.ffn_up.weight", 0, 500, 16, x)
 
 
+def test_graph_replay_matches_eager(gpu):
+    """The GEMV launches captured in a HIP graph (no memset nodes; the
+    workspace tickets reset inside the kernel) give the eager result on
+    every replay, with eager work in between."""
+    import torch
+
+    n_rows, in_dim = 6144, 12288
+    w = synth.iq3xxs_matrix(63, 0, n_rows, in_dim)
+    t64 = G.tile(dev(w.reshape(-1), gpu), n_rows, in_dim)
+    x = dev(synth.normal(63, 1, in_dim), gpu)
+    act = G.prep_act(x, G.act_buffer(in_dim, 1, gpu))
+    ws = G.gemv_workspace(in_dim, n_rows, 1, 1, gpu)
+    y = torch.empty(1, n_rows, device=gpu)
+    G.gemv_act(t64, n_rows, 0, in_dim, n_rows, act, 1, out=y, ws=ws)
+    torch.cuda.synchronize()
+    want = host(y).copy()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            G.gemv_act(t64, n_rows, 0, in_dim, n_rows, act, 1, out=y, ws=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for r in range(4):
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32)), r
+        G.gemv_act(t64, n_rows, 0, in_dim, n_rows, act, 1, ws=ws)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_device_smoke(gpu):
     assert G.device_count() >= 1
     assert G.device_name(0) not in ("", "<none>")
