@@ -76,6 +76,8 @@ def lib():
             "gpeed_iq3xxs_gemv_ws_bytes": ([i32, i64, i64, i32], sz),
             "gpeed_iq3xxs_gemv_act": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv2_act": ([vp, vp, u64, u64, i32, i32, vp, i32, vp, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_gemm_ws_bytes": ([i64, i64, i32], sz),
+            "gpeed_iq3xxs_gemm": ([vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, sz, vp], i32),
             "gpeed_prof_start": ([i32], i32),
             "gpeed_prof_read": ([i32, vp, i32, vp], i32),
             "gpeed_moe_route_ws_bytes": ([i32, i32, i32], sz),
@@ -239,6 +241,26 @@ def matmul(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None
         ws = matmul_workspace(in_dim, out_dim, n_tok, X.device)
     _check(lib().gpeed_iq3xxs_matmul(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(X), n_tok, _ptr(out),
                                      _ptr(ws), ws.numel(), _stream(stream)), "matmul")
+    return out
+
+
+X_F32, X_BF16 = 0, 1
+
+
+def gemm(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None, ws=None, stream=None):
+    """Prefill GEMM: Y [n_tok, out_dim] = X [n_tok, in_dim] (fp32 or bf16) @ W[row0:row0+out_dim]^T."""
+    torch = _torch()
+    _require_cuda(w_t64, X)
+    n_tok = X.shape[0]
+    xd = X_BF16 if X.dtype == torch.bfloat16 else X_F32
+    if xd == X_F32 and X.dtype != torch.float32:
+        raise ValueError("gemm: X must be float32 or bfloat16")
+    if out is None:
+        out = torch.empty(n_tok, out_dim, dtype=torch.float32, device=X.device)
+    if ws is None:
+        ws = _zeros(lib().gpeed_iq3xxs_gemm_ws_bytes(n_tok, in_dim, xd), X.device)
+    _check(lib().gpeed_iq3xxs_gemm(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(X), xd, n_tok, _ptr(out),
+                                   _ptr(ws), ws.numel(), _stream(stream)), "gemm")
     return out
 
 

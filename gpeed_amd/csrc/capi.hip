@@ -468,6 +468,30 @@ int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "moe_experts launch");
 }
 
+size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int x_dtype) {
+    if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(in_dim) || (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16))
+        return 0;
+    return gpeed::gemm_ws_bytes((int)n_tok, (int)in_dim, x_dtype == GPEED_X_BF16);
+}
+
+int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const void* X,
+                      int x_dtype, int n_tok, float* Y, void* ws, size_t ws_bytes, gpeed_stream_t stream) {
+    if (n_tok <= 0 || out_dim <= 0) return GPEED_OK;  // weights.cpp:88
+    int rc = check_mv_args(w_t64, n_rows, row0, in_dim, out_dim, X, Y, "gemm");
+    if (rc) return rc;
+    if (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16) return fail(GPEED_ERR_INVALID, "gemm: x_dtype");
+    if (n_tok > (1 << 20)) return fail(GPEED_ERR_INVALID, "gemm: n_tok too large");
+    if (row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "gemm: row0 must be a multiple of 64 on the T64 layout");
+    if (!aligned(w_t64, 16) || !aligned(X, 4)) return fail(GPEED_ERR_INVALID, "gemm: misaligned operand");
+    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::gemm_ws_bytes(n_tok, in_dim, x_dtype == GPEED_X_BF16))
+        return fail(GPEED_ERR_WORKSPACE, "gemm: workspace missing, misaligned or too small");
+    hipError_t e = gpeed::launch_gemm(static_cast<const uint8_t*>(w_t64), row0, in_dim, out_dim, X,
+                                      x_dtype == GPEED_X_BF16, n_tok, Y, static_cast<uint8_t*>(ws),
+                                      static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm launch");
+}
+
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,
                             int out_dim, const float* x, float* dst, gpeed_stream_t stream) {
     if (out_dim <= 0) return GPEED_OK;

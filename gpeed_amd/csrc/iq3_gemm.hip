@@ -1,0 +1,337 @@
+// IQ3_XXS prefill GEMM (gfx950): Y[m][n] = sum_k X[m][k] * W[row0+n][k]
+// for many tokens (matmul_quant, weights.cpp:86-165, at prefill sizes).
+//
+// Operands. W tiles are dequantized into LDS as fp16 holding
+// +-grid * (2s+1): an integer of at most 62 * 31 = 1922, exact in fp16 (bf16
+// would round it), so the only per-weight scale left is the block's d/4,
+// applied once per 256-wide block to the fp32 partial of that block. X is
+// converted once (k_gemm_prep_x) to fp16 with a power-of-two scale per token
+// row (bf16 input: one image, exact for every value within 2^24 of the row
+// maximum; fp32 input: an fp16 hi image and an fp16 lo image, two MFMAs per
+// step). Products are exact; sums are fp32 in the MFMA.
+//
+// Tiling. A 256-thread workgroup computes a 128 (tokens) x 128 (rows) tile;
+// its four wavefronts own 64 x 64 quadrants as 4 x 4 v_mfma_f32_16x16x32_f16
+// accumulator tiles. K advances by half an IQ3 block (128): the X tile is
+// staged to LDS from fp16 global memory, the W tile decoded from T64 records
+// (one thread per (row, sub-block): 8 lookups in a replicated fp16 grid
+// table, rotate-and-mask signs, an exact fp16 multiply by 2s+1), both double
+// buffered so the loads and decode of step s+1 overlap the MFMAs of step s.
+// Workgroups are ordered so that the eight XCDs each work on their own band
+// of W rows (the band stays in that XCD's L2 while all token tiles use it).
+#include <type_traits>
+
+#include "iq3_common.h"
+#include "iq3_gemv_core.h"
+#include "iq3_kernels.h"
+#include "iq3_prof.h"
+
+namespace gpeed {
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v_t __attribute__((ext_vector_type(2)));
+
+constexpr int BM = 128, BN = 128;
+constexpr int kGemmThreads = 256;
+constexpr int kRowPad = 8;  // halves of padding per LDS row
+constexpr int kTblReplicas = 8;
+
+// K step: half an IQ3 block with one X image, a quarter with two.
+template <int V>
+struct GemmCfg {
+    static constexpr int BK = 128 / V;
+    static constexpr int kLdsRow = BK + kRowPad;
+    static constexpr int kTileHalves = BM * kLdsRow;
+    static constexpr int kStepsPerBlock = kQK / BK;
+    static constexpr int kSubPerStep = BK / 32;
+    static constexpr int kItems = BN * kSubPerStep / kGemmThreads;  // (row, sub-block) per thread
+    static constexpr int kXChunks = BK / 2 / 8;                      // 16-byte X loads per thread per image
+};
+constexpr int kTblBytes = 256 * kTblReplicas * 8;  // 16 KiB
+
+// ---------------------------------------------------------------------------
+// X -> fp16 images with a power-of-two scale per token row. One workgroup per
+// row. IN = 0: fp32 input (hi and lo images); IN = 1: bf16 input (one image).
+template <int IN>
+__global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X, int M, int K,
+                                                     _Float16* __restrict__ xh, float* __restrict__ unscale) {
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x;
+    __shared__ float red[4];
+    auto ld = [&](int k) -> float {
+        if (IN == 1) {
+            const uint16_t b = reinterpret_cast<const uint16_t*>(X)[(size_t)m * K + k];
+            return __uint_as_float((uint32_t)b << 16);
+        }
+        return reinterpret_cast<const float*>(X)[(size_t)m * K + k];
+    };
+    float mx = 0.0f;
+    for (int k = tid; k < K; k += 256) mx = fmaxf(mx, fabsf(ld(k)));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int sc = 0;
+    if (mx > 0.0f && mx < __builtin_inff()) {
+        int ex;
+        (void)frexpf(mx, &ex);
+        sc = 14 - ex;
+        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
+    }
+    const size_t plane = (size_t)M * K;
+    for (int k = tid; k < K; k += 256) {
+        const float v = ldexpf(ld(k), sc);
+        const _Float16 hi = (_Float16)v;
+        xh[(size_t)m * K + k] = hi;
+        if (IN == 0) xh[plane + (size_t)m * K + k] = (_Float16)(v - (float)hi);
+    }
+    if (tid == 0) unscale[m] = ldexpf(1.0f, -sc);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM
+
+struct GemmArgs {
+    const uint8_t* w;       // T64 records of the first requested tile
+    const _Float16* xh;     // [V][M][K] fp16 images
+    const float* unscale;   // [M]
+    float* y;               // [M][N]
+    int M, N, K, nb;
+    int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ uint32_t ld_dword(const uint8_t* rec, int lane, int idx) {
+    // dword idx (0..23) of lane `lane` in a T64 record
+    return *reinterpret_cast<const uint32_t*>(rec + (idx >> 2) * kUnitBytes + lane * 16 + (idx & 3) * 4);
+}
+
+// One (row, sub-block) of W: 32 fp16 of +-grid*(2s+1), in k order.
+__device__ __forceinline__ void decode_sub(const uint8_t* tbl, uint32_t rb, uint32_t q0, uint32_t q1, uint32_t w,
+                                           u32x4_t (&out)[4]) {
+    const uint32_t sw = t64_full_signs(w);
+    const _Float16 s2 = (_Float16)(float)((w >> 27) | 1u);
+    const half2v_t s22 = {s2, s2};
+    static_for<0, 8>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        const uint32_t q = m < 4 ? q0 : q1;
+        constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
+        // entry idx, replica r at (idx << 6) | (r << 3)
+        const uint32_t addr = (__builtin_amdgcn_perm(q, 0u, sel) >> 2) | rb;
+        const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
+        constexpr int l = m >> 1, h = m & 1;
+        constexpr int a0 = 4 * (2 * h) + l, a1 = 4 * (2 * h + 1) + l;
+        const uint32_t bx = (__builtin_amdgcn_alignbit(sw, sw, (a0 + 17) & 31) & 0x80008000u) | g.x;
+        const uint32_t by = (__builtin_amdgcn_alignbit(sw, sw, (a1 + 17) & 31) & 0x80008000u) | g.y;
+        const half2v_t vx = __builtin_bit_cast(half2v_t, bx) * s22;
+        const half2v_t vy = __builtin_bit_cast(half2v_t, by) * s22;
+        out[m >> 1][(m & 1) * 2] = __builtin_bit_cast(uint32_t, vx);
+        out[m >> 1][(m & 1) * 2 + 1] = __builtin_bit_cast(uint32_t, vy);
+    });
+}
+
+template <int V>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_iq3(GemmArgs g) {
+    using Cfg = GemmCfg<V>;
+    constexpr int BK = Cfg::BK, kLdsRow = Cfg::kLdsRow, SPB = Cfg::kStepsPerBlock;
+    __shared__ __attribute__((aligned(16))) uint8_t tbl[kTblBytes];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][V][Cfg::kTileHalves];
+    __shared__ __attribute__((aligned(16))) _Float16 ws[2][Cfg::kTileHalves];
+    __shared__ float d4s[BN];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int wm = wave & 1, wn = wave >> 1;
+
+    // XCD-aware order: consecutive workgroup ids go to different XCDs, so
+    // with xcd = id % 8 each XCD takes its own band of row tiles (when the
+    // row tiles split evenly into 8 bands) and every token tile of it.
+    const int id = blockIdx.x;
+    int tn, tm;
+    if (g.tiles_n % 8 == 0) {
+        const int per_band = g.tiles_n / 8;
+        const int xcd = id & 7, local = id >> 3;
+        tn = xcd * per_band + local % per_band;
+        tm = local / per_band;
+    } else {
+        tn = id % g.tiles_n;
+        tm = id / g.tiles_n;
+    }
+    if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    // grid table: 256 entries x 8 replicas of 4 unsigned fp16
+    for (int it = tid; it < 256 * kTblReplicas; it += kGemmThreads) {
+        const int idx = it / kTblReplicas;
+        const uint32_t v = kIq3xxsGrid[idx];
+        *reinterpret_cast<u32x2_t*>(tbl + it * 8) =
+            u32x2_t{f16_pair_of_bytes(v & 255u, (v >> 8) & 255u), f16_pair_of_bytes((v >> 16) & 255u, v >> 24)};
+    }
+
+    // Loader roles. X: thread -> (row tid/2, BK/2 halves at (tid&1)*BK/2) per
+    // image. W: Cfg::kItems (row, sub-block) items per thread: row = tid & 127,
+    // sub-blocks j = (tid >> 7) + 2t of the step.
+    const int xr = tid >> 1, xc = (tid & 1) * (BK / 2);
+    const int xrow = min(m0 + xr, g.M - 1);
+    const int wr = tid & 127, wj0 = tid >> 7;
+    const int wrow = min(n0 + wr, g.N - 1);  // rows past N: a clamped, unused row
+    const int wtile = wrow >> 6, wlane = wrow & 63;
+    const uint32_t rb = (uint32_t)(lane & (kTblReplicas - 1)) << 3;
+
+    u32x4_t xreg[V][Cfg::kXChunks];
+    uint32_t wq[Cfg::kItems][3];
+    uint32_t wd = 0;
+    auto load_step = [&](int s) {
+        const int k0 = s * BK;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const _Float16* src = g.xh + (size_t)v * g.M * g.K + (size_t)xrow * g.K + k0 + xc;
+#pragma unroll
+            for (int i = 0; i < Cfg::kXChunks; ++i) xreg[v][i] = *reinterpret_cast<const u32x4_t*>(src + i * 8);
+        }
+        const int b = s / SPB, part = s % SPB;
+        const uint8_t* rec = g.w + ((size_t)wtile * g.nb + b) * kRecordBytes;
+#pragma unroll
+        for (int t = 0; t < Cfg::kItems; ++t) {
+            const int ib = part * Cfg::kSubPerStep + wj0 + 2 * t;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) wq[t][c] = ld_dword(rec, wlane, 3 * ib + c);
+        }
+        wd = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + wlane * 2);
+    };
+    auto store_step = [&](int buf) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            _Float16* dst = &xs[buf][v][xr * kLdsRow + xc];
+#pragma unroll
+            for (int i = 0; i < Cfg::kXChunks; ++i) *reinterpret_cast<u32x4_t*>(dst + i * 8) = xreg[v][i];
+        }
+#pragma unroll
+        for (int t = 0; t < Cfg::kItems; ++t) {
+            u32x4_t o[4];
+            decode_sub(tbl, rb, wq[t][0], wq[t][1], wq[t][2], o);
+            _Float16* dst = &ws[buf][wr * kLdsRow + (wj0 + 2 * t) * 32];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(dst + i * 8) = o[i];
+        }
+    };
+
+    float4_t acc[4][4], blk[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            blk[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+
+    const int steps = g.K / BK;
+    load_step(0);
+    __syncthreads();  // grid table ready
+    store_step(0);
+    if (tid < BN) d4s[tid] = (float)__builtin_bit_cast(_Float16, (uint16_t)wd) * 0.25f;
+    __syncthreads();
+
+    const int lr = lane & 15, lg = lane >> 4;
+    for (int s = 0; s < steps; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < steps) load_step(s + 1);
+        // MFMAs of step s
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+            half8_t a[V][4], b[4];
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                    a[v][mt] = *reinterpret_cast<const half8_t*>(
+                        &xs[buf][v][(wm * 64 + mt * 16 + lr) * kLdsRow + kk * 32 + lg * 8]);
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                b[nt] = *reinterpret_cast<const half8_t*>(&ws[buf][(wn * 64 + nt * 16 + lr) * kLdsRow + kk * 32 + lg * 8]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+                    for (int v = 0; v < V; ++v)
+                        blk[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[v][mt], b[nt], blk[mt][nt], 0, 0, 0);
+        }
+        if (s % SPB == SPB - 1) {
+            // block finished: acc += d/4 * partial (column n = W row)
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+                const float d4 = d4s[wn * 64 + nt * 16 + lr];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[mt][nt][i] = fmaf(d4, blk[mt][nt][i], acc[mt][nt][i]);
+                    blk[mt][nt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+        }
+        __syncthreads();  // all reads of the other buffer and of d4s are done
+        if (s + 1 < steps) {
+            store_step(buf ^ 1);
+            if ((s + 1) % SPB == 0 && tid < BN)
+                d4s[tid] = (float)__builtin_bit_cast(_Float16, (uint16_t)wd) * 0.25f;
+        }
+        __syncthreads();
+    }
+
+    // epilogue: D row = token (4 per lane), column = W row
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = m0 + wm * 64 + mt * 16 + lg * 4 + i;
+            if (m >= g.M) continue;
+            const float us = g.unscale[m];
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+                const int n = n0 + wn * 64 + nt * 16 + lr;
+                if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][nt][i] * us;
+            }
+        }
+}
+
+}  // namespace
+
+size_t gemm_ws_bytes(int M, int K, int x_bf16) {
+    const size_t v = x_bf16 ? 1 : 2;
+    const size_t a = (v * (size_t)M * K * 2 + 255) / 256 * 256;
+    return a + ((size_t)M * 4 + 255) / 256 * 256;
+}
+
+hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
+                       int M, float* Y, uint8_t* ws, hipStream_t s) {
+    if (M <= 0 || out_dim <= 0) return hipSuccess;
+    const int v = x_bf16 ? 1 : 2;
+    _Float16* xh = reinterpret_cast<_Float16*>(ws);
+    float* uns = reinterpret_cast<float*>(ws + ((size_t)v * M * in_dim * 2 + 255) / 256 * 256);
+    if (x_bf16)
+        hipLaunchKernelGGL(k_gemm_prep_x<1>, dim3(M), dim3(256), 0, s, X, M, in_dim, xh, uns);
+    else
+        hipLaunchKernelGGL(k_gemm_prep_x<0>, dim3(M), dim3(256), 0, s, X, M, in_dim, xh, uns);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    GemmArgs a{};
+    a.nb = in_dim / kQK;
+    a.w = w + (size_t)(row0 / kTileRows) * a.nb * kRecordBytes;
+    a.xh = xh;
+    a.unscale = uns;
+    a.y = Y;
+    a.M = M;
+    a.N = out_dim;
+    a.K = in_dim;
+    a.tiles_m = (M + BM - 1) / BM;
+    a.tiles_n = (out_dim + BN - 1) / BN;
+    const int grid = a.tiles_n * a.tiles_m;
+    if (x_bf16) return launch_timed(kProfGemm, k_gemm_iq3<1>, dim3(grid), dim3(kGemmThreads), 0, s, a);
+    return launch_timed(kProfGemm, k_gemm_iq3<2>, dim3(grid), dim3(kGemmThreads), 0, s, a);
+}
+
+}  // namespace gpeed

@@ -66,4 +66,11 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
                               int I, const float* X, int T, int K, const int* eptr, const int* tok,
                               const float* wt, float lim, float* Y, uint8_t* ws, int num_cus, hipStream_t s);
 
+// Prefill GEMM: Y[m][j] = sum_k X[m][k] W[row0+j][k] for M tokens from the
+// T64 copy. X is fp32 (x_bf16 = 0) or bf16 (x_bf16 = 1), row-major [M][in_dim];
+// ws: gemm_ws_bytes(M, in_dim, x_bf16) bytes of scratch (fp16 images).
+size_t gemm_ws_bytes(int M, int K, int x_bf16);
+hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
+                       int M, float* Y, uint8_t* ws, hipStream_t s);
+
 }  // namespace gpeed
