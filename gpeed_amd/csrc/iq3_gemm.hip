@@ -298,6 +298,222 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_iq3(GemmArgs g) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// GEMM, register-decode form. A 256-thread workgroup computes 128 tokens x
+// 192 rows; wavefront w owns rows [48w, 48w+48) as 3 column tiles of
+// v_mfma_f32_16x16x32_f16 and all 8 token tiles, so no W value is decoded
+// twice. A lane's B operand is 8 consecutive weights of one row (group g =
+// lane/16 of a 32-weight sub-block); it is decoded straight into registers
+// from two dwords of the T64 record (grid-index word, sign/scale word): two
+// lookups in an LDS table of grid * (2s+1) (exact fp16, scale folded in by
+// the index), the group's eighth sign from a popcount, four rotate-and-mask
+// sign insertions. X images are staged through LDS 64 columns at a time
+// (double buffered); W dwords are prefetched two stages ahead.
+
+constexpr int BM2 = 128, BN2 = 192, BK2 = 64;
+constexpr int kRow2 = BK2 + 8;                  // LDS row stride in halves
+constexpr int kTbl2Bytes = kGridTableBytes;  // replicated unsigned grid, as the GEMV
+
+struct WRing {
+    uint32_t q[2][3];  // [sub-block in stage][column tile]
+    uint32_t w[2][3];
+};
+
+// byte offset of dword idx (0..23) inside a lane slot of a T64 record
+constexpr uint32_t slot_dword_off(int idx) { return (uint32_t)((idx >> 2) * kUnitBytes + (idx & 3) * 4); }
+
+template <int V>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) uint8_t tbl[kTbl2Bytes];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][V][BM2 * kRow2];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t lane = tid & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+
+    const int id = blockIdx.x;
+    int tn, tm;
+    if (g.tiles_n % 8 == 0) {
+        const int per_band = g.tiles_n / 8;
+        const int xcd = id & 7, local = id >> 3;
+        tn = xcd * per_band + local % per_band;
+        tm = local / per_band;
+    } else {
+        tn = id % g.tiles_n;
+        tm = id / g.tiles_n;
+    }
+    if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
+    const int m0 = tm * BM2, n0 = tn * BN2;
+
+    {
+        GridWords<kGemmThreads> gw;
+        grid_words<kGemmThreads>(gw, tid);
+        grid_table_store<kGemmThreads>(tbl, gw, tid);
+    }
+
+    // This lane's three W rows (clamped past N) as 32-bit byte offsets of
+    // their lane slot (and of their d) in block 0; block b adds b * 6272.
+    uint32_t rowoff[3], doff[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int r = min(n0 + wave * 48 + j * 16 + lr, g.N - 1);
+        const uint32_t base = (uint32_t)(r >> 6) * (uint32_t)g.nb * kRecordBytes;
+        rowoff[j] = base + (uint32_t)(r & 63) * 16u;
+        doff[j] = base + (uint32_t)kRecordDOffset + (uint32_t)(r & 63) * 2u;
+    }
+    const bool q1 = (lg >> 1) != 0;                                // q0 for groups 0,1; q1 for 2,3
+    const uint32_t p0 = 2 * (lg & 1), p1 = p0 + 1;                 // byte of each grid index
+    const uint32_t sel0 = 0x0C0C0000u | ((4u + p0) << 8);
+    const uint32_t sel1 = 0x0C0C0000u | ((4u + p1) << 8);
+    const uint32_t lb = (lane & 31u) << 3;  // this lane's replica of the grid table
+
+    // stage s = K columns [64s, 64s+64): sub-blocks 2P, 2P+1 (P = s % 4) of
+    // block s / 4. Loads are issued for a clamped stage so that no load sits
+    // under a branch.
+    auto load_w = [&](WRing& r, int s, auto Pc) {
+        constexpr int P = decltype(Pc)::value;
+        const uint32_t boff = (uint32_t)(s >> 2) * kRecordBytes;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int ib = 2 * P + t;
+            const uint32_t qo = q1 ? slot_dword_off(3 * ib + 1) : slot_dword_off(3 * ib);
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const uint32_t o = rowoff[j] + boff;
+                r.q[t][j] = *reinterpret_cast<const uint32_t*>(g.w + (o + qo));
+                r.w[t][j] = *reinterpret_cast<const uint32_t*>(g.w + (o + slot_dword_off(3 * ib + 2)));
+            }
+        }
+    };
+    // X staging: the stage's 128 rows x 64 columns are 1024 16-byte pieces;
+    // piece tid + 256 i is row (tid >> 3) + 32 i, columns ((tid & 7) * 8)..+7,
+    // so 8 consecutive lanes read one row's 128 contiguous bytes.
+    const int xr = tid >> 3, xc = (tid & 7) * 8;
+    int xrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xrow[i] = min(m0 + xr + 32 * i, g.M - 1);
+    u32x4_t xreg[V][4];
+    auto load_x = [&](int s) {
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                xreg[v][i] = *reinterpret_cast<const u32x4_t*>(g.xh + (size_t)v * g.M * g.K + (size_t)xrow[i] * g.K +
+                                                               s * BK2 + xc);
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<u32x4_t*>(&xs[buf][v][(xr + 32 * i) * kRow2 + xc]) = xreg[v][i];
+    };
+    // B operand (8 weights of one row, group lg) from its grid word and sign
+    // word: unsigned grid values, signs on the fp16 sign bits, then an exact
+    // packed fp16 multiply by 2s+1 (|q (2s+1)| <= 1922)
+    auto decode_b = [&](uint32_t q, uint32_t w) -> half8_t {
+        uint32_t wg = __builtin_amdgcn_alignbit(w, w, (uint32_t)lg);  // group lg's bits at 4c, 4c+16
+        const uint32_t par = __builtin_popcount(wg & 0x01111111u) & 1u;
+        wg = (wg & 0x0FFFFFFFu) | (par << 28);
+        const _Float16 s2 = (_Float16)(float)((w >> 27) | 1u);
+        const half2v_t s22 = {s2, s2};
+        const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, lb, sel0));
+        const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, lb, sel1));
+        const half2v_t v0 = __builtin_bit_cast(half2v_t, g0.x | (__builtin_amdgcn_alignbit(wg, wg, 17) & 0x80008000u)) * s22;
+        const half2v_t v1 = __builtin_bit_cast(half2v_t, g0.y | (__builtin_amdgcn_alignbit(wg, wg, 21) & 0x80008000u)) * s22;
+        const half2v_t v2 = __builtin_bit_cast(half2v_t, g1.x | (__builtin_amdgcn_alignbit(wg, wg, 25) & 0x80008000u)) * s22;
+        const half2v_t v3 = __builtin_bit_cast(half2v_t, g1.y | (__builtin_amdgcn_alignbit(wg, wg, 29) & 0x80008000u)) * s22;
+        const u32x4_t r = {__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                           __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)};
+        return __builtin_bit_cast(half8_t, r);
+    };
+
+    float4_t acc[8][3], blk[8][3];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const float4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int steps = g.K / BK2;  // a multiple of 4
+    WRing ring[4];
+    uint32_t dreg[3];
+    load_w(ring[0], 0, std::integral_constant<int, 0>{});
+    load_w(ring[1], min(1, steps - 1), std::integral_constant<int, 1>{});
+    load_x(0);
+    store_x(0);
+    __syncthreads();  // table and first X stage ready
+
+    for (int s0 = 0; s0 < steps; s0 += 4) {
+        static_for<0, 4>([&](auto Uc) {
+            constexpr int U = decltype(Uc)::value;
+            const int s = s0 + U;
+            const int buf = U & 1;  // s0 is a multiple of 4
+            if constexpr (U == 0) {
+                // this block's d, used three stages later
+                const uint32_t boff = (uint32_t)(s >> 2) * kRecordBytes;
+#pragma unroll
+                for (int j = 0; j < 3; ++j) dreg[j] = *reinterpret_cast<const uint16_t*>(g.w + (doff[j] + boff));
+            }
+            // X for the next stage first: the wait for it before store_x then
+            // leaves the W loads of stage s+2 in flight
+            load_x(min(s + 1, steps - 1));
+            load_w(ring[(U + 2) & 3], min(s + 2, steps - 1), std::integral_constant<int, (U + 2) & 3>{});
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                half8_t bop[3];
+#pragma unroll
+                for (int j = 0; j < 3; ++j) bop[j] = decode_b(ring[U].q[t][j], ring[U].w[t][j]);
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt) {
+                    half8_t a[V];
+#pragma unroll
+                    for (int v = 0; v < V; ++v)
+                        a[v] = *reinterpret_cast<const half8_t*>(&xs[buf][v][(mt * 16 + lr) * kRow2 + t * 32 + lg * 8]);
+#pragma unroll
+                    for (int j = 0; j < 3; ++j)
+#pragma unroll
+                        for (int v = 0; v < V; ++v) {
+                            // a block's first MFMA starts from zero: no reset of blk
+                            const bool first = U == 0 && t == 0 && v == 0;
+                            blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[v], bop[j], first ? zero4 : blk[mt][j],
+                                                                                 0, 0, 0);
+                        }
+                }
+            }
+            if constexpr (U == 3) {
+                // block complete: acc += d/4 * partial (column = this lane's row)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)dreg[j]) * 0.25f;
+#pragma unroll
+                    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(d4, blk[mt][j][i], acc[mt][j][i]);
+                }
+            }
+            __syncthreads();  // everyone finished reading xs[buf ^ 1] (stage s - 1)
+            store_x(buf ^ 1);
+            __syncthreads();
+        });
+    }
+
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = m0 + mt * 16 + lg * 4 + i;
+            if (m >= g.M) continue;
+            const float us = g.unscale[m];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int n = n0 + wave * 48 + j * 16 + lr;
+                if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][j][i] * us;
+            }
+        }
+}
+
 }  // namespace
 
 size_t gemm_ws_bytes(int M, int K, int x_bf16) {
@@ -327,11 +543,11 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
     a.M = M;
     a.N = out_dim;
     a.K = in_dim;
-    a.tiles_m = (M + BM - 1) / BM;
-    a.tiles_n = (out_dim + BN - 1) / BN;
+    a.tiles_m = (M + BM2 - 1) / BM2;
+    a.tiles_n = (out_dim + BN2 - 1) / BN2;
     const int grid = a.tiles_n * a.tiles_m;
-    if (x_bf16) return launch_timed(kProfGemm, k_gemm_iq3<1>, dim3(grid), dim3(kGemmThreads), 0, s, a);
-    return launch_timed(kProfGemm, k_gemm_iq3<2>, dim3(grid), dim3(kGemmThreads), 0, s, a);
+    if (x_bf16) return launch_timed(kProfGemm, k_gemm2<1>, dim3(grid), dim3(kGemmThreads), 0, s, a);
+    return launch_timed(kProfGemm, k_gemm2<2>, dim3(grid), dim3(kGemmThreads), 0, s, a);
 }
 
 }  // namespace gpeed
