@@ -3,9 +3,9 @@
 
 Headline workload (value / metric): the dense-layer decode step at batch 1
 (dense_mlp, model.cpp:677-690) with IQ3_XXS weights gate/up 12288x6144
-(K=6144) and down 6144x12288 (K=12288): prepare x, one launch for gate and
-up sharing the prepared activation, SwiGLU fused into the down projection's
-activation prep, down. Weights are synthetic (seeded, the block distribution
+(K=6144) and down 6144x12288 (K=12288) as two launches: gate and up in one
+GEMV (each workgroup prepares the activation blocks it uses), then the down
+GEMV with the SwiGLU of gate and up computed inside it. Weights are synthetic (seeded, the block distribution
 of gpeed_amd.synth), x ~ N(0,1) fp32, resident in HBM before timing. To
 measure HBM rather than the 256 MB Infinity Cache, `--copies` distinct
 copies of the three tensors (default 8, 694 MB) are rotated step by step.
@@ -13,9 +13,9 @@ copies of the three tensors (default 8, 694 MB) are rotated step by step.
 value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
 roofline = the GEMV kernel (k_gemv_t64: one gate+up launch and one down
 launch per step): algorithmic bytes of a gate+up + down launch pair (packed
-W + prepared activation + outputs) / the pair's duration, timed with HIP
-events on the launch stream around replays of a HIP graph holding only
-those launches (all copies in turn, so still HBM-bound).
+W + fp32 inputs + outputs) / the pair's duration, timed with HIP events on
+the launch stream around replays of a HIP graph holding those launches
+(all copies in turn, so still HBM-bound).
 cpu_baseline = the reference's own CPU path (oracle/_ref: WeightStore::
 matvec_quant compiled from the reference sources, single-threaded as the
 reference builds on Linux) on one full step of the same workload; the
@@ -23,7 +23,10 @@ oracle's C restatement stands in if oracle/_ref was not built.
 
 Secondary line items (same JSON object, key "extra"): the routed-expert
 decode batch (64 experts of gate/up 2048x6144 and down 6144x2048, 32
-tokens, softmax top-8: GB/s over the packed bytes of the touched experts).
+tokens, softmax top-8: GB/s over the packed bytes of the touched experts),
+and the prefill GEMM (W 12288x6144, X bf16 [M,6144], M = 512 and 2048:
+TFLOP/s = 2*M*N*K / kernel time from dispatch-stamped events, against the
+2.5 PFLOP/s dense bf16/fp16 MFMA peak).
 """
 from __future__ import annotations
 
@@ -66,7 +69,8 @@ def cpu_baseline(wg, wu, wd, x):
             u = stores[1].matvec(0, H, I, x)
             gi = np.minimum(g, np.float32(SWIGLU_LIMIT))
             ui = np.clip(u, -SWIGLU_LIMIT, SWIGLU_LIMIT).astype(np.float32)
-            h = (gi / (np.float32(1.0) + np.exp(-gi))) * ui
+            with np.errstate(over="ignore"):  # exp(-g) overflows to inf for g << 0: silu -> -0, as in C
+                h = (gi / (np.float32(1.0) + np.exp(-gi))) * ui
             return stores[2].matvec(0, I, H, h.astype(np.float32))
 
         kind = "reference"
@@ -164,6 +168,39 @@ def moe_decode(torch, G, synth, dev, steps, warmup):
     }
 
 
+def prefill_gemm(torch, G, synth, dev, reps):
+    """Prefill GEMM: IQ3_XXS W 12288x6144, X bf16 [M, 6144], Y fp32 [M, 12288], M = 512 and 2048."""
+    N, K = 12288, 6144
+    w = synth.iq3xxs_matrix(2026, 0, N, K)
+    t64 = G.tile(torch.from_numpy(w.reshape(-1)).to(dev), N, K)
+    out = {"workload": "prefill GEMM: IQ3_XXS W 12288x6144 dequantized into LDS (exact fp16 q*(2s+1)), "
+                       "X bf16 [M,6144] ~ N(0,1), Y fp32 [M,12288]",
+           "peak_TFLOPs": 2500.0}
+    for M in (512, 2048):
+        X = torch.from_numpy(synth.normal(2026, M, M * K).reshape(M, K)).to(dev).to(torch.bfloat16)
+        Y = torch.empty(M, N, device=dev)
+        ws = torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, K, G.X_BF16), dtype=torch.uint8, device=dev)
+        for _ in range(3):
+            G.gemm(t64, N, 0, K, N, X, out=Y, ws=ws)
+        torch.cuda.synchronize()
+        G.prof_start(reps + 8)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            G.gemm(t64, N, 0, K, N, X, out=Y, ws=ws)
+        b.record()
+        torch.cuda.synchronize()
+        call_ms = a.elapsed_time(b) / reps
+        k_ms = float(G.prof_read(G.PROF_GEMM).astype(np.float64).mean())
+        fl = 2.0 * M * N * K
+        out[f"M{M}"] = {"kernel_us": round(k_ms * 1e3, 2), "call_us": round(call_ms * 1e3, 2),
+                        "TFLOPs_kernel": round(fl / (k_ms * 1e-3) / 1e12, 1),
+                        "TFLOPs_call": round(fl / (call_ms * 1e-3) / 1e12, 1),
+                        "frac_of_bf16_peak": round(fl / (k_ms * 1e-3) / 1e12 / 2500.0, 4)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,20 +232,17 @@ def main():
     base = [G.tile(torch.from_numpy(a.reshape(-1)).to(dev), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I))]
     copies = [base] + [[t.clone() for t in base] for _ in range(args.copies - 1)]
     xd = torch.from_numpy(x).to(dev)
-    act = G.act_buffer(H, 1, dev)
-    act2 = G.act_buffer(I, 1, dev)
     ws_gu = G.gemv_workspace(H, I, 1, 2, dev)
     ws_d = G.gemv_workspace(I, H, 1, 1, dev)
-    g = torch.empty(1, I, device=dev)
-    u = torch.empty(1, I, device=dev)
-    y = torch.empty(1, H, device=dev)
+    g = torch.empty(I, device=dev)
+    u = torch.empty(I, device=dev)
+    y = torch.empty(H, device=dev)
 
     def step(c):
+        # two launches: gate+up (activation preparation fused), down (SwiGLU fused)
         tg, tu, td = copies[c]
-        G.prep_act(xd, act)
-        G.gemv2_act(tg, tu, I, 0, H, I, act, 1, out_a=g, out_b=u, ws=ws_gu)
-        G.prep_swiglu(g, u, act2, SWIGLU_LIMIT)
-        G.gemv_act(td, H, 0, I, H, act2, 1, out=y, ws=ws_d)
+        G.gemv2_x(tg, tu, I, 0, H, I, xd, out_a=g, out_b=u, ws=ws_gu)
+        G.gemv_swiglu(td, H, 0, I, H, g, u, SWIGLU_LIMIT, out=y, ws=ws_d)
 
     log("warmup")
     for i in range(args.warmup):
@@ -216,7 +250,7 @@ def main():
     torch.cuda.synchronize()
     step(0)
     torch.cuda.synchronize()
-    y_gpu = y.cpu().numpy()[0].copy()
+    y_gpu = y.cpu().numpy().copy()
 
     log("timed")
     t0 = torch.cuda.Event(enable_timing=True)
@@ -230,11 +264,11 @@ def main():
     ms = t0.elapsed_time(t1) / args.steps
     value = W_BYTES / (ms * 1e-3) / 1e9
 
-    # Kernel timing: the GEMV launches of the step alone (gate+up, down for
-    # every copy in turn, activations already prepared), captured in one HIP
-    # graph so that consecutive launches leave no host gaps; one event pair
-    # on the launch stream brackets the replays. Per-launch duration =
-    # elapsed / launches (inter-launch gaps included, so it errs low).
+    # Kernel timing: the step's two GEMV launches for every copy in turn,
+    # captured in one HIP graph so consecutive launches leave no host gaps;
+    # one event pair on the launch stream brackets the replays. Per-launch
+    # duration = elapsed / launches (inter-launch gaps included, so it errs
+    # low).
     log("kernel timing")
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -242,9 +276,7 @@ def main():
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=side):
             for c in range(args.copies):
-                tg, tu, td = copies[c]
-                G.gemv2_act(tg, tu, I, 0, H, I, act, 1, out_a=g, out_b=u, ws=ws_gu)
-                G.gemv_act(td, H, 0, I, H, act2, 1, out=y, ws=ws_d)
+                step(c)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     reps = max(4, args.steps // args.copies)
@@ -264,10 +296,9 @@ def main():
         step(i % args.copies)
     dur = G.prof_read(G.PROF_GEMV).astype(np.float64)  # launch order: gate+up, down, ...
     per_kind = {"gate+up": dur[0::2], "down": dur[1::2]}
-    # k_gemv_t64 launches: bytes = packed W + prepared activation + outputs
-    act_bytes = {"gate+up": G.lib().gpeed_iq3xxs_act_bytes(H, 1), "down": G.lib().gpeed_iq3xxs_act_bytes(I, 1)}
-    launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + act_bytes["gate+up"] + 2 * I * 4,
-                    "down": W_BYTES // 3 + act_bytes["down"] + H * 4}
+    # k_gemv_t64 launches: bytes = packed W + fp32 input vector(s) + outputs
+    launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + H * 4 + 2 * I * 4,
+                    "down": W_BYTES // 3 + 2 * I * 4 + H * 4}
     pair_bytes = launch_bytes["gate+up"] + launch_bytes["down"]
     achieved = pair_bytes / (pair_ms * 1e-3) / 1e9
     kinds = {k: {"dispatch_event_us": round(float(v.mean()) * 1e3, 3), "algorithmic_bytes": launch_bytes[k]}
@@ -288,7 +319,7 @@ def main():
         "data": "synthetic (seeded IQ3_XXS blocks, x ~ N(0,1)); weights resident in HBM, "
                 f"{args.copies} rotated copies ({args.copies * W_BYTES / 1e6:.0f} MB)",
         "config": {"workload": "dense-layer decode at batch 1: IQ3_XXS gate/up 12288x6144, "
-                               "down 6144x12288 (prep, gate+up GEMV, SwiGLU-prep, down GEMV)",
+                               "down 6144x12288 (gate+up GEMV, down GEMV with SwiGLU fused)",
                    "packed_weight_bytes_per_step": W_BYTES, "batch": 1,
                    "arithmetic": "iq3_xxs weights decoded to exact fp16, fp32 activations as fp16 hi+lo, "
                                  "f16 MFMA with fp32 accumulation"},
@@ -302,6 +333,8 @@ def main():
         del copies, base
         torch.cuda.empty_cache()
         rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(10, args.steps // 10), 3)}
+        torch.cuda.empty_cache()
+        rec["extra"]["prefill_gemm"] = prefill_gemm(torch, G, synth, dev, 20)
     if not args.no_cpu:
         log("cpu baseline")
         cb, y_ref = cpu_baseline(wg, wu, wd, x)

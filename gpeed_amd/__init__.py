@@ -76,6 +76,9 @@ def lib():
             "gpeed_iq3xxs_gemv_ws_bytes": ([i32, i64, i64, i32], sz),
             "gpeed_iq3xxs_gemv_act": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv2_act": ([vp, vp, u64, u64, i32, i32, vp, i32, vp, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_gemv_x": ([vp, u64, u64, i32, i32, vp, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_gemv2_x": ([vp, vp, u64, u64, i32, i32, vp, vp, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_gemv_swiglu": ([vp, u64, u64, i32, i32, vp, vp, C.c_float, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemm_ws_bytes": ([i64, i64, i32], sz),
             "gpeed_iq3xxs_gemm": ([vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, sz, vp], i32),
             "gpeed_prof_start": ([i32], i32),
@@ -303,6 +306,49 @@ def gemv_act(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, act, n_to
         ws = gemv_workspace(in_dim, out_dim, n_tok, 1, act.device)
     _check(lib().gpeed_iq3xxs_gemv_act(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(act), n_tok, _ptr(out),
                                        _ptr(ws), ws.numel(), _stream(stream)), "gemv_act")
+    return out
+
+
+def gemv_x(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None, ws=None, stream=None):
+    """y = W[row0:row0+out_dim] @ x for one fp32 vector, preparation fused (one launch)."""
+    torch = _torch()
+    _require_cuda(w_t64, x)
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = gemv_workspace(in_dim, out_dim, 1, 1, x.device)
+    _check(lib().gpeed_iq3xxs_gemv_x(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out), _ptr(ws),
+                                     ws.numel(), _stream(stream)), "gemv_x")
+    return out
+
+
+def gemv2_x(w_a, w_b, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out_a=None, out_b=None, ws=None,
+            stream=None):
+    """Two same-shape tensors against one fp32 vector, preparation fused (one launch)."""
+    torch = _torch()
+    _require_cuda(w_a, w_b, x)
+    if out_a is None:
+        out_a = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    if out_b is None:
+        out_b = torch.empty(out_dim, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = gemv_workspace(in_dim, out_dim, 1, 2, x.device)
+    _check(lib().gpeed_iq3xxs_gemv2_x(_ptr(w_a), _ptr(w_b), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out_a),
+                                      _ptr(out_b), _ptr(ws), ws.numel(), _stream(stream)), "gemv2_x")
+    return out_a, out_b
+
+
+def gemv_swiglu(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, g, u, limit: float = 10.0, out=None,
+                ws=None, stream=None):
+    """y = W @ (silu(min(g,limit)) * clamp(u,-limit,limit)), SwiGLU computed inside the GEMV (one launch)."""
+    torch = _torch()
+    _require_cuda(w_t64, g, u)
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.float32, device=g.device)
+    if ws is None:
+        ws = gemv_workspace(in_dim, out_dim, 1, 1, g.device)
+    _check(lib().gpeed_iq3xxs_gemv_swiglu(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(g), _ptr(u), limit,
+                                          _ptr(out), _ptr(ws), ws.numel(), _stream(stream)), "gemv_swiglu")
     return out
 
 

@@ -381,6 +381,56 @@ int gpeed_iq3xxs_gemv2_act(const void* w_a, const void* w_b, uint64_t n_rows, ui
     return gemv_n(w, d, 2, n_rows, row0, in_dim, out_dim, act, n_tok, ws, ws_bytes, stream);
 }
 
+static int gemv_x_n(const void* const* w, float* const* dst, int n_tensors, uint64_t n_rows, uint64_t row0,
+                    int in_dim, int out_dim, const float* x, const float* x2, float lim, void* ws, size_t ws_bytes,
+                    gpeed_stream_t stream, const char* who) {
+    if (out_dim <= 0) return GPEED_OK;
+    for (int i = 0; i < n_tensors; ++i) {
+        int rc = check_mv_args(w[i], n_rows, row0, in_dim, out_dim, x, dst[i], who);
+        if (rc) return rc;
+        if (!aligned(w[i], 16)) return fail(GPEED_ERR_INVALID, std::string(who) + ": T64 weights must be 16-byte aligned");
+    }
+    if (in_dim > 16384) return fail(GPEED_ERR_UNIMPLEMENTED, std::string(who) + ": in_dim > 16384 (use prep + gemv_act)");
+    if (!aligned(x, 16) || (x2 && !aligned(x2, 16)))
+        return fail(GPEED_ERR_INVALID, std::string(who) + ": input not 16-byte aligned");
+    if (row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, std::string(who) + ": row0 must be a multiple of 64 on the T64 layout");
+    if (!ws || !aligned(ws, 16) || ws_bytes < gpeed::gemv_ws_bytes(n_tensors, in_dim, out_dim, 1))
+        return fail(GPEED_ERR_WORKSPACE, std::string(who) + ": workspace missing, misaligned or too small");
+    const DeviceState* st = nullptr;
+    int rc = device_state(&st);
+    if (rc) return rc;
+    const uint8_t* wp[2] = {static_cast<const uint8_t*>(w[0]), static_cast<const uint8_t*>(w[n_tensors > 1 ? 1 : 0])};
+    float* yp[2] = {dst[0], dst[n_tensors > 1 ? 1 : 0]};
+    hipError_t e = gpeed::launch_gemv_x(wp, yp, n_tensors, in_dim, row0, out_dim, x, x2, lim, static_cast<uint8_t*>(ws),
+                                        st->num_cus, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, std::string(who + std::string(" launch")).c_str());
+}
+
+int gpeed_iq3xxs_gemv_x(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const float* x,
+                        float* dst, void* ws, size_t ws_bytes, gpeed_stream_t stream) {
+    const void* w[1] = {w_t64};
+    float* d[1] = {dst};
+    return gemv_x_n(w, d, 1, n_rows, row0, in_dim, out_dim, x, nullptr, 0.0f, ws, ws_bytes, stream, "gemv_x");
+}
+
+int gpeed_iq3xxs_gemv2_x(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                         const float* x, float* dst_a, float* dst_b, void* ws, size_t ws_bytes,
+                         gpeed_stream_t stream) {
+    const void* w[2] = {w_a, w_b};
+    float* d[2] = {dst_a, dst_b};
+    return gemv_x_n(w, d, 2, n_rows, row0, in_dim, out_dim, x, nullptr, 0.0f, ws, ws_bytes, stream, "gemv2_x");
+}
+
+int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                             const float* g, const float* u, float limit, float* dst, void* ws, size_t ws_bytes,
+                             gpeed_stream_t stream) {
+    if (!u) return fail(GPEED_ERR_INVALID, "gemv_swiglu: null u");
+    const void* w[1] = {w_t64};
+    float* d[1] = {dst};
+    return gemv_x_n(w, d, 1, n_rows, row0, in_dim, out_dim, g, u, limit, ws, ws_bytes, stream, "gemv_swiglu");
+}
+
 int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* X, int n_tok, float* Y, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream) {
@@ -410,6 +460,17 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
 int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* x, float* dst, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream) {
+    // one launch (preparation fused) where the activation fits the kernel's LDS
+    if (in_dim > 0 && in_dim % gpeed::kQK == 0 && in_dim <= 16384) {
+        if (out_dim <= 0) return GPEED_OK;
+        const size_t need = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, 1);
+        if (!ws || !aligned(ws, 256) || ws_bytes < need)
+            return fail(GPEED_ERR_WORKSPACE, "matvec: workspace missing, misaligned or too small");
+        // same workspace layout as matmul: [activation images][GEMV tickets/partials]
+        const size_t a_bytes = align256(gpeed::act_bytes(in_dim, 1));
+        return gpeed_iq3xxs_gemv_x(w_t64, n_rows, row0, in_dim, out_dim, x, dst, static_cast<uint8_t*>(ws) + a_bytes,
+                                   ws_bytes - a_bytes, stream);
+    }
     return gpeed_iq3xxs_matmul(w_t64, n_rows, row0, in_dim, out_dim, x, 1, dst, ws, ws_bytes, stream);
 }
 

@@ -132,27 +132,80 @@ struct GemvArgs {
     int out_dim;
     int chunk;             // records per workgroup
     int max_parts;
+    const float* x;        // fused preparation: fp32 x (or g) ...
+    const float* x2;       // ... and u for the SwiGLU input
+    float lim;
 };
 
-template <int NT>
+// Fused activation preparation (one vector, K <= 16384): the workgroup
+// prepares the blocks its chunk touches straight into LDS.
+constexpr int kPrepMaxNb = 64;
+template <int NT, int MODE>
+struct Slots {
+    static constexpr int value = MODE == 0 ? GemvCfg<NT>::kSlots : 4;
+};
+
+template <int NT, int MODE>
 __device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g, int rec, uint32_t lane) {
     const int per_tensor = g.n_tiles * g.nb;
     const int ten = rec >= per_tensor ? 1 : 0;
     const int rl = rec - ten * per_tensor;
-    const int b = rl - (rl / g.nb) * g.nb;
-    load_record<(NT + 1) / 2>(r, g.w[ten] + (size_t)rl * kRecordBytes, g.act + (size_t)b * NT * 1024, lane, NT);
+    if constexpr (MODE != 0) {
+        load_record_w(r, g.w[ten] + (size_t)rl * kRecordBytes, lane);  // images come from LDS
+    } else {
+        const int b = rl - (rl / g.nb) * g.nb;
+        load_record<(NT + 1) / 2>(r, g.w[ten] + (size_t)rl * kRecordBytes, g.act + (size_t)b * NT * 1024, lane, NT);
+    }
 }
 
-template <int NT>
+__device__ __forceinline__ float swiglu1(float gv, float uv, float lim) {
+    const float gi = fminf(gv, lim);
+    const float ui = fminf(fmaxf(uv, -lim), lim);
+    return (gi / (1.0f + expf(-gi))) * ui;
+}
+
+// Power-of-two block scale (max |v| of the wavefront's 256 values into
+// [2^13, 2^14)) and the fp16 hi/lo split of this lane's 4 values; returns
+// the unscale.
+__device__ __forceinline__ float split_hi_lo(const float (&e)[4], u32x2_t& hi2, u32x2_t& lo2) {
+    float m = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    int sc = 0;
+    if (m > 0.0f && m < __builtin_inff()) {
+        int ex;
+        (void)frexpf(m, &ex);
+        sc = 14 - ex;
+        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
+    }
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float xs = ldexpf(e[c], sc);
+        hi[c] = (_Float16)xs;
+        lo[c] = (_Float16)(xs - (float)hi[c]);
+    }
+    hi2 = __builtin_bit_cast(u32x2_t, hi);
+    lo2 = __builtin_bit_cast(u32x2_t, lo);
+    return ldexpf(1.0f, -sc);
+}
+
+// MODE 0: prepared activation from global memory (act / xsc); MODE 1: fp32
+// x prepared in the kernel; MODE 2: SwiGLU(g = x, u = x2) prepared in the
+// kernel (MODE 1 and 2 take one vector).
+template <int NT, int MODE>
 __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs g) {
+    static_assert(MODE == 0 || NT == 1, "fused preparation takes one vector");
     constexpr int W = GemvCfg<NT>::kWaves;
     constexpr int PF = GemvCfg<NT>::kPF;
-    constexpr int S = GemvCfg<NT>::kSlots;
+    constexpr int S = Slots<NT, MODE>::value;
     constexpr int NP = GemvCfg<NT>::kPairs;
     constexpr int kThreads = W * 64;
     __shared__ __attribute__((aligned(16))) uint8_t tbl[kGridTableBytes];
     __shared__ float red[S][W][NT][64];
     __shared__ int last_flag[S];
+    __shared__ __attribute__((aligned(16))) uint8_t xsl[MODE ? kPrepMaxNb * 1024 : 16];
+    __shared__ float xscl[MODE ? kPrepMaxNb : 1];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -164,13 +217,49 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
     const int n_mine = c1 - c0 > wave ? (c1 - c0 - wave + W - 1) / W : 0;
     const int tile0 = c0 / g.nb;
 
-    // The codebook words go out first, then the records; the table is built
-    // while the records are in flight (the loads complete in issue order).
+    // The codebook words (and, fused, the activation blocks) go out first,
+    // then the records; the table and the activation images are built while
+    // the records are in flight (the loads complete in issue order).
     GridWords<kThreads> gw;
     grid_words<kThreads>(gw, tid);
+    constexpr int kPrepPer = (kPrepMaxNb + W - 1) / W;  // blocks per wave
+    const int n_pblk = MODE ? min(c1 - c0, g.nb) : 0;   // the chunk's blocks: b = (c0 + i) % nb
+    float4 xv[MODE ? kPrepPer : 1], uv[MODE == 2 ? kPrepPer : 1];
+    if constexpr (MODE != 0) {
+#pragma unroll
+        for (int j = 0; j < kPrepPer; ++j) {
+            const int i = min(wave + j * W, n_pblk - 1);
+            const int b = (c0 + i) % g.nb;
+            xv[j] = *reinterpret_cast<const float4*>(g.x + (size_t)b * 256 + 4 * lane);
+            if constexpr (MODE == 2) uv[j] = *reinterpret_cast<const float4*>(g.x2 + (size_t)b * 256 + 4 * lane);
+        }
+    }
     Rec<NP> ring[PF];
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load_rec<NT>(ring[s], g, min(c0 + wave + s * W, c1 - 1), lane);
+    for (int s = 0; s < PF; ++s) load_rec<NT, MODE>(ring[s], g, min(c0 + wave + s * W, c1 - 1), lane);
+    if constexpr (MODE != 0) {
+#pragma unroll
+        for (int j = 0; j < kPrepPer; ++j) {
+            const int i = wave + j * W;
+            if (i < n_pblk) {
+                const int b = (c0 + i) % g.nb;
+                float e[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+                if constexpr (MODE == 2) {
+                    const float us[4] = {uv[j].x, uv[j].y, uv[j].z, uv[j].w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) e[c] = swiglu1(e[c], us[c], g.lim);
+                }
+                u32x2_t hi, lo;
+                const float unscale = split_hi_lo(e, hi, lo);
+                // single-vector images: lane 4*beta+rho of register a holds
+                // variant rho (0 hi, 1 lo) of slice beta at a*256 + (2*beta+rho)*8
+                const int a = lane >> 4, beta = lane & 15;
+                *reinterpret_cast<u32x2_t*>(xsl + b * 1024 + a * 256 + (2 * beta) * 8) = hi;
+                *reinterpret_cast<u32x2_t*>(xsl + b * 1024 + a * 256 + (2 * beta + 1) * 8) = lo;
+                if (lane == 0) xscl[b] = unscale;
+            }
+        }
+    }
     grid_table_store<kThreads>(tbl, gw, tid);
     for (int i = tid; i < S * W * NT * 64; i += kThreads) (&red[0][0][0][0])[i] = 0.0f;
     lds_barrier();
@@ -201,17 +290,27 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
                 cur_slot = slot;
             }
             if (valid) {
+                if constexpr (MODE != 0) {
+                    const uint32_t off_half = ((lane >> 2) * 2 + (lane & 1)) * 8u;
+#pragma unroll
+                    for (int a = 0; a < 4; ++a)
+                        ring[s].a[0][a] = *reinterpret_cast<const u32x2_t*>(xsl + b * 1024 + a * 256 + off_half);
+                }
                 float blk[2 * NP];
 #pragma unroll
                 for (int t = 0; t < 2 * NP; ++t) blk[t] = 0.0f;
                 record_dot<NP>(tbl, ring[s], lb, blk);
                 const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)ring[s].d) * 0.25f;
-                const float* xs = g.xsc + (size_t)b * NT;
+                if constexpr (MODE != 0) {
+                    acc[0] = fmaf(d4 * xscl[b], blk[0], acc[0]);
+                } else {
+                    const float* xs = g.xsc + (size_t)b * NT;
 #pragma unroll
-                for (int t = 0; t < NT; ++t) acc[t] = fmaf(d4 * xs[t], blk[t], acc[t]);
+                    for (int t = 0; t < NT; ++t) acc[t] = fmaf(d4 * xs[t], blk[t], acc[t]);
+                }
             }
             // refill, clamped to the chunk's last record (a valid address)
-            load_rec<NT>(ring[s], g, min(c0 + wave + (k + PF) * W, c1 - 1), lane);
+            load_rec<NT, MODE>(ring[s], g, min(c0 + wave + (k + PF) * W, c1 - 1), lane);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -328,11 +427,11 @@ __global__ __launch_bounds__(256) void k_matvec_raw(const uint8_t* __restrict__ 
     if (lane == 0) y[j] = acc;
 }
 
-template <int NT>
+template <int NT, int MODE = 0>
 hipError_t launch_gemv_nt(const GemvPlan& plan, GemvArgs a, hipStream_t s) {
     a.chunk = plan.chunk;
     a.max_parts = plan.max_parts;
-    return launch_timed(kProfGemv, k_gemv_t64<NT>, dim3(plan.grid), dim3(GemvCfg<NT>::kWaves * 64), 0, s, a);
+    return launch_timed(kProfGemv, k_gemv_t64<NT, MODE>, dim3(plan.grid), dim3(GemvCfg<NT>::kWaves * 64), 0, s, a);
 }
 
 }  // namespace
@@ -361,7 +460,7 @@ hipError_t launch_prep_swiglu(const float* g, const float* u, float lim, int in_
     return hipGetLastError();
 }
 
-GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus) {
+GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus, bool fused) {
     GemvPlan p{};
     const int nb = in_dim / kQK;
     const int n_tiles = (out_dim + kTileRows - 1) / kTileRows;
@@ -372,7 +471,7 @@ GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cu
     long long chunk = (recs + cus - 1) / cus;
     int cap = 0;
     switch (n_tok) {
-        case 1: cap = max_chunk<1>(nb); break;
+        case 1: cap = fused ? (Slots<1, 1>::value - 1) * nb + 1 : max_chunk<1>(nb); break;
         case 2: cap = max_chunk<2>(nb); break;
         case 3: case 4: cap = max_chunk<4>(nb); break;
         default: cap = max_chunk<8>(nb); break;
@@ -396,7 +495,7 @@ size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok) {
 hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                            unsigned long long row0, int out_dim, int n_tok, const uint8_t* act,
                            uint8_t* ws, int num_cus, hipStream_t s) {
-    const GemvPlan plan = plan_gemv(n_tensors, in_dim, out_dim, n_tok, num_cus);
+    const GemvPlan plan = plan_gemv(n_tensors, in_dim, out_dim, n_tok, num_cus, false);
     if (plan.grid == 0) return hipSuccess;
     GemvArgs a{};
     a.nb = in_dim / kQK;
@@ -424,6 +523,31 @@ hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tenso
         case 8: return launch_gemv_nt<8>(plan, a, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
+                         unsigned long long row0, int out_dim, const float* x, const float* x2, float lim,
+                         uint8_t* ws, int num_cus, hipStream_t s) {
+    const GemvPlan plan = plan_gemv(n_tensors, in_dim, out_dim, 1, num_cus, true);
+    if (plan.grid == 0) return hipSuccess;
+    GemvArgs a{};
+    a.nb = in_dim / kQK;
+    const size_t skip = (size_t)(row0 / kTileRows) * a.nb * kRecordBytes;
+    for (int i = 0; i < 2; ++i) {
+        const int k = i < n_tensors ? i : 0;
+        a.w[i] = w[k] + skip;
+        a.y[i] = y[k];
+    }
+    a.n_tiles = (out_dim + kTileRows - 1) / kTileRows;
+    a.n_records = (int)plan.n_records;
+    a.out_dim = out_dim;
+    a.cnt = reinterpret_cast<uint32_t*>(ws);
+    a.part = reinterpret_cast<float*>(ws + ((size_t)plan.n_tiles_all * 4 + 255) / 256 * 256);
+    a.x = x;
+    a.x2 = x2;
+    a.lim = lim;
+    if (x2) return launch_gemv_nt<1, 2>(plan, a, s);
+    return launch_gemv_nt<1, 1>(plan, a, s);
 }
 
 hipError_t launch_matvec_raw(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,

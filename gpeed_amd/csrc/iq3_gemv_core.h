@@ -98,6 +98,15 @@ __device__ __forceinline__ void load_record(Rec<NP>& r, const uint8_t* rec, cons
     }
 }
 
+// The weight part only (the activation images are read elsewhere).
+template <int NP>
+__device__ __forceinline__ void load_record_w(Rec<NP>& r, const uint8_t* rec, uint32_t lane) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+        r.u[i] = *reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u);
+    r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
+}
+
 // One record: lane n's 256 weights of row n against the NP token pairs;
 // blk[t] += (2s+1) * partial, per sub-block (blk[2p+1] of a single-token
 // last pair is meaningless).

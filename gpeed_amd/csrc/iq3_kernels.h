@@ -34,7 +34,7 @@ struct GemvPlan {
     int grid;
     int max_parts;
 };
-GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus);
+GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus, bool fused);
 // Workspace of a GEMV launch: tickets for the tiles shared between
 // workgroups, then their partial sums. Zero-filled once before first use;
 // every launch leaves the tickets at zero again.
@@ -45,6 +45,12 @@ size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok);
 hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                            unsigned long long row0, int out_dim, int n_tok, const uint8_t* act,
                            uint8_t* ws, int num_cus, hipStream_t s);
+// One fp32 vector x (in_dim <= 16384), prepared inside the GEMV workgroups
+// (no separate preparation launch); with x2 != null the input is
+// silu(min(x,lim)) * clamp(x2,-lim,lim) (SwiGLU of gate x and up x2).
+hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
+                         unsigned long long row0, int out_dim, const float* x, const float* x2, float lim,
+                         uint8_t* ws, int num_cus, hipStream_t s);
 // Same product (one vector) straight from GGUF rows (VALU decode, no repacking).
 hipError_t launch_matvec_raw(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
                              const float* x, float* y, hipStream_t s);

@@ -164,6 +164,21 @@ size_t gpeed_iq3xxs_gemv_ws_bytes(int n_tensors, int64_t in_dim, int64_t out_dim
 int gpeed_iq3xxs_gemv_act(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                           const void* act, int n_tok, float* dst, void* ws, size_t ws_bytes,
                           gpeed_stream_t stream);
+/* One fp32 vector x straight in (in_dim <= 16384; larger returns
+ * GPEED_ERR_UNIMPLEMENTED): the GEMV workgroups prepare the activation blocks
+ * they use themselves, so a product is one launch. gemv2_x: two same-shape
+ * tensors (gate and up); gemv_swiglu: the input is silu(min(g,limit)) *
+ * clamp(u,-limit,limit) computed in the kernel (the down projection of
+ * model.cpp:683-689). ws as gpeed_iq3xxs_gemv_ws_bytes(n_tensors, in_dim,
+ * out_dim, 1). */
+int gpeed_iq3xxs_gemv_x(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const float* x,
+                        float* dst, void* ws, size_t ws_bytes, gpeed_stream_t stream);
+int gpeed_iq3xxs_gemv2_x(const void* w_a, const void* w_b, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                         const float* x, float* dst_a, float* dst_b, void* ws, size_t ws_bytes,
+                         gpeed_stream_t stream);
+int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                             const float* g, const float* u, float limit, float* dst, void* ws, size_t ws_bytes,
+                             gpeed_stream_t stream);
 /* Two same-shape tensors against one prepared activation in one launch
  * (gate and up of model.cpp:681-682, or of the shared expert at 747-748);
  * ws sized for n_tensors = 2. */

@@ -292,6 +292,40 @@ def test_dense_mlp_step(gpu, n_tok):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("n_rows,in_dim,row0,out_dim", [(6144, 12288, 0, 6144), (12288, 6144, 0, 12288),
+                                                      (200, 1280, 64, 100), (128, 16384, 0, 128), (33000, 256, 0, 33000)])
+def test_gemv_x_fused_preparation(gpu, n_rows, in_dim, row0, out_dim):
+    """One-launch GEMV (activation blocks prepared inside the workgroups)."""
+    w = synth.iq3xxs_matrix(64, 0, n_rows, in_dim)
+    t64 = G.tile(dev(w.reshape(-1), gpu), n_rows, in_dim)
+    x = synth.normal(64, 1, in_dim)
+    x[::89] *= np.float32(40.0)
+    y = host(G.gemv_x(t64, n_rows, row0, in_dim, out_dim, dev(x, gpu)))
+    e = rel_err(y, oracle.matvec(w, row0, in_dim, out_dim, x))
+    assert e < TIGHT, e
+
+
+def test_dense_mlp_fused_launches(gpu):
+    """dense_mlp (model.cpp:677-690) as two launches: gate+up with the
+    preparation fused, down with SwiGLU fused."""
+    H, I = 6144, 12288
+    wg = synth.iq3xxs_matrix(65, 0, I, H)
+    wu = synth.iq3xxs_matrix(65, 1, I, H)
+    wd = synth.iq3xxs_matrix(65, 2, H, I)
+    x = synth.normal(65, 9, H) * np.float32(4.0)
+    tg, tu, td = (G.tile(dev(a.reshape(-1), gpu), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I)))
+    g, u = G.gemv2_x(tg, tu, I, 0, H, I, dev(x, gpu))
+    assert rel_err(host(g), oracle.matvec(wg, 0, H, I, x)) < TIGHT
+    assert rel_err(host(u), oracle.matvec(wu, 0, H, I, x)) < TIGHT
+    y = host(G.gemv_swiglu(td, H, 0, I, H, g, u, 10.0))
+    ref = oracle.dense_mlp(wg, wu, wd, H, I, x[None, :], 10.0)[0]
+    e = rel_err(y, ref)
+    assert e < 1e-4, e
+    with pytest.raises(G.GpeedError) as err:
+        G.gemv_x(td, H, 0, 20480, 64, dev(np.zeros(20480, np.float32), gpu))
+    assert err.value.code in (-4, -1)
+
+
 def test_weight_store_mirror(gpu):
     w = synth.iq3xxs_matrix(57, 0, 128, 512)
     ws = G.WeightStore(device=gpu)
