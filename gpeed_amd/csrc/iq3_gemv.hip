@@ -104,11 +104,24 @@ __global__ __launch_bounds__(256) void k_prep_act(const float* __restrict__ x,
 // ---------------------------------------------------------------------------
 // GEMV
 
+#ifndef GEMV_WAVES
+#define GEMV_WAVES 8
+#endif
+#ifndef GEMV_PF
+#define GEMV_PF 2
+#endif
+#ifndef GEMV_PRE
+#define GEMV_PRE 1
+#endif
+
 template <int NT>
 struct GemvCfg {
     static constexpr int kPairs = (NT + 1) / 2;
-    static constexpr int kWaves = NT <= 2 ? 16 : 8;
-    static constexpr int kPF = 2;
+    static constexpr int kWaves = GEMV_WAVES;
+    static constexpr int kPF = GEMV_PF;
+    // ring slots filled before the prologue barrier: a wavefront stuck
+    // issuing record loads (the CU's queue full) must not hold the barrier
+    static constexpr int kPre = GEMV_PRE;
     // tiles one chunk may touch (LDS partial slots)
     static constexpr int kSlots = NT == 1 ? 8 : (NT == 2 ? 4 : 2);
 };
@@ -140,6 +153,8 @@ struct GemvArgs {
 // Fused activation preparation (one vector, K <= 16384): the workgroup
 // prepares the blocks its chunk touches straight into LDS.
 constexpr int kPrepMaxNb = 64;
+// buffer resource word 3 for raw (untyped) buffer loads on gfx9
+constexpr int kBufferDword3 = 0x00020000;
 template <int NT, int MODE>
 struct Slots {
     static constexpr int value = MODE == 0 ? GemvCfg<NT>::kSlots : 4;
@@ -217,26 +232,38 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
     const int n_mine = c1 - c0 > wave ? (c1 - c0 - wave + W - 1) / W : 0;
     const int tile0 = c0 / g.nb;
 
-    // The codebook words (and, fused, the activation blocks) go out first,
-    // then the records; the table and the activation images are built while
-    // the records are in flight (the loads complete in issue order).
-    GridWords<kThreads> gw;
-    grid_words<kThreads>(gw, tid);
+    // The activation blocks (fused preparation) go out first, then the
+    // first record of every wavefront; the grid table (immediate data) and
+    // the activation images are built while those are in flight.
+    constexpr int PRE = GemvCfg<NT>::kPre;
     constexpr int kPrepPer = (kPrepMaxNb + W - 1) / W;  // blocks per wave
     const int n_pblk = MODE ? min(c1 - c0, g.nb) : 0;   // the chunk's blocks: b = (c0 + i) % nb
     float4 xv[MODE ? kPrepPer : 1], uv[MODE == 2 ? kPrepPer : 1];
     if constexpr (MODE != 0) {
+        // buffer loads: an offset past the end returns zeros without a
+        // memory access, so every wave issues the same loads, unbranched
+        const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.x), 0, g.nb * 1024, kBufferDword3);
+        const auto ur = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.x2), 0, g.nb * 1024, kBufferDword3);
 #pragma unroll
         for (int j = 0; j < kPrepPer; ++j) {
-            const int i = min(wave + j * W, n_pblk - 1);
-            const int b = (c0 + i) % g.nb;
-            xv[j] = *reinterpret_cast<const float4*>(g.x + (size_t)b * 256 + 4 * lane);
-            if constexpr (MODE == 2) uv[j] = *reinterpret_cast<const float4*>(g.x2 + (size_t)b * 256 + 4 * lane);
+            const int i = wave + j * W;
+            const uint32_t off = i < n_pblk ? (uint32_t)((c0 + i) % g.nb) * 1024u + lane * 16u : 0x80000000u;
+            xv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            if constexpr (MODE == 2)
+                uv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, 0));
         }
     }
+    // A CU serves its vector memory queue in order: the small loads above
+    // must all be queued before any wave's records, or a late wave's
+    // activation (and with it the barrier below) waits for HBM. s_barrier
+    // waits for issue only, not for data.
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     Rec<NP> ring[PF];
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load_rec<NT, MODE>(ring[s], g, min(c0 + wave + s * W, c1 - 1), lane);
+    for (int s = 0; s < PRE; ++s) load_rec<NT, MODE>(ring[s], g, min(c0 + wave + s * W, c1 - 1), lane);
+    grid_table_literal<W>(tbl, wave, lane);
+    for (int i = tid; i < S * W * NT * 64; i += kThreads) (&red[0][0][0][0])[i] = 0.0f;
     if constexpr (MODE != 0) {
 #pragma unroll
         for (int j = 0; j < kPrepPer; ++j) {
@@ -260,9 +287,9 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
             }
         }
     }
-    grid_table_store<kThreads>(tbl, gw, tid);
-    for (int i = tid; i < S * W * NT * 64; i += kThreads) (&red[0][0][0][0])[i] = 0.0f;
     lds_barrier();
+#pragma unroll
+    for (int s = PRE; s < PF; ++s) load_rec<NT, MODE>(ring[s], g, min(c0 + wave + s * W, c1 - 1), lane);
 
     float acc[NT];
 #pragma unroll

@@ -47,6 +47,44 @@ __device__ __forceinline__ uint32_t f16_pair_of_bytes(uint32_t lo, uint32_t hi) 
            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)hi) << 16);
 }
 
+// Exact fp16 bit pattern of a small non-negative integer (< 2048).
+constexpr uint32_t f16_bits_of_uint(uint32_t a) {
+    if (a == 0) return 0;
+    int e = 0;
+    while ((a >> (e + 1)) != 0) ++e;  // a in [2^e, 2^(e+1))
+    return ((uint32_t)(e + 15) << 10) | ((a << (10 - e)) & 0x3FFu);
+}
+
+// Grid entry idx as two packed fp16 pairs: half 0 = values 0, 1; half 1 =
+// values 2, 3.
+constexpr uint32_t grid_f16_pair(int idx, int half) {
+    return f16_bits_of_uint((kIq3xxsGrid[idx] >> (16 * half)) & 255u) |
+           (f16_bits_of_uint((kIq3xxsGrid[idx] >> (16 * half + 8)) & 255u) << 16);
+}
+
+// The replicated grid table written from immediate operands (no memory
+// loads, so no wait behind other loads): wavefront w of W writes entries
+// [w*256/W, (w+1)*256/W), two per store (lanes 0-31 the even entry's 32
+// replicas, lanes 32-63 the odd one's).
+template <int W>
+__device__ __forceinline__ void grid_table_literal(uint8_t* tbl, int wave, uint32_t lane) {
+    static_assert(256 % (2 * W) == 0, "wavefront share");
+    constexpr int kPer = 256 / W;
+    const bool odd = lane >= 32;
+    uint8_t* base = tbl + ((lane >> 5) << 8) + ((lane & 31u) << 3);
+    static_for<0, W>([&](auto wc) {
+        constexpr int w = decltype(wc)::value;
+        if (wave == w) {
+            static_for<0, kPer / 2>([&](auto ic) {
+                constexpr int e0 = w * kPer + 2 * decltype(ic)::value;
+                const uint32_t lo = odd ? grid_f16_pair(e0 + 1, 0) : grid_f16_pair(e0, 0);
+                const uint32_t hi = odd ? grid_f16_pair(e0 + 1, 1) : grid_f16_pair(e0, 1);
+                *reinterpret_cast<u32x2_t*>(base + (e0 << 8)) = u32x2_t{lo, hi};
+            });
+        }
+    });
+}
+
 // Entry idx, replica r at byte (idx << 8) | (r << 3): 4 unsigned fp16.
 template <int kThreads>
 __device__ __forceinline__ void grid_table_store(uint8_t* tbl, const GridWords<kThreads>& gw, int tid) {
