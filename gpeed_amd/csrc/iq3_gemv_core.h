@@ -156,6 +156,10 @@ __device__ __forceinline__ void record_dot(const uint8_t* tbl, const Rec<NP>& r,
         constexpr int ib = decltype(ibc)::value;
         const uint32_t q0 = dw[3 * ib], q1 = dw[3 * ib + 1], w = dw[3 * ib + 2];
         const uint32_t sw = t64_full_signs(w);
+        // The signs of a group's second pair sit 4 bits above those of its
+        // first pair, so {sw >> 4, sw} shifted left by one 64-bit shift puts
+        // both pairs' signs on bits 15 and 31 of the two halves.
+        const uint64_t sw2 = ((uint64_t)(sw >> 4) << 32) | sw;
         const float sc = (float)((w >> 27) | 1u);  // 2s+1
         float4_t D[NP];
 #pragma unroll
@@ -167,9 +171,12 @@ __device__ __forceinline__ void record_dot(const uint8_t* tbl, const Rec<NP>& r,
             const uint32_t addr = __builtin_amdgcn_perm(q, lb, sel);  // (idx << 8) | lb
             const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
             constexpr int l = m >> 1, h = m & 1;
-            constexpr int a0 = 4 * (2 * h) + l, a1 = 4 * (2 * h + 1) + l;  // sign-bit pairs
-            const uint32_t bx = (__builtin_amdgcn_alignbit(sw, sw, (a0 + 17) & 31) & 0x80008000u) | g.x;
-            const uint32_t by = (__builtin_amdgcn_alignbit(sw, sw, (a1 + 17) & 31) & 0x80008000u) | g.y;
+            constexpr int a0 = 4 * (2 * h) + l;  // first pair's sign bits: a0, a0 + 16
+            // one v_lshlrev_b64 (the compiler would split a C shift into two)
+            uint64_t rs;
+            asm("v_lshlrev_b64 %0, %1, %2" : "=v"(rs) : "n"(15 - a0), "v"(sw2));
+            const uint32_t bx = ((uint32_t)rs & 0x80008000u) | g.x;
+            const uint32_t by = ((uint32_t)(rs >> 32) & 0x80008000u) | g.y;
             const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
 #pragma unroll
             for (int p = 0; p < NP; ++p)
