@@ -3,9 +3,10 @@
 
 Headline workload (value / metric): the dense-layer decode step at batch 1
 (dense_mlp, model.cpp:677-690) with IQ3_XXS weights gate/up 12288x6144
-(K=6144) and down 6144x12288 (K=12288) as two launches: gate and up in one
-GEMV (each workgroup prepares the activation blocks it uses), then the down
-GEMV with the SwiGLU of gate and up computed inside it. Weights are synthetic (seeded, the block distribution
+(K=6144) and down 6144x12288 (K=12288) as two launches (gpeed_iq3xxs_dense_mlp):
+gate and up in one GEMV (each wavefront prepares the activation blocks of
+its records) whose last workgroup per 64 rows writes SwiGLU(gate, up) as the
+down projection's prepared activation, then the down GEMV. Weights are synthetic (seeded, the block distribution
 of gpeed_amd.synth), x ~ N(0,1) fp32, resident in HBM before timing. To
 measure HBM rather than the 256 MB Infinity Cache, `--copies` distinct
 copies of the three tensors (default 8, 694 MB) are rotated step by step.
@@ -13,7 +14,7 @@ copies of the three tensors (default 8, 694 MB) are rotated step by step.
 value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
 roofline = the GEMV kernel (k_gemv_t64: one gate+up launch and one down
 launch per step): algorithmic bytes of a gate+up + down launch pair (packed
-W + fp32 inputs + outputs) / the pair's duration, timed with HIP events on
+W + fp32 x + the SwiGLU activation written and read + y) / the pair's duration, timed with HIP events on
 the launch stream around replays of a HIP graph holding those launches
 (all copies in turn, so still HBM-bound).
 cpu_baseline = the reference's own CPU path (oracle/_ref: WeightStore::
@@ -232,17 +233,14 @@ def main():
     base = [G.tile(torch.from_numpy(a.reshape(-1)).to(dev), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I))]
     copies = [base] + [[t.clone() for t in base] for _ in range(args.copies - 1)]
     xd = torch.from_numpy(x).to(dev)
-    ws_gu = G.gemv_workspace(H, I, 1, 2, dev)
-    ws_d = G.gemv_workspace(I, H, 1, 1, dev)
-    g = torch.empty(I, device=dev)
-    u = torch.empty(I, device=dev)
+    ws_mlp = G.dense_mlp_workspace(H, I, dev)
     y = torch.empty(H, device=dev)
 
     def step(c):
-        # two launches: gate+up (activation preparation fused), down (SwiGLU fused)
+        # two launches: gate+up (x prepared inside; the SwiGLU written as the
+        # down projection's activation), down
         tg, tu, td = copies[c]
-        G.gemv2_x(tg, tu, I, 0, H, I, xd, out_a=g, out_b=u, ws=ws_gu)
-        G.gemv_swiglu(td, H, 0, I, H, g, u, SWIGLU_LIMIT, out=y, ws=ws_d)
+        G.dense_mlp(tg, tu, td, H, I, xd, SWIGLU_LIMIT, out=y, ws=ws_mlp)
 
     log("warmup")
     for i in range(args.warmup):
@@ -296,9 +294,11 @@ def main():
         step(i % args.copies)
     dur = G.prof_read(G.PROF_GEMV).astype(np.float64)  # launch order: gate+up, down, ...
     per_kind = {"gate+up": dur[0::2], "down": dur[1::2]}
-    # k_gemv_t64 launches: bytes = packed W + fp32 input vector(s) + outputs
-    launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + H * 4 + 2 * I * 4,
-                    "down": W_BYTES // 3 + 2 * I * 4 + H * 4}
+    # k_gemv_t64 launches: bytes = packed W + input + output (the SwiGLU
+    # activation between them: I/256 blocks of 1024 B images + 16 B unscales)
+    act64 = (I // 256) * (1024 + 16)
+    launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + H * 4 + act64,
+                    "down": W_BYTES // 3 + act64 + H * 4}
     pair_bytes = launch_bytes["gate+up"] + launch_bytes["down"]
     achieved = pair_bytes / (pair_ms * 1e-3) / 1e9
     kinds = {k: {"dispatch_event_us": round(float(v.mean()) * 1e3, 3), "algorithmic_bytes": launch_bytes[k]}
@@ -319,7 +319,7 @@ def main():
         "data": "synthetic (seeded IQ3_XXS blocks, x ~ N(0,1)); weights resident in HBM, "
                 f"{args.copies} rotated copies ({args.copies * W_BYTES / 1e6:.0f} MB)",
         "config": {"workload": "dense-layer decode at batch 1: IQ3_XXS gate/up 12288x6144, "
-                               "down 6144x12288 (gate+up GEMV, down GEMV with SwiGLU fused)",
+                               "down 6144x12288 (gate+up GEMV writing the SwiGLU activation, down GEMV)",
                    "packed_weight_bytes_per_step": W_BYTES, "batch": 1,
                    "arithmetic": "iq3_xxs weights decoded to exact fp16, fp32 activations as fp16 hi+lo, "
                                  "f16 MFMA with fp32 accumulation"},

@@ -79,6 +79,8 @@ def lib():
             "gpeed_iq3xxs_gemv_x": ([vp, u64, u64, i32, i32, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv2_x": ([vp, vp, u64, u64, i32, i32, vp, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv_swiglu": ([vp, u64, u64, i32, i32, vp, vp, C.c_float, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_dense_mlp_ws_bytes": ([i64, i64], sz),
+            "gpeed_iq3xxs_dense_mlp": ([vp, vp, vp, i32, i32, vp, C.c_float, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemm_ws_bytes": ([i64, i64, i32], sz),
             "gpeed_iq3xxs_gemm": ([vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, sz, vp], i32),
             "gpeed_prof_start": ([i32], i32),
@@ -336,6 +338,28 @@ def gemv2_x(w_a, w_b, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out_
     _check(lib().gpeed_iq3xxs_gemv2_x(_ptr(w_a), _ptr(w_b), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out_a),
                                       _ptr(out_b), _ptr(ws), ws.numel(), _stream(stream)), "gemv2_x")
     return out_a, out_b
+
+
+def dense_mlp_workspace(hidden: int, inter: int, device="cuda"):
+    """Zero-filled workspace of dense_mlp for one (hidden, inter) shape."""
+    n = lib().gpeed_iq3xxs_dense_mlp_ws_bytes(hidden, inter)
+    if n == 0:
+        raise ValueError("dense_mlp: hidden and inter must be positive multiples of 256")
+    return _zeros(n, device)
+
+
+def dense_mlp(w_gate, w_up, w_down, hidden: int, inter: int, x, limit: float = 10.0, out=None, ws=None,
+              stream=None):
+    """Model::dense_mlp (model.cpp:677-690): y = W_down swiglu(W_gate x, W_up x), two launches."""
+    torch = _torch()
+    _require_cuda(w_gate, w_up, w_down, x)
+    if out is None:
+        out = torch.empty(hidden, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = dense_mlp_workspace(hidden, inter, x.device)
+    _check(lib().gpeed_iq3xxs_dense_mlp(_ptr(w_gate), _ptr(w_up), _ptr(w_down), hidden, inter, _ptr(x), limit,
+                                        _ptr(out), _ptr(ws), ws.numel(), _stream(stream)), "dense_mlp")
+    return out
 
 
 def gemv_swiglu(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, g, u, limit: float = 10.0, out=None,

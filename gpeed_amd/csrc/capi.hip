@@ -390,7 +390,6 @@ static int gemv_x_n(const void* const* w, float* const* dst, int n_tensors, uint
         if (rc) return rc;
         if (!aligned(w[i], 16)) return fail(GPEED_ERR_INVALID, std::string(who) + ": T64 weights must be 16-byte aligned");
     }
-    if (in_dim > 16384) return fail(GPEED_ERR_UNIMPLEMENTED, std::string(who) + ": in_dim > 16384 (use prep + gemv_act)");
     if (!aligned(x, 16) || (x2 && !aligned(x2, 16)))
         return fail(GPEED_ERR_INVALID, std::string(who) + ": input not 16-byte aligned");
     if (row0 % gpeed::kTileRows)
@@ -431,6 +430,38 @@ int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, 
     return gemv_x_n(w, d, 1, n_rows, row0, in_dim, out_dim, g, u, limit, ws, ws_bytes, stream, "gemv_swiglu");
 }
 
+size_t gpeed_iq3xxs_dense_mlp_ws_bytes(int64_t hidden, int64_t inter) {
+    if (hidden <= 0 || inter <= 0 || hidden % gpeed::kQK || inter % gpeed::kQK || hidden > (1 << 24) ||
+        inter > (1 << 24))
+        return 0;
+    // [act64 of h][gate/up tickets + partials][down tickets + partials]
+    return align256(gpeed::act64_bytes((int)inter)) + align256(gpeed::gate_up_ws_bytes((int)hidden, (int)inter)) +
+           align256(gpeed::gemv_ws_bytes(1, (int)inter, (int)hidden, 1));
+}
+
+int gpeed_iq3xxs_dense_mlp(const void* w_gate, const void* w_up, const void* w_down, int hidden, int inter,
+                           const float* x, float limit, float* y, void* ws, size_t ws_bytes, gpeed_stream_t stream) {
+    if (!w_gate || !w_up || !w_down || !x || !y) return fail(GPEED_ERR_INVALID, "dense_mlp: null pointer");
+    const size_t need = gpeed_iq3xxs_dense_mlp_ws_bytes(hidden, inter);
+    if (need == 0) return fail(GPEED_ERR_NOT_MULTIPLE, "dense_mlp: hidden and inter must be positive multiples of 256");
+    if (!aligned(w_gate, 16) || !aligned(w_up, 16) || !aligned(w_down, 16) || !aligned(x, 16))
+        return fail(GPEED_ERR_INVALID, "dense_mlp: weights and x must be 16-byte aligned");
+    if (!ws || !aligned(ws, 256) || ws_bytes < need)
+        return fail(GPEED_ERR_WORKSPACE, "dense_mlp: workspace missing, misaligned or too small");
+    const DeviceState* st = nullptr;
+    int rc = device_state(&st);
+    if (rc) return rc;
+    uint8_t* act = static_cast<uint8_t*>(ws);
+    uint8_t* ws_gu = act + align256(gpeed::act64_bytes(inter));
+    uint8_t* ws_d = ws_gu + align256(gpeed::gate_up_ws_bytes(hidden, inter));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = gpeed::launch_gate_up_swiglu(static_cast<const uint8_t*>(w_gate), static_cast<const uint8_t*>(w_up),
+                                                hidden, inter, x, limit, act, ws_gu, st->num_cus, s);
+    if (e != hipSuccess) return hip_fail(e, "dense_mlp gate/up launch");
+    e = gpeed::launch_gemv_act64(static_cast<const uint8_t*>(w_down), inter, 0, hidden, act, y, ws_d, st->num_cus, s);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "dense_mlp down launch");
+}
+
 int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* X, int n_tok, float* Y, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream) {
@@ -460,8 +491,8 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
 int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* x, float* dst, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream) {
-    // one launch (preparation fused) where the activation fits the kernel's LDS
-    if (in_dim > 0 && in_dim % gpeed::kQK == 0 && in_dim <= 16384) {
+    // one launch (activation prepared inside the GEMV)
+    if (in_dim > 0 && in_dim % gpeed::kQK == 0) {
         if (out_dim <= 0) return GPEED_OK;
         const size_t need = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, 1);
         if (!ws || !aligned(ws, 256) || ws_bytes < need)

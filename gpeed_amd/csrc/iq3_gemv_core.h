@@ -191,4 +191,35 @@ __device__ __forceinline__ void record_dot(const uint8_t* tbl, const Rec<NP>& r,
     });
 }
 
+// One vector whose activation has one scale per 64 elements (register
+// image a = sub-blocks 2a, 2a+1): blk[a] += (2s+1) * partial over the
+// image's two sub-blocks.
+__device__ __forceinline__ void record_dot_img(const uint8_t* tbl, const Rec<1>& r, uint32_t lb, float (&blk)[4]) {
+    const uint32_t* dw = reinterpret_cast<const uint32_t*>(&r.u[0]);
+    static_for<0, 8>([&](auto ibc) {
+        constexpr int ib = decltype(ibc)::value;
+        const uint32_t q0 = dw[3 * ib], q1 = dw[3 * ib + 1], w = dw[3 * ib + 2];
+        const uint32_t sw = t64_full_signs(w);
+        const uint64_t sw2 = ((uint64_t)(sw >> 4) << 32) | sw;
+        const float sc = (float)((w >> 27) | 1u);  // 2s+1
+        float4_t D = {0.0f, 0.0f, 0.0f, 0.0f};
+        static_for<0, 8>([&](auto mc) {
+            constexpr int m = decltype(mc)::value;
+            const uint32_t q = m < 4 ? q0 : q1;
+            constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
+            const uint32_t addr = __builtin_amdgcn_perm(q, lb, sel);
+            const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
+            constexpr int a0 = 8 * (m & 1) + (m >> 1);
+            uint64_t rs;
+            asm("v_lshlrev_b64 %0, %1, %2" : "=v"(rs) : "n"(15 - a0), "v"(sw2));
+            const uint32_t bx = ((uint32_t)rs & 0x80008000u) | g.x;
+            const uint32_t by = ((uint32_t)(rs >> 32) & 0x80008000u) | g.y;
+            const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
+            D = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, r.a[0][ib >> 1]), B, D, 4,
+                                                    8 * (ib & 1) + m, 0);
+        });
+        blk[ib >> 1] = fmaf(sc, D[0] + D[1], blk[ib >> 1]);
+    });
+}
+
 }  // namespace gpeed

@@ -34,7 +34,10 @@ struct GemvPlan {
     int grid;
     int max_parts;
 };
-GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus, bool fused);
+// kind: how the launch gets its activation (prepared images, prepared in
+// the kernel, or prepared in the kernel with the gate/up SwiGLU epilogue).
+enum { kPlanAct = 0, kPlanPrep = 1, kPlanSwigluPairs = 2 };
+GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus, int kind);
 // Workspace of a GEMV launch: tickets for the tiles shared between
 // workgroups, then their partial sums. Zero-filled once before first use;
 // every launch leaves the tickets at zero again.
@@ -45,12 +48,28 @@ size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok);
 hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                            unsigned long long row0, int out_dim, int n_tok, const uint8_t* act,
                            uint8_t* ws, int num_cus, hipStream_t s);
-// One fp32 vector x (in_dim <= 16384), prepared inside the GEMV workgroups
+// One fp32 vector x, prepared inside the GEMV workgroups
 // (no separate preparation launch); with x2 != null the input is
 // silu(min(x,lim)) * clamp(x2,-lim,lim) (SwiGLU of gate x and up x2).
 hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                          unsigned long long row0, int out_dim, const float* x, const float* x2, float lim,
                          uint8_t* ws, int num_cus, hipStream_t s);
+// Dense-MLP pair of launches (model.cpp:677-690) without a host round trip:
+// launch_gate_up_swiglu runs gate and up (same shape, out_dim rows of
+// in_dim) against one fp32 x, and the workgroup that completes a row tile
+// writes h = silu(min(g,lim)) * clamp(u,-lim,lim) of its 64 rows as
+// "act64": per 256-element block four fp16 hi/lo images of 64 elements,
+// each with its own power-of-two unscale (act64_bytes(out_dim) bytes).
+// launch_gemv_act64 then multiplies an act64 activation (the down
+// projection). gate_up_ws_bytes: the first launch's workspace (zero-filled
+// once per shape, left at zero by every launch).
+size_t act64_bytes(int in_dim);
+size_t gate_up_ws_bytes(int in_dim, int out_dim);
+hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int in_dim, int out_dim,
+                                 const float* x, float lim, uint8_t* act_out, uint8_t* ws, int num_cus,
+                                 hipStream_t s);
+hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
+                             const uint8_t* act64, float* y, uint8_t* ws, int num_cus, hipStream_t s);
 // Same product (one vector) straight from GGUF rows (VALU decode, no repacking).
 hipError_t launch_matvec_raw(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
                              const float* x, float* y, hipStream_t s);

@@ -164,9 +164,8 @@ size_t gpeed_iq3xxs_gemv_ws_bytes(int n_tensors, int64_t in_dim, int64_t out_dim
 int gpeed_iq3xxs_gemv_act(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                           const void* act, int n_tok, float* dst, void* ws, size_t ws_bytes,
                           gpeed_stream_t stream);
-/* One fp32 vector x straight in (in_dim <= 16384; larger returns
- * GPEED_ERR_UNIMPLEMENTED): the GEMV workgroups prepare the activation blocks
- * they use themselves, so a product is one launch. gemv2_x: two same-shape
+/* One fp32 vector x straight in: the GEMV workgroups prepare the activation
+ * blocks they use themselves, so a product is one launch. gemv2_x: two same-shape
  * tensors (gate and up); gemv_swiglu: the input is silu(min(g,limit)) *
  * clamp(u,-limit,limit) computed in the kernel (the down projection of
  * model.cpp:683-689). ws as gpeed_iq3xxs_gemv_ws_bytes(n_tensors, in_dim,
@@ -179,6 +178,19 @@ int gpeed_iq3xxs_gemv2_x(const void* w_a, const void* w_b, uint64_t n_rows, uint
 int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                              const float* g, const float* u, float limit, float* dst, void* ws, size_t ws_bytes,
                              gpeed_stream_t stream);
+/* Model::dense_mlp (model.cpp:677-690) on the device, in two launches and
+ * without the intermediate vectors: y = W_down (silu(min(g,limit)) *
+ * clamp(u,-limit,limit)) with g = W_gate x, u = W_up x. The first launch
+ * runs gate and up together; the workgroup that completes 64 rows of g and
+ * u writes their SwiGLU straight into the down projection's prepared
+ * activation (one power-of-two scale per 64 values), which the second
+ * launch multiplies. gate/up are T64 copies of inter x hidden, down of
+ * hidden x inter (rows from 0); hidden and inter multiples of 256. ws:
+ * gpeed_iq3xxs_dense_mlp_ws_bytes bytes, zero-filled once per shape (every
+ * call leaves its tickets at zero); one workspace per stream. */
+size_t gpeed_iq3xxs_dense_mlp_ws_bytes(int64_t hidden, int64_t inter);
+int gpeed_iq3xxs_dense_mlp(const void* w_gate, const void* w_up, const void* w_down, int hidden, int inter,
+                           const float* x, float limit, float* y, void* ws, size_t ws_bytes, gpeed_stream_t stream);
 /* Two same-shape tensors against one prepared activation in one launch
  * (gate and up of model.cpp:681-682, or of the shared expert at 747-748);
  * ws sized for n_tensors = 2. */
