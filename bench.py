@@ -3,20 +3,20 @@
 
 Headline workload (value / metric): the dense-layer decode step at batch 1
 (dense_mlp, model.cpp:677-690) with IQ3_XXS weights gate/up 12288x6144
-(K=6144) and down 6144x12288 (K=12288) as two launches (gpeed_iq3xxs_dense_mlp):
-gate and up in one GEMV (each wavefront prepares the activation blocks of
-its records) whose last workgroup per 64 rows writes SwiGLU(gate, up) as the
-down projection's prepared activation, then the down GEMV. Weights are synthetic (seeded, the block distribution
+(K=6144) and down 6144x12288 (K=12288) through gpeed_iq3xxs_dense_mlp: a
+gate+up launch (each wavefront prepares the activation blocks of its records;
+the workgroup that completes 64 rows writes SwiGLU(gate, up) as the down
+projection's prepared activation), then the down launch. Weights are synthetic (seeded, the block distribution
 of gpeed_amd.synth), x ~ N(0,1) fp32, resident in HBM before timing. To
 measure HBM rather than the 256 MB Infinity Cache, `--copies` distinct
 copies of the three tensors (default 8, 694 MB) are rotated step by step.
 
 value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
-roofline = the GEMV kernel (k_gemv_t64: one gate+up launch and one down
-launch per step): algorithmic bytes of a gate+up + down launch pair (packed
-W + fp32 x + the SwiGLU activation written and read + y) / the pair's duration, timed with HIP events on
-the launch stream around replays of a HIP graph holding those launches
-(all copies in turn, so still HBM-bound).
+roofline = the GEMV kernel (k_gemv_t64: the gate+up launch and the down
+launch of a step): algorithmic bytes of the pair (packed W + fp32 x + the
+SwiGLU activation written and read + y) / the pair's duration, timed with
+HIP events on the launch stream around replays of a HIP graph of all copies
+in turn (no host gaps; still HBM-bound).
 cpu_baseline = the reference's own CPU path (oracle/_ref: WeightStore::
 matvec_quant compiled from the reference sources, single-threaded as the
 reference builds on Linux) on one full step of the same workload; the
@@ -237,8 +237,6 @@ def main():
     y = torch.empty(H, device=dev)
 
     def step(c):
-        # two launches: gate+up (x prepared inside; the SwiGLU written as the
-        # down projection's activation), down
         tg, tu, td = copies[c]
         G.dense_mlp(tg, tu, td, H, I, xd, SWIGLU_LIMIT, out=y, ws=ws_mlp)
 
@@ -268,34 +266,50 @@ def main():
     # duration = elapsed / launches (inter-launch gaps included, so it errs
     # low).
     log("kernel timing")
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=side):
-            for c in range(args.copies):
-                step(c)
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    reps = max(4, args.steps // args.copies)
-    graph.replay()
-    torch.cuda.synchronize()
-    k0 = torch.cuda.Event(enable_timing=True)
-    k1 = torch.cuda.Event(enable_timing=True)
-    k0.record()
-    for _ in range(reps):
-        graph.replay()
-    k1.record()
-    torch.cuda.synchronize()
-    pair_ms = k0.elapsed_time(k1) / (reps * args.copies)  # one gate+up + one down launch
+
+    def time_per_step(fn):
+        """ms per step: HIP graph replays of all copies in turn where the launches
+        can be captured (no host gaps), else back-to-back eager steps."""
+        reps = max(4, args.steps // args.copies)
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=side):
+                    for c in range(args.copies):
+                        fn(c)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / (reps * args.copies), "graph"
+        except Exception as exc:  # capture unsupported for this launch
+            log(f"graph capture unavailable ({type(exc).__name__}): eager timing")
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps * args.copies):
+                fn(i % args.copies)
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / (reps * args.copies), "eager"
+
+    pair_ms, pair_timing = time_per_step(step)
     # dispatch-stamped events split the pair per kind (they add a little each)
     G.prof_start(2 * 64 + 8)
     for i in range(64):
         step(i % args.copies)
     dur = G.prof_read(G.PROF_GEMV).astype(np.float64)  # launch order: gate+up, down, ...
     per_kind = {"gate+up": dur[0::2], "down": dur[1::2]}
-    # k_gemv_t64 launches: bytes = packed W + input + output (the SwiGLU
-    # activation between them: I/256 blocks of 1024 B images + 16 B unscales)
+    # algorithmic bytes: packed W + x + the SwiGLU activation written and read
+    # (I/256 blocks of 1024 B images + 16 B unscales) + y
     act64 = (I // 256) * (1024 + 16)
     launch_bytes = {"gate+up": 2 * (W_BYTES // 3) + H * 4 + act64,
                     "down": W_BYTES // 3 + act64 + H * 4}
@@ -326,8 +340,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "k_gemv_t64", "avg_launch_us": round(pair_ms * 1e3 / 2, 3),
-                     "pair_us": round(pair_ms * 1e3, 3), "pair_algorithmic_bytes": pair_bytes,
-                     "launch_kinds": kinds},
+                     "pair_us": round(pair_ms * 1e3, 3), "timing": pair_timing,
+                     "pair_algorithmic_bytes": pair_bytes, "launch_kinds": kinds},
     }
     if not args.no_extra:
         del copies, base

@@ -1,5 +1,6 @@
 // C ABI (include/gpeed_iq3.h) over the gfx950 kernels.
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -434,9 +435,7 @@ size_t gpeed_iq3xxs_dense_mlp_ws_bytes(int64_t hidden, int64_t inter) {
     if (hidden <= 0 || inter <= 0 || hidden % gpeed::kQK || inter % gpeed::kQK || hidden > (1 << 24) ||
         inter > (1 << 24))
         return 0;
-    // [act64 of h][gate/up tickets + partials][down tickets + partials]
-    return align256(gpeed::act64_bytes((int)inter)) + align256(gpeed::gate_up_ws_bytes((int)hidden, (int)inter)) +
-           align256(gpeed::gemv_ws_bytes(1, (int)inter, (int)hidden, 1));
+    return gpeed::dense_mlp_ws_bytes((int)hidden, (int)inter);
 }
 
 int gpeed_iq3xxs_dense_mlp(const void* w_gate, const void* w_up, const void* w_down, int hidden, int inter,
@@ -451,15 +450,10 @@ int gpeed_iq3xxs_dense_mlp(const void* w_gate, const void* w_up, const void* w_d
     const DeviceState* st = nullptr;
     int rc = device_state(&st);
     if (rc) return rc;
-    uint8_t* act = static_cast<uint8_t*>(ws);
-    uint8_t* ws_gu = act + align256(gpeed::act64_bytes(inter));
-    uint8_t* ws_d = ws_gu + align256(gpeed::gate_up_ws_bytes(hidden, inter));
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e = gpeed::launch_gate_up_swiglu(static_cast<const uint8_t*>(w_gate), static_cast<const uint8_t*>(w_up),
-                                                hidden, inter, x, limit, act, ws_gu, st->num_cus, s);
-    if (e != hipSuccess) return hip_fail(e, "dense_mlp gate/up launch");
-    e = gpeed::launch_gemv_act64(static_cast<const uint8_t*>(w_down), inter, 0, hidden, act, y, ws_d, st->num_cus, s);
-    return e == hipSuccess ? GPEED_OK : hip_fail(e, "dense_mlp down launch");
+    const hipError_t e = gpeed::launch_dense_mlp(
+        static_cast<const uint8_t*>(w_gate), static_cast<const uint8_t*>(w_up), static_cast<const uint8_t*>(w_down),
+        hidden, inter, x, limit, y, static_cast<uint8_t*>(ws), st->num_cus, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "dense_mlp launch");
 }
 
 int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,

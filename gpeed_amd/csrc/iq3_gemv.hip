@@ -139,8 +139,9 @@ struct ModeCfg {
     // (prepared from x, g/u, or copied from act64 images)
     static constexpr bool kPrep = MODE == 1 || MODE == 2 || MODE == 3;
     // MODE 1/2: records per wavefront (chunk <= kWaves * kMaxPer); each
-    // wavefront prepares the activation blocks of its own records
-    static constexpr int kMaxPer = 6;
+    // wavefront prepares the activation blocks of its own records (48
+    // records, 48 KB of images, per workgroup)
+    static constexpr int kMaxPer = 48 / GEMV_WAVES;
 };
 
 // act64 layout (one vector, n = K/256 blocks): block b at b*1024, its
@@ -166,10 +167,14 @@ struct GemvArgs {
     const float* x2;       // ... and u for the SwiGLU input
     float lim;
     uint8_t* act_out;      // EPI 1: act64 images of SwiGLU(gate, up)
+    uint32_t w_bytes;      // bytes of each tensor's records from w[i] (< 2^31)
 };
 
 // buffer resource word 3 for raw (untyped) buffer loads on gfx9
 constexpr int kBufferDword3 = 0x00020000;
+// a buffer offset no resource here reaches: the load returns zeros and
+// touches no memory
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 template <int NT, int MODE>
 struct Slots {
@@ -179,8 +184,10 @@ struct Slots {
 // Record rec of the launch (in chunk order): virtual tile vt = rec / nb;
 // EPI 0 keeps the tensors one after the other (vt = tensor * n_tiles +
 // row tile), EPI 1 interleaves them (vt = 2 * row tile + tensor).
-template <int EPI>
-__device__ __forceinline__ const uint8_t* record_ptr(const GemvArgs& g, int rec) {
+template <int NT, int MODE, int EPI>
+__device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g, int rec, bool live,
+                                         uint32_t lane) {
+    constexpr int NP = (NT + 1) / 2;
     const int vt = rec / g.nb;
     const int b = rec - vt * g.nb;
     int ten, rt;
@@ -191,17 +198,31 @@ __device__ __forceinline__ const uint8_t* record_ptr(const GemvArgs& g, int rec)
         ten = vt >= g.n_tiles ? 1 : 0;
         rt = vt - ten * g.n_tiles;
     }
-    return g.w[ten] + ((size_t)rt * g.nb + b) * kRecordBytes;
-}
-
-template <int NT, int MODE, int EPI>
-__device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g, int rec, uint32_t lane) {
-    const uint8_t* p = record_ptr<EPI>(g, rec);
-    if constexpr (ModeCfg<MODE>::kPrep) {
-        load_record_w(r, p, lane);  // images come from LDS
-    } else {
-        const int b = rec % g.nb;
-        load_record<(NT + 1) / 2>(r, p, g.act + (size_t)b * NT * 1024, lane, NT);
+    // buffer loads: a slot refilled past the wavefront's records gets an
+    // out-of-range offset, so it costs no memory traffic (and no place in
+    // the queue ahead of the epilogue's loads and stores)
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.w[ten]), 0, g.w_bytes, kBufferDword3);
+    const uint32_t off = live ? (uint32_t)(rt * g.nb + b) * (uint32_t)kRecordBytes : kOutOfRange;
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+        r.u[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off + i * kUnitBytes + lane * 16u, 0, 0));
+    r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, off + kRecordDOffset + lane * 2u, 0, 0);
+    if constexpr (!ModeCfg<MODE>::kPrep) {
+        // the record's prepared activation (n_tok vectors; a last pair with
+        // one token stores rows 0, 1 only, 256-byte images)
+        const auto ra =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.act), 0, g.nb * NT * 1024, kBufferDword3);
+        const uint32_t aoff = live ? (uint32_t)b * NT * 1024u : kOutOfRange;
+        const uint32_t off_half = ((lane >> 2) * 2 + (lane & 1)) * 8u;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const bool half = (p == NP - 1) && (NT & 1);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const uint32_t o = aoff + p * 2048 + (half ? a * 256u + off_half : a * 512u + lane * 8u);
+                r.a[p][a] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ra, o, 0, 0));
+            }
+        }
     }
 }
 
@@ -243,142 +264,158 @@ __device__ __forceinline__ float split_hi_lo(const float (&e)[4], u32x2_t& hi2, 
     return ldexpf(1.0f, -sc);
 }
 
-// y (per tensor) or, EPI 1, act64 images from the per-workgroup row sums.
-// Structure:
-//   prologue  grid table from immediates, the wavefronts' activation loads
-//             (MODE 1/2), one workgroup barrier (no memory wait before it),
-//             then the record ring and each wavefront's own preparation;
-//   loop      wavefront w streams records c0+w, c0+w+W, ... of its chunk;
-//   epilogue  per-tile sums over the wavefronts, shared tiles completed by
-//             the last workgroup to arrive (ticket), partials added in chunk
-//             order (results do not depend on timing).
+// ---------------------------------------------------------------------------
+// GEMV workgroup building blocks. A workgroup owns records [c0, c1) of a
+// launch (chunk order); wavefront w streams records c0+w, c0+w+W, ... (its
+// k-th record is c0 + w + k*W) through a register ring of PF slots.
+
+// LDS of one workgroup; layout L = 1 when the activation images sit in
+// per-wavefront regions (MODE 1, 2, 3), 0 when they come with the records.
+template <int MODE>
+constexpr int shared_layout() { return ModeCfg<MODE>::kPrep ? 1 : 0; }
+
+template <int NT, int L>
+struct GemvShared {
+    static constexpr int W = GemvCfg<NT>::kWaves;
+    static constexpr int S = L ? 4 : GemvCfg<NT>::kSlots;
+    static constexpr bool kPrep = L != 0;
+    static constexpr int KP = kPrep ? ModeCfg<1>::kMaxPer : 1;
+    __attribute__((aligned(16))) uint8_t tbl[kGridTableBytes];  // replicated grid table
+    float red[S][W][NT][64];                                     // wavefront row sums per tile slot
+    __attribute__((aligned(16))) uint8_t xsl[kPrep ? W * KP * 1024 : 16];  // per-wavefront activation images
+    __attribute__((aligned(16))) float xscl[kPrep ? W * KP * 4 : 4];      // and their unscales
+    float vsum[S][64];                                           // workgroup row sums (SwiGLU epilogue)
+    int flag[S];
+};
+
+// The chunk of workgroup `blk` and this wavefront's share of it.
+struct Chunk {
+    int c0, c1, n_mine, tile0;
+    __device__ Chunk(const GemvArgs& g, int blk, int wave, int W) {
+        c0 = blk * g.chunk;
+        c1 = min(c0 + g.chunk, g.n_records);
+        n_mine = c1 - c0 > wave ? (c1 - c0 - wave + W - 1) / W : 0;
+        tile0 = c0 / g.nb;
+    }
+    __device__ int rec(int k, int wave, int W) const { return min(c0 + wave + k * W, c1 - 1); }
+};
+
+// Records of one launch for the ring: k-th record of this wavefront.
 template <int NT, int MODE, int EPI>
-__global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs g) {
-    static_assert(MODE == 0 || NT == 1, "prepared-in-kernel and act64 activations take one vector");
-    static_assert(EPI == 0 || (NT == 1 && MODE == 1), "the SwiGLU epilogue takes gate/up of one vector");
-    constexpr int W = GemvCfg<NT>::kWaves;
-    constexpr int PF = GemvCfg<NT>::kPF;
-    constexpr int S = Slots<NT, MODE>::value;
-    constexpr int NP = GemvCfg<NT>::kPairs;
-    constexpr int kThreads = W * 64;
-    constexpr bool kPrep = ModeCfg<MODE>::kPrep;
-    constexpr int KP = kPrep ? ModeCfg<MODE>::kMaxPer : 1;
-    __shared__ __attribute__((aligned(16))) uint8_t tbl[kGridTableBytes];
-    __shared__ float red[S][W][NT][64];
-    __shared__ int last_flag[S];
-    __shared__ __attribute__((aligned(16))) uint8_t xsl[kPrep ? W * KP * 1024 : 16];
-    __shared__ __attribute__((aligned(16))) float xscl[kPrep ? W * KP * (MODE == 3 ? 4 : 1) : 1];
+struct OnePhase {
+    const GemvArgs& g;
+    Chunk ch;
+    int wave;
+    static constexpr int W = GemvCfg<NT>::kWaves;
+    __device__ void load(Rec<(NT + 1) / 2>& r, int k, uint32_t lane) const {
+        load_rec<NT, MODE, EPI>(r, g, ch.rec(k, wave, W), k < ch.n_mine, lane);
+    }
+};
 
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t lane = tid & 63;
-    const uint32_t lb = (lane & 31u) << 3;  // this lane's replica of the grid table
+// Grid table (immediate data) and zeroed row sums: LDS writes only.
+template <int NT, int MODE>
+__device__ __forceinline__ void gemv_lds_init(GemvShared<NT, shared_layout<MODE>()>& sh, int wave, uint32_t lane,
+                                              int tid) {
+    constexpr int W = GemvCfg<NT>::kWaves, S = GemvShared<NT, shared_layout<MODE>()>::S;
+    grid_table_literal<W>(sh.tbl, wave, lane);
+    for (int i = tid; i < S * W * NT * 64; i += W * 64) (&sh.red[0][0][0][0])[i] = 0.0f;
+}
 
-    // grid table and zeroed partials: LDS writes only, no memory dependence
-    grid_table_literal<W>(tbl, wave, lane);
-    for (int i = tid; i < S * W * NT * 64; i += kThreads) (&red[0][0][0][0])[i] = 0.0f;
-
-    const int c0 = blockIdx.x * g.chunk;
-    const int c1 = min(c0 + g.chunk, g.n_records);
-    const int n_mine = c1 - c0 > wave ? (c1 - c0 - wave + W - 1) / W : 0;
-    const int tile0 = c0 / g.nb;
-
-    // The activation of each of this wavefront's records: its fp32 block
-    // (MODE 1), g and u blocks (MODE 2) or its act64 images and unscales
-    // (MODE 3), 16 bytes per lane. Buffer loads: an offset past the end
-    // returns zeros without a memory access, so every wavefront issues the
-    // same loads, unbranched.
+// The activation of each of this wavefront's records: its fp32 block
+// (MODE 1), g and u blocks (MODE 2) or its act64 images and unscales
+// (MODE 3), 16 bytes per lane. Buffer loads: an offset past the end returns
+// zeros without a memory access, so every wavefront issues the same loads,
+// unbranched. kCoherent: read past other XCDs' caches (data written by
+// other workgroups of the same launch).
+template <int MODE, int KP, int W, bool kCoherent = false>
+struct ActLoads {
     float4 xv[KP], uv[MODE == 2 ? KP : 1], sv[MODE == 3 ? KP : 1];
-    if constexpr (kPrep) {
+    __device__ void issue(const GemvArgs& g, const Chunk& ch, int wave, uint32_t lane) {
+        constexpr int kAux = kCoherent ? 16 : 0;  // sc1
         const void* src = MODE == 3 ? static_cast<const void*>(g.act) : static_cast<const void*>(g.x);
         const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(src), 0, g.nb * 1024, kBufferDword3);
         const auto ur = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(MODE == 3 ? g.xsc : g.x2), 0,
                                                           MODE == 3 ? g.nb * 16 : g.nb * 1024, kBufferDword3);
 #pragma unroll
         for (int k = 0; k < KP; ++k) {
-            const int b = (c0 + wave + k * W) % g.nb;
-            const bool ok = k < n_mine;
+            const int b = (ch.c0 + wave + k * W) % g.nb;
+            const bool ok = k < ch.n_mine;
             const uint32_t off = ok ? (uint32_t)b * 1024u + lane * 16u : 0x80000000u;
-            xv[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            xv[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kAux));
             if constexpr (MODE == 2)
-                uv[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, 0));
+                uv[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, kAux));
             if constexpr (MODE == 3)
                 sv[k] = __builtin_bit_cast(
-                    float4, __builtin_amdgcn_raw_buffer_load_b128(ur, ok ? (uint32_t)b * 16u : 0x80000000u, 0, 0));
+                    float4, __builtin_amdgcn_raw_buffer_load_b128(ur, ok ? (uint32_t)b * 16u : 0x80000000u, 0, kAux));
         }
     }
-    // One barrier: the table is complete, and (a CU serves its vector memory
-    // queue in order) every wavefront's activation loads are queued ahead of
-    // all record loads. Nothing before it waits for memory.
-    lds_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-
-    // First ring slot, then this wavefront's activation (its loads were
-    // queued first, so waiting for them does not wait for the records),
-    // then the remaining slots: a CU takes only so many outstanding loads,
-    // and a wavefront stalled issuing records cannot prepare.
-    Rec<NP> ring[PF];
-    load_rec<NT, MODE, EPI>(ring[0], g, min(c0 + wave, c1 - 1), lane);
-
-    if constexpr (MODE == 3) {
-        // copy: the act64 block keeps its layout in the private region
+    // images (prepared, or copied for MODE 3) into the wavefront's region
+    template <int NT>
+    __device__ void commit(GemvShared<NT, 1>& sh, const GemvArgs& g, const Chunk& ch, int wave, uint32_t lane) {
 #pragma unroll
         for (int k = 0; k < KP; ++k) {
-            if (k < n_mine) {
-                *reinterpret_cast<float4*>(xsl + (wave * KP + k) * 1024 + lane * 16) = xv[k];
-                if (lane == 0) *reinterpret_cast<float4*>(&xscl[(wave * KP + k) * 4]) = sv[k];
-            }
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    } else if constexpr (kPrep) {
-        // this wavefront's images (private LDS region: no workgroup barrier)
-        const int a = lane >> 4, beta = lane & 15;
+            if (k < ch.n_mine) {
+                uint8_t* region = sh.xsl + (wave * KP + k) * 1024;
+                if constexpr (MODE == 3) {
+                    *reinterpret_cast<float4*>(region + lane * 16) = xv[k];  // act64 keeps its layout
+                    if (lane == 0) *reinterpret_cast<float4*>(&sh.xscl[(wave * KP + k) * 4]) = sv[k];
+                } else {
+                    float e[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+                    if constexpr (MODE == 2) {
+                        const float us[4] = {uv[k].x, uv[k].y, uv[k].z, uv[k].w};
 #pragma unroll
-        for (int k = 0; k < KP; ++k) {
-            if (k < n_mine) {
-                float e[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
-                if constexpr (MODE == 2) {
-                    const float us[4] = {uv[k].x, uv[k].y, uv[k].z, uv[k].w};
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) e[c] = swiglu1(e[c], us[c], g.lim);
+                        for (int c = 0; c < 4; ++c) e[c] = swiglu1(e[c], us[c], g.lim);
+                    }
+                    u32x2_t hi, lo;
+                    const float unscale = split_hi_lo(e, hi, lo);
+                    // lane 4*beta+rho of register a holds variant rho (0 hi,
+                    // 1 lo) of slice beta at a*256 + (2*beta+rho)*8
+                    uint8_t* dst = region + (lane >> 4) * 256 + (lane & 15) * 16;
+                    *reinterpret_cast<u32x2_t*>(dst) = hi;
+                    *reinterpret_cast<u32x2_t*>(dst + 8) = lo;
+                    if (lane == 0) sh.xscl[(wave * KP + k) * 4] = unscale;
                 }
-                u32x2_t hi, lo;
-                const float unscale = split_hi_lo(e, hi, lo);
-                // lane 4*beta+rho of register a holds variant rho (0 hi, 1 lo)
-                // of slice beta at a*256 + (2*beta+rho)*8
-                uint8_t* dst = xsl + (wave * KP + k) * 1024 + a * 256 + beta * 16;
-                *reinterpret_cast<u32x2_t*>(dst) = hi;
-                *reinterpret_cast<u32x2_t*>(dst + 8) = lo;
-                if (lane == 0) xscl[wave * KP + k] = unscale;
             }
         }
         // lanes read other lanes' writes of the same wavefront: LDS
         // operations of one wavefront complete in order
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-#pragma unroll
-    for (int s = 1; s < PF; ++s) load_rec<NT, MODE, EPI>(ring[s], g, min(c0 + wave + s * W, c1 - 1), lane);
+};
 
+// Records k in [kbeg, kend) of this wavefront's sequence `src`, whose ring
+// slot k % PF already holds record k; the row sums go to sh.red by tile
+// slot. A slot is refilled with record k + PF after its use, and only
+// then: past kend it keeps its record (the next phase's), so the loads stay
+// the same whatever the branch and the compiler waits for exactly the slot
+// it needs.
+template <int NT, int MODE, int EPI, typename Src>
+__device__ __forceinline__ void gemv_stream(GemvShared<NT, shared_layout<MODE>()>& sh, const GemvArgs& g,
+                                            Rec<(NT + 1) / 2> (&ring)[GemvCfg<NT>::kPF],
+                                            const Src& src, const Chunk& ch, int kbeg, int kend, int wave,
+                                            uint32_t lane) {
+    constexpr int W = GemvCfg<NT>::kWaves, PF = GemvCfg<NT>::kPF, NP = GemvCfg<NT>::kPairs;
+    constexpr bool kPrep = ModeCfg<MODE>::kPrep;
+    constexpr int KP = GemvShared<NT, shared_layout<MODE>()>::KP;
+    const uint32_t lb = (lane & 31u) << 3;  // this lane's replica of the grid table
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     int cur_slot = -1;
-    // Every iteration issues the same loads whatever the branch (a refill
-    // past the wave's last record re-reads the chunk's last one), so the
-    // compiler waits for exactly the ring slot it needs, not for every load.
-    for (int k0 = 0; k0 < n_mine; k0 += PF) {
+    for (int k0 = kbeg - kbeg % PF; k0 < kend; k0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; ++s) {
             const int k = k0 + s;
-            const bool valid = k < n_mine;
-            const int rec = min(c0 + wave + k * W, c1 - 1);
+            const int kk = k - kbeg;  // index within this phase
+            const bool valid = k >= kbeg && k < kend;
+            const int rec = ch.rec(kk, wave, W);
             const int tile = rec / g.nb;
             const int b = rec - tile * g.nb;
-            const int slot = tile - tile0;
+            const int slot = tile - ch.tile0;
             if (valid && slot != cur_slot) {
                 if (cur_slot >= 0) {
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) red[cur_slot][wave][t][lane] = acc[t];
+                    for (int t = 0; t < NT; ++t) sh.red[cur_slot][wave][t][lane] = acc[t];
                 }
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -387,25 +424,23 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
             if (valid) {
                 const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)ring[s].d) * 0.25f;
                 if constexpr (kPrep) {
-                    const uint8_t* src = xsl + (wave * KP + k) * 1024 + ((lane >> 2) * 2 + (lane & 1)) * 8;
+                    const uint8_t* a_src = sh.xsl + (wave * KP + kk) * 1024 + ((lane >> 2) * 2 + (lane & 1)) * 8;
 #pragma unroll
-                    for (int a = 0; a < 4; ++a) ring[s].a[0][a] = *reinterpret_cast<const u32x2_t*>(src + a * 256);
+                    for (int a = 0; a < 4; ++a) ring[s].a[0][a] = *reinterpret_cast<const u32x2_t*>(a_src + a * 256);
                 }
                 if constexpr (MODE == 3) {
                     float blk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                    record_dot_img(tbl, ring[s], lb, blk);
-                    const float4 xs = *reinterpret_cast<const float4*>(&xscl[(wave * KP + k) * 4]);
+                    record_dot<1, true>(sh.tbl, ring[s], lb, blk);
+                    const float4 xs = *reinterpret_cast<const float4*>(&sh.xscl[(wave * KP + kk) * 4]);
                     acc[0] = fmaf(d4, fmaf(xs.x, blk[0], fmaf(xs.y, blk[1], fmaf(xs.z, blk[2], xs.w * blk[3]))),
                                   acc[0]);
                 } else {
-                    float us = 0.0f;
-                    if constexpr (kPrep) us = xscl[wave * KP + k];
                     float blk[2 * NP];
 #pragma unroll
                     for (int t = 0; t < 2 * NP; ++t) blk[t] = 0.0f;
-                    record_dot<NP>(tbl, ring[s], lb, blk);
+                    record_dot<NP>(sh.tbl, ring[s], lb, blk);
                     if constexpr (kPrep) {
-                        acc[0] = fmaf(d4 * us, blk[0], acc[0]);
+                        acc[0] = fmaf(d4 * sh.xscl[(wave * KP + kk) * 4], blk[0], acc[0]);
                     } else {
                         const float* xs = g.xsc + (size_t)b * NT;
 #pragma unroll
@@ -413,153 +448,203 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
                     }
                 }
             }
-            // refill, clamped to the chunk's last record (a valid address)
-            load_rec<NT, MODE, EPI>(ring[s], g, min(c0 + wave + (k + PF) * W, c1 - 1), lane);
+            // refill with record k + PF once used; otherwise reload what the
+            // slot holds (k + PF before kbeg, k itself from kend on)
+            src.load(ring[s], k < kend ? k + PF : k, lane);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
     if (cur_slot >= 0) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) red[cur_slot][wave][t][lane] = acc[t];
+        for (int t = 0; t < NT; ++t) sh.red[cur_slot][wave][t][lane] = acc[t];
     }
-    lds_barrier();
+}
 
-    const int n_slots = (c1 - 1) / g.nb - tile0 + 1;
+// EPI 0 epilogue: sum the wavefront partials per (tile, token, row) in wave
+// order; whole tiles go straight to y, tiles shared with a neighbouring
+// chunk (only the chunk's first and last can be) through the workspace,
+// completed by the last workgroup to take the tile's ticket, which adds the
+// partials in chunk order. Call after a barrier that completes sh.red.
+template <int NT, int MODE>
+__device__ __forceinline__ void gemv_epilogue_y(GemvShared<NT, shared_layout<MODE>()>& sh, const GemvArgs& g,
+                                                const Chunk& ch, int blk, int tid) {
+    constexpr int W = GemvCfg<NT>::kWaves, kThreads = W * 64;
+    const int n_slots = (ch.c1 - 1) / g.nb - ch.tile0 + 1;
     auto first_chunk = [&](int vt) { return vt * g.nb / g.chunk; };
     auto last_chunk = [&](int vt) { return ((vt + 1) * g.nb - 1) / g.chunk; };
-    if constexpr (EPI == 0) {
-        // Sum the wavefront partials per (tile, token, row) in wave order;
-        // whole tiles go straight to y, tiles shared with a neighbouring
-        // chunk (only the chunk's first and last can be) to the workspace.
-        for (int o = tid; o < n_slots * NT * 64; o += kThreads) {
-            const int slot = o / (NT * 64), t = (o / 64) % NT, n = o & 63;
-            float sum = 0.0f;
+    for (int o = tid; o < n_slots * NT * 64; o += kThreads) {
+        const int slot = o / (NT * 64), t = (o / 64) % NT, n = o & 63;
+        float sum = 0.0f;
 #pragma unroll
-            for (int v = 0; v < W; ++v) sum += red[slot][v][t][n];
-            const int tile = tile0 + slot;
-            const int first = first_chunk(tile);
-            if (first == last_chunk(tile)) {
-                const int ten = tile >= g.n_tiles ? 1 : 0;
-                const int row = (tile - ten * g.n_tiles) * kTileRows + n;
-                if (row < g.out_dim) g.y[ten][(size_t)t * g.out_dim + row] = sum;
-            } else {
-                // coherent across the XCDs' L2s without a full-cache writeback
-                __hip_atomic_store(g.part + (((size_t)tile * g.max_parts + (blockIdx.x - first)) * NT + t) * 64 + n,
-                                   sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        const int tile_end = tile0 + n_slots - 1;
-        const bool any_shared = first_chunk(tile0) != last_chunk(tile0) ||
-                                first_chunk(tile_end) != last_chunk(tile_end);
-        if (!any_shared) return;  // uniform
-        // Partials complete (vmcnt(0)) before any thread of the workgroup
-        // takes a ticket; the ticket holder that completes a tile then reads
-        // the other chunks' partials with coherent loads.
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        __syncthreads();
-        if (tid < n_slots) {
-            const int tile = tile0 + tid;
-            const int first = first_chunk(tile), last = last_chunk(tile);
-            int is_last = 0;
-            if (first != last) {
-                const uint32_t old = __hip_atomic_fetch_add(g.cnt + tile, 1u, __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT);
-                is_last = old == (uint32_t)(last - first);
-            }
-            last_flag[tid] = is_last;
-        }
-        __syncthreads();
-        for (int o = tid; o < n_slots * NT * 64; o += kThreads) {
-            const int slot = o / (NT * 64), t = (o / 64) % NT, n = o & 63;
-            if (!last_flag[slot]) continue;
-            const int tile = tile0 + slot;
-            const int parts = last_chunk(tile) - first_chunk(tile) + 1;
-            float sum = 0.0f;
-            for (int j = 0; j < parts; ++j)
-                sum += __hip_atomic_load(g.part + (((size_t)tile * g.max_parts + j) * NT + t) * 64 + n,
-                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int v = 0; v < W; ++v) sum += sh.red[slot][v][t][n];
+        const int tile = ch.tile0 + slot;
+        const int first = first_chunk(tile);
+        if (first == last_chunk(tile)) {
             const int ten = tile >= g.n_tiles ? 1 : 0;
             const int row = (tile - ten * g.n_tiles) * kTileRows + n;
             if (row < g.out_dim) g.y[ten][(size_t)t * g.out_dim + row] = sum;
+        } else {
+            // coherent across the XCDs' L2s without a full-cache writeback
+            __hip_atomic_store(g.part + (((size_t)tile * g.max_parts + (blk - first)) * NT + t) * 64 + n, sum,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (tid < n_slots && last_flag[tid])
-            __hip_atomic_store(g.cnt + tile0 + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const int tile_end = ch.tile0 + n_slots - 1;
+    const bool any_shared = first_chunk(ch.tile0) != last_chunk(ch.tile0) ||
+                            first_chunk(tile_end) != last_chunk(tile_end);
+    if (!any_shared) return;  // uniform
+    // Partials complete (vmcnt(0)) before any thread of the workgroup takes
+    // a ticket; the ticket holder that completes a tile then reads the other
+    // chunks' partials with coherent loads.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (tid < n_slots) {
+        const int tile = ch.tile0 + tid;
+        const int first = first_chunk(tile), last = last_chunk(tile);
+        int is_last = 0;
+        if (first != last) {
+            const uint32_t old = __hip_atomic_fetch_add(g.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            is_last = old == (uint32_t)(last - first);
+        }
+        sh.flag[tid] = is_last;
+    }
+    __syncthreads();
+    for (int o = tid; o < n_slots * NT * 64; o += kThreads) {
+        const int slot = o / (NT * 64), t = (o / 64) % NT, n = o & 63;
+        if (!sh.flag[slot]) continue;
+        const int tile = ch.tile0 + slot;
+        const int parts = last_chunk(tile) - first_chunk(tile) + 1;
+        float sum = 0.0f;
+        for (int j = 0; j < parts; ++j)
+            sum += __hip_atomic_load(g.part + (((size_t)tile * g.max_parts + j) * NT + t) * 64 + n, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        const int ten = tile >= g.n_tiles ? 1 : 0;
+        const int row = (tile - ten * g.n_tiles) * kTileRows + n;
+        if (row < g.out_dim) g.y[ten][(size_t)t * g.out_dim + row] = sum;
+    }
+    if (tid < n_slots && sh.flag[tid])
+        __hip_atomic_store(g.cnt + ch.tile0 + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// EPI 1 epilogue: virtual tiles 2r (gate) and 2r+1 (up) of row tile r form
+// a pair shared by chunks first_chunk(2r) .. last_chunk(2r+1); the
+// workgroup completing a pair writes SwiGLU of its 64 rows as act64 images.
+__device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const GemvArgs& g, const Chunk& ch,
+                                                     int blk, int tid, int wave, uint32_t lane) {
+    constexpr int W = GemvCfg<1>::kWaves, kThreads = W * 64;
+    const int n_slots = (ch.c1 - 1) / g.nb - ch.tile0 + 1;
+    auto first_chunk = [&](int vt) { return vt * g.nb / g.chunk; };
+    auto last_chunk = [&](int vt) { return ((vt + 1) * g.nb - 1) / g.chunk; };
+    const int p0 = ch.tile0 >> 1;
+    const int n_pairs = (ch.tile0 + n_slots - 1) / 2 - p0 + 1;
+    // (a) wavefront sums of every touched virtual tile
+    for (int o = tid; o < n_slots * 64; o += kThreads) {
+        const int slot = o / 64, n = o & 63;
+        float sum = 0.0f;
+#pragma unroll
+        for (int v = 0; v < W; ++v) sum += sh.red[slot][v][0][n];
+        sh.vsum[slot][n] = sum;
+    }
+    __syncthreads();
+    // (b) pairs wholly inside this chunk are final here; the others publish
+    // their partials and take a ticket
+    for (int o = tid; o < n_slots * 64; o += kThreads) {
+        const int slot = o / 64, n = o & 63;
+        const int vt = ch.tile0 + slot, pr = vt >> 1;
+        const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
+        if (first != last)
+            __hip_atomic_store(g.part + (((size_t)pr * g.max_parts + (blk - first)) * 2 + (vt & 1)) * 64 + n,
+                               sh.vsum[slot][n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (tid < n_pairs) {
+        const int pr = p0 + tid;
+        const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
+        int st = 1;
+        if (first != last) {
+            const uint32_t old = __hip_atomic_fetch_add(g.cnt + pr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            st = old == (uint32_t)(last - first) ? 1 : 0;
+        }
+        sh.flag[tid] = st;
+    }
+    __syncthreads();
+    // (c) wavefront q completes pair p0+q: gate and up rows, SwiGLU, one
+    // power-of-two scale over the 64 values, fp16 hi/lo act64 images
+    for (int q = wave; q < n_pairs; q += W) {
+        if (!sh.flag[q]) continue;  // uniform per wavefront
+        const int pr = p0 + q;
+        const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
+        float v[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int vt = 2 * pr + h;
+            if (first == last) {
+                v[h] = sh.vsum[vt - ch.tile0][lane];
+            } else {
+                v[h] = 0.0f;
+                const int j0 = first_chunk(vt) - first, j1 = last_chunk(vt) - first;
+                for (int j = j0; j <= j1; ++j)
+                    v[h] += __hip_atomic_load(g.part + (((size_t)pr * g.max_parts + j) * 2 + h) * 64 + lane,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        const float hv = swiglu1(v[0], v[1], g.lim);
+        const int sc = pow2_scale(fabsf(hv));
+        const float xs = ldexpf(hv, sc);
+        const _Float16 hi = (_Float16)xs;
+        const _Float16 lo = (_Float16)(xs - (float)hi);
+        // element `lane` of image a = pr & 3 of block pr >> 2: slice beta =
+        // lane >> 2 at +beta*16, hi at +2c, lo at +8+2c (c = lane & 3)
+        const int blk_o = pr >> 2, a = pr & 3, beta = lane >> 2, c = lane & 3;
+        uint8_t* dst = g.act_out + (size_t)blk_o * 1024 + a * 256 + beta * 16;
+        float* usc = reinterpret_cast<float*>(g.act_out + (size_t)(g.n_tiles / 4) * 1024);
+        *reinterpret_cast<_Float16*>(dst + 2 * c) = hi;
+        *reinterpret_cast<_Float16*>(dst + 8 + 2 * c) = lo;
+        if (lane == 0) usc[blk_o * 4 + a] = ldexpf(1.0f, -sc);
+        if (lane == 0 && first != last)
+            __hip_atomic_store(g.cnt + pr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// y (per tensor) or, EPI 1, act64 images: prologue (grid table, the
+// wavefronts' activation loads, one workgroup barrier with no memory wait
+// before it, first ring slot, the wavefront's own activation images, the
+// other slots), the record stream, the epilogue.
+template <int NT, int MODE, int EPI>
+__global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs g) {
+    static_assert(MODE == 0 || NT == 1, "prepared-in-kernel and act64 activations take one vector");
+    static_assert(EPI == 0 || (NT == 1 && MODE == 1), "the SwiGLU epilogue takes gate/up of one vector");
+    constexpr int W = GemvCfg<NT>::kWaves;
+    constexpr int PF = GemvCfg<NT>::kPF;
+    constexpr bool kPrep = ModeCfg<MODE>::kPrep;
+    constexpr int KP = GemvShared<NT, shared_layout<MODE>()>::KP;
+    __shared__ GemvShared<NT, shared_layout<MODE>()> sh;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t lane = tid & 63;
+    gemv_lds_init<NT, MODE>(sh, wave, lane, tid);
+    const Chunk ch(g, blockIdx.x, wave, W);
+    ActLoads<MODE, KP, W> act;
+    if constexpr (kPrep) act.issue(g, ch, wave, lane);
+    // the table is complete, and (a CU serves its vector memory queue in
+    // order) every wavefront's activation loads are queued ahead of all
+    // record loads
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const OnePhase<NT, MODE, EPI> src{g, ch, wave};
+    Rec<(NT + 1) / 2> ring[PF];
+    src.load(ring[0], 0, lane);
+    if constexpr (kPrep) act.commit(sh, g, ch, wave, lane);
+#pragma unroll
+    for (int s = 1; s < PF; ++s) src.load(ring[s], s, lane);
+    gemv_stream<NT, MODE, EPI>(sh, g, ring, src, ch, 0, ch.n_mine, wave, lane);
+    lds_barrier();
+    if constexpr (EPI == 0) {
+        gemv_epilogue_y<NT, MODE>(sh, g, ch, blockIdx.x, tid);
     } else {
-        // EPI 1: virtual tiles 2r (gate) and 2r+1 (up) of row tile r; the
-        // pair is shared by the chunks first_chunk(2r) .. last_chunk(2r+1).
-        __shared__ int pair_state[S];  // 1: this workgroup completes the pair
-        const int p0 = tile0 >> 1;
-        const int n_pairs = (tile0 + n_slots - 1) / 2 - p0 + 1;
-        // (a) wave sums of every touched virtual tile
-        __shared__ float vsum[S][64];
-        for (int o = tid; o < n_slots * 64; o += kThreads) {
-            const int slot = o / 64, n = o & 63;
-            float sum = 0.0f;
-#pragma unroll
-            for (int v = 0; v < W; ++v) sum += red[slot][v][0][n];
-            vsum[slot][n] = sum;
-        }
-        __syncthreads();
-        // (b) pairs wholly inside this chunk are final; the others publish
-        // their partials and take a ticket
-        for (int o = tid; o < n_slots * 64; o += kThreads) {
-            const int slot = o / 64, n = o & 63;
-            const int vt = tile0 + slot, pr = vt >> 1;
-            const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
-            if (first != last)
-                __hip_atomic_store(g.part + (((size_t)pr * g.max_parts + (blockIdx.x - first)) * 2 + (vt & 1)) * 64 + n,
-                                   vsum[slot][n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        __syncthreads();
-        if (tid < n_pairs) {
-            const int pr = p0 + tid;
-            const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
-            int st = 1;
-            if (first != last) {
-                const uint32_t old = __hip_atomic_fetch_add(g.cnt + pr, 1u, __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT);
-                st = old == (uint32_t)(last - first) ? 1 : 0;
-            }
-            pair_state[tid] = st;
-        }
-        __syncthreads();
-        // (c) wavefront q completes pair p0+q: gate and up rows, SwiGLU,
-        // power-of-two scale over the 64 values, fp16 hi/lo act64 images
-        for (int q = wave; q < n_pairs; q += W) {
-            if (!pair_state[q]) continue;  // uniform per wavefront
-            const int pr = p0 + q;
-            const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
-            float v[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int vt = 2 * pr + h;
-                if (first == last) {
-                    v[h] = vsum[vt - tile0][lane];
-                } else {
-                    v[h] = 0.0f;
-                    const int j0 = first_chunk(vt) - first, j1 = last_chunk(vt) - first;
-                    for (int j = j0; j <= j1; ++j)
-                        v[h] += __hip_atomic_load(g.part + (((size_t)pr * g.max_parts + j) * 2 + h) * 64 + lane,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            const float hv = swiglu1(v[0], v[1], g.lim);
-            const int sc = pow2_scale(fabsf(hv));
-            const float xs = ldexpf(hv, sc);
-            const _Float16 hi = (_Float16)xs;
-            const _Float16 lo = (_Float16)(xs - (float)hi);
-            const int blk = pr >> 2, a = pr & 3, beta = lane >> 2, c = lane & 3;
-            uint8_t* dst = g.act_out + (size_t)blk * 1024 + a * 256 + beta * 16 + c * 2;
-            *reinterpret_cast<_Float16*>(dst) = hi;
-            *reinterpret_cast<_Float16*>(dst + 8) = lo;
-            if (lane == 0) {
-                float* usc = reinterpret_cast<float*>(g.act_out + (size_t)(g.n_tiles / 4) * 1024);
-                usc[blk * 4 + a] = ldexpf(1.0f, -sc);
-            }
-            if (lane == 0 && first != last)
-                __hip_atomic_store(g.cnt + pr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        gemv_epilogue_swiglu(sh, g, ch, blockIdx.x, tid, wave, lane);
     }
 }
 
@@ -611,6 +696,8 @@ __global__ __launch_bounds__(256) void k_matvec_raw(const uint8_t* __restrict__ 
 
 template <int NT, int MODE = 0, int EPI = 0>
 hipError_t launch_gemv_nt(const GemvPlan& plan, GemvArgs a, hipStream_t s) {
+    // records are addressed by 32-bit buffer offsets below kOutOfRange
+    if ((size_t)a.n_tiles * a.nb * kRecordBytes >= kOutOfRange) return hipErrorInvalidValue;
     a.chunk = plan.chunk;
     a.max_parts = plan.max_parts;
     return launch_timed(kProfGemv, k_gemv_t64<NT, MODE, EPI>, dim3(plan.grid), dim3(GemvCfg<NT>::kWaves * 64), 0, s,
@@ -635,6 +722,7 @@ GemvArgs base_args(const GemvPlan& plan, const uint8_t* const* w, float* const* 
     a.out_dim = out_dim;
     a.cnt = reinterpret_cast<uint32_t*>(ws);
     a.part = reinterpret_cast<float*>(ws + ((size_t)plan.n_tiles_all * 4 + 255) / 256 * 256);
+    a.w_bytes = (uint32_t)((size_t)a.n_tiles * a.nb * kRecordBytes);
     return a;
 }
 
@@ -760,6 +848,22 @@ hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int
     a.lim = lim;
     a.act_out = act_out;
     return launch_gemv_nt<1, 1, 1>(plan, a, s);
+}
+
+size_t dense_mlp_ws_bytes(int hidden, int inter) {
+    const auto a256 = [](size_t b) { return (b + 255) / 256 * 256; };
+    return a256(act64_bytes(inter)) + a256(gate_up_ws_bytes(hidden, inter)) + a256(gemv_ws_bytes(1, inter, hidden, 1));
+}
+
+hipError_t launch_dense_mlp(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int hidden, int inter,
+                            const float* x, float lim, float* y, uint8_t* ws, int num_cus, hipStream_t s) {
+    const auto a256 = [](size_t b) { return (b + 255) / 256 * 256; };
+    uint8_t* act = ws;
+    uint8_t* ws_a = act + a256(act64_bytes(inter));
+    uint8_t* ws_b = ws_a + a256(gate_up_ws_bytes(hidden, inter));
+    hipError_t e = launch_gate_up_swiglu(w_gate, w_up, hidden, inter, x, lim, act, ws_a, num_cus, s);
+    if (e != hipSuccess) return e;
+    return launch_gemv_act64(w_down, inter, 0, hidden, act, y, ws_b, num_cus, s);
 }
 
 hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,

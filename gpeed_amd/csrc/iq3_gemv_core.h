@@ -145,80 +145,79 @@ __device__ __forceinline__ void load_record_w(Rec<NP>& r, const uint8_t* rec, ui
     r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
 }
 
-// One record: lane n's 256 weights of row n against the NP token pairs;
-// blk[t] += (2s+1) * partial, per sub-block (blk[2p+1] of a single-token
-// last pair is meaningless).
-template <int NP>
+// The 8 grid lookups of one sub-block (two index words, 4 bytes each).
+__device__ __forceinline__ void grid_lookups(const uint8_t* tbl, uint32_t lb, uint32_t q0, uint32_t q1,
+                                             u32x2_t (&g)[8]) {
+    static_for<0, 8>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        const uint32_t q = m < 4 ? q0 : q1;
+        constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
+        g[m] = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, lb, sel));  // (idx << 8) | lb
+    });
+}
+
+// Sub-block ib of a record: sign word w, the 8 lookups g, products with the
+// NP token-pair images a; D[p] += A_p . B over the sub-block's 32 weights.
+template <int NP, int ib>
+__device__ __forceinline__ void subblock_dot(uint32_t w, const u32x2_t (&g)[8], const u32x2_t (&a)[NP][4],
+                                             float4_t (&D)[NP]) {
+    const uint32_t sw = t64_full_signs(w);
+    // The signs of a group's second pair sit 4 bits above those of its first
+    // pair, so {sw >> 4, sw} shifted left by one 64-bit shift puts both
+    // pairs' signs on bits 15 and 31 of the two halves.
+    const uint64_t sw2 = ((uint64_t)(sw >> 4) << 32) | sw;
+    static_for<0, 8>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        constexpr int a0 = 8 * (m & 1) + (m >> 1);  // first pair's sign bits: a0, a0 + 16
+        // one v_lshlrev_b64 (the compiler would split a C shift into two)
+        uint64_t rs;
+        asm("v_lshlrev_b64 %0, %1, %2" : "=v"(rs) : "n"(15 - a0), "v"(sw2));
+        const uint32_t bx = ((uint32_t)rs & 0x80008000u) | g[m].x;
+        const uint32_t by = ((uint32_t)(rs >> 32) & 0x80008000u) | g[m].y;
+        const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            D[p] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, a[p][ib >> 1]), B, D[p], 4,
+                                                      8 * (ib & 1) + m, 0);
+    });
+}
+
+// One record: lane n's 256 weights of row n against the NP token pairs.
+// Per group of 4 weights one LDS lookup in the lane's own replica of the
+// grid table (4 unsigned fp16), the signs set with a shift and a masked or,
+// and one v_mfma_f32_4x4x4_16b_f16 whose A operand is broadcast (CBSZ=4)
+// from block ABID of a register pair holding 16 activation slices.
+// kPerImage (one vector): blk[a] += (2s+1) * partial of register image a
+// (sub-blocks 2a, 2a+1); else blk[t] += (2s+1) * partial of token t
+// (blk[2p+1] of a single-token last pair is meaningless). With kPipe the
+// lookups of sub-block ib+1 are issued before the products of sub-block ib
+// (8 more VGPRs pairs; off for 3-4 token pairs, whose rings fill the file).
+template <int NP, bool kPerImage = false, bool kPipe = (NP <= 2)>
 __device__ __forceinline__ void record_dot(const uint8_t* tbl, const Rec<NP>& r, uint32_t lb,
-                                           float (&blk)[2 * NP]) {
+                                           float (&blk)[kPerImage ? 4 : 2 * NP]) {
+    static_assert(!kPerImage || NP == 1, "per-image partials take one vector");
     const uint32_t* dw = reinterpret_cast<const uint32_t*>(&r.u[0]);
+    u32x2_t g[2][8];
+    if constexpr (kPipe) grid_lookups(tbl, lb, dw[0], dw[1], g[0]);
     static_for<0, 8>([&](auto ibc) {
         constexpr int ib = decltype(ibc)::value;
-        const uint32_t q0 = dw[3 * ib], q1 = dw[3 * ib + 1], w = dw[3 * ib + 2];
-        const uint32_t sw = t64_full_signs(w);
-        // The signs of a group's second pair sit 4 bits above those of its
-        // first pair, so {sw >> 4, sw} shifted left by one 64-bit shift puts
-        // both pairs' signs on bits 15 and 31 of the two halves.
-        const uint64_t sw2 = ((uint64_t)(sw >> 4) << 32) | sw;
+        if constexpr (!kPipe) grid_lookups(tbl, lb, dw[3 * ib], dw[3 * ib + 1], g[ib & 1]);
+        else if constexpr (ib < 7) grid_lookups(tbl, lb, dw[3 * (ib + 1)], dw[3 * (ib + 1) + 1], g[(ib + 1) & 1]);
+        const uint32_t w = dw[3 * ib + 2];
         const float sc = (float)((w >> 27) | 1u);  // 2s+1
         float4_t D[NP];
 #pragma unroll
         for (int p = 0; p < NP; ++p) D[p] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        static_for<0, 8>([&](auto mc) {
-            constexpr int m = decltype(mc)::value;
-            const uint32_t q = m < 4 ? q0 : q1;
-            constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
-            const uint32_t addr = __builtin_amdgcn_perm(q, lb, sel);  // (idx << 8) | lb
-            const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
-            constexpr int l = m >> 1, h = m & 1;
-            constexpr int a0 = 4 * (2 * h) + l;  // first pair's sign bits: a0, a0 + 16
-            // one v_lshlrev_b64 (the compiler would split a C shift into two)
-            uint64_t rs;
-            asm("v_lshlrev_b64 %0, %1, %2" : "=v"(rs) : "n"(15 - a0), "v"(sw2));
-            const uint32_t bx = ((uint32_t)rs & 0x80008000u) | g.x;
-            const uint32_t by = ((uint32_t)(rs >> 32) & 0x80008000u) | g.y;
-            const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
+        subblock_dot<NP, ib>(w, g[ib & 1], r.a, D);
+        if constexpr (kPerImage) {
+            blk[ib >> 1] = fmaf(sc, D[0][0] + D[0][1], blk[ib >> 1]);
+        } else {
 #pragma unroll
-            for (int p = 0; p < NP; ++p)
-                D[p] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, r.a[p][ib >> 1]), B, D[p],
-                                                          4, 8 * (ib & 1) + m, 0);
-        });
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            blk[2 * p] = fmaf(sc, D[p][0] + D[p][1], blk[2 * p]);
-            blk[2 * p + 1] = fmaf(sc, D[p][2] + D[p][3], blk[2 * p + 1]);
+            for (int p = 0; p < NP; ++p) {
+                blk[2 * p] = fmaf(sc, D[p][0] + D[p][1], blk[2 * p]);
+                blk[2 * p + 1] = fmaf(sc, D[p][2] + D[p][3], blk[2 * p + 1]);
+            }
         }
-    });
-}
-
-// One vector whose activation has one scale per 64 elements (register
-// image a = sub-blocks 2a, 2a+1): blk[a] += (2s+1) * partial over the
-// image's two sub-blocks.
-__device__ __forceinline__ void record_dot_img(const uint8_t* tbl, const Rec<1>& r, uint32_t lb, float (&blk)[4]) {
-    const uint32_t* dw = reinterpret_cast<const uint32_t*>(&r.u[0]);
-    static_for<0, 8>([&](auto ibc) {
-        constexpr int ib = decltype(ibc)::value;
-        const uint32_t q0 = dw[3 * ib], q1 = dw[3 * ib + 1], w = dw[3 * ib + 2];
-        const uint32_t sw = t64_full_signs(w);
-        const uint64_t sw2 = ((uint64_t)(sw >> 4) << 32) | sw;
-        const float sc = (float)((w >> 27) | 1u);  // 2s+1
-        float4_t D = {0.0f, 0.0f, 0.0f, 0.0f};
-        static_for<0, 8>([&](auto mc) {
-            constexpr int m = decltype(mc)::value;
-            const uint32_t q = m < 4 ? q0 : q1;
-            constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
-            const uint32_t addr = __builtin_amdgcn_perm(q, lb, sel);
-            const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
-            constexpr int a0 = 8 * (m & 1) + (m >> 1);
-            uint64_t rs;
-            asm("v_lshlrev_b64 %0, %1, %2" : "=v"(rs) : "n"(15 - a0), "v"(sw2));
-            const uint32_t bx = ((uint32_t)rs & 0x80008000u) | g.x;
-            const uint32_t by = ((uint32_t)(rs >> 32) & 0x80008000u) | g.y;
-            const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
-            D = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, r.a[0][ib >> 1]), B, D, 4,
-                                                    8 * (ib & 1) + m, 0);
-        });
-        blk[ib >> 1] = fmaf(sc, D[0] + D[1], blk[ib >> 1]);
     });
 }
 

@@ -70,6 +70,11 @@ hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int
                                  hipStream_t s);
 hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
                              const uint8_t* act64, float* y, uint8_t* ws, int num_cus, hipStream_t s);
+// Both (the act64 buffer, then each launch's tickets and partials in one
+// workspace of dense_mlp_ws_bytes, zero-filled once per shape).
+size_t dense_mlp_ws_bytes(int hidden, int inter);
+hipError_t launch_dense_mlp(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int hidden, int inter,
+                            const float* x, float lim, float* y, uint8_t* ws, int num_cus, hipStream_t s);
 // Same product (one vector) straight from GGUF rows (VALU decode, no repacking).
 hipError_t launch_matvec_raw(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
                              const float* x, float* y, hipStream_t s);

@@ -178,16 +178,15 @@ int gpeed_iq3xxs_gemv2_x(const void* w_a, const void* w_b, uint64_t n_rows, uint
 int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                              const float* g, const float* u, float limit, float* dst, void* ws, size_t ws_bytes,
                              gpeed_stream_t stream);
-/* Model::dense_mlp (model.cpp:677-690) on the device, in two launches and
- * without the intermediate vectors: y = W_down (silu(min(g,limit)) *
- * clamp(u,-limit,limit)) with g = W_gate x, u = W_up x. The first launch
- * runs gate and up together; the workgroup that completes 64 rows of g and
- * u writes their SwiGLU straight into the down projection's prepared
- * activation (one power-of-two scale per 64 values), which the second
- * launch multiplies. gate/up are T64 copies of inter x hidden, down of
- * hidden x inter (rows from 0); hidden and inter multiples of 256. ws:
+/* Model::dense_mlp (model.cpp:677-690) on the device without the
+ * intermediate vectors: y = W_down (silu(min(g,limit)) * clamp(u,-limit,limit))
+ * with g = W_gate x, u = W_up x. gate and up run together; the workgroup
+ * that completes 64 rows of g and u writes their SwiGLU straight into the
+ * down projection's prepared activation (one power-of-two scale per 64
+ * values); the second launch multiplies it. gate/up are T64 copies of inter x hidden, down
+ * of hidden x inter (rows from 0); hidden and inter multiples of 256. ws:
  * gpeed_iq3xxs_dense_mlp_ws_bytes bytes, zero-filled once per shape (every
- * call leaves its tickets at zero); one workspace per stream. */
+ * call leaves it ready for the next); one workspace per stream. */
 size_t gpeed_iq3xxs_dense_mlp_ws_bytes(int64_t hidden, int64_t inter);
 int gpeed_iq3xxs_dense_mlp(const void* w_gate, const void* w_up, const void* w_down, int hidden, int inter,
                            const float* x, float limit, float* y, void* ws, size_t ws_bytes, gpeed_stream_t stream);

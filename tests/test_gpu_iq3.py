@@ -327,10 +327,10 @@ def test_dense_mlp_fused_launches(gpu):
 
 
 @pytest.mark.parametrize("H,I", [(6144, 12288), (1024, 2048), (256, 768), (512, 256), (2304, 5376)])
-def test_dense_mlp_two_launches(gpu, H, I):
+def test_dense_mlp(gpu, H, I):
     """dense_mlp (model.cpp:677-690) through gpeed_iq3xxs_dense_mlp: gate and
-    up in one launch whose last workgroup per 64 rows writes the SwiGLU as
-    the down projection's activation; down in the second launch. Repeated
+    up in one launch, the workgroup completing 64 rows writing their SwiGLU
+    as the down projection's activation; down in a second launch. Repeated
     calls on one workspace give identical results."""
     wg = synth.iq3xxs_matrix(66, 0, I, H)
     wu = synth.iq3xxs_matrix(66, 1, I, H)
@@ -347,6 +347,10 @@ def test_dense_mlp_two_launches(gpu, H, I):
     for _ in range(3):
         y2 = host(G.dense_mlp(tg, tu, td, H, I, xd, 10.0, ws=ws))
         assert np.array_equal(y, y2)
+    # a second input on the same workspace (the completion counters move on)
+    x2 = synth.normal(66, 10, H)
+    y3 = host(G.dense_mlp(tg, tu, td, H, I, dev(x2, gpu), 10.0, ws=ws))
+    assert rel_err(y3, oracle.dense_mlp(wg, wu, wd, H, I, x2[None, :], 10.0)[0]) < 1e-4
 
 
 def test_dense_mlp_errors(gpu):
