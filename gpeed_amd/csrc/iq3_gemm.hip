@@ -33,23 +33,12 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v_t __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 128;
 constexpr int kGemmThreads = 256;
-constexpr int kRowPad = 8;  // halves of padding per LDS row
-constexpr int kTblReplicas = 8;
 
-// K step: half an IQ3 block with one X image, a quarter with two.
-template <int V>
-struct GemmCfg {
-    static constexpr int BK = 128 / V;
-    static constexpr int kLdsRow = BK + kRowPad;
-    static constexpr int kTileHalves = BM * kLdsRow;
-    static constexpr int kStepsPerBlock = kQK / BK;
-    static constexpr int kSubPerStep = BK / 32;
-    static constexpr int kItems = BN * kSubPerStep / kGemmThreads;  // (row, sub-block) per thread
-    static constexpr int kXChunks = BK / 2 / 8;                      // 16-byte X loads per thread per image
-};
-constexpr int kTblBytes = 256 * kTblReplicas * 8;  // 16 KiB
+__device__ __forceinline__ uint32_t f16_pair_of_floats(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
 
 // ---------------------------------------------------------------------------
 // X -> fp16 images with a power-of-two scale per token row. One workgroup per
@@ -103,201 +92,6 @@ struct GemmArgs {
     int tiles_m, tiles_n;
 };
 
-__device__ __forceinline__ uint32_t ld_dword(const uint8_t* rec, int lane, int idx) {
-    // dword idx (0..23) of lane `lane` in a T64 record
-    return *reinterpret_cast<const uint32_t*>(rec + (idx >> 2) * kUnitBytes + lane * 16 + (idx & 3) * 4);
-}
-
-// One (row, sub-block) of W: 32 fp16 of +-grid*(2s+1), in k order.
-__device__ __forceinline__ void decode_sub(const uint8_t* tbl, uint32_t rb, uint32_t q0, uint32_t q1, uint32_t w,
-                                           u32x4_t (&out)[4]) {
-    const uint32_t sw = t64_full_signs(w);
-    const _Float16 s2 = (_Float16)(float)((w >> 27) | 1u);
-    const half2v_t s22 = {s2, s2};
-    static_for<0, 8>([&](auto mc) {
-        constexpr int m = decltype(mc)::value;
-        const uint32_t q = m < 4 ? q0 : q1;
-        constexpr uint32_t sel = 0x0C0C0000u | ((4u + (m & 3)) << 8);
-        // entry idx, replica r at (idx << 6) | (r << 3)
-        const uint32_t addr = (__builtin_amdgcn_perm(q, 0u, sel) >> 2) | rb;
-        const u32x2_t g = *reinterpret_cast<const u32x2_t*>(tbl + addr);
-        constexpr int l = m >> 1, h = m & 1;
-        constexpr int a0 = 4 * (2 * h) + l, a1 = 4 * (2 * h + 1) + l;
-        const uint32_t bx = (__builtin_amdgcn_alignbit(sw, sw, (a0 + 17) & 31) & 0x80008000u) | g.x;
-        const uint32_t by = (__builtin_amdgcn_alignbit(sw, sw, (a1 + 17) & 31) & 0x80008000u) | g.y;
-        const half2v_t vx = __builtin_bit_cast(half2v_t, bx) * s22;
-        const half2v_t vy = __builtin_bit_cast(half2v_t, by) * s22;
-        out[m >> 1][(m & 1) * 2] = __builtin_bit_cast(uint32_t, vx);
-        out[m >> 1][(m & 1) * 2 + 1] = __builtin_bit_cast(uint32_t, vy);
-    });
-}
-
-template <int V>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm_iq3(GemmArgs g) {
-    using Cfg = GemmCfg<V>;
-    constexpr int BK = Cfg::BK, kLdsRow = Cfg::kLdsRow, SPB = Cfg::kStepsPerBlock;
-    __shared__ __attribute__((aligned(16))) uint8_t tbl[kTblBytes];
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][V][Cfg::kTileHalves];
-    __shared__ __attribute__((aligned(16))) _Float16 ws[2][Cfg::kTileHalves];
-    __shared__ float d4s[BN];
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-    const int wm = wave & 1, wn = wave >> 1;
-
-    // XCD-aware order: consecutive workgroup ids go to different XCDs, so
-    // with xcd = id % 8 each XCD takes its own band of row tiles (when the
-    // row tiles split evenly into 8 bands) and every token tile of it.
-    const int id = blockIdx.x;
-    int tn, tm;
-    if (g.tiles_n % 8 == 0) {
-        const int per_band = g.tiles_n / 8;
-        const int xcd = id & 7, local = id >> 3;
-        tn = xcd * per_band + local % per_band;
-        tm = local / per_band;
-    } else {
-        tn = id % g.tiles_n;
-        tm = id / g.tiles_n;
-    }
-    if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
-    const int m0 = tm * BM, n0 = tn * BN;
-
-    // grid table: 256 entries x 8 replicas of 4 unsigned fp16
-    for (int it = tid; it < 256 * kTblReplicas; it += kGemmThreads) {
-        const int idx = it / kTblReplicas;
-        const uint32_t v = kIq3xxsGrid[idx];
-        *reinterpret_cast<u32x2_t*>(tbl + it * 8) =
-            u32x2_t{f16_pair_of_bytes(v & 255u, (v >> 8) & 255u), f16_pair_of_bytes((v >> 16) & 255u, v >> 24)};
-    }
-
-    // Loader roles. X: thread -> (row tid/2, BK/2 halves at (tid&1)*BK/2) per
-    // image. W: Cfg::kItems (row, sub-block) items per thread: row = tid & 127,
-    // sub-blocks j = (tid >> 7) + 2t of the step.
-    const int xr = tid >> 1, xc = (tid & 1) * (BK / 2);
-    const int xrow = min(m0 + xr, g.M - 1);
-    const int wr = tid & 127, wj0 = tid >> 7;
-    const int wrow = min(n0 + wr, g.N - 1);  // rows past N: a clamped, unused row
-    const int wtile = wrow >> 6, wlane = wrow & 63;
-    const uint32_t rb = (uint32_t)(lane & (kTblReplicas - 1)) << 3;
-
-    u32x4_t xreg[V][Cfg::kXChunks];
-    uint32_t wq[Cfg::kItems][3];
-    uint32_t wd = 0;
-    auto load_step = [&](int s) {
-        const int k0 = s * BK;
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-            const _Float16* src = g.xh + (size_t)v * g.M * g.K + (size_t)xrow * g.K + k0 + xc;
-#pragma unroll
-            for (int i = 0; i < Cfg::kXChunks; ++i) xreg[v][i] = *reinterpret_cast<const u32x4_t*>(src + i * 8);
-        }
-        const int b = s / SPB, part = s % SPB;
-        const uint8_t* rec = g.w + ((size_t)wtile * g.nb + b) * kRecordBytes;
-#pragma unroll
-        for (int t = 0; t < Cfg::kItems; ++t) {
-            const int ib = part * Cfg::kSubPerStep + wj0 + 2 * t;
-#pragma unroll
-            for (int c = 0; c < 3; ++c) wq[t][c] = ld_dword(rec, wlane, 3 * ib + c);
-        }
-        wd = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + wlane * 2);
-    };
-    auto store_step = [&](int buf) {
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-            _Float16* dst = &xs[buf][v][xr * kLdsRow + xc];
-#pragma unroll
-            for (int i = 0; i < Cfg::kXChunks; ++i) *reinterpret_cast<u32x4_t*>(dst + i * 8) = xreg[v][i];
-        }
-#pragma unroll
-        for (int t = 0; t < Cfg::kItems; ++t) {
-            u32x4_t o[4];
-            decode_sub(tbl, rb, wq[t][0], wq[t][1], wq[t][2], o);
-            _Float16* dst = &ws[buf][wr * kLdsRow + (wj0 + 2 * t) * 32];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(dst + i * 8) = o[i];
-        }
-    };
-
-    float4_t acc[4][4], blk[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            blk[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-
-    const int steps = g.K / BK;
-    load_step(0);
-    __syncthreads();  // grid table ready
-    store_step(0);
-    if (tid < BN) d4s[tid] = (float)__builtin_bit_cast(_Float16, (uint16_t)wd) * 0.25f;
-    __syncthreads();
-
-    const int lr = lane & 15, lg = lane >> 4;
-    for (int s = 0; s < steps; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < steps) load_step(s + 1);
-        // MFMAs of step s
-#pragma unroll
-        for (int kk = 0; kk < BK / 32; ++kk) {
-            half8_t a[V][4], b[4];
-#pragma unroll
-            for (int v = 0; v < V; ++v)
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
-                    a[v][mt] = *reinterpret_cast<const half8_t*>(
-                        &xs[buf][v][(wm * 64 + mt * 16 + lr) * kLdsRow + kk * 32 + lg * 8]);
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt)
-                b[nt] = *reinterpret_cast<const half8_t*>(&ws[buf][(wn * 64 + nt * 16 + lr) * kLdsRow + kk * 32 + lg * 8]);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-                    for (int v = 0; v < V; ++v)
-                        blk[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[v][mt], b[nt], blk[mt][nt], 0, 0, 0);
-        }
-        if (s % SPB == SPB - 1) {
-            // block finished: acc += d/4 * partial (column n = W row)
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const float d4 = d4s[wn * 64 + nt * 16 + lr];
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[mt][nt][i] = fmaf(d4, blk[mt][nt][i], acc[mt][nt][i]);
-                    blk[mt][nt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                }
-            }
-        }
-        __syncthreads();  // all reads of the other buffer and of d4s are done
-        if (s + 1 < steps) {
-            store_step(buf ^ 1);
-            if ((s + 1) % SPB == 0 && tid < BN)
-                d4s[tid] = (float)__builtin_bit_cast(_Float16, (uint16_t)wd) * 0.25f;
-        }
-        __syncthreads();
-    }
-
-    // epilogue: D row = token (4 per lane), column = W row
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + wm * 64 + mt * 16 + lg * 4 + i;
-            if (m >= g.M) continue;
-            const float us = g.unscale[m];
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const int n = n0 + wn * 64 + nt * 16 + lr;
-                if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][nt][i] * us;
-            }
-        }
-}
-
 // ---------------------------------------------------------------------------
 // GEMM, register-decode form. A 256-thread workgroup computes 128 tokens x
 // 192 rows; wavefront w owns rows [48w, 48w+48) as 3 column tiles of
@@ -305,10 +99,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_iq3(GemmArgs g) {
 // twice. A lane's B operand is 8 consecutive weights of one row (group g =
 // lane/16 of a 32-weight sub-block); it is decoded straight into registers
 // from two dwords of the T64 record (grid-index word, sign/scale word): two
-// lookups in an LDS table of grid * (2s+1) (exact fp16, scale folded in by
-// the index), the group's eighth sign from a popcount, four rotate-and-mask
-// sign insertions. X images are staged through LDS 64 columns at a time
-// (double buffered); W dwords are prefetched two stages ahead.
+// lookups in the replicated unsigned grid table, the group's eighth sign
+// from a popcount, four rotate-and-mask sign insertions and an exact fp16
+// multiply by 2s+1. X images are staged through LDS 64 columns at a time
+// (double buffered); W dwords are prefetched two stages ahead. Used for fp32
+// X (two images); bf16 X takes k_gemm3.
 
 constexpr int BM2 = 128, BN2 = 192, BK2 = 64;
 constexpr int kRow2 = BK2 + 8;                  // LDS row stride in halves
@@ -514,6 +309,291 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
         }
 }
 
+
+// ---------------------------------------------------------------------------
+// GEMM, pipelined form (one X image: bf16 input). Same tile and wavefront
+// split as k_gemm2 (128 tokens x 192 rows, wavefront w owns rows 48w..48w+47
+// and all 128 tokens), reorganised so that the matrix cores are fed every
+// cycle the wavefront can give them:
+//   * W arrives as whole record units: per 256-wide block the workgroup
+//     copies the three row tiles' six 1 KiB units and their d values into
+//     LDS (coalesced 16-byte loads, one block ahead), and the decode reads
+//     its two words per (row, sub-block) from there;
+//   * the B operands of stage s+1 (64 columns) are decoded while the MFMAs
+//     of stage s run, from a grid table that already holds grid * (2s+1)
+//     (entry (idx, s) at (idx << 8) | (s << 4), two replicas), so a group of
+//     8 weights costs two lookups, a popcount for its eighth sign and two
+//     64-bit shifts that put four pairs of signs on the fp16 sign bits;
+//   * A operands are read one half-stage ahead from a ring of three X
+//     stages, loaded two stages ahead into registers;
+//   * one workgroup barrier per stage.
+// Products stay exact (|q (2s+1)| <= 1922 in fp16, X an exact fp16 image);
+// the block's d/4 scales its fp32 partial once per 256 columns. (Folding d
+// into B would round every weight to fp16: about 3e-4 rms relative error
+// per product, which exceeds 1e-3 of max(|y_i|, rms(y)) on outputs near
+// the rms.)
+
+constexpr int BM3 = 128, BN3 = 192, BK3 = 64;
+constexpr int kRow3 = BK3 + 8;                       // X LDS row stride (halves)
+constexpr int kWBlk3 = 3 * 6 * kUnitBytes;           // one block: 3 row tiles x 6 units
+constexpr int kWItems3 = 5;                          // W copy items per lane-slot per block
+
+struct GemmSmem3 {
+    uint8_t tbl[kGridTableBytes];                    // grid * (2s+1), see above
+    _Float16 xs[3][BM3 * kRow3];                     // X stages (ring of 3)
+    uint8_t wb[2][kWBlk3];                           // W blocks: [tile][unit][64 lanes x 16 B]
+    uint8_t wd[2][512];                              // their d: [tile][64 fp16] (+ padding)
+};
+
+// Entry (idx, s) of the scaled grid, both replicas: thread (s = tid & 15)
+// fills 16 entries idx = (tid >> 4) + 16 i; 16 lanes write 256 contiguous
+// bytes per store.
+__device__ __forceinline__ void scaled_grid_table(uint8_t* tbl, int tid) {
+    const uint32_t s = tid & 15;
+    const float m = (float)(2 * s + 1);
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t idx = (tid >> 4) + 16 * i;
+        const uint32_t v = kIq3xxsGrid[idx];
+        const uint32_t lo = f16_pair_of_floats((float)(v & 255u) * m, (float)((v >> 8) & 255u) * m);
+        const uint32_t hi = f16_pair_of_floats((float)((v >> 16) & 255u) * m, (float)(v >> 24) * m);
+        *reinterpret_cast<u32x4_t*>(tbl + (idx << 8) + (s << 4)) = u32x4_t{lo, hi, lo, hi};
+    }
+}
+
+// B operand of v_mfma_f32_16x16x32_f16 for one lane: the 8 weights of group
+// lg (columns 8lg..8lg+7 of a sub-block) of one W row, as fp16
+// +-grid*(2s+1), from the sub-block's grid-index word q (bytes p0, p0+1
+// hold the group's two indices) and sign/scale word w. sel0/sel1 pick those
+// bytes; rs = replica offset (0 or 8).
+__device__ __forceinline__ half8_t decode_group(const uint8_t* tbl, uint32_t q, uint32_t w, uint32_t lg,
+                                                uint32_t sel0, uint32_t sel1, uint32_t rs) {
+    // group lg's signs: pair c at bits 4c and 4c+16 (c = 0..3); bit 28 then
+    // holds a scale bit instead of the eighth sign
+    uint32_t wg = __builtin_amdgcn_alignbit(w, w, lg);
+    // the eighth sign is the parity of the other seven: adding
+    // popcount(bits 0,4,..,28) << 28 turns bit 28 into exactly that parity
+    // (the carry only reaches bits 29-31, which no pair of this group uses)
+    wg += (uint32_t)__builtin_popcount(wg & 0x11111111u) << 28;
+    // pairs 0/1 and 2/3: one 64-bit shift of {wg >> 4, wg} each puts a
+    // pair's two signs on bits 15 and 31 of both halves
+    const uint64_t sw2 = ((uint64_t)(wg >> 4) << 32) | wg;
+    uint64_t r01, r23;
+    asm("v_lshlrev_b64 %0, 15, %1" : "=v"(r01) : "v"(sw2));
+    asm("v_lshlrev_b64 %0, 7, %1" : "=v"(r23) : "v"(sw2));
+    const uint32_t sr = ((w >> 24) & 0xF0u) | rs;  // (s << 4) | replica
+    const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, sr, sel0));
+    const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, sr, sel1));
+    const u32x4_t r = {((uint32_t)r01 & 0x80008000u) | g0.x, ((uint32_t)(r01 >> 32) & 0x80008000u) | g0.y,
+                       ((uint32_t)r23 & 0x80008000u) | g1.x, ((uint32_t)(r23 >> 32) & 0x80008000u) | g1.y};
+    return __builtin_bit_cast(half8_t, r);
+}
+
+__global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) GemmSmem3 sm;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t lane = tid & 63;
+    const int lr = lane & 15;
+    const uint32_t lg = lane >> 4;
+
+    const int id = blockIdx.x;
+    int tn, tm;
+    if (g.tiles_n % 8 == 0) {
+        const int per_band = g.tiles_n / 8;
+        const int xcd = id & 7, local = id >> 3;
+        tn = xcd * per_band + local % per_band;
+        tm = local / per_band;
+    } else {
+        tn = id % g.tiles_n;
+        tm = id / g.tiles_n;
+    }
+    if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
+    const int m0 = tm * BM3, n0 = tn * BN3;
+
+    const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
+    scaled_grid_table(sm.tbl, tid);
+
+    // W copy items of this lane-slot (wave * 5 + i): 0..17 = (row tile
+    // item / 6, unit item % 6), 18 and 19 = the three tiles' d (lanes
+    // 0..23, 16 bytes each; 19 repeats 18). Row tiles past the tensor are
+    // clamped to its last tile (their rows are computed, never stored).
+    uint32_t w_goff[kWItems3], w_loff[kWItems3];
+#pragma unroll
+    for (int i = 0; i < kWItems3; ++i) {
+        const int item = wave * kWItems3 + i;
+        if (item < 18) {
+            const int jt = item / 6, u = item % 6;
+            const int tile = min(n0 / kTileRows + jt, last_tile);
+            w_goff[i] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + u * kUnitBytes + lane * 16u;
+            w_loff[i] = (uint32_t)(jt * 6 + u) * kUnitBytes + lane * 16u;
+        } else {
+            const uint32_t l = min(lane, 23u);
+            const int jt = l >> 3;
+            const int tile = min(n0 / kTileRows + jt, last_tile);
+            w_goff[i] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + kRecordDOffset + (l & 7) * 16u;
+            w_loff[i] = kWBlk3 + (uint32_t)jt * 128u + (l & 7) * 16u;  // past wb: into wd
+        }
+    }
+    u32x4_t wreg[kWItems3];
+    auto load_w = [&](int b) {
+        const uint32_t boff = (uint32_t)b * kRecordBytes;
+#pragma unroll
+        for (int i = 0; i < kWItems3; ++i) wreg[i] = *reinterpret_cast<const u32x4_t*>(g.w + (w_goff[i] + boff));
+    };
+    auto store_w = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < kWItems3; ++i) {
+            const uint32_t lo = w_loff[i];
+            uint8_t* dst = lo < (uint32_t)kWBlk3 ? &sm.wb[slot][lo] : &sm.wd[slot][lo - kWBlk3];
+            *reinterpret_cast<u32x4_t*>(dst) = wreg[i];
+        }
+    };
+
+    // This lane's rows (j = 0..2): row tile and lane slot inside the block copy.
+    uint32_t w_rowoff[3], d_off[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int r = wave * 48 + j * 16 + lr;  // 0..191
+        w_rowoff[j] = (uint32_t)(r >> 6) * 6 * kUnitBytes + (uint32_t)(r & 63) * 16u;
+        d_off[j] = (uint32_t)(r >> 6) * 128u + (uint32_t)(r & 63) * 2u;
+    }
+    const uint32_t p0 = 2 * (lg & 1);
+    const uint32_t sel0 = 0x0C0C0000u | ((4u + p0) << 8);
+    const uint32_t sel1 = 0x0C0C0000u | ((5u + p0) << 8);
+    // lanes of one row that share an index word read different replicas
+    const uint32_t rs = (lg & 1u) << 3;
+    const bool hiq = lg >= 2;  // the group's indices sit in the sub-block's second index word
+
+    // B operands of sub-block t of stage s: [j]
+    auto decode_half = [&](half8_t (&bop)[3], int s, int t) {
+        const uint8_t* wb = sm.wb[(s >> 2) & 1];
+        const int ib = 2 * (s & 3) + t;
+        const int dq = 3 * ib + (hiq ? 1 : 0), dw = 3 * ib + 2;
+        const uint32_t oq = (uint32_t)(dq >> 2) * kUnitBytes + (dq & 3) * 4;
+        const uint32_t ow = (uint32_t)(dw >> 2) * kUnitBytes + (dw & 3) * 4;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const uint32_t q = *reinterpret_cast<const uint32_t*>(wb + w_rowoff[j] + oq);
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(wb + w_rowoff[j] + ow);
+            bop[j] = decode_group(sm.tbl, q, w, lg, sel0, sel1, rs);
+        }
+    };
+
+    // X staging: piece tid + 256 i = row (tid >> 3) + 32 i, columns (tid & 7) * 8 .. +7
+    const int xr = tid >> 3, xc = (tid & 7) * 8;
+    const _Float16* xsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xsrc[i] = g.xh + (size_t)min(m0 + xr + 32 * i, g.M - 1) * g.K + xc;
+    u32x4_t xreg[2][4];
+    auto load_x = [&](u32x4_t (&r)[4], int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + s * BK3);
+    };
+    auto store_x = [&](const u32x4_t (&r)[4], int xb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(&sm.xs[xb][(xr + 32 * i) * kRow3 + xc]) = r[i];
+    };
+    // A operands of sub-block t of the stage in X buffer xb: [mt]
+    auto read_a = [&](half8_t (&a)[8], int xb, int t) {
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+            a[mt] = *reinterpret_cast<const half8_t*>(&sm.xs[xb][(mt * 16 + lr) * kRow3 + t * 32 + lg * 8]);
+    };
+
+    float4_t acc[8][3], blk[8][3];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const float4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int steps = g.K / BK3;  // a multiple of 4
+    const int nblk = g.nb;
+    // Prologue: X stages 0, 1 in LDS (buffers 0, 1), stage 2 in registers,
+    // W block 0 in LDS; then the A operands of stage 0's first sub-block and
+    // the B operands of stage 0.
+    load_w(0);
+    load_x(xreg[0], 0);
+    load_x(xreg[1], min(1, steps - 1));
+    store_w(0);
+    store_x(xreg[0], 0);
+    store_x(xreg[1], 1);
+    load_x(xreg[0], min(2, steps - 1));
+    __syncthreads();  // table, W block 0, X stages 0 and 1
+    half8_t a[2][8];
+    half8_t bop[2][2][3];  // [stage parity][t][j]
+    read_a(a[0], 0, 0);
+    decode_half(bop[0][0], 0, 0);
+    decode_half(bop[0][1], 0, 1);
+
+    // X buffer of stage s: s % 3. Stage s stores X(s + 2) into (s + 2) % 3,
+    // the buffer of stage s - 1, whose last reads (its second sub-block)
+    // happened before the previous stage's barrier.
+    int xb0 = 0;
+    for (int s0 = 0; s0 < steps; s0 += 4) {
+        static_for<0, 4>([&](auto Uc) {
+            constexpr int U = decltype(Uc)::value;
+            const int s = s0 + U;
+            const int c = s >> 2;  // block
+            const int xb1 = xb0 == 2 ? 0 : xb0 + 1, xb2 = xb1 == 2 ? 0 : xb1 + 1;
+            load_x(xreg[(U + 1) & 1], min(s + 3, steps - 1));
+            if constexpr (U == 0) load_w(min(c + 1, nblk - 1));
+            // sub-block 0: MFMAs on a[0]; meanwhile A of sub-block 1 and the
+            // next stage's B operands of its sub-block 0
+            read_a(a[1], xb0, 1);
+            decode_half(bop[(U + 1) & 1][0], s + 1, 0);
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+                for (int j = 0; j < 3; ++j)
+                    blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][mt], bop[U & 1][0][j],
+                                                                         U == 0 ? zero4 : blk[mt][j], 0, 0, 0);
+            // sub-block 1: MFMAs on a[1]; meanwhile A of the next stage's
+            // sub-block 0 and its B operands of sub-block 1
+            read_a(a[0], xb1, 0);
+            decode_half(bop[(U + 1) & 1][1], s + 1, 1);
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+                for (int j = 0; j < 3; ++j)
+                    blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][mt], bop[U & 1][1][j], blk[mt][j], 0,
+                                                                         0, 0);
+            if constexpr (U == 3) {
+                // block complete: acc += d/4 * partial (column = this lane's row)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const uint16_t dh = *reinterpret_cast<const uint16_t*>(&sm.wd[c & 1][d_off[j]]);
+                    const float d4 = (float)__builtin_bit_cast(_Float16, dh) * 0.25f;
+#pragma unroll
+                    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(d4, blk[mt][j][i], acc[mt][j][i]);
+                }
+            }
+            store_x(xreg[U & 1], xb2);  // X(s + 2), loaded a stage ago
+            if constexpr (U == 2) store_w((c + 1) & 1);
+            __syncthreads();
+            xb0 = xb1;
+        });
+    }
+
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = m0 + mt * 16 + (int)lg * 4 + i;
+            if (m >= g.M) continue;
+            const float us = g.unscale[m];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int n = n0 + wave * 48 + j * 16 + lr;
+                if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][j][i] * us;
+            }
+        }
+}
+
 }  // namespace
 
 size_t gemm_ws_bytes(int M, int K, int x_bf16) {
@@ -546,7 +626,11 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
     a.tiles_m = (M + BM2 - 1) / BM2;
     a.tiles_n = (out_dim + BN2 - 1) / BN2;
     const int grid = a.tiles_n * a.tiles_m;
-    if (x_bf16) return launch_timed(kProfGemm, k_gemm2<1>, dim3(grid), dim3(kGemmThreads), 0, s, a);
+    if (x_bf16) {
+        a.tiles_m = (M + BM3 - 1) / BM3;
+        a.tiles_n = (out_dim + BN3 - 1) / BN3;
+        return launch_timed(kProfGemm, k_gemm3, dim3(a.tiles_n * a.tiles_m), dim3(kGemmThreads), 0, s, a);
+    }
     return launch_timed(kProfGemm, k_gemm2<2>, dim3(grid), dim3(kGemmThreads), 0, s, a);
 }
 
