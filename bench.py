@@ -47,6 +47,22 @@ METRIC = "IQ3_XXS GEMV weight GB/s (% of HBM peak) at batch 1; prefill GEMM TFLO
 HBM_PEAK_GBS = 8000.0
 H, I = 6144, 12288
 SWIGLU_LIMIT = 10.0
+# HBM traffic of the GEMV pair, measured with rocprofv3 --pmc (FETCH_SIZE and
+# WRITE_SIZE per dispatch, each scaled by what the counter reads for an
+# elementwise copy of known size); see the summary file for the commands.
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "k_gemv_t64_dense_decode_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per gate+up + down pair from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_pair:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -174,8 +190,9 @@ def prefill_gemm(torch, G, synth, dev, reps):
     N, K = 12288, 6144
     w = synth.iq3xxs_matrix(2026, 0, N, K)
     t64 = G.tile(torch.from_numpy(w.reshape(-1)).to(dev), N, K)
-    out = {"workload": "prefill GEMM: IQ3_XXS W 12288x6144 dequantized into LDS (exact fp16 q*(2s+1)), "
-                       "X bf16 [M,6144] ~ N(0,1), Y fp32 [M,12288]",
+    out = {"workload": "prefill GEMM: IQ3_XXS W 12288x6144 (record units staged through LDS, decoded to exact "
+                       "fp16 q*(2s+1) MFMA operands, d/4 per block in fp32), X bf16 [M,6144] ~ N(0,1), "
+                       "Y fp32 [M,12288]",
            "peak_TFLOPs": 2500.0}
     for M in (512, 2048):
         X = torch.from_numpy(synth.normal(2026, M, M * K).reshape(M, K)).to(dev).to(torch.bfloat16)
@@ -210,6 +227,9 @@ def main():
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run 5 elementwise copies of 256 MiB (counter calibration), then 20 dense steps, and "
+                         "exit; meant to run under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the multi-GPU "
@@ -239,6 +259,17 @@ def main():
     def step(c):
         tg, tu, td = copies[c]
         G.dense_mlp(tg, tu, td, H, I, xd, SWIGLU_LIMIT, out=y, ws=ws_mlp)
+
+    if args.traffic_probe:
+        src = torch.ones(64 << 20, device=dev)  # 256 MiB fp32
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.add(src, 0.0, out=dst)  # reads 256 MiB, writes 256 MiB
+        for i in range(20):
+            step(i % args.copies)
+        torch.cuda.synchronize()
+        log("traffic probe done")
+        return
 
     log("warmup")
     for i in range(args.warmup):
@@ -338,7 +369,9 @@ def main():
                    "arithmetic": "iq3_xxs weights decoded to exact fp16, fp32 activations as fp16 hi+lo, "
                                  "f16 MFMA with fp32 accumulation"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_per": "gate+up + down launch pair, bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                    "copy-calibrated)",
                      "kernel": "k_gemv_t64", "avg_launch_us": round(pair_ms * 1e3 / 2, 3),
                      "pair_us": round(pair_ms * 1e3, 3), "timing": pair_timing,
                      "pair_algorithmic_bytes": pair_bytes, "launch_kinds": kinds},

@@ -569,7 +569,7 @@ int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_
     if (n_tok > (1 << 20)) return fail(GPEED_ERR_INVALID, "gemm: n_tok too large");
     if (row0 % gpeed::kTileRows)
         return fail(GPEED_ERR_LAYOUT, "gemm: row0 must be a multiple of 64 on the T64 layout");
-    if (!aligned(w_t64, 16) || !aligned(X, 4)) return fail(GPEED_ERR_INVALID, "gemm: misaligned operand");
+    if (!aligned(w_t64, 16) || !aligned(X, 16)) return fail(GPEED_ERR_INVALID, "gemm: misaligned operand");
     if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::gemm_ws_bytes(n_tok, in_dim, x_dtype == GPEED_X_BF16))
         return fail(GPEED_ERR_WORKSPACE, "gemm: workspace missing, misaligned or too small");
     hipError_t e = gpeed::launch_gemm(static_cast<const uint8_t*>(w_t64), row0, in_dim, out_dim, X,

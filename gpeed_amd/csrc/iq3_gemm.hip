@@ -1,24 +1,22 @@
 // IQ3_XXS prefill GEMM (gfx950): Y[m][n] = sum_k X[m][k] * W[row0+n][k]
 // for many tokens (matmul_quant, weights.cpp:86-165, at prefill sizes).
 //
-// Operands. W tiles are dequantized into LDS as fp16 holding
-// +-grid * (2s+1): an integer of at most 62 * 31 = 1922, exact in fp16 (bf16
-// would round it), so the only per-weight scale left is the block's d/4,
-// applied once per 256-wide block to the fp32 partial of that block. X is
-// converted once (k_gemm_prep_x) to fp16 with a power-of-two scale per token
-// row (bf16 input: one image, exact for every value within 2^24 of the row
-// maximum; fp32 input: an fp16 hi image and an fp16 lo image, two MFMAs per
-// step). Products are exact; sums are fp32 in the MFMA.
+// Operands. W is decoded to fp16 holding +-grid * (2s+1): an integer of at
+// most 62 * 31 = 1922, exact in fp16 (bf16 would round it), so the only
+// per-weight scale left is the block's d/4, applied once per 256-wide block
+// to the fp32 partial of that block. X is converted once (k_gemm_prep_x) to
+// fp16 with a power-of-two scale per token row (bf16 input: one image, exact
+// for every value within 2^24 of the row maximum; fp32 input: an fp16 hi
+// image and an fp16 lo image, two MFMAs per step). Products are exact; sums
+// are fp32 in v_mfma_f32_16x16x32_f16.
 //
-// Tiling. A 256-thread workgroup computes a 128 (tokens) x 128 (rows) tile;
-// its four wavefronts own 64 x 64 quadrants as 4 x 4 v_mfma_f32_16x16x32_f16
-// accumulator tiles. K advances by half an IQ3 block (128): the X tile is
-// staged to LDS from fp16 global memory, the W tile decoded from T64 records
-// (one thread per (row, sub-block): 8 lookups in a replicated fp16 grid
-// table, rotate-and-mask signs, an exact fp16 multiply by 2s+1), both double
-// buffered so the loads and decode of step s+1 overlap the MFMAs of step s.
-// Workgroups are ordered so that the eight XCDs each work on their own band
-// of W rows (the band stays in that XCD's L2 while all token tiles use it).
+// Tiling. A 256-thread workgroup computes 128 tokens x 192 W rows; wavefront
+// w owns rows 48w..48w+47 (3 column tiles) for all 8 token tiles, so every W
+// value is decoded exactly once per workgroup, straight into the MFMA B
+// operand registers. Workgroups are ordered so that the eight XCDs each
+// work on their own band of W rows (the band stays in that XCD's L2 while
+// all token tiles use it). k_gemm3 (bf16 X) and k_gemm2 (fp32 X) differ in
+// how W and X reach the wavefronts; see each kernel.
 #include <type_traits>
 
 #include "iq3_common.h"
@@ -49,15 +47,30 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
     __shared__ float red[4];
-    auto ld = [&](int k) -> float {
-        if (IN == 1) {
-            const uint16_t b = reinterpret_cast<const uint16_t*>(X)[(size_t)m * K + k];
-            return __uint_as_float((uint32_t)b << 16);
+    // 8 consecutive values per access (16-byte loads; K is a multiple of 256)
+    auto ld8 = [&](int c, float (&v)[8]) {
+        if constexpr (IN == 1) {
+            const u32x4_t u = reinterpret_cast<const u32x4_t*>(X)[((size_t)m * K >> 3) + c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = __uint_as_float(u[i] << 16);
+                v[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+            }
+        } else {
+            const float4* p = reinterpret_cast<const float4*>(X) + ((size_t)m * K >> 2) + 2 * c;
+            const float4 a = p[0], b = p[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
         }
-        return reinterpret_cast<const float*>(X)[(size_t)m * K + k];
     };
+    const int n8 = K >> 3;
     float mx = 0.0f;
-    for (int k = tid; k < K; k += 256) mx = fmaxf(mx, fabsf(ld(k)));
+    for (int c = tid; c < n8; c += 256) {
+        float v[8];
+        ld8(c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
@@ -71,11 +84,19 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
         sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
     }
     const size_t plane = (size_t)M * K;
-    for (int k = tid; k < K; k += 256) {
-        const float v = ldexpf(ld(k), sc);
-        const _Float16 hi = (_Float16)v;
-        xh[(size_t)m * K + k] = hi;
-        if (IN == 0) xh[plane + (size_t)m * K + k] = (_Float16)(v - (float)hi);
+    for (int c = tid; c < n8; c += 256) {
+        float v[8];
+        ld8(c, v);
+        u32x4_t hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = ldexpf(v[2 * i], sc), b = ldexpf(v[2 * i + 1], sc);
+            const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+            hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+            lo[i] = f16_pair_of_floats(a - (float)ha, b - (float)hb);
+        }
+        reinterpret_cast<u32x4_t*>(xh + (size_t)m * K)[c] = hi;
+        if constexpr (IN == 0) reinterpret_cast<u32x4_t*>(xh + plane + (size_t)m * K)[c] = lo;
     }
     if (tid == 0) unscale[m] = ldexpf(1.0f, -sc);
 }

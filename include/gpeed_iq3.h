@@ -132,11 +132,11 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
 
 /* Prefill GEMM: Y[t][j] = sum_i W[row0+j][i] * X[t][i] for t < n_tok, with
  * X [n_tok][in_dim] fp32 (x_dtype GPEED_X_F32) or bf16 (GPEED_X_BF16), Y fp32
- * [n_tok][out_dim]. W tiles are dequantized into LDS (as exact fp16 values
- * of q*(2s+1)) and fed to MFMA; the block scale d/4 is applied to each
- * block's fp32 partial. The prefill-sized case of matmul_quant
- * (weights.cpp:86-165, model_batch.cpp:30-95 / 151-162). ws:
- * gpeed_iq3xxs_gemm_ws_bytes bytes (no zero-fill needed). */
+ * [n_tok][out_dim]. W records are staged through LDS and decoded to exact
+ * fp16 values of q*(2s+1) as MFMA operands; the block scale d/4 is applied
+ * to each block's fp32 partial. The prefill-sized case of matmul_quant
+ * (weights.cpp:86-165, model_batch.cpp:30-95 / 151-162). X 16-byte aligned;
+ * ws: gpeed_iq3xxs_gemm_ws_bytes bytes (no zero-fill needed). */
 size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int x_dtype);
 int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const void* X,
                       int x_dtype, int n_tok, float* Y, void* ws, size_t ws_bytes, gpeed_stream_t stream);
