@@ -522,7 +522,7 @@ int gpeed_moe_route(const float* logits, int n_tok, int n_exp, int top_k, int mo
 }
 
 size_t gpeed_iq3xxs_moe_ws_bytes(int n_tok, int n_exp, int top_k, int hidden, int inter) {
-    if (n_tok < 1 || n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp) return 0;
+    if (n_tok < 1 || n_tok > 8192 || n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp) return 0;
     if (!dims_ok(hidden) || !dims_ok(inter)) return 0;
     return gpeed::moe_ws_bytes(n_tok, n_exp, top_k, hidden, inter);
 }
@@ -537,7 +537,7 @@ int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w
     if (!dims_ok(hidden) || !dims_ok(inter)) return fail(GPEED_ERR_INVALID, "moe_experts: size too large");
     if (n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp)
         return fail(GPEED_ERR_UNIMPLEMENTED, "moe_experts: needs 1 <= top_k <= min(32, n_exp), n_exp <= 1024");
-    if ((int64_t)n_tok * top_k > (1 << 24)) return fail(GPEED_ERR_INVALID, "moe_experts: too many assignments");
+    if (n_tok > 8192) return fail(GPEED_ERR_INVALID, "moe_experts: at most 8192 tokens per call");
     if (!w_gate || !w_up || !w_down || !X || !eptr || !tok || !wt || !Y)
         return fail(GPEED_ERR_INVALID, "moe_experts: null pointer");
     if (!aligned(w_gate, 16) || !aligned(w_up, 16) || !aligned(w_down, 16) || !aligned(X, 16) || !aligned(Y, 16))

@@ -28,6 +28,7 @@ namespace {
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kSegTok = 8;
+constexpr int kPlanMaxTok = 8192;  // tokens per routed batch (plan's per-token counters live in LDS)
 
 // ---------------------------------------------------------------------------
 // Router
@@ -37,6 +38,26 @@ __device__ __forceinline__ bool ranks_before(float ka, int a, float kb, int b) {
     return ka > kb || (ka == kb && a < b);
 }
 
+// Exclusive scan of v[0..n) in LDS into out (n <= 1024, 1024 threads);
+// returns the total. tmp: 1024 ints of scratch.
+__device__ __forceinline__ int block_exclusive_scan(const int* v, int* out, int* tmp, int n) {
+    const int tid = threadIdx.x;
+    tmp[tid] = tid < n ? v[tid] : 0;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int add = tid >= off ? tmp[tid - off] : 0;
+        __syncthreads();
+        tmp[tid] += add;
+        __syncthreads();
+    }
+    const int total = tmp[1023];
+    if (tid < n) out[tid] = tmp[tid] - v[tid];
+    __syncthreads();
+    return total;
+}
+
+// J = register slots per lane: expert e lives in lane e % 64, slot e / 64.
+template <int J>
 __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ logits, int T, int E, int K,
                                                     int mode, const float* __restrict__ bias,
                                                     float routed_scale, int norm_topk, int* __restrict__ eptr,
@@ -52,7 +73,6 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ lo
     __syncthreads();
 
     // 1. top-k per token (one wavefront per token); lane l holds experts l + 64j
-    constexpr int J = kMaxExperts / 64;
     for (int t = wave; t < T; t += 16) {
         float key[J], sc[J];
         unsigned taken = 0;
@@ -124,16 +144,9 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ lo
 
     // 2. exclusive scan of the expert counts (model_batch.cpp:205-209)
     {
-        int run = 0;
-        if (tid == 0) {
-            for (int e = 0; e < E; ++e) {
-                const int c = cnt[e];
-                cursor[e] = run;
-                eptr[e] = run;
-                run += c;
-            }
-            eptr[E] = run;
-        }
+        const int total = block_exclusive_scan(cnt, cursor, chunk_e, E);
+        for (int e = tid; e < E; e += 1024) eptr[e] = cursor[e];
+        if (tid == 0) eptr[E] = total;
     }
     __syncthreads();
 
@@ -177,17 +190,19 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
                                                    int T, int E, int K, MoePlan pl) {
     __shared__ int ep[kMaxExperts + 1];
     __shared__ int sstart[kMaxExperts + 1];
+    __shared__ int nseg[kMaxExperts];
+    __shared__ int tmp[1024];
+    __shared__ int tcnt[kPlanMaxTok];
     const int tid = threadIdx.x;
     for (int e = tid; e <= E; e += 1024) ep[e] = eptr[e];
+    for (int t = tid; t < T; t += 1024) tcnt[t] = 0;
     __syncthreads();
+    for (int e = tid; e < E; e += 1024) nseg[e] = (ep[e + 1] - ep[e] + kSegTok - 1) / kSegTok;
+    __syncthreads();
+    const int n_seg = block_exclusive_scan(nseg, sstart, tmp, E);
     if (tid == 0) {
-        int run = 0;
-        for (int e = 0; e < E; ++e) {
-            sstart[e] = run;
-            run += (ep[e + 1] - ep[e] + kSegTok - 1) / kSegTok;
-        }
-        sstart[E] = run;
-        *pl.n_seg = run;
+        sstart[E] = n_seg;
+        *pl.n_seg = n_seg;
         // the grouped GEMVs take work from these with device-scope atomics
         __hip_atomic_store(pl.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(pl.ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -214,11 +229,32 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
         pl.seg_of[p] = sstart[lo] + r / kSegTok;
         pl.idx_of[p] = r % kSegTok;
     }
-    // each token's slots in bucket order = expert order
+    // each token's slots in bucket order = expert order: every slot appends
+    // itself to its token's list, then each list (at most K entries) is
+    // sorted
+    for (int p = tid; p < N; p += 1024) {
+        const int t = tok[p];
+        if (t >= 0 && t < T) {
+            const int c = atomicAdd(&tcnt[t], 1);
+            if (c < K) pl.pos[(size_t)t * K + c] = p;
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
     for (int t = tid; t < T; t += 1024) {
-        int c = 0;
-        for (int p = 0; p < N && c < K; ++p)
-            if (tok[p] == t) pl.pos[(size_t)t * K + c++] = p;
+        int v[kMaxTopK];
+        const int n = min(tcnt[t], K);
+        for (int c = 0; c < n; ++c) v[c] = pl.pos[(size_t)t * K + c];
+        for (int i = 1; i < n; ++i) {
+            const int x = v[i];
+            int j = i - 1;
+            while (j >= 0 && v[j] > x) {
+                v[j + 1] = v[j];
+                --j;
+            }
+            v[j + 1] = x;
+        }
+        for (int c = 0; c < n; ++c) pl.pos[(size_t)t * K + c] = v[c];
     }
 }
 
@@ -452,8 +488,14 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int K, int mode, 
                             uint8_t* ws, hipStream_t s) {
     int* asg_e = reinterpret_cast<int*>(ws);
     float* asg_w = reinterpret_cast<float*>(ws + align256((size_t)T * K * 4));
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale,
-                       norm_topk, eptr, tok, wt, sel, asg_e, asg_w);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(1), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale, norm_topk,
+                           eptr, tok, wt, sel, asg_e, asg_w);
+    };
+    if (E <= 64) go(k_moe_route<1>);
+    else if (E <= 128) go(k_moe_route<2>);
+    else if (E <= 256) go(k_moe_route<4>);
+    else go(k_moe_route<kMaxExperts / 64>);
     return hipGetLastError();
 }
 

@@ -221,8 +221,8 @@ int gpeed_moe_route(const float* logits, int n_tok, int n_exp, int top_k, int mo
  * swiglu_limit, down = rows e*hidden.. of w_down ([n_exp*hidden, inter],
  * ffn_down_exps); Y[t] = sum over the token's experts, in expert order, of
  * wt * down (Y overwritten; the shared expert is not included). hidden and
- * inter are multiples of 256. eptr/tok/wt as gpeed_moe_route makes them.
- * ws: gpeed_iq3xxs_moe_ws_bytes bytes (no zero-fill needed). */
+ * inter are multiples of 256; n_tok <= 8192. eptr/tok/wt as gpeed_moe_route
+ * makes them. ws: gpeed_iq3xxs_moe_ws_bytes bytes (no zero-fill needed). */
 size_t gpeed_iq3xxs_moe_ws_bytes(int n_tok, int n_exp, int top_k, int hidden, int inter);
 int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w_down, int n_exp, int hidden,
                              int inter, const float* X, int n_tok, int top_k, const int* eptr, const int* tok,
