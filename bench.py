@@ -25,9 +25,11 @@ oracle's C restatement stands in if oracle/_ref was not built.
 Secondary line items (same JSON object, key "extra"): the routed-expert
 decode batch (64 experts of gate/up 2048x6144 and down 6144x2048, 32
 tokens, softmax top-8: GB/s over the packed bytes of the touched experts),
-and the prefill GEMM (W 12288x6144, X bf16 [M,6144], M = 512 and 2048:
+the prefill GEMM (W 12288x6144, X bf16 [M,6144], M = 512 and 2048:
 TFLOP/s = 2*M*N*K / kernel time from dispatch-stamped events, against the
-2.5 PFLOP/s dense bf16/fp16 MFMA peak).
+2.5 PFLOP/s dense bf16/fp16 MFMA peak), and the continuous-batching decode
+mix (64 tokens through the latent projections and the shared-expert FFN:
+GB/s over the packed weights and TFLOP/s, both fractions).
 """
 from __future__ import annotations
 
@@ -197,7 +199,7 @@ def prefill_gemm(torch, G, synth, dev, reps):
     for M in (512, 2048):
         X = torch.from_numpy(synth.normal(2026, M, M * K).reshape(M, K)).to(dev).to(torch.bfloat16)
         Y = torch.empty(M, N, device=dev)
-        ws = torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, K, G.X_BF16), dtype=torch.uint8, device=dev)
+        ws = torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, K, N, G.X_BF16), dtype=torch.uint8, device=dev)
         for _ in range(3):
             G.gemm(t64, N, 0, K, N, X, out=Y, ws=ws)
         torch.cuda.synchronize()
@@ -217,6 +219,60 @@ def prefill_gemm(torch, G, synth, dev, reps):
                         "TFLOPs_call": round(fl / (call_ms * 1e-3) / 1e12, 1),
                         "frac_of_bf16_peak": round(fl / (k_ms * 1e-3) / 1e12 / 2500.0, 4)}
     return out
+
+
+def decode_mix(torch, G, synth, dev, reps, copies=4):
+    """Continuous-batching decode mix: 64 tokens (fp32 X [64, 6144]) through the MLA latent projections
+    kv_a 576x6144 and q_a 1536x6144 and the shared-expert FFN (gate, up 12288x6144; down 6144x12288 with
+    SwiGLU formed in its GEMM), all IQ3_XXS GEMMs. `copies` rotated weight sets keep it out of the
+    Infinity Cache."""
+    M, HM = 64, 6144
+    shapes = [("kv_a", 576, HM), ("q_a", 1536, HM), ("gate", 12288, HM), ("up", 12288, HM), ("down", HM, 12288)]
+    log("decode mix: generating weights")
+    sets = []
+    for c in range(copies):
+        if c == 0:
+            base = {n: G.tile(torch.from_numpy(synth.iq3xxs_matrix(2027, i, r, k).reshape(-1)).to(dev), r, k)
+                    for i, (n, r, k) in enumerate(shapes)}
+            sets.append(base)
+        else:
+            sets.append({n: t.clone() for n, t in sets[0].items()})
+    X = torch.from_numpy(synth.normal(2027, 10, M * HM).reshape(M, HM)).to(dev)
+    out = {n: torch.empty(M, r, device=dev) for n, r, _ in shapes}
+    ws = {n: torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, k, r, G.X_F32), dtype=torch.uint8, device=dev)
+          for n, r, k in shapes}
+
+    def step(c):
+        W = sets[c % copies]
+        for n, r, k in shapes[:4]:
+            G.gemm(W[n], r, 0, k, r, X, out=out[n], ws=ws[n])
+        G.gemm_swiglu(W["down"], HM, 0, 12288, HM, out["gate"], out["up"], SWIGLU_LIMIT, out=out["down"],
+                      ws=ws["down"])
+
+    for c in range(3):
+        step(c)
+    torch.cuda.synchronize()
+    G.prof_start(5 * reps + 8)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for c in range(reps):
+        step(c)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    k_ms = float(G.prof_read(G.PROF_GEMM).astype(np.float64).sum()) / reps
+    w_bytes = sum(r * k // 256 * 98 for _, r, k in shapes)
+    flops = sum(2.0 * M * r * k for _, r, k in shapes)
+    return {"workload": "continuous-batching decode mix: 64 tokens, fp32 X [64,6144], IQ3_XXS kv_a 576x6144, "
+                        "q_a 1536x6144, shared expert gate/up 12288x6144 and down 6144x12288 (SwiGLU in the "
+                        "down GEMM); five GEMMs with K split over workgroups",
+            "packed_bytes_per_step": w_bytes, "gflop_per_step": round(flops / 1e9, 2),
+            "ms_per_step": round(ms, 4), "kernel_ms_per_step": round(k_ms, 4),
+            "GBps": round(w_bytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(w_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_of_fp16_peak": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4)}
 
 
 def main():
@@ -382,6 +438,8 @@ def main():
         rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(10, args.steps // 10), 3)}
         torch.cuda.empty_cache()
         rec["extra"]["prefill_gemm"] = prefill_gemm(torch, G, synth, dev, 20)
+        torch.cuda.empty_cache()
+        rec["extra"]["decode_mix"] = decode_mix(torch, G, synth, dev, 20)
     if not args.no_cpu:
         log("cpu baseline")
         cb, y_ref = cpu_baseline(wg, wu, wd, x)

@@ -81,7 +81,8 @@ def lib():
             "gpeed_iq3xxs_gemv_swiglu": ([vp, u64, u64, i32, i32, vp, vp, C.c_float, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_dense_mlp_ws_bytes": ([i64, i64], sz),
             "gpeed_iq3xxs_dense_mlp": ([vp, vp, vp, i32, i32, vp, C.c_float, vp, vp, sz, vp], i32),
-            "gpeed_iq3xxs_gemm_ws_bytes": ([i64, i64, i32], sz),
+            "gpeed_iq3xxs_gemm_ws_bytes": ([i64, i64, i64, i32], sz),
+            "gpeed_iq3xxs_gemm_swiglu": ([vp, u64, u64, i32, i32, vp, vp, C.c_float, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemm": ([vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, sz, vp], i32),
             "gpeed_prof_start": ([i32], i32),
             "gpeed_prof_read": ([i32, vp, i32, vp], i32),
@@ -263,9 +264,26 @@ def gemm(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None, 
     if out is None:
         out = torch.empty(n_tok, out_dim, dtype=torch.float32, device=X.device)
     if ws is None:
-        ws = _zeros(lib().gpeed_iq3xxs_gemm_ws_bytes(n_tok, in_dim, xd), X.device)
+        ws = _zeros(lib().gpeed_iq3xxs_gemm_ws_bytes(n_tok, in_dim, out_dim, xd), X.device)
     _check(lib().gpeed_iq3xxs_gemm(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(X), xd, n_tok, _ptr(out),
                                    _ptr(ws), ws.numel(), _stream(stream)), "gemm")
+    return out
+
+
+def gemm_swiglu(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, G, U, limit: float = 10.0, out=None,
+                ws=None, stream=None):
+    """Y [n_tok, out_dim] = SwiGLU(G, U) [n_tok, in_dim] (fp32) @ W[row0:row0+out_dim]^T, one GEMM."""
+    torch = _torch()
+    _require_cuda(w_t64, G, U)
+    if G.dtype != torch.float32 or U.dtype != torch.float32 or G.shape != U.shape:
+        raise ValueError("gemm_swiglu: G and U must be float32 of one shape")
+    n_tok = G.shape[0]
+    if out is None:
+        out = torch.empty(n_tok, out_dim, dtype=torch.float32, device=G.device)
+    if ws is None:
+        ws = _zeros(lib().gpeed_iq3xxs_gemm_ws_bytes(n_tok, in_dim, out_dim, X_F32), G.device)
+    _check(lib().gpeed_iq3xxs_gemm_swiglu(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(G), _ptr(U), limit, n_tok,
+                                          _ptr(out), _ptr(ws), ws.numel(), _stream(stream)), "gemm_swiglu")
     return out
 
 

@@ -554,10 +554,13 @@ int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "moe_experts launch");
 }
 
-size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int x_dtype) {
-    if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(in_dim) || (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16))
+size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_dim, int x_dtype) {
+    if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(in_dim) || out_dim < 1 || out_dim > (1 << 24) ||
+        (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16))
         return 0;
-    return gpeed::gemm_ws_bytes((int)n_tok, (int)in_dim, x_dtype == GPEED_X_BF16);
+    const DeviceState* st = nullptr;
+    if (device_state(&st)) return 0;
+    return gpeed::gemm_ws_bytes((int)n_tok, (int)out_dim, (int)in_dim, x_dtype == GPEED_X_BF16, st->num_cus);
 }
 
 int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const void* X,
@@ -570,12 +573,39 @@ int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_
     if (row0 % gpeed::kTileRows)
         return fail(GPEED_ERR_LAYOUT, "gemm: row0 must be a multiple of 64 on the T64 layout");
     if (!aligned(w_t64, 16) || !aligned(X, 16)) return fail(GPEED_ERR_INVALID, "gemm: misaligned operand");
-    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::gemm_ws_bytes(n_tok, in_dim, x_dtype == GPEED_X_BF16))
+    const DeviceState* st = nullptr;
+    rc = device_state(&st);
+    if (rc) return rc;
+    if (!ws || !aligned(ws, 256) ||
+        ws_bytes < gpeed::gemm_ws_bytes(n_tok, out_dim, in_dim, x_dtype == GPEED_X_BF16, st->num_cus))
         return fail(GPEED_ERR_WORKSPACE, "gemm: workspace missing, misaligned or too small");
     hipError_t e = gpeed::launch_gemm(static_cast<const uint8_t*>(w_t64), row0, in_dim, out_dim, X,
-                                      x_dtype == GPEED_X_BF16, n_tok, Y, static_cast<uint8_t*>(ws),
+                                      x_dtype == GPEED_X_BF16, n_tok, Y, static_cast<uint8_t*>(ws), st->num_cus,
                                       static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm launch");
+}
+
+int gpeed_iq3xxs_gemm_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                             const float* G, const float* U, float limit, int n_tok, float* Y, void* ws,
+                             size_t ws_bytes, gpeed_stream_t stream) {
+    if (n_tok <= 0 || out_dim <= 0) return GPEED_OK;
+    int rc = check_mv_args(w_t64, n_rows, row0, in_dim, out_dim, G, Y, "gemm_swiglu");
+    if (rc) return rc;
+    if (!U) return fail(GPEED_ERR_INVALID, "gemm_swiglu: null pointer");
+    if (n_tok > (1 << 20)) return fail(GPEED_ERR_INVALID, "gemm_swiglu: n_tok too large");
+    if (row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "gemm_swiglu: row0 must be a multiple of 64 on the T64 layout");
+    if (!aligned(w_t64, 16) || !aligned(G, 16) || !aligned(U, 16))
+        return fail(GPEED_ERR_INVALID, "gemm_swiglu: misaligned operand");
+    const DeviceState* st = nullptr;
+    rc = device_state(&st);
+    if (rc) return rc;
+    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::gemm_ws_bytes(n_tok, out_dim, in_dim, 0, st->num_cus))
+        return fail(GPEED_ERR_WORKSPACE, "gemm_swiglu: workspace missing, misaligned or too small");
+    hipError_t e = gpeed::launch_gemm(static_cast<const uint8_t*>(w_t64), row0, in_dim, out_dim, G, 0, n_tok, Y,
+                                      static_cast<uint8_t*>(ws), st->num_cus, static_cast<hipStream_t>(stream), U,
+                                      limit);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm_swiglu launch");
 }
 
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,

@@ -113,6 +113,14 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 // the parity of the other seven) written over the scale nibble. Group l's
 // bits are exactly the positions = l (mod 4), so three xor-folds give all
 // four parities at once, in bits 0..3.
+// SwiGLU with the reference's clamp (model_batch.cpp:245-253):
+// silu(min(g, lim)) * clamp(u, -lim, lim).
+__device__ __forceinline__ float swiglu1(float gv, float uv, float lim) {
+    const float gi = fminf(gv, lim);
+    const float ui = fminf(fmaxf(uv, -lim), lim);
+    return (gi / (1.0f + expf(-gi))) * ui;
+}
+
 __device__ __forceinline__ uint32_t t64_full_signs(uint32_t w) {
     const uint32_t m = w & 0x0FFFFFFFu;
     uint32_t t = m ^ (m >> 16);

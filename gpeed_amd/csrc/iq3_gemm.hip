@@ -40,10 +40,12 @@ __device__ __forceinline__ uint32_t f16_pair_of_floats(float lo, float hi) {
 
 // ---------------------------------------------------------------------------
 // X -> fp16 images with a power-of-two scale per token row. One workgroup per
-// row. IN = 0: fp32 input (hi and lo images); IN = 1: bf16 input (one image).
+// row. IN = 0: fp32 input (hi and lo images); IN = 1: bf16 input (one image);
+// IN = 2: X = SwiGLU(X, U) of fp32 gate and up rows (hi and lo images).
 template <int IN>
-__global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X, int M, int K,
-                                                     _Float16* __restrict__ xh, float* __restrict__ unscale) {
+__global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X, const float* __restrict__ U,
+                                                     float lim, int M, int K, _Float16* __restrict__ xh,
+                                                     float* __restrict__ unscale) {
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
     __shared__ float red[4];
@@ -61,6 +63,13 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
             const float4 a = p[0], b = p[1];
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
             v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            if constexpr (IN == 2) {
+                const float4* q = reinterpret_cast<const float4*>(U) + ((size_t)m * K >> 2) + 2 * c;
+                const float4 ua = q[0], ub = q[1];
+                const float u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = swiglu1(v[i], u[i], lim);
+            }
         }
     };
     const int n8 = K >> 3;
@@ -96,7 +105,7 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
             lo[i] = f16_pair_of_floats(a - (float)ha, b - (float)hb);
         }
         reinterpret_cast<u32x4_t*>(xh + (size_t)m * K)[c] = hi;
-        if constexpr (IN == 0) reinterpret_cast<u32x4_t*>(xh + plane + (size_t)m * K)[c] = lo;
+        if constexpr (IN != 1) reinterpret_cast<u32x4_t*>(xh + plane + (size_t)m * K)[c] = lo;
     }
     if (tid == 0) unscale[m] = ldexpf(1.0f, -sc);
 }
@@ -111,7 +120,119 @@ struct GemmArgs {
     float* y;               // [M][N]
     int M, N, K, nb;
     int tiles_m, tiles_n;
+    int ks;                 // K splits per result tile (1: no partials)
+    uint32_t* cnt;          // ks > 1: tickets per tile (zero between launches)
+    float* part;            // ks > 1: [tile][split][128][192] fp32 partials
 };
+
+constexpr int kTileM = 128, kTileN = 192;  // result tile of both GEMM kernels
+
+// Workgroup -> result tile (tm, tn) and K split kz (blocks [b0, b1)); the
+// splits of a tile have consecutive workgroup ids. Tiles are ordered so
+// that the eight XCDs (workgroup id % 8) each work on their own band of W
+// row tiles when the row tiles split evenly into 8 bands.
+struct GemmTile {
+    int tm, tn, kz, b0, b1;
+};
+__device__ __forceinline__ GemmTile gemm_tile(const GemmArgs& g) {
+    GemmTile t;
+    t.kz = blockIdx.x % g.ks;
+    const int id = blockIdx.x / g.ks;
+    if (g.ks == 1 && g.tiles_n % 8 == 0) {
+        const int per_band = g.tiles_n / 8;
+        const int xcd = id & 7, local = id >> 3;
+        t.tn = xcd * per_band + local % per_band;
+        t.tm = local / per_band;
+    } else {
+        t.tn = id % g.tiles_n;
+        t.tm = id / g.tiles_n;
+    }
+    t.b0 = t.kz * g.nb / g.ks;
+    t.b1 = (t.kz + 1) * g.nb / g.ks;
+    return t;
+}
+
+// The result tile from this workgroup's fp32 sums acc[mt][j][i] (token
+// m0 + 16 mt + 4 lg + i, W row n0 + 48 wave + 16 j + lr). One K split:
+// Y = acc * unscale[m]. Several: each split stores its partial with
+// device-coherent stores; after vmcnt(0) it takes the tile's ticket, and
+// the last one adds the partials in split order (bitwise repeatable) and
+// writes Y, then clears the ticket.
+__device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t, const float4_t (&acc)[8][3],
+                                           int m0, int n0, int wave, int lr, int lg, int tid, int* flag) {
+    if (g.ks == 1) {
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + mt * 16 + lg * 4 + i;
+                if (m >= g.M) continue;
+                const float us = g.unscale[m];
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const int n = n0 + wave * 48 + j * 16 + lr;
+                    if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][j][i] * us;
+                }
+            }
+        return;
+    }
+    const int tile = t.tm * g.tiles_n + t.tn;
+    float* base = g.part + (size_t)tile * g.ks * (kTileM * kTileN);
+    float* mine = base + (size_t)t.kz * (kTileM * kTileN);
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ml = mt * 16 + lg * 4 + i;
+            if (m0 + ml >= g.M) continue;
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int nl = wave * 48 + j * 16 + lr;
+                if (n0 + nl < g.N)
+                    __hip_atomic_store(mine + ml * kTileN + nl, acc[mt][j][i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this split's partial is acknowledged
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(g.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == (uint32_t)(g.ks - 1);
+    }
+    __syncthreads();
+    if (!*flag) return;  // uniform
+    // four columns per thread and step; all splits' loads issued before the
+    // adds (buffer loads with sc1: past this XCD's L2, which may hold the
+    // workspace from an earlier call)
+    const int rows = min(kTileM, g.M - m0), cols = min(kTileN, g.N - n0);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(g.ks * kTileM * kTileN * 4), 0x00020000);
+    for (int q = tid; q < rows * (kTileN / 4); q += kGemmThreads) {
+        const int ml = q / (kTileN / 4), nl = (q - ml * (kTileN / 4)) * 4;
+        if (nl >= cols) continue;
+        float4 v[8];
+#pragma unroll
+        for (int z = 0; z < 8; ++z) {
+            const uint32_t off = z < g.ks ? (uint32_t)(((z * kTileM + ml) * kTileN + nl) * 4) : 0x80000000u;
+            v[z] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16));
+        }
+        float4 sum = v[0];
+#pragma unroll
+        for (int z = 1; z < 8; ++z)
+            if (z < g.ks) {
+                sum.x += v[z].x;
+                sum.y += v[z].y;
+                sum.z += v[z].z;
+                sum.w += v[z].w;
+            }
+        const float us = g.unscale[m0 + ml];
+        float* yrow = g.y + (size_t)(m0 + ml) * g.N + n0 + nl;
+        const float o[4] = {sum.x * us, sum.y * us, sum.z * us, sum.w * us};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (nl + c < cols) yrow[c] = o[c];
+    }
+    if (tid == 0) __hip_atomic_store(g.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // ---------------------------------------------------------------------------
 // GEMM, register-decode form. A 256-thread workgroup computes 128 tokens x
@@ -148,19 +269,12 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
     const uint32_t lane = tid & 63;
     const int lr = lane & 15, lg = lane >> 4;
 
-    const int id = blockIdx.x;
-    int tn, tm;
-    if (g.tiles_n % 8 == 0) {
-        const int per_band = g.tiles_n / 8;
-        const int xcd = id & 7, local = id >> 3;
-        tn = xcd * per_band + local % per_band;
-        tm = local / per_band;
-    } else {
-        tn = id % g.tiles_n;
-        tm = id / g.tiles_n;
-    }
+    __shared__ int last_flag;
+    const GemmTile tl = gemm_tile(g);
+    const int tn = tl.tn, tm = tl.tm;
     if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
     const int m0 = tm * BM2, n0 = tn * BN2;
+    const uint32_t kboff = (uint32_t)tl.b0 * kRecordBytes;  // this split's first block
 
     {
         GridWords<kGemmThreads> gw;
@@ -174,7 +288,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
         const int r = min(n0 + wave * 48 + j * 16 + lr, g.N - 1);
-        const uint32_t base = (uint32_t)(r >> 6) * (uint32_t)g.nb * kRecordBytes;
+        const uint32_t base = (uint32_t)(r >> 6) * (uint32_t)g.nb * kRecordBytes + kboff;
         rowoff[j] = base + (uint32_t)(r & 63) * 16u;
         doff[j] = base + (uint32_t)kRecordDOffset + (uint32_t)(r & 63) * 2u;
     }
@@ -216,7 +330,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 xreg[v][i] = *reinterpret_cast<const u32x4_t*>(g.xh + (size_t)v * g.M * g.K + (size_t)xrow[i] * g.K +
-                                                               s * BK2 + xc);
+                                                               tl.b0 * kQK + s * BK2 + xc);
     };
     auto store_x = [&](int buf) {
 #pragma unroll
@@ -252,7 +366,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
         for (int j = 0; j < 3; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     const float4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int steps = g.K / BK2;  // a multiple of 4
+    const int steps = (tl.b1 - tl.b0) * (kQK / BK2);  // this split's stages, a multiple of 4
     WRing ring[4];
     uint32_t dreg[3];
     load_w(ring[0], 0, std::integral_constant<int, 0>{});
@@ -315,19 +429,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
         });
     }
 
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + mt * 16 + lg * 4 + i;
-            if (m >= g.M) continue;
-            const float us = g.unscale[m];
-#pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const int n = n0 + wave * 48 + j * 16 + lr;
-                if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][j][i] * us;
-            }
-        }
+    gemm_store(g, tl, acc, m0, n0, wave, lr, lg, tid, &last_flag);
 }
 
 
@@ -364,6 +466,7 @@ struct GemmSmem3 {
     _Float16 xs[3][BM3 * kRow3];                     // X stages (ring of 3)
     uint8_t wb[2][kWBlk3];                           // W blocks: [tile][unit][64 lanes x 16 B]
     uint8_t wd[2][512];                              // their d: [tile][64 fp16] (+ padding)
+    int last_flag;                                   // this workgroup completes its tile
 };
 
 // Entry (idx, s) of the scaled grid, both replicas: thread (s = tid & 15)
@@ -419,19 +522,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
     const int lr = lane & 15;
     const uint32_t lg = lane >> 4;
 
-    const int id = blockIdx.x;
-    int tn, tm;
-    if (g.tiles_n % 8 == 0) {
-        const int per_band = g.tiles_n / 8;
-        const int xcd = id & 7, local = id >> 3;
-        tn = xcd * per_band + local % per_band;
-        tm = local / per_band;
-    } else {
-        tn = id % g.tiles_n;
-        tm = id / g.tiles_n;
-    }
+    const GemmTile tl = gemm_tile(g);
+    const int tn = tl.tn, tm = tl.tm;
     if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
     const int m0 = tm * BM3, n0 = tn * BN3;
+    const uint32_t kboff = (uint32_t)tl.b0 * kRecordBytes;  // this split's first block
 
     const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
     scaled_grid_table(sm.tbl, tid);
@@ -447,13 +542,13 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
         if (item < 18) {
             const int jt = item / 6, u = item % 6;
             const int tile = min(n0 / kTileRows + jt, last_tile);
-            w_goff[i] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + u * kUnitBytes + lane * 16u;
+            w_goff[i] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + kboff + u * kUnitBytes + lane * 16u;
             w_loff[i] = (uint32_t)(jt * 6 + u) * kUnitBytes + lane * 16u;
         } else {
             const uint32_t l = min(lane, 23u);
             const int jt = l >> 3;
             const int tile = min(n0 / kTileRows + jt, last_tile);
-            w_goff[i] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + kRecordDOffset + (l & 7) * 16u;
+            w_goff[i] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + kboff + kRecordDOffset + (l & 7) * 16u;
             w_loff[i] = kWBlk3 + (uint32_t)jt * 128u + (l & 7) * 16u;  // past wb: into wd
         }
     }
@@ -506,7 +601,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
     const int xr = tid >> 3, xc = (tid & 7) * 8;
     const _Float16* xsrc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xsrc[i] = g.xh + (size_t)min(m0 + xr + 32 * i, g.M - 1) * g.K + xc;
+    for (int i = 0; i < 4; ++i) xsrc[i] = g.xh + (size_t)min(m0 + xr + 32 * i, g.M - 1) * g.K + tl.b0 * kQK + xc;
     u32x4_t xreg[2][4];
     auto load_x = [&](u32x4_t (&r)[4], int s) {
 #pragma unroll
@@ -530,8 +625,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
         for (int j = 0; j < 3; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     const float4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int steps = g.K / BK3;  // a multiple of 4
-    const int nblk = g.nb;
+    const int nblk = tl.b1 - tl.b0;  // this split's blocks
+    const int steps = nblk * (kQK / BK3);
     // Prologue: X stages 0, 1 in LDS (buffers 0, 1), stage 2 in registers,
     // W block 0 in LDS; then the A operands of stage 0's first sub-block and
     // the B operands of stage 0.
@@ -600,39 +695,58 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
         });
     }
 
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + mt * 16 + (int)lg * 4 + i;
-            if (m >= g.M) continue;
-            const float us = g.unscale[m];
-#pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const int n = n0 + wave * 48 + j * 16 + lr;
-                if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][j][i] * us;
-            }
-        }
+    gemm_store(g, tl, acc, m0, n0, wave, lr, (int)lg, tid, &sm.last_flag);
 }
 
 }  // namespace
 
-size_t gemm_ws_bytes(int M, int K, int x_bf16) {
+// K splits per result tile: one when the tiles fill half the CUs, else
+// enough to fill them (at most 8, at least one block per split).
+int gemm_splits(int M, int N, int K, int num_cus) {
+    const int tiles = ((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
+    const int cus = num_cus > 0 ? num_cus : 256;
+    if (2 * tiles > cus) return 1;
+    int ks = (cus + tiles - 1) / tiles;
+    ks = ks > 8 ? 8 : ks;
+    const int nb = K / kQK;
+    return ks > nb ? nb : ks;
+}
+
+namespace {
+struct GemmWs {
+    size_t img, uns, cnt, part, total;
+};
+GemmWs gemm_ws(int M, int N, int K, int x_bf16, int ks) {
+    const auto a256 = [](size_t b) { return (b + 255) / 256 * 256; };
+    GemmWs w{};
     const size_t v = x_bf16 ? 1 : 2;
-    const size_t a = (v * (size_t)M * K * 2 + 255) / 256 * 256;
-    return a + ((size_t)M * 4 + 255) / 256 * 256;
+    w.img = 0;
+    w.uns = a256(v * (size_t)M * K * 2);
+    w.cnt = w.uns + a256((size_t)M * 4);
+    const size_t tiles = (size_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
+    w.part = w.cnt + (ks > 1 ? a256(tiles * 4) : 0);
+    w.total = w.part + (ks > 1 ? tiles * ks * kTileM * kTileN * 4 : 0);
+    return w;
+}
+}  // namespace
+
+size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus) {
+    return gemm_ws(M, N, K, x_bf16, gemm_splits(M, N, K, num_cus)).total;
 }
 
 hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
-                       int M, float* Y, uint8_t* ws, hipStream_t s) {
+                       int M, float* Y, uint8_t* ws, int num_cus, hipStream_t s, const float* U, float lim) {
     if (M <= 0 || out_dim <= 0) return hipSuccess;
-    const int v = x_bf16 ? 1 : 2;
-    _Float16* xh = reinterpret_cast<_Float16*>(ws);
-    float* uns = reinterpret_cast<float*>(ws + ((size_t)v * M * in_dim * 2 + 255) / 256 * 256);
+    const int ks = gemm_splits(M, out_dim, in_dim, num_cus);
+    const GemmWs L = gemm_ws(M, out_dim, in_dim, x_bf16, ks);
+    _Float16* xh = reinterpret_cast<_Float16*>(ws + L.img);
+    float* uns = reinterpret_cast<float*>(ws + L.uns);
     if (x_bf16)
-        hipLaunchKernelGGL(k_gemm_prep_x<1>, dim3(M), dim3(256), 0, s, X, M, in_dim, xh, uns);
+        hipLaunchKernelGGL(k_gemm_prep_x<1>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns);
+    else if (U)
+        hipLaunchKernelGGL(k_gemm_prep_x<2>, dim3(M), dim3(256), 0, s, X, U, lim, M, in_dim, xh, uns);
     else
-        hipLaunchKernelGGL(k_gemm_prep_x<0>, dim3(M), dim3(256), 0, s, X, M, in_dim, xh, uns);
+        hipLaunchKernelGGL(k_gemm_prep_x<0>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmArgs a{};
@@ -644,14 +758,13 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
     a.M = M;
     a.N = out_dim;
     a.K = in_dim;
-    a.tiles_m = (M + BM2 - 1) / BM2;
-    a.tiles_n = (out_dim + BN2 - 1) / BN2;
-    const int grid = a.tiles_n * a.tiles_m;
-    if (x_bf16) {
-        a.tiles_m = (M + BM3 - 1) / BM3;
-        a.tiles_n = (out_dim + BN3 - 1) / BN3;
-        return launch_timed(kProfGemm, k_gemm3, dim3(a.tiles_n * a.tiles_m), dim3(kGemmThreads), 0, s, a);
-    }
+    a.tiles_m = (M + kTileM - 1) / kTileM;
+    a.tiles_n = (out_dim + kTileN - 1) / kTileN;
+    a.ks = ks;
+    a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
+    a.part = reinterpret_cast<float*>(ws + L.part);
+    const int grid = a.tiles_n * a.tiles_m * ks;
+    if (x_bf16) return launch_timed(kProfGemm, k_gemm3, dim3(grid), dim3(kGemmThreads), 0, s, a);
     return launch_timed(kProfGemm, k_gemm2<2>, dim3(grid), dim3(kGemmThreads), 0, s, a);
 }
 

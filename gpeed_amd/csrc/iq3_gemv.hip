@@ -226,12 +226,6 @@ __device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g
     }
 }
 
-__device__ __forceinline__ float swiglu1(float gv, float uv, float lim) {
-    const float gi = fminf(gv, lim);
-    const float ui = fminf(fmaxf(uv, -lim), lim);
-    return (gi / (1.0f + expf(-gi))) * ui;
-}
-
 // Power of two that brings max|v| over the wavefront (m: this lane's max)
 // into [2^13, 2^14).
 __device__ __forceinline__ int pow2_scale(float m) {

@@ -98,9 +98,15 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
 
 // Prefill GEMM: Y[m][j] = sum_k X[m][k] W[row0+j][k] for M tokens from the
 // T64 copy. X is fp32 (x_bf16 = 0) or bf16 (x_bf16 = 1), row-major [M][in_dim];
-// ws: gemm_ws_bytes(M, in_dim, x_bf16) bytes of scratch (fp16 images).
-size_t gemm_ws_bytes(int M, int K, int x_bf16);
+// ws: gemm_ws_bytes(M, out_dim, in_dim, x_bf16, num_cus) bytes (fp16
+// images; when the result tiles fill fewer than half the CUs, K is split
+// and the ws also holds tickets, zero-filled once, and fp32 partials).
+int gemm_splits(int M, int N, int K, int num_cus);
+size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus);
+// U (fp32, with x_bf16 = 0): X is SwiGLU(X, U) with clamp lim, formed while
+// the images are prepared.
 hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
-                       int M, float* Y, uint8_t* ws, hipStream_t s);
+                       int M, float* Y, uint8_t* ws, int num_cus, hipStream_t s, const float* U = nullptr,
+                       float lim = 0.0f);
 
 }  // namespace gpeed

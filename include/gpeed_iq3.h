@@ -135,11 +135,24 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
  * [n_tok][out_dim]. W records are staged through LDS and decoded to exact
  * fp16 values of q*(2s+1) as MFMA operands; the block scale d/4 is applied
  * to each block's fp32 partial. The prefill-sized case of matmul_quant
- * (weights.cpp:86-165, model_batch.cpp:30-95 / 151-162). X 16-byte aligned;
- * ws: gpeed_iq3xxs_gemm_ws_bytes bytes (no zero-fill needed). */
-size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int x_dtype);
+ * (weights.cpp:86-165, model_batch.cpp:30-95 / 151-162). When the 128 x 192
+ * result tiles fill fewer than half the device's CUs (few tokens or few
+ * rows), K is split over workgroups and the partials are added in a fixed
+ * order (bitwise repeatable). X 16-byte aligned; ws:
+ * gpeed_iq3xxs_gemm_ws_bytes bytes for this device, zero-filled once per
+ * shape (every call leaves it ready for the next); calls on one ws must not
+ * overlap. */
+size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_dim, int x_dtype);
 int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const void* X,
                       int x_dtype, int n_tok, float* Y, void* ws, size_t ws_bytes, gpeed_stream_t stream);
+/* The down projection of dense_mlp_batch (model_batch.cpp:145-163, SwiGLU
+ * clamp as model_batch.cpp:245-253) as one GEMM: X[t] = silu(min(G[t],
+ * limit)) * clamp(U[t], -limit, limit) for G, U fp32 [n_tok][in_dim], formed
+ * while the fp16 images are prepared. ws: gpeed_iq3xxs_gemm_ws_bytes with
+ * x_dtype GPEED_X_F32. */
+int gpeed_iq3xxs_gemm_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                             const float* G, const float* U, float limit, int n_tok, float* Y, void* ws,
+                             size_t ws_bytes, gpeed_stream_t stream);
 
 /* The two halves of the products, for callers that reuse one activation
  * across several tensors (gate and up of model.cpp:681-682) or fuse the

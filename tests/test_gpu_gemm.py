@@ -73,6 +73,60 @@ def test_gemm_prefill_full_size(gpu, M):
         assert e < TIGHT, (r0, e)
 
 
+@pytest.mark.parametrize("N,K,x_bf16", [
+    (576, 6144, False),    # MLA kv_a at 64 tokens, fp32 X: 3 row tiles, K split 8 ways
+    (1536, 6144, True),    # q_a
+    (12288, 6144, False),  # shared-expert gate/up: 64 row tiles, K split 4 ways
+    (6144, 12288, True),   # shared-expert down: 32 row tiles, K split 8 ways
+])
+def test_gemm_decode_mix_split_k(gpu, N, K, x_bf16):
+    """64 concurrent decode tokens through the latent projections and the
+    shared-expert FFN shapes: few result tiles, so K is split over
+    workgroups and the partials added in split order. Row slices against
+    the oracle; a second call on the same workspace gives the same bits
+    (its tickets are back at zero)."""
+    import torch
+
+    M = 64
+    w = synth.iq3xxs_matrix(94, N, N, K)
+    X = synth.normal(94, K, M * K).reshape(M, K)
+    if x_bf16:
+        X = bf16_round(X)
+    t64 = G.tile(dev(w.reshape(-1), gpu), N, K)
+    Xd = as_bf16_tensor(X, gpu) if x_bf16 else dev(X, gpu)
+    xd = G.X_BF16 if x_bf16 else G.X_F32
+    ws = torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, K, N, xd), dtype=torch.uint8, device=gpu)
+    Y = G.gemm(t64, N, 0, K, N, Xd, ws=ws).cpu().numpy()
+    for r0 in sorted({0, 64 * ((N // 64) // 2), N - 64}):
+        ref = oracle.matmul(w, r0, K, 64, X[::4])
+        e = max(rel_err(Y[::4, r0:r0 + 64][t], ref[t]) for t in range(ref.shape[0]))
+        assert e < TIGHT, (r0, e)
+    Y2 = G.gemm(t64, N, 0, K, N, Xd, ws=ws).cpu().numpy()
+    assert np.array_equal(Y, Y2)
+
+
+@pytest.mark.parametrize("M,H,I", [(64, 1024, 2048), (200, 512, 768), (64, 6144, 12288)])
+def test_dense_mlp_batch_gemm(gpu, M, H, I):
+    """dense_mlp_batch (model_batch.cpp:145-163) through the GEMM: gate and
+    up GEMMs, then the down GEMM with SwiGLU formed while its images are
+    prepared (gpeed_iq3xxs_gemm_swiglu). Against the oracle's dense MLP
+    (silu through the device expf differs by ulps from glibc's); the full
+    decode-mix shape on token slices."""
+    wg = synth.iq3xxs_matrix(95, 0, I, H)
+    wu = synth.iq3xxs_matrix(95, 1, I, H)
+    wd = synth.iq3xxs_matrix(95, 2, H, I)
+    X = synth.normal(95, M, M * H).reshape(M, H) * np.float32(3.0)
+    tg, tu, td = (G.tile(dev(a.reshape(-1), gpu), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I)))
+    Xd = dev(X, gpu)
+    Gm = G.gemm(tg, I, 0, H, I, Xd)
+    Um = G.gemm(tu, I, 0, H, I, Xd)
+    Y = G.gemm_swiglu(td, H, 0, I, H, Gm, Um, 10.0).cpu().numpy()
+    step = 1 if H * I <= 1 << 22 else 16
+    ref = oracle.dense_mlp(wg, wu, wd, H, I, X[::step], 10.0)
+    e = max(rel_err(Y[::step][t], ref[t]) for t in range(ref.shape[0]))
+    assert e < 1e-4, e
+
+
 def test_gemm_matches_gemv(gpu):
     """Same fp32 tokens through the GEMM and the multi-token GEMV."""
     M, N, K = 8, 640, 2048
