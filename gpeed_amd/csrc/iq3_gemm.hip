@@ -125,7 +125,7 @@ struct GemmArgs {
     float* part;            // ks > 1: [tile][split][128][192] fp32 partials
 };
 
-constexpr int kTileM = 128, kTileN = 192;  // result tile of both GEMM kernels
+constexpr int kTileN = 192;  // result tile: 128 (or 64) tokens x 192 W rows
 
 // Workgroup -> result tile (tm, tn) and K split kz (blocks [b0, b1)); the
 // splits of a tile have consecutive workgroup ids. Tiles are ordered so
@@ -152,17 +152,19 @@ __device__ __forceinline__ GemmTile gemm_tile(const GemmArgs& g) {
     return t;
 }
 
-// The result tile from this workgroup's fp32 sums acc[mt][j][i] (token
+// The result tile (16 MT tokens x 192 rows) from this workgroup's fp32 sums acc[mt][j][i] (token
 // m0 + 16 mt + 4 lg + i, W row n0 + 48 wave + 16 j + lr). One K split:
 // Y = acc * unscale[m]. Several: each split stores its partial with
 // device-coherent stores; after vmcnt(0) it takes the tile's ticket, and
 // the last one adds the partials in split order (bitwise repeatable) and
 // writes Y, then clears the ticket.
-__device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t, const float4_t (&acc)[8][3],
+template <int MT>
+__device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t, const float4_t (&acc)[MT][3],
                                            int m0, int n0, int wave, int lr, int lg, int tid, int* flag) {
+    constexpr int BM = 16 * MT;
     if (g.ks == 1) {
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = m0 + mt * 16 + lg * 4 + i;
@@ -177,10 +179,10 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
         return;
     }
     const int tile = t.tm * g.tiles_n + t.tn;
-    float* base = g.part + (size_t)tile * g.ks * (kTileM * kTileN);
-    float* mine = base + (size_t)t.kz * (kTileM * kTileN);
+    float* base = g.part + (size_t)tile * g.ks * (BM * kTileN);
+    float* mine = base + (size_t)t.kz * (BM * kTileN);
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int ml = mt * 16 + lg * 4 + i;
@@ -204,15 +206,15 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
     // four columns per thread and step; all splits' loads issued before the
     // adds (buffer loads with sc1: past this XCD's L2, which may hold the
     // workspace from an earlier call)
-    const int rows = min(kTileM, g.M - m0), cols = min(kTileN, g.N - n0);
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(g.ks * kTileM * kTileN * 4), 0x00020000);
+    const int rows = min(BM, g.M - m0), cols = min(kTileN, g.N - n0);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(g.ks * BM * kTileN * 4), 0x00020000);
     for (int q = tid; q < rows * (kTileN / 4); q += kGemmThreads) {
         const int ml = q / (kTileN / 4), nl = (q - ml * (kTileN / 4)) * 4;
         if (nl >= cols) continue;
         float4 v[8];
 #pragma unroll
         for (int z = 0; z < 8; ++z) {
-            const uint32_t off = z < g.ks ? (uint32_t)(((z * kTileM + ml) * kTileN + nl) * 4) : 0x80000000u;
+            const uint32_t off = z < g.ks ? (uint32_t)(((z * BM + ml) * kTileN + nl) * 4) : 0x80000000u;
             v[z] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16));
         }
         float4 sum = v[0];
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
         });
     }
 
-    gemm_store(g, tl, acc, m0, n0, wave, lr, lg, tid, &last_flag);
+    gemm_store<8>(g, tl, acc, m0, n0, wave, lr, lg, tid, &last_flag);
 }
 
 
@@ -456,14 +458,15 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
 // per product, which exceeds 1e-3 of max(|y_i|, rms(y)) on outputs near
 // the rms.)
 
-constexpr int BM3 = 128, BN3 = 192, BK3 = 64;
+constexpr int BN3 = 192, BK3 = 64;
 constexpr int kRow3 = BK3 + 8;                       // X LDS row stride (halves)
 constexpr int kWBlk3 = 3 * 6 * kUnitBytes;           // one block: 3 row tiles x 6 units
 constexpr int kWItems3 = 5;                          // W copy items per lane-slot per block
 
+template <int BM, int V>
 struct GemmSmem3 {
     uint8_t tbl[kGridTableBytes];                    // grid * (2s+1), see above
-    _Float16 xs[3][BM3 * kRow3];                     // X stages (ring of 3)
+    _Float16 xs[3][V][BM * kRow3];                   // X stages (ring of 3), V images each
     uint8_t wb[2][kWBlk3];                           // W blocks: [tile][unit][64 lanes x 16 B]
     uint8_t wd[2][512];                              // their d: [tile][64 fp16] (+ padding)
     int last_flag;                                   // this workgroup completes its tile
@@ -513,8 +516,11 @@ __device__ __forceinline__ half8_t decode_group(const uint8_t* tbl, uint32_t q, 
     return __builtin_bit_cast(half8_t, r);
 }
 
+template <int BM, int V>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) GemmSmem3 sm;
+    constexpr int MT = BM / 16;  // token tiles per wavefront
+    constexpr int XP = BM / 32;  // X pieces per thread per image and stage
+    __shared__ __attribute__((aligned(16))) GemmSmem3<BM, V> sm;
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -525,7 +531,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
     const GemmTile tl = gemm_tile(g);
     const int tn = tl.tn, tm = tl.tm;
     if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
-    const int m0 = tm * BM3, n0 = tn * BN3;
+    const int m0 = tm * BM, n0 = tn * BN3;
     const uint32_t kboff = (uint32_t)tl.b0 * kRecordBytes;  // this split's first block
 
     const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
@@ -599,28 +605,38 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
 
     // X staging: piece tid + 256 i = row (tid >> 3) + 32 i, columns (tid & 7) * 8 .. +7
     const int xr = tid >> 3, xc = (tid & 7) * 8;
-    const _Float16* xsrc[4];
+    const _Float16* xsrc[V][XP];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xsrc[i] = g.xh + (size_t)min(m0 + xr + 32 * i, g.M - 1) * g.K + tl.b0 * kQK + xc;
-    u32x4_t xreg[2][4];
-    auto load_x = [&](u32x4_t (&r)[4], int s) {
+    for (int v = 0; v < V; ++v)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + s * BK3);
+        for (int i = 0; i < XP; ++i)
+            xsrc[v][i] = g.xh + (size_t)v * g.M * g.K + (size_t)min(m0 + xr + 32 * i, g.M - 1) * g.K + tl.b0 * kQK + xc;
+    u32x4_t xreg[2][V][XP];
+    auto load_x = [&](u32x4_t (&r)[V][XP], int s) {
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+#pragma unroll
+            for (int i = 0; i < XP; ++i) r[v][i] = *reinterpret_cast<const u32x4_t*>(xsrc[v][i] + s * BK3);
     };
-    auto store_x = [&](const u32x4_t (&r)[4], int xb) {
+    auto store_x = [&](const u32x4_t (&r)[V][XP], int xb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(&sm.xs[xb][(xr + 32 * i) * kRow3 + xc]) = r[i];
+        for (int v = 0; v < V; ++v)
+#pragma unroll
+            for (int i = 0; i < XP; ++i)
+                *reinterpret_cast<u32x4_t*>(&sm.xs[xb][v][(xr + 32 * i) * kRow3 + xc]) = r[v][i];
     };
-    // A operands of sub-block t of the stage in X buffer xb: [mt]
-    auto read_a = [&](half8_t (&a)[8], int xb, int t) {
+    // A operands of sub-block t of the stage in X buffer xb: [image][mt]
+    auto read_a = [&](half8_t (&a)[V][MT], int xb, int t) {
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt)
-            a[mt] = *reinterpret_cast<const half8_t*>(&sm.xs[xb][(mt * 16 + lr) * kRow3 + t * 32 + lg * 8]);
+        for (int v = 0; v < V; ++v)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                a[v][mt] = *reinterpret_cast<const half8_t*>(&sm.xs[xb][v][(mt * 16 + lr) * kRow3 + t * 32 + lg * 8]);
     };
 
-    float4_t acc[8][3], blk[8][3];
+    float4_t acc[MT][3], blk[MT][3];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < 3; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     const float4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -638,7 +654,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
     store_x(xreg[1], 1);
     load_x(xreg[0], min(2, steps - 1));
     __syncthreads();  // table, W block 0, X stages 0 and 1
-    half8_t a[2][8];
+    half8_t a[2][V][MT];
     half8_t bop[2][2][3];  // [stage parity][t][j]
     read_a(a[0], 0, 0);
     decode_half(bop[0][0], 0, 0);
@@ -661,21 +677,25 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
             read_a(a[1], xb0, 1);
             decode_half(bop[(U + 1) & 1][0], s + 1, 0);
 #pragma unroll
-            for (int mt = 0; mt < 8; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int j = 0; j < 3; ++j)
-                    blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][mt], bop[U & 1][0][j],
-                                                                         U == 0 ? zero4 : blk[mt][j], 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < V; ++v)
+                        blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            a[0][v][mt], bop[U & 1][0][j], U == 0 && v == 0 ? zero4 : blk[mt][j], 0, 0, 0);
             // sub-block 1: MFMAs on a[1]; meanwhile A of the next stage's
             // sub-block 0 and its B operands of sub-block 1
             read_a(a[0], xb1, 0);
             decode_half(bop[(U + 1) & 1][1], s + 1, 1);
 #pragma unroll
-            for (int mt = 0; mt < 8; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int j = 0; j < 3; ++j)
-                    blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][mt], bop[U & 1][1][j], blk[mt][j], 0,
-                                                                         0, 0);
+#pragma unroll
+                    for (int v = 0; v < V; ++v)
+                        blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][v][mt], bop[U & 1][1][j],
+                                                                             blk[mt][j], 0, 0, 0);
             if constexpr (U == 3) {
                 // block complete: acc += d/4 * partial (column = this lane's row)
 #pragma unroll
@@ -683,7 +703,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
                     const uint16_t dh = *reinterpret_cast<const uint16_t*>(&sm.wd[c & 1][d_off[j]]);
                     const float d4 = (float)__builtin_bit_cast(_Float16, dh) * 0.25f;
 #pragma unroll
-                    for (int mt = 0; mt < 8; ++mt)
+                    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                         for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(d4, blk[mt][j][i], acc[mt][j][i]);
                 }
@@ -695,15 +715,19 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
         });
     }
 
-    gemm_store(g, tl, acc, m0, n0, wave, lr, (int)lg, tid, &sm.last_flag);
+    gemm_store<MT>(g, tl, acc, m0, n0, wave, lr, (int)lg, tid, &sm.last_flag);
 }
 
 }  // namespace
 
 // K splits per result tile: one when the tiles fill half the CUs, else
 // enough to fill them (at most 8, at least one block per split).
+// Token rows per result tile: 64 for at most 64 tokens (no padding), else 128.
+int gemm_tile_m(int M) { return M <= 64 ? 64 : 128; }
+
 int gemm_splits(int M, int N, int K, int num_cus) {
-    const int tiles = ((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
+    const int bm = gemm_tile_m(M);
+    const int tiles = ((M + bm - 1) / bm) * ((N + kTileN - 1) / kTileN);
     const int cus = num_cus > 0 ? num_cus : 256;
     if (2 * tiles > cus) return 1;
     int ks = (cus + tiles - 1) / tiles;
@@ -723,9 +747,10 @@ GemmWs gemm_ws(int M, int N, int K, int x_bf16, int ks) {
     w.img = 0;
     w.uns = a256(v * (size_t)M * K * 2);
     w.cnt = w.uns + a256((size_t)M * 4);
-    const size_t tiles = (size_t)((M + kTileM - 1) / kTileM) * ((N + kTileN - 1) / kTileN);
+    const int bm = gemm_tile_m(M);
+    const size_t tiles = (size_t)((M + bm - 1) / bm) * ((N + kTileN - 1) / kTileN);
     w.part = w.cnt + (ks > 1 ? a256(tiles * 4) : 0);
-    w.total = w.part + (ks > 1 ? tiles * ks * kTileM * kTileN * 4 : 0);
+    w.total = w.part + (ks > 1 ? tiles * ks * bm * kTileN * 4 : 0);
     return w;
 }
 }  // namespace
@@ -758,14 +783,19 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
     a.M = M;
     a.N = out_dim;
     a.K = in_dim;
-    a.tiles_m = (M + kTileM - 1) / kTileM;
+    const int bm = gemm_tile_m(M);
+    a.tiles_m = (M + bm - 1) / bm;
     a.tiles_n = (out_dim + kTileN - 1) / kTileN;
     a.ks = ks;
     a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
     a.part = reinterpret_cast<float*>(ws + L.part);
     const int grid = a.tiles_n * a.tiles_m * ks;
-    if (x_bf16) return launch_timed(kProfGemm, k_gemm3, dim3(grid), dim3(kGemmThreads), 0, s, a);
-    return launch_timed(kProfGemm, k_gemm2<2>, dim3(grid), dim3(kGemmThreads), 0, s, a);
+    const dim3 gd(grid), bd(kGemmThreads);
+    if (bm == 64)
+        return x_bf16 ? launch_timed(kProfGemm, k_gemm3<64, 1>, gd, bd, 0, s, a)
+                      : launch_timed(kProfGemm, k_gemm3<64, 2>, gd, bd, 0, s, a);
+    return x_bf16 ? launch_timed(kProfGemm, k_gemm3<128, 1>, gd, bd, 0, s, a)
+                  : launch_timed(kProfGemm, k_gemm2<2>, gd, bd, 0, s, a);
 }
 
 }  // namespace gpeed
