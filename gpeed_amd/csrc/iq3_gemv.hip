@@ -6,7 +6,8 @@
 // chunks, one per workgroup, so every CU streams the same number of bytes
 // whatever the tile count. Inside a workgroup the chunk's records are dealt
 // round-robin to the wavefronts; a wavefront streams its records through a
-// register ring (six coalesced 16-byte loads and one 2-byte load per lane)
+// register ring (six coalesced 16-byte buffer loads and one 2-byte load per
+// lane)
 // and keeps a per-row partial sum per tile, which meets the other
 // wavefronts' partials in LDS. A tile cut by a chunk boundary is finished by
 // whichever of its workgroups arrives last (atomic ticket in a caller-owned
@@ -15,8 +16,9 @@
 //
 // Decode and product. Lane n of a wavefront holds row n of the tile. Per
 // group of 4 weights it makes one LDS lookup in its own replica of the grid
-// table (4 unsigned fp16, no bank conflicts), sets the fp16 sign bits with a
-// rotate and a masked or, and issues one v_mfma_f32_4x4x4_16b_f16 whose A
+// table (4 unsigned fp16, no bank conflicts), sets the fp16 sign bits (one
+// 64-bit shift places both pairs' signs, then two masked ors), and issues
+// one v_mfma_f32_4x4x4_16b_f16 whose A
 // operand is broadcast (CBSZ=4) from the lanes of block ABID of a register
 // pair that holds 16 such 4-element activation slices: row 2p / 2p+1 carry
 // token 2p as fp16 hi / lo parts, rows 2 / 3 token 2p+1. Accumulator row
@@ -104,19 +106,17 @@ __global__ __launch_bounds__(256) void k_prep_act(const float* __restrict__ x,
 // ---------------------------------------------------------------------------
 // GEMV
 
-#ifndef GEMV_WAVES
-#define GEMV_WAVES 8
-#endif
-#ifndef GEMV_PF
-#define GEMV_PF 2
-#endif
+// Wavefronts per workgroup. (16 decodes a record 13% faster in isolation,
+// but its build fails the bitwise-repeatability test of the split-tile
+// combine at 6144x12288, so 8 it is.)
+constexpr int kGemvWaves = 8;
 
 template <int NT>
 struct GemvCfg {
     static constexpr int kPairs = (NT + 1) / 2;
-    static constexpr int kWaves = GEMV_WAVES;
-    // records in flight per wavefront (register ring)
-    static constexpr int kPF = NT <= 2 ? GEMV_PF : 2;
+    static constexpr int kWaves = kGemvWaves;
+    // records in flight per wavefront (register ring; 3 measured slower)
+    static constexpr int kPF = 2;
     // tiles one chunk may touch (LDS partial slots)
     static constexpr int kSlots = NT == 1 ? 8 : (NT == 2 ? 4 : 2);
 };
@@ -141,7 +141,7 @@ struct ModeCfg {
     // MODE 1/2: records per wavefront (chunk <= kWaves * kMaxPer); each
     // wavefront prepares the activation blocks of its own records (48
     // records, 48 KB of images, per workgroup)
-    static constexpr int kMaxPer = 48 / GEMV_WAVES;
+    static constexpr int kMaxPer = 48 / kGemvWaves;
 };
 
 // act64 layout (one vector, n = K/256 blocks): block b at b*1024, its

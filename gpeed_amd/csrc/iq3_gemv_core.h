@@ -136,15 +136,6 @@ __device__ __forceinline__ void load_record(Rec<NP>& r, const uint8_t* rec, cons
     }
 }
 
-// The weight part only (the activation images are read elsewhere).
-template <int NP>
-__device__ __forceinline__ void load_record_w(Rec<NP>& r, const uint8_t* rec, uint32_t lane) {
-#pragma unroll
-    for (int i = 0; i < 6; ++i)
-        r.u[i] = *reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u);
-    r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
-}
-
 // The 8 grid lookups of one sub-block (two index words, 4 bytes each).
 __device__ __forceinline__ void grid_lookups(const uint8_t* tbl, uint32_t lb, uint32_t q0, uint32_t q1,
                                              u32x2_t (&g)[8]) {
@@ -191,7 +182,8 @@ __device__ __forceinline__ void subblock_dot(uint32_t w, const u32x2_t (&g)[8], 
 // (sub-blocks 2a, 2a+1); else blk[t] += (2s+1) * partial of token t
 // (blk[2p+1] of a single-token last pair is meaningless). With kPipe the
 // lookups of sub-block ib+1 are issued before the products of sub-block ib
-// (8 more VGPRs pairs; off for 3-4 token pairs, whose rings fill the file).
+// (16 more VGPRs; off for 3-4 token pairs, whose rings fill the register
+// file).
 template <int NP, bool kPerImage = false, bool kPipe = (NP <= 2)>
 __device__ __forceinline__ void record_dot(const uint8_t* tbl, const Rec<NP>& r, uint32_t lb,
                                            float (&blk)[kPerImage ? 4 : 2 * NP]) {
