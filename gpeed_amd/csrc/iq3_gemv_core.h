@@ -113,8 +113,12 @@ struct Rec {
 };
 
 // rec: the record; ab: its block's prepared activation (n_tok vectors,
-// 2*NP - 1 <= n_tok <= 2*NP). The loads do not depend on a branch, so the
-// compiler can wait for one ring slot at a time.
+// 2*NP - 1 <= n_tok <= 2*NP) in the lane-major layout of the grouped
+// products: pair p at p * 2048, lane slot L (32 bytes: its 4 register
+// images) at L * 32, two 16-byte loads per pair. A last pair holding one
+// token stores the 32 slots of rows 0, 1 only (1 KiB); rows 2, 3 then read
+// a duplicate and are never used. The loads do not depend on a branch, so
+// the compiler can wait for one ring slot at a time.
 template <int NP>
 __device__ __forceinline__ void load_record(Rec<NP>& r, const uint8_t* rec, const uint8_t* ab,
                                             uint32_t lane, int n_tok) {
@@ -122,17 +126,17 @@ __device__ __forceinline__ void load_record(Rec<NP>& r, const uint8_t* rec, cons
     for (int i = 0; i < 6; ++i)
         r.u[i] = *reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u);
     r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
-    // a last pair holding one token stores rows 0, 1 only (256-byte images);
-    // rows 2, 3 then read a duplicate and are never used
-    const uint32_t off_half = ((lane >> 2) * 2 + (lane & 1)) * 8u;
+    const uint32_t slot_half = (lane >> 2) * 2 + (lane & 1);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
         const bool half = (p == NP - 1) && (n_tok & 1);
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-            const uint32_t off = half ? a * 256u + off_half : a * 512u + lane * 8u;
-            r.a[p][a] = *reinterpret_cast<const u32x2_t*>(ab + p * 2048 + off);
-        }
+        const uint8_t* src = ab + p * 2048 + (half ? slot_half : lane) * 32u;
+        const u32x4_t v0 = *reinterpret_cast<const u32x4_t*>(src);
+        const u32x4_t v1 = *reinterpret_cast<const u32x4_t*>(src + 16);
+        r.a[p][0] = u32x2_t{v0.x, v0.y};
+        r.a[p][1] = u32x2_t{v0.z, v0.w};
+        r.a[p][2] = u32x2_t{v1.x, v1.y};
+        r.a[p][3] = u32x2_t{v1.z, v1.w};
     }
 }
 

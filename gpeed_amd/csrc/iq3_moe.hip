@@ -261,12 +261,14 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
 // ---------------------------------------------------------------------------
 // Activation gather / SwiGLU into per-segment prepared activations
 
+// Lane-major prepared activation of one segment (see load_record): token t
+// of n_tok, block b, register image a, slice beta, hi (hl = 0) or lo part.
 __device__ __forceinline__ size_t act_off(int n_tok, int b, int t, int a, int beta, int hl) {
     const int p = t >> 1;
     const bool half_pair = (n_tok & 1) && (p == (n_tok >> 1));
     const size_t base = (size_t)b * n_tok * 1024 + (size_t)p * 2048;
-    if (half_pair) return base + a * 256 + (2 * beta + hl) * 8;
-    return base + a * 512 + (4 * beta + 2 * (t & 1) + hl) * 8;
+    if (half_pair) return base + (2 * beta + hl) * 32 + a * 8;
+    return base + (4 * beta + 2 * (t & 1) + hl) * 32 + a * 8;
 }
 
 // One wavefront per (slot p, block b). MODE 0: v = X[tok[p]]; MODE 1:
