@@ -223,6 +223,11 @@ __device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g
                 r.a[p][a] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ra, o, 0, 0));
             }
         }
+        if constexpr (MODE == 0) {
+            const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.xsc), 0, g.nb * NT * 4, kBufferDword3);
+            const uint32_t t = min(lane & 7u, (uint32_t)NT - 1u);
+            r.xs = __builtin_amdgcn_raw_buffer_load_b32(rx, live ? ((uint32_t)b * NT + t) * 4u : kOutOfRange, 0, 0);
+        }
     }
 }
 
@@ -436,9 +441,8 @@ __device__ __forceinline__ void gemv_stream(GemvShared<NT, shared_layout<MODE>()
                     if constexpr (kPrep) {
                         acc[0] = fmaf(d4 * sh.xscl[(wave * KP + kk) * 4], blk[0], acc[0]);
                     } else {
-                        const float* xs = g.xsc + (size_t)b * NT;
 #pragma unroll
-                        for (int t = 0; t < NT; ++t) acc[t] = fmaf(d4 * xs[t], blk[t], acc[t]);
+                        for (int t = 0; t < NT; ++t) acc[t] = fmaf(d4 * rec_unscale(ring[s], t), blk[t], acc[t]);
                     }
                 }
             }

@@ -103,14 +103,24 @@ __device__ __forceinline__ void grid_table_store(uint8_t* tbl, const GridWords<k
     }
 }
 
-// One record as a lane holds it: its row's 24 dwords and d, and the NP
-// activation register images (token pairs) of the record's block.
+// One record as a lane holds it: its row's 24 dwords and d, the NP
+// activation register images (token pairs) of the record's block and, where
+// the unscales come from global memory, token (lane & 7)'s unscale of the
+// block (read back with v_readlane: loaded with the record, it is covered by
+// the record's wait).
 template <int NP>
 struct Rec {
     u32x4_t u[6];
     uint32_t d;
     u32x2_t a[NP][4];
+    uint32_t xs;
 };
+
+// Token t's block unscale from a record's lane-distributed copy.
+template <int NP>
+__device__ __forceinline__ float rec_unscale(const Rec<NP>& r, int t) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(r.xs, t));
+}
 
 // rec: the record; ab: its block's prepared activation (n_tok vectors,
 // 2*NP - 1 <= n_tok <= 2*NP) in the lane-major layout of the grouped

@@ -345,11 +345,18 @@ __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, ui
                                              const uint8_t* act, int n, int nb, float* y, int rows, int row0) {
     constexpr int PF = 2;
     const float* xsc = reinterpret_cast<const float*>(act + (size_t)nb * n * 1024);
+    // The block unscales travel with the record ring: one wait per record
+    // covers both, where a load issued at the product would expose its
+    // latency.
     Rec<NP> ring[PF];
+    const int tl = min((int)(lane & 7u), n - 1);
 #pragma unroll
     for (int s = 0; s < PF; ++s) {
         const int b = min(s, nb - 1);
         load_record<NP>(ring[s], rec0 + (size_t)b * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
+        ring[s].xs = __builtin_bit_cast(uint32_t, xsc[(size_t)b * n + tl]);
+        // slot order kept, so the loop's first wait covers slot 0 only
+        __builtin_amdgcn_sched_barrier(0);
     }
     float acc[2 * NP];
 #pragma unroll
@@ -366,10 +373,11 @@ __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, ui
                 const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)ring[s].d) * 0.25f;
 #pragma unroll
                 for (int t = 0; t < 2 * NP; ++t)
-                    if (t < n) acc[t] = fmaf(d4 * xsc[(size_t)k * n + t], blk[t], acc[t]);
+                    if (t < n) acc[t] = fmaf(d4 * rec_unscale(ring[s], t), blk[t], acc[t]);
             }
             const int b = min(k + PF, nb - 1);
             load_record<NP>(ring[s], rec0 + (size_t)b * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
+            ring[s].xs = __builtin_bit_cast(uint32_t, xsc[(size_t)b * n + tl]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
