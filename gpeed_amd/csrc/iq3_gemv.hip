@@ -156,7 +156,7 @@ struct GemvArgs {
     const uint8_t* act;    // MODE 0/3: prepared activation
     const float* xsc;      // MODE 0: [nb][n_tok]; MODE 3: [nb][4] unscales
     uint32_t* cnt;         // tickets (zero between launches)
-    float* part;           // chunk partials of shared tiles
+    uint64_t* part;        // chunk partials of shared tiles (tagged words)
     int nb;
     int n_tiles;           // row tiles per tensor
     int n_records;         // n_tensors * n_tiles * nb
@@ -284,7 +284,6 @@ struct GemvShared {
     __attribute__((aligned(16))) uint8_t xsl[kPrep ? W * KP * 1024 : 16];  // per-wavefront activation images
     __attribute__((aligned(16))) float xscl[kPrep ? W * KP * 4 : 4];      // and their unscales
     float vsum[S][64];                                           // workgroup row sums (SwiGLU epilogue)
-    int flag[S];
 };
 
 // The chunk of workgroup `blk` and this wavefront's share of it.
@@ -458,75 +457,131 @@ __device__ __forceinline__ void gemv_stream(GemvShared<NT, shared_layout<MODE>()
     }
 }
 
-// EPI 0 epilogue: sum the wavefront partials per (tile, token, row) in wave
-// order; whole tiles go straight to y, tiles shared with a neighbouring
-// chunk (only the chunk's first and last can be) through the workspace,
-// completed by the last workgroup to take the tile's ticket, which adds the
-// partials in chunk order. Call after a barrier that completes sh.red.
+// Shared-tile partials. A tile (or gate/up pair) cut by chunk boundaries
+// has one part per chunk; each part's values are published as tagged 64-bit
+// words (value bits | 1 << 32, single-copy atomic), so a reader knows a
+// value has landed without waiting for the writer's stores to complete.
+// The workgroup that takes the unit's last ticket (one relaxed atomic per
+// unit, issued right after its own words) sums the parts in part order;
+// another part's word not yet landed is read again (its writer issued it
+// before taking its ticket, so it lands: the bound only guards against a
+// corrupted workspace). The summing workgroup clears the words and the
+// ticket, leaving the workspace zero for the next launch.
+constexpr int kTagSpin = 1 << 20;
+
+__device__ __forceinline__ void put_tagged(uint64_t* p, float v) {
+    __hip_atomic_store(p, (1ull << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_tagged(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// acc[t] = sum over parts j0[t]..j1[t] (in order) of word p[j * part_stride
+// + t * 64]; part `me` contributes mine[t] instead. The loads of up to four
+// parts are in flight at once. The words read are cleared.
+template <int NT>
+__device__ __forceinline__ void sum_tagged_parts(uint64_t* p, size_t part_stride, const int (&j0)[NT],
+                                                 const int (&j1)[NT], int me, const float (&mine)[NT],
+                                                 float (&acc)[NT]) {
+    int lo = j0[0], hi = j1[0];
+#pragma unroll
+    for (int t = 1; t < NT; ++t) {
+        lo = min(lo, j0[t]);
+        hi = max(hi, j1[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    for (int jb = lo; jb <= hi; jb += 4) {
+        uint64_t v[4][NT];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = jb + i;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                v[i][t] = (j >= j0[t] && j <= j1[t] && j != me) ? get_tagged(p + j * part_stride + t * 64) : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = jb + i;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (j < j0[t] || j > j1[t]) continue;
+                float x = mine[t];
+                if (j != me) {
+                    uint64_t w = v[i][t];
+                    for (int spin = 0; (w >> 32) == 0 && spin < kTagSpin; ++spin)
+                        w = get_tagged(p + j * part_stride + t * 64);
+                    x = __builtin_bit_cast(float, (uint32_t)w);
+                }
+                acc[t] += x;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        for (int j = j0[t]; j <= j1[t]; ++j)
+            __hip_atomic_store(p + j * part_stride + t * 64, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Ticket of a shared unit, taken by lane 0 and returned to the wavefront.
+__device__ __forceinline__ uint32_t take_ticket(uint32_t* cnt, uint32_t lane) {
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_amdgcn_readfirstlane(old);
+}
+
+// EPI 0 epilogue: wavefront w finishes the chunk's tile slots w, w + W, ...:
+// the wavefront partials summed in wave order; a whole tile goes straight
+// to y, a shared tile's part is published, and the last ticket holder adds
+// the parts in chunk order — bitwise repeatable. Call after a barrier that
+// completes sh.red.
 template <int NT, int MODE>
 __device__ __forceinline__ void gemv_epilogue_y(GemvShared<NT, shared_layout<MODE>()>& sh, const GemvArgs& g,
-                                                const Chunk& ch, int blk, int tid) {
-    constexpr int W = GemvCfg<NT>::kWaves, kThreads = W * 64;
+                                                const Chunk& ch, int blk, int wave, uint32_t lane) {
+    constexpr int W = GemvCfg<NT>::kWaves;
     const int n_slots = (ch.c1 - 1) / g.nb - ch.tile0 + 1;
-    auto first_chunk = [&](int vt) { return vt * g.nb / g.chunk; };
-    auto last_chunk = [&](int vt) { return ((vt + 1) * g.nb - 1) / g.chunk; };
-    for (int o = tid; o < n_slots * NT * 64; o += kThreads) {
-        const int slot = o / (NT * 64), t = (o / 64) % NT, n = o & 63;
-        float sum = 0.0f;
+    for (int slot = wave; slot < n_slots; slot += W) {
+        const int tile = ch.tile0 + slot;
+        const int first = tile * g.nb / g.chunk, last = ((tile + 1) * g.nb - 1) / g.chunk;
+        float sum[NT];
 #pragma unroll
-        for (int v = 0; v < W; ++v) sum += sh.red[slot][v][t][n];
-        const int tile = ch.tile0 + slot;
-        const int first = first_chunk(tile);
-        if (first == last_chunk(tile)) {
-            const int ten = tile >= g.n_tiles ? 1 : 0;
-            const int row = (tile - ten * g.n_tiles) * kTileRows + n;
-            if (row < g.out_dim) g.y[ten][(size_t)t * g.out_dim + row] = sum;
-        } else {
-            // coherent across the XCDs' L2s without a full-cache writeback
-            __hip_atomic_store(g.part + (((size_t)tile * g.max_parts + (blk - first)) * NT + t) * 64 + n, sum,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int t = 0; t < NT; ++t) {
+            sum[t] = 0.0f;
+#pragma unroll
+            for (int v = 0; v < W; ++v) sum[t] += sh.red[slot][v][t][lane];
         }
-    }
-    const int tile_end = ch.tile0 + n_slots - 1;
-    const bool any_shared = first_chunk(ch.tile0) != last_chunk(ch.tile0) ||
-                            first_chunk(tile_end) != last_chunk(tile_end);
-    if (!any_shared) return;  // uniform
-    // Partials complete (vmcnt(0)) before any thread of the workgroup takes
-    // a ticket; the ticket holder that completes a tile then reads the other
-    // chunks' partials with coherent loads.
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (tid < n_slots) {
-        const int tile = ch.tile0 + tid;
-        const int first = first_chunk(tile), last = last_chunk(tile);
-        int is_last = 0;
         if (first != last) {
-            const uint32_t old = __hip_atomic_fetch_add(g.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            is_last = old == (uint32_t)(last - first);
+            uint64_t* p = g.part + ((size_t)tile * g.max_parts * NT) * 64 + lane;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) put_tagged(p + ((size_t)(blk - first) * NT + t) * 64, sum[t]);
+            if (take_ticket(g.cnt + tile, lane) != (uint32_t)(last - first)) continue;  // uniform
+            float tot[NT];
+            int j0[NT], j1[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                j0[t] = 0;
+                j1[t] = last - first;
+            }
+            sum_tagged_parts<NT>(p, (size_t)NT * 64, j0, j1, blk - first, sum, tot);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) sum[t] = tot[t];
+            if (lane == 0) __hip_atomic_store(g.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        sh.flag[tid] = is_last;
-    }
-    __syncthreads();
-    for (int o = tid; o < n_slots * NT * 64; o += kThreads) {
-        const int slot = o / (NT * 64), t = (o / 64) % NT, n = o & 63;
-        if (!sh.flag[slot]) continue;
-        const int tile = ch.tile0 + slot;
-        const int parts = last_chunk(tile) - first_chunk(tile) + 1;
-        float sum = 0.0f;
-        for (int j = 0; j < parts; ++j)
-            sum += __hip_atomic_load(g.part + (((size_t)tile * g.max_parts + j) * NT + t) * 64 + n, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
         const int ten = tile >= g.n_tiles ? 1 : 0;
-        const int row = (tile - ten * g.n_tiles) * kTileRows + n;
-        if (row < g.out_dim) g.y[ten][(size_t)t * g.out_dim + row] = sum;
+        const int row = (tile - ten * g.n_tiles) * kTileRows + lane;
+        if (row < g.out_dim) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) g.y[ten][(size_t)t * g.out_dim + row] = sum[t];
+        }
     }
-    if (tid < n_slots && sh.flag[tid])
-        __hip_atomic_store(g.cnt + ch.tile0 + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // EPI 1 epilogue: virtual tiles 2r (gate) and 2r+1 (up) of row tile r form
-// a pair shared by chunks first_chunk(2r) .. last_chunk(2r+1); the
-// workgroup completing a pair writes SwiGLU of its 64 rows as act64 images.
+// a pair shared by chunks first_chunk(2r) .. last_chunk(2r+1); wavefront q
+// finishes the chunk's pair p0 + q (publishes its parts; if it completes
+// the pair, writes SwiGLU of the 64 rows as act64 images).
 __device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const GemvArgs& g, const Chunk& ch,
                                                      int blk, int tid, int wave, uint32_t lane) {
     constexpr int W = GemvCfg<1>::kWaves, kThreads = W * 64;
@@ -535,7 +590,7 @@ __device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const
     auto last_chunk = [&](int vt) { return ((vt + 1) * g.nb - 1) / g.chunk; };
     const int p0 = ch.tile0 >> 1;
     const int n_pairs = (ch.tile0 + n_slots - 1) / 2 - p0 + 1;
-    // (a) wavefront sums of every touched virtual tile
+    // wavefront sums of every touched virtual tile
     for (int o = tid; o < n_slots * 64; o += kThreads) {
         const int slot = o / 64, n = o & 63;
         float sum = 0.0f;
@@ -543,49 +598,32 @@ __device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const
         for (int v = 0; v < W; ++v) sum += sh.red[slot][v][0][n];
         sh.vsum[slot][n] = sum;
     }
-    __syncthreads();
-    // (b) pairs wholly inside this chunk are final here; the others publish
-    // their partials and take a ticket
-    for (int o = tid; o < n_slots * 64; o += kThreads) {
-        const int slot = o / 64, n = o & 63;
-        const int vt = ch.tile0 + slot, pr = vt >> 1;
-        const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
-        if (first != last)
-            __hip_atomic_store(g.part + (((size_t)pr * g.max_parts + (blk - first)) * 2 + (vt & 1)) * 64 + n,
-                               sh.vsum[slot][n], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (tid < n_pairs) {
-        const int pr = p0 + tid;
-        const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
-        int st = 1;
-        if (first != last) {
-            const uint32_t old = __hip_atomic_fetch_add(g.cnt + pr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            st = old == (uint32_t)(last - first) ? 1 : 0;
-        }
-        sh.flag[tid] = st;
-    }
-    __syncthreads();
-    // (c) wavefront q completes pair p0+q: gate and up rows, SwiGLU, one
-    // power-of-two scale over the 64 values, fp16 hi/lo act64 images
+    lds_barrier();
     for (int q = wave; q < n_pairs; q += W) {
-        if (!sh.flag[q]) continue;  // uniform per wavefront
         const int pr = p0 + q;
         const int first = first_chunk(2 * pr), last = last_chunk(2 * pr + 1);
         float v[2];
+        if (first == last) {
+            v[0] = sh.vsum[2 * pr - ch.tile0][lane];
+            v[1] = sh.vsum[2 * pr + 1 - ch.tile0][lane];
+        } else {
+            uint64_t* p = g.part + ((size_t)pr * g.max_parts * 2) * 64 + lane;
+            const int me = blk - first;
+            float mine[2] = {0.0f, 0.0f};
+            int j0[2], j1[2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int vt = 2 * pr + h;
-            if (first == last) {
-                v[h] = sh.vsum[vt - ch.tile0][lane];
-            } else {
-                v[h] = 0.0f;
-                const int j0 = first_chunk(vt) - first, j1 = last_chunk(vt) - first;
-                for (int j = j0; j <= j1; ++j)
-                    v[h] += __hip_atomic_load(g.part + (((size_t)pr * g.max_parts + j) * 2 + h) * 64 + lane,
-                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int h = 0; h < 2; ++h) {
+                const int vt = 2 * pr + h, slot = vt - ch.tile0;
+                j0[h] = first_chunk(vt) - first;
+                j1[h] = last_chunk(vt) - first;
+                if (slot >= 0 && slot < n_slots) {
+                    mine[h] = sh.vsum[slot][lane];
+                    put_tagged(p + ((size_t)me * 2 + h) * 64, mine[h]);
+                }
             }
+            if (take_ticket(g.cnt + pr, lane) != (uint32_t)(last - first)) continue;  // uniform
+            sum_tagged_parts<2>(p, 2 * 64, j0, j1, me, mine, v);
+            if (lane == 0) __hip_atomic_store(g.cnt + pr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         const float hv = swiglu1(v[0], v[1], g.lim);
         const int sc = pow2_scale(fabsf(hv));
@@ -600,8 +638,6 @@ __device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const
         *reinterpret_cast<_Float16*>(dst + 2 * c) = hi;
         *reinterpret_cast<_Float16*>(dst + 8 + 2 * c) = lo;
         if (lane == 0) usc[blk_o * 4 + a] = ldexpf(1.0f, -sc);
-        if (lane == 0 && first != last)
-            __hip_atomic_store(g.cnt + pr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -640,7 +676,7 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
     gemv_stream<NT, MODE, EPI>(sh, g, ring, src, ch, 0, ch.n_mine, wave, lane);
     lds_barrier();
     if constexpr (EPI == 0) {
-        gemv_epilogue_y<NT, MODE>(sh, g, ch, blockIdx.x, tid);
+        gemv_epilogue_y<NT, MODE>(sh, g, ch, blockIdx.x, wave, lane);
     } else {
         gemv_epilogue_swiglu(sh, g, ch, blockIdx.x, tid, wave, lane);
     }
@@ -719,7 +755,7 @@ GemvArgs base_args(const GemvPlan& plan, const uint8_t* const* w, float* const* 
     a.n_records = (int)plan.n_records;
     a.out_dim = out_dim;
     a.cnt = reinterpret_cast<uint32_t*>(ws);
-    a.part = reinterpret_cast<float*>(ws + ((size_t)plan.n_tiles_all * 4 + 255) / 256 * 256);
+    a.part = reinterpret_cast<uint64_t*>(ws + ((size_t)plan.n_tiles_all * 4 + 255) / 256 * 256);
     a.w_bytes = (uint32_t)((size_t)a.n_tiles * a.nb * kRecordBytes);
     return a;
 }
@@ -787,7 +823,7 @@ size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok) {
     const long long nb = in_dim / kQK;
     const long long tiles = (long long)((out_dim + kTileRows - 1) / kTileRows) * n_tensors;
     const size_t cnt = ((size_t)tiles * 4 + 255) / 256 * 256;
-    return cnt + (size_t)tiles * (size_t)nb * (size_t)n_tok * 64 * 4;
+    return cnt + (size_t)tiles * (size_t)nb * (size_t)n_tok * 64 * 8;
 }
 
 hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
@@ -830,7 +866,7 @@ size_t gate_up_ws_bytes(int in_dim, int out_dim) {
     const long long nb = in_dim / kQK;
     const long long tiles = (out_dim + kTileRows - 1) / kTileRows;
     const size_t cnt = ((size_t)(2 * tiles) * 4 + 255) / 256 * 256;
-    return cnt + (size_t)tiles * (size_t)(2 * nb) * 2 * 64 * 4;
+    return cnt + (size_t)tiles * (size_t)(2 * nb) * 2 * 64 * 8;
 }
 
 hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int in_dim, int out_dim,
