@@ -109,10 +109,6 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-// The T64 sign word with the four implied signs (element 7 of each group,
-// the parity of the other seven) written over the scale nibble. Group l's
-// bits are exactly the positions = l (mod 4), so three xor-folds give all
-// four parities at once, in bits 0..3.
 // SwiGLU with the reference's clamp (model_batch.cpp:245-253):
 // silu(min(g, lim)) * clamp(u, -lim, lim).
 __device__ __forceinline__ float swiglu1(float gv, float uv, float lim) {
@@ -121,6 +117,45 @@ __device__ __forceinline__ float swiglu1(float gv, float uv, float lim) {
     return (gi / (1.0f + expf(-gi))) * ui;
 }
 
+// Maximum of m over the wavefront's 64 lanes, returned in every lane: DPP
+// exchanges inside each row of 16 lanes (pairs, quads, half-row and row
+// mirrors), then the four row maxima read back with v_readlane — no LDS
+// round trip.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_max(float m) {
+    m = fmaxf(m, dpp_f32<0xB1>(m));   // quad_perm [1, 0, 3, 2]
+    m = fmaxf(m, dpp_f32<0x4E>(m));   // quad_perm [2, 3, 0, 1]
+    m = fmaxf(m, dpp_f32<0x141>(m));  // row_half_mirror
+    m = fmaxf(m, dpp_f32<0x140>(m));  // row_mirror
+    const int b = __builtin_bit_cast(int, m);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Power of two that brings a maximum magnitude m into [2^13, 2^14) (0 when
+// m is 0, infinite or NaN), clamped to +-120.
+__device__ __forceinline__ int pow2_scale_of_max(float m) {
+    int sc = 0;
+    if (m > 0.0f && m < __builtin_inff()) {
+        int ex;
+        (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
+        sc = 14 - ex;
+        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
+    }
+    return sc;
+}
+
+// The T64 sign word with the four implied signs (element 7 of each group,
+// the parity of the other seven) written over the scale nibble. Group l's
+// bits are exactly the positions = l (mod 4), so three xor-folds give all
+// four parities at once, in bits 0..3.
 __device__ __forceinline__ uint32_t t64_full_signs(uint32_t w) {
     const uint32_t m = w & 0x0FFFFFFFu;
     uint32_t t = m ^ (m >> 16);

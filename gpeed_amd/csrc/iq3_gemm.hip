@@ -80,18 +80,10 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
 #pragma unroll
         for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = wave_max(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int sc = 0;
-    if (mx > 0.0f && mx < __builtin_inff()) {
-        int ex;
-        (void)frexpf(mx, &ex);
-        sc = 14 - ex;
-        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
-    }
+    const int sc = pow2_scale_of_max(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
     const size_t plane = (size_t)M * K;
     for (int c = tid; c < n8; c += 256) {
         float v[8];

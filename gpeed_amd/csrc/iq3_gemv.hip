@@ -77,16 +77,8 @@ __global__ __launch_bounds__(256) void k_prep_act(const float* __restrict__ x,
             e[c] = (gi / (1.0f + expf(-gi))) * ui;
         }
     }
-    float m = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    int sc = 0;
-    if (m > 0.0f && m < __builtin_inff()) {
-        int ex;
-        (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
-        sc = 14 - ex;          // scaled max in [2^13, 2^14)
-        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
-    }
+    const int sc =
+        pow2_scale_of_max(wave_max(fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])))));
     _Float16 hi[4], lo[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -233,35 +225,7 @@ __device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g
 
 // Power of two that brings max|v| over the wavefront (m: this lane's max)
 // into [2^13, 2^14).
-__device__ __forceinline__ int pow2_scale(float m) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    int sc = 0;
-    if (m > 0.0f && m < __builtin_inff()) {
-        int ex;
-        (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
-        sc = 14 - ex;
-        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
-    }
-    return sc;
-}
-
-// Block scale of the wavefront's 256 values and the fp16 hi/lo split of
-// this lane's 4 values; returns the unscale.
-__device__ __forceinline__ float split_hi_lo(const float (&e)[4], u32x2_t& hi2, u32x2_t& lo2) {
-    const int sc =
-        pow2_scale(fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3]))));
-    _Float16 hi[4], lo[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const float xs = ldexpf(e[c], sc);
-        hi[c] = (_Float16)xs;
-        lo[c] = (_Float16)(xs - (float)hi[c]);
-    }
-    hi2 = __builtin_bit_cast(u32x2_t, hi);
-    lo2 = __builtin_bit_cast(u32x2_t, lo);
-    return ldexpf(1.0f, -sc);
-}
+__device__ __forceinline__ int pow2_scale(float m) { return pow2_scale_of_max(wave_max(m)); }
 
 // ---------------------------------------------------------------------------
 // GEMV workgroup building blocks. A workgroup owns records [c0, c1) of a
@@ -350,28 +314,50 @@ struct ActLoads {
     // images (prepared, or copied for MODE 3) into the wavefront's region
     template <int NT>
     __device__ void commit(GemvShared<NT, 1>& sh, const GemvArgs& g, const Chunk& ch, int wave, uint32_t lane) {
+        if constexpr (MODE == 3) {
 #pragma unroll
-        for (int k = 0; k < KP; ++k) {
-            if (k < ch.n_mine) {
-                uint8_t* region = sh.xsl + (wave * KP + k) * 1024;
-                if constexpr (MODE == 3) {
+            for (int k = 0; k < KP; ++k) {
+                if (k < ch.n_mine) {
+                    uint8_t* region = sh.xsl + (wave * KP + k) * 1024;
                     *reinterpret_cast<float4*>(region + lane * 16) = xv[k];  // act64 keeps its layout
                     if (lane == 0) *reinterpret_cast<float4*>(&sh.xscl[(wave * KP + k) * 4]) = sv[k];
-                } else {
-                    float e[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
-                    if constexpr (MODE == 2) {
-                        const float us[4] = {uv[k].x, uv[k].y, uv[k].z, uv[k].w};
+                }
+            }
+        } else {
+            // the block scales of all records first, unbranched (a record
+            // past the wavefront's share holds zeros), so their wavefront
+            // reductions overlap
+            float e[KP][4];
+            int sc[KP];
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) e[c] = swiglu1(e[c], us[c], g.lim);
+            for (int k = 0; k < KP; ++k) {
+                e[k][0] = xv[k].x;
+                e[k][1] = xv[k].y;
+                e[k][2] = xv[k].z;
+                e[k][3] = xv[k].w;
+                if constexpr (MODE == 2) {
+                    const float us[4] = {uv[k].x, uv[k].y, uv[k].z, uv[k].w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) e[k][c] = swiglu1(e[k][c], us[c], g.lim);
+                }
+                sc[k] = pow2_scale(fmaxf(fmaxf(fabsf(e[k][0]), fabsf(e[k][1])), fmaxf(fabsf(e[k][2]), fabsf(e[k][3]))));
+            }
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                if (k < ch.n_mine) {
+                    _Float16 hi[4], lo[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float xs = ldexpf(e[k][c], sc[k]);
+                        hi[c] = (_Float16)xs;
+                        lo[c] = (_Float16)(xs - (float)hi[c]);
                     }
-                    u32x2_t hi, lo;
-                    const float unscale = split_hi_lo(e, hi, lo);
                     // lane 4*beta+rho of register a holds variant rho (0 hi,
                     // 1 lo) of slice beta at a*256 + (2*beta+rho)*8
-                    uint8_t* dst = region + (lane >> 4) * 256 + (lane & 15) * 16;
-                    *reinterpret_cast<u32x2_t*>(dst) = hi;
-                    *reinterpret_cast<u32x2_t*>(dst + 8) = lo;
-                    if (lane == 0) sh.xscl[(wave * KP + k) * 4] = unscale;
+                    uint8_t* dst = sh.xsl + (wave * KP + k) * 1024 + (lane >> 4) * 256 + (lane & 15) * 16;
+                    *reinterpret_cast<u32x2_t*>(dst) = __builtin_bit_cast(u32x2_t, hi);
+                    *reinterpret_cast<u32x2_t*>(dst + 8) = __builtin_bit_cast(u32x2_t, lo);
+                    if (lane == 0) sh.xscl[(wave * KP + k) * 4] = ldexpf(1.0f, -sc[k]);
                 }
             }
         }
@@ -641,10 +627,10 @@ __device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const
     }
 }
 
-// y (per tensor) or, EPI 1, act64 images: prologue (grid table, the
-// wavefronts' activation loads, one workgroup barrier with no memory wait
-// before it, first ring slot, the wavefront's own activation images, the
-// other slots), the record stream, the epilogue.
+// y (per tensor) or, EPI 1, act64 images: prologue (the wavefronts'
+// activation loads, a workgroup barrier with no memory wait, the first ring
+// slot, the grid table, the wavefront's own activation images, the other
+// slots), the record stream, the epilogue.
 template <int NT, int MODE, int EPI>
 __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs g) {
     static_assert(MODE == 0 || NT == 1, "prepared-in-kernel and act64 activations take one vector");
@@ -658,18 +644,21 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lane = tid & 63;
-    gemv_lds_init<NT, MODE>(sh, wave, lane, tid);
     const Chunk ch(g, blockIdx.x, wave, W);
     ActLoads<MODE, KP, W> act;
     if constexpr (kPrep) act.issue(g, ch, wave, lane);
-    // the table is complete, and (a CU serves its vector memory queue in
-    // order) every wavefront's activation loads are queued ahead of all
-    // record loads
-    lds_barrier();
+    // (a CU serves its vector memory queue in order) every wavefront's
+    // activation loads are queued ahead of all record loads
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     const OnePhase<NT, MODE, EPI> src{g, ch, wave};
     Rec<(NT + 1) / 2> ring[PF];
     src.load(ring[0], 0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    // the LDS set-up runs while the first loads are in flight
+    gemv_lds_init<NT, MODE>(sh, wave, lane, tid);
+    lds_barrier();
     if constexpr (kPrep) act.commit(sh, g, ch, wave, lane);
 #pragma unroll
     for (int s = 1; s < PF; ++s) src.load(ring[s], s, lane);

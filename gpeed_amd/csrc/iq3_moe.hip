@@ -297,16 +297,8 @@ __global__ __launch_bounds__(256) void k_prep_grouped(const float* __restrict__ 
             e[c] = (gi / (1.0f + expf(-gi))) * ui;
         }
     }
-    float m = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    int sc = 0;
-    if (m > 0.0f && m < __builtin_inff()) {
-        int ex;
-        (void)frexpf(m, &ex);
-        sc = 14 - ex;
-        sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
-    }
+    const int sc =
+        pow2_scale_of_max(wave_max(fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])))));
     _Float16 hi[4], lo[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
