@@ -15,6 +15,7 @@
 // k_moe_combine  Y[t] = sum over the token's slots, in expert order, of
 //                wt * down row (one fma per term, like axpy_f32).
 #include <climits>
+#include <type_traits>
 
 #include "iq3_common.h"
 #include "iq3_gemv_core.h"
@@ -38,6 +39,39 @@ __device__ __forceinline__ bool ranks_before(float ka, int a, float kb, int b) {
     return ka > kb || (ka == kb && a < b);
 }
 
+// The same order as one unsigned 64-bit number (larger ranks first): the
+// key's bits made monotonic (non-NaN keys, -0 taken as +0), then the
+// complemented id. 0 ranks after every candidate.
+__device__ __forceinline__ uint64_t rank_word(float key, int id) {
+    uint32_t u = __builtin_bit_cast(uint32_t, key + 0.0f);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)~id;
+}
+
+// Largest rank word over the wavefront, in every lane: DPP exchanges
+// inside rows of 16 lanes, then the four row winners read back.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    auto step = [&](auto ctrl) {
+        constexpr int c = decltype(ctrl)::value;
+        const uint32_t hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), c, 0xF, 0xF, false);
+        const uint32_t lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, c, 0xF, 0xF, false);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    };
+    step(std::integral_constant<int, 0xB1>{});   // quad_perm [1, 0, 3, 2]
+    step(std::integral_constant<int, 0x4E>{});   // quad_perm [2, 3, 0, 1]
+    step(std::integral_constant<int, 0x141>{});  // row_half_mirror
+    step(std::integral_constant<int, 0x140>{});  // row_mirror
+    uint64_t best = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint64_t w = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), 16 * r) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
+        best = w > best ? w : best;
+    }
+    return best;
+}
+
 // Exclusive scan of v[0..n) in LDS into out (n <= 1024, 1024 threads);
 // returns the total. tmp: 1024 ints of scratch.
 __device__ __forceinline__ int block_exclusive_scan(const int* v, int* out, int* tmp, int n) {
@@ -56,8 +90,14 @@ __device__ __forceinline__ int block_exclusive_scan(const int* v, int* out, int*
     return total;
 }
 
+// Assignments (token, k) kept in LDS when there are at most this many: the
+// top-k loop then issues no global store (on gfx9 a wavefront's next global
+// load would wait for its stores).
+constexpr int kRouteLdsAsg = 2048;
+
 // J = register slots per lane: expert e lives in lane e % 64, slot e / 64.
-template <int J>
+// kLds: T * K <= kRouteLdsAsg, the assignments stay in LDS.
+template <int J, bool kLds>
 __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ logits, int T, int E, int K,
                                                     int mode, const float* __restrict__ bias,
                                                     float routed_scale, int norm_topk, int* __restrict__ eptr,
@@ -66,26 +106,52 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ lo
                                                     float* __restrict__ asg_w) {
     __shared__ int cnt[kMaxExperts];
     __shared__ int cursor[kMaxExperts];
-    __shared__ int chunk_e[1024];
+    __shared__ __attribute__((aligned(16))) int chunk_e[1024];
     __shared__ float rank_score[16][kMaxTopK];
+    __shared__ int lds_e[kLds ? kRouteLdsAsg : 1];
+    __shared__ float lds_w[kLds ? kRouteLdsAsg : 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    auto put_e = [&](size_t i, int v) {
+        if constexpr (kLds) lds_e[i] = v;
+        else asg_e[i] = v;
+    };
+    auto put_w = [&](size_t i, float v) {
+        if constexpr (kLds) lds_w[i] = v;
+        else asg_w[i] = v;
+    };
     for (int e = tid; e < E; e += 1024) cnt[e] = 0;
     __syncthreads();
 
-    // 1. top-k per token (one wavefront per token); lane l holds experts l + 64j
-    for (int t = wave; t < T; t += 16) {
-        float key[J], sc[J];
-        unsigned taken = 0;
+    // 1. top-k per token (one wavefront per token); lane l holds experts
+    // l + 64j. The next token's logits are loaded while this one is ranked.
+    float nxt[J];
+    auto load_logits = [&](int t) {
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int e = lane + 64 * j;
+            nxt[j] = (t < T && e < E) ? logits[(size_t)t * E + e] : 0.0f;
+        }
+    };
+    load_logits(wave);
+    float bias_j[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int e = lane + 64 * j;
+        bias_j[j] = (mode == 0 && bias && e < E) ? bias[e] : 0.0f;
+    }
+    for (int t = wave; t < T; t += 16) {
+        float key[J], sc[J];
+        uint64_t rw[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int e = lane + 64 * j;
+            const float l = nxt[j];
             key[j] = -__builtin_inff();
             sc[j] = 0.0f;
             if (e < E) {
-                const float l = logits[(size_t)t * E + e];
                 if (mode == 0) {
                     sc[j] = 1.0f / (1.0f + expf(-l));
-                    key[j] = sc[j] + (bias ? bias[e] : 0.0f);
+                    key[j] = sc[j] + bias_j[j];
                 } else {
                     sc[j] = l;
                     key[j] = l;
@@ -93,54 +159,73 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ lo
                 // a NaN key ranks last (it still ranks, so every pick is an expert)
                 if (__builtin_isnan(key[j])) key[j] = -__builtin_inff();
             }
+            rw[j] = e < E ? rank_word(key[j], e) : 0;
         }
-        for (int k = 0; k < K; ++k) {
-            float bk = -__builtin_inff(), bs = 0.0f;
-            int be = INT_MAX;
+        load_logits(t + 16);
+        if constexpr (J == 1) {
+            // rank of this lane's expert among all: one comparison per expert
+            int rank = 0;
+            for (int l2 = 0; l2 < E; ++l2) {  // uniform
+                const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(rw[0] >> 32), l2) << 32) |
+                                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)rw[0], l2);
+                rank += o > rw[0];
+            }
+            if (lane < E && rank < K) {
+                rank_score[wave][rank] = sc[0];
+                put_e((size_t)t * K + rank, lane);
+                if (!kLds && sel) sel[(size_t)t * K + rank] = lane;
+                atomicAdd(&cnt[lane], 1);
+            }
+        } else {
+            // K rounds: this lane's best remaining expert, then the wavefront's
+            unsigned taken = 0;
+            for (int k = 0; k < K; ++k) {
+                uint64_t mine = 0;
 #pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const int e = lane + 64 * j;
-                if (e < E && !((taken >> j) & 1u) && ranks_before(key[j], e, bk, be)) {
-                    bk = key[j];
-                    be = e;
-                    bs = sc[j];
+                for (int j = 0; j < J; ++j) {
+                    const uint64_t c = ((taken >> j) & 1u) ? 0 : rw[j];
+                    mine = c > mine ? c : mine;
+                }
+                const int be = (int)~(uint32_t)wave_max_u64(mine);  // uniform
+                float bs = 0.0f;
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                    if ((be >> 6) == j)
+                        bs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc[j]), be & 63));
+                if ((be & 63) == lane) taken |= 1u << (be >> 6);
+                if (lane == 0) {
+                    rank_score[wave][k] = bs;
+                    put_e((size_t)t * K + k, be);
+                    if (!kLds && sel) sel[(size_t)t * K + k] = be;
+                    atomicAdd(&cnt[be], 1);
                 }
             }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ok = __shfl_xor(bk, off);
-                const int oe = __shfl_xor(be, off);
-                const float os = __shfl_xor(bs, off);
-                if (ranks_before(ok, oe, bk, be)) {
-                    bk = ok;
-                    be = oe;
-                    bs = os;
-                }
-            }
-            if ((be & 63) == lane) taken |= 1u << (be >> 6);
-            if (lane == 0) {
-                rank_score[wave][k] = bs;
-                asg_e[(size_t)t * K + k] = be;
-                if (sel) sel[(size_t)t * K + k] = be;
-                atomicAdd(&cnt[be], 1);
-            }
         }
-        if (lane == 0) {
-            // combine weights, summed in rank order (model_batch.cpp:195-200)
+        // combine weights (model_batch.cpp:195-200): lane k < K takes rank
+        // k; the denominator is summed in rank order. LDS writes of one
+        // wavefront complete in order, so the ranks' scores are in place.
+        const float s_k = lane < K ? rank_score[wave][lane] : 0.0f;
+        float num = s_k;
+        if (mode != 0) num = lane < K ? expf(s_k - rank_score[wave][0]) : 0.0f;
+        float denom = mode == 0 ? 1e-20f : 0.0f;
+        for (int k = 0; k < K; ++k)  // uniform
+            denom += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, num), k));
+        if (lane < K) {
+            float w;
             if (mode == 0) {
-                float denom = 1e-20f;
-                for (int k = 0; k < K; ++k) denom += rank_score[wave][k];
                 const float inv = norm_topk ? routed_scale / denom : routed_scale;
-                for (int k = 0; k < K; ++k) asg_w[(size_t)t * K + k] = rank_score[wave][k] * inv;
+                w = s_k * inv;
             } else {
-                const float lmax = rank_score[wave][0];
-                float denom = 0.0f;
-                for (int k = 0; k < K; ++k) denom += expf(rank_score[wave][k] - lmax);
-                for (int k = 0; k < K; ++k) asg_w[(size_t)t * K + k] = expf(rank_score[wave][k] - lmax) / denom;
+                w = num / denom;
             }
+            put_w((size_t)t * K + lane, w);
         }
     }
     __syncthreads();
+    if constexpr (kLds) {
+        if (sel)
+            for (int i = tid; i < T * K; i += 1024) sel[i] = lds_e[i];
+    }
 
     // 2. exclusive scan of the expert counts (model_batch.cpp:205-209)
     {
@@ -156,15 +241,23 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ lo
     const int N = T * K;
     for (int c0 = 0; c0 < N; c0 += 1024) {
         const int a = c0 + tid;
-        const int ea = a < N ? asg_e[a] : -1;
+        const int ea = a < N ? (kLds ? lds_e[a] : asg_e[a]) : -1;
         chunk_e[tid] = ea;
         __syncthreads();
         if (a < N) {
+            // earlier assignments of the same expert in this chunk, four per
+            // LDS read
             int rank = 0;
-            for (int j = 0; j < tid; ++j) rank += chunk_e[j] == ea;
+            const int4* ce4 = reinterpret_cast<const int4*>(chunk_e);
+#pragma unroll 4
+            for (int j = 0; j < (tid >> 2); ++j) {
+                const int4 v = ce4[j];
+                rank += (v.x == ea) + (v.y == ea) + (v.z == ea) + (v.w == ea);
+            }
+            for (int j = tid & ~3; j < tid; ++j) rank += chunk_e[j] == ea;
             const int p = cursor[ea] + rank;
             tok[p] = a / K;
-            wt[p] = asg_w[a];
+            wt[p] = kLds ? lds_w[a] : asg_w[a];
         }
         __syncthreads();
         if (a < N) atomicAdd(&cursor[ea], 1);
@@ -494,10 +587,11 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int K, int mode, 
         hipLaunchKernelGGL(kern, dim3(1), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale, norm_topk,
                            eptr, tok, wt, sel, asg_e, asg_w);
     };
-    if (E <= 64) go(k_moe_route<1>);
-    else if (E <= 128) go(k_moe_route<2>);
-    else if (E <= 256) go(k_moe_route<4>);
-    else go(k_moe_route<kMaxExperts / 64>);
+    const bool lds = (long long)T * K <= kRouteLdsAsg;
+    if (E <= 64) lds ? go(k_moe_route<1, true>) : go(k_moe_route<1, false>);
+    else if (E <= 128) lds ? go(k_moe_route<2, true>) : go(k_moe_route<2, false>);
+    else if (E <= 256) lds ? go(k_moe_route<4, true>) : go(k_moe_route<4, false>);
+    else lds ? go(k_moe_route<kMaxExperts / 64, true>) : go(k_moe_route<kMaxExperts / 64, false>);
     return hipGetLastError();
 }
 
