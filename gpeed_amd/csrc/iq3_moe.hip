@@ -3,15 +3,17 @@
 // k_moe_route    router top-k per token, expert histogram, exclusive scan and
 //                a stable scatter of the (token, k) assignments into expert
 //                buckets: eptr / tok / wt exactly as the CPU builds them.
-// k_moe_plan     expert buckets -> work segments of at most 8 tokens, the
-//                segment of every bucket slot, each token's slots in expert
-//                order; zeroes the work counters.
+// k_moe_plan     expert buckets -> work segments of at most 8 tokens
+//                (numbered heaviest first), the segment of every bucket
+//                slot, each token's slots in expert order; zeroes the work
+//                counters.
 // k_prep_grouped gathers each slot's activation (MODE 0: X[tok], MODE 1:
 //                SwiGLU of the gate/up rows) into its segment's prepared
 //                activation.
 // k_gemv_grouped ragged grouped GEMV: a wavefront takes (segment, tensor,
-//                tile) items from an atomic counter and streams the tile's
-//                records over the whole row (no partial sums leave it).
+//                tile) items (its first by its index, the others from an
+//                atomic counter) and streams the tile's records over the
+//                whole row (no partial sums leave it).
 // k_moe_combine  Y[t] = sum over the token's slots, in expert order, of
 //                wt * down row (one fma per term, like axpy_f32).
 #include <climits>
@@ -282,34 +284,57 @@ struct MoePlan {
 __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr, const int* __restrict__ tok,
                                                    int T, int E, int K, MoePlan pl) {
     __shared__ int ep[kMaxExperts + 1];
-    __shared__ int sstart[kMaxExperts + 1];
-    __shared__ int nseg[kMaxExperts];
+    __shared__ int fstart[kMaxExperts + 1];
+    __shared__ int nfull[kMaxExperts];
+    __shared__ int pid[kMaxExperts];
+    __shared__ int ccount[kSegTok], ccursor[kSegTok];
     __shared__ int tmp[1024];
     __shared__ int tcnt[kPlanMaxTok];
     const int tid = threadIdx.x;
     for (int e = tid; e <= E; e += 1024) ep[e] = eptr[e];
     for (int t = tid; t < T; t += 1024) tcnt[t] = 0;
+    if (tid < kSegTok) ccount[tid] = 0;
     __syncthreads();
-    for (int e = tid; e < E; e += 1024) nseg[e] = (ep[e + 1] - ep[e] + kSegTok - 1) / kSegTok;
+    // Segments are numbered heaviest first (the grouped GEMVs hand them out
+    // in that order, so the last items left are the light ones): every
+    // expert's full segments of kSegTok tokens in expert order, then the
+    // experts' last partial segments by size, kSegTok-1 tokens down to 1.
+    for (int e = tid; e < E; e += 1024) {
+        const int g = ep[e + 1] - ep[e];
+        nfull[e] = g / kSegTok;
+        if (g % kSegTok) atomicAdd(&ccount[g % kSegTok], 1);
+    }
     __syncthreads();
-    const int n_seg = block_exclusive_scan(nseg, sstart, tmp, E);
+    const int n_full = block_exclusive_scan(nfull, fstart, tmp, E);
     if (tid == 0) {
-        sstart[E] = n_seg;
-        *pl.n_seg = n_seg;
+        int base = n_full;
+        for (int c = kSegTok - 1; c >= 1; --c) {
+            ccursor[c] = base;
+            base += ccount[c];
+        }
+        *pl.n_seg = base;
         // the grouped GEMVs take work from these with device-scope atomics
         __hip_atomic_store(pl.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(pl.ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     for (int e = tid; e < E; e += 1024) {
-        const int g = ep[e + 1] - ep[e];
-        for (int j = 0; j * kSegTok < g; ++j) {
-            const int s = sstart[e] + j;
-            pl.seg_e[s] = e;
-            pl.seg_p0[s] = ep[e] + j * kSegTok;
-            pl.seg_n[s] = min(kSegTok, g - j * kSegTok);
+        const int g = ep[e + 1] - ep[e], c = g % kSegTok;
+        // order among equal-size partial segments is free: no result depends on it
+        pid[e] = c ? atomicAdd(&ccursor[c], 1) : -1;
+        for (int j = 0; j < nfull[e]; ++j) {
+            const int sg = fstart[e] + j;
+            pl.seg_e[sg] = e;
+            pl.seg_p0[sg] = ep[e] + j * kSegTok;
+            pl.seg_n[sg] = kSegTok;
+        }
+        if (c) {
+            pl.seg_e[pid[e]] = e;
+            pl.seg_p0[pid[e]] = ep[e] + nfull[e] * kSegTok;
+            pl.seg_n[pid[e]] = c;
         }
     }
+    __syncthreads();
     const int N = ep[E];
     for (int p = tid; p < N; p += 1024) {
         int lo = 0, hi = E;  // largest e with ep[e] <= p
@@ -318,8 +343,8 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
             if (ep[mid] <= p) lo = mid; else hi = mid;
         }
         while (lo < E - 1 && ep[lo + 1] <= p) ++lo;  // skip empty buckets
-        const int r = p - ep[lo];
-        pl.seg_of[p] = sstart[lo] + r / kSegTok;
+        const int r = p - ep[lo], j = r / kSegTok;
+        pl.seg_of[p] = j < nfull[lo] ? fstart[lo] + j : pid[lo];
         pl.idx_of[p] = r % kSegTok;
     }
     // each token's slots in bucket order = expert order: every slot appends
@@ -484,11 +509,13 @@ __global__ __launch_bounds__(kGroupedThreads, 2) void k_gemv_grouped(GroupedArgs
     lds_barrier();
     const int per_seg = g.n_tensors * g.tiles;
     const int n_items = *g.pl.n_seg * per_seg;
+    // the first round is static (wavefront i takes item i), the rest come
+    // from the counter: 2048 wavefronts taking tickets on one address at
+    // once serialise for tens of microseconds
+    constexpr int kWavesPerGroup = kGroupedThreads / 64;
+    const uint32_t n_waves = gridDim.x * kWavesPerGroup;
+    uint32_t item = blockIdx.x * kWavesPerGroup + (tid >> 6);
     while (true) {
-        uint32_t item = 0;
-        if (lane == 0)
-            item = __hip_atomic_fetch_add(g.pl.ctr + g.ctr_index, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        item = __builtin_amdgcn_readfirstlane(__shfl(item, 0));
         if (item >= (uint32_t)n_items) break;
         const int s = item / per_seg;
         const int rem = item - s * per_seg;
@@ -503,6 +530,9 @@ __global__ __launch_bounds__(kGroupedThreads, 2) void k_gemv_grouped(GroupedArgs
             case 3: grouped_tile<3>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
             default: grouped_tile<4>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
         }
+        uint32_t t = 0;
+        if (lane == 0) t = __hip_atomic_fetch_add(g.pl.ctr + g.ctr_index, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        item = n_waves + __builtin_amdgcn_readfirstlane(__shfl(t, 0));
     }
 }
 
