@@ -15,8 +15,9 @@ value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
 roofline = the GEMV kernel (k_gemv_t64: the gate+up launch and the down
 launch of a step): algorithmic bytes of the pair (packed W + fp32 x + the
 SwiGLU activation written and read + y) / the pair's duration, timed with
-HIP events on the launch stream around replays of a HIP graph of all copies
-in turn (no host gaps; still HBM-bound).
+HIP events on the launch stream around back-to-back steps of all copies in
+turn, as C-ABI calls or as replays of a HIP graph, whichever is faster (no
+host gaps either way; still HBM-bound).
 cpu_baseline = the reference's own CPU path (oracle/_ref: WeightStore::
 matvec_quant compiled from the reference sources, single-threaded as the
 reference builds on Linux) on one full step of the same workload; the
@@ -316,6 +317,21 @@ def main():
         tg, tu, td = copies[c]
         G.dense_mlp(tg, tu, td, H, I, xd, SWIGLU_LIMIT, out=y, ws=ws_mlp)
 
+    # The timed loops call the C ABI with argument tuples built beforehand:
+    # a call then costs the host a few microseconds, well under the GPU's
+    # step, so the launches queue back to back (the Python wrapper's checks
+    # would leave the GPU waiting for the host).
+    import ctypes
+    fn_mlp = G.lib().gpeed_iq3xxs_dense_mlp
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    call_args = [(vp(tg), vp(tu), vp(td), H, I, vp(xd), ctypes.c_float(SWIGLU_LIMIT), vp(y), vp(ws_mlp),
+                  ws_mlp.numel(), cur) for tg, tu, td in copies]
+
+    def step_fast(c):
+        if fn_mlp(*call_args[c]) != 0:
+            raise RuntimeError(f"dense_mlp: {G.lib().gpeed_last_error().decode(errors='replace')}")
+
     if args.traffic_probe:
         src = torch.ones(64 << 20, device=dev)  # 256 MiB fp32
         dst = torch.empty_like(src)
@@ -341,7 +357,7 @@ def main():
     torch.cuda.synchronize()
     t0.record()
     for i in range(args.steps):
-        step(i % args.copies)
+        step_fast(i % args.copies)
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
@@ -355,9 +371,18 @@ def main():
     log("kernel timing")
 
     def time_per_step(fn):
-        """ms per step: HIP graph replays of all copies in turn where the launches
-        can be captured (no host gaps), else back-to-back eager steps."""
+        """ms per step: the faster of HIP graph replays of all copies in turn
+        and back-to-back eager steps (graph kernel nodes carry their own
+        per-node cost on this stack; neither leaves host gaps)."""
         reps = max(4, args.steps // args.copies)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps * args.copies):
+            step_fast(i % args.copies)
+        e1.record()
+        torch.cuda.synchronize()
+        eager_ms = e0.elapsed_time(e1) / (reps * args.copies)
         try:
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
@@ -376,17 +401,11 @@ def main():
                 graph.replay()
             e1.record()
             torch.cuda.synchronize()
-            return e0.elapsed_time(e1) / (reps * args.copies), "graph"
+            graph_ms = e0.elapsed_time(e1) / (reps * args.copies)
         except Exception as exc:  # capture unsupported for this launch
             log(f"graph capture unavailable ({type(exc).__name__}): eager timing")
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for i in range(reps * args.copies):
-                fn(i % args.copies)
-            e1.record()
-            torch.cuda.synchronize()
-            return e0.elapsed_time(e1) / (reps * args.copies), "eager"
+            return eager_ms, "eager"
+        return (graph_ms, "graph") if graph_ms < eager_ms else (eager_ms, "eager")
 
     pair_ms, pair_timing = time_per_step(step)
     # dispatch-stamped events split the pair per kind (they add a little each)
