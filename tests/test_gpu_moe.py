@@ -60,6 +60,21 @@ def test_route_ties_lower_id_first(gpu):
     assert host(sel).tolist() == [[0, 1, 2, 3], [5, 0, 1, 2], [0, 1, 2, 3]]
 
 
+@pytest.mark.parametrize("E", [16, 100])  # one rank slot per lane, and two (E > 64)
+def test_route_signed_zero_ties(gpu, E):
+    # -0.0 and +0.0 compare equal (model_batch.cpp ranks with float >): ties
+    # go to the lower id whichever zero a logit holds
+    logits = np.zeros((3, E), np.float32)
+    logits[0, 0] = -0.0
+    logits[1, 1] = -0.0
+    logits[1, E - 1] = 0.5
+    logits[2, :] = -0.0
+    logits[2, 70 % E] = 0.0
+    eptr, tok, wt, sel = G.moe_route(dev(logits, gpu), 4, 1)
+    r_sel = oracle.moe_route(logits, 4, 1)[3]
+    assert host(sel).tolist() == r_sel.tolist() == [[0, 1, 2, 3], [E - 1, 0, 1, 2], [0, 1, 2, 3]]
+
+
 def experts_case(gpu, seed, T, E, K, H, I, mode=1):
     wg = synth.iq3xxs_matrix(seed, 0, E * I, H)
     wu = synth.iq3xxs_matrix(seed, 1, E * I, H)
