@@ -139,6 +139,18 @@ __device__ __forceinline__ float wave_max(float m) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// v << N as one v_lshlrev_b64 (the compiler splits a constant 64-bit shift
+// into two 32-bit ones). The amount reaches it through an SGPR, so the shift
+// stays an ordinary instruction that the compiler schedules and checks for
+// hazards (a shift written as inline assembly is invisible to its MFMA
+// read-after-write and write-after-read checks).
+template <int N>
+__device__ __forceinline__ uint64_t shl64(uint64_t v) {
+    int sh;
+    asm("s_mov_b32 %0, %1" : "=s"(sh) : "n"(N));
+    return v << sh;
+}
+
 // Power of two that brings a maximum magnitude m into [2^13, 2^14) (0 when
 // m is 0, infinite or NaN), clamped to +-120.
 __device__ __forceinline__ int pow2_scale_of_max(float m) {

@@ -497,9 +497,7 @@ __device__ __forceinline__ half8_t decode_group(const uint8_t* tbl, uint32_t q, 
     // pairs 0/1 and 2/3: one 64-bit shift of {wg >> 4, wg} each puts a
     // pair's two signs on bits 15 and 31 of both halves
     const uint64_t sw2 = ((uint64_t)(wg >> 4) << 32) | wg;
-    uint64_t r01, r23;
-    asm("v_lshlrev_b64 %0, 15, %1" : "=v"(r01) : "v"(sw2));
-    asm("v_lshlrev_b64 %0, 7, %1" : "=v"(r23) : "v"(sw2));
+    const uint64_t r01 = shl64<15>(sw2), r23 = shl64<7>(sw2);
     const uint32_t sr = ((w >> 24) & 0xF0u) | rs;  // (s << 4) | replica
     const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, sr, sel0));
     const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, sr, sel1));

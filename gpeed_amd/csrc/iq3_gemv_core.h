@@ -174,9 +174,7 @@ __device__ __forceinline__ void subblock_dot(uint32_t w, const u32x2_t (&g)[8], 
     static_for<0, 8>([&](auto mc) {
         constexpr int m = decltype(mc)::value;
         constexpr int a0 = 8 * (m & 1) + (m >> 1);  // first pair's sign bits: a0, a0 + 16
-        // one v_lshlrev_b64 (the compiler would split a C shift into two)
-        uint64_t rs;
-        asm("v_lshlrev_b64 %0, %1, %2" : "=v"(rs) : "n"(15 - a0), "v"(sw2));
+        const uint64_t rs = shl64<15 - a0>(sw2);
         const uint32_t bx = ((uint32_t)rs & 0x80008000u) | g[m].x;
         const uint32_t by = ((uint32_t)(rs >> 32) & 0x80008000u) | g[m].y;
         const half4_t B = __builtin_bit_cast(half4_t, u32x2_t{bx, by});
