@@ -248,13 +248,19 @@ def decode_mix(torch, G, synth, dev, reps, copies=4):
             sets.append({n: t.clone() for n, t in sets[0].items()})
     X = torch.from_numpy(synth.normal(2027, 10, M * HM).reshape(M, HM)).to(dev)
     out = {n: torch.empty(M, r, device=dev) for n, r, _ in shapes}
-    ws = {n: torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, k, r, G.X_F32), dtype=torch.uint8, device=dev)
-          for n, r, k in shapes}
+    # kv_a + q_a and gate + up share X: one two-tensor GEMM each (X prepared
+    # once, both tensors' result tiles in one grid), then the down GEMM
+    ws = {"lat": G.lib().gpeed_iq3xxs_gemm2_ws_bytes(M, HM, 576, 1536, G.X_F32),
+          "ffn": G.lib().gpeed_iq3xxs_gemm2_ws_bytes(M, HM, 12288, 12288, G.X_F32),
+          "down": G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, 12288, HM, G.X_F32)}
+    ws = {n: torch.zeros(b, dtype=torch.uint8, device=dev) for n, b in ws.items()}
 
     def step(c):
         W = sets[c % copies]
-        for n, r, k in shapes[:4]:
-            G.gemm(W[n], r, 0, k, r, X, out=out[n], ws=ws[n])
+        G.gemm2(W["kv_a"], 576, 0, 576, W["q_a"], 1536, 0, 1536, HM, X, out_a_t=out["kv_a"], out_b_t=out["q_a"],
+                ws=ws["lat"])
+        G.gemm2(W["gate"], 12288, 0, 12288, W["up"], 12288, 0, 12288, HM, X, out_a_t=out["gate"],
+                out_b_t=out["up"], ws=ws["ffn"])
         G.gemm_swiglu(W["down"], HM, 0, 12288, HM, out["gate"], out["up"], SWIGLU_LIMIT, out=out["down"],
                       ws=ws["down"])
 
@@ -266,8 +272,10 @@ def decode_mix(torch, G, synth, dev, reps, copies=4):
     calls = []
     for c in range(copies):
         W = sets[c]
-        cl = [(L.gpeed_iq3xxs_gemm, (vp(W[n]), r, 0, k, r, vp(X), G.X_F32, M, vp(out[n]), vp(ws[n]), ws[n].numel(),
-                                     cur)) for n, r, k in shapes[:4]]
+        cl = []
+        for (a, ra), (b, rb), w_name in ((("kv_a", 576), ("q_a", 1536), "lat"), (("gate", 12288), ("up", 12288), "ffn")):
+            cl.append((L.gpeed_iq3xxs_gemm2, (vp(W[a]), ra, 0, ra, vp(W[b]), rb, 0, rb, HM, vp(X), G.X_F32, M,
+                                              vp(out[a]), vp(out[b]), vp(ws[w_name]), ws[w_name].numel(), cur)))
         cl.append((L.gpeed_iq3xxs_gemm_swiglu, (vp(W["down"]), HM, 0, 12288, HM, vp(out["gate"]), vp(out["up"]),
                                                 ctypes.c_float(SWIGLU_LIMIT), M, vp(out["down"]), vp(ws["down"]),
                                                 ws["down"].numel(), cur)))
@@ -292,7 +300,7 @@ def decode_mix(torch, G, synth, dev, reps, copies=4):
     ms = a.elapsed_time(b) / reps
     # GEMM kernel durations from dispatch-stamped launches, in a loop of their
     # own (the stamps add to the step)
-    G.prof_start(5 * reps + 8)
+    G.prof_start(3 * reps + 8)
     for c in range(reps):
         step_fast(c)
     torch.cuda.synchronize()
@@ -301,7 +309,8 @@ def decode_mix(torch, G, synth, dev, reps, copies=4):
     flops = sum(2.0 * M * r * k for _, r, k in shapes)
     return {"workload": "continuous-batching decode mix: 64 tokens, fp32 X [64,6144], IQ3_XXS kv_a 576x6144, "
                         "q_a 1536x6144, shared expert gate/up 12288x6144 and down 6144x12288 (SwiGLU in the "
-                        "down GEMM); five GEMMs with K split over workgroups",
+                        "down GEMM); kv_a+q_a and gate+up as two-tensor GEMMs on the shared X, K split over "
+                        "workgroups",
             "packed_bytes_per_step": w_bytes, "gflop_per_step": round(flops / 1e9, 2),
             "ms_per_step": round(ms, 4), "kernel_ms_per_step": round(k_ms, 4),
             "GBps": round(w_bytes / (ms * 1e-3) / 1e9, 1),

@@ -84,6 +84,9 @@ def lib():
             "gpeed_iq3xxs_gemm_ws_bytes": ([i64, i64, i64, i32], sz),
             "gpeed_iq3xxs_gemm_swiglu": ([vp, u64, u64, i32, i32, vp, vp, C.c_float, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemm": ([vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_gemm2_ws_bytes": ([i64, i64, i64, i64, i32], sz),
+            "gpeed_iq3xxs_gemm2": ([vp, u64, u64, i32, vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, vp, sz, vp],
+                                   i32),
             "gpeed_prof_start": ([i32], i32),
             "gpeed_prof_read": ([i32, vp, i32, vp], i32),
             "gpeed_moe_route_ws_bytes": ([i32, i32, i32], sz),
@@ -268,6 +271,27 @@ def gemm(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None, 
     _check(lib().gpeed_iq3xxs_gemm(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(X), xd, n_tok, _ptr(out),
                                    _ptr(ws), ws.numel(), _stream(stream)), "gemm")
     return out
+
+
+def gemm2(w_a, n_rows_a: int, row0_a: int, out_a: int, w_b, n_rows_b: int, row0_b: int, out_b: int, in_dim: int, X,
+          out_a_t=None, out_b_t=None, ws=None, stream=None):
+    """Two prefill GEMMs on one X in one launch: (Y_a [n_tok, out_a], Y_b [n_tok, out_b])."""
+    torch = _torch()
+    _require_cuda(w_a, w_b, X)
+    n_tok = X.shape[0]
+    xd = X_BF16 if X.dtype == torch.bfloat16 else X_F32
+    if xd == X_F32 and X.dtype != torch.float32:
+        raise ValueError("gemm2: X must be float32 or bfloat16")
+    if out_a_t is None:
+        out_a_t = torch.empty(n_tok, out_a, dtype=torch.float32, device=X.device)
+    if out_b_t is None:
+        out_b_t = torch.empty(n_tok, out_b, dtype=torch.float32, device=X.device)
+    if ws is None:
+        ws = _zeros(lib().gpeed_iq3xxs_gemm2_ws_bytes(n_tok, in_dim, out_a, out_b, xd), X.device)
+    _check(lib().gpeed_iq3xxs_gemm2(_ptr(w_a), n_rows_a, row0_a, out_a, _ptr(w_b), n_rows_b, row0_b, out_b, in_dim,
+                                    _ptr(X), xd, n_tok, _ptr(out_a_t), _ptr(out_b_t), _ptr(ws), ws.numel(),
+                                    _stream(stream)), "gemm2")
+    return out_a_t, out_b_t
 
 
 def gemm_swiglu(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, G, U, limit: float = 10.0, out=None,

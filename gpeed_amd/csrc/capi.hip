@@ -585,6 +585,48 @@ int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm launch");
 }
 
+size_t gpeed_iq3xxs_gemm2_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_a, int64_t out_b, int x_dtype) {
+    if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(in_dim) || out_a < 0 || out_b < 0 || out_a + out_b < 1 ||
+        out_a > (1 << 24) || out_b > (1 << 24) || (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16))
+        return 0;
+    const DeviceState* st = nullptr;
+    if (device_state(&st)) return 0;
+    return gpeed::gemm2_ws_bytes((int)n_tok, (int)out_a, (int)out_b, (int)in_dim, x_dtype == GPEED_X_BF16,
+                                 st->num_cus);
+}
+
+int gpeed_iq3xxs_gemm2(const void* w_a, uint64_t n_rows_a, uint64_t row0_a, int out_a, const void* w_b,
+                       uint64_t n_rows_b, uint64_t row0_b, int out_b, int in_dim, const void* X, int x_dtype,
+                       int n_tok, float* Y_a, float* Y_b, void* ws, size_t ws_bytes, gpeed_stream_t stream) {
+    if (n_tok <= 0 || (out_a <= 0 && out_b <= 0)) return GPEED_OK;  // weights.cpp:88
+    if (out_a <= 0 || out_b <= 0) {  // one tensor left: the ordinary GEMM
+        const bool a = out_a > 0;
+        return gpeed_iq3xxs_gemm(a ? w_a : w_b, a ? n_rows_a : n_rows_b, a ? row0_a : row0_b, in_dim,
+                                 a ? out_a : out_b, X, x_dtype, n_tok, a ? Y_a : Y_b, ws, ws_bytes, stream);
+    }
+    int rc = check_mv_args(w_a, n_rows_a, row0_a, in_dim, out_a, X, Y_a, "gemm2");
+    if (rc) return rc;
+    rc = check_mv_args(w_b, n_rows_b, row0_b, in_dim, out_b, X, Y_b, "gemm2");
+    if (rc) return rc;
+    if (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16) return fail(GPEED_ERR_INVALID, "gemm2: x_dtype");
+    if (n_tok > (1 << 20)) return fail(GPEED_ERR_INVALID, "gemm2: n_tok too large");
+    if (row0_a % gpeed::kTileRows || row0_b % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "gemm2: row0 must be a multiple of 64 on the T64 layout");
+    if (!aligned(w_a, 16) || !aligned(w_b, 16) || !aligned(X, 16))
+        return fail(GPEED_ERR_INVALID, "gemm2: misaligned operand");
+    const DeviceState* st = nullptr;
+    rc = device_state(&st);
+    if (rc) return rc;
+    if (!ws || !aligned(ws, 256) ||
+        ws_bytes < gpeed::gemm2_ws_bytes(n_tok, out_a, out_b, in_dim, x_dtype == GPEED_X_BF16, st->num_cus))
+        return fail(GPEED_ERR_WORKSPACE, "gemm2: workspace missing, misaligned or too small");
+    hipError_t e = gpeed::launch_gemm2(static_cast<const uint8_t*>(w_a), row0_a, out_a,
+                                       static_cast<const uint8_t*>(w_b), row0_b, out_b, in_dim, X,
+                                       x_dtype == GPEED_X_BF16, n_tok, Y_a, Y_b, static_cast<uint8_t*>(ws),
+                                       st->num_cus, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm2 launch");
+}
+
 int gpeed_iq3xxs_gemm_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                              const float* G, const float* U, float limit, int n_tok, float* Y, void* ws,
                              size_t ws_bytes, gpeed_stream_t stream) {

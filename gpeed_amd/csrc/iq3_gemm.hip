@@ -111,10 +111,15 @@ struct GemmArgs {
     const float* unscale;   // [M]
     float* y;               // [M][N]
     int M, N, K, nb;
-    int tiles_m, tiles_n;
+    int tiles_m, tiles_n;   // tiles_n: result tiles of both tensors
     int ks;                 // K splits per result tile (1: no partials)
     uint32_t* cnt;          // ks > 1: tickets per tile (zero between launches)
     float* part;            // ks > 1: [tile][split][128][192] fp32 partials
+    // a second tensor on the same X: result tiles tn >= tiles_n1 are its
+    // tiles tn - tiles_n1 (w2, y2 [M][N2]); tiles_n1 = tiles_n for one tensor
+    const uint8_t* w2;
+    float* y2;
+    int N2, tiles_n1;
 };
 
 constexpr int kTileN = 192;  // result tile: 128 (or 64) tokens x 192 W rows
@@ -142,6 +147,20 @@ __device__ __forceinline__ GemmTile gemm_tile(const GemmArgs& g) {
     t.b0 = t.kz * g.nb / g.ks;
     t.b1 = (t.kz + 1) * g.nb / g.ks;
     return t;
+}
+
+// The arguments of the tensor that result tile t belongs to (w, y, N its
+// own) and the tile's index inside that tensor.
+__device__ __forceinline__ GemmArgs gemm_tensor(const GemmArgs& g, const GemmTile& t, int& tn_local) {
+    GemmArgs a = g;
+    tn_local = t.tn;
+    if (t.tn >= g.tiles_n1) {
+        a.w = g.w2;
+        a.y = g.y2;
+        a.N = g.N2;
+        tn_local = t.tn - g.tiles_n1;
+    }
+    return a;
 }
 
 // The result tile (16 MT tokens x 192 rows) from this workgroup's fp32 sums acc[mt][j][i] (token
@@ -254,7 +273,7 @@ struct WRing {
 constexpr uint32_t slot_dword_off(int idx) { return (uint32_t)((idx >> 2) * kUnitBytes + (idx & 3) * 4); }
 
 template <int V>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g_all) {
     __shared__ __attribute__((aligned(16))) uint8_t tbl[kTbl2Bytes];
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][V][BM2 * kRow2];
 
@@ -264,9 +283,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g) {
     const int lr = lane & 15, lg = lane >> 4;
 
     __shared__ int last_flag;
-    const GemmTile tl = gemm_tile(g);
-    const int tn = tl.tn, tm = tl.tm;
-    if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
+    const GemmTile tl = gemm_tile(g_all);
+    if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
+    int tn;
+    const GemmArgs g = gemm_tensor(g_all, tl, tn);
+    const int tm = tl.tm;
     const int m0 = tm * BM2, n0 = tn * BN2;
     const uint32_t kboff = (uint32_t)tl.b0 * kRecordBytes;  // this split's first block
 
@@ -507,7 +528,7 @@ __device__ __forceinline__ half8_t decode_group(const uint8_t* tbl, uint32_t q, 
 }
 
 template <int BM, int V>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
     constexpr int MT = BM / 16;  // token tiles per wavefront
     constexpr int XP = BM / 32;  // X pieces per thread per image and stage
     __shared__ __attribute__((aligned(16))) GemmSmem3<BM, V> sm;
@@ -518,9 +539,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g) {
     const int lr = lane & 15;
     const uint32_t lg = lane >> 4;
 
-    const GemmTile tl = gemm_tile(g);
-    const int tn = tl.tn, tm = tl.tm;
-    if (tm >= g.tiles_m || tn >= g.tiles_n) return;  // uniform
+    const GemmTile tl = gemm_tile(g_all);
+    if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
+    int tn;
+    const GemmArgs g = gemm_tensor(g_all, tl, tn);
+    const int tm = tl.tm;
     const int m0 = tm * BM, n0 = tn * BN3;
     const uint32_t kboff = (uint32_t)tl.b0 * kRecordBytes;  // this split's first block
 
@@ -749,11 +772,15 @@ size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus) {
     return gemm_ws(M, N, K, x_bf16, gemm_splits(M, N, K, num_cus)).total;
 }
 
-hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
-                       int M, float* Y, uint8_t* ws, int num_cus, hipStream_t s, const float* U, float lim) {
-    if (M <= 0 || out_dim <= 0) return hipSuccess;
-    const int ks = gemm_splits(M, out_dim, in_dim, num_cus);
-    const GemmWs L = gemm_ws(M, out_dim, in_dim, x_bf16, ks);
+hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, const uint8_t* wb,
+                        unsigned long long row0b, int out_b, int in_dim, const void* X, int x_bf16, int M, float* Ya,
+                        float* Yb, uint8_t* ws, int num_cus, hipStream_t s, const float* U, float lim) {
+    if (M <= 0 || out_a <= 0) return hipSuccess;
+    if (!wb) out_b = 0;
+    const int tiles_a = (out_a + kTileN - 1) / kTileN, tiles_b = (out_b + kTileN - 1) / kTileN;
+    const int n_eq = (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
+    const int ks = gemm_splits(M, n_eq, in_dim, num_cus);
+    const GemmWs L = gemm_ws(M, n_eq, in_dim, x_bf16, ks);
     _Float16* xh = reinterpret_cast<_Float16*>(ws + L.img);
     float* uns = reinterpret_cast<float*>(ws + L.uns);
     if (x_bf16)
@@ -766,16 +793,20 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
     if (e != hipSuccess) return e;
     GemmArgs a{};
     a.nb = in_dim / kQK;
-    a.w = w + (size_t)(row0 / kTileRows) * a.nb * kRecordBytes;
+    a.w = wa + (size_t)(row0a / kTileRows) * a.nb * kRecordBytes;
     a.xh = xh;
     a.unscale = uns;
-    a.y = Y;
+    a.y = Ya;
     a.M = M;
-    a.N = out_dim;
+    a.N = out_a;
     a.K = in_dim;
     const int bm = gemm_tile_m(M);
     a.tiles_m = (M + bm - 1) / bm;
-    a.tiles_n = (out_dim + kTileN - 1) / kTileN;
+    a.tiles_n1 = tiles_a;
+    a.tiles_n = tiles_a + tiles_b;
+    a.w2 = out_b > 0 ? wb + (size_t)(row0b / kTileRows) * a.nb * kRecordBytes : a.w;
+    a.y2 = out_b > 0 ? Yb : Ya;
+    a.N2 = out_b > 0 ? out_b : out_a;
     a.ks = ks;
     a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
     a.part = reinterpret_cast<float*>(ws + L.part);
@@ -786,6 +817,16 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
                       : launch_timed(kProfGemm, k_gemm3<64, 2>, gd, bd, 0, s, a);
     return x_bf16 ? launch_timed(kProfGemm, k_gemm3<128, 1>, gd, bd, 0, s, a)
                   : launch_timed(kProfGemm, k_gemm2<2>, gd, bd, 0, s, a);
+}
+
+hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
+                       int M, float* Y, uint8_t* ws, int num_cus, hipStream_t s, const float* U, float lim) {
+    return launch_gemm2(w, row0, out_dim, nullptr, 0, 0, in_dim, X, x_bf16, M, Y, nullptr, ws, num_cus, s, U, lim);
+}
+
+size_t gemm2_ws_bytes(int M, int out_a, int out_b, int K, int x_bf16, int num_cus) {
+    const int n_eq = ((out_a + kTileN - 1) / kTileN + (out_b + kTileN - 1) / kTileN) * kTileN;
+    return gemm_ws_bytes(M, n_eq, K, x_bf16, num_cus);
 }
 
 }  // namespace gpeed

@@ -108,5 +108,12 @@ size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus);
 hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
                        int M, float* Y, uint8_t* ws, int num_cus, hipStream_t s, const float* U = nullptr,
                        float lim = 0.0f);
+// Two tensors on the same X in one launch (X prepared once): Ya [M][out_a]
+// from wa, Yb [M][out_b] from wb; ws: gemm2_ws_bytes bytes.
+size_t gemm2_ws_bytes(int M, int out_a, int out_b, int K, int x_bf16, int num_cus);
+hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, const uint8_t* wb,
+                        unsigned long long row0b, int out_b, int in_dim, const void* X, int x_bf16, int M, float* Ya,
+                        float* Yb, uint8_t* ws, int num_cus, hipStream_t s, const float* U = nullptr,
+                        float lim = 0.0f);
 
 }  // namespace gpeed

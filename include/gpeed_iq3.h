@@ -153,6 +153,16 @@ int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_
 int gpeed_iq3xxs_gemm_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                              const float* G, const float* U, float limit, int n_tok, float* Y, void* ws,
                              size_t ws_bytes, gpeed_stream_t stream);
+/* Two matmul_quant calls on the same X (kv_a and q_a, model_batch.cpp:62,72;
+ * gate and up, model_batch.cpp:151-162) as one launch: X is prepared once
+ * and the result tiles of both tensors share the grid, so neither product
+ * waits for the other. Y_a [n_tok][out_a] from rows row0_a.. of w_a, Y_b
+ * [n_tok][out_b] from w_b, each exactly as gpeed_iq3xxs_gemm would give it.
+ * ws: gpeed_iq3xxs_gemm2_ws_bytes bytes (same rules as the GEMM's). */
+size_t gpeed_iq3xxs_gemm2_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_a, int64_t out_b, int x_dtype);
+int gpeed_iq3xxs_gemm2(const void* w_a, uint64_t n_rows_a, uint64_t row0_a, int out_a, const void* w_b,
+                       uint64_t n_rows_b, uint64_t row0_b, int out_b, int in_dim, const void* X, int x_dtype,
+                       int n_tok, float* Y_a, float* Y_b, void* ws, size_t ws_bytes, gpeed_stream_t stream);
 
 /* The two halves of the products, for callers that reuse one activation
  * across several tensors (gate and up of model.cpp:681-682) or fuse the

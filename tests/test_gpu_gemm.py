@@ -127,6 +127,39 @@ def test_dense_mlp_batch_gemm(gpu, M, H, I):
     assert e < 1e-4, e
 
 
+@pytest.mark.parametrize("M,Na,Nb,K,row0a,row0b,x_bf16", [
+    (64, 576, 1536, 6144, 0, 0, False),    # decode-mix kv_a + q_a, K split over workgroups
+    (100, 200, 330, 768, 64, 128, True),   # partial token and row tiles, row offsets
+    (200, 384, 192, 512, 0, 64, False),    # fp32 X over 64 tokens (the hi/lo form)
+    (512, 6144, 6144, 1024, 0, 0, True),   # one K split, XCD bands across both tensors
+])
+def test_gemm2_two_tensors(gpu, M, Na, Nb, K, row0a, row0b, x_bf16):
+    """Two products on one X in one launch (gpeed_iq3xxs_gemm2): each output
+    against the oracle's matmul_quant of its own tensor, on token slices; a
+    second call on the same workspace gives the same bits."""
+    import torch
+
+    wa = synth.iq3xxs_matrix(96, 0, row0a + Na, K)
+    wb = synth.iq3xxs_matrix(96, 1, row0b + Nb, K)
+    X = synth.normal(96, M, M * K).reshape(M, K)
+    if x_bf16:
+        X = bf16_round(X)
+    ta = G.tile(dev(wa.reshape(-1), gpu), row0a + Na, K)
+    tb = G.tile(dev(wb.reshape(-1), gpu), row0b + Nb, K)
+    Xd = as_bf16_tensor(X, gpu) if x_bf16 else dev(X, gpu)
+    xd = G.X_BF16 if x_bf16 else G.X_F32
+    ws = torch.zeros(G.lib().gpeed_iq3xxs_gemm2_ws_bytes(M, K, Na, Nb, xd), dtype=torch.uint8, device=gpu)
+    Ya, Yb = G.gemm2(ta, row0a + Na, row0a, Na, tb, row0b + Nb, row0b, Nb, K, Xd, ws=ws)
+    Ya, Yb = Ya.cpu().numpy(), Yb.cpu().numpy()
+    step = 1 if M * K <= 1 << 16 else 8
+    for Y, w, r0, N in ((Ya, wa, row0a, Na), (Yb, wb, row0b, Nb)):
+        ref = oracle.matmul(w, r0, K, N, X[::step])
+        e = max(rel_err(Y[::step][t], ref[t]) for t in range(ref.shape[0]))
+        assert e < TIGHT, (N, e)
+    Ya2, Yb2 = G.gemm2(ta, row0a + Na, row0a, Na, tb, row0b + Nb, row0b, Nb, K, Xd, ws=ws)
+    assert np.array_equal(Ya, Ya2.cpu().numpy()) and np.array_equal(Yb, Yb2.cpu().numpy())
+
+
 def test_gemm_matches_gemv(gpu):
     """Same fp32 tokens through the GEMM and the multi-token GEMV."""
     M, N, K = 8, 640, 2048
