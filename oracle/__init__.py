@@ -1,7 +1,8 @@
 """CPU oracle for the IQ3_XXS dequantize-and-multiply path (TEST INFRASTRUCTURE ONLY).
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
-import this package, and only as the checker / the timed CPU baseline. The
+import this package, and only as the correctness reference / the timed CPU
+baseline. The
 product (``gpeed_amd``) never imports it and has no CPU fallback.
 
 ``lib()``  -> liboracle.so, the plain-C restatement (iq3_oracle.c), with numpy

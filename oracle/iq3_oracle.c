@@ -1,6 +1,6 @@
 /* CPU oracle for the IQ3_XXS dequantize-and-multiply path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for tests/, smoke() and bench.py's
+ * TEST INFRASTRUCTURE ONLY: the correctness reference for tests/, smoke() and bench.py's
  * cpu_baseline leg. The product never links or calls this file.
  *
  * Build with -ffp-contract=off and spell every fused multiply-add as fmaf():

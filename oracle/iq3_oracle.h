@@ -1,8 +1,9 @@
 /* CPU oracle for the IQ3_XXS dequantize-and-multiply path.
  *
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's
- * CPU algorithm, used as the checker by tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py. Nothing in the product (gpeed_amd/) links,
+ * CPU algorithm, used as the correctness reference by tests/,
+ * __graft_entry__.smoke() and the cpu_baseline leg of bench.py. Nothing in
+ * the product (gpeed_amd/) links,
  * imports or calls it, and no product path falls back to it.
  *
  * Every function cites the reference file:line it restates (paths relative to

@@ -1,7 +1,7 @@
 """pytest configuration: the `gpu` marker and shared fixtures.
 
 Tests marked ``gpu`` need an MI355X (run with ``-m gpu``); everything else runs
-on the CPU. The oracle package (oracle/) is the checker for both.
+on the CPU. The oracle package (oracle/) is the correctness reference for both.
 """
 import os
 import sys

@@ -2,7 +2,7 @@
 into LDS as exact fp16 q*(2s+1), X as fp16 images (bf16 input exact, fp32
 input as hi+lo), fp32 MFMA accumulation. Checked against the oracle's
 matmul_quant (weights.cpp:86-165) on the same bf16-representable or fp32
-inputs: rel_err < 2e-5 (north-star bar 1e-3). Full-size shapes are checked on
+inputs: rel_err < 2e-5 (the parity bar is 1e-3). Full-size shapes are checked on
 row slices the CPU oracle finishes quickly."""
 import numpy as np
 import pytest

@@ -1,7 +1,7 @@
 """GPU parity tests for the IQ3_XXS path, through the C ABI (gpeed_amd -> libgpeed_iq3.so).
 
 Bars: dequantized weights and layout conversions bit-exact; products within
-1e-3 of the oracle under rel_err (conftest.rel_err, the north-star gate) and,
+1e-3 of the oracle under rel_err (conftest.rel_err, the parity bar) and,
 as a tighter design check, within 2e-5 -- the MFMA path multiplies exactly
 (fp16 signed grid values times fp16 hi/lo activation halves, then the exact
 (2s+1) and d/4 scales), so only fp32 accumulation order separates it from the

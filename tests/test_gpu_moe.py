@@ -3,7 +3,7 @@
 The router's integer outputs (bucket offsets, token order, ranked choices)
 must equal the oracle's bit for bit; combine weights differ from the CPU's
 only by the last-ulp of expf (rel 1e-6); the experts' output is held to the
-product bar (rel_err < 2e-5, north-star 1e-3).
+product bar (rel_err < 2e-5; the parity bar is 1e-3).
 """
 import numpy as np
 import pytest

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/iq3_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/iq3_oracle.c) before it is trusted as the reference.
 
 Each check is chosen so that a plausible slip in the restatement (a dropped
 term, a wrong shift, a transposed operand, a different summation order) fails:
