@@ -443,6 +443,7 @@ struct GroupedArgs {
     int n_tensors;
     int nb;                   // blocks per row
     int tiles;                // 64-row tiles per expert
+    int tiles_per_item;       // consecutive row tiles one work item streams (divides tiles)
     int rows;                 // rows per expert (= output width)
     MoePlan pl;
     int ctr_index;
@@ -450,32 +451,42 @@ struct GroupedArgs {
 
 // One (segment, tensor, tile) item: the wavefront walks the tile's nb
 // records through a 2-deep ring and writes the 64 rows x n tokens result.
+// nt consecutive row tiles (records rec0 .. rec0 + nt*nb - 1, tile-major) of
+// one segment: the ring runs on across the tile boundaries; each tile's sums
+// go to y at its end.
 template <int NP>
 __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, uint32_t lane, const uint8_t* rec0,
-                                             const uint8_t* act, int n, int nb, float* y, int rows, int row0) {
+                                             const uint8_t* act, int n, int nb, int nt, float* y, int rows,
+                                             int row0) {
     constexpr int PF = 2;
+    const int nrec = nt * nb;
     const float* xsc = reinterpret_cast<const float*>(act + (size_t)nb * n * 1024);
     // The block unscales travel with the record ring: one wait per record
     // covers both, where a load issued at the product would expose its
     // latency.
     Rec<NP> ring[PF];
     const int tl = min((int)(lane & 7u), n - 1);
+    auto fill = [&](Rec<NP>& r, int k) {  // record k of the item (clamped to the last)
+        k = min(k, nrec - 1);
+        const int b = k % nb;
+        load_record<NP>(r, rec0 + (size_t)k * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
+        r.xs = __builtin_bit_cast(uint32_t, xsc[(size_t)b * n + tl]);
+    };
 #pragma unroll
     for (int s = 0; s < PF; ++s) {
-        const int b = min(s, nb - 1);
-        load_record<NP>(ring[s], rec0 + (size_t)b * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
-        ring[s].xs = __builtin_bit_cast(uint32_t, xsc[(size_t)b * n + tl]);
+        fill(ring[s], s);
         // slot order kept, so the loop's first wait covers slot 0 only
         __builtin_amdgcn_sched_barrier(0);
     }
     float acc[2 * NP];
 #pragma unroll
     for (int t = 0; t < 2 * NP; ++t) acc[t] = 0.0f;
-    for (int k0 = 0; k0 < nb; k0 += PF) {
+    int kb = 0, tile = 0;  // block within the tile, tile within the item
+    for (int k0 = 0; k0 < nrec; k0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; ++s) {
             const int k = k0 + s;
-            if (k < nb) {
+            if (k < nrec) {
                 float blk[2 * NP];
 #pragma unroll
                 for (int t = 0; t < 2 * NP; ++t) blk[t] = 0.0f;
@@ -484,16 +495,20 @@ __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, ui
 #pragma unroll
                 for (int t = 0; t < 2 * NP; ++t)
                     if (t < n) acc[t] = fmaf(d4 * rec_unscale(ring[s], t), blk[t], acc[t]);
+                if (++kb == nb) {  // uniform
+#pragma unroll
+                    for (int t = 0; t < 2 * NP; ++t) {
+                        if (t < n) y[(size_t)t * rows + row0 + tile * kTileRows + lane] = acc[t];
+                        acc[t] = 0.0f;
+                    }
+                    kb = 0;
+                    ++tile;
+                }
             }
-            const int b = min(k + PF, nb - 1);
-            load_record<NP>(ring[s], rec0 + (size_t)b * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
-            ring[s].xs = __builtin_bit_cast(uint32_t, xsc[(size_t)b * n + tl]);
+            fill(ring[s], k + PF);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-#pragma unroll
-    for (int t = 0; t < 2 * NP; ++t)
-        if (t < n) y[(size_t)t * rows + row0 + lane] = acc[t];
 }
 
 constexpr int kGroupedThreads = 256;
@@ -507,7 +522,8 @@ __global__ __launch_bounds__(kGroupedThreads, 2) void k_gemv_grouped(GroupedArgs
     grid_words<kGroupedThreads>(gw, tid);
     grid_table_store<kGroupedThreads>(tbl, gw, tid);
     lds_barrier();
-    const int per_seg = g.n_tensors * g.tiles;
+    const int groups = g.tiles / g.tiles_per_item;  // items per segment and tensor
+    const int per_seg = g.n_tensors * groups;
     const int n_items = *g.pl.n_seg * per_seg;
     // the first round is static (wavefront i takes item i), the rest come
     // from the counter: 2048 wavefronts taking tickets on one address at
@@ -519,16 +535,17 @@ __global__ __launch_bounds__(kGroupedThreads, 2) void k_gemv_grouped(GroupedArgs
         if (item >= (uint32_t)n_items) break;
         const int s = item / per_seg;
         const int rem = item - s * per_seg;
-        const int ten = rem / g.tiles, tile = rem - ten * g.tiles;
+        const int ten = rem / groups, tile = (rem - ten * groups) * g.tiles_per_item;
         const int e = g.pl.seg_e[s], p0 = g.pl.seg_p0[s], n = g.pl.seg_n[s];
         const uint8_t* rec0 = g.w[ten] + ((size_t)e * g.tiles + tile) * g.nb * kRecordBytes;
         const uint8_t* act = g.act + (size_t)s * g.seg_stride;
         float* y = g.y[ten] + (size_t)p0 * g.rows;
+        const int nt = g.tiles_per_item;
         switch ((n + 1) >> 1) {
-            case 1: grouped_tile<1>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
-            case 2: grouped_tile<2>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
-            case 3: grouped_tile<3>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
-            default: grouped_tile<4>(tbl, lb, lane, rec0, act, n, g.nb, y, g.rows, tile * kTileRows); break;
+            case 1: grouped_tile<1>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
+            case 2: grouped_tile<2>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
+            case 3: grouped_tile<3>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
+            default: grouped_tile<4>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
         }
         uint32_t t = 0;
         if (lane == 0) t = __hip_atomic_fetch_add(g.pl.ctr + g.ctr_index, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -653,6 +670,7 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     ga.n_tensors = 2;
     ga.nb = nbH;
     ga.tiles = I / kTileRows;
+    ga.tiles_per_item = 1;
     ga.rows = I;
     ga.pl = pl;
     ga.ctr_index = 0;
@@ -670,6 +688,11 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     gd.n_tensors = 1;
     gd.nb = nbI;
     gd.tiles = H / kTileRows;
+    // short rows (few blocks per tile) take several tiles per item, so the
+    // ring's start-up is paid once per ~16 records
+    gd.tiles_per_item = 1;
+    while (gd.tiles_per_item < 4 && gd.tiles % (2 * gd.tiles_per_item) == 0 && gd.nb * gd.tiles_per_item < 16)
+        gd.tiles_per_item *= 2;
     gd.rows = H;
     gd.ctr_index = 1;
     e = launch_timed(kProfGrouped, k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, gd);
