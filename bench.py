@@ -327,6 +327,9 @@ def main():
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="gpeed_stream_read over rotated buffers of the GEMV sizes, "
+                         "for the read-ceiling profile (run under rocprofv3 --kernel-trace --stats)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 elementwise copies of 256 MiB (counter calibration), then 20 dense steps, and "
                          "exit; meant to run under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE)")
@@ -374,6 +377,28 @@ def main():
     def step_fast(c):
         if fn_mlp(*call_args[c]) != 0:
             raise RuntimeError(f"dense_mlp: {G.lib().gpeed_last_error().decode(errors='replace')}")
+
+    if args.stream_probe:
+        # one streaming read per launch at each GEMV weight size (down; gate+up;
+        # the whole step), buffers rotated over the GEMV steps' 694 MB so every
+        # byte comes from HBM, not the 256 MB Infinity Cache
+        import ctypes
+        out = torch.zeros(1024, dtype=torch.int32, device=dev)
+        cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for nbytes in (W_BYTES // 3, 2 * (W_BYTES // 3), W_BYTES):
+            n_bufs = -(-args.copies * W_BYTES // nbytes)  # as many bytes rotated as the GEMV steps rotate
+            bufs = [torch.ones(nbytes // 16 * 4, device=dev) for _ in range(n_bufs)]
+            for groups in (256, 512, 1024):  # workgroups of 512 threads: 1, 2, 4 per CU
+                for _ in range(10):
+                    for b in bufs:
+                        if G.lib().gpeed_stream_read(ctypes.c_void_p(b.data_ptr()), b.numel() * 4,
+                                                     ctypes.c_void_p(out.data_ptr()), groups, cur) != 0:
+                            raise RuntimeError("stream_read failed")
+                torch.cuda.synchronize()
+                log(f"stream probe: {nbytes} B, {groups} workgroups, x {10 * len(bufs)} reads")
+            del bufs
+            torch.cuda.empty_cache()
+        return
 
     if args.traffic_probe:
         src = torch.ones(64 << 20, device=dev)  # 256 MiB fp32

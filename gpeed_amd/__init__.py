@@ -87,6 +87,7 @@ def lib():
             "gpeed_iq3xxs_gemm2_ws_bytes": ([i64, i64, i64, i64, i32], sz),
             "gpeed_iq3xxs_gemm2": ([vp, u64, u64, i32, vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, vp, sz, vp],
                                    i32),
+            "gpeed_stream_read": ([vp, sz, vp, sz, vp], i32),
             "gpeed_prof_start": ([i32], i32),
             "gpeed_prof_read": ([i32, vp, i32, vp], i32),
             "gpeed_moe_route_ws_bytes": ([i32, i32, i32], sz),
@@ -170,6 +171,20 @@ def add_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     b = np.ascontiguousarray(b, np.float32)
     out = np.empty_like(a)
     _check(lib().gpeed_add_f32(a.ctypes.data, b.ctypes.data, out.ctypes.data, a.size), "gpeed_add_f32")
+    return out
+
+
+def stream_read(buf, groups: int, out=None, stream=None):
+    """Reads the bytes of device tensor `buf` once (gpeed_stream_read: `groups`
+    workgroups, each a contiguous share) and returns the int32 per-workgroup
+    XOR folds. A measurement aid: its duration is a plain streaming read of
+    buf.nbytes bytes."""
+    torch = _torch()
+    _require_cuda(buf)
+    if out is None:
+        out = torch.empty(groups, dtype=torch.int32, device=buf.device)
+    _check(lib().gpeed_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(out), groups,
+                                   _stream(stream)), "gpeed_stream_read")
     return out
 
 

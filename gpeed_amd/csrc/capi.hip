@@ -197,6 +197,16 @@ int gpeed_add_f32(const float* a, const float* b, float* dst, int n) {
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gpeed_add_f32");
 }
 
+int gpeed_stream_read(const void* p, size_t bytes, uint32_t* out, size_t out_words, gpeed_stream_t stream) {
+    if (bytes == 0) return GPEED_OK;
+    if (!p || !out || !aligned(p, 16)) return fail(GPEED_ERR_INVALID, "stream_read: null or misaligned pointer");
+    if (bytes % 16) return fail(GPEED_ERR_INVALID, "stream_read: bytes is not a multiple of 16");
+    if (out_words == 0 || out_words > 65535) return fail(GPEED_ERR_INVALID, "stream_read: out_words outside [1, 65535]");
+    hipError_t e = gpeed::launch_stream_read(static_cast<const uint8_t*>(p), bytes, out, (int)out_words,
+                                             static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "stream_read launch");
+}
+
 int gpeed_init(void) {
     if (gpeed_device_count() <= 0) return fail(GPEED_ERR_NO_DEVICE, "no HIP device");
     const DeviceState* st = nullptr;

@@ -117,6 +117,40 @@ __global__ __launch_bounds__(256) void k_untile(const uint8_t* __restrict__ t64,
     }
 }
 
+// Streaming read (measurement aid): workgroup i reads the i-th contiguous
+// share of `bytes` once, 16 bytes per lane per load, eight loads in flight
+// per lane, and folds what it read into one word (so no load is dead).
+__global__ __launch_bounds__(512) void k_stream_read(const uint8_t* __restrict__ p, unsigned long long bytes,
+                                                     uint32_t* __restrict__ out) {
+    const unsigned long long share = (bytes / gridDim.x + 4095) & ~4095ull;
+    const unsigned long long beg = share * blockIdx.x;
+    const unsigned long long end = beg + share < bytes ? beg + share : bytes;
+    uint32_t acc = 0;
+    constexpr unsigned long long kStep = 512 * 16;  // bytes one load of the workgroup covers
+    unsigned long long o = beg + threadIdx.x * 16ull;
+    for (; o + 7 * kStep + 16 <= end; o += 8 * kStep) {  // eight unguarded loads
+        uint4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const uint4*>(p + o + i * kStep);
+        __builtin_amdgcn_sched_barrier(0);  // all eight loads issue before the first use
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    }
+    for (; o + 16 <= end; o += kStep) {  // the share's tail
+        const uint4 v = *reinterpret_cast<const uint4*>(p + o);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    __shared__ uint32_t red[8];
+    for (int off = 32; off > 0; off >>= 1) acc ^= __shfl_xor(acc, off);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t a = 0;
+        for (int w = 0; w < 8; ++w) a ^= red[w];
+        out[blockIdx.x] = a;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_add(const float* __restrict__ a, const float* __restrict__ b,
                                              float* __restrict__ d, int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -124,6 +158,13 @@ __global__ __launch_bounds__(256) void k_add(const float* __restrict__ a, const 
 }
 
 }  // namespace
+
+hipError_t launch_stream_read(const uint8_t* p, unsigned long long bytes, uint32_t* out, int n_groups,
+                              hipStream_t s) {
+    if (bytes == 0 || n_groups <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_stream_read, dim3(n_groups), dim3(512), 0, s, p, bytes, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_dequant_raw(const uint8_t* src, float* dst, unsigned long long n, hipStream_t s) {
     const unsigned long long groups = n / 8;

@@ -10,6 +10,10 @@ namespace gpeed {
 
 // quant.cpp:186-210 over n/256 raw GGUF blocks -> fp32 (bit-exact).
 hipError_t launch_dequant_raw(const uint8_t* src, float* dst, unsigned long long n, hipStream_t s);
+// Streaming read of `bytes` from p (16-byte aligned) by n_groups workgroups;
+// out[i] = a fold of what workgroup i read.
+hipError_t launch_stream_read(const uint8_t* p, unsigned long long bytes, uint32_t* out, int n_groups,
+                              hipStream_t s);
 // GGUF rows -> T64 (tiled) and back. n_rows rows of in_dim weights.
 hipError_t launch_tile(const uint8_t* raw, unsigned long long n_rows, int in_dim, uint8_t* t64,
                        hipStream_t s);

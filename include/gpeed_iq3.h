@@ -54,6 +54,13 @@ int gpeed_add_f32(const float* a, const float* b, float* dst, int n);
 int gpeed_init(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char* gpeed_last_error(void);
+/* Measurement aid, no reference counterpart: reads `bytes` from device
+ * memory p (16-byte aligned, bytes a multiple of 16) once with out_words
+ * (1..65535) workgroups of
+ * 512 threads, each streaming a contiguous share in 16-byte loads; out[i]
+ * receives a fold of what workgroup i read. Its duration is the plain
+ * streaming-read time the GEMV is set against. */
+int gpeed_stream_read(const void* p, size_t bytes, uint32_t* out, size_t out_words, gpeed_stream_t stream);
 
 /* Device memory and copies for callers without HIP headers (the C++ host
  * layer; no reference counterpart: the reference keeps weights in host RAM,

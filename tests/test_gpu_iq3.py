@@ -418,6 +418,33 @@ def test_graph_replay_matches_eager(gpu):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("n_bytes,groups", [(16, 1), (4096 * 5 + 48, 3), (1 << 20, 256), (3 * (1 << 20) + 4080, 1024)])
+def test_stream_read_covers_every_byte(gpu, n_bytes, groups):
+    """Workgroup i folds (XOR of 32-bit words) exactly its share: shares are
+    ceil(bytes / groups) rounded up to 4 KiB, the last ones short or empty."""
+    rng = np.random.default_rng(n_bytes + groups)
+    words = rng.integers(0, 2**32, n_bytes // 4, dtype=np.uint64).astype(np.uint32)
+    got = host(G.stream_read(dev(words.view(np.int32), gpu), groups)).view(np.uint32)
+    share = (n_bytes // groups + 4095) & ~4095
+    want = np.zeros(groups, np.uint32)
+    for i in range(groups):
+        seg = words[i * share // 4:min((i + 1) * share, n_bytes) // 4]
+        want[i] = np.bitwise_xor.reduce(seg) if seg.size else 0
+    assert np.array_equal(got, want)
+
+
+def test_stream_read_errors(gpu):
+    import ctypes
+
+    buf = dev(np.zeros(64, np.int32), gpu)
+    out = dev(np.zeros(4, np.int32), gpu)
+    p, o = ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(out.data_ptr())
+    assert G.lib().gpeed_stream_read(p, 20, o, 4, None) != 0  # not a multiple of 16
+    assert G.lib().gpeed_stream_read(ctypes.c_void_p(buf.data_ptr() + 4), 32, o, 4, None) != 0
+    assert G.lib().gpeed_stream_read(p, 32, o, 0, None) != 0
+    assert G.lib().gpeed_stream_read(p, 0, o, 4, None) == 0  # nothing to read
+
+
 def test_device_smoke(gpu):
     assert G.device_count() >= 1
     assert G.device_name(0) not in ("", "<none>")
