@@ -152,9 +152,31 @@ def moe_decode(torch, G, synth, dev, steps, warmup):
         G.moe_experts(tens[0], tens[1], tens[2], E, HM, IM, X, K, eptr, tok, wt, SWIGLU_LIMIT, out=Y, ws=ws_e)
         return eptr
 
+    # timed through the C ABI with prebuilt arguments (as the dense step):
+    # the Python wrappers' host time per step is of the order of the GPU's
+    import ctypes
+    L = G.lib()
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    r_eptr = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    r_tok = torch.empty(T * K, dtype=torch.int32, device=dev)
+    r_wt = torch.empty(T * K, dtype=torch.float32, device=dev)
+    r_sel = torch.empty(T, K, dtype=torch.int32, device=dev)
+    route_args = (vp(logits), T, E, K, 1, ctypes.c_void_p(0), ctypes.c_float(1.0), 1, vp(r_eptr), vp(r_tok),
+                  vp(r_wt), vp(r_sel), vp(ws_r), ws_r.numel(), cur)
+    exp_args = (vp(tens[0]), vp(tens[1]), vp(tens[2]), E, HM, IM, vp(X), T, K, vp(r_eptr), vp(r_tok), vp(r_wt),
+                ctypes.c_float(SWIGLU_LIMIT), vp(Y), vp(ws_e), ws_e.numel(), cur)
+
+    def step_fast():
+        if L.gpeed_moe_route(*route_args) != 0 or L.gpeed_iq3xxs_moe_experts(*exp_args) != 0:
+            raise RuntimeError(f"moe: {L.gpeed_last_error().decode(errors='replace')}")
+
     for _ in range(warmup):
         eptr = step()
+        step_fast()
     torch.cuda.synchronize()
+    if not torch.equal(r_eptr, eptr):
+        raise RuntimeError("moe: prebuilt and wrapper routes differ")
     counts = np.diff(eptr.cpu().numpy())
     touched = int((counts > 0).sum())
     blk_bytes = IM * HM // 256 * 98  # one expert's gate (or up, or down) tensor
@@ -163,15 +185,21 @@ def moe_decode(torch, G, synth, dev, steps, warmup):
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(steps):
-        step()
+        step_fast()
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_wrapped = t0.elapsed_time(t1) / steps
     # kernel durations from dispatch-stamped launches, in a loop of their own
     # (the stamps add to the step)
     G.prof_start(4 * steps + 8)
     for _ in range(steps):
-        step()
+        step_fast()
     torch.cuda.synchronize()
     d = G.prof_read(G.PROF_GROUPED).astype(np.float64)  # launch order: gate+up, down, ...
     gu, dn = d[0::2], d[1::2]
@@ -183,7 +211,8 @@ def moe_decode(torch, G, synth, dev, steps, warmup):
         "workload": "routed-expert decode batch: 64 experts x (gate/up 2048x6144 + down 6144x2048) IQ3_XXS, "
                     "32 tokens, softmax top-8, router + grouped GEMVs + combine on the GPU",
         "touched_experts": touched, "packed_bytes_per_step": moe_bytes,
-        "ms_per_step": round(ms, 4), "GBps": round(moe_bytes / (ms * 1e-3) / 1e9, 1),
+        "ms_per_step": round(ms, 4), "ms_per_step_python_wrappers": round(ms_wrapped, 4),
+        "GBps": round(moe_bytes / (ms * 1e-3) / 1e9, 1),
         "frac_of_hbm_peak": round(moe_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "grouped_gemv": {"kernel": "k_gemv_grouped", "gate_up_us": round(float(gu.mean()) * 1e3, 2),
                          "down_us": round(float(dn.mean()) * 1e3, 2),
@@ -522,7 +551,7 @@ def main():
     if not args.no_extra:
         del copies, base
         torch.cuda.empty_cache()
-        rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(10, args.steps // 10), 3)}
+        rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(30, args.steps // 5), 30)}
         torch.cuda.empty_cache()
         rec["extra"]["prefill_gemm"] = prefill_gemm(torch, G, synth, dev, 20)
         torch.cuda.empty_cache()
