@@ -132,7 +132,7 @@ def cpu_baseline(wg, wu, wd, x):
     return out, y_ref
 
 
-def moe_decode(torch, G, synth, dev, steps, warmup):
+def moe_decode(torch, G, synth, dev, steps, warmup_s):
     """Routed-expert decode batch: route + grouped gate/up + SwiGLU + grouped down + combine."""
     E, T, K, HM, IM = 64, 32, 8, 6144, 2048
     log("moe: generating 64 experts")
@@ -171,10 +171,15 @@ def moe_decode(torch, G, synth, dev, steps, warmup):
         if L.gpeed_moe_route(*route_args) != 0 or L.gpeed_iq3xxs_moe_experts(*exp_args) != 0:
             raise RuntimeError(f"moe: {L.gpeed_last_error().decode(errors='replace')}")
 
-    for _ in range(warmup):
-        eptr = step()
-        step_fast()
-    torch.cuda.synchronize()
+    # warm-up by time, not count: after the CPU-bound weight generation the
+    # GPU runs the first ~100 ms of steps measurably slower
+    import time
+    eptr = step()
+    t_end = time.perf_counter() + warmup_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            step_fast()
+        torch.cuda.synchronize()
     if not torch.equal(r_eptr, eptr):
         raise RuntimeError("moe: prebuilt and wrapper routes differ")
     counts = np.diff(eptr.cpu().numpy())
@@ -183,12 +188,18 @@ def moe_decode(torch, G, synth, dev, steps, warmup):
     moe_bytes = touched * 3 * blk_bytes
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    # each timed loop follows an untimed lead-in of the same length with no
+    # synchronisation between them, so it measures back-to-back steps
+    for _ in range(steps):
+        step_fast()
     t0.record()
     for _ in range(steps):
         step_fast()
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    for _ in range(steps):
+        step()
     t0.record()
     for _ in range(steps):
         step()
@@ -551,7 +562,7 @@ def main():
     if not args.no_extra:
         del copies, base
         torch.cuda.empty_cache()
-        rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(30, args.steps // 5), 30)}
+        rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(30, args.steps // 5), 0.3)}
         torch.cuda.empty_cache()
         rec["extra"]["prefill_gemm"] = prefill_gemm(torch, G, synth, dev, 20)
         torch.cuda.empty_cache()
