@@ -95,6 +95,8 @@ def experts_case(gpu, seed, T, E, K, H, I, mode=1):
     (5, 8, 2, 512, 256, 1),
     (32, 16, 4, 1024, 512, 0),     # experts with up to ~20 tokens: several segments each
     (3, 4, 4, 768, 1280, 1),       # every expert touched by every token
+    (1, 64, 8, 1024, 512, 0),      # one token (moe_forward, model.cpp:692-756): 8 experts of one token each
+    (1, 4, 1, 256, 256, 1),        # one token, top-1: a single expert, a single segment
 ])
 def test_experts_small(gpu, T, E, K, H, I, mode):
     Y, ref = experts_case(gpu, 72, T, E, K, H, I, mode)
