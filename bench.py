@@ -373,6 +373,9 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run 5 elementwise copies of 256 MiB (counter calibration), then 20 dense steps, and "
                          "exit; meant to run under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE)")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="run the prefill GEMM (W 12288x6144, bf16 X [512, 6144]) 20 times and the dense "
+                         "decode step 20 times, and exit; meant to run under rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the multi-GPU "
@@ -438,6 +441,20 @@ def main():
                 log(f"stream probe: {nbytes} B, {groups} workgroups, x {10 * len(bufs)} reads")
             del bufs
             torch.cuda.empty_cache()
+        return
+
+    if args.gemm_probe:
+        N_, K_, M_ = 12288, 6144, 512
+        t64 = G.tile(torch.from_numpy(synth.iq3xxs_matrix(2026, 0, N_, K_).reshape(-1)).to(dev), N_, K_)
+        X = torch.from_numpy(synth.normal(2026, M_, M_ * K_).reshape(M_, K_)).to(dev).to(torch.bfloat16)
+        Yg = torch.empty(M_, N_, device=dev)
+        wsg = torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M_, K_, N_, G.X_BF16), dtype=torch.uint8, device=dev)
+        for _ in range(20):
+            G.gemm(t64, N_, 0, K_, N_, X, out=Yg, ws=wsg)
+        for i in range(20):
+            step(i % args.copies)
+        torch.cuda.synchronize()
+        log("gemm probe done")
         return
 
     if args.traffic_probe:
