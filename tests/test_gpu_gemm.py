@@ -41,6 +41,8 @@ def as_bf16_tensor(xf, device):
     (300, 384, 1536, 0, True),
     (64, 576, 6144, 0, False),      # the decode-mix latent projection, fp32
     (37, 1536, 6144, 0, True),
+    (1, 64, 256, 0, True),          # one token, one row tile, one block
+    (65, 192, 512, 0, False),       # one token past the 64-token tile: 128-token tiles, fp32 input
 ])
 def test_gemm_small(gpu, M, N, K, row0, x_bf16):
     n_rows = row0 + N
