@@ -439,8 +439,30 @@ def main():
                             raise RuntimeError("stream_read failed")
                 torch.cuda.synchronize()
                 log(f"stream probe: {nbytes} B, {groups} workgroups, x {10 * len(bufs)} reads")
+            if nbytes == W_BYTES // 3:
+                # independent readers of the same bytes: the runtime's
+                # device-to-device copy (reads and writes them) and torch's
+                # sum reduction (reads them)
+                dst = [torch.empty_like(bufs[0]) for _ in range(4)]
+                for _ in range(10):
+                    for i, b in enumerate(bufs):
+                        dst[i % 4].copy_(b)
+                for _ in range(10):
+                    for b in bufs:
+                        torch.sum(b)
+                torch.cuda.synchronize()
+                log(f"stream probe: {nbytes} B, runtime copy and torch.sum, x {10 * len(bufs)} each")
+                del dst
             del bufs
             torch.cuda.empty_cache()
+        # the same two readers at 256 MiB (the asymptotic rate)
+        big = [torch.ones(64 << 20, device=dev) for _ in range(3)]
+        for _ in range(8):
+            for i in range(3):
+                big[(i + 1) % 3].copy_(big[i])
+                torch.sum(big[i])
+        torch.cuda.synchronize()
+        log("stream probe: 256 MiB runtime copy and torch.sum, x 24 each")
         return
 
     if args.gemm_probe:

@@ -30,7 +30,9 @@ ERRORS = {
     -6: "T64 operand off a 64-row tile boundary",
     -7: "workspace missing or too small",
     -8: "no HIP device",
+    -9: "a kernel flagged its workspace",
 }
+WS_TICKET, WS_TIMEOUT, WS_BUCKETS = 1, 2, 4
 DTYPE_IQ3_XXS = 18
 QK = 256
 BLOCK_BYTES = 98
@@ -90,6 +92,10 @@ def lib():
             "gpeed_stream_read": ([vp, sz, vp, sz, vp], i32),
             "gpeed_prof_start": ([i32], i32),
             "gpeed_prof_read": ([i32, vp, i32, vp], i32),
+            "gpeed_ws_status": ([vp, vp], i32),
+            "gpeed_ws_init": ([vp, sz, vp], i32),
+            "gpeed_moe_check_buckets": ([vp, vp, i32, i32, i32], i32),
+            "gpeed_iq3xxs_matmul_gemm_min_tok": ([], i32),
             "gpeed_moe_route_ws_bytes": ([i32, i32, i32], sz),
             "gpeed_moe_route": ([vp, i32, i32, i32, i32, vp, C.c_float, i32, vp, vp, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_moe_ws_bytes": ([i32, i32, i32, i32, i32], sz),
@@ -226,14 +232,44 @@ def untile(t64, n_rows: int, in_dim: int, out=None, stream=None):
 
 
 def _zeros(nbytes: int, device):
-    """Zero-filled device buffer; a size the library rejects (0) still gets a
-    small buffer so that the call itself reports why."""
+    """Initialised workspace (gpeed_ws_init); a size the library rejects (0)
+    still gets a small buffer so that the call itself reports why."""
     torch = _torch()
-    return torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+    ws = torch.empty((max(nbytes, 256) + 255) // 256 * 256, dtype=torch.uint8, device=device)
+    ws_init(ws)
+    return ws
+
+
+def ws_init(ws, stream=None):
+    """Zero-fill a workspace with the library's fill kernel (gpeed_ws_init)."""
+    _require_cuda(ws)
+    _check(lib().gpeed_ws_init(_ptr(ws), ws.numel() * ws.element_size(), _stream(stream)), "ws_init")
+    return ws
+
+
+def ws_status(ws, stream=None):
+    """Waits for the stream; raises GpeedError (status -9) if a kernel flagged
+    the workspace since the last check (the flags are cleared)."""
+    _require_cuda(ws)
+    _check(lib().gpeed_ws_status(_ptr(ws), _stream(stream)), "ws_status")
+
+
+def moe_check_buckets(eptr: np.ndarray, tok: np.ndarray, n_exp: int, n_tok: int, top_k: int):
+    """Checks host expert buckets against the router's invariants (raises GpeedError)."""
+    e = np.ascontiguousarray(eptr, np.int32)
+    t = np.ascontiguousarray(tok, np.int32)
+    if e.size < n_exp + 1 or t.size < n_tok * top_k:
+        raise ValueError("moe_check_buckets: arrays shorter than n_exp + 1 / n_tok * top_k")
+    _check(lib().gpeed_moe_check_buckets(e.ctypes.data, t.ctypes.data, n_exp, n_tok, top_k), "moe_check_buckets")
+
+
+def matmul_gemm_min_tok() -> int:
+    """Token count from which matmul runs the prefill GEMM instead of GEMV passes."""
+    return lib().gpeed_iq3xxs_matmul_gemm_min_tok()
 
 
 def matmul_workspace(in_dim: int, out_dim: int, n_tok: int = 1, device="cuda"):
-    """Zero-filled workspace for matvec / matmul (reusable, one per stream)."""
+    """Initialised workspace for matvec / matmul of up to n_tok tokens (one per stream)."""
     return _zeros(lib().gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, n_tok), device)
 
 
@@ -255,7 +291,10 @@ def matvec(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out=None
 
 
 def matmul(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None, ws=None, stream=None):
-    """Y[t] = W[row0:row0+out_dim] @ X[t] for X [n_tok, in_dim] fp32; Y [n_tok, out_dim]."""
+    """Y[t] = W[row0:row0+out_dim] @ X[t] for X [n_tok, in_dim] fp32; Y [n_tok, out_dim].
+
+    GEMV passes of up to 8 tokens below matmul_gemm_min_tok() tokens, the
+    prefill GEMM with fp32 X from there on."""
     torch = _torch()
     _require_cuda(w_t64, X)
     n_tok = X.shape[0] if X.dim() == 2 else 1
@@ -506,9 +545,12 @@ class WeightStore:
     ``add(name, payload, in_dim, n_rows)`` uploads GGUF rows once and keeps
     their T64 copy in HBM (the role of pin_nonexpert, weights.cpp:70-84).
     ``matvec_quant`` follows weights.cpp:167-203: ``dst[j] = sum_i
-    W[row0+j][i] * x[i]`` for ``j < out_dim``; ``matmul_quant`` follows
-    weights.cpp:86-165 (``Y[t][j]`` for ``t < n_tok``, nothing done when
-    ``n_tok <= 0`` or ``out_dim <= 0``). Host numpy arrays in, host numpy out
+    W[row0+j][i] * x[i]`` for ``j < out_dim`` (one launch); ``matmul_quant``
+    follows weights.cpp:86-165 (``Y[t][j]`` for ``t < n_tok``, nothing done
+    when ``n_tok <= 0`` or ``out_dim <= 0``): 8-token GEMV passes below
+    ``matmul_gemm_min_tok()`` tokens, the prefill GEMM (one pass over W) from
+    there on, as at the reference's prefill call sites
+    (model_batch.cpp:30-95, 151-162). Host numpy arrays in, host numpy out
     (synchronous, like the reference), or device tensors in and out.
     """
 
@@ -540,9 +582,12 @@ class WeightStore:
         return self.tensors[name]
 
     def _workspace(self, in_dim: int, out_dim: int, n_tok: int):
-        key = (in_dim, out_dim, min(n_tok, 8))
+        # one workspace per shape, grown when a call needs more (a workspace
+        # sized for n_tok tokens serves every smaller call)
+        key = (in_dim, out_dim)
+        need = lib().gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, n_tok)
         ws = self._ws.get(key)
-        if ws is None:
+        if ws is None or ws.numel() < need:
             ws = self._ws[key] = matmul_workspace(in_dim, out_dim, n_tok, self.device)
         return ws
 
@@ -553,8 +598,10 @@ class WeightStore:
         if out_dim <= 0:
             return dst
         xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(self.device) if host else x
-        yd = matvec(t64, n_rows, row0, in_dim, out_dim, xd, ws=self._workspace(in_dim, out_dim, 1))
+        ws = self._workspace(in_dim, out_dim, 1)
+        yd = matvec(t64, n_rows, row0, in_dim, out_dim, xd, ws=ws)
         if host:
+            ws_status(ws)  # synchronous, like the reference: report a flagged workspace here
             y = yd.cpu().numpy()
             if dst is not None:
                 dst[:out_dim] = y
@@ -573,8 +620,10 @@ class WeightStore:
         host = isinstance(X, np.ndarray)
         Xd = torch.from_numpy(np.ascontiguousarray(X, np.float32).reshape(n_tok, in_dim)).to(self.device) \
             if host else X.reshape(n_tok, in_dim)
-        Yd = matmul(t64, n_rows, row0, in_dim, out_dim, Xd, ws=self._workspace(in_dim, out_dim, n_tok))
+        ws = self._workspace(in_dim, out_dim, n_tok)
+        Yd = matmul(t64, n_rows, row0, in_dim, out_dim, Xd, ws=ws)
         if host:
+            ws_status(ws)
             y = Yd.cpu().numpy()
             if Y is not None:
                 Y.reshape(n_tok, out_dim)[:] = y

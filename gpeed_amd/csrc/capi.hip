@@ -1,4 +1,5 @@
 // C ABI (include/gpeed_iq3.h) over the gfx950 kernels.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -213,6 +214,55 @@ int gpeed_init(void) {
     return device_state(&st);
 }
 
+int gpeed_ws_status(void* ws, gpeed_stream_t stream) {
+    if (!ws || !aligned(ws, 16)) return fail(GPEED_ERR_INVALID, "ws_status: null or misaligned workspace");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t flags = 0;
+    hipError_t e = hipMemcpyAsync(&flags, ws, sizeof flags, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "ws_status");
+    if (flags == 0) return GPEED_OK;
+    e = gpeed::launch_fill_zero(ws, 16, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "ws_status: clearing the flags");
+    std::string msg = "ws_status: workspace flagged:";
+    if (flags & gpeed::kWsTicket) msg += " ticket count past the parts of a tile (not initialised or shared)";
+    if (flags & gpeed::kWsTimeout) msg += " a wait for another workgroup's partial gave up";
+    if (flags & gpeed::kWsBuckets) msg += " expert buckets break the router's invariants";
+    return fail(GPEED_ERR_WS_STATE, msg);
+}
+
+int gpeed_ws_init(void* ws, size_t ws_bytes, gpeed_stream_t stream) {
+    if (ws_bytes == 0) return GPEED_OK;
+    if (!ws || !aligned(ws, 16) || ws_bytes % 16)
+        return fail(GPEED_ERR_INVALID, "ws_init: workspace null, not 16-byte aligned or not a multiple of 16 bytes");
+    hipError_t e = gpeed::launch_fill_zero(ws, ws_bytes, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "ws_init launch");
+}
+
+int gpeed_moe_check_buckets(const int* eptr, const int* tok, int n_exp, int n_tok, int top_k) {
+    if (!eptr || (!tok && n_tok > 0)) return fail(GPEED_ERR_INVALID, "moe_check_buckets: null pointer");
+    if (n_exp < 1 || top_k < 1 || n_tok < 0) return fail(GPEED_ERR_INVALID, "moe_check_buckets: bad sizes");
+    const long long n = (long long)n_tok * top_k;
+    if (eptr[0] != 0) return fail(GPEED_ERR_INVALID, "moe_check_buckets: eptr[0] != 0");
+    for (int e = 0; e < n_exp; ++e)
+        if (eptr[e + 1] < eptr[e])
+            return fail(GPEED_ERR_INVALID, "moe_check_buckets: eptr decreases at expert " + std::to_string(e));
+    if (eptr[n_exp] != n) return fail(GPEED_ERR_INVALID, "moe_check_buckets: eptr[n_exp] != n_tok * top_k");
+    std::vector<int> cnt((size_t)n_tok, 0);
+    for (long long p = 0; p < n; ++p) {
+        const int t = tok[p];
+        if (t < 0 || t >= n_tok)
+            return fail(GPEED_ERR_INVALID, "moe_check_buckets: tok[" + std::to_string(p) + "] out of range");
+        ++cnt[(size_t)t];
+    }
+    for (int t = 0; t < n_tok; ++t)
+        if (cnt[(size_t)t] != top_k)
+            return fail(GPEED_ERR_INVALID, "moe_check_buckets: token " + std::to_string(t) + " appears " +
+                                               std::to_string(cnt[(size_t)t]) + " times, not top_k");
+    return GPEED_OK;
+}
+
 size_t gpeed_iq3xxs_row_bytes(int64_t in_dim) {
     if (in_dim <= 0 || in_dim % gpeed::kQK) return 0;
     return gpeed::iq3_row_bytes(in_dim);
@@ -291,15 +341,54 @@ size_t gpeed_iq3xxs_gemv_ws_bytes(int n_tensors, int64_t in_dim, int64_t out_dim
     if (!dims_ok(in_dim) || out_dim <= 0 || out_dim > (1 << 30) || n_tensors < 1 || n_tensors > 2 ||
         n_tok < 1 || n_tok > kMaxTok)
         return 0;
-    return gpeed::gemv_ws_bytes(n_tensors, (int)in_dim, (int)out_dim, n_tok);
+    return gpeed::kWsHeader + gpeed::gemv_ws_bytes(n_tensors, (int)in_dim, (int)out_dim, n_tok);
+}
+
+// From this many tokens matmul runs the prefill GEMM (W read once) instead of
+// ceil(n_tok / 8) GEMV passes (W read once per pass). Measured on MI355X over
+// the 576..12288-row shapes of the decode mix and the dense MLP.
+constexpr int kMatmulGemmMinTok = 16;
+
+int gpeed_iq3xxs_matmul_gemm_min_tok(void) { return kMatmulGemmMinTok; }
+
+// Layout of a matvec / matmul workspace:
+//   [0, kWsHeader)        header (error word)
+//   [kWsHeader, front)    GEMV tickets and tagged partials, indexed so that a
+//                         region sized for 8 tokens covers every token count
+//   [front, ...)          per-call scratch: prepared activations of an 8-token
+//                         pass, or the prefill GEMM's images and partials
+// The front region of a matvec workspace is sized for one token; a matmul
+// workspace's for 8, and its tail for the largest need of any token count
+// up to the one it was sized for, so one buffer serves them all.
+static size_t matmul_front(int64_t in_dim, int64_t out_dim, int n_tok) {
+    return gpeed::kWsHeader + align256(gpeed::gemv_ws_bytes(1, (int)in_dim, (int)out_dim, n_tok));
+}
+
+static size_t matmul_tail(int64_t in_dim, int64_t out_dim, int n_tok, int num_cus) {
+    if (n_tok < 2) return 0;
+    size_t t = align256(gpeed::act_bytes((int)in_dim, n_tok < kMaxTok ? n_tok : kMaxTok));
+    if (n_tok >= kMatmulGemmMinTok) {
+        // the GEMM's partials change only where the token tile count does
+        // (64-token tiles up to 64 tokens, 128-token tiles above), and its
+        // images grow with the tokens: the largest need up to n_tok is at
+        // one of those boundaries or at n_tok itself
+        auto g = [&](int m) {
+            return align256(gpeed::gemm_ws_bytes(m, (int)out_dim, (int)in_dim, 0, num_cus));
+        };
+        size_t best = g(n_tok);
+        for (int m = 64; m < n_tok; m += (m < 128 ? 64 : 128))
+            if (m >= kMatmulGemmMinTok) best = std::max(best, g(m));
+        t = std::max(t, best);
+    }
+    return t;
 }
 
 size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok) {
-    if (n_tok < 1) return 0;
-    const int nt = n_tok < kMaxTok ? n_tok : kMaxTok;
-    const size_t a = gpeed_iq3xxs_act_bytes(in_dim, nt), w = gpeed_iq3xxs_gemv_ws_bytes(1, in_dim, out_dim, nt);
-    if (!a || !w) return 0;
-    return align256(a) + w;
+    if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(in_dim) || out_dim <= 0 || out_dim > (1 << 24)) return 0;
+    if (n_tok == 1) return matmul_front(in_dim, out_dim, 1);
+    const DeviceState* st = nullptr;
+    if (device_state(&st)) return 0;
+    return matmul_front(in_dim, out_dim, kMaxTok) + matmul_tail(in_dim, out_dim, n_tok, st->num_cus);
 }
 
 size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim, int64_t out_dim) {
@@ -362,7 +451,8 @@ static int gemv_n(const void* const* w, float* const* dst, int n_tensors, uint64
     if (!aligned(act, 16)) return fail(GPEED_ERR_WORKSPACE, "gemv: activation misaligned");
     if (row0 % gpeed::kTileRows)
         return fail(GPEED_ERR_LAYOUT, "gemv: row0 must be a multiple of 64 on the T64 layout");
-    if (!ws || !aligned(ws, 16) || ws_bytes < gpeed::gemv_ws_bytes(n_tensors, in_dim, out_dim, n_tok))
+    if (!ws || !aligned(ws, 256) ||
+        ws_bytes < gpeed::kWsHeader + gpeed::gemv_ws_bytes(n_tensors, in_dim, out_dim, n_tok))
         return fail(GPEED_ERR_WORKSPACE, "gemv: workspace missing, misaligned or too small");
     const DeviceState* st = nullptr;
     int rc = device_state(&st);
@@ -371,7 +461,8 @@ static int gemv_n(const void* const* w, float* const* dst, int n_tensors, uint64
                             static_cast<const uint8_t*>(w[n_tensors > 1 ? 1 : 0])};
     float* yp[2] = {dst[0], dst[n_tensors > 1 ? 1 : 0]};
     hipError_t e = gpeed::launch_gemv_t64(wp, yp, n_tensors, in_dim, row0, out_dim, n_tok,
-                                          static_cast<const uint8_t*>(act), static_cast<uint8_t*>(ws),
+                                          static_cast<const uint8_t*>(act),
+                                          static_cast<uint8_t*>(ws) + gpeed::kWsHeader, static_cast<uint32_t*>(ws),
                                           st->num_cus, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemv launch");
 }
@@ -405,14 +496,15 @@ static int gemv_x_n(const void* const* w, float* const* dst, int n_tensors, uint
         return fail(GPEED_ERR_INVALID, std::string(who) + ": input not 16-byte aligned");
     if (row0 % gpeed::kTileRows)
         return fail(GPEED_ERR_LAYOUT, std::string(who) + ": row0 must be a multiple of 64 on the T64 layout");
-    if (!ws || !aligned(ws, 16) || ws_bytes < gpeed::gemv_ws_bytes(n_tensors, in_dim, out_dim, 1))
+    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::kWsHeader + gpeed::gemv_ws_bytes(n_tensors, in_dim, out_dim, 1))
         return fail(GPEED_ERR_WORKSPACE, std::string(who) + ": workspace missing, misaligned or too small");
     const DeviceState* st = nullptr;
     int rc = device_state(&st);
     if (rc) return rc;
     const uint8_t* wp[2] = {static_cast<const uint8_t*>(w[0]), static_cast<const uint8_t*>(w[n_tensors > 1 ? 1 : 0])};
     float* yp[2] = {dst[0], dst[n_tensors > 1 ? 1 : 0]};
-    hipError_t e = gpeed::launch_gemv_x(wp, yp, n_tensors, in_dim, row0, out_dim, x, x2, lim, static_cast<uint8_t*>(ws),
+    hipError_t e = gpeed::launch_gemv_x(wp, yp, n_tensors, in_dim, row0, out_dim, x, x2, lim,
+                                        static_cast<uint8_t*>(ws) + gpeed::kWsHeader, static_cast<uint32_t*>(ws),
                                         st->num_cus, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GPEED_OK : hip_fail(e, std::string(who + std::string(" launch")).c_str());
 }
@@ -470,24 +562,40 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
                         const float* X, int n_tok, float* Y, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream) {
     if (n_tok <= 0 || out_dim <= 0) return GPEED_OK;  // weights.cpp:88
+    if (n_tok == 1) return gpeed_iq3xxs_matvec(w_t64, n_rows, row0, in_dim, out_dim, X, Y, ws, ws_bytes, stream);
     int rc = check_mv_args(w_t64, n_rows, row0, in_dim, out_dim, X, Y, "matmul");
     if (rc) return rc;
+    if (n_tok > (1 << 20)) return fail(GPEED_ERR_INVALID, "matmul: n_tok too large");
     if (row0 % gpeed::kTileRows)
         return fail(GPEED_ERR_LAYOUT, "matmul: row0 must be a multiple of 64 on the T64 layout");
+    if (!aligned(w_t64, 16) || !aligned(X, 16)) return fail(GPEED_ERR_INVALID, "matmul: misaligned operand");
     const size_t need = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, n_tok);
     if (!ws || !aligned(ws, 256) || ws_bytes < need)
         return fail(GPEED_ERR_WORKSPACE, "matmul: workspace missing, misaligned or too small");
-    const int nt_max = n_tok < kMaxTok ? n_tok : kMaxTok;
-    const size_t a_bytes = align256(gpeed::act_bytes(in_dim, nt_max));
-    uint8_t* act = static_cast<uint8_t*>(ws);
-    uint8_t* gws = act + a_bytes;
+    const DeviceState* st = nullptr;
+    rc = device_state(&st);
+    if (rc) return rc;
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    uint32_t* err = static_cast<uint32_t*>(ws);
+    uint8_t* tail = base + matmul_front(in_dim, out_dim, kMaxTok);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t* w = static_cast<const uint8_t*>(w_t64);
+    if (n_tok >= kMatmulGemmMinTok) {
+        // one pass over W for all tokens (model_batch.cpp:30-95, 151-162 at
+        // prefill chunk sizes)
+        const hipError_t e = gpeed::launch_gemm(w, row0, in_dim, out_dim, X, 0, n_tok, Y, tail, err, st->num_cus, s);
+        if (e == hipErrorInvalidValue) return fail(GPEED_ERR_INVALID, "matmul: tensor slice of 4 GiB or more");
+        return e == hipSuccess ? GPEED_OK : hip_fail(e, "matmul gemm launch");
+    }
+    const uint8_t* wp[2] = {w, w};
     for (int t0 = 0; t0 < n_tok; t0 += kMaxTok) {
         const int nt = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
-        rc = gpeed_iq3xxs_prep_act(X + (size_t)t0 * in_dim, in_dim, nt, act, a_bytes, stream);
-        if (rc) return rc;
-        rc = gpeed_iq3xxs_gemv_act(w_t64, n_rows, row0, in_dim, out_dim, act, nt, Y + (size_t)t0 * out_dim,
-                                   gws, ws_bytes - a_bytes, stream);
-        if (rc) return rc;
+        float* yp[2] = {Y + (size_t)t0 * out_dim, Y + (size_t)t0 * out_dim};
+        hipError_t e = gpeed::launch_prep_act(X + (size_t)t0 * in_dim, in_dim, nt, tail, s);
+        if (e == hipSuccess)
+            e = gpeed::launch_gemv_t64(wp, yp, 1, in_dim, row0, out_dim, nt, tail, base + gpeed::kWsHeader, err,
+                                       st->num_cus, s);
+        if (e != hipSuccess) return hip_fail(e, "matmul gemv launch");
     }
     return GPEED_OK;
 }
@@ -495,18 +603,15 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
 int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* x, float* dst, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream) {
-    // one launch (activation prepared inside the GEMV)
-    if (in_dim > 0 && in_dim % gpeed::kQK == 0) {
-        if (out_dim <= 0) return GPEED_OK;
-        const size_t need = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, 1);
-        if (!ws || !aligned(ws, 256) || ws_bytes < need)
-            return fail(GPEED_ERR_WORKSPACE, "matvec: workspace missing, misaligned or too small");
-        // same workspace layout as matmul: [activation images][GEMV tickets/partials]
-        const size_t a_bytes = align256(gpeed::act_bytes(in_dim, 1));
-        return gpeed_iq3xxs_gemv_x(w_t64, n_rows, row0, in_dim, out_dim, x, dst, static_cast<uint8_t*>(ws) + a_bytes,
-                                   ws_bytes - a_bytes, stream);
-    }
-    return gpeed_iq3xxs_matmul(w_t64, n_rows, row0, in_dim, out_dim, x, 1, dst, ws, ws_bytes, stream);
+    // one launch (activation prepared inside the GEMV), on the front region
+    // of a matvec / matmul workspace
+    if (out_dim <= 0) return GPEED_OK;  // weights.cpp:88
+    if (in_dim <= 0 || in_dim % gpeed::kQK) return fail(GPEED_ERR_UNALIGNED_ROW, "matvec: row not block aligned");
+    if (!dims_ok(in_dim)) return fail(GPEED_ERR_INVALID, "matvec: size too large");
+    const size_t need = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, 1);
+    if (!ws || !aligned(ws, 256) || ws_bytes < need)
+        return fail(GPEED_ERR_WORKSPACE, "matvec: workspace missing, misaligned or too small");
+    return gpeed_iq3xxs_gemv_x(w_t64, n_rows, row0, in_dim, out_dim, x, dst, ws, need, stream);
 }
 
 size_t gpeed_moe_route_ws_bytes(int n_tok, int n_exp, int top_k) {
@@ -570,7 +675,8 @@ size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_dim
         return 0;
     const DeviceState* st = nullptr;
     if (device_state(&st)) return 0;
-    return gpeed::gemm_ws_bytes((int)n_tok, (int)out_dim, (int)in_dim, x_dtype == GPEED_X_BF16, st->num_cus);
+    return gpeed::kWsHeader +
+           gpeed::gemm_ws_bytes((int)n_tok, (int)out_dim, (int)in_dim, x_dtype == GPEED_X_BF16, st->num_cus);
 }
 
 int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const void* X,
@@ -587,11 +693,12 @@ int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_
     rc = device_state(&st);
     if (rc) return rc;
     if (!ws || !aligned(ws, 256) ||
-        ws_bytes < gpeed::gemm_ws_bytes(n_tok, out_dim, in_dim, x_dtype == GPEED_X_BF16, st->num_cus))
+        ws_bytes < gpeed::kWsHeader + gpeed::gemm_ws_bytes(n_tok, out_dim, in_dim, x_dtype == GPEED_X_BF16, st->num_cus))
         return fail(GPEED_ERR_WORKSPACE, "gemm: workspace missing, misaligned or too small");
     hipError_t e = gpeed::launch_gemm(static_cast<const uint8_t*>(w_t64), row0, in_dim, out_dim, X,
-                                      x_dtype == GPEED_X_BF16, n_tok, Y, static_cast<uint8_t*>(ws), st->num_cus,
-                                      static_cast<hipStream_t>(stream));
+                                      x_dtype == GPEED_X_BF16, n_tok, Y, static_cast<uint8_t*>(ws) + gpeed::kWsHeader,
+                                      static_cast<uint32_t*>(ws), st->num_cus, static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue) return fail(GPEED_ERR_INVALID, "gemm: tensor slice of 4 GiB or more");
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm launch");
 }
 
@@ -601,8 +708,8 @@ size_t gpeed_iq3xxs_gemm2_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_a,
         return 0;
     const DeviceState* st = nullptr;
     if (device_state(&st)) return 0;
-    return gpeed::gemm2_ws_bytes((int)n_tok, (int)out_a, (int)out_b, (int)in_dim, x_dtype == GPEED_X_BF16,
-                                 st->num_cus);
+    return gpeed::kWsHeader + gpeed::gemm2_ws_bytes((int)n_tok, (int)out_a, (int)out_b, (int)in_dim,
+                                                    x_dtype == GPEED_X_BF16, st->num_cus);
 }
 
 int gpeed_iq3xxs_gemm2(const void* w_a, uint64_t n_rows_a, uint64_t row0_a, int out_a, const void* w_b,
@@ -628,12 +735,15 @@ int gpeed_iq3xxs_gemm2(const void* w_a, uint64_t n_rows_a, uint64_t row0_a, int 
     rc = device_state(&st);
     if (rc) return rc;
     if (!ws || !aligned(ws, 256) ||
-        ws_bytes < gpeed::gemm2_ws_bytes(n_tok, out_a, out_b, in_dim, x_dtype == GPEED_X_BF16, st->num_cus))
+        ws_bytes < gpeed::kWsHeader +
+                       gpeed::gemm2_ws_bytes(n_tok, out_a, out_b, in_dim, x_dtype == GPEED_X_BF16, st->num_cus))
         return fail(GPEED_ERR_WORKSPACE, "gemm2: workspace missing, misaligned or too small");
     hipError_t e = gpeed::launch_gemm2(static_cast<const uint8_t*>(w_a), row0_a, out_a,
                                        static_cast<const uint8_t*>(w_b), row0_b, out_b, in_dim, X,
-                                       x_dtype == GPEED_X_BF16, n_tok, Y_a, Y_b, static_cast<uint8_t*>(ws),
+                                       x_dtype == GPEED_X_BF16, n_tok, Y_a, Y_b,
+                                       static_cast<uint8_t*>(ws) + gpeed::kWsHeader, static_cast<uint32_t*>(ws),
                                        st->num_cus, static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue) return fail(GPEED_ERR_INVALID, "gemm2: tensor slice of 4 GiB or more");
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm2 launch");
 }
 
@@ -652,11 +762,13 @@ int gpeed_iq3xxs_gemm_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, 
     const DeviceState* st = nullptr;
     rc = device_state(&st);
     if (rc) return rc;
-    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::gemm_ws_bytes(n_tok, out_dim, in_dim, 0, st->num_cus))
+    if (!ws || !aligned(ws, 256) ||
+        ws_bytes < gpeed::kWsHeader + gpeed::gemm_ws_bytes(n_tok, out_dim, in_dim, 0, st->num_cus))
         return fail(GPEED_ERR_WORKSPACE, "gemm_swiglu: workspace missing, misaligned or too small");
     hipError_t e = gpeed::launch_gemm(static_cast<const uint8_t*>(w_t64), row0, in_dim, out_dim, G, 0, n_tok, Y,
-                                      static_cast<uint8_t*>(ws), st->num_cus, static_cast<hipStream_t>(stream), U,
-                                      limit);
+                                      static_cast<uint8_t*>(ws) + gpeed::kWsHeader, static_cast<uint32_t*>(ws),
+                                      st->num_cus, static_cast<hipStream_t>(stream), U, limit);
+    if (e == hipErrorInvalidValue) return fail(GPEED_ERR_INVALID, "gemm_swiglu: tensor slice of 4 GiB or more");
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm_swiglu launch");
 }
 

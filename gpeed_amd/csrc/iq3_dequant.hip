@@ -157,7 +157,23 @@ __global__ __launch_bounds__(256) void k_add(const float* __restrict__ a, const 
     if (i < n) d[i] = a[i] + b[i];
 }
 
+// n16 16-byte words set to zero, grid-stride.
+__global__ __launch_bounds__(256) void k_fill_zero(u32x4_t* __restrict__ p, unsigned long long n16) {
+    const unsigned long long stride = (unsigned long long)gridDim.x * 256;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+        p[i] = u32x4_t{0u, 0u, 0u, 0u};
+}
+
 }  // namespace
+
+hipError_t launch_fill_zero(void* p, size_t n, hipStream_t s) {
+    const unsigned long long n16 = n / 16;
+    if (n16 == 0) return hipSuccess;
+    unsigned long long grid = (n16 + 255) / 256;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)grid), dim3(256), 0, s, static_cast<u32x4_t*>(p), n16);
+    return hipGetLastError();
+}
 
 hipError_t launch_stream_read(const uint8_t* p, unsigned long long bytes, uint32_t* out, int n_groups,
                               hipStream_t s) {

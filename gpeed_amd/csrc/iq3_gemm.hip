@@ -42,12 +42,16 @@ __device__ __forceinline__ uint32_t f16_pair_of_floats(float lo, float hi) {
 // X -> fp16 images with a power-of-two scale per token row. One workgroup per
 // row. IN = 0: fp32 input (hi and lo images); IN = 1: bf16 input (one image);
 // IN = 2: X = SwiGLU(X, U) of fp32 gate and up rows (hi and lo images).
+// The workgroups also clear the n_cnt split-K tickets of the GEMM launch
+// that follows on the same stream, so a workspace needs no initialisation.
 template <int IN>
 __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X, const float* __restrict__ U,
                                                      float lim, int M, int K, _Float16* __restrict__ xh,
-                                                     float* __restrict__ unscale) {
+                                                     float* __restrict__ unscale, uint32_t* __restrict__ cnt,
+                                                     int n_cnt) {
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
+    for (int i = m * 256 + tid; i < n_cnt; i += M * 256) cnt[i] = 0u;
     __shared__ float red[4];
     // 8 consecutive values per access (16-byte loads; K is a multiple of 256)
     auto ld8 = [&](int c, float (&v)[8]) {
@@ -113,8 +117,9 @@ struct GemmArgs {
     int M, N, K, nb;
     int tiles_m, tiles_n;   // tiles_n: result tiles of both tensors
     int ks;                 // K splits per result tile (1: no partials)
-    uint32_t* cnt;          // ks > 1: tickets per tile (zero between launches)
+    uint32_t* cnt;          // ks > 1: tickets per tile (cleared by k_gemm_prep_x)
     float* part;            // ks > 1: [tile][split][128][192] fp32 partials
+    uint32_t* err;          // the workspace's error word (kWs* flags)
     // a second tensor on the same X: result tiles tn >= tiles_n1 are its
     // tiles tn - tiles_n1 (w2, y2 [M][N2]); tiles_n1 = tiles_n for one tensor
     const uint8_t* w2;
@@ -169,6 +174,19 @@ __device__ __forceinline__ GemmArgs gemm_tensor(const GemmArgs& g, const GemmTil
 // device-coherent stores; after vmcnt(0) it takes the tile's ticket, and
 // the last one adds the partials in split order (bitwise repeatable) and
 // writes Y, then clears the ticket.
+//
+// Why this hand-off is ordered without release/acquire fences (gfx950
+// memory model): the partials are agent-scope atomic stores, which the
+// compiler emits as stores that write through this XCD's L2 (sc1) instead
+// of leaving dirty lines there; s_waitcnt vmcnt(0) returns only once every
+// one of them is acknowledged by memory; the ticket is an agent-scope
+// atomic performed at memory after that, so a split that sees the last
+// ticket value sees every earlier split's completed stores; and the reader
+// loads with sc1, missing in its own L2, which can hold stale lines of the
+// workspace from an earlier call. A release fence would add a write-back of
+// all of this XCD's dirty L2 lines (other tiles' Y) that no reader needs. A
+// ticket past the split count (two launches sharing the workspace) sets
+// kWsTicket.
 template <int MT>
 __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t, const float4_t (&acc)[MT][3],
                                            int m0, int n0, int wave, int lr, int lg, int tid, int* flag) {
@@ -211,6 +229,7 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
     if (tid == 0) {
         const uint32_t old = __hip_atomic_fetch_add(g.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *flag = old == (uint32_t)(g.ks - 1);
+        if (old >= (uint32_t)g.ks) __hip_atomic_fetch_or(g.err, kWsTicket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!*flag) return;  // uniform
@@ -774,21 +793,33 @@ size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus) {
 
 hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, const uint8_t* wb,
                         unsigned long long row0b, int out_b, int in_dim, const void* X, int x_bf16, int M, float* Ya,
-                        float* Yb, uint8_t* ws, int num_cus, hipStream_t s, const float* U, float lim) {
+                        float* Yb, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s, const float* U,
+                        float lim) {
     if (M <= 0 || out_a <= 0) return hipSuccess;
     if (!wb) out_b = 0;
     const int tiles_a = (out_a + kTileN - 1) / kTileN, tiles_b = (out_b + kTileN - 1) / kTileN;
+    // record offsets inside a tensor's requested rows are 32-bit
+    const size_t nb_sz = (size_t)(in_dim / kQK);
+    if ((size_t)tiles_a * 3 * nb_sz * kRecordBytes >= (1ull << 32) ||
+        (size_t)tiles_b * 3 * nb_sz * kRecordBytes >= (1ull << 32))
+        return hipErrorInvalidValue;
     const int n_eq = (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
     const int ks = gemm_splits(M, n_eq, in_dim, num_cus);
     const GemmWs L = gemm_ws(M, n_eq, in_dim, x_bf16, ks);
     _Float16* xh = reinterpret_cast<_Float16*>(ws + L.img);
     float* uns = reinterpret_cast<float*>(ws + L.uns);
+    const int bm = gemm_tile_m(M);
+    const int tiles_m = (M + bm - 1) / bm;
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
+    const int n_cnt = ks > 1 ? tiles_m * (tiles_a + tiles_b) : 0;
     if (x_bf16)
-        hipLaunchKernelGGL(k_gemm_prep_x<1>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns);
+        hipLaunchKernelGGL(k_gemm_prep_x<1>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns, cnt,
+                           n_cnt);
     else if (U)
-        hipLaunchKernelGGL(k_gemm_prep_x<2>, dim3(M), dim3(256), 0, s, X, U, lim, M, in_dim, xh, uns);
+        hipLaunchKernelGGL(k_gemm_prep_x<2>, dim3(M), dim3(256), 0, s, X, U, lim, M, in_dim, xh, uns, cnt, n_cnt);
     else
-        hipLaunchKernelGGL(k_gemm_prep_x<0>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns);
+        hipLaunchKernelGGL(k_gemm_prep_x<0>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns, cnt,
+                           n_cnt);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmArgs a{};
@@ -800,16 +831,16 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     a.M = M;
     a.N = out_a;
     a.K = in_dim;
-    const int bm = gemm_tile_m(M);
-    a.tiles_m = (M + bm - 1) / bm;
+    a.tiles_m = tiles_m;
     a.tiles_n1 = tiles_a;
     a.tiles_n = tiles_a + tiles_b;
     a.w2 = out_b > 0 ? wb + (size_t)(row0b / kTileRows) * a.nb * kRecordBytes : a.w;
     a.y2 = out_b > 0 ? Yb : Ya;
     a.N2 = out_b > 0 ? out_b : out_a;
     a.ks = ks;
-    a.cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
+    a.cnt = cnt;
     a.part = reinterpret_cast<float*>(ws + L.part);
+    a.err = err;
     const int grid = a.tiles_n * a.tiles_m * ks;
     const dim3 gd(grid), bd(kGemmThreads);
     if (bm == 64)
@@ -820,8 +851,10 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
 }
 
 hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
-                       int M, float* Y, uint8_t* ws, int num_cus, hipStream_t s, const float* U, float lim) {
-    return launch_gemm2(w, row0, out_dim, nullptr, 0, 0, in_dim, X, x_bf16, M, Y, nullptr, ws, num_cus, s, U, lim);
+                       int M, float* Y, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s, const float* U,
+                       float lim) {
+    return launch_gemm2(w, row0, out_dim, nullptr, 0, 0, in_dim, X, x_bf16, M, Y, nullptr, ws, err, num_cus, s, U,
+                        lim);
 }
 
 size_t gemm2_ws_bytes(int M, int out_a, int out_b, int K, int x_bf16, int num_cus) {

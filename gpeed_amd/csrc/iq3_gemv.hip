@@ -149,6 +149,7 @@ struct GemvArgs {
     const float* xsc;      // MODE 0: [nb][n_tok]; MODE 3: [nb][4] unscales
     uint32_t* cnt;         // tickets (zero between launches)
     uint64_t* part;        // chunk partials of shared tiles (tagged words)
+    uint32_t* err;         // the workspace's error word (kWs* flags)
     int nb;
     int n_tiles;           // row tiles per tensor
     int n_records;         // n_tensors * n_tiles * nb
@@ -393,9 +394,7 @@ __device__ __forceinline__ void gemv_stream(GemvShared<NT, shared_layout<MODE>()
             const int kk = k - kbeg;  // index within this phase
             const bool valid = k >= kbeg && k < kend;
             const int rec = ch.rec(kk, wave, W);
-            const int tile = rec / g.nb;
-            const int b = rec - tile * g.nb;
-            const int slot = tile - ch.tile0;
+            const int slot = rec / g.nb - ch.tile0;
             if (valid && slot != cur_slot) {
                 if (cur_slot >= 0) {
 #pragma unroll
@@ -446,14 +445,21 @@ __device__ __forceinline__ void gemv_stream(GemvShared<NT, shared_layout<MODE>()
 // Shared-tile partials. A tile (or gate/up pair) cut by chunk boundaries
 // has one part per chunk; each part's values are published as tagged 64-bit
 // words (value bits | 1 << 32, single-copy atomic), so a reader knows a
-// value has landed without waiting for the writer's stores to complete.
+// value has landed without waiting for the writer's stores to complete
+// (the tag is the only ordering the hand-off needs: no fence is required).
 // The workgroup that takes the unit's last ticket (one relaxed atomic per
 // unit, issued right after its own words) sums the parts in part order;
 // another part's word not yet landed is read again (its writer issued it
 // before taking its ticket, so it lands: the bound only guards against a
-// corrupted workspace). The summing workgroup clears the words and the
-// ticket, leaving the workspace zero for the next launch.
+// corrupted or shared workspace, and giving up sets kWsTimeout). A ticket
+// beyond the unit's part count (a workspace not zero-filled, or shared by
+// overlapping launches) sets kWsTicket. The summing workgroup clears the
+// words and the ticket, leaving the workspace zero for the next launch.
 constexpr int kTagSpin = 1 << 20;
+
+__device__ __forceinline__ void flag_ws(uint32_t* err, uint32_t bits) {
+    __hip_atomic_fetch_or(err, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ void put_tagged(uint64_t* p, float v) {
     __hip_atomic_store(p, (1ull << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
@@ -470,7 +476,7 @@ __device__ __forceinline__ uint64_t get_tagged(const uint64_t* p) {
 template <int NT>
 __device__ __forceinline__ void sum_tagged_parts(uint64_t* p, size_t part_stride, const int (&j0)[NT],
                                                  const int (&j1)[NT], int me, const float (&mine)[NT],
-                                                 float (&acc)[NT]) {
+                                                 float (&acc)[NT], uint32_t* err) {
     int lo = j0[0], hi = j1[0];
 #pragma unroll
     for (int t = 1; t < NT; ++t) {
@@ -499,6 +505,7 @@ __device__ __forceinline__ void sum_tagged_parts(uint64_t* p, size_t part_stride
                     uint64_t w = v[i][t];
                     for (int spin = 0; (w >> 32) == 0 && spin < kTagSpin; ++spin)
                         w = get_tagged(p + j * part_stride + t * 64);
+                    if ((w >> 32) == 0) flag_ws(err, kWsTimeout);
                     x = __builtin_bit_cast(float, (uint32_t)w);
                 }
                 acc[t] += x;
@@ -511,10 +518,14 @@ __device__ __forceinline__ void sum_tagged_parts(uint64_t* p, size_t part_stride
             __hip_atomic_store(p + j * part_stride + t * 64, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Ticket of a shared unit, taken by lane 0 and returned to the wavefront.
-__device__ __forceinline__ uint32_t take_ticket(uint32_t* cnt, uint32_t lane) {
+// Ticket of a shared unit with n_parts parts, taken by lane 0 and returned
+// to the wavefront; a ticket past the last sets kWsTicket.
+__device__ __forceinline__ uint32_t take_ticket(uint32_t* cnt, uint32_t lane, int n_parts, uint32_t* err) {
     uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) {
+        old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old >= (uint32_t)n_parts) flag_ws(err, kWsTicket);
+    }
     return __builtin_amdgcn_readfirstlane(old);
 }
 
@@ -542,7 +553,7 @@ __device__ __forceinline__ void gemv_epilogue_y(GemvShared<NT, shared_layout<MOD
             uint64_t* p = g.part + ((size_t)tile * g.max_parts * NT) * 64 + lane;
 #pragma unroll
             for (int t = 0; t < NT; ++t) put_tagged(p + ((size_t)(blk - first) * NT + t) * 64, sum[t]);
-            if (take_ticket(g.cnt + tile, lane) != (uint32_t)(last - first)) continue;  // uniform
+            if (take_ticket(g.cnt + tile, lane, last - first + 1, g.err) != (uint32_t)(last - first)) continue;
             float tot[NT];
             int j0[NT], j1[NT];
 #pragma unroll
@@ -550,7 +561,7 @@ __device__ __forceinline__ void gemv_epilogue_y(GemvShared<NT, shared_layout<MOD
                 j0[t] = 0;
                 j1[t] = last - first;
             }
-            sum_tagged_parts<NT>(p, (size_t)NT * 64, j0, j1, blk - first, sum, tot);
+            sum_tagged_parts<NT>(p, (size_t)NT * 64, j0, j1, blk - first, sum, tot, g.err);
 #pragma unroll
             for (int t = 0; t < NT; ++t) sum[t] = tot[t];
             if (lane == 0) __hip_atomic_store(g.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -607,8 +618,8 @@ __device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const
                     put_tagged(p + ((size_t)me * 2 + h) * 64, mine[h]);
                 }
             }
-            if (take_ticket(g.cnt + pr, lane) != (uint32_t)(last - first)) continue;  // uniform
-            sum_tagged_parts<2>(p, 2 * 64, j0, j1, me, mine, v);
+            if (take_ticket(g.cnt + pr, lane, last - first + 1, g.err) != (uint32_t)(last - first)) continue;
+            sum_tagged_parts<2>(p, 2 * 64, j0, j1, me, mine, v, g.err);
             if (lane == 0) __hip_atomic_store(g.cnt + pr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         const float hv = swiglu1(v[0], v[1], g.lim);
@@ -731,7 +742,7 @@ hipError_t launch_gemv_nt(const GemvPlan& plan, GemvArgs a, hipStream_t s) {
 constexpr int max_chunk_slots(int slots, int nb) { return (slots - 1) * nb + 1; }
 
 GemvArgs base_args(const GemvPlan& plan, const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
-                   unsigned long long row0, int out_dim, uint8_t* ws) {
+                   unsigned long long row0, int out_dim, uint8_t* ws, uint32_t* err) {
     GemvArgs a{};
     a.nb = in_dim / kQK;
     const size_t skip = (size_t)(row0 / kTileRows) * a.nb * kRecordBytes;
@@ -745,6 +756,7 @@ GemvArgs base_args(const GemvPlan& plan, const uint8_t* const* w, float* const* 
     a.out_dim = out_dim;
     a.cnt = reinterpret_cast<uint32_t*>(ws);
     a.part = reinterpret_cast<uint64_t*>(ws + ((size_t)plan.n_tiles_all * 4 + 255) / 256 * 256);
+    a.err = err;
     a.w_bytes = (uint32_t)((size_t)a.n_tiles * a.nb * kRecordBytes);
     return a;
 }
@@ -817,10 +829,10 @@ size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok) {
 
 hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                            unsigned long long row0, int out_dim, int n_tok, const uint8_t* act,
-                           uint8_t* ws, int num_cus, hipStream_t s) {
+                           uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s) {
     const GemvPlan plan = plan_gemv(n_tensors, in_dim, out_dim, n_tok, num_cus, kPlanAct);
     if (plan.grid == 0) return hipSuccess;
-    GemvArgs a = base_args(plan, w, y, n_tensors, in_dim, row0, out_dim, ws);
+    GemvArgs a = base_args(plan, w, y, n_tensors, in_dim, row0, out_dim, ws, err);
     a.act = act;
     a.xsc = reinterpret_cast<const float*>(act + (size_t)a.nb * n_tok * 1024);
     switch (n_tok) {
@@ -838,10 +850,10 @@ hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tenso
 
 hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                          unsigned long long row0, int out_dim, const float* x, const float* x2, float lim,
-                         uint8_t* ws, int num_cus, hipStream_t s) {
+                         uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s) {
     const GemvPlan plan = plan_gemv(n_tensors, in_dim, out_dim, 1, num_cus, kPlanPrep);
     if (plan.grid == 0) return hipSuccess;
-    GemvArgs a = base_args(plan, w, y, n_tensors, in_dim, row0, out_dim, ws);
+    GemvArgs a = base_args(plan, w, y, n_tensors, in_dim, row0, out_dim, ws, err);
     a.x = x;
     a.x2 = x2;
     a.lim = lim;
@@ -859,13 +871,13 @@ size_t gate_up_ws_bytes(int in_dim, int out_dim) {
 }
 
 hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int in_dim, int out_dim,
-                                 const float* x, float lim, uint8_t* act_out, uint8_t* ws, int num_cus,
-                                 hipStream_t s) {
+                                 const float* x, float lim, uint8_t* act_out, uint8_t* ws, uint32_t* err,
+                                 int num_cus, hipStream_t s) {
     if (out_dim % kQK) return hipErrorInvalidValue;  // act64 blocks of the output
     const GemvPlan plan = plan_gemv(2, in_dim, out_dim, 1, num_cus, kPlanSwigluPairs);
     if (plan.grid == 0) return hipSuccess;
     const uint8_t* w[2] = {w_gate, w_up};
-    GemvArgs a = base_args(plan, w, nullptr, 2, in_dim, 0, out_dim, ws);
+    GemvArgs a = base_args(plan, w, nullptr, 2, in_dim, 0, out_dim, ws, err);
     a.x = x;
     a.x2 = x;
     a.lim = lim;
@@ -873,29 +885,34 @@ hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int
     return launch_gemv_nt<1, 1, 1>(plan, a, s);
 }
 
+// [header][gate/up region][down region][act64]: the regions that must stay
+// zero between launches come first, the scratch last.
 size_t dense_mlp_ws_bytes(int hidden, int inter) {
     const auto a256 = [](size_t b) { return (b + 255) / 256 * 256; };
-    return a256(act64_bytes(inter)) + a256(gate_up_ws_bytes(hidden, inter)) + a256(gemv_ws_bytes(1, inter, hidden, 1));
+    return kWsHeader + a256(gate_up_ws_bytes(hidden, inter)) + a256(gemv_ws_bytes(1, inter, hidden, 1)) +
+           a256(act64_bytes(inter));
 }
 
 hipError_t launch_dense_mlp(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int hidden, int inter,
                             const float* x, float lim, float* y, uint8_t* ws, int num_cus, hipStream_t s) {
     const auto a256 = [](size_t b) { return (b + 255) / 256 * 256; };
-    uint8_t* act = ws;
-    uint8_t* ws_a = act + a256(act64_bytes(inter));
+    uint32_t* err = reinterpret_cast<uint32_t*>(ws);
+    uint8_t* ws_a = ws + kWsHeader;
     uint8_t* ws_b = ws_a + a256(gate_up_ws_bytes(hidden, inter));
-    hipError_t e = launch_gate_up_swiglu(w_gate, w_up, hidden, inter, x, lim, act, ws_a, num_cus, s);
+    uint8_t* act = ws_b + a256(gemv_ws_bytes(1, inter, hidden, 1));
+    hipError_t e = launch_gate_up_swiglu(w_gate, w_up, hidden, inter, x, lim, act, ws_a, err, num_cus, s);
     if (e != hipSuccess) return e;
-    return launch_gemv_act64(w_down, inter, 0, hidden, act, y, ws_b, num_cus, s);
+    return launch_gemv_act64(w_down, inter, 0, hidden, act, y, ws_b, err, num_cus, s);
 }
 
 hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
-                             const uint8_t* act64, float* y, uint8_t* ws, int num_cus, hipStream_t s) {
+                             const uint8_t* act64, float* y, uint8_t* ws, uint32_t* err, int num_cus,
+                             hipStream_t s) {
     const GemvPlan plan = plan_gemv(1, in_dim, out_dim, 1, num_cus, kPlanPrep);
     if (plan.grid == 0) return hipSuccess;
     float* yy[1] = {y};
     const uint8_t* ww[1] = {w};
-    GemvArgs a = base_args(plan, ww, yy, 1, in_dim, row0, out_dim, ws);
+    GemvArgs a = base_args(plan, ww, yy, 1, in_dim, row0, out_dim, ws, err);
     a.act = act64;
     a.xsc = reinterpret_cast<const float*>(act64 + (size_t)a.nb * 1024);
     return launch_gemv_nt<1, 3>(plan, a, s);

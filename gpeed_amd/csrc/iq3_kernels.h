@@ -8,6 +8,17 @@
 
 namespace gpeed {
 
+// Every product workspace starts with this many bytes of header; word 0
+// collects the error flags below (read by gpeed_ws_status). The launchers
+// take the header's error word and the region after the header.
+constexpr size_t kWsHeader = 256;
+constexpr uint32_t kWsTicket = 1u;   // a ticket counted more arrivals than the unit has parts
+constexpr uint32_t kWsTimeout = 2u;  // a bounded wait for another workgroup's partial gave up
+constexpr uint32_t kWsBuckets = 4u;  // expert buckets break the router's invariants
+
+// Zero-fill of n bytes (16-byte aligned, n a multiple of 16) with a kernel.
+hipError_t launch_fill_zero(void* p, size_t n, hipStream_t s);
+
 // quant.cpp:186-210 over n/256 raw GGUF blocks -> fp32 (bit-exact).
 hipError_t launch_dequant_raw(const uint8_t* src, float* dst, unsigned long long n, hipStream_t s);
 // Streaming read of `bytes` from p (16-byte aligned) by n_groups workgroups;
@@ -42,22 +53,24 @@ struct GemvPlan {
 // the kernel, or prepared in the kernel with the gate/up SwiGLU epilogue).
 enum { kPlanAct = 0, kPlanPrep = 1, kPlanSwigluPairs = 2 };
 GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus, int kind);
-// Workspace of a GEMV launch: tickets for the tiles shared between
-// workgroups, then their partial sums. Zero-filled once before first use;
-// every launch leaves the tickets at zero again.
+// Workspace region of a GEMV launch (after the header): tickets for the
+// tiles shared between workgroups, then their tagged partial sums, indexed
+// so that a region sized for n_tok covers every launch with fewer tokens.
+// Zero-filled once before first use; every launch leaves the words it used
+// at zero again.
 size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok);
 // y_i[t][j] = sum_k W_i[row0+j][k] x_t[k] over the T64 payloads of n_tensors
 // (1 or 2) same-shape tensors sharing one prepared activation of n_tok
 // (1..8) vectors.
 hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                            unsigned long long row0, int out_dim, int n_tok, const uint8_t* act,
-                           uint8_t* ws, int num_cus, hipStream_t s);
+                           uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s);
 // One fp32 vector x, prepared inside the GEMV workgroups
 // (no separate preparation launch); with x2 != null the input is
 // silu(min(x,lim)) * clamp(x2,-lim,lim) (SwiGLU of gate x and up x2).
 hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                          unsigned long long row0, int out_dim, const float* x, const float* x2, float lim,
-                         uint8_t* ws, int num_cus, hipStream_t s);
+                         uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s);
 // Dense-MLP pair of launches (model.cpp:677-690) without a host round trip:
 // launch_gate_up_swiglu runs gate and up (same shape, out_dim rows of
 // in_dim) against one fp32 x, and the workgroup that completes a row tile
@@ -65,17 +78,18 @@ hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors
 // "act64": per 256-element block four fp16 hi/lo images of 64 elements,
 // each with its own power-of-two unscale (act64_bytes(out_dim) bytes).
 // launch_gemv_act64 then multiplies an act64 activation (the down
-// projection). gate_up_ws_bytes: the first launch's workspace (zero-filled
-// once per shape, left at zero by every launch).
+// projection). gate_up_ws_bytes: the first launch's workspace region
+// (zero-filled once, left at zero by every launch).
 size_t act64_bytes(int in_dim);
 size_t gate_up_ws_bytes(int in_dim, int out_dim);
 hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int in_dim, int out_dim,
-                                 const float* x, float lim, uint8_t* act_out, uint8_t* ws, int num_cus,
-                                 hipStream_t s);
+                                 const float* x, float lim, uint8_t* act_out, uint8_t* ws, uint32_t* err,
+                                 int num_cus, hipStream_t s);
 hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
-                             const uint8_t* act64, float* y, uint8_t* ws, int num_cus, hipStream_t s);
-// Both (the act64 buffer, then each launch's tickets and partials in one
-// workspace of dense_mlp_ws_bytes, zero-filled once per shape).
+                             const uint8_t* act64, float* y, uint8_t* ws, uint32_t* err, int num_cus,
+                             hipStream_t s);
+// Both (the header, the act64 buffer, then each launch's tickets and
+// partials in one workspace of dense_mlp_ws_bytes, zero-filled once).
 size_t dense_mlp_ws_bytes(int hidden, int inter);
 hipError_t launch_dense_mlp(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int hidden, int inter,
                             const float* x, float lim, float* y, uint8_t* ws, int num_cus, hipStream_t s);
@@ -94,7 +108,8 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int K, int mode, 
                             uint8_t* ws, hipStream_t s);
 // Routed experts (model_batch.cpp:221-262): gate/up/down of every touched
 // expert over its bucket of tokens, SwiGLU between, weighted combine into
-// Y [T][H] (overwritten). ws: moe_ws_bytes(...) bytes of scratch.
+// Y [T][H] (overwritten). ws: moe_ws_bytes(...) bytes (header included);
+// buckets that break the router's invariants set kWsBuckets and give Y = 0.
 size_t moe_ws_bytes(int T, int E, int K, int H, int I);
 hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int E, int H,
                               int I, const float* X, int T, int K, const int* eptr, const int* tok,
@@ -102,22 +117,24 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
 
 // Prefill GEMM: Y[m][j] = sum_k X[m][k] W[row0+j][k] for M tokens from the
 // T64 copy. X is fp32 (x_bf16 = 0) or bf16 (x_bf16 = 1), row-major [M][in_dim];
-// ws: gemm_ws_bytes(M, out_dim, in_dim, x_bf16, num_cus) bytes (fp16
-// images; when the result tiles fill fewer than half the CUs, K is split
-// and the ws also holds tickets, zero-filled once, and fp32 partials).
+// ws: a region of gemm_ws_bytes(M, out_dim, in_dim, x_bf16, num_cus) bytes
+// (fp16 images; when the result tiles fill fewer than half the CUs, K is
+// split and the region also holds tickets, cleared by the X preparation of
+// every launch, and fp32 partials). Returns hipErrorInvalidValue when a
+// tensor's requested rows hold 4 GiB of records or more (32-bit offsets).
 int gemm_splits(int M, int N, int K, int num_cus);
 size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus);
 // U (fp32, with x_bf16 = 0): X is SwiGLU(X, U) with clamp lim, formed while
 // the images are prepared.
 hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
-                       int M, float* Y, uint8_t* ws, int num_cus, hipStream_t s, const float* U = nullptr,
-                       float lim = 0.0f);
+                       int M, float* Y, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s,
+                       const float* U = nullptr, float lim = 0.0f);
 // Two tensors on the same X in one launch (X prepared once): Ya [M][out_a]
 // from wa, Yb [M][out_b] from wb; ws: gemm2_ws_bytes bytes.
 size_t gemm2_ws_bytes(int M, int out_a, int out_b, int K, int x_bf16, int num_cus);
 hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, const uint8_t* wb,
                         unsigned long long row0b, int out_b, int in_dim, const void* X, int x_bf16, int M, float* Ya,
-                        float* Yb, uint8_t* ws, int num_cus, hipStream_t s, const float* U = nullptr,
+                        float* Yb, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s, const float* U = nullptr,
                         float lim = 0.0f);
 
 }  // namespace gpeed

@@ -36,12 +36,8 @@ constexpr int kPlanMaxTok = 8192;  // tokens per routed batch (plan's per-token 
 // ---------------------------------------------------------------------------
 // Router
 
-// (key, id) rank order: larger key first, equal keys lower id first.
-__device__ __forceinline__ bool ranks_before(float ka, int a, float kb, int b) {
-    return ka > kb || (ka == kb && a < b);
-}
-
-// The same order as one unsigned 64-bit number (larger ranks first): the
+// Rank order of (key, id) pairs: larger key first, equal keys lower id
+// first, as one unsigned 64-bit number (larger ranks first): the
 // key's bits made monotonic (non-NaN keys, -0 taken as +0), then the
 // complemented id. 0 ranks after every candidate.
 __device__ __forceinline__ uint64_t rank_word(float key, int id) {
@@ -272,6 +268,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ lo
 
 struct MoePlan {
     int* n_seg;      // [1]
+    int* n_valid;    // [1] bucket slots to multiply: eptr[E], or 0 for buckets that break the invariants
     int* seg_e;      // [S]
     int* seg_p0;     // [S]
     int* seg_n;      // [S]
@@ -279,6 +276,7 @@ struct MoePlan {
     int* idx_of;     // [N] token index of slot p inside its segment
     int* pos;        // [T][K] slots of token t, in expert order
     uint32_t* ctr;   // [2] work counters (gate/up, down)
+    uint32_t* err;   // the workspace's error word (kWsBuckets)
 };
 
 __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr, const int* __restrict__ tok,
@@ -290,11 +288,44 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
     __shared__ int ccount[kSegTok], ccursor[kSegTok];
     __shared__ int tmp[1024];
     __shared__ int tcnt[kPlanMaxTok];
+    __shared__ int bad;
     const int tid = threadIdx.x;
     for (int e = tid; e <= E; e += 1024) ep[e] = eptr[e];
     for (int t = tid; t < T; t += 1024) tcnt[t] = 0;
     if (tid < kSegTok) ccount[tid] = 0;
+    if (tid == 0) bad = 0;
     __syncthreads();
+    // The buckets must be what the router makes (model_batch.cpp:205-219):
+    // offsets from 0, non-decreasing, ending at T*K; tokens in range, each
+    // present K times. Anything else multiplies nothing: every token's
+    // slots are marked empty (the combine writes zeros) and kWsBuckets is set.
+    for (int e = tid; e < E; e += 1024)
+        if (ep[e + 1] < ep[e]) bad = 1;
+    if (tid == 0 && (ep[0] != 0 || ep[E] != T * K)) bad = 1;
+    __syncthreads();
+    if (!bad) {
+        for (int p = tid; p < T * K; p += 1024) {
+            const int t = tok[p];
+            if (t < 0 || t >= T) bad = 1;
+            else atomicAdd(&tcnt[t], 1);
+        }
+        __syncthreads();
+        for (int t = tid; t < T; t += 1024) {
+            if (tcnt[t] != K) bad = 1;
+            tcnt[t] = 0;
+        }
+    }
+    __syncthreads();
+    if (bad) {
+        for (int i = tid; i < T * K; i += 1024) pl.pos[i] = -1;
+        if (tid == 0) {
+            *pl.n_seg = 0;
+            *pl.n_valid = 0;
+            __hip_atomic_fetch_or(pl.err, kWsBuckets, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;  // uniform
+    }
+    if (tid == 0) *pl.n_valid = ep[E];
     // Segments are numbered heaviest first (the grouped GEMVs hand them out
     // in that order, so the last items left are the light ones): every
     // expert's full segments of kSegTok tokens in expert order, then the
@@ -398,7 +429,7 @@ __global__ __launch_bounds__(256) void k_prep_grouped(const float* __restrict__ 
                                                       uint8_t* __restrict__ act, size_t seg_stride) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + wave;
-    const int N = eptr[E];
+    const int N = *pl.n_valid;
     if (item >= N * nb) return;
     const int p = item / nb, b = item - p * nb;
     const size_t row = MODE == 0 ? (size_t)tok[p] : (size_t)p;
@@ -567,6 +598,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ D
     float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int k = 0; k < K; ++k) {
         const int p = pos[(size_t)t * K + k];
+        if (p < 0) continue;  // buckets rejected by the plan
         const float w = wt[p];
         const float4 d = *reinterpret_cast<const float4*>(D + (size_t)p * H + h);
         y.x = fmaf(w, d.x, y.x);
@@ -590,7 +622,7 @@ MoeLayout moe_layout(int T, int E, int K, int H, int I) {
     MoeLayout L{};
     const size_t N = (size_t)T * K;
     L.seg_max = (int)((N + (size_t)(kSegTok - 1) * E) / kSegTok + 1);
-    size_t off = 0;
+    size_t off = kWsHeader;
     const size_t sizes[8] = {256, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max,
                              4 * N, 4 * N, 4 * N, 256};
     for (int i = 0; i < 8; ++i) {
@@ -611,6 +643,8 @@ MoeLayout moe_layout(int T, int E, int K, int H, int I) {
 MoePlan plan_ptrs(uint8_t* ws, const MoeLayout& L) {
     MoePlan p;
     p.n_seg = reinterpret_cast<int*>(ws + L.plan_off[0]);
+    p.n_valid = p.n_seg + 1;
+    p.err = reinterpret_cast<uint32_t*>(ws);
     p.ctr = reinterpret_cast<uint32_t*>(ws + L.plan_off[7]);
     p.seg_e = reinterpret_cast<int*>(ws + L.plan_off[1]);
     p.seg_p0 = reinterpret_cast<int*>(ws + L.plan_off[2]);

@@ -39,19 +39,25 @@ WeightStore::~WeightStore() {
         (void)gpeed_free(b->p);
 }
 
-void* WeightStore::scratch(Buffer& b, size_t bytes, bool zero) {
+void* WeightStore::scratch(Buffer& b, size_t bytes, bool init) {
     if (bytes > b.bytes) {
         check(gpeed_free(b.p), "free");
         b.p = nullptr;
         b.bytes = 0;
+        bytes = (bytes + 255) / 256 * 256;
         check(gpeed_malloc(&b.p, bytes), "malloc");
         b.bytes = bytes;
-        if (zero) {
-            check(gpeed_zero(b.p, bytes, nullptr), "zero");
+        if (init) {
+            check(gpeed_ws_init(b.p, bytes, nullptr), "workspace init");
             check(gpeed_stream_sync(nullptr), "sync");
         }
     }
     return b.p;
+}
+
+void WeightStore::check_ws(void* ws, const std::string& what) {
+    if (gpeed_ws_status(ws, nullptr) != GPEED_OK)
+        throw std::runtime_error(what + ": " + gpeed_last_error());
 }
 
 void WeightStore::add(const std::string& name, const void* gguf_rows, uint64_t n_rows, int in_dim) {
@@ -91,7 +97,21 @@ const WeightStore::Tensor& WeightStore::get(const std::string& name, int in_dim)
 
 void WeightStore::matvec_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* x,
                                float* dst) {
-    matmul_quant(name, row0, in_dim, out_dim, x, 1, dst);
+    if (out_dim <= 0) return;  // weights.cpp:88
+    const Tensor& t = get(name, in_dim);
+    const size_t xb = (size_t)in_dim * sizeof(float), yb = (size_t)out_dim * sizeof(float);
+    void* xd = scratch(x_, xb, false);
+    void* yd = scratch(y_, yb, false);
+    const size_t wsb = gpeed_iq3xxs_matvec_ws_bytes(in_dim, out_dim);
+    if (wsb == 0) throw std::runtime_error("weights: unsupported shape for " + name);
+    Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
+    void* ws = scratch(wbuf, wsb, true);
+    check(gpeed_memcpy(xd, x, xb, kH2D), "weights: upload x");
+    check(gpeed_iq3xxs_matvec(t.t64, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd),
+                              static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
+          ("weights: matvec_quant " + name).c_str());
+    check_ws(ws, "weights: matvec_quant " + name);
+    check(gpeed_memcpy(dst, yd, yb, kD2H), "weights: download y");
 }
 
 void WeightStore::matmul_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* X,
@@ -103,12 +123,13 @@ void WeightStore::matmul_quant(const std::string& name, uint64_t row0, int in_di
     void* yd = scratch(y_, yb, false);
     const size_t wsb = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, n_tok);
     if (wsb == 0) throw std::runtime_error("weights: unsupported shape for " + name);
-    Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim, n_tok < 8 ? n_tok : 8)];
+    Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
     void* ws = scratch(wbuf, wsb, true);
     check(gpeed_memcpy(xd, X, xb, kH2D), "weights: upload x");
     check(gpeed_iq3xxs_matmul(t.t64, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd), n_tok,
                               static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
           ("weights: matmul_quant " + name).c_str());
+    check_ws(ws, "weights: matmul_quant " + name);
     check(gpeed_memcpy(Y, yd, yb, kD2H), "weights: download y");
 }
 
@@ -130,7 +151,7 @@ void WeightStore::moe_experts(const std::string& gate, const std::string& up, co
     const size_t mwsb = gpeed_iq3xxs_moe_ws_bytes(n_tok, n_exp, top_k, hidden, inter);
     if (rwsb == 0 || mwsb == 0) throw std::runtime_error("moe: unsupported shape");
     void* rws = scratch(route_ws_, rwsb, false);
-    void* mws = scratch(moe_ws_, mwsb, false);
+    void* mws = scratch(moe_ws_, mwsb, true);
     const size_t xb = (size_t)n_tok * hidden * sizeof(float);
     void* xd = scratch(x_, xb, false);
     void* yd = scratch(y_, xb, false);
@@ -146,6 +167,7 @@ void WeightStore::moe_experts(const std::string& gate, const std::string& up, co
                                    static_cast<const float*>(wt), swiglu_limit, static_cast<float*>(yd), mws,
                                    moe_ws_.bytes, nullptr),
           "moe: experts");
+    check_ws(mws, "moe: experts");
     check(gpeed_memcpy(Y, yd, xb, kD2H), "moe: download y");
 }
 

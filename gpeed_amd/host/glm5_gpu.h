@@ -46,10 +46,13 @@ public:
     bool has(const std::string& name) const { return tensors_.count(name) != 0; }
     size_t resident_bytes() const { return resident_bytes_; }
 
-    // dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim (weights.cpp:167-203).
+    // dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim (weights.cpp:167-203):
+    // one GEMV launch.
     void matvec_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* x,
                       float* dst);
-    // Y[t][j] = sum_i W[row0+j][i] * X[t][i], t < n_tok (weights.cpp:86-165).
+    // Y[t][j] = sum_i W[row0+j][i] * X[t][i], t < n_tok (weights.cpp:86-165):
+    // 8-token GEMV passes for decode-sized batches, the prefill GEMM (one
+    // pass over W) from gpeed_iq3xxs_matmul_gemm_min_tok() tokens on.
     void matmul_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* X,
                       int n_tok, float* Y);
 
@@ -74,13 +77,16 @@ private:
         size_t bytes = 0;
     };
     const Tensor& get(const std::string& name, int in_dim) const;
-    void* scratch(Buffer& b, size_t bytes, bool zero);
+    void* scratch(Buffer& b, size_t bytes, bool init);
+    // throws if a kernel flagged the workspace (waits for the stream)
+    static void check_ws(void* ws, const std::string& what);
 
     std::unordered_map<std::string, Tensor> tensors_;
     size_t resident_bytes_ = 0;
-    // GEMV workspaces are zero-filled once per (in_dim, out_dim, tokens)
-    // shape and then kept: each launch leaves its tickets at zero.
-    std::map<std::tuple<int, int, int>, Buffer> ws_;
+    // One matvec / matmul workspace per (in_dim, out_dim), initialised when
+    // it is made and grown when a call needs more; each launch leaves its
+    // tickets at zero, and one sized for n_tok serves every smaller call.
+    std::map<std::tuple<int, int>, Buffer> ws_;
     Buffer x_, y_, route_ws_, moe_ws_, logits_, bias_, eptr_, tok_, wt_;
 };
 

@@ -31,6 +31,15 @@ typedef void* gpeed_stream_t;
 #define GPEED_ERR_LAYOUT (-6)         /* T64 operand addressed off a 64-row tile boundary */
 #define GPEED_ERR_WORKSPACE (-7)      /* workspace missing or too small */
 #define GPEED_ERR_NO_DEVICE (-8)      /* no HIP device visible */
+#define GPEED_ERR_WS_STATE (-9)       /* a kernel flagged its workspace (gpeed_ws_status) */
+
+/* Flags of a workspace's error word (gpeed_ws_status). */
+#define GPEED_WS_TICKET 1u            /* a shared tile's ticket counted more arrivals than the tile has
+                                       * parts: the workspace was not initialised, is shared by calls
+                                       * that overlap, or was left by a call that flagged an error */
+#define GPEED_WS_TIMEOUT 2u           /* a bounded wait for another workgroup's partial gave up (its
+                                       * rows are wrong) */
+#define GPEED_WS_BUCKETS 4u           /* expert buckets (eptr / tok) break the router's invariants */
 
 #define GPEED_DTYPE_IQ3_XXS 18        /* common.h:27 */
 
@@ -82,6 +91,28 @@ int gpeed_stream_sync(gpeed_stream_t stream);
 int gpeed_prof_start(int max_launches);
 int gpeed_prof_read(int kind, float* durations_ms, int max_n, int* n);
 
+/* ---- workspaces (no reference counterpart: the reference computes on the
+ *      host with per-thread scratch, weights.cpp:100-107, 180-187) -------- */
+
+/* Every workspace of the products below (GEMV, matvec / matmul, dense MLP,
+ * GEMM, routed experts) starts with a 256-byte header whose first word
+ * collects the GPEED_WS_* flags of the kernels that used it. A call returns
+ * before its kernels run, so these conditions cannot be its status; they
+ * stay in the header until gpeed_ws_status reads them. */
+
+/* Waits for `stream`, then returns GPEED_OK if no kernel flagged ws since the
+ * last check, else GPEED_ERR_WS_STATE (gpeed_last_error names the flags) and
+ * clears the flags. After a flag, results written since the last check are
+ * unreliable and the workspace must be initialised again. */
+int gpeed_ws_status(void* ws, gpeed_stream_t stream);
+/* Zero-fills ws[0..ws_bytes) with a fill kernel on `stream` (safe under graph
+ * capture). Needed once for every new workspace (its header must start at
+ * zero), and for GEMV, matvec / matmul and dense-MLP workspaces again after
+ * a flagged error; those calls leave every word they count on at zero
+ * again, for any shape the workspace is sized for. GEMM and routed-expert
+ * kernels clear their own counters on every call. */
+int gpeed_ws_init(void* ws, size_t ws_bytes, gpeed_stream_t stream);
+
 /* ---- geometry (replaces quant.cpp:52-126 for IQ3_XXS) ------------------- */
 
 /* dtype_row_bytes(IQ3_XXS, in_dim) (quant.cpp:119-126): 0 if in_dim % 256. */
@@ -118,21 +149,29 @@ int gpeed_iq3xxs_untile(const void* t64, uint64_t n_rows, int64_t in_dim, void* 
  *      weights.cpp:167-203, and matmul_quant, weights.h:47-48,
  *      weights.cpp:86-165) ----------------------------------------------- */
 
-/* Workspace bytes of gpeed_iq3xxs_matvec / gpeed_iq3xxs_matmul for n_tok
- * vectors (n_tok = 1 for matvec). The workspace must be zero-filled before
- * its first use with a given (in_dim, out_dim, min(n_tok, 8)); calls leave it
- * ready for the next call of that shape. One workspace per stream: calls
- * that run concurrently must not share one. */
+/* Workspace bytes of gpeed_iq3xxs_matvec / gpeed_iq3xxs_matmul for up to
+ * n_tok vectors (n_tok = 1 for matvec) on the current device. A workspace
+ * sized for n_tok serves every call with fewer tokens and the same
+ * (in_dim, out_dim), and matvec. Initialise it once (gpeed_ws_init). One
+ * workspace per stream: calls that run concurrently must not share one. */
 size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim, int64_t out_dim);
 size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok);
+/* Token count from which gpeed_iq3xxs_matmul runs the prefill GEMM (one pass
+ * over W) instead of 8-token GEMV passes (one pass per 8 tokens). */
+int gpeed_iq3xxs_matmul_gemm_min_tok(void);
 /* dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim, from the T64 copy of a
- * tensor with n_rows rows. row0 % 64 == 0. x, dst: fp32 device arrays. */
+ * tensor with n_rows rows. row0 % 64 == 0. x, dst: fp32 device arrays (x
+ * 16-byte aligned). One launch: the GEMV workgroups prepare the activation
+ * blocks they use. */
 int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* x, float* dst, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream);
 /* Y[t][j] = sum_i W[row0+j][i] * X[t][i] for t < n_tok (X [n_tok][in_dim],
  * Y [n_tok][out_dim], fp32, row-major). Row t of Y is the matvec of X[t]
- * (weights.cpp:86-165 makes the same promise). */
+ * (weights.cpp:86-165 makes the same promise) up to fp32 summation order.
+ * Below gpeed_iq3xxs_matmul_gemm_min_tok() tokens: GEMV passes of up to 8
+ * tokens; from there on: the prefill GEMM with fp32 X (gpeed_iq3xxs_gemm),
+ * so W is read once whatever n_tok. */
 int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* X, int n_tok, float* Y, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream);
@@ -146,9 +185,11 @@ int gpeed_iq3xxs_matmul(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
  * result tiles fill fewer than half the device's CUs (few tokens or few
  * rows), K is split over workgroups and the partials are added in a fixed
  * order (bitwise repeatable). X 16-byte aligned; ws:
- * gpeed_iq3xxs_gemm_ws_bytes bytes for this device, zero-filled once per
- * shape (every call leaves it ready for the next); calls on one ws must not
- * overlap. */
+ * gpeed_iq3xxs_gemm_ws_bytes bytes for this device (initialised once for
+ * its header: the X preparation clears the split-K tickets of every call);
+ * calls on one ws must not overlap. W records are addressed with 32-bit
+ * offsets: a tensor whose requested rows hold 4 GiB of records or more is
+ * rejected (GPEED_ERR_INVALID). */
 size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_dim, int x_dtype);
 int gpeed_iq3xxs_gemm(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim, const void* X,
                       int x_dtype, int n_tok, float* Y, void* ws, size_t ws_bytes, gpeed_stream_t stream);
@@ -177,9 +218,10 @@ int gpeed_iq3xxs_gemm2(const void* w_a, uint64_t n_rows_a, uint64_t row0_a, int 
  * "prepared activation" holds 1..8 fp32 vectors as the fp16 hi/lo MFMA
  * operand plus a power-of-two scale per 256 elements, in a caller-owned
  * device buffer of gpeed_iq3xxs_act_bytes(in_dim, n_tok) bytes (16-byte
- * aligned). The GEMV workspace (gpeed_iq3xxs_gemv_ws_bytes; zero-filled
- * before its first use with a given shape, one per stream) holds the
- * tickets and partial sums of row tiles that workgroups share. */
+ * aligned). The GEMV workspace (gpeed_iq3xxs_gemv_ws_bytes; initialised
+ * once with gpeed_ws_init, one per stream) holds the tickets and partial
+ * sums of row tiles that workgroups share; a workspace sized for n_tok
+ * serves every call with fewer tokens on the same shape. */
 size_t gpeed_iq3xxs_act_bytes(int64_t in_dim, int n_tok);
 int gpeed_iq3xxs_prep_act(const float* x, int64_t in_dim, int n_tok, void* act, size_t act_bytes,
                           gpeed_stream_t stream);
@@ -215,8 +257,9 @@ int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, 
  * down projection's prepared activation (one power-of-two scale per 64
  * values); the second launch multiplies it. gate/up are T64 copies of inter x hidden, down
  * of hidden x inter (rows from 0); hidden and inter multiples of 256. ws:
- * gpeed_iq3xxs_dense_mlp_ws_bytes bytes, zero-filled once per shape (every
- * call leaves it ready for the next); one workspace per stream. */
+ * gpeed_iq3xxs_dense_mlp_ws_bytes bytes, initialised once with
+ * gpeed_ws_init (every call leaves it ready for the next); one workspace per
+ * stream. */
 size_t gpeed_iq3xxs_dense_mlp_ws_bytes(int64_t hidden, int64_t inter);
 int gpeed_iq3xxs_dense_mlp(const void* w_gate, const void* w_up, const void* w_down, int hidden, int inter,
                            const float* x, float limit, float* y, void* ws, size_t ws_bytes, gpeed_stream_t stream);
@@ -252,12 +295,22 @@ int gpeed_moe_route(const float* logits, int n_tok, int n_exp, int top_k, int mo
  * ffn_down_exps); Y[t] = sum over the token's experts, in expert order, of
  * wt * down (Y overwritten; the shared expert is not included). hidden and
  * inter are multiples of 256; n_tok <= 8192. eptr/tok/wt as gpeed_moe_route
- * makes them. ws: gpeed_iq3xxs_moe_ws_bytes bytes (no zero-fill needed). */
+ * makes them: eptr[0] = 0, non-decreasing, eptr[n_exp] = n_tok*top_k, every
+ * tok entry in [0, n_tok) and every token present top_k times. Buckets that
+ * break these rules are not multiplied: Y is zero and the workspace's
+ * GPEED_WS_BUCKETS flag is set. ws: gpeed_iq3xxs_moe_ws_bytes bytes
+ * (initialised once for its header). */
 size_t gpeed_iq3xxs_moe_ws_bytes(int n_tok, int n_exp, int top_k, int hidden, int inter);
 int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w_down, int n_exp, int hidden,
                              int inter, const float* X, int n_tok, int top_k, const int* eptr, const int* tok,
                              const float* wt, float swiglu_limit, float* Y, void* ws, size_t ws_bytes,
                              gpeed_stream_t stream);
+
+/* Checks expert buckets held in HOST memory against the invariants above
+ * (what the reference's bucket sort, model_batch.cpp:205-219, produces):
+ * GPEED_OK, or GPEED_ERR_INVALID with the first violation in
+ * gpeed_last_error. For callers that build eptr / tok on the host. */
+int gpeed_moe_check_buckets(const int* eptr, const int* tok, int n_exp, int n_tok, int top_k);
 
 /* Same product as gpeed_iq3xxs_matvec straight from GGUF rows (no tiling;
  * any row0), one wavefront per row. */

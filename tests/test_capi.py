@@ -166,3 +166,24 @@ def test_decode_model_matches_oracle(grid_table):
 
 def test_device_count_without_gpu_is_nonnegative():
     assert gpeed_amd.device_count() >= 0
+
+
+def test_moe_check_buckets_host():
+    """The host-side bucket check (gpeed_moe_check_buckets) accepts what the
+    router makes and rejects each broken invariant the device plan rejects."""
+    T, E, K = 9, 12, 3
+    logits = synth.normal(97, 0, T * E).reshape(T, E)
+    eptr, tok, _, _ = oracle.moe_route(logits, K, 1)
+    gpeed_amd.moe_check_buckets(eptr, tok, E, T, K)
+    cases = []
+    e = eptr.copy(); e[0] = 1; cases.append((e, tok, "eptr[0]"))
+    e = eptr.copy(); e[E] -= 1; cases.append((e, tok, "eptr[n_exp]"))
+    nz = int(np.nonzero(np.diff(eptr))[0][0])  # first expert with tokens
+    e = eptr.copy(); e[nz + 1] = e[nz] - 1; cases.append((e, tok, "decreases"))
+    t = tok.copy(); t[4] = T; cases.append((eptr, t, "out of range"))
+    t = tok.copy(); t[4] = -1; cases.append((eptr, t, "out of range"))
+    t = tok.copy(); t[0:K + 1] = t[0]; cases.append((eptr, t, "appears"))
+    for e, t, what in cases:
+        with pytest.raises(gpeed_amd.GpeedError) as err:
+            gpeed_amd.moe_check_buckets(e, t, E, T, K)
+        assert err.value.code == -1 and what in str(err.value), (what, str(err.value))

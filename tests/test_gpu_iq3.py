@@ -176,7 +176,8 @@ def test_gemv_deterministic_and_workspace_reset(gpu):
     assert all(np.array_equal(ys[0].view(np.uint32), y.view(np.uint32)) for y in ys[1:])
     torch.cuda.synchronize()
     n_tiles = n_rows // 64
-    assert not host(ws[:4 * n_tiles]).any()
+    assert not host(ws[:256 + 4 * n_tiles]).any()  # header (error word) and tickets
+    G.ws_status(ws)
     assert rel_err(ys[0][0], oracle.matvec(w, 0, in_dim, n_rows, x)) < TIGHT
 
 
