@@ -346,8 +346,9 @@ size_t gpeed_iq3xxs_gemv_ws_bytes(int n_tensors, int64_t in_dim, int64_t out_dim
 
 // From this many tokens matmul runs the prefill GEMM (W read once) instead of
 // ceil(n_tok / 8) GEMV passes (W read once per pass). Measured on MI355X over
-// the 576..12288-row shapes of the decode mix and the dense MLP.
-constexpr int kMatmulGemmMinTok = 16;
+// the 576..12288-row shapes of the decode mix and the dense MLP: from 9
+// tokens (two GEMV passes) the GEMM is faster on every one of them.
+constexpr int kMatmulGemmMinTok = 9;
 
 int gpeed_iq3xxs_matmul_gemm_min_tok(void) { return kMatmulGemmMinTok; }
 
