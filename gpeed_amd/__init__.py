@@ -72,6 +72,7 @@ def lib():
             "gpeed_iq3xxs_matvec": ([vp, u64, u64, i32, i32, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_matmul": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_matvec_raw": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
+            "gpeed_iq3xxs_matvec_noalloc": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
             "gpeed_iq3xxs_act_bytes": ([i64, i32], sz),
             "gpeed_iq3xxs_prep_act": ([vp, i64, i32, vp, sz, vp], i32),
             "gpeed_iq3xxs_prep_swiglu": ([vp, vp, i64, i32, C.c_float, vp, sz, vp], i32),

@@ -53,6 +53,36 @@ int device_state(const DeviceState** out) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Scratch of gpeed_iq3xxs_matvec_noalloc: a GEMV workspace (header, tickets,
+// tagged partials) in a fixed device array, one copy per GPU that loads the
+// library, held until the process ends. Host code never uses the array's
+// name as an address: each device's copy is reached through the pointer
+// hipGetSymbolAddress returned for it (g_noalloc[dev]).
+constexpr size_t kNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_noalloc_mu;
+void* g_noalloc[kMaxDevices] = {};
+
+// This device's copy of `scratch` (looked up once per device, with that
+// device current) and zero-filled on `s` the first time. No allocation.
+int noalloc_scratch(int dev, hipStream_t s, void** out) {
+    void* p = __atomic_load_n(&g_noalloc[dev], __ATOMIC_ACQUIRE);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_noalloc_mu);
+        p = g_noalloc[dev];
+        if (!p) {
+            hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+            e = gpeed::launch_fill_zero(p, kNoAllocScratchBytes, s);
+            if (e != hipSuccess) return hip_fail(e, "clearing the no-allocation scratch");
+            __atomic_store_n(&g_noalloc[dev], p, __ATOMIC_RELEASE);
+        }
+    }
+    *out = p;
+    return GPEED_OK;
+}
+
 // Launch timing pool (see iq3_prof.h). One pool per process, guarded by a
 // mutex; events are created on the device current at gpeed_prof_start.
 struct ProfPool {
@@ -211,7 +241,18 @@ int gpeed_stream_read(const void* p, size_t bytes, uint32_t* out, size_t out_wor
 int gpeed_init(void) {
     if (gpeed_device_count() <= 0) return fail(GPEED_ERR_NO_DEVICE, "no HIP device");
     const DeviceState* st = nullptr;
-    return device_state(&st);
+    int rc = device_state(&st);
+    if (rc) return rc;
+    // the no-allocation entry point's scratch for this device (cleared on the
+    // null stream, waited for here so that no later call depends on it)
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    void* p = nullptr;
+    rc = noalloc_scratch(dev, nullptr, &p);
+    if (rc) return rc;
+    e = hipStreamSynchronize(nullptr);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "gpeed_init: hipStreamSynchronize");
 }
 
 int gpeed_ws_status(void* ws, gpeed_stream_t stream) {
@@ -613,6 +654,39 @@ int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
     if (!ws || !aligned(ws, 256) || ws_bytes < need)
         return fail(GPEED_ERR_WORKSPACE, "matvec: workspace missing, misaligned or too small");
     return gpeed_iq3xxs_gemv_x(w_t64, n_rows, row0, in_dim, out_dim, x, dst, ws, need, stream);
+}
+
+int gpeed_iq3xxs_matvec_noalloc(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                                const float* x, float* dst, gpeed_stream_t stream) {
+    if (out_dim <= 0) return GPEED_OK;  // weights.cpp:88
+    int rc = check_mv_args(w_t64, n_rows, row0, in_dim, out_dim, x, dst, "matvec_noalloc");
+    if (rc) return rc;
+    if (!aligned(w_t64, 16) || !aligned(x, 16))
+        return fail(GPEED_ERR_INVALID, "matvec_noalloc: weights and x must be 16-byte aligned");
+    if (row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "matvec_noalloc: row0 must be a multiple of 64 on the T64 layout");
+    const DeviceState* st = nullptr;
+    rc = device_state(&st);
+    if (rc) return rc;
+    const size_t need =
+        gpeed::kWsHeader + gpeed::gemv_ws_bytes_planned(1, in_dim, out_dim, 1, st->num_cus, gpeed::kPlanPrep);
+    if (need > kNoAllocScratchBytes)
+        return fail(GPEED_ERR_INVALID, "matvec_noalloc: this shape needs " + std::to_string(need) +
+                                           " bytes of scratch, more than the fixed " +
+                                           std::to_string(kNoAllocScratchBytes));
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    void* sp = nullptr;
+    rc = noalloc_scratch(dev, s, &sp);
+    if (rc) return rc;
+    const uint8_t* wp[2] = {static_cast<const uint8_t*>(w_t64), static_cast<const uint8_t*>(w_t64)};
+    float* yp[2] = {dst, dst};
+    e = gpeed::launch_gemv_x(wp, yp, 1, in_dim, row0, out_dim, x, nullptr, 0.0f,
+                             static_cast<uint8_t*>(sp) + gpeed::kWsHeader, static_cast<uint32_t*>(sp), st->num_cus,
+                             s);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec_noalloc launch");
 }
 
 size_t gpeed_moe_route_ws_bytes(int n_tok, int n_exp, int top_k) {

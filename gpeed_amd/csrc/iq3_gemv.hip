@@ -827,6 +827,12 @@ size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok) {
     return cnt + (size_t)tiles * (size_t)nb * (size_t)n_tok * 64 * 8;
 }
 
+size_t gemv_ws_bytes_planned(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus, int kind) {
+    const GemvPlan p = plan_gemv(n_tensors, in_dim, out_dim, n_tok, num_cus, kind);
+    const size_t cnt = ((size_t)p.n_tiles_all * 4 + 255) / 256 * 256;
+    return cnt + (size_t)p.n_tiles_all * (size_t)p.max_parts * (size_t)n_tok * 64 * 8;
+}
+
 hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                            unsigned long long row0, int out_dim, int n_tok, const uint8_t* act,
                            uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s) {

@@ -59,6 +59,10 @@ GemvPlan plan_gemv(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cu
 // Zero-filled once before first use; every launch leaves the words it used
 // at zero again.
 size_t gemv_ws_bytes(int n_tensors, int in_dim, int out_dim, int n_tok);
+// The region one launch of this plan kind actually touches on a device with
+// num_cus CUs (part words for max_parts parts per tile rather than one per
+// block): what a fixed-size scratch must hold.
+size_t gemv_ws_bytes_planned(int n_tensors, int in_dim, int out_dim, int n_tok, int num_cus, int kind);
 // y_i[t][j] = sum_k W_i[row0+j][k] x_t[k] over the T64 payloads of n_tensors
 // (1 or 2) same-shape tensors sharing one prepared activation of n_tok
 // (1..8) vectors.

@@ -166,6 +166,19 @@ int gpeed_iq3xxs_matmul_gemm_min_tok(void);
 int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                         const float* x, float* dst, void* ws, size_t ws_bytes,
                         gpeed_stream_t stream);
+/* No counterpart in the reference: gpeed_iq3xxs_matvec for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc) and so bring no workspace either. The
+ * same kernel and result, bit for bit; its tickets and partial sums live in
+ * a fixed 4 MiB device array per GPU (set up by gpeed_init or the first
+ * call on a device, held until the process ends). A shape whose launch
+ * needs more than that is refused (GPEED_ERR_INVALID; the dense shapes up
+ * to 12288 x 12288 fit). Every call on a GPU shares that GPU's array, so
+ * calls that overlap on one GPU (other streams, other threads) race and
+ * may give wrong rows; calls in order on one stream are safe. Allocates
+ * nothing and calls no allocating routine. */
+int gpeed_iq3xxs_matvec_noalloc(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                                const float* x, float* dst, gpeed_stream_t stream);
 /* Y[t][j] = sum_i W[row0+j][i] * X[t][i] for t < n_tok (X [n_tok][in_dim],
  * Y [n_tok][out_dim], fp32, row-major). Row t of Y is the matvec of X[t]
  * (weights.cpp:86-165 makes the same promise) up to fp32 summation order.
