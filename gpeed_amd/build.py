@@ -62,7 +62,7 @@ def build_host() -> str:
     cxx = os.environ.get("CXX", "g++")
     tmp = HOST_LIB + ".tmp"
     _run([cxx, "-std=c++17", "-O2", "-Wall", "-fPIC", "-shared", os.path.join(HERE, "host", "glm5_gpu.cpp"),
-          "-o", tmp, "-L" + HERE, "-lgpeed_iq3", "-Wl,-rpath,$ORIGIN"])
+          os.path.join(HERE, "host", "gguf.cpp"), "-o", tmp, "-L" + HERE, "-lgpeed_iq3", "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, HOST_LIB)
     tmp = HOST_CHECK + ".tmp"
     _run([cxx, "-std=c++17", "-O2", "-Wall", os.path.join(ROOT, "tests", "cpp", "host_check.cpp"), "-o", tmp,

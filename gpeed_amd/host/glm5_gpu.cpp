@@ -1,8 +1,11 @@
 // C++ host layer over the gpeed C ABI (see glm5_gpu.h).
 #include "glm5_gpu.h"
 
+#include <climits>
+#include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "../../include/gpeed_iq3.h"
 
@@ -31,6 +34,58 @@ void cuda_add(const float* a, const float* b, float* dst, int n) { check(gpeed_a
 namespace gpu {
 
 WeightStore::WeightStore() { check(gpeed_init(), "gpeed_init"); }
+
+WeightStore::WeightStore(const GgufModel& model) : WeightStore() { model_ = &model; }
+
+void WeightStore::pin(const std::string& name) {
+    if (!model_) throw std::runtime_error("weights: no GGUF model attached for " + name);
+    const TensorInfo* t = model_->find_tensor(name);
+    if (!t) throw std::runtime_error("weights: missing tensor " + name);
+    if (t->type != DType::IQ3_XXS)
+        throw std::runtime_error(std::string("weights: ") + dtype_name(t->type) + " is not on the GPU path for " + name);
+    if (t->dims.empty() || t->dims[0] > (uint64_t)INT32_MAX || t->dims[0] % 256)
+        throw std::runtime_error("weights: row not block aligned for " + name);
+    // straight from the file mapping when there is one, else through a host copy
+    const GgufFile& f = model_->file((size_t)t->shard);
+    std::vector<uint8_t> tmp;
+    const void* src = f.data_ptr() ? static_cast<const void*>(f.data_ptr() + t->offset) : nullptr;
+    if (!src) {
+        tmp.resize((size_t)t->n_bytes());
+        model_->read_tensor(*t, tmp.data());
+        src = tmp.data();
+    }
+    add(name, src, t->n_rows(), (int)t->dims[0]);
+}
+
+size_t WeightStore::pin_matching(bool experts) {
+    if (!model_) throw std::runtime_error("weights: no GGUF model attached");
+    for (const std::string& name : model_->tensor_names()) {
+        const bool is_expert = name.find("exps.weight") != std::string::npos;  // weights.cpp:72-73
+        if (is_expert != experts || has(name)) continue;
+        const TensorInfo* t = model_->find_tensor(name);
+        if (!t || t->type != DType::IQ3_XXS || t->dims.empty() || t->dims[0] % 256) continue;
+        pin(name);
+    }
+    return resident_bytes_;
+}
+
+size_t WeightStore::pin_nonexpert() { return pin_matching(false); }
+
+size_t WeightStore::pin_experts() { return pin_matching(true); }
+
+void WeightStore::read_resident(const std::string& name, void* dst) const {
+    auto it = tensors_.find(name);
+    if (it == tensors_.end()) throw std::runtime_error("weights: missing tensor " + name);
+    const Tensor& t = it->second;
+    const size_t raw_bytes = gpeed_iq3xxs_row_bytes(t.in_dim) * t.n_rows;
+    void* raw = nullptr;
+    check(gpeed_malloc(&raw, raw_bytes), "malloc");
+    int rc = gpeed_iq3xxs_untile(t.t64, t.n_rows, t.in_dim, raw, nullptr);
+    if (rc == GPEED_OK) rc = gpeed_stream_sync(nullptr);
+    if (rc == GPEED_OK) rc = gpeed_memcpy(dst, raw, raw_bytes, kD2H);
+    (void)gpeed_free(raw);
+    check(rc, "weights: read back");
+}
 
 WeightStore::~WeightStore() {
     for (auto& kv : tensors_) (void)gpeed_free(kv.second.t64);
@@ -88,8 +143,12 @@ void WeightStore::add(const std::string& name, const void* gguf_rows, uint64_t n
     resident_bytes_ += t.bytes;
 }
 
-const WeightStore::Tensor& WeightStore::get(const std::string& name, int in_dim) const {
+const WeightStore::Tensor& WeightStore::get(const std::string& name, int in_dim) {
     auto it = tensors_.find(name);
+    if (it == tensors_.end() && model_ && model_->find_tensor(name) && in_dim % 256 == 0) {
+        pin(name);  // first use of a tensor of the attached model
+        it = tensors_.find(name);
+    }
     if (it == tensors_.end()) throw std::runtime_error("weights: missing tensor " + name);
     if (in_dim % 256 != 0) throw std::runtime_error("weights: row not block aligned for " + name);
     return it->second;

@@ -23,6 +23,8 @@
 #include <tuple>
 #include <unordered_map>
 
+#include "gguf.h"
+
 namespace glm5 {
 
 int cuda_device_count();
@@ -35,6 +37,12 @@ namespace gpu {
 class WeightStore {
 public:
     WeightStore();
+    // A store that takes its tensors from a parsed GGUF model (the reference's
+    // WeightStore(const GgufModel&), weights.cpp:10-11). pin_nonexpert /
+    // pin_experts upload them; a product on an IQ3_XXS tensor not yet
+    // resident uploads it first (where the reference would stream it from the
+    // file, weights.cpp:94-107). The model must outlive the store.
+    explicit WeightStore(const GgufModel& model);
     ~WeightStore();
     WeightStore(const WeightStore&) = delete;
     WeightStore& operator=(const WeightStore&) = delete;
@@ -45,6 +53,22 @@ public:
     void add(const std::string& name, const void* gguf_rows, uint64_t n_rows, int in_dim);
     bool has(const std::string& name) const { return tensors_.count(name) != 0; }
     size_t resident_bytes() const { return resident_bytes_; }
+
+    // pin_nonexpert (weights.cpp:70-84) on the device: every IQ3_XXS tensor of
+    // the attached model except the routed experts (names containing
+    // "exps.weight"), uploaded once and kept in HBM in the T64 layout.
+    // Tensors of other types stay with the caller's CPU path. Returns the
+    // bytes held in HBM.
+    size_t pin_nonexpert();
+    // The routed-expert tensors as well (the reference keeps them on disk; the
+    // whole model fits in 288 GB of HBM). Returns the bytes held in HBM.
+    size_t pin_experts();
+    // Uploads one IQ3_XXS tensor of the attached model (rows = n_elements /
+    // dims[0], so a 3-D expert tensor is [n_exp * rows_per_expert, in_dim]).
+    void pin(const std::string& name);
+    // The GGUF bytes of a resident tensor, read back from its HBM copy
+    // (n_rows * row_bytes into host memory at dst).
+    void read_resident(const std::string& name, void* dst) const;
 
     // dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim (weights.cpp:167-203):
     // one GEMV launch.
@@ -76,11 +100,14 @@ private:
         void* p = nullptr;
         size_t bytes = 0;
     };
-    const Tensor& get(const std::string& name, int in_dim) const;
+    const Tensor& get(const std::string& name, int in_dim);
     void* scratch(Buffer& b, size_t bytes, bool init);
     // throws if a kernel flagged the workspace (waits for the stream)
     static void check_ws(void* ws, const std::string& what);
 
+    size_t pin_matching(bool experts);
+
+    const GgufModel* model_ = nullptr;
     std::unordered_map<std::string, Tensor> tensors_;
     size_t resident_bytes_ = 0;
     // One matvec / matmul workspace per (in_dim, out_dim), initialised when

@@ -160,8 +160,38 @@ def ref(openmp: bool = False):
             L.ref_store_matmul.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_int, _f32p, C.c_int, _f32p]
             L.ref_store_close.argtypes = [C.c_void_p]
             L.ref_openmp_threads.restype = C.c_int
+            L.ref_gguf_dump.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+            L.ref_gguf_dump.restype = C.c_long
+            L.ref_gguf_read.argtypes = [C.c_char_p, C.c_char_p, C.c_void_p, C.c_size_t]
+            L.ref_gguf_read.restype = C.c_long
             _ref[key] = L
     return _ref[key]
+
+
+def ref_gguf_dump(path: str) -> dict:
+    """What the reference's own GGUF loader parses from a file (JSON dict)."""
+    import json
+
+    L = ref()
+    if L is None:
+        raise RuntimeError("oracle/_ref is not built")
+    buf = C.create_string_buffer(1 << 22)
+    n = L.ref_gguf_dump(path.encode(), buf, len(buf))
+    if n < 0:
+        raise RuntimeError(L.ref_last_error().decode())
+    return json.loads(buf.value.decode())
+
+
+def ref_gguf_read(path: str, name: str, nbytes: int) -> bytes:
+    """GgufModel::read_tensor of one tensor, by the reference's loader."""
+    L = ref()
+    if L is None:
+        raise RuntimeError("oracle/_ref is not built")
+    out = C.create_string_buffer(max(nbytes, 1))
+    n = L.ref_gguf_read(path.encode(), name.encode(), out, nbytes)
+    if n < 0:
+        raise RuntimeError(L.ref_last_error().decode())
+    return out.raw[:n]
 
 
 class RefStore:

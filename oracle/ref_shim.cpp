@@ -15,6 +15,7 @@
 #include <cstring>
 #include <exception>
 #include <memory>
+#include <stdexcept>
 #include <string>
 #include <unistd.h>
 #include <vector>
@@ -47,6 +48,45 @@ void put_u64(std::vector<uint8_t>& b, uint64_t v) {
 void put_str(std::vector<uint8_t>& b, const std::string& s) {
     put_u64(b, s.size());
     b.insert(b.end(), s.begin(), s.end());
+}
+
+// JSON of what the reference loader parsed, in the schema of the product
+// loader's dump (tests/cpp/host_check gguf-info), for a field-by-field
+// comparison.
+std::string jstr(const std::string& v) {
+    std::string o = "\"";
+    for (unsigned char c : v) {
+        if (c == '"' || c == '\\') {
+            o += '\\';
+            o += (char)c;
+        } else if (c < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\u%04x", c);
+            o += buf;
+        } else {
+            o += (char)c;
+        }
+    }
+    return o + "\"";
+}
+
+std::string jval(const glm5::GgufValue& v) {
+    using T = glm5::GgufValueType;
+    char buf[64];
+    switch (v.type) {
+        case T::STRING: return jstr(v.as_str());
+        case T::ARRAY: {
+            std::string o = "[";
+            for (size_t i = 0; i < v.array.size(); ++i) o += (i ? "," : "") + jval(v.array[i]);
+            return o + "]";
+        }
+        case T::FLOAT32: case T::FLOAT64: std::snprintf(buf, sizeof buf, "%.17g", v.as_f64()); return buf;
+        case T::BOOL: return v.as_bool() ? "true" : "false";
+        case T::INT8: case T::INT16: case T::INT32: case T::INT64:
+            std::snprintf(buf, sizeof buf, "%lld", (long long)v.as_i64());
+            return buf;
+        default: std::snprintf(buf, sizeof buf, "%llu", (unsigned long long)v.as_u64()); return buf;
+    }
 }
 
 }  // namespace
@@ -151,6 +191,66 @@ int ref_store_matmul(void* hp, uint64_t row0, int in_dim, int out_dim, const flo
 }
 
 void ref_store_close(void* hp) { delete static_cast<RefStore*>(hp); }
+
+// The reference loader's view of a GGUF model (GgufModel::load over the
+// shards GgufModel::discover_shards finds), as JSON into out (len bytes);
+// returns the JSON length, or -1 (message in ref_last_error).
+long ref_gguf_dump(const char* path, char* out, size_t len) {
+    try {
+        glm5::GgufModel m;
+        m.load(glm5::GgufModel::discover_shards(path));
+        const glm5::GgufFile& f0 = m.file(0);
+        std::string o = "{\"version\":" + std::to_string(f0.version()) +
+                        ",\"data_offset\":" + std::to_string(f0.data_offset()) +
+                        ",\"shards\":" + std::to_string(m.files().size()) + ",\"kv\":{";
+        const auto keys = m.keys();
+        for (size_t i = 0; i < keys.size(); ++i) {
+            const glm5::GgufValue* v = m.find(keys[i]);
+            o += (i ? "," : "") + jstr(keys[i]) + ":{\"type\":" + std::to_string((unsigned)v->type) +
+                 ",\"array_type\":" + std::to_string((unsigned)v->array_type) + ",\"value\":" + jval(*v) + "}";
+        }
+        o += "},\"tensors\":[";
+        const auto& names = m.tensor_names();
+        for (size_t i = 0; i < names.size(); ++i) {
+            const glm5::TensorInfo* t = m.find_tensor(names[i]);
+            std::string dims;
+            for (size_t d = 0; d < t->dims.size(); ++d) dims += (d ? "," : "") + std::to_string(t->dims[d]);
+            const uint64_t rows = t->dims.empty() ? 0 : t->n_elements() / t->dims[0];
+            o += std::string(i ? "," : "") + "{\"name\":" + jstr(t->name) + ",\"type\":" +
+                 std::to_string((unsigned)t->type) + ",\"dims\":[" + dims + "],\"offset\":" +
+                 std::to_string(t->offset) + ",\"shard\":" + std::to_string(t->shard) + ",\"n_bytes\":" +
+                 std::to_string(t->row_bytes() * rows) + ",\"rows\":" + std::to_string(rows) + "}";
+        }
+        o += "]}";
+        if (o.size() + 1 > len) {
+            g_err = "ref_gguf_dump: buffer too small";
+            return -1;
+        }
+        std::memcpy(out, o.c_str(), o.size() + 1);
+        return (long)o.size();
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// GgufModel::read_tensor of one tensor into dst (len bytes at most).
+long ref_gguf_read(const char* path, const char* name, void* dst, size_t len) {
+    try {
+        glm5::GgufModel m;
+        m.load(glm5::GgufModel::discover_shards(path));
+        const glm5::TensorInfo* t = m.find_tensor(name);
+        if (!t) throw std::runtime_error(std::string("no tensor ") + name);
+        const uint64_t rows = t->dims.empty() ? 0 : t->n_elements() / t->dims[0];
+        const size_t n = (size_t)(t->row_bytes() * rows);
+        if (n > len) throw std::runtime_error("ref_gguf_read: buffer too small");
+        m.read_tensor(*t, dst);
+        return (long)n;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
 
 // Threads the OpenMP regions of matvec_quant / matmul_quant will use (1 for
 // the library built without -fopenmp, as the reference is on Linux).

@@ -10,10 +10,23 @@
 //       token 0) and <dir>/Y.bin (matmul_quant)
 //   host_check moe <dir> <n_exp> <hidden> <inter> <n_tok> <top_k> <mode>
 //       reads gate.bin up.bin down.bin x.bin logits.bin; writes Y.bin
+//   host_check gguf-info <file>          (no device use)
+//       the GGUF model (shards discovered from the name) as one JSON object
+//   host_check gguf-read <file> <tensor> <out>   (no device use)
+//       the tensor's payload bytes
+//   host_check gguf-store <file> <script>
+//       a WeightStore over the model, driven by the script's lines:
+//         pin_nonexpert | pin_experts          prints "resident <bytes>"
+//         readback <tensor> <out>              GGUF bytes from the HBM copy
+//         matvec <tensor> <row0> <in> <out> <x> <y>
+//         matmul <tensor> <row0> <in> <out> <n_tok> <X> <Y>
+//         moe <gate> <up> <down> <E> <H> <I> <T> <K> <X> <logits> <Y>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <functional>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -38,6 +51,69 @@ void spit(const std::string& path, const void* p, size_t n) {
     FILE* f = std::fopen(path.c_str(), "wb");
     if (!f || std::fwrite(p, 1, n, f) != n) throw std::runtime_error("cannot write " + path);
     std::fclose(f);
+}
+
+std::string json_str(const std::string& v) {
+    std::string o = "\"";
+    for (unsigned char c : v) {
+        if (c == '"' || c == '\\') {
+            o += '\\';
+            o += (char)c;
+        } else if (c < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\u%04x", c);
+            o += buf;
+        } else {
+            o += (char)c;
+        }
+    }
+    return o + "\"";
+}
+
+std::string json_value(const glm5::gpu::GgufValue& v) {
+    using T = glm5::gpu::GgufValueType;
+    char buf[64];
+    switch (v.type) {
+        case T::STRING: return json_str(v.str);
+        case T::ARRAY: {
+            std::string o = "[";
+            for (size_t i = 0; i < v.array.size(); ++i) o += (i ? "," : "") + json_value(v.array[i]);
+            return o + "]";
+        }
+        case T::FLOAT32: case T::FLOAT64: std::snprintf(buf, sizeof buf, "%.17g", v.as_f64()); return buf;
+        case T::BOOL: return v.as_bool() ? "true" : "false";
+        case T::INT8: case T::INT16: case T::INT32: case T::INT64:
+            std::snprintf(buf, sizeof buf, "%lld", (long long)v.as_i64());
+            return buf;
+        default: std::snprintf(buf, sizeof buf, "%llu", (unsigned long long)v.as_u64()); return buf;
+    }
+}
+
+void gguf_info(const std::string& path) {
+    glm5::gpu::GgufModel m;
+    m.load(glm5::gpu::GgufModel::discover_shards(path));
+    const auto& f0 = m.file(0);
+    std::printf("{\"version\":%u,\"alignment\":%u,\"data_offset\":%llu,\"shards\":%zu,\"kv\":{", f0.version(),
+                f0.alignment(), (unsigned long long)f0.data_offset(), m.files().size());
+    const auto keys = m.keys();
+    for (size_t i = 0; i < keys.size(); ++i) {
+        const auto* v = m.find(keys[i]);
+        std::printf("%s%s:{\"type\":%u,\"array_type\":%u,\"value\":%s}", i ? "," : "", json_str(keys[i]).c_str(),
+                    (unsigned)v->type, (unsigned)v->array_type, json_value(*v).c_str());
+    }
+    std::printf("},\"tensors\":[");
+    const auto& names = m.tensor_names();
+    for (size_t i = 0; i < names.size(); ++i) {
+        const auto* t = m.find_tensor(names[i]);
+        std::string dims;
+        for (size_t d = 0; d < t->dims.size(); ++d) dims += (d ? "," : "") + std::to_string(t->dims[d]);
+        std::printf("%s{\"name\":%s,\"type\":%u,\"type_name\":\"%s\",\"dims\":[%s],\"offset\":%llu,\"shard\":%d,"
+                    "\"n_bytes\":%llu,\"rows\":%llu}",
+                    i ? "," : "", json_str(t->name).c_str(), (unsigned)t->type, glm5::gpu::dtype_name(t->type),
+                    dims.c_str(), (unsigned long long)t->offset, t->shard, (unsigned long long)t->n_bytes(),
+                    (unsigned long long)t->n_rows());
+    }
+    std::printf("]}\n");
 }
 
 bool throws_with(const std::function<void()>& fn, const std::string& what) {
@@ -116,7 +192,73 @@ int main(int argc, char** argv) {
             spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
             return 0;
         }
-        std::fprintf(stderr, "usage: host_check kernels|errors|matmul ...|moe ...\n");
+        if (mode == "gguf-info" && argc == 3) {
+            gguf_info(argv[2]);
+            return 0;
+        }
+        if (mode == "gguf-read" && argc == 5) {
+            glm5::gpu::GgufModel m;
+            m.load(glm5::gpu::GgufModel::discover_shards(argv[2]));
+            const auto* t = m.find_tensor(argv[3]);
+            if (!t) throw std::runtime_error(std::string("no tensor ") + argv[3]);
+            std::vector<char> buf((size_t)t->n_bytes());
+            m.read_tensor(*t, buf.data());
+            spit(argv[4], buf.data(), buf.size());
+            return 0;
+        }
+        if (mode == "gguf-store" && argc == 4) {
+            glm5::gpu::GgufModel m;
+            m.load(glm5::gpu::GgufModel::discover_shards(argv[2]));
+            glm5::gpu::WeightStore ws(m);
+            std::ifstream script(argv[3]);
+            std::string line;
+            while (std::getline(script, line)) {
+                std::istringstream in(line);
+                std::string op;
+                if (!(in >> op)) continue;
+                if (op == "pin_nonexpert" || op == "pin_experts") {
+                    const size_t b = op == "pin_nonexpert" ? ws.pin_nonexpert() : ws.pin_experts();
+                    std::printf("resident %zu\n", b);
+                } else if (op == "readback") {
+                    std::string name, out;
+                    in >> name >> out;
+                    const auto* t = m.find_tensor(name);
+                    if (!t) throw std::runtime_error("no tensor " + name);
+                    std::vector<char> buf((size_t)t->n_bytes());
+                    ws.read_resident(name, buf.data());
+                    spit(out, buf.data(), buf.size());
+                } else if (op == "matvec" || op == "matmul") {
+                    std::string name, xf, yf;
+                    uint64_t row0 = 0;
+                    int in_dim = 0, out_dim = 0, n_tok = 1;
+                    in >> name >> row0 >> in_dim >> out_dim;
+                    if (op == "matmul") in >> n_tok;
+                    in >> xf >> yf;
+                    const std::vector<char> x = slurp(xf);
+                    std::vector<float> y((size_t)n_tok * out_dim);
+                    if (op == "matvec")
+                        ws.matvec_quant(name, row0, in_dim, out_dim, reinterpret_cast<const float*>(x.data()), y.data());
+                    else
+                        ws.matmul_quant(name, row0, in_dim, out_dim, reinterpret_cast<const float*>(x.data()), n_tok,
+                                        y.data());
+                    spit(yf, y.data(), y.size() * 4);
+                } else if (op == "moe") {
+                    std::string g, u, d, xf, lf, yf;
+                    int E, H, I, T, K;
+                    in >> g >> u >> d >> E >> H >> I >> T >> K >> xf >> lf >> yf;
+                    const std::vector<char> x = slurp(xf), lg = slurp(lf);
+                    std::vector<float> Y((size_t)T * H);
+                    ws.moe_experts(g, u, d, E, H, I, reinterpret_cast<const float*>(x.data()), T,
+                                   reinterpret_cast<const float*>(lg.data()), K, 1, nullptr, 1.0f, true, 10.0f, Y.data());
+                    spit(yf, Y.data(), Y.size() * 4);
+                } else {
+                    throw std::runtime_error("bad script line: " + line);
+                }
+            }
+            std::printf("resident %zu\n", ws.resident_bytes());
+            return 0;
+        }
+        std::fprintf(stderr, "usage: host_check kernels|errors|matmul ...|moe ...|gguf-info|gguf-read|gguf-store\n");
         return 2;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "host_check: %s\n", e.what());
