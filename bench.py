@@ -30,7 +30,9 @@ the prefill GEMM (W 12288x6144, X bf16 [M,6144], M = 512 and 2048:
 TFLOP/s = 2*M*N*K / kernel time from dispatch-stamped events, against the
 2.5 PFLOP/s dense bf16/fp16 MFMA peak), and the continuous-batching decode
 mix (64 tokens through the latent projections and the shared-expert FFN:
-GB/s over the packed weights and TFLOP/s, both fractions).
+GB/s over the packed weights and TFLOP/s, both fractions), and the MLA
+per-head projections attn_k_b / attn_v_b (64 heads each, one launch per
+tensor, against 64 matvec launches).
 """
 from __future__ import annotations
 
@@ -267,6 +269,45 @@ def prefill_gemm(torch, G, synth, dev, reps):
                         "TFLOPs_kernel": round(fl / (k_ms * 1e-3) / 1e12, 1),
                         "TFLOPs_call": round(fl / (call_ms * 1e-3) / 1e12, 1),
                         "frac_of_bf16_peak": round(fl / (k_ms * 1e-3) / 1e12 / 2500.0, 4)}
+    return out
+
+
+def mla_heads(torch, G, synth, dev, reps, copies=64):
+    """MLA per-head absorbed projections of one layer (model.cpp:638-643, 664-665): attn_k_b (64 heads of
+    512 rows over 256) and attn_v_b (64 heads of 256 rows over 512), each one launch of
+    gpeed_iq3xxs_matvec_heads, against the reference's pattern of 64 matvec_quant calls per tensor.
+    `copies` rotated weight sets (2 x 3.2 MB each) keep the reads in HBM."""
+    NH, KVL, DK, DV = 64, 512, 256, 256
+    shapes = {"attn_k_b": (NH * KVL, DK, KVL), "attn_v_b": (NH * DV, KVL, DV)}
+    out = {"workload": "MLA per-head projections, one launch each: attn_k_b 64 heads x (512x256), "
+                       "attn_v_b 64 heads x (256x512), fp32 per-head inputs"}
+    for i, (name, (rows, k, rph)) in enumerate(shapes.items()):
+        base = G.tile(torch.from_numpy(synth.iq3xxs_matrix(2030, i, rows, k).reshape(-1)).to(dev), rows, k)
+        ws_list = [base] + [base.clone() for _ in range(copies - 1)]
+        x = torch.from_numpy(synth.normal(2030, 10 + i, NH * k).reshape(NH, k)).to(dev)
+        y = torch.empty(NH, rph, device=dev)
+        ws = G.gemv_workspace(k, rows, 1, 1, dev)
+        wsv = G.matvec_workspace(k, rph, dev)
+        for c in range(copies):
+            G.matvec_heads(ws_list[c], rows, 0, k, rph, x, out=y, ws=ws)
+        torch.cuda.synchronize()
+        G.prof_start(reps * copies + 8)
+        for r in range(reps * copies):
+            G.matvec_heads(ws_list[r % copies], rows, 0, k, rph, x, out=y, ws=ws)
+        torch.cuda.synchronize()
+        one = G.prof_read(G.PROF_GEMV).astype(np.float64) * 1e3
+        G.prof_start(reps * NH * 4 + 8)  # the reference's pattern: one matvec per head
+        for r in range(reps):
+            for h in range(NH):
+                G.matvec(ws_list[(r * NH + h) % copies], rows, h * rph, k, rph, x[h], out=y[h], ws=wsv)
+        torch.cuda.synchronize()
+        per = G.prof_read(G.PROF_GEMV).astype(np.float64) * 1e3
+        nbytes = rows * k // 256 * 98
+        out[name] = {"one_launch_kernel_us": round(float(np.median(one)), 2),
+                     "GBs": round(nbytes / (float(np.median(one)) * 1e-6) / 1e9, 1),
+                     "per_head_launches_kernel_us_sum": round(float(np.median(per)) * NH, 2),
+                     "packed_bytes": nbytes}
+        del ws_list
     return out
 
 
@@ -606,6 +647,8 @@ def main():
         rec["extra"]["prefill_gemm"] = prefill_gemm(torch, G, synth, dev, 20)
         torch.cuda.empty_cache()
         rec["extra"]["decode_mix"] = decode_mix(torch, G, synth, dev, 20)
+        torch.cuda.empty_cache()
+        rec["extra"]["mla_heads"] = mla_heads(torch, G, synth, dev, 20)
     if not args.no_cpu:
         log("cpu baseline")
         cb, y_ref = cpu_baseline(wg, wu, wd, x)

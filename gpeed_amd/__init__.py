@@ -82,6 +82,7 @@ def lib():
             "gpeed_iq3xxs_gemv_x": ([vp, u64, u64, i32, i32, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv2_x": ([vp, vp, u64, u64, i32, i32, vp, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemv_swiglu": ([vp, u64, u64, i32, i32, vp, vp, C.c_float, vp, vp, sz, vp], i32),
+            "gpeed_iq3xxs_matvec_heads": ([vp, u64, u64, i32, i32, i32, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_dense_mlp_ws_bytes": ([i64, i64], sz),
             "gpeed_iq3xxs_dense_mlp": ([vp, vp, vp, i32, i32, vp, C.c_float, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_gemm_ws_bytes": ([i64, i64, i64, i32], sz),
@@ -435,6 +436,22 @@ def gemv2_x(w_a, w_b, n_rows: int, row0: int, in_dim: int, out_dim: int, x, out_
     _check(lib().gpeed_iq3xxs_gemv2_x(_ptr(w_a), _ptr(w_b), n_rows, row0, in_dim, out_dim, _ptr(x), _ptr(out_a),
                                       _ptr(out_b), _ptr(ws), ws.numel(), _stream(stream)), "gemv2_x")
     return out_a, out_b
+
+
+def matvec_heads(w_t64, n_rows: int, row0: int, in_dim: int, rows_per_head: int, x, out=None, ws=None,
+                 stream=None):
+    """Per-head projections in one launch: x [n_heads, in_dim] -> [n_heads, rows_per_head], head h
+    using rows row0 + h*rows_per_head .. (attn_k_b / attn_v_b, model.cpp:638-643, 664-665)."""
+    torch = _torch()
+    _require_cuda(w_t64, x)
+    n_heads = x.shape[0]
+    if out is None:
+        out = torch.empty(n_heads, rows_per_head, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = gemv_workspace(in_dim, n_heads * rows_per_head, 1, 1, x.device)
+    _check(lib().gpeed_iq3xxs_matvec_heads(_ptr(w_t64), n_rows, row0, in_dim, rows_per_head, n_heads, _ptr(x),
+                                           _ptr(out), _ptr(ws), ws.numel(), _stream(stream)), "matvec_heads")
+    return out
 
 
 def dense_mlp_workspace(hidden: int, inter: int, device="cuda"):

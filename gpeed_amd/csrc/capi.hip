@@ -575,6 +575,32 @@ int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, 
     return gemv_x_n(w, d, 1, n_rows, row0, in_dim, out_dim, g, u, limit, ws, ws_bytes, stream, "gemv_swiglu");
 }
 
+int gpeed_iq3xxs_matvec_heads(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int rows_per_head,
+                              int n_heads, const float* x, float* dst, void* ws, size_t ws_bytes,
+                              gpeed_stream_t stream) {
+    if (n_heads <= 0 || rows_per_head <= 0) return GPEED_OK;
+    if (rows_per_head % gpeed::kTileRows || row0 % gpeed::kTileRows)
+        return fail(GPEED_ERR_LAYOUT, "matvec_heads: rows_per_head and row0 must be multiples of 64");
+    if ((int64_t)rows_per_head * n_heads > (1 << 30)) return fail(GPEED_ERR_INVALID, "matvec_heads: too many rows");
+    const int out_dim = rows_per_head * n_heads;
+    int rc = check_mv_args(w_t64, n_rows, row0, in_dim, out_dim, x, dst, "matvec_heads");
+    if (rc) return rc;
+    if (!aligned(w_t64, 16) || !aligned(x, 16))
+        return fail(GPEED_ERR_INVALID, "matvec_heads: weights and x must be 16-byte aligned");
+    if ((int64_t)n_heads * in_dim * 4 >= ((int64_t)1 << 31))
+        return fail(GPEED_ERR_INVALID, "matvec_heads: inputs of 2 GiB or more");
+    if (!ws || !aligned(ws, 256) || ws_bytes < gpeed::kWsHeader + gpeed::gemv_ws_bytes(1, in_dim, out_dim, 1))
+        return fail(GPEED_ERR_WORKSPACE, "matvec_heads: workspace missing, misaligned or too small");
+    const DeviceState* st = nullptr;
+    rc = device_state(&st);
+    if (rc) return rc;
+    const hipError_t e = gpeed::launch_gemv_heads(static_cast<const uint8_t*>(w_t64), in_dim, row0, rows_per_head,
+                                                  n_heads, x, dst, static_cast<uint8_t*>(ws) + gpeed::kWsHeader,
+                                                  static_cast<uint32_t*>(ws), st->num_cus,
+                                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec_heads launch");
+}
+
 size_t gpeed_iq3xxs_dense_mlp_ws_bytes(int64_t hidden, int64_t inter) {
     if (hidden <= 0 || inter <= 0 || hidden % gpeed::kQK || inter % gpeed::kQK || hidden > (1 << 24) ||
         inter > (1 << 24))

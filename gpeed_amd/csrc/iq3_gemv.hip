@@ -161,6 +161,13 @@ struct GemvArgs {
     float lim;
     uint8_t* act_out;      // EPI 1: act64 images of SwiGLU(gate, up)
     uint32_t w_bytes;      // bytes of each tensor's records from w[i] (< 2^31)
+    // MODE 1: row tiles [h*tiles_per_head, (h+1)*tiles_per_head) take their
+    // activation from x + h*head_stride bytes (one input vector per head of
+    // a per-head projection); one vector for all rows: tiles_per_head huge,
+    // head_stride 0. x_bytes: bytes readable from x.
+    int tiles_per_head;
+    uint32_t head_stride;
+    uint32_t x_bytes;
 };
 
 // buffer resource word 3 for raw (untyped) buffer loads on gfx9
@@ -296,14 +303,18 @@ struct ActLoads {
     __device__ void issue(const GemvArgs& g, const Chunk& ch, int wave, uint32_t lane) {
         constexpr int kAux = kCoherent ? 16 : 0;  // sc1
         const void* src = MODE == 3 ? static_cast<const void*>(g.act) : static_cast<const void*>(g.x);
-        const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(src), 0, g.nb * 1024, kBufferDword3);
+        const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(src), 0,
+                                                          MODE == 3 ? g.nb * 1024 : (int)g.x_bytes, kBufferDword3);
         const auto ur = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(MODE == 3 ? g.xsc : g.x2), 0,
                                                           MODE == 3 ? g.nb * 16 : g.nb * 1024, kBufferDword3);
 #pragma unroll
         for (int k = 0; k < KP; ++k) {
-            const int b = (ch.c0 + wave + k * W) % g.nb;
+            const int rec = ch.c0 + wave + k * W;
+            const int b = rec % g.nb;
             const bool ok = k < ch.n_mine;
-            const uint32_t off = ok ? (uint32_t)b * 1024u + lane * 16u : 0x80000000u;
+            // the head of the record's row tile (MODE 1 per-head inputs)
+            const uint32_t hoff = MODE == 1 ? (uint32_t)(rec / g.nb / g.tiles_per_head) * g.head_stride : 0u;
+            const uint32_t off = ok ? hoff + (uint32_t)b * 1024u + lane * 16u : 0x80000000u;
             xv[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kAux));
             if constexpr (MODE == 2)
                 uv[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, kAux));
@@ -757,6 +768,9 @@ GemvArgs base_args(const GemvPlan& plan, const uint8_t* const* w, float* const* 
     a.cnt = reinterpret_cast<uint32_t*>(ws);
     a.part = reinterpret_cast<uint64_t*>(ws + ((size_t)plan.n_tiles_all * 4 + 255) / 256 * 256);
     a.err = err;
+    a.tiles_per_head = 1 << 30;
+    a.head_stride = 0;
+    a.x_bytes = (uint32_t)a.nb * 1024u;
     a.w_bytes = (uint32_t)((size_t)a.n_tiles * a.nb * kRecordBytes);
     return a;
 }
@@ -864,6 +878,22 @@ hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors
     a.x2 = x2;
     a.lim = lim;
     if (x2) return launch_gemv_nt<1, 2>(plan, a, s);
+    return launch_gemv_nt<1, 1>(plan, a, s);
+}
+
+hipError_t launch_gemv_heads(const uint8_t* w, int in_dim, unsigned long long row0, int rows_per_head, int n_heads,
+                             const float* x, float* y, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s) {
+    const int out_dim = rows_per_head * n_heads;
+    const GemvPlan plan = plan_gemv(1, in_dim, out_dim, 1, num_cus, kPlanPrep);
+    if (plan.grid == 0) return hipSuccess;
+    if ((size_t)n_heads * in_dim * 4 >= kOutOfRange) return hipErrorInvalidValue;
+    const uint8_t* ww[1] = {w};
+    float* yy[1] = {y};
+    GemvArgs a = base_args(plan, ww, yy, 1, in_dim, row0, out_dim, ws, err);
+    a.x = x;
+    a.tiles_per_head = rows_per_head / kTileRows;
+    a.head_stride = (uint32_t)in_dim * 4u;
+    a.x_bytes = (uint32_t)((size_t)n_heads * in_dim * 4);
     return launch_gemv_nt<1, 1>(plan, a, s);
 }
 

@@ -75,6 +75,12 @@ hipError_t launch_gemv_t64(const uint8_t* const* w, float* const* y, int n_tenso
 hipError_t launch_gemv_x(const uint8_t* const* w, float* const* y, int n_tensors, int in_dim,
                          unsigned long long row0, int out_dim, const float* x, const float* x2, float lim,
                          uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s);
+// Per-head products in one launch: head h < n_heads multiplies its own
+// vector x[h*in_dim ..] by rows row0 + h*rows_per_head .. (rows_per_head a
+// multiple of 64), y[h*rows_per_head + j]. ws/err as launch_gemv_x with
+// out_dim = n_heads * rows_per_head.
+hipError_t launch_gemv_heads(const uint8_t* w, int in_dim, unsigned long long row0, int rows_per_head, int n_heads,
+                             const float* x, float* y, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s);
 // Dense-MLP pair of launches (model.cpp:677-690) without a host round trip:
 // launch_gate_up_swiglu runs gate and up (same shape, out_dim rows of
 // in_dim) against one fp32 x, and the workgroup that completes a row tile

@@ -1,6 +1,7 @@
 // C++ host layer over the gpeed C ABI (see glm5_gpu.h).
 #include "glm5_gpu.h"
 
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 #include <stdexcept>
@@ -190,6 +191,26 @@ void WeightStore::matmul_quant(const std::string& name, uint64_t row0, int in_di
           ("weights: matmul_quant " + name).c_str());
     check_ws(ws, "weights: matmul_quant " + name);
     check(gpeed_memcpy(Y, yd, yb, kD2H), "weights: download y");
+}
+
+void WeightStore::matvec_heads(const std::string& name, uint64_t row0, int in_dim, int rows_per_head, int n_heads,
+                               const float* x, float* dst) {
+    if (n_heads <= 0 || rows_per_head <= 0) return;
+    const Tensor& t = get(name, in_dim);
+    const int out_dim = rows_per_head * n_heads;
+    const size_t xb = (size_t)n_heads * in_dim * sizeof(float), yb = (size_t)out_dim * sizeof(float);
+    void* xd = scratch(x_, xb, false);
+    void* yd = scratch(y_, yb, false);
+    const size_t wsb = gpeed_iq3xxs_gemv_ws_bytes(1, in_dim, out_dim, 1);
+    if (wsb == 0) throw std::runtime_error("weights: unsupported shape for " + name);
+    Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
+    void* ws = scratch(wbuf, std::max(wsb, gpeed_iq3xxs_matvec_ws_bytes(in_dim, out_dim)), true);
+    check(gpeed_memcpy(xd, x, xb, kH2D), "weights: upload x");
+    check(gpeed_iq3xxs_matvec_heads(t.t64, t.n_rows, row0, in_dim, rows_per_head, n_heads,
+                                    static_cast<const float*>(xd), static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
+          ("weights: matvec_heads " + name).c_str());
+    check_ws(ws, "weights: matvec_heads " + name);
+    check(gpeed_memcpy(dst, yd, yb, kD2H), "weights: download y");
 }
 
 void WeightStore::moe_experts(const std::string& gate, const std::string& up, const std::string& down, int n_exp,

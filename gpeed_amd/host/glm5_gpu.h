@@ -80,6 +80,13 @@ public:
     void matmul_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* X,
                       int n_tok, float* Y);
 
+    // The per-head absorbed projections of MLA attention (model.cpp:638-643,
+    // 664-665) as one launch: for h < n_heads, dst[h*rows_per_head ..] =
+    // rows row0 + h*rows_per_head .. of the tensor times x[h*in_dim ..]; the
+    // same as n_heads matvec_quant calls. rows_per_head, row0 multiples of 64.
+    void matvec_heads(const std::string& name, uint64_t row0, int in_dim, int rows_per_head, int n_heads,
+                      const float* x, float* dst);
+
     // Model::moe_batch steps 1-3: router top_k over logits [n_tok][n_exp]
     // (mode 0: sigmoid + bias with routed_scale / norm_topk as the reference;
     // mode 1: softmax over the top_k), expert buckets, per-expert gate/up

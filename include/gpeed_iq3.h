@@ -263,6 +263,18 @@ int gpeed_iq3xxs_gemv2_x(const void* w_a, const void* w_b, uint64_t n_rows, uint
 int gpeed_iq3xxs_gemv_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                              const float* g, const float* u, float limit, float* dst, void* ws, size_t ws_bytes,
                              gpeed_stream_t stream);
+/* The per-head absorbed projections of MLA attention in one launch: for
+ * head h < n_heads, dst[h*rows_per_head + j] = sum_i W[row0 + h*rows_per_head
+ * + j][i] * x[h*in_dim + i], j < rows_per_head. These are the n_heads
+ * matvec_quant calls with row0 = h * rows_per_head on each head's own
+ * vector: attn_k_b at model.cpp:638-643 (rows h*kv_lora, in_dim qk_nope)
+ * and attn_v_b at model.cpp:664-665 (rows h*v_head, in_dim kv_lora).
+ * x [n_heads][in_dim], dst [n_heads][rows_per_head] fp32; rows_per_head and
+ * row0 multiples of 64. ws: gpeed_iq3xxs_gemv_ws_bytes(1, in_dim,
+ * n_heads * rows_per_head, 1) bytes, initialised once. */
+int gpeed_iq3xxs_matvec_heads(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int rows_per_head,
+                              int n_heads, const float* x, float* dst, void* ws, size_t ws_bytes,
+                              gpeed_stream_t stream);
 /* Model::dense_mlp (model.cpp:677-690) on the device without the
  * intermediate vectors: y = W_down (silu(min(g,limit)) * clamp(u,-limit,limit))
  * with g = W_gate x, u = W_up x. gate and up run together; the workgroup

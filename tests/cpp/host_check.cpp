@@ -21,6 +21,7 @@
 //         matvec <tensor> <row0> <in> <out> <x> <y>
 //         matmul <tensor> <row0> <in> <out> <n_tok> <X> <Y>
 //         moe <gate> <up> <down> <E> <H> <I> <T> <K> <X> <logits> <Y>
+//         heads <tensor> <row0> <in> <rows_per_head> <n_heads> <x> <y>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -241,6 +242,15 @@ int main(int argc, char** argv) {
                     else
                         ws.matmul_quant(name, row0, in_dim, out_dim, reinterpret_cast<const float*>(x.data()), n_tok,
                                         y.data());
+                    spit(yf, y.data(), y.size() * 4);
+                } else if (op == "heads") {
+                    std::string name, xf, yf;
+                    uint64_t row0 = 0;
+                    int in_dim = 0, rph = 0, nh = 0;
+                    in >> name >> row0 >> in_dim >> rph >> nh >> xf >> yf;
+                    const std::vector<char> x = slurp(xf);
+                    std::vector<float> y((size_t)rph * nh);
+                    ws.matvec_heads(name, row0, in_dim, rph, nh, reinterpret_cast<const float*>(x.data()), y.data());
                     spit(yf, y.data(), y.size() * 4);
                 } else if (op == "moe") {
                     std::string g, u, d, xf, lf, yf;

@@ -226,27 +226,32 @@ def test_store_products_by_name(gpu, tmp_path):
     model (tensors uploaded on first use) and the routed-expert step on the
     file's 3-D expert tensors, against the oracle."""
     H, I, E, T, K = 512, 256, 8, 5, 2
+    NH, KVL, DK = 16, 512, 256  # attn_k_b: NH heads of KVL rows over DK
     wq = synth.iq3xxs_matrix(79, 0, 384, 1024)
+    wk = synth.iq3xxs_matrix(79, 8, NH * KVL, DK)
     wg = synth.iq3xxs_matrix(79, 1, E * I, H)
     wu = synth.iq3xxs_matrix(79, 2, E * I, H)
     wd = synth.iq3xxs_matrix(79, 3, E * H, I)
     tensors = [("blk.3.attn_q_b.weight", [1024, 384], gguf.IQ3_XXS, wq.tobytes()),
                ("blk.3.ffn_gate_exps.weight", [H, I, E], gguf.IQ3_XXS, wg.tobytes()),
                ("blk.3.ffn_up_exps.weight", [H, I, E], gguf.IQ3_XXS, wu.tobytes()),
-               ("blk.3.ffn_down_exps.weight", [I, H, E], gguf.IQ3_XXS, wd.tobytes())]
+               ("blk.3.ffn_down_exps.weight", [I, H, E], gguf.IQ3_XXS, wd.tobytes()),
+               ("blk.3.attn_k_b.weight", [DK, NH * KVL], gguf.IQ3_XXS, wk.tobytes())]
     path = str(tmp_path / "m.gguf")
     gguf.write(path, [("general.alignment", gguf.UINT32, 32)], tensors)
     x = synth.normal(79, 4, 1024)
     X = synth.normal(79, 5, 12 * 1024).reshape(12, 1024)
     Xm = synth.normal(79, 6, T * H).reshape(T, H)
     logits = synth.normal(79, 7, T * E).reshape(T, E)
-    for name, a in (("x", x), ("X", X), ("Xm", Xm), ("lg", logits)):
+    qn = synth.normal(79, 9, NH * DK).reshape(NH, DK)
+    for name, a in (("x", x), ("X", X), ("Xm", Xm), ("lg", logits), ("qn", qn)):
         a.astype(np.float32).tofile(tmp_path / f"{name}.bin")
     (tmp_path / "s.txt").write_text(
         f"matvec blk.3.attn_q_b.weight 64 1024 300 {tmp_path / 'x.bin'} {tmp_path / 'y.bin'}\n"
         f"matmul blk.3.attn_q_b.weight 0 1024 384 12 {tmp_path / 'X.bin'} {tmp_path / 'Y.bin'}\n"
         f"moe blk.3.ffn_gate_exps.weight blk.3.ffn_up_exps.weight blk.3.ffn_down_exps.weight {E} {H} {I} {T} {K} "
-        f"{tmp_path / 'Xm.bin'} {tmp_path / 'lg.bin'} {tmp_path / 'Ym.bin'}\n")
+        f"{tmp_path / 'Xm.bin'} {tmp_path / 'lg.bin'} {tmp_path / 'Ym.bin'}\n"
+        f"heads blk.3.attn_k_b.weight 0 {DK} {KVL} {NH} {tmp_path / 'qn.bin'} {tmp_path / 'qa.bin'}\n")
     run("gguf-store", path, tmp_path / "s.txt")
     y = np.fromfile(tmp_path / "y.bin", np.float32)
     assert rel_err(y, oracle.matvec(wq, 64, 1024, 300, x)) < TIGHT
@@ -257,3 +262,6 @@ def test_store_products_by_name(gpu, tmp_path):
     eptr, tok, wt, _ = oracle.moe_route(logits, K, 1)
     refm = oracle.moe_experts(wg, wu, wd, H, I, Xm, eptr, tok, wt, 10.0)
     assert max(rel_err(Ym[t], refm[t]) for t in range(T)) < TIGHT
+    qa = np.fromfile(tmp_path / "qa.bin", np.float32).reshape(NH, KVL)
+    for h in range(NH):  # each head: the matvec_quant of model.cpp:640
+        assert rel_err(qa[h], oracle.matvec(wk, h * KVL, DK, KVL, qn[h])) < TIGHT, h
