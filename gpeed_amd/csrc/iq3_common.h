@@ -18,12 +18,19 @@
 //   units (dwords 4u..4u+3 in unit u, at byte u*1024 + 16n). Sub-block ib
 //   of the row sits at dwords 3ib..3ib+2:
 //     q0 = qs[8ib..8ib+3], q1 = qs[8ib+4..8ib+7] (bytes unchanged)
-//     W  = the sign/scale word. The 8 elements 8l..8l+7 of group l form four
-//          pairs (elements 2c, 2c+1 for c = 0..3); pair c of group l owns
-//          bits a and a+16 with a = 4c + l (lower element at bit a). So
-//          rotr(W, a + 17) puts a pair's two signs on the fp16 sign bits of
-//          a packed pair. Bits 28..31 (the implied eighth sign of each group)
-//          hold the scale s instead, bit 28+l = bit l of s.
+//     W  = the sign/scale word. Decoded (t64_signs), it holds the 32
+//          element signs: the 8 elements 8l..8l+7 of group l form four
+//          pairs (elements 2c, 2c+1 for c = 0..3), and pair c of group l owns
+//          bits a and a+16 with a = 4c + l (lower element at bit a), so
+//          rotr(S, a + 17) puts a pair's two signs on the fp16 sign bits of
+//          a packed pair. Group l's bits are 4k + l for k = 0..7, a chain
+//          visiting elements 0, 2, 4, 6, 1, 3, 5, 7. W stores, at chain
+//          position k < 7, the parity of the group's signs at positions
+//          0..k (a prefix parity); the signs are then S = W ^ (W << 4) over
+//          the 28 chain bits, and position 7 (the implied eighth sign, the
+//          parity of all seven stored ones) comes out of the shift as the
+//          stored parity at position 6. Bits 28..31 of W hold the scale s,
+//          bit 28+l = bit l of s.
 // A wavefront loads one record with six fully coalesced 16-byte loads and a
 // 2-byte load; lane n then holds all 256 weights of row n for block b.
 //
@@ -78,22 +85,36 @@ constexpr int t64_sign_bit(int e) {
     return 4 * ((e & 7) >> 1) + (e >> 3) + 16 * (e & 1);
 }
 
-// T64 sign/scale word from a GGUF aux word (see the layout above).
+// Element (within its group of 8) at chain position k of the T64 sign word.
+constexpr int t64_chain_elem(int k) { return k < 4 ? 2 * k : 2 * (k - 4) + 1; }
+
+// T64 sign/scale word from a GGUF aux word (see the layout above): prefix
+// parities of each group's seven stored signs along the chain, and the scale.
 __host__ __device__ inline uint32_t aux_to_t64(uint32_t aux) {
     uint32_t w = (aux >> 28) << 28;
 #pragma unroll
-    for (int l = 0; l < 4; ++l)
+    for (int l = 0; l < 4; ++l) {
+        uint32_t p = 0;
 #pragma unroll
-        for (int j = 0; j < 7; ++j) w |= ((aux >> (7 * l + j)) & 1u) << t64_sign_bit(8 * l + j);
+        for (int k = 0; k < 7; ++k) {
+            p ^= (aux >> (7 * l + t64_chain_elem(k))) & 1u;
+            w |= p << (4 * k + l);
+        }
+    }
     return w;
 }
 
+// The 32 element signs of a T64 sign word at their t64_sign_bit positions,
+// the implied eighth sign of each group included.
+__host__ __device__ inline uint32_t t64_signs(uint32_t w) { return (w & 0x0FFFFFFFu) ^ (w << 4); }
+
 __host__ __device__ inline uint32_t t64_to_aux(uint32_t w) {
+    const uint32_t sgn = t64_signs(w);
     uint32_t aux = (w >> 28) << 28;
 #pragma unroll
     for (int l = 0; l < 4; ++l)
 #pragma unroll
-        for (int j = 0; j < 7; ++j) aux |= ((w >> t64_sign_bit(8 * l + j)) & 1u) << (7 * l + j);
+        for (int j = 0; j < 7; ++j) aux |= ((sgn >> t64_sign_bit(8 * l + j)) & 1u) << (7 * l + j);
     return aux;
 }
 
@@ -162,18 +183,6 @@ __device__ __forceinline__ int pow2_scale_of_max(float m) {
         sc = sc > 120 ? 120 : (sc < -120 ? -120 : sc);
     }
     return sc;
-}
-
-// The T64 sign word with the four implied signs (element 7 of each group,
-// the parity of the other seven) written over the scale nibble. Group l's
-// bits are exactly the positions = l (mod 4), so three xor-folds give all
-// four parities at once, in bits 0..3.
-__device__ __forceinline__ uint32_t t64_full_signs(uint32_t w) {
-    const uint32_t m = w & 0x0FFFFFFFu;
-    uint32_t t = m ^ (m >> 16);
-    t ^= t >> 8;
-    t ^= t >> 4;
-    return m | (t << 28);
 }
 
 // fp16 bit pattern -> fp32, integer-only (exact for every pattern, NaN

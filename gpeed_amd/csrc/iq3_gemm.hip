@@ -274,7 +274,7 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
 // lane/16 of a 32-weight sub-block); it is decoded straight into registers
 // from two dwords of the T64 record (grid-index word, sign/scale word): two
 // lookups in the replicated unsigned grid table, the group's eighth sign
-// from a popcount, four rotate-and-mask sign insertions and an exact fp16
+// from the prefix-parity decode, four rotate-and-mask sign insertions and an exact fp16
 // multiply by 2s+1. X images are staged through LDS 64 columns at a time
 // (double buffered); W dwords are prefetched two stages ahead. Used for fp32
 // X (two images); bf16 X takes k_gemm3.
@@ -377,9 +377,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g_all) {
     // word: unsigned grid values, signs on the fp16 sign bits, then an exact
     // packed fp16 multiply by 2s+1 (|q (2s+1)| <= 1922)
     auto decode_b = [&](uint32_t q, uint32_t w) -> half8_t {
-        uint32_t wg = __builtin_amdgcn_alignbit(w, w, (uint32_t)lg);  // group lg's bits at 4c, 4c+16
-        const uint32_t par = __builtin_popcount(wg & 0x01111111u) & 1u;
-        wg = (wg & 0x0FFFFFFFu) | (par << 28);
+        const uint32_t sw = t64_signs(w);                              // all 32 signs
+        const uint32_t wg = __builtin_amdgcn_alignbit(sw, sw, (uint32_t)lg);  // group lg's at 4c, 4c+16
         const _Float16 s2 = (_Float16)(float)((w >> 27) | 1u);
         const half2v_t s22 = {s2, s2};
         const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, lb, sel0));
@@ -479,7 +478,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g_all) {
 //   * the B operands of stage s+1 (64 columns) are decoded while the MFMAs
 //     of stage s run, from a grid table that already holds grid * (2s+1)
 //     (entry (idx, s) at (idx << 8) | (s << 4), two replicas), so a group of
-//     8 weights costs two lookups, a popcount for its eighth sign and two
+//     8 weights costs two lookups, the sign word's decode and two
 //     64-bit shifts that put four pairs of signs on the fp16 sign bits;
 //   * A operands are read one half-stage ahead from a ring of three X
 //     stages, loaded two stages ahead into registers;
@@ -527,13 +526,9 @@ __device__ __forceinline__ void scaled_grid_table(uint8_t* tbl, int tid) {
 // bytes; rs = replica offset (0 or 8).
 __device__ __forceinline__ half8_t decode_group(const uint8_t* tbl, uint32_t q, uint32_t w, uint32_t lg,
                                                 uint32_t sel0, uint32_t sel1, uint32_t rs) {
-    // group lg's signs: pair c at bits 4c and 4c+16 (c = 0..3); bit 28 then
-    // holds a scale bit instead of the eighth sign
-    uint32_t wg = __builtin_amdgcn_alignbit(w, w, lg);
-    // the eighth sign is the parity of the other seven: adding
-    // popcount(bits 0,4,..,28) << 28 turns bit 28 into exactly that parity
-    // (the carry only reaches bits 29-31, which no pair of this group uses)
-    wg += (uint32_t)__builtin_popcount(wg & 0x11111111u) << 28;
+    // group lg's signs, the eighth included: pair c at bits 4c and 4c+16
+    const uint32_t sw = t64_signs(w);
+    const uint32_t wg = __builtin_amdgcn_alignbit(sw, sw, lg);
     // pairs 0/1 and 2/3: one 64-bit shift of {wg >> 4, wg} each puts a
     // pair's two signs on bits 15 and 31 of both halves
     const uint64_t sw2 = ((uint64_t)(wg >> 4) << 32) | wg;

@@ -166,7 +166,7 @@ __device__ __forceinline__ void grid_lookups(const uint8_t* tbl, uint32_t lb, ui
 template <int NP, int ib>
 __device__ __forceinline__ void subblock_dot(uint32_t w, const u32x2_t (&g)[8], const u32x2_t (&a)[NP][4],
                                              float4_t (&D)[NP]) {
-    const uint32_t sw = t64_full_signs(w);
+    const uint32_t sw = t64_signs(w);
     // The signs of a group's second pair sit 4 bits above those of its first
     // pair, so {sw >> 4, sw} shifted left by one 64-bit shift puts both
     // pairs' signs on bits 15 and 31 of the two halves.

@@ -73,11 +73,19 @@ def sign_bit(e):
     return 4 * (j // 2) + l + 16 * (j & 1)
 
 
+CHAIN = [0, 2, 4, 6, 1, 3, 5, 7]  # group element at chain position k (bit 4k + l)
+
+
 def aux_t64_model(aux):
+    """T64 sign/scale word restated from the layout definition: at chain
+    position k < 7 of group l (bit 4k + l) the parity of the group's signs at
+    chain positions 0..k; the scale in bits 28..31."""
     out = (aux >> 28) << 28
     for l in range(4):
-        for j in range(7):
-            out |= ((aux >> (7 * l + j)) & 1) << sign_bit(8 * l + j)
+        p = 0
+        for k in range(7):
+            p ^= (aux >> (7 * l + CHAIN[k])) & 1
+            out |= p << (4 * k + l)
     return out
 
 
@@ -90,11 +98,41 @@ def test_sign_bits_layout():
     assert all(sign_bit(e) % 4 == e // 8 for e in range(32))
 
 
+def test_sign_chain_positions():
+    """Chain position k of group l is bit 4k + l and holds element CHAIN[k],
+    which is the layout's sign bit of that element."""
+    for l in range(4):
+        for k in range(8):
+            assert sign_bit(8 * l + CHAIN[k]) == 4 * k + l
+
+
 def test_aux_word_matches_model():
     L = gpeed_amd.lib()
     words = synth.u64(3, 0, 4000) & np.uint64(0xFFFFFFFF)
     for w in [0, 0xFFFFFFFF, 0x80000000, 0x0FFFFFFF] + [int(v) for v in words]:
         assert L.gpeed_t64_aux_word(w) == aux_t64_model(w), hex(w)
+
+
+def test_sign_decode_exhaustive():
+    """For every group and every 7-bit sign index (and both extreme scales),
+    the kernels' decode S = (W & 0x0FFFFFFF) ^ (W << 4) of the library's T64
+    word puts each of the group's 8 signs -- the implied eighth, the parity of
+    the seven, included (quant.cpp:196-205) -- on its layout bit."""
+    L = gpeed_amd.lib()
+    for l in range(4):
+        for idx in range(128):
+            for sc in (0, 15):
+                aux = (sc << 28) | (idx << (7 * l))
+                w = L.gpeed_t64_aux_word(aux)
+                assert w >> 28 == sc
+                dec = full_signs_model(w)
+                signs = [(idx >> j) & 1 for j in range(7)]
+                signs.append(sum(signs) & 1)
+                for j in range(8):
+                    assert (dec >> sign_bit(8 * l + j)) & 1 == signs[j], (l, idx, j)
+                for e in range(32):  # the other groups' signs are all +
+                    if e // 8 != l:
+                        assert (dec >> sign_bit(e)) & 1 == 0
 
 
 @pytest.fixture(scope="module")
@@ -106,13 +144,10 @@ def grid_table():
 
 
 def full_signs_model(w):
-    """The kernel's sign word: implied eighth signs (even parity per group)
-    folded in over the scale nibble with three xor-folds (t64_full_signs)."""
-    m = w & 0x0FFFFFFF
-    t = m ^ (m >> 16)
-    t ^= t >> 8
-    t ^= t >> 4
-    return (m | (t << 28)) & 0xFFFFFFFF
+    """The kernels' decoded sign word (t64_signs): each chain bit XORed with
+    the one before it in its group, the eighth signs shifted up from the
+    stored parity at chain position 6 (over the scale nibble)."""
+    return ((w & 0x0FFFFFFF) ^ (w << 4)) & 0xFFFFFFFF
 
 
 def test_grid_table_replicas_conflict_free(grid_table):
