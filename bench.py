@@ -74,6 +74,17 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(wg, wu, wd, x):
     """Reference CPU dense-MLP decode step; returns (record, y_ref)."""
     import oracle
@@ -109,7 +120,7 @@ def cpu_baseline(wg, wu, wd, x):
         step()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    out = {"value": round(W_BYTES / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+    out = {"value": round(W_BYTES / med / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind, "cpu_model": _cpu_model(),
            "sample": f"{len(times)} dense-MLP decode steps (3 matvecs, {W_BYTES} packed bytes each), "
                      f"median; best {W_BYTES / min(times) / 1e9:.4f} GB/s"}
     ref_omp = oracle.ref(openmp=True) if kind == "reference" else None
@@ -611,6 +622,10 @@ def main():
     achieved = pair_bytes / (pair_ms * 1e-3) / 1e9
     kinds = {k: {"dispatch_event_us": round(float(v.mean()) * 1e3, 3), "algorithmic_bytes": launch_bytes[k]}
              for k, v in per_kind.items()}
+    # the down projection (6144x12288) alone: its bytes over its own
+    # dispatch-stamped launch time
+    down_us = float(per_kind["down"].mean()) * 1e3
+    down_gbs = launch_bytes["down"] / (down_us * 1e-6) / 1e9
 
     rec = {
         "metric": METRIC,
@@ -637,7 +652,9 @@ def main():
                                     "copy-calibrated)",
                      "kernel": "k_gemv_t64", "avg_launch_us": round(pair_ms * 1e3 / 2, 3),
                      "pair_us": round(pair_ms * 1e3, 3), "timing": pair_timing,
-                     "pair_algorithmic_bytes": pair_bytes, "launch_kinds": kinds},
+                     "pair_algorithmic_bytes": pair_bytes, "launch_kinds": kinds,
+                     "down": {"shape": "6144x12288", "launch_us": round(down_us, 3),
+                              "achieved": round(down_gbs, 1), "frac": round(down_gbs / HBM_PEAK_GBS, 4)}},
     }
     if not args.no_extra:
         del copies, base

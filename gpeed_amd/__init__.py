@@ -34,6 +34,11 @@ ERRORS = {
 }
 WS_TICKET, WS_TIMEOUT, WS_BUCKETS = 1, 2, 4
 DTYPE_IQ3_XXS = 18
+# ggml type ids of the formats a UD-IQ3_XXS file holds (common.h:10-43)
+DTYPE_F32, DTYPE_F16, DTYPE_Q8_0, DTYPE_Q2_K, DTYPE_Q3_K, DTYPE_Q6_K = 0, 1, 8, 10, 11, 14
+DTYPE_IQ3_S, DTYPE_IQ2_S, DTYPE_IQ4_XS, DTYPE_BF16 = 21, 22, 23, 30
+DTYPES_DECODED = (DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_Q8_0, DTYPE_Q2_K, DTYPE_Q3_K, DTYPE_Q6_K, DTYPE_IQ3_XXS,
+                  DTYPE_IQ3_S, DTYPE_IQ2_S, DTYPE_IQ4_XS)
 QK = 256
 BLOCK_BYTES = 98
 
@@ -63,6 +68,10 @@ def lib():
             "gpeed_iq3xxs_row_bytes": ([i64], sz),
             "gpeed_iq3xxs_t64_bytes": ([u64, i64], sz),
             "gpeed_dequantize": ([i32, vp, vp, u64, vp], i32),
+            "gpeed_dtype_block_size": ([i32], i32),
+            "gpeed_dtype_row_bytes": ([i32, u64], sz),
+            "gpeed_matmul_rows": ([i32, vp, u64, u64, i32, i32, vp, i32, vp, vp], i32),
+            "gpeed_codebook": ([i32, vp, sz], i32),
             "gpeed_t64_grid_table": ([vp, sz], i32),
             "gpeed_t64_aux_word": ([C.c_uint32], C.c_uint32),
             "gpeed_iq3xxs_tile": ([vp, u64, i64, vp, vp], i32),
@@ -204,8 +213,27 @@ def t64_bytes(n_rows: int, in_dim: int) -> int:
     return lib().gpeed_iq3xxs_t64_bytes(n_rows, in_dim)
 
 
+def dtype_block_size(dtype: int) -> int:
+    """dtype_block_size (quant.cpp:52-81) for the decoded types, else 0."""
+    return lib().gpeed_dtype_block_size(dtype)
+
+
+def dtype_row_bytes(dtype: int, n: int) -> int:
+    """dtype_row_bytes (quant.cpp:119-126) for the decoded types, else 0."""
+    return lib().gpeed_dtype_row_bytes(dtype, n)
+
+
+def codebook(dtype: int) -> np.ndarray:
+    """The expanded grid the kernels use for IQ2_S, IQ3_S or IQ3_XXS (uint64 per entry)."""
+    n = {DTYPE_IQ2_S: 1024, DTYPE_IQ3_S: 512, DTYPE_IQ3_XXS: 256}[dtype]
+    out = np.zeros(n, np.uint64)
+    _check(lib().gpeed_codebook(dtype, out.ctypes.data, n), "codebook")
+    return out
+
+
 def dequantize(raw, n: int, out=None, dtype: int = DTYPE_IQ3_XXS, stream=None):
-    """fp32 [n] from GGUF bytes on the device (bit-exact with quant.cpp:186-210)."""
+    """fp32 [n] from GGUF bytes of any decoded type on the device (bit-exact
+    with quant.cpp:165-563)."""
     torch = _torch()
     _require_cuda(raw)
     if out is None:
@@ -557,6 +585,21 @@ def moe_experts(w_gate, w_up, w_down, n_exp: int, hidden: int, inter: int, X, to
     return out
 
 
+def matmul_rows(dtype: int, w, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None, stream=None):
+    """Y[t][j] = sum_i W[row0+j][i] * X[t][i] over GGUF rows of any decoded type
+    kept on the device (weights.cpp:86-203). X: [in_dim] or [n_tok, in_dim]."""
+    torch = _torch()
+    _require_cuda(w, X)
+    vec = X.dim() == 1
+    X2 = X.reshape(1 if vec else X.shape[0], in_dim)
+    n_tok = X2.shape[0]
+    if out is None:
+        out = torch.empty((n_tok, out_dim), dtype=torch.float32, device=X.device)
+    _check(lib().gpeed_matmul_rows(dtype, _ptr(w), n_rows, row0, in_dim, out_dim, _ptr(X2), n_tok, _ptr(out),
+                                   _stream(stream)), "matmul_rows")
+    return out.reshape(out_dim) if vec else out
+
+
 class WeightStore:
     """Device-resident IQ3_XXS tensors behind the reference's matvec_quant contract.
 
@@ -577,17 +620,22 @@ class WeightStore:
         self.tensors = {}
         self._ws = {}
 
-    def add(self, name: str, payload, in_dim: int, n_rows: int):
+    def add(self, name: str, payload, in_dim: int, n_rows: int, dtype: int = DTYPE_IQ3_XXS):
+        """IQ3_XXS rows are kept in the T64 layout; the other decoded types as
+        their GGUF rows."""
         torch = _torch()
-        if in_dim % QK:
+        bs = dtype_block_size(dtype)
+        if bs == 0:
+            raise RuntimeError(f"weights: type {dtype} is not decoded")
+        if in_dim % bs:
             raise RuntimeError(f"weights: row not block aligned for {name}")
         if isinstance(payload, np.ndarray):
             raw = torch.from_numpy(np.ascontiguousarray(payload).reshape(-1).view(np.uint8)).to(self.device)
         else:
             raw = payload.reshape(-1)
-        t64 = tile(raw, n_rows, in_dim)
-        self.tensors[name] = (t64, in_dim, n_rows)
-        return t64
+        dev = tile(raw, n_rows, in_dim) if dtype == DTYPE_IQ3_XXS else raw.clone()
+        self.tensors[name] = (dev, in_dim, n_rows, dtype)
+        return dev
 
     def has(self, name: str) -> bool:
         return name in self.tensors
@@ -595,7 +643,7 @@ class WeightStore:
     def _get(self, name: str, in_dim: int):
         if name not in self.tensors:
             raise RuntimeError(f"weights: missing tensor {name}")
-        if in_dim % QK:
+        if in_dim % dtype_block_size(self.tensors[name][3]):
             raise RuntimeError(f"weights: row not block aligned for {name}")
         return self.tensors[name]
 
@@ -611,15 +659,20 @@ class WeightStore:
 
     def matvec_quant(self, name: str, row0: int, in_dim: int, out_dim: int, x, dst=None):
         torch = _torch()
-        t64, _, n_rows = self._get(name, in_dim)
+        t64, _, n_rows, dtype = self._get(name, in_dim)
         host = isinstance(x, np.ndarray)
         if out_dim <= 0:
             return dst
         xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(self.device) if host else x
-        ws = self._workspace(in_dim, out_dim, 1)
-        yd = matvec(t64, n_rows, row0, in_dim, out_dim, xd, ws=ws)
+        if dtype != DTYPE_IQ3_XXS:
+            yd = matmul_rows(dtype, t64, n_rows, row0, in_dim, out_dim, xd.reshape(in_dim))
+            ws = None
+        else:
+            ws = self._workspace(in_dim, out_dim, 1)
+            yd = matvec(t64, n_rows, row0, in_dim, out_dim, xd, ws=ws)
         if host:
-            ws_status(ws)  # synchronous, like the reference: report a flagged workspace here
+            if ws is not None:
+                ws_status(ws)  # synchronous, like the reference: report a flagged workspace here
             y = yd.cpu().numpy()
             if dst is not None:
                 dst[:out_dim] = y
@@ -632,16 +685,21 @@ class WeightStore:
 
     def matmul_quant(self, name: str, row0: int, in_dim: int, out_dim: int, X, n_tok: int, Y=None):
         torch = _torch()
-        t64, _, n_rows = self._get(name, in_dim)
+        t64, _, n_rows, dtype = self._get(name, in_dim)
         if n_tok <= 0 or out_dim <= 0:
             return Y
         host = isinstance(X, np.ndarray)
         Xd = torch.from_numpy(np.ascontiguousarray(X, np.float32).reshape(n_tok, in_dim)).to(self.device) \
             if host else X.reshape(n_tok, in_dim)
-        ws = self._workspace(in_dim, out_dim, n_tok)
-        Yd = matmul(t64, n_rows, row0, in_dim, out_dim, Xd, ws=ws)
+        if dtype != DTYPE_IQ3_XXS:
+            Yd = matmul_rows(dtype, t64, n_rows, row0, in_dim, out_dim, Xd)
+            ws = None
+        else:
+            ws = self._workspace(in_dim, out_dim, n_tok)
+            Yd = matmul(t64, n_rows, row0, in_dim, out_dim, Xd, ws=ws)
         if host:
-            ws_status(ws)
+            if ws is not None:
+                ws_status(ws)
             y = Yd.cpu().numpy()
             if Y is not None:
                 Y.reshape(n_tok, out_dim)[:] = y

@@ -16,7 +16,7 @@ LIB = os.path.join(HERE, "libgpeed_iq3.so")
 HOST_LIB = os.path.join(HERE, "libgpeed_glm5.so")
 ROOT = os.path.dirname(HERE)
 HOST_CHECK = os.path.join(ROOT, "tests", "cpp", "host_check")
-SOURCES = ["capi.hip", "iq3_dequant.hip", "iq3_gemv.hip", "iq3_moe.hip", "iq3_gemm.hip"]
+SOURCES = ["capi.hip", "iq3_dequant.hip", "iq3_gemv.hip", "iq3_moe.hip", "iq3_gemm.hip", "quant_rows.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",

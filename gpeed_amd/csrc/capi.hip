@@ -314,18 +314,61 @@ size_t gpeed_iq3xxs_t64_bytes(uint64_t n_rows, int64_t in_dim) {
     return gpeed::t64_bytes(n_rows, in_dim);
 }
 
+int gpeed_dtype_block_size(int dtype) { return gpeed::rows_block_elems(dtype); }
+
+size_t gpeed_dtype_row_bytes(int dtype, uint64_t n) {
+    const int be = gpeed::rows_block_elems(dtype);
+    if (be == 0 || n % (uint64_t)be) return 0;
+    return (size_t)(n / (uint64_t)be) * gpeed::rows_block_bytes(dtype);
+}
+
 int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_stream_t stream) {
-    if (dtype != GPEED_DTYPE_IQ3_XXS)
-        return fail(GPEED_ERR_UNIMPLEMENTED, "dequantize: dtype not handled on the GPU path");
-    if (n % gpeed::kQK)
+    const int be = gpeed::rows_block_elems(dtype);
+    if (be == 0) return fail(GPEED_ERR_UNIMPLEMENTED, "dequantize: unimplemented type " + std::to_string(dtype));
+    if (n % (uint64_t)be)
         return fail(GPEED_ERR_NOT_MULTIPLE, "dequantize: element count not a multiple of block size");
     if (n == 0) return GPEED_OK;
     if (!src || !dst) return fail(GPEED_ERR_INVALID, "dequantize: null pointer");
-    if (!aligned(src, 2) || !aligned(dst, 16))
-        return fail(GPEED_ERR_INVALID, "dequantize: src must be 2-byte and dst 16-byte aligned");
-    hipError_t e = gpeed::launch_dequant_raw(static_cast<const uint8_t*>(src), dst, n,
-                                             static_cast<hipStream_t>(stream));
+    const size_t src_align = dtype == GPEED_DTYPE_F32 ? 4 : 2;
+    if (!aligned(src, src_align) || !aligned(dst, 16))
+        return fail(GPEED_ERR_INVALID, "dequantize: src must be element-aligned (2 bytes, F32 4) and dst 16-byte aligned");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = dtype == GPEED_DTYPE_IQ3_XXS
+                       ? gpeed::launch_dequant_raw(static_cast<const uint8_t*>(src), dst, n, s)
+                       : gpeed::launch_dequant_rows(dtype, static_cast<const uint8_t*>(src), dst, n, s);
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "dequantize launch");
+}
+
+int gpeed_matmul_rows(int dtype, const void* w, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                      const float* X, int n_tok, float* Y, gpeed_stream_t stream) {
+    if (n_tok <= 0 || out_dim <= 0) return GPEED_OK;  // weights.cpp:88
+    const int be = gpeed::rows_block_elems(dtype);
+    if (be == 0) return fail(GPEED_ERR_UNIMPLEMENTED, "matmul_rows: unimplemented type " + std::to_string(dtype));
+    // the kernels walk rows in 32-weight runs
+    if (in_dim <= 0 || in_dim % be || in_dim % 32)
+        return fail(GPEED_ERR_UNALIGNED_ROW, "matmul_rows: row not block aligned (and a multiple of 32)");
+    if (in_dim > (1 << 28) || n_tok > (1 << 24)) return fail(GPEED_ERR_INVALID, "matmul_rows: size too large");
+    if (!w || !X || !Y) return fail(GPEED_ERR_INVALID, "matmul_rows: null pointer");
+    if (row0 > n_rows || (uint64_t)out_dim > n_rows - row0)
+        return fail(GPEED_ERR_INVALID, "matmul_rows: rows [row0, row0 + out_dim) outside the tensor");
+    if (!aligned(w, dtype == GPEED_DTYPE_F32 ? 4 : 2) || !aligned(X, 16) || !aligned(Y, 4))
+        return fail(GPEED_ERR_INVALID, "matmul_rows: w element-aligned, X 16-byte and Y 4-byte aligned");
+    const size_t rb = gpeed_dtype_row_bytes(dtype, (uint64_t)in_dim);
+    hipError_t e = gpeed::launch_matmul_rows(dtype, static_cast<const uint8_t*>(w), rb, row0, in_dim, out_dim, X,
+                                             n_tok, Y, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matmul_rows launch");
+}
+
+int gpeed_codebook(int dtype, uint64_t* out, size_t n) {
+    const size_t len = dtype == GPEED_DTYPE_IQ2_S ? 1024 : dtype == GPEED_DTYPE_IQ3_S ? 512
+                                                      : dtype == GPEED_DTYPE_IQ3_XXS ? 256 : 0;
+    if (len == 0) return fail(GPEED_ERR_UNIMPLEMENTED, "codebook: no grid for this type");
+    if (!out || n < len) return fail(GPEED_ERR_INVALID, "codebook: buffer too small");
+    for (size_t i = 0; i < len; ++i)
+        out[i] = dtype == GPEED_DTYPE_IQ2_S ? gpeed::rows_iq2s_grid((int)i)
+                 : dtype == GPEED_DTYPE_IQ3_S ? gpeed::rows_iq3s_grid((int)i)
+                                              : gpeed::kIq3xxsGrid[i];
+    return GPEED_OK;
 }
 
 int gpeed_t64_grid_table(uint16_t* out, size_t n) {

@@ -21,6 +21,17 @@ hipError_t launch_fill_zero(void* p, size_t n, hipStream_t s);
 
 // quant.cpp:186-210 over n/256 raw GGUF blocks -> fp32 (bit-exact).
 hipError_t launch_dequant_raw(const uint8_t* src, float* dst, unsigned long long n, hipStream_t s);
+
+// Raw GGUF rows of any format the reference decodes (quant_rows.hip):
+// geometry (0 for other types), dequantization of n weights, and
+// Y[t][j] = sum_i W[row0 + j][i] * X[t][i].
+int rows_block_elems(int dtype);
+size_t rows_block_bytes(int dtype);
+hipError_t launch_dequant_rows(int dtype, const uint8_t* src, float* dst, unsigned long long n, hipStream_t s);
+hipError_t launch_matmul_rows(int dtype, const uint8_t* w, size_t row_bytes, unsigned long long row0, int in_dim,
+                              int out_dim, const float* X, int n_tok, float* Y, hipStream_t s);
+uint64_t rows_iq2s_grid(int i);
+uint32_t rows_iq3s_grid(int i);
 // Streaming read of `bytes` from p (16-byte aligned) by n_groups workgroups;
 // out[i] = a fold of what workgroup i read.
 hipError_t launch_stream_read(const uint8_t* p, unsigned long long bytes, uint32_t* out, int n_groups,

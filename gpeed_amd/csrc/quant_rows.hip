@@ -1,0 +1,470 @@
+// The other GGUF formats of a UD-IQ3_XXS file on the GPU (gfx950): F32, F16,
+// BF16, Q8_0, Q2_K, Q3_K, Q6_K, IQ2_S, IQ3_S, IQ4_XS (and IQ3_XXS through the
+// same code): dequantization and products over raw GGUF rows.
+//
+// The unit of work is a 32-weight sub-block: every format's scales are
+// constant over 16 or 32 weights, so one lane decodes 32 weights with two
+// scales at most. Each decoder mirrors the reference's block function
+// (quant.cpp:165-502) operation for operation with FP contraction off, so
+// every dequantized value is bit-identical to the CPU decode; the products
+// then accumulate y * x in fp32 with fused multiply-adds.
+//
+// The codebooks (IQ2_S 1024 x 8 bytes, IQ3_S 512 x 4, IQ3_XXS 256 x 4, the
+// 16 IQ4 levels) are expanded at compile time and copied into LDS by each
+// workgroup.
+#include "iq3_common.h"
+#include "iq3_kernels.h"
+#include "quant_grids.h"
+
+#include <type_traits>
+
+namespace gpeed {
+
+namespace {
+
+constexpr int kDtF32 = 0, kDtF16 = 1, kDtQ8_0 = 8, kDtQ2_K = 10, kDtQ3_K = 11, kDtQ6_K = 14, kDtIQ3_XXS = 18,
+              kDtIQ3_S = 21, kDtIQ2_S = 22, kDtIQ4_XS = 23, kDtBF16 = 30;
+
+struct Iq2sGrid { uint64_t v[1024]; };
+struct Iq3sGrid { uint32_t v[512]; };
+constexpr uint16_t kIq2sPacked[1024] = {GPEED_IQ2S_PACKED};
+constexpr uint16_t kIq3sPacked[512] = {GPEED_IQ3S_PACKED};
+constexpr uint8_t kIq2sLevel[3] = {GPEED_IQ2S_LEVELS};
+constexpr int8_t kIq4nl[16] = {GPEED_IQ4NL_VALUES};
+
+constexpr Iq2sGrid expand_iq2s() {
+    Iq2sGrid g{};
+    for (int i = 0; i < 1024; ++i) {
+        uint64_t e = 0;
+        for (int j = 0; j < 8; ++j) e |= (uint64_t)kIq2sLevel[(kIq2sPacked[i] >> (2 * j)) & 3] << (8 * j);
+        g.v[i] = e;
+    }
+    return g;
+}
+constexpr Iq3sGrid expand_iq3s() {
+    Iq3sGrid g{};
+    for (int i = 0; i < 512; ++i) {
+        uint32_t e = 0;
+        for (int j = 0; j < 4; ++j) e |= (2u * ((kIq3sPacked[i] >> (3 * j)) & 7u) + 1u) << (8 * j);
+        g.v[i] = e;
+    }
+    return g;
+}
+constexpr Iq2sGrid kIq2sGrid = expand_iq2s();
+constexpr Iq3sGrid kIq3sGrid = expand_iq3s();
+
+// Geometry (quant.cpp:52-114): weights per block, bytes per block. Scalar
+// types are handled in 32-weight runs.
+template <int DT> struct Fmt;
+template <> struct Fmt<kDtF32> { static constexpr int kElems = 32, kBytes = 128; };
+template <> struct Fmt<kDtF16> { static constexpr int kElems = 32, kBytes = 64; };
+template <> struct Fmt<kDtBF16> { static constexpr int kElems = 32, kBytes = 64; };
+template <> struct Fmt<kDtQ8_0> { static constexpr int kElems = 32, kBytes = 34; };
+template <> struct Fmt<kDtQ2_K> { static constexpr int kElems = 256, kBytes = 84; };
+template <> struct Fmt<kDtQ3_K> { static constexpr int kElems = 256, kBytes = 110; };
+template <> struct Fmt<kDtQ6_K> { static constexpr int kElems = 256, kBytes = 210; };
+template <> struct Fmt<kDtIQ3_XXS> { static constexpr int kElems = 256, kBytes = 98; };
+template <> struct Fmt<kDtIQ3_S> { static constexpr int kElems = 256, kBytes = 110; };
+template <> struct Fmt<kDtIQ2_S> { static constexpr int kElems = 256, kBytes = 82; };
+template <> struct Fmt<kDtIQ4_XS> { static constexpr int kElems = 256, kBytes = 136; };
+
+// Codebook copies in LDS (only the one the format uses is sized).
+template <int DT>
+struct Tables {
+    static constexpr int kN = DT == kDtIQ2_S ? 1024 : DT == kDtIQ3_S ? 512 : DT == kDtIQ3_XXS ? 256 : 16;
+    using T = typename std::conditional<DT == kDtIQ2_S, uint64_t, uint32_t>::type;
+    T v[kN];
+    __device__ void load(int tid, int nthreads) {
+        for (int i = tid; i < kN; i += nthreads) {
+            if constexpr (DT == kDtIQ2_S) v[i] = kIq2sGrid.v[i];
+            else if constexpr (DT == kDtIQ3_S) v[i] = kIq3sGrid.v[i];
+            else if constexpr (DT == kDtIQ3_XXS) v[i] = kIq3xxsGrid[i];
+            else v[i] = (uint32_t)(int32_t)kIq4nl[i];
+        }
+    }
+};
+
+// Loads of block fields: blocks sit at 2-byte-aligned addresses (every
+// block size is even), so wider fields are assembled from 16-bit loads.
+__device__ __forceinline__ uint32_t u8(const uint8_t* p) { return *p; }
+__device__ __forceinline__ uint32_t u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ __forceinline__ uint32_t u32a2(const uint8_t* p) { return u16(p) | (u16(p + 2) << 16); }
+// 32 bytes from a 2-byte-aligned address as 8 little-endian words
+__device__ __forceinline__ void bytes32(const uint8_t* p, uint32_t (&w)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = u32a2(p + 4 * i);
+}
+__device__ __forceinline__ uint32_t byte_of(const uint32_t (&w)[8], int i) { return (w[i >> 2] >> (8 * (i & 3))) & 255u; }
+
+// decode32: weights 32*sb .. 32*sb+31 of the block at blk into y. Each
+// formula restates the reference's block function for those weights; the
+// comment gives its lines and the byte layout.
+template <int DT>
+__device__ __forceinline__ void decode32(const uint8_t* __restrict__ blk, int sb, const Tables<DT>& tb, float (&y)[32]) {
+#pragma clang fp contract(off)
+    if constexpr (DT == kDtF32) {
+        // quant.cpp:528-531: a copy
+        const float* f = reinterpret_cast<const float*>(blk);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) y[i] = f[i];
+    } else if constexpr (DT == kDtF16 || DT == kDtBF16) {
+        // quant.cpp:532-545 (f16_to_f32 :130-154, bf16_to_f32 :156-161)
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const uint32_t h = u16(blk + 2 * i);
+            y[i] = DT == kDtF16 ? f16_bits_to_f32(h) : __uint_as_float(h << 16);
+        }
+    } else if constexpr (DT == kDtQ8_0) {
+        // quant.cpp:165-184: d (fp16), 32 int8 codes; y = d * q
+        const float d = f16_bits_to_f32(u16(blk));
+        uint32_t w[8];
+        bytes32(blk + 2, w);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) y[i] = d * (float)(int8_t)byte_of(w, i);
+    } else if constexpr (DT == kDtQ6_K) {
+        // quant.cpp:212-306: ql[128] qh[64] sc[16] d. Sub-block sb: half
+        // h = sb/4, quarter q = sb%4; weight l < 32 takes the low (q < 2)
+        // or high nibble of ql[64h + 32(q&1) + l], bits 2q of qh[32h + l],
+        // scale sc[8h + 2q + l/16]; y = (d * sc) * (v - 32).
+        const int h = sb >> 2, q = sb & 3;
+        const float d = f16_bits_to_f32(u16(blk + 208));
+        const float ds0 = d * (float)(int8_t)u8(blk + 192 + 8 * h + 2 * q);
+        const float ds1 = d * (float)(int8_t)u8(blk + 192 + 8 * h + 2 * q + 1);
+        uint32_t lo[8], hi[8];
+        bytes32(blk + 64 * h + 32 * (q & 1), lo);
+        bytes32(blk + 128 + 32 * h, hi);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) {
+            const uint32_t b = byte_of(lo, l);
+            const uint32_t nib = q >= 2 ? b >> 4 : b & 15u;
+            const int v = (int)(nib | (((byte_of(hi, l) >> (2 * q)) & 3u) << 4)) - 32;
+            y[l] = (l < 16 ? ds0 : ds1) * (float)v;
+        }
+    } else if constexpr (DT == kDtQ2_K) {
+        // quant.cpp:309-335: scales[16] qs[64] d dmin. Sub-block sb: half
+        // h = sb/4, plane j = sb%4; weight l < 32: code (qs[32h + l] >> 2j)
+        // & 3, scale byte scales[8h + 2j + l/16];
+        // y = (d * (sc & 15)) * code - dmin * (sc >> 4).
+        const int h = sb >> 2, j = sb & 3;
+        const float d = f16_bits_to_f32(u16(blk + 80));
+        const float mn = f16_bits_to_f32(u16(blk + 82));
+        const uint32_t s0 = u8(blk + 8 * h + 2 * j), s1 = u8(blk + 8 * h + 2 * j + 1);
+        const float dl0 = d * (float)(s0 & 15u), ml0 = mn * (float)(s0 >> 4);
+        const float dl1 = d * (float)(s1 & 15u), ml1 = mn * (float)(s1 >> 4);
+        uint32_t w[8];
+        bytes32(blk + 16 + 32 * h, w);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) {
+            const float c = (float)((byte_of(w, l) >> (2 * j)) & 3u);
+            y[l] = l < 16 ? dl0 * c - ml0 : dl1 * c - ml1;
+        }
+    } else if constexpr (DT == kDtQ3_K) {
+        // quant.cpp:337-370: hmask[32] qs[64] scales[12] d. Sub-block sb:
+        // h = sb/4, j = sb%4; weight l < 32: code (qs[32h + l] >> 2j) & 3,
+        // minus 4 where bit 4h + j of hmask[l] is clear; 6-bit scale k =
+        // 8h + 2j + l/16 unpacked from the 12 bytes (low nibble of byte k,
+        // or high nibble of byte k-8 for k >= 8; top bits from byte 8 + k%4
+        // at 2*(k/4)); y = (d * (scale - 32)) * value.
+        const int h = sb >> 2, j = sb & 3;
+        const float d = f16_bits_to_f32(u16(blk + 108));
+        float dl[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int k = 8 * h + 2 * j + s;
+            const uint32_t low = k < 8 ? u8(blk + 96 + k) & 15u : u8(blk + 96 + k - 8) >> 4;
+            const uint32_t top = (u8(blk + 104 + (k & 3)) >> (2 * (k >> 2))) & 3u;
+            dl[s] = d * (float)((int)(int8_t)(uint8_t)(low | (top << 4)) - 32);
+        }
+        uint32_t w[8], m[8];
+        bytes32(blk + 32 + 32 * h, w);
+        bytes32(blk, m);
+#pragma unroll
+        for (int l = 0; l < 32; ++l) {
+            const int code = (int)((byte_of(w, l) >> (2 * j)) & 3u);
+            const int v = code - (((byte_of(m, l) >> (4 * h + j)) & 1u) ? 0 : 4);
+            y[l] = dl[l >> 4] * (float)v;
+        }
+    } else if constexpr (DT == kDtIQ3_XXS) {
+        // quant.cpp:186-210: d, qs[64] grid indices, 8 words of 4 x 7 sign
+        // bits + 4-bit scale; the eighth sign of a group makes the parity
+        // even. y = ((d * (0.5 + s)) * 0.5) * grid * sign.
+        const float d = f16_bits_to_f32(u16(blk));
+        const uint32_t aux = u32a2(blk + 66 + 4 * sb);
+        const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t qq = u16(blk + 2 + 8 * sb + 2 * l);
+            const uint32_t s7 = (aux >> (7 * l)) & 127u;
+            const uint32_t sg = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+            const uint32_t g1 = tb.v[qq & 255u], g2 = tb.v[qq >> 8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t gv = ((e < 4 ? g1 : g2) >> (8 * (e & 3))) & 255u;
+                y[8 * l + e] = db * (float)gv * (((sg >> e) & 1u) ? -1.0f : 1.0f);
+            }
+        }
+    } else if constexpr (DT == kDtIQ2_S) {
+        // quant.cpp:373-418: d, qs[32] grid low bytes, signs[32], qh[8],
+        // scales[8]. Group l < 4 of sub-block sb: index qs[4sb + l] | bits
+        // 2l, 2l+1 of qh[sb] as bits 8-9; scale nibble (low for l < 2) of
+        // scales[sb]; y = ((d * (0.5 + s)) * 0.25) * grid * sign, sign bit e
+        // of signs[4sb + l].
+        const float d = f16_bits_to_f32(u16(blk));
+        const uint32_t qh = u8(blk + 66 + sb), sc = u8(blk + 74 + sb);
+        const float db0 = d * (0.5f + (float)(sc & 15u)) * 0.25f;
+        const float db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+        const uint32_t qs = u32a2(blk + 2 + 4 * sb), sg = u32a2(blk + 34 + 4 * sb);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t idx = ((qs >> (8 * l)) & 255u) | ((qh << (8 - 2 * l)) & 0x300u);
+            const uint64_t g = tb.v[idx];
+            const uint32_t s = sg >> (8 * l);
+            const float dl = l < 2 ? db0 : db1;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                y[8 * l + e] = dl * (float)(uint32_t)((g >> (8 * e)) & 255u) * (((s >> e) & 1u) ? -1.0f : 1.0f);
+        }
+    } else if constexpr (DT == kDtIQ3_S) {
+        // quant.cpp:421-482: d, qs[64], qh[8], signs[32], scales[4]. Group
+        // l < 4 of sub-block sb: indices qs[8sb + 2l], qs[8sb + 2l + 1] with
+        // bit 8 from bits 2l and 2l+1 of qh[sb]; scale nibble of
+        // scales[sb/2] (low for even sb); y = (d * (1 + 2s)) * grid * sign,
+        // sign bit e of signs[4sb + l].
+        const float d = f16_bits_to_f32(u16(blk));
+        const uint32_t qh = u8(blk + 66 + sb);
+        const uint32_t scb = u8(blk + 106 + (sb >> 1));
+        const float db = d * (1.0f + 2.0f * (float)((sb & 1) ? scb >> 4 : scb & 15u));
+        const uint32_t sg = u32a2(blk + 74 + 4 * sb);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t qq = u16(blk + 2 + 8 * sb + 2 * l);
+            const uint32_t i1 = (qq & 255u) | ((qh << (8 - 2 * l)) & 256u);
+            const uint32_t i2 = (qq >> 8) | ((qh << (7 - 2 * l)) & 256u);
+            const uint32_t g1 = tb.v[i1], g2 = tb.v[i2];
+            const uint32_t s = sg >> (8 * l);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t gv = ((e < 4 ? g1 : g2) >> (8 * (e & 3))) & 255u;
+                y[8 * l + e] = db * (float)gv * (((s >> e) & 1u) ? -1.0f : 1.0f);
+            }
+        }
+    } else if constexpr (DT == kDtIQ4_XS) {
+        // quant.cpp:485-502: d, scales_h (u16), scales_l[4], qs[128].
+        // Sub-block sb: 6-bit scale = nibble sb%2 of scales_l[sb/2] | bits
+        // 2sb, 2sb+1 of scales_h << 4; weight i < 16 is the low nibble of
+        // qs[16sb + i], weight 16 + i its high nibble;
+        // y = (d * (ls - 32)) * level[code].
+        const float d = f16_bits_to_f32(u16(blk));
+        const uint32_t sh = u16(blk + 2);
+        const int ls = (int)(((u8(blk + 4 + (sb >> 1)) >> (4 * (sb & 1))) & 15u) | (((sh >> (2 * sb)) & 3u) << 4));
+        const float dl = d * (float)(ls - 32);
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = u32a2(blk + 8 + 16 * sb + 4 * i);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t b = (w[i >> 2] >> (8 * (i & 3))) & 255u;
+            y[i] = dl * (float)(int32_t)tb.v[b & 15u];
+            y[16 + i] = dl * (float)(int32_t)tb.v[b >> 4];
+        }
+    }
+}
+
+// Sub-blocks per block and the sub-block's block address.
+template <int DT>
+__device__ __forceinline__ const uint8_t* sub_block(const uint8_t* row, long long sbi, int& sb) {
+    constexpr int kSub = Fmt<DT>::kElems / 32;
+    sb = (int)(sbi % kSub);
+    return row + (size_t)(sbi / kSub) * Fmt<DT>::kBytes;
+}
+
+// One thread per 32-weight sub-block, grid-stride; y written as 8 float4.
+template <int DT>
+__global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t* __restrict__ src, float* __restrict__ dst,
+                                                      long long n_sub) {
+    __shared__ Tables<DT> tb;
+    tb.load(threadIdx.x, 256);
+    __syncthreads();
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n_sub; i += (long long)gridDim.x * 256) {
+        int sb;
+        const uint8_t* blk = sub_block<DT>(src, i, sb);
+        float y[32];
+        decode32<DT>(blk, sb, tb, y);
+        float4* out = reinterpret_cast<float4*>(dst + i * 32);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) out[k] = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+    }
+}
+
+// Scalar types with any element count: one thread per element.
+template <int DT>
+__global__ __launch_bounds__(256) void k_dequant_scalar(const uint8_t* __restrict__ src, float* __restrict__ dst,
+                                                        long long n) {
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+        if constexpr (DT == kDtF32) dst[i] = reinterpret_cast<const float*>(src)[i];
+        else if constexpr (DT == kDtF16) dst[i] = f16_bits_to_f32(u16(src + 2 * i));
+        else dst[i] = __uint_as_float(u16(src + 2 * i) << 16);
+    }
+}
+
+// Y[t][j] = sum_i W[row0 + j][i] * X[t][i] over raw GGUF rows: one
+// wavefront per row (grid-stride over rows), lanes over the row's 32-weight
+// sub-blocks, NT tokens per launch column (blockIdx.y), fp32 FMA
+// accumulation and a butterfly reduction.
+template <int DT, int NT>
+__global__ __launch_bounds__(256) void k_matmul_rows(const uint8_t* __restrict__ w, size_t row_bytes,
+                                                     unsigned long long row0, int in_dim, int out_dim,
+                                                     const float* __restrict__ X, int n_tok,
+                                                     float* __restrict__ Y) {
+    __shared__ Tables<DT> tb;
+    tb.load(threadIdx.x, 256);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.y * NT;
+    const int nt = n_tok - t0 < NT ? n_tok - t0 : NT;
+    const int n_sub = in_dim / 32;
+    for (int j = blockIdx.x * 4 + wave; j < out_dim; j += gridDim.x * 4) {
+        const uint8_t* row = w + (size_t)(row0 + (unsigned long long)j) * row_bytes;
+        float acc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+        for (int s = lane; s < n_sub; s += 64) {
+            int sb;
+            const uint8_t* blk = sub_block<DT>(row, s, sb);
+            float y[32];
+            decode32<DT>(blk, sb, tb, y);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (t < nt) {
+                    const float4* xv = reinterpret_cast<const float4*>(X + (size_t)(t0 + t) * in_dim + 32 * s);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const float4 v = xv[k];
+                        acc[t] = fmaf(y[4 * k], v.x, acc[t]);
+                        acc[t] = fmaf(y[4 * k + 1], v.y, acc[t]);
+                        acc[t] = fmaf(y[4 * k + 2], v.z, acc[t]);
+                        acc[t] = fmaf(y[4 * k + 3], v.w, acc[t]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) acc[t] += __shfl_xor(acc[t], off);
+            if (lane == 0 && t < nt) Y[(size_t)(t0 + t) * out_dim + j] = acc[t];
+        }
+    }
+}
+
+template <int DT>
+hipError_t dequant_dt(const uint8_t* src, float* dst, unsigned long long n, hipStream_t s) {
+    if constexpr (DT == kDtF32 || DT == kDtF16 || DT == kDtBF16) {
+        unsigned long long grid = (n + 255) / 256;
+        if (grid > 8192) grid = 8192;
+        hipLaunchKernelGGL(k_dequant_scalar<DT>, dim3((unsigned)grid), dim3(256), 0, s, src, dst, (long long)n);
+    } else {
+        const unsigned long long n_sub = n / 32;
+        unsigned long long grid = (n_sub + 255) / 256;
+        if (grid > 8192) grid = 8192;
+        hipLaunchKernelGGL(k_dequant_rows<DT>, dim3((unsigned)grid), dim3(256), 0, s, src, dst, (long long)n_sub);
+    }
+    return hipGetLastError();
+}
+
+template <int DT, int NT>
+hipError_t matmul_dt_nt(const uint8_t* w, size_t rb, unsigned long long row0, int in_dim, int out_dim, const float* X,
+                        int n_tok, float* Y, hipStream_t s) {
+    int grid = (out_dim + 3) / 4;
+    if (grid > 2048) grid = 2048;
+    // at most 32768 token columns per launch (grid.y stays far below its limit)
+    constexpr int kMaxTok = 32768 * NT;
+    for (int t = 0; t < n_tok; t += kMaxTok) {
+        const int nt = n_tok - t < kMaxTok ? n_tok - t : kMaxTok;
+        hipLaunchKernelGGL((k_matmul_rows<DT, NT>), dim3(grid, (nt + NT - 1) / NT), dim3(256), 0, s, w, rb, row0,
+                           in_dim, out_dim, X + (size_t)t * in_dim, nt, Y + (size_t)t * out_dim);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+template <int DT>
+hipError_t matmul_dt(const uint8_t* w, size_t rb, unsigned long long row0, int in_dim, int out_dim, const float* X,
+                     int n_tok, float* Y, hipStream_t s) {
+    if (n_tok == 1) return matmul_dt_nt<DT, 1>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
+    if (n_tok == 2) return matmul_dt_nt<DT, 2>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
+    if (n_tok <= 4) return matmul_dt_nt<DT, 4>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
+    return matmul_dt_nt<DT, 8>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
+}
+
+}  // namespace
+
+int rows_block_elems(int dtype) {
+    switch (dtype) {
+        case kDtF32: case kDtF16: case kDtBF16: return 1;
+        case kDtQ8_0: return 32;
+        case kDtQ2_K: case kDtQ3_K: case kDtQ6_K: case kDtIQ3_XXS: case kDtIQ3_S: case kDtIQ2_S: case kDtIQ4_XS:
+            return 256;
+        default: return 0;
+    }
+}
+
+size_t rows_block_bytes(int dtype) {
+    switch (dtype) {
+        case kDtF32: return 4;
+        case kDtF16: case kDtBF16: return 2;
+        case kDtQ8_0: return Fmt<kDtQ8_0>::kBytes;
+        case kDtQ2_K: return Fmt<kDtQ2_K>::kBytes;
+        case kDtQ3_K: return Fmt<kDtQ3_K>::kBytes;
+        case kDtQ6_K: return Fmt<kDtQ6_K>::kBytes;
+        case kDtIQ3_XXS: return Fmt<kDtIQ3_XXS>::kBytes;
+        case kDtIQ3_S: return Fmt<kDtIQ3_S>::kBytes;
+        case kDtIQ2_S: return Fmt<kDtIQ2_S>::kBytes;
+        case kDtIQ4_XS: return Fmt<kDtIQ4_XS>::kBytes;
+        default: return 0;
+    }
+}
+
+hipError_t launch_dequant_rows(int dtype, const uint8_t* src, float* dst, unsigned long long n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    switch (dtype) {
+        case kDtF32: return dequant_dt<kDtF32>(src, dst, n, s);
+        case kDtF16: return dequant_dt<kDtF16>(src, dst, n, s);
+        case kDtBF16: return dequant_dt<kDtBF16>(src, dst, n, s);
+        case kDtQ8_0: return dequant_dt<kDtQ8_0>(src, dst, n, s);
+        case kDtQ2_K: return dequant_dt<kDtQ2_K>(src, dst, n, s);
+        case kDtQ3_K: return dequant_dt<kDtQ3_K>(src, dst, n, s);
+        case kDtQ6_K: return dequant_dt<kDtQ6_K>(src, dst, n, s);
+        case kDtIQ3_XXS: return dequant_dt<kDtIQ3_XXS>(src, dst, n, s);
+        case kDtIQ3_S: return dequant_dt<kDtIQ3_S>(src, dst, n, s);
+        case kDtIQ2_S: return dequant_dt<kDtIQ2_S>(src, dst, n, s);
+        case kDtIQ4_XS: return dequant_dt<kDtIQ4_XS>(src, dst, n, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_matmul_rows(int dtype, const uint8_t* w, size_t row_bytes, unsigned long long row0, int in_dim,
+                              int out_dim, const float* X, int n_tok, float* Y, hipStream_t s) {
+    if (n_tok <= 0 || out_dim <= 0) return hipSuccess;
+    switch (dtype) {
+        case kDtF32: return matmul_dt<kDtF32>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtF16: return matmul_dt<kDtF16>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtBF16: return matmul_dt<kDtBF16>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtQ8_0: return matmul_dt<kDtQ8_0>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtQ2_K: return matmul_dt<kDtQ2_K>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtQ3_K: return matmul_dt<kDtQ3_K>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtQ6_K: return matmul_dt<kDtQ6_K>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtIQ3_XXS: return matmul_dt<kDtIQ3_XXS>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtIQ3_S: return matmul_dt<kDtIQ3_S>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtIQ2_S: return matmul_dt<kDtIQ2_S>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        case kDtIQ4_XS: return matmul_dt<kDtIQ4_XS>(w, row_bytes, row0, in_dim, out_dim, X, n_tok, Y, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// Expanded codebook entries (host copies of the tables the kernels use).
+uint64_t rows_iq2s_grid(int i) { return kIq2sGrid.v[i & 1023]; }
+uint32_t rows_iq3s_grid(int i) { return kIq3sGrid.v[i & 511]; }
+
+}  // namespace gpeed

@@ -34,6 +34,28 @@ void cuda_add(const float* a, const float* b, float* dst, int n) { check(gpeed_a
 
 namespace gpu {
 
+void dequantize(DType t, const void* src, float* dst, uint64_t n) {
+    const int bs = gpeed_dtype_block_size((int)t);
+    if (bs == 0) throw std::runtime_error(std::string("dequantize: unimplemented type ") + dtype_name(t));
+    if (n % (uint64_t)bs) throw std::runtime_error("dequantize: element count not a multiple of block size");
+    if (n == 0) return;
+    check(gpeed_init(), "gpeed_init");
+    const size_t in_bytes = gpeed_dtype_row_bytes((int)t, n), out_bytes = (size_t)n * sizeof(float);
+    void* s = nullptr;
+    void* d = nullptr;
+    int rc = gpeed_malloc(&s, in_bytes);
+    if (rc == GPEED_OK) rc = gpeed_malloc(&d, out_bytes);
+    if (rc == GPEED_OK) rc = gpeed_memcpy(s, src, in_bytes, kH2D);
+    if (rc == GPEED_OK) rc = gpeed_dequantize((int)t, s, static_cast<float*>(d), n, nullptr);
+    if (rc == GPEED_OK) rc = gpeed_stream_sync(nullptr);
+    if (rc == GPEED_OK) rc = gpeed_memcpy(dst, d, out_bytes, kD2H);
+    (void)gpeed_free(s);
+    (void)gpeed_free(d);
+    check(rc, "dequantize");
+}
+
+void dequantize_row(DType t, const void* src, float* dst, uint64_t n) { dequantize(t, src, dst, n); }
+
 WeightStore::WeightStore() { check(gpeed_init(), "gpeed_init"); }
 
 WeightStore::WeightStore(const GgufModel& model) : WeightStore() { model_ = &model; }
@@ -42,9 +64,10 @@ void WeightStore::pin(const std::string& name) {
     if (!model_) throw std::runtime_error("weights: no GGUF model attached for " + name);
     const TensorInfo* t = model_->find_tensor(name);
     if (!t) throw std::runtime_error("weights: missing tensor " + name);
-    if (t->type != DType::IQ3_XXS)
-        throw std::runtime_error(std::string("weights: ") + dtype_name(t->type) + " is not on the GPU path for " + name);
-    if (t->dims.empty() || t->dims[0] > (uint64_t)INT32_MAX || t->dims[0] % 256)
+    const int bs = gpeed_dtype_block_size((int)t->type);
+    if (bs == 0)
+        throw std::runtime_error(std::string("weights: ") + dtype_name(t->type) + " is not decoded for " + name);
+    if (t->dims.empty() || t->dims[0] > (uint64_t)INT32_MAX || t->dims[0] % (uint64_t)bs || t->dims[0] % 32)
         throw std::runtime_error("weights: row not block aligned for " + name);
     // straight from the file mapping when there is one, else through a host copy
     const GgufFile& f = model_->file((size_t)t->shard);
@@ -55,7 +78,7 @@ void WeightStore::pin(const std::string& name) {
         model_->read_tensor(*t, tmp.data());
         src = tmp.data();
     }
-    add(name, src, t->n_rows(), (int)t->dims[0]);
+    add(name, src, t->n_rows(), (int)t->dims[0], t->type);
 }
 
 size_t WeightStore::pin_matching(bool experts) {
@@ -64,7 +87,11 @@ size_t WeightStore::pin_matching(bool experts) {
         const bool is_expert = name.find("exps.weight") != std::string::npos;  // weights.cpp:72-73
         if (is_expert != experts || has(name)) continue;
         const TensorInfo* t = model_->find_tensor(name);
-        if (!t || t->type != DType::IQ3_XXS || t->dims.empty() || t->dims[0] % 256) continue;
+        // as weights.cpp:74-76: F32 tensors and payloads under 4 KiB stay on
+        // the host; so do types the kernels do not decode
+        if (!t || t->type == DType::F32 || t->n_bytes() < 4096) continue;
+        const int bs = gpeed_dtype_block_size((int)t->type);
+        if (bs == 0 || t->dims.empty() || t->dims[0] % (uint64_t)bs || t->dims[0] % 32) continue;
         pin(name);
     }
     return resident_bytes_;
@@ -78,10 +105,14 @@ void WeightStore::read_resident(const std::string& name, void* dst) const {
     auto it = tensors_.find(name);
     if (it == tensors_.end()) throw std::runtime_error("weights: missing tensor " + name);
     const Tensor& t = it->second;
-    const size_t raw_bytes = gpeed_iq3xxs_row_bytes(t.in_dim) * t.n_rows;
+    const size_t raw_bytes = gpeed_dtype_row_bytes(t.dtype, (uint64_t)t.in_dim) * t.n_rows;
+    if (t.dtype != GPEED_DTYPE_IQ3_XXS) {  // kept as its GGUF rows
+        check(gpeed_memcpy(dst, t.data, raw_bytes, kD2H), "weights: read back");
+        return;
+    }
     void* raw = nullptr;
     check(gpeed_malloc(&raw, raw_bytes), "malloc");
-    int rc = gpeed_iq3xxs_untile(t.t64, t.n_rows, t.in_dim, raw, nullptr);
+    int rc = gpeed_iq3xxs_untile(t.data, t.n_rows, t.in_dim, raw, nullptr);
     if (rc == GPEED_OK) rc = gpeed_stream_sync(nullptr);
     if (rc == GPEED_OK) rc = gpeed_memcpy(dst, raw, raw_bytes, kD2H);
     (void)gpeed_free(raw);
@@ -89,7 +120,7 @@ void WeightStore::read_resident(const std::string& name, void* dst) const {
 }
 
 WeightStore::~WeightStore() {
-    for (auto& kv : tensors_) (void)gpeed_free(kv.second.t64);
+    for (auto& kv : tensors_) (void)gpeed_free(kv.second.data);
     for (auto& kv : ws_) (void)gpeed_free(kv.second.p);
     for (Buffer* b : {&x_, &y_, &route_ws_, &moe_ws_, &logits_, &bias_, &eptr_, &tok_, &wt_})
         (void)gpeed_free(b->p);
@@ -117,28 +148,42 @@ void WeightStore::check_ws(void* ws, const std::string& what) {
 }
 
 void WeightStore::add(const std::string& name, const void* gguf_rows, uint64_t n_rows, int in_dim) {
-    const size_t rb = gpeed_iq3xxs_row_bytes(in_dim);
-    if (rb == 0) throw std::runtime_error("weights: row not block aligned for " + name);
+    add(name, gguf_rows, n_rows, in_dim, DType::IQ3_XXS);
+}
+
+void WeightStore::add(const std::string& name, const void* gguf_rows, uint64_t n_rows, int in_dim, DType type) {
+    const int bs = gpeed_dtype_block_size((int)type);
+    if (bs == 0) throw std::runtime_error(std::string("weights: ") + dtype_name(type) + " is not decoded for " + name);
+    const size_t rb = gpeed_dtype_row_bytes((int)type, in_dim > 0 ? (uint64_t)in_dim : 0);
+    if (rb == 0 || in_dim % 32) throw std::runtime_error("weights: row not block aligned for " + name);
     const size_t raw_bytes = rb * n_rows;
-    void* raw = nullptr;
-    check(gpeed_malloc(&raw, raw_bytes), "malloc");
     Tensor t;
     t.n_rows = n_rows;
     t.in_dim = in_dim;
-    t.bytes = gpeed_iq3xxs_t64_bytes(n_rows, in_dim);
-    int rc = gpeed_memcpy(raw, gguf_rows, raw_bytes, kH2D);
-    if (rc == GPEED_OK) rc = gpeed_malloc(&t.t64, t.bytes);
-    if (rc == GPEED_OK) rc = gpeed_iq3xxs_tile(raw, n_rows, in_dim, t.t64, nullptr);
-    if (rc == GPEED_OK) rc = gpeed_stream_sync(nullptr);
-    (void)gpeed_free(raw);
+    t.dtype = (int)type;
+    int rc = GPEED_OK;
+    if (type == DType::IQ3_XXS) {  // kept in the T64 layout
+        void* raw = nullptr;
+        check(gpeed_malloc(&raw, raw_bytes), "malloc");
+        t.bytes = gpeed_iq3xxs_t64_bytes(n_rows, in_dim);
+        rc = gpeed_memcpy(raw, gguf_rows, raw_bytes, kH2D);
+        if (rc == GPEED_OK) rc = gpeed_malloc(&t.data, t.bytes);
+        if (rc == GPEED_OK) rc = gpeed_iq3xxs_tile(raw, n_rows, in_dim, t.data, nullptr);
+        if (rc == GPEED_OK) rc = gpeed_stream_sync(nullptr);
+        (void)gpeed_free(raw);
+    } else {  // kept as its GGUF rows
+        t.bytes = raw_bytes;
+        rc = gpeed_malloc(&t.data, t.bytes);
+        if (rc == GPEED_OK) rc = gpeed_memcpy(t.data, gguf_rows, raw_bytes, kH2D);
+    }
     if (rc != GPEED_OK) {
-        (void)gpeed_free(t.t64);
+        (void)gpeed_free(t.data);
         check(rc, "weights: upload");
     }
     auto it = tensors_.find(name);
     if (it != tensors_.end()) {
         resident_bytes_ -= it->second.bytes;
-        (void)gpeed_free(it->second.t64);
+        (void)gpeed_free(it->second.data);
     }
     tensors_[name] = t;
     resident_bytes_ += t.bytes;
@@ -146,19 +191,36 @@ void WeightStore::add(const std::string& name, const void* gguf_rows, uint64_t n
 
 const WeightStore::Tensor& WeightStore::get(const std::string& name, int in_dim) {
     auto it = tensors_.find(name);
-    if (it == tensors_.end() && model_ && model_->find_tensor(name) && in_dim % 256 == 0) {
+    if (it == tensors_.end() && model_) {
+        const TensorInfo* ti = model_->find_tensor(name);
+        if (!ti) throw std::runtime_error("weights: missing tensor " + name);
+        const int bs = gpeed_dtype_block_size((int)ti->type);
+        if (bs == 0)
+            throw std::runtime_error(std::string("weights: ") + dtype_name(ti->type) + " is not decoded for " + name);
+        if (in_dim % bs != 0) throw std::runtime_error("weights: row not block aligned for " + name);
         pin(name);  // first use of a tensor of the attached model
         it = tensors_.find(name);
     }
     if (it == tensors_.end()) throw std::runtime_error("weights: missing tensor " + name);
-    if (in_dim % 256 != 0) throw std::runtime_error("weights: row not block aligned for " + name);
+    if (in_dim % gpeed_dtype_block_size(it->second.dtype) != 0)
+        throw std::runtime_error("weights: row not block aligned for " + name);
     return it->second;
+}
+
+const WeightStore::Tensor& WeightStore::get_iq3(const std::string& name, int in_dim) {
+    const Tensor& t = get(name, in_dim);
+    if (t.dtype != GPEED_DTYPE_IQ3_XXS) throw std::runtime_error("weights: " + name + " is not IQ3_XXS");
+    return t;
 }
 
 void WeightStore::matvec_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* x,
                                float* dst) {
     if (out_dim <= 0) return;  // weights.cpp:88
     const Tensor& t = get(name, in_dim);
+    if (t.dtype != GPEED_DTYPE_IQ3_XXS) {
+        rows_product(t, name, row0, in_dim, out_dim, x, 1, dst);
+        return;
+    }
     const size_t xb = (size_t)in_dim * sizeof(float), yb = (size_t)out_dim * sizeof(float);
     void* xd = scratch(x_, xb, false);
     void* yd = scratch(y_, yb, false);
@@ -167,7 +229,7 @@ void WeightStore::matvec_quant(const std::string& name, uint64_t row0, int in_di
     Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
     void* ws = scratch(wbuf, wsb, true);
     check(gpeed_memcpy(xd, x, xb, kH2D), "weights: upload x");
-    check(gpeed_iq3xxs_matvec(t.t64, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd),
+    check(gpeed_iq3xxs_matvec(t.data, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd),
                               static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
           ("weights: matvec_quant " + name).c_str());
     check_ws(ws, "weights: matvec_quant " + name);
@@ -178,6 +240,10 @@ void WeightStore::matmul_quant(const std::string& name, uint64_t row0, int in_di
                                int n_tok, float* Y) {
     if (n_tok <= 0 || out_dim <= 0) return;  // weights.cpp:88
     const Tensor& t = get(name, in_dim);
+    if (t.dtype != GPEED_DTYPE_IQ3_XXS) {
+        rows_product(t, name, row0, in_dim, out_dim, X, n_tok, Y);
+        return;
+    }
     const size_t xb = (size_t)n_tok * in_dim * sizeof(float), yb = (size_t)n_tok * out_dim * sizeof(float);
     void* xd = scratch(x_, xb, false);
     void* yd = scratch(y_, yb, false);
@@ -186,17 +252,29 @@ void WeightStore::matmul_quant(const std::string& name, uint64_t row0, int in_di
     Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
     void* ws = scratch(wbuf, wsb, true);
     check(gpeed_memcpy(xd, X, xb, kH2D), "weights: upload x");
-    check(gpeed_iq3xxs_matmul(t.t64, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd), n_tok,
+    check(gpeed_iq3xxs_matmul(t.data, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd), n_tok,
                               static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
           ("weights: matmul_quant " + name).c_str());
     check_ws(ws, "weights: matmul_quant " + name);
     check(gpeed_memcpy(Y, yd, yb, kD2H), "weights: download y");
 }
 
+void WeightStore::rows_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,
+                               const float* X, int n_tok, float* Y) {
+    const size_t xb = (size_t)n_tok * in_dim * sizeof(float), yb = (size_t)n_tok * out_dim * sizeof(float);
+    void* xd = scratch(x_, xb, false);
+    void* yd = scratch(y_, yb, false);
+    check(gpeed_memcpy(xd, X, xb, kH2D), "weights: upload x");
+    check(gpeed_matmul_rows(t.dtype, t.data, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd), n_tok,
+                            static_cast<float*>(yd), nullptr),
+          ("weights: product over " + name).c_str());
+    check(gpeed_memcpy(Y, yd, yb, kD2H), "weights: download y");
+}
+
 void WeightStore::matvec_heads(const std::string& name, uint64_t row0, int in_dim, int rows_per_head, int n_heads,
                                const float* x, float* dst) {
     if (n_heads <= 0 || rows_per_head <= 0) return;
-    const Tensor& t = get(name, in_dim);
+    const Tensor& t = get_iq3(name, in_dim);
     const int out_dim = rows_per_head * n_heads;
     const size_t xb = (size_t)n_heads * in_dim * sizeof(float), yb = (size_t)out_dim * sizeof(float);
     void* xd = scratch(x_, xb, false);
@@ -206,7 +284,7 @@ void WeightStore::matvec_heads(const std::string& name, uint64_t row0, int in_di
     Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
     void* ws = scratch(wbuf, std::max(wsb, gpeed_iq3xxs_matvec_ws_bytes(in_dim, out_dim)), true);
     check(gpeed_memcpy(xd, x, xb, kH2D), "weights: upload x");
-    check(gpeed_iq3xxs_matvec_heads(t.t64, t.n_rows, row0, in_dim, rows_per_head, n_heads,
+    check(gpeed_iq3xxs_matvec_heads(t.data, t.n_rows, row0, in_dim, rows_per_head, n_heads,
                                     static_cast<const float*>(xd), static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
           ("weights: matvec_heads " + name).c_str());
     check_ws(ws, "weights: matvec_heads " + name);
@@ -218,9 +296,9 @@ void WeightStore::moe_experts(const std::string& gate, const std::string& up, co
                               int mode, const float* bias, float routed_scale, bool norm_topk, float swiglu_limit,
                               float* Y) {
     if (n_tok <= 0) return;
-    const Tensor& tg = get(gate, hidden);
-    const Tensor& tu = get(up, hidden);
-    const Tensor& td = get(down, inter);
+    const Tensor& tg = get_iq3(gate, hidden);
+    const Tensor& tu = get_iq3(up, hidden);
+    const Tensor& td = get_iq3(down, inter);
     const size_t n_asg = (size_t)n_tok * top_k;
     void* lg = scratch(logits_, (size_t)n_tok * n_exp * sizeof(float), false);
     void* bd = bias ? scratch(bias_, (size_t)n_exp * sizeof(float), false) : nullptr;
@@ -242,7 +320,7 @@ void WeightStore::moe_experts(const std::string& gate, const std::string& up, co
                           routed_scale, norm_topk ? 1 : 0, static_cast<int*>(ep), static_cast<int*>(tk),
                           static_cast<float*>(wt), nullptr, rws, route_ws_.bytes, nullptr),
           "moe: route");
-    check(gpeed_iq3xxs_moe_experts(tg.t64, tu.t64, td.t64, n_exp, hidden, inter, static_cast<const float*>(xd),
+    check(gpeed_iq3xxs_moe_experts(tg.data, tu.data, td.data, n_exp, hidden, inter, static_cast<const float*>(xd),
                                    n_tok, top_k, static_cast<const int*>(ep), static_cast<const int*>(tk),
                                    static_cast<const float*>(wt), swiglu_limit, static_cast<float*>(yd), mws,
                                    moe_ws_.bytes, nullptr),

@@ -34,6 +34,15 @@ void cuda_add(const float* a, const float* b, float* dst, int n);
 
 namespace gpu {
 
+// dequantize / dequantize_row (quant.h:18-22) over host arrays, computed on
+// the device: n weights of type t at src into dst, bit-exact with the
+// reference, for F32, F16, BF16, Q8_0, Q2_K, Q3_K, Q6_K, IQ3_XXS, IQ3_S,
+// IQ2_S and IQ4_XS. Throws the reference's messages ("dequantize:
+// unimplemented type <name>", "dequantize: element count not a multiple of
+// block size").
+void dequantize(DType t, const void* src, float* dst, uint64_t n);
+void dequantize_row(DType t, const void* src, float* dst, uint64_t n);
+
 class WeightStore {
 public:
     WeightStore();
@@ -51,27 +60,31 @@ public:
     // keeps their T64 copy in HBM (the role of pin_nonexpert,
     // weights.cpp:70-84). Replaces a tensor of the same name.
     void add(const std::string& name, const void* gguf_rows, uint64_t n_rows, int in_dim);
+    // The same for a tensor of another decoded type, kept in HBM as its GGUF
+    // rows (in_dim a multiple of the block size and of 32).
+    void add(const std::string& name, const void* gguf_rows, uint64_t n_rows, int in_dim, DType type);
     bool has(const std::string& name) const { return tensors_.count(name) != 0; }
     size_t resident_bytes() const { return resident_bytes_; }
 
-    // pin_nonexpert (weights.cpp:70-84) on the device: every IQ3_XXS tensor of
-    // the attached model except the routed experts (names containing
-    // "exps.weight"), uploaded once and kept in HBM in the T64 layout.
-    // Tensors of other types stay with the caller's CPU path. Returns the
-    // bytes held in HBM.
+    // pin_nonexpert (weights.cpp:70-84) on the device: every tensor of the
+    // attached model except the routed experts (names containing
+    // "exps.weight"), F32 tensors and payloads under 4 KiB, as the
+    // reference, uploaded once and kept in HBM (IQ3_XXS in the T64 layout,
+    // the other decoded types as GGUF rows). Returns the bytes held in HBM.
     size_t pin_nonexpert();
     // The routed-expert tensors as well (the reference keeps them on disk; the
     // whole model fits in 288 GB of HBM). Returns the bytes held in HBM.
     size_t pin_experts();
-    // Uploads one IQ3_XXS tensor of the attached model (rows = n_elements /
-    // dims[0], so a 3-D expert tensor is [n_exp * rows_per_expert, in_dim]).
+    // Uploads one tensor of a decoded type of the attached model (rows =
+    // n_elements / dims[0], so a 3-D expert tensor is
+    // [n_exp * rows_per_expert, in_dim]).
     void pin(const std::string& name);
     // The GGUF bytes of a resident tensor, read back from its HBM copy
     // (n_rows * row_bytes into host memory at dst).
     void read_resident(const std::string& name, void* dst) const;
 
     // dst[j] = sum_i W[row0+j][i] * x[i], j < out_dim (weights.cpp:167-203):
-    // one GEMV launch.
+    // one GEMV launch (IQ3_XXS), or the raw-row product for another type.
     void matvec_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* x,
                       float* dst);
     // Y[t][j] = sum_i W[row0+j][i] * X[t][i], t < n_tok (weights.cpp:86-165):
@@ -98,9 +111,10 @@ public:
 
 private:
     struct Tensor {
-        void* t64 = nullptr;
+        void* data = nullptr;  // T64 copy (IQ3_XXS) or GGUF rows
         uint64_t n_rows = 0;
         int in_dim = 0;
+        int dtype = 18;
         size_t bytes = 0;
     };
     struct Buffer {
@@ -108,6 +122,9 @@ private:
         size_t bytes = 0;
     };
     const Tensor& get(const std::string& name, int in_dim);
+    const Tensor& get_iq3(const std::string& name, int in_dim);
+    void rows_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,
+                      const float* X, int n_tok, float* Y);
     void* scratch(Buffer& b, size_t bytes, bool init);
     // throws if a kernel flagged the workspace (waits for the stream)
     static void check_ws(void* ws, const std::string& what);

@@ -73,3 +73,49 @@ def iq3xxs_matrix(seed: int, stream: int, n_rows: int, in_dim: int, d_scale: flo
 
 def row_bytes(in_dim: int) -> int:
     return in_dim // QK * BLOCK_BYTES
+
+
+# GGUF block formats other than IQ3_XXS (quant.cpp:83-114, 165-502): ggml
+# type id -> (weights per block, bytes per block, byte offsets of the fp16
+# scale fields)
+FORMATS = {
+    8: (32, 34, (0,)),          # Q8_0: d
+    10: (256, 84, (80, 82)),    # Q2_K: d, dmin
+    11: (256, 110, (108,)),     # Q3_K: d
+    14: (256, 210, (208,)),     # Q6_K: d
+    18: (256, 98, (0,)),        # IQ3_XXS: d
+    21: (256, 110, (0,)),       # IQ3_S: d
+    22: (256, 82, (0,)),        # IQ2_S: d
+    23: (256, 136, (0,)),       # IQ4_XS: d
+}
+SCALAR_FORMATS = {0: np.float32, 1: np.float16, 30: "bf16"}
+
+
+def quant_blocks(seed: int, stream: int, dtype: int, n_blocks: int, d_scale: float = 0.02) -> np.ndarray:
+    """``n_blocks`` blocks of a GGUF block format: uniform random bytes with
+    every fp16 scale field set to |N(0,1)| * d_scale. uint8 [n_blocks, bytes]."""
+    _, nbytes, d_offs = FORMATS[dtype]
+    words = u64(seed, stream * 4 + 0, (n_blocks * nbytes + 7) // 8)
+    out = words.view(np.uint8)[: n_blocks * nbytes].reshape(n_blocks, nbytes).copy()
+    for k, off in enumerate(d_offs):
+        d = (np.abs(normal(seed, stream * 4 + 1 + k, n_blocks, np.float64)) * d_scale).astype(np.float16)
+        out[:, off:off + 2] = d.view(np.uint8).reshape(n_blocks, 2)
+    return out
+
+
+def quant_matrix(seed: int, stream: int, dtype: int, n_rows: int, in_dim: int, d_scale: float = 0.02) -> np.ndarray:
+    """GGUF row-major payload of an [n_rows, in_dim] weight of any decoded type:
+    uint8 [n_rows, row_bytes]. Scalar types hold N(0,1) * d_scale * 16."""
+    if dtype in SCALAR_FORMATS:
+        v = normal(seed, stream, n_rows * in_dim, np.float64) * d_scale * 16
+        if dtype == 30:
+            bits = np.asarray(v, np.float32).view(np.uint32)
+            raw = ((bits + np.uint32(0x7FFF) + ((bits >> 16) & np.uint32(1))) >> 16).astype(np.uint16)
+        else:
+            raw = v.astype(SCALAR_FORMATS[dtype])
+        return raw.view(np.uint8).reshape(n_rows, -1)
+    elems, nbytes, _ = FORMATS[dtype]
+    if in_dim % elems:
+        raise ValueError(f"in_dim must be a multiple of {elems}")
+    nb = in_dim // elems
+    return quant_blocks(seed, stream, dtype, n_rows * nb, d_scale).reshape(n_rows, nb * nbytes)

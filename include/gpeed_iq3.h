@@ -42,6 +42,17 @@ typedef void* gpeed_stream_t;
 #define GPEED_WS_BUCKETS 4u           /* expert buckets (eptr / tok) break the router's invariants */
 
 #define GPEED_DTYPE_IQ3_XXS 18        /* common.h:27 */
+/* the other types a UD-IQ3_XXS file holds (common.h:10-43) */
+#define GPEED_DTYPE_F32 0
+#define GPEED_DTYPE_F16 1
+#define GPEED_DTYPE_Q8_0 8
+#define GPEED_DTYPE_Q2_K 10
+#define GPEED_DTYPE_Q3_K 11
+#define GPEED_DTYPE_Q6_K 14
+#define GPEED_DTYPE_IQ3_S 21
+#define GPEED_DTYPE_IQ2_S 22
+#define GPEED_DTYPE_IQ4_XS 23
+#define GPEED_DTYPE_BF16 30
 
 #define GPEED_X_F32 0                 /* activation element types of gpeed_iq3xxs_gemm */
 #define GPEED_X_BF16 1
@@ -123,10 +134,36 @@ size_t gpeed_iq3xxs_t64_bytes(uint64_t n_rows, int64_t in_dim);
 
 /* ---- dequantize (replaces quant.h:18-22, quant.cpp:565-573) ------------- */
 
-/* dequantize(DType, src, dst, n) for dtype == IQ3_XXS: dst[0..n) fp32 from the
- * GGUF bytes at src (device pointers; dst 16-byte aligned). Bit-exact with
- * the reference. Other dtypes return GPEED_ERR_UNIMPLEMENTED. */
+/* dequantize(DType, src, dst, n): dst[0..n) fp32 from the GGUF bytes at src
+ * (device pointers; src 2-byte aligned, 4 for F32; dst 16-byte aligned), for
+ * F32, F16, BF16, Q8_0, Q2_K, Q3_K, Q6_K, IQ3_XXS, IQ3_S, IQ2_S and IQ4_XS,
+ * the types the reference decodes (quant.cpp:507-563). Bit-exact with the
+ * reference (NaN payloads aside). Other dtypes return
+ * GPEED_ERR_UNIMPLEMENTED, n not a multiple of the block size
+ * GPEED_ERR_NOT_MULTIPLE (quant.cpp:523-524). */
 int gpeed_dequantize(int dtype, const void* src, float* dst, uint64_t n, gpeed_stream_t stream);
+/* dtype_block_size (quant.cpp:52-81) for the types above, else 0. */
+int gpeed_dtype_block_size(int dtype);
+/* dtype_row_bytes (quant.cpp:119-126) for the types above: 0 for another
+ * type or when n is not a multiple of the block size. */
+size_t gpeed_dtype_row_bytes(int dtype, uint64_t n);
+
+/* ---- products over raw GGUF rows of any decoded type -------------------- */
+
+/* matmul_quant / matvec_quant (weights.cpp:86-203) on a tensor kept in HBM
+ * as its GGUF rows (n_rows rows of gpeed_dtype_row_bytes(dtype, in_dim)
+ * bytes, device pointer, 2-byte aligned, 4 for F32): Y[t][j] = sum_i
+ * W[row0 + j][i] * X[t][i] for t < n_tok, j < out_dim, with the weights
+ * dequantized bit-exactly and fp32 accumulation. X [n_tok][in_dim] fp32
+ * (16-byte aligned), Y [n_tok][out_dim] fp32. in_dim must be a multiple of
+ * the block size and of 32. No workspace. The IQ3_XXS entry points above
+ * (T64 layout) are the fast path for IQ3_XXS; this one takes every type. */
+int gpeed_matmul_rows(int dtype, const void* w, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
+                      const float* X, int n_tok, float* Y, gpeed_stream_t stream);
+/* Host-only (no reference counterpart): the expanded codebook the kernels
+ * use for IQ2_S (1024 entries of 8 bytes), IQ3_S (512 of 4) or IQ3_XXS
+ * (256 of 4), one entry per uint64. */
+int gpeed_codebook(int dtype, uint64_t* out, size_t n);
 
 /* ---- weight residency (replaces weights.cpp:62-84 pin_nonexpert/payload) */
 

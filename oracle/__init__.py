@@ -50,6 +50,15 @@ def lib():
         L.orc_grid_entry.restype = C.c_uint32
         L.orc_iq3xxs_block.argtypes = [_u8p, _f32p]
         L.orc_dequantize.argtypes = [C.c_int, C.c_void_p, _f32p, C.c_uint64]
+        L.orc_matmul_rows.argtypes = [C.c_int, C.c_void_p, C.c_uint64, C.c_int, C.c_int, _f32p, C.c_int, _f32p,
+                                      _f32p]
+        L.orc_block_elems.argtypes = [C.c_int]
+        L.orc_block_bytes.argtypes = [C.c_int]
+        L.orc_iq2s_grid.argtypes = [C.c_uint32]
+        L.orc_iq2s_grid.restype = C.c_uint64
+        L.orc_iq3s_grid.argtypes = [C.c_uint32]
+        L.orc_iq3s_grid.restype = C.c_uint32
+        L.orc_iq4nl_value.argtypes = [C.c_int]
         L.orc_dot_f32.argtypes = [_f32p, _f32p, C.c_int]
         L.orc_dot_f32.restype = C.c_float
         L.orc_axpy_f32.argtypes = [_f32p, _f32p, C.c_float, C.c_int]
@@ -76,6 +85,34 @@ def dequantize(raw: np.ndarray, n: int, dtype: int = 18) -> np.ndarray:
     if rc != 0:
         raise RuntimeError(f"orc_dequantize rc={rc}")
     return out
+
+
+def matmul_rows(dtype: int, w: np.ndarray, row0: int, in_dim: int, out_dim: int, X: np.ndarray) -> np.ndarray:
+    """weights.cpp:86-203 over GGUF rows of any decoded type (Y[t][j], reference order)."""
+    X = np.ascontiguousarray(np.atleast_2d(X), np.float32)
+    Y = np.empty((X.shape[0], out_dim), np.float32)
+    buf = np.empty(in_dim, np.float32)
+    rc = lib().orc_matmul_rows(dtype, _ptr(np.ascontiguousarray(w)), row0, in_dim, out_dim, X, X.shape[0], Y, buf)
+    if rc != 0:
+        raise RuntimeError(f"orc_matmul_rows rc={rc}")
+    return Y
+
+
+def block_geometry(dtype: int):
+    """(weights per block, bytes per block) of a decoded type (quant.cpp:52-114), else (0, 0)."""
+    return lib().orc_block_elems(dtype), lib().orc_block_bytes(dtype)
+
+
+def iq2s_grid() -> np.ndarray:
+    return np.array([lib().orc_iq2s_grid(i) for i in range(1024)], np.uint64)
+
+
+def iq3s_grid() -> np.ndarray:
+    return np.array([lib().orc_iq3s_grid(i) for i in range(512)], np.uint64)
+
+
+def iq4nl_values() -> np.ndarray:
+    return np.array([lib().orc_iq4nl_value(i) for i in range(16)], np.int64)
 
 
 def dot_f32(a: np.ndarray, b: np.ndarray) -> float:
@@ -156,6 +193,8 @@ def ref(openmp: bool = False):
             L.ref_axpy_f32.argtypes = [_f32p, _f32p, C.c_float, C.c_int]
             L.ref_store_open.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_char_p, C.c_char_p]
             L.ref_store_open.restype = C.c_void_p
+            L.ref_store_open_typed.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_int, C.c_char_p, C.c_char_p]
+            L.ref_store_open_typed.restype = C.c_void_p
             L.ref_store_matvec.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_int, _f32p, _f32p]
             L.ref_store_matmul.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_int, _f32p, C.c_int, _f32p]
             L.ref_store_close.argtypes = [C.c_void_p]
@@ -195,16 +234,17 @@ def ref_gguf_read(path: str, name: str, nbytes: int) -> bytes:
 
 
 class RefStore:
-    """One IQ3_XXS tensor held by the reference's WeightStore (pinned in RAM)."""
+    """One tensor (IQ3_XXS unless dtype says otherwise) held by the reference's
+    WeightStore (pinned in RAM)."""
 
     def __init__(self, payload: np.ndarray, n_rows: int, in_dim: int, openmp: bool = False,
-                 name: str = "blk.0.ffn_down.weight"):
+                 name: str = "blk.0.ffn_down.weight", dtype: int = 18):
         self.L = ref(openmp)
         if self.L is None:
             raise RuntimeError("oracle/_ref is not built")
         self.payload = np.ascontiguousarray(payload)
         tmp = os.environ.get("TMPDIR", "/tmp")
-        self.h = self.L.ref_store_open(_ptr(self.payload), n_rows, in_dim, name.encode(), tmp.encode())
+        self.h = self.L.ref_store_open_typed(_ptr(self.payload), n_rows, in_dim, dtype, name.encode(), tmp.encode())
         if not self.h:
             raise RuntimeError(self.L.ref_last_error().decode())
 

@@ -94,7 +94,8 @@ void orc_iq3xxs_block(const uint8_t* blk, float* y) {
     }
 }
 
-/* quant.cpp:521-573 (dequantize_impl), restricted to the types on this path. */
+/* quant.cpp:521-573 (dequantize_impl): F32, F16, BF16 and every block format
+ * the reference decodes (quant.cpp:507-519). */
 int orc_dequantize(int dtype, const void* src, float* dst, uint64_t n) {
     const uint8_t* p = (const uint8_t*)src;
     switch (dtype) {
@@ -111,13 +112,17 @@ int orc_dequantize(int dtype, const void* src, float* dst, uint64_t n) {
                 memcpy(dst + i, &bits, 4);
             }
             return ORC_OK;
-        case ORC_DTYPE_IQ3_XXS:
-            if (n % ORC_QK_K) return ORC_ERR_NOT_MULTIPLE;
-            for (uint64_t b = 0; b < n / ORC_QK_K; ++b)
-                orc_iq3xxs_block(p + b * ORC_IQ3XXS_BLOCK_BYTES, dst + b * ORC_QK_K);
+        default: {
+            /* quant.cpp:546-563: one block function per type over n / block */
+            const int be = orc_block_elems(dtype), bb = orc_block_bytes(dtype);
+            if (be <= 1) return ORC_ERR_UNIMPLEMENTED;
+            if (n % (uint64_t)be) return ORC_ERR_NOT_MULTIPLE;
+            for (uint64_t b = 0; b < n / (uint64_t)be; ++b) {
+                const int rc = orc_dequant_block(dtype, p + b * (uint64_t)bb, dst + b * (uint64_t)be);
+                if (rc) return rc;
+            }
             return ORC_OK;
-        default:
-            return ORC_ERR_UNIMPLEMENTED;
+        }
     }
 }
 

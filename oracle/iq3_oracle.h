@@ -22,6 +22,12 @@
  *   orc_moe_route        brute-force re-derivation of top-k + integer
  *                        invariants of the stable bucket sort
  *   orc_moe_experts      vs an fp64 dense restatement of each expert FFN
+ *   orc_dequant_block    (Q8_0, Q2_K, Q3_K, Q6_K, IQ2_S, IQ3_S, IQ4_XS)
+ *                        bitwise vs oracle/_ref over random blocks and blocks
+ *                        of special values, codebooks vs the reference
+ *                        header, closed forms for single-code blocks
+ *   orc_matmul_rows      bitwise vs oracle/_ref's WeightStore::matvec_quant /
+ *                        matmul_quant on tensors of each type
  */
 #ifndef GPEED_IQ3_ORACLE_H
 #define GPEED_IQ3_ORACLE_H
@@ -36,7 +42,14 @@ extern "C" {
 /* ggml type id of IQ3_XXS (common.h:27) and its geometry (quant.cpp:69,108). */
 #define ORC_DTYPE_F32 0
 #define ORC_DTYPE_F16 1
+#define ORC_DTYPE_Q8_0 8
+#define ORC_DTYPE_Q2_K 10
+#define ORC_DTYPE_Q3_K 11
+#define ORC_DTYPE_Q6_K 14
 #define ORC_DTYPE_IQ3_XXS 18
+#define ORC_DTYPE_IQ3_S 21
+#define ORC_DTYPE_IQ2_S 22
+#define ORC_DTYPE_IQ4_XS 23
 #define ORC_DTYPE_BF16 30
 #define ORC_QK_K 256
 #define ORC_IQ3XXS_BLOCK_BYTES 98
@@ -47,6 +60,17 @@ extern "C" {
 #define ORC_ERR_UNALIGNED_ROW (-3) /* weights.cpp:93-94 */
 
 size_t orc_iq3xxs_row_bytes(uint64_t n_elements);
+
+/* quant_oracle.c: the other block formats (quant.cpp:165-502) */
+int orc_block_elems(int dtype);
+int orc_block_bytes(int dtype);
+size_t orc_row_bytes(int dtype, uint64_t n);
+int orc_dequant_block(int dtype, const uint8_t* blk, float* y);
+uint64_t orc_iq2s_grid(uint32_t i);
+uint32_t orc_iq3s_grid(uint32_t i);
+int orc_iq4nl_value(int i);
+int orc_matmul_rows(int dtype, const uint8_t* w, uint64_t row0, int in_dim, int out_dim, const float* X,
+                    int n_tok, float* Y, float* row_buf);
 float orc_f16_to_f32(uint16_t h);
 uint8_t orc_sign_byte(unsigned idx7);
 uint32_t orc_grid_entry(unsigned idx);

@@ -119,14 +119,16 @@ float ref_dot_f32(const float* a, const float* b, int n) { return glm5::dot_f32(
 
 void ref_axpy_f32(float* a, const float* b, float s, int n) { glm5::axpy_f32(a, b, s, n); }
 
-// Registers `n_rows` rows of `in_dim` IQ3_XXS weights (payload in GGUF row
-// order) as tensor `name`. Returns a handle, or nullptr with ref_last_error().
-void* ref_store_open(const uint8_t* payload, uint64_t n_rows, int in_dim, const char* name,
-                     const char* tmpdir) {
+// Registers `n_rows` rows of `in_dim` weights of type `dtype` (payload in
+// GGUF row order) as tensor `name`. Returns a handle, or nullptr with
+// ref_last_error().
+void* ref_store_open_typed(const uint8_t* payload, uint64_t n_rows, int in_dim, int dtype, const char* name,
+                           const char* tmpdir) {
     try {
         auto* h = new RefStore();
         h->name = name;
-        const size_t rb = glm5::dtype_row_bytes(glm5::DType::IQ3_XXS, static_cast<uint64_t>(in_dim));
+        const auto type = static_cast<glm5::DType>(dtype);
+        const size_t rb = glm5::dtype_row_bytes(type, static_cast<uint64_t>(in_dim));
         const size_t bytes = rb * n_rows;
         std::vector<uint8_t> hdr;
         put_u32(hdr, 0x46554747u);  // "GGUF"
@@ -140,7 +142,7 @@ void* ref_store_open(const uint8_t* payload, uint64_t n_rows, int in_dim, const 
         put_u32(hdr, 2);
         put_u64(hdr, static_cast<uint64_t>(in_dim));
         put_u64(hdr, n_rows);
-        put_u32(hdr, static_cast<uint32_t>(glm5::DType::IQ3_XXS));
+        put_u32(hdr, static_cast<uint32_t>(type));
         put_u64(hdr, 0);
         while (hdr.size() % 32) hdr.push_back(0);
         std::string path = std::string(tmpdir ? tmpdir : "/tmp") + "/gpeed_ref_" +
@@ -160,6 +162,10 @@ void* ref_store_open(const uint8_t* payload, uint64_t n_rows, int in_dim, const 
         g_err = e.what();
         return nullptr;
     }
+}
+
+void* ref_store_open(const uint8_t* payload, uint64_t n_rows, int in_dim, const char* name, const char* tmpdir) {
+    return ref_store_open_typed(payload, n_rows, in_dim, static_cast<int>(glm5::DType::IQ3_XXS), name, tmpdir);
 }
 
 int ref_store_resident_bytes(void* hp, uint64_t* out) {

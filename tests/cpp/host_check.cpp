@@ -10,6 +10,7 @@
 //       token 0) and <dir>/Y.bin (matmul_quant)
 //   host_check moe <dir> <n_exp> <hidden> <inter> <n_tok> <top_k> <mode>
 //       reads gate.bin up.bin down.bin x.bin logits.bin; writes Y.bin
+//   host_check dequant <dtype> <raw file> <n> <out>
 //   host_check gguf-info <file>          (no device use)
 //       the GGUF model (shards discovered from the name) as one JSON object
 //   host_check gguf-read <file> <tensor> <out>   (no device use)
@@ -193,6 +194,15 @@ int main(int argc, char** argv) {
             spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
             return 0;
         }
+        if (mode == "dequant" && argc == 6) {  // host-array dequantize (quant.h:18-22)
+            const int dtype = std::atoi(argv[2]);
+            const uint64_t n = std::strtoull(argv[4], nullptr, 10);
+            const std::vector<char> raw = slurp(argv[3]);
+            std::vector<float> out(n);
+            glm5::gpu::dequantize(static_cast<glm5::gpu::DType>(dtype), raw.data(), out.data(), n);
+            spit(argv[5], out.data(), out.size() * 4);
+            return 0;
+        }
         if (mode == "gguf-info" && argc == 3) {
             gguf_info(argv[2]);
             return 0;
@@ -268,7 +278,7 @@ int main(int argc, char** argv) {
             std::printf("resident %zu\n", ws.resident_bytes());
             return 0;
         }
-        std::fprintf(stderr, "usage: host_check kernels|errors|matmul ...|moe ...|gguf-info|gguf-read|gguf-store\n");
+        std::fprintf(stderr, "usage: host_check kernels|errors|matmul ...|moe ...|dequant ...|gguf-info|gguf-read|gguf-store\n");
         return 2;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "host_check: %s\n", e.what());

@@ -16,6 +16,11 @@ and the GPU kernels where the checkout is absent. Inputs are built here:
 * matvec: a 48-row x 1024 weight (seeded), one x and three tokens through
   WeightStore::matvec_quant / matmul_quant (rows 16..47 and 8..39).
 * dot: dot_f32 over lengths that exercise the 16-wide, 8-wide and scalar tails.
+* quant_formats: for Q8_0, Q2_K, Q3_K, Q6_K, IQ3_S, IQ2_S, IQ4_XS, F16, BF16
+  and F32, seeded blocks (the first eight with fp16 scales +-0, the smallest
+  subnormal, the largest finite, +-inf, NaN and 1.0) through dequantize, and
+  a 12-row x 512 weight with two tokens through WeightStore::matmul_quant
+  (rows 2..9).
 
 Run: python tests/golden/make_golden.py   (needs `make -C oracle ref`)
 """
@@ -64,6 +69,35 @@ def edge_blocks() -> np.ndarray:
     return blocks
 
 
+SPECIAL_D = [0x0000, 0x8000, 0x0001, 0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x3C00]
+
+
+def quant_formats(R) -> dict:
+    out = {}
+    for dt in [8, 10, 11, 14, 21, 22, 23, 0, 1, 30]:
+        if dt in synth.FORMATS:
+            elems, nbytes, d_offs = synth.FORMATS[dt]
+            raw = synth.quant_blocks(21, dt, dt, 16)
+            for i, h in enumerate(SPECIAL_D):
+                for off in d_offs:
+                    raw[i, off:off + 2] = np.frombuffer(struct.pack("<H", h), dtype=np.uint8)
+            n = 16 * elems
+        else:
+            n = 600
+            raw = synth.quant_matrix(21, dt, dt, 1, n).reshape(-1)
+            if dt != 0:
+                raw[: 2 * len(SPECIAL_D)] = np.frombuffer(struct.pack("<8H", *SPECIAL_D), dtype=np.uint8)
+        deq = np.empty(n, np.float32)
+        assert R.ref_dequantize(dt, np.ascontiguousarray(raw).ctypes.data, deq, n) == 0
+        w = synth.quant_matrix(22, dt, dt, 12, 512)
+        X = synth.normal(22, 100 + dt, 2 * 512).reshape(2, 512)
+        st = oracle.RefStore(w, 12, 512, name="t.weight", dtype=dt)
+        Y = st.matmul(2, 512, 8, X)
+        st.close()
+        out.update({f"raw_{dt}": raw, f"deq_{dt}": deq, f"w_{dt}": w, f"X_{dt}": X, f"Y_{dt}": Y})
+    return out
+
+
 def main():
     R = oracle.ref()
     if R is None:
@@ -91,6 +125,7 @@ def main():
     b = synth.normal(12, 1, 1000)
     dots = np.array([R.ref_dot_f32(a, b, int(n)) for n in lens], np.float32)
     np.savez(os.path.join(HERE, "dot.npz"), a=a, b=b, lens=lens, dots=dots)
+    np.savez(os.path.join(HERE, "quant_formats.npz"), **quant_formats(R))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -200,31 +200,42 @@ def test_gguf_rejects_damaged_files(tmp_path, damage, msg):
 
 @pytest.mark.gpu
 def test_store_pins_and_reads_back(gpu, tmp_path):
-    """pin_nonexpert holds every IQ3_XXS tensor but the routed experts;
-    pin_experts adds them; each HBM copy reads back to the file's bytes."""
+    """pin_nonexpert holds, as the reference's (weights.cpp:70-84), every
+    tensor but the routed experts, F32 tensors, payloads under 4 KiB and
+    (here) types the kernels do not decode; pin_experts adds the experts.
+    Each HBM copy (T64 for IQ3_XXS, GGUF rows otherwise) reads back to the
+    file's bytes."""
     path = str(tmp_path / "t.gguf")
-    _, tensors = selftest_file(path)
-    iq = {n: p for n, d, t, p in tensors if t == gguf.IQ3_XXS}
+    wq6 = synth.quant_matrix(78, 0, 14, 16, 512)
+    wq8 = synth.quant_matrix(78, 1, 8, 64, 512)
+    extra = [("blk.0.attn_output.weight", [512, 16], gguf.Q6_K, wq6.tobytes()),
+             ("blk.0.attn_kv_a_mqa.weight", [512, 64], gguf.Q8_0, wq8.tobytes()),
+             ("blk.0.attn_norm.weight", [2048], gguf.F32, synth.normal(78, 2, 2048).tobytes()),
+             ("blk.0.q4_0.weight", [512, 16], 2, bytes(16 * 16 * 18))]
+    _, tensors = selftest_file(path, extra_tensors=extra)
+    pinned = {"blk.0.attn_q_a.weight", "blk.0.attn_output.weight", "blk.0.attn_kv_a_mqa.weight"}
+    payload = {n: p for n, d, t, p in tensors}
     script = tmp_path / "s.txt"
     lines = ["pin_nonexpert"]
-    lines += [f"readback {n} {tmp_path / (n + '.raw')}" for n in iq if "exps" not in n]
+    lines += [f"readback {n} {tmp_path / (n + '.raw')}" for n in sorted(pinned)]
     lines += ["pin_experts", f"readback blk.0.ffn_gate_exps.weight {tmp_path / 'exps.raw'}"]
     script.write_text("\n".join(lines) + "\n")
     out = run("gguf-store", path, script).stdout.split("\n")
     res = [int(l.split()[1]) for l in out if l.startswith("resident")]
     t64 = lambda rows, k: -(-rows // 64) * 64 * k // 256 * 98  # noqa: E731
-    assert res[0] == t64(1, 256) + t64(70, 512)          # test.iq3_xxs + attn_q_a (T64 copies)
-    assert res[1] == res[0] + t64(512, 512)              # + the 4-expert tensor
-    for n, p in iq.items():
-        f = tmp_path / ("exps.raw" if "exps" in n else n + ".raw")
-        assert f.read_bytes() == p, n
+    assert res[0] == t64(70, 512) + wq6.nbytes + wq8.nbytes
+    assert res[1] == res[0] + t64(512, 512)  # + the 4-expert tensor
+    for n in pinned:
+        assert (tmp_path / (n + ".raw")).read_bytes() == payload[n], n
+    assert (tmp_path / "exps.raw").read_bytes() == payload["blk.0.ffn_gate_exps.weight"]
 
 
 @pytest.mark.gpu
 def test_store_products_by_name(gpu, tmp_path):
     """matvec_quant / matmul_quant by tensor name on a store attached to a GGUF
-    model (tensors uploaded on first use) and the routed-expert step on the
-    file's 3-D expert tensors, against the oracle."""
+    model (tensors uploaded on first use, IQ3_XXS and other formats) and the
+    routed-expert step on the file's 3-D expert tensors, against the
+    oracle."""
     H, I, E, T, K = 512, 256, 8, 5, 2
     NH, KVL, DK = 16, 512, 256  # attn_k_b: NH heads of KVL rows over DK
     wq = synth.iq3xxs_matrix(79, 0, 384, 1024)
@@ -232,11 +243,15 @@ def test_store_products_by_name(gpu, tmp_path):
     wg = synth.iq3xxs_matrix(79, 1, E * I, H)
     wu = synth.iq3xxs_matrix(79, 2, E * I, H)
     wd = synth.iq3xxs_matrix(79, 3, E * H, I)
+    wo = synth.quant_matrix(79, 10, 14, 96, 1024)
+    wkv = synth.quant_matrix(79, 11, 8, 80, 1024)
     tensors = [("blk.3.attn_q_b.weight", [1024, 384], gguf.IQ3_XXS, wq.tobytes()),
                ("blk.3.ffn_gate_exps.weight", [H, I, E], gguf.IQ3_XXS, wg.tobytes()),
                ("blk.3.ffn_up_exps.weight", [H, I, E], gguf.IQ3_XXS, wu.tobytes()),
                ("blk.3.ffn_down_exps.weight", [I, H, E], gguf.IQ3_XXS, wd.tobytes()),
-               ("blk.3.attn_k_b.weight", [DK, NH * KVL], gguf.IQ3_XXS, wk.tobytes())]
+               ("blk.3.attn_k_b.weight", [DK, NH * KVL], gguf.IQ3_XXS, wk.tobytes()),
+               ("blk.3.attn_output.weight", [1024, 96], gguf.Q6_K, wo.tobytes()),
+               ("blk.3.attn_kv_a_mqa.weight", [1024, 80], gguf.Q8_0, wkv.tobytes())]
     path = str(tmp_path / "m.gguf")
     gguf.write(path, [("general.alignment", gguf.UINT32, 32)], tensors)
     x = synth.normal(79, 4, 1024)
@@ -251,7 +266,9 @@ def test_store_products_by_name(gpu, tmp_path):
         f"matmul blk.3.attn_q_b.weight 0 1024 384 12 {tmp_path / 'X.bin'} {tmp_path / 'Y.bin'}\n"
         f"moe blk.3.ffn_gate_exps.weight blk.3.ffn_up_exps.weight blk.3.ffn_down_exps.weight {E} {H} {I} {T} {K} "
         f"{tmp_path / 'Xm.bin'} {tmp_path / 'lg.bin'} {tmp_path / 'Ym.bin'}\n"
-        f"heads blk.3.attn_k_b.weight 0 {DK} {KVL} {NH} {tmp_path / 'qn.bin'} {tmp_path / 'qa.bin'}\n")
+        f"heads blk.3.attn_k_b.weight 0 {DK} {KVL} {NH} {tmp_path / 'qn.bin'} {tmp_path / 'qa.bin'}\n"
+        f"matvec blk.3.attn_output.weight 16 1024 80 {tmp_path / 'x.bin'} {tmp_path / 'yo.bin'}\n"
+        f"matmul blk.3.attn_kv_a_mqa.weight 0 1024 80 12 {tmp_path / 'X.bin'} {tmp_path / 'Ykv.bin'}\n")
     run("gguf-store", path, tmp_path / "s.txt")
     y = np.fromfile(tmp_path / "y.bin", np.float32)
     assert rel_err(y, oracle.matvec(wq, 64, 1024, 300, x)) < TIGHT
@@ -265,3 +282,8 @@ def test_store_products_by_name(gpu, tmp_path):
     qa = np.fromfile(tmp_path / "qa.bin", np.float32).reshape(NH, KVL)
     for h in range(NH):  # each head: the matvec_quant of model.cpp:640
         assert rel_err(qa[h], oracle.matvec(wk, h * KVL, DK, KVL, qn[h])) < TIGHT, h
+    # the other formats by name (Q6_K, Q8_0), uploaded on first use
+    yo = np.fromfile(tmp_path / "yo.bin", np.float32)
+    assert rel_err(yo, oracle.matmul_rows(14, wo, 16, 1024, 80, x)[0]) < TIGHT
+    Ykv = np.fromfile(tmp_path / "Ykv.bin", np.float32).reshape(12, 80)
+    assert rel_err(Ykv, oracle.matmul_rows(8, wkv, 0, 1024, 80, X)) < TIGHT
