@@ -322,6 +322,40 @@ def mla_heads(torch, G, synth, dev, reps, copies=64):
     return out
 
 
+def other_formats(torch, G, synth, dev, reps, min_bytes=600e6):
+    """Batch-1 products over raw GGUF rows of the other formats of a UD-IQ3_XXS file
+    (gpeed_matmul_rows; weights.cpp:167-203 for any decoded type): a 6144x6144 weight per
+    format, rotated copies (at least `min_bytes` in all) so the reads come from HBM. Time per
+    launch from events around `reps` back-to-back launches."""
+    K = N = 6144
+    out = {"workload": "matvec over 6144x6144 GGUF rows, one token, fp32 x, per format"}
+    names = {8: "Q8_0", 10: "Q2_K", 11: "Q3_K", 14: "Q6_K", 21: "IQ3_S", 22: "IQ2_S", 23: "IQ4_XS", 1: "F16",
+             30: "BF16", 18: "IQ3_XXS (raw rows)"}
+    x = torch.from_numpy(synth.normal(2031, 0, K)).to(dev)
+    y = torch.empty(N, device=dev)
+    for dt, name in names.items():
+        w = torch.from_numpy(synth.quant_matrix(2031, dt, dt, N, K).reshape(-1)).to(dev)
+        nbytes = w.numel()
+        copies = max(2, int(min_bytes // nbytes) + 1)
+        ws = [w] + [w.clone() for _ in range(copies - 1)]
+        for c in range(copies):
+            G.matmul_rows(dt, ws[c], N, 0, K, N, x, out=y)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for r in range(reps * copies):
+            G.matmul_rows(dt, ws[r % copies], N, 0, K, N, x, out=y)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "packed_bytes": nbytes, "GBs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del ws, w
+        torch.cuda.empty_cache()
+    return out
+
+
 def decode_mix(torch, G, synth, dev, reps, copies=4):
     """Continuous-batching decode mix: 64 tokens (fp32 X [64, 6144]) through the MLA latent projections
     kv_a 576x6144 and q_a 1536x6144 and the shared-expert FFN (gate, up 12288x6144; down 6144x12288 with
@@ -666,6 +700,8 @@ def main():
         rec["extra"]["decode_mix"] = decode_mix(torch, G, synth, dev, 20)
         torch.cuda.empty_cache()
         rec["extra"]["mla_heads"] = mla_heads(torch, G, synth, dev, 20)
+        torch.cuda.empty_cache()
+        rec["extra"]["other_formats"] = other_formats(torch, G, synth, dev, 5)
     if not args.no_cpu:
         log("cpu baseline")
         cb, y_ref = cpu_baseline(wg, wu, wd, x)

@@ -108,11 +108,12 @@ __device__ __forceinline__ void decode32(const uint8_t* __restrict__ blk, int sb
 #pragma unroll
         for (int i = 0; i < 32; ++i) y[i] = f[i];
     } else if constexpr (DT == kDtF16 || DT == kDtBF16) {
-        // quant.cpp:532-545 (f16_to_f32 :130-154, bf16_to_f32 :156-161)
+        // quant.cpp:532-545 (f16_to_f32 :130-154, bf16_to_f32 :156-161); the
+        // hardware fp16 conversion is exact (subnormals included)
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
             const uint32_t h = u16(blk + 2 * i);
-            y[i] = DT == kDtF16 ? f16_bits_to_f32(h) : __uint_as_float(h << 16);
+            y[i] = DT == kDtF16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : __uint_as_float(h << 16);
         }
     } else if constexpr (DT == kDtQ8_0) {
         // quant.cpp:165-184: d (fp16), 32 int8 codes; y = d * q
@@ -302,57 +303,138 @@ __global__ __launch_bounds__(256) void k_dequant_scalar(const uint8_t* __restric
                                                         long long n) {
     for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
         if constexpr (DT == kDtF32) dst[i] = reinterpret_cast<const float*>(src)[i];
-        else if constexpr (DT == kDtF16) dst[i] = f16_bits_to_f32(u16(src + 2 * i));
+        else if constexpr (DT == kDtF16) dst[i] = (float)__builtin_bit_cast(_Float16, (uint16_t)u16(src + 2 * i));
         else dst[i] = __uint_as_float(u16(src + 2 * i) << 16);
     }
 }
 
-// Y[t][j] = sum_i W[row0 + j][i] * X[t][i] over raw GGUF rows: one
-// wavefront per row (grid-stride over rows), lanes over the row's 32-weight
-// sub-blocks, NT tokens per launch column (blockIdx.y), fp32 FMA
-// accumulation and a butterfly reduction.
+// Rows per wavefront and the bytes of one 64-sub-block chunk of a row.
+template <int DT> struct RowsCfg {
+    static constexpr int kRW = DT == kDtF32 ? 1 : (DT == kDtF16 || DT == kDtBF16) ? 2 : 4;
+    static constexpr int kChunkBytes = 64 * 32 / Fmt<DT>::kElems * Fmt<DT>::kBytes;  // 64 sub-blocks
+    static constexpr int kSegs = (kChunkBytes + 15) / 16 + 1;  // 16-byte segments covering it, any alignment
+    static constexpr int kLoads = (kSegs + 63) / 64;           // per lane
+    static constexpr int kStride = kLoads * 64 * 16;           // LDS bytes per staged row chunk
+};
+
+constexpr int kBufferDword3 = 0x00020000;
+
+// Y[t][j] = sum_i W[j][i] * X[t][i] over raw GGUF rows (w = the first row of
+// this launch's slice at byte `lead` of base[0, base_bytes), base 16-byte
+// aligned; Y rows ldy apart). Each wavefront takes kRW consecutive rows
+// (grid-stride) and walks them in chunks of 64 sub-blocks: a chunk of each
+// row is fetched with coalesced 16-byte buffer loads (the next chunk's loads
+// are in flight while this one is decoded), staged in the wavefront's LDS
+// region, and lane l decodes sub-block l of it for every row, against the
+// same 32 activations per token. fp32 FMA accumulation and a butterfly
+// reduction per row and token. (Splitting a row group's K range over the
+// workgroup's wavefronts measured no faster.)
 template <int DT, int NT>
-__global__ __launch_bounds__(256) void k_matmul_rows(const uint8_t* __restrict__ w, size_t row_bytes,
-                                                     unsigned long long row0, int in_dim, int out_dim,
-                                                     const float* __restrict__ X, int n_tok,
-                                                     float* __restrict__ Y) {
+__global__ __launch_bounds__(256) void k_matmul_rows(const uint8_t* base, int base_bytes, uint32_t lead,
+                                                     uint32_t row_bytes, int in_dim, int out_dim,
+                                                     const float* __restrict__ X, int n_tok, float* __restrict__ Y,
+                                                     int ldy) {
+    using C = RowsCfg<DT>;
+    constexpr int RW = C::kRW, kSub = Fmt<DT>::kElems / 32, kBB = Fmt<DT>::kBytes;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, base_bytes, kBufferDword3);
     __shared__ Tables<DT> tb;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[4][RW][C::kStride];
     tb.load(threadIdx.x, 256);
     __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t0 = blockIdx.y * NT;
     const int nt = n_tok - t0 < NT ? n_tok - t0 : NT;
     const int n_sub = in_dim / 32;
-    for (int j = blockIdx.x * 4 + wave; j < out_dim; j += gridDim.x * 4) {
-        const uint8_t* row = w + (size_t)(row0 + (unsigned long long)j) * row_bytes;
-        float acc[NT];
+    // segment loads of the chunk at sub-block sb of the rows into registers
+    auto fetch = [&](int j0, int sb, u32x4_t (&seg)[RW][C::kLoads]) {
+        const int cnt = n_sub - sb < 64 ? n_sub - sb : 64;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-        for (int s = lane; s < n_sub; s += 64) {
-            int sb;
-            const uint8_t* blk = sub_block<DT>(row, s, sb);
-            float y[32];
-            decode32<DT>(blk, sb, tb, y);
+        for (int r = 0; r < RW; ++r) {
+            const int j = j0 + r;
+            const uint32_t a0 = lead + (uint32_t)j * row_bytes + (uint32_t)(sb / kSub) * kBB;
+            const uint32_t a1 = a0 + (uint32_t)(cnt / kSub) * kBB;
+            const uint32_t b0 = a0 & ~15u;
+            const uint32_t nseg = j < out_dim ? (a1 - b0 + 15) >> 4 : 0;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                if (t < nt) {
-                    const float4* xv = reinterpret_cast<const float4*>(X + (size_t)(t0 + t) * in_dim + 32 * s);
+            for (int k = 0; k < C::kLoads; ++k) {
+                const uint32_t i = (uint32_t)(lane + 64 * k);
+                const uint32_t off = i < nseg ? b0 + 16 * i : 0x80000000u;  // past the range: zeros, no access
+                seg[r][k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+            }
+        }
+    };
+    for (int j0 = (blockIdx.x * 4 + wave) * RW; j0 < out_dim; j0 += gridDim.x * 4 * RW) {
+        float acc[RW][NT];
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[r][t] = 0.0f;
+        u32x4_t seg[RW][C::kLoads];
+        fetch(j0, 0, seg);
+        for (int sb = 0; sb < n_sub; sb += 64) {
+            // stage this chunk (the reads of the previous one came first: one
+            // wavefront's LDS operations complete in order)
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int k = 0; k < C::kLoads; ++k)
+                    *reinterpret_cast<u32x4_t*>(&stage[wave][r][(lane + 64 * k) * 16]) = seg[r][k];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (sb + 64 < n_sub) fetch(j0, sb + 64, seg);
+            const int s = sb + lane;
+            if (s < n_sub) {
+                const uint32_t lead_c = (lead + (uint32_t)(sb / kSub) * kBB) & 15u;
+                float xs[NT == 1 ? 32 : 1];
+                if constexpr (NT == 1) {
+                    const float4* xv = reinterpret_cast<const float4*>(X + (size_t)t0 * in_dim + 32 * s);
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
                         const float4 v = xv[k];
-                        acc[t] = fmaf(y[4 * k], v.x, acc[t]);
-                        acc[t] = fmaf(y[4 * k + 1], v.y, acc[t]);
-                        acc[t] = fmaf(y[4 * k + 2], v.z, acc[t]);
-                        acc[t] = fmaf(y[4 * k + 3], v.w, acc[t]);
+                        xs[4 * k] = v.x; xs[4 * k + 1] = v.y; xs[4 * k + 2] = v.z; xs[4 * k + 3] = v.w;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    // the row's chunk starts (its byte address) mod 16 bytes into its
+                    // staged copy; row_bytes is even, so blocks stay 2-byte aligned
+                    const uint32_t o = (lead_c + (uint32_t)(j0 + r) * row_bytes) & 15u;
+                    const uint8_t* blk = &stage[wave][r][o + (uint32_t)((s - sb) / kSub) * kBB];
+                    float y[32];
+                    decode32<DT>(blk, s % kSub, tb, y);
+                    if constexpr (NT == 1) {
+#pragma unroll
+                        for (int e = 0; e < 32; ++e) acc[r][0] = fmaf(y[e], xs[e], acc[r][0]);
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            if (t < nt) {
+                                const float4* xv =
+                                    reinterpret_cast<const float4*>(X + (size_t)(t0 + t) * in_dim + 32 * s);
+#pragma unroll
+                                for (int k = 0; k < 8; ++k) {
+                                    const float4 v = xv[k];
+                                    acc[r][t] = fmaf(y[4 * k], v.x, acc[r][t]);
+                                    acc[r][t] = fmaf(y[4 * k + 1], v.y, acc[r][t]);
+                                    acc[r][t] = fmaf(y[4 * k + 2], v.z, acc[r][t]);
+                                    acc[r][t] = fmaf(y[4 * k + 3], v.w, acc[r][t]);
+                                }
+                            }
+                        }
                     }
                 }
             }
+            // every lane's reads of this chunk before the next chunk's writes
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
+        for (int r = 0; r < RW; ++r) {
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) acc[t] += __shfl_xor(acc[t], off);
-            if (lane == 0 && t < nt) Y[(size_t)(t0 + t) * out_dim + j] = acc[t];
+            for (int t = 0; t < NT; ++t) {
+                float v = acc[r][t];
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+                if (lane == 0 && t < nt && j0 + r < out_dim) Y[(size_t)(t0 + t) * ldy + j0 + r] = v;
+            }
         }
     }
 }
@@ -373,18 +455,29 @@ hipError_t dequant_dt(const uint8_t* src, float* dst, unsigned long long n, hipS
 }
 
 template <int DT, int NT>
-hipError_t matmul_dt_nt(const uint8_t* w, size_t rb, unsigned long long row0, int in_dim, int out_dim, const float* X,
-                        int n_tok, float* Y, hipStream_t s) {
-    int grid = (out_dim + 3) / 4;
-    if (grid > 2048) grid = 2048;
-    // at most 32768 token columns per launch (grid.y stays far below its limit)
+hipError_t matmul_dt_nt(const uint8_t* w, size_t rb, int in_dim, int out_dim, const float* X, int n_tok, float* Y,
+                        hipStream_t s) {
+    // row slices whose bytes stay below 2 GiB (32-bit buffer offsets); at
+    // most 32768 token columns per launch
+    constexpr int RW = RowsCfg<DT>::kRW;
+    const long long max_rows = ((1ll << 31) - 64) / (long long)rb / (4 * RW) * (4 * RW);
     constexpr int kMaxTok = 32768 * NT;
-    for (int t = 0; t < n_tok; t += kMaxTok) {
-        const int nt = n_tok - t < kMaxTok ? n_tok - t : kMaxTok;
-        hipLaunchKernelGGL((k_matmul_rows<DT, NT>), dim3(grid, (nt + NT - 1) / NT), dim3(256), 0, s, w, rb, row0,
-                           in_dim, out_dim, X + (size_t)t * in_dim, nt, Y + (size_t)t * out_dim);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+    for (int j = 0; j < out_dim; j += (int)max_rows) {
+        const int rows = out_dim - j < max_rows ? out_dim - j : (int)max_rows;
+        const uint8_t* wj = w + (size_t)j * rb;
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(wj) & ~(uintptr_t)15);
+        const uint32_t lead = (uint32_t)(wj - base);
+        const int base_bytes = (int)(lead + (size_t)rows * rb);
+        int grid = (rows + 4 * RW - 1) / (4 * RW);
+        if (grid > 2048) grid = 2048;
+        for (int t = 0; t < n_tok; t += kMaxTok) {
+            const int nt = n_tok - t < kMaxTok ? n_tok - t : kMaxTok;
+            hipLaunchKernelGGL((k_matmul_rows<DT, NT>), dim3(grid, (nt + NT - 1) / NT), dim3(256), 0, s, base, base_bytes, lead,
+                               (uint32_t)rb, in_dim, rows, X + (size_t)t * in_dim, nt,
+                               Y + (size_t)t * out_dim + j, out_dim);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }
@@ -392,10 +485,11 @@ hipError_t matmul_dt_nt(const uint8_t* w, size_t rb, unsigned long long row0, in
 template <int DT>
 hipError_t matmul_dt(const uint8_t* w, size_t rb, unsigned long long row0, int in_dim, int out_dim, const float* X,
                      int n_tok, float* Y, hipStream_t s) {
-    if (n_tok == 1) return matmul_dt_nt<DT, 1>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
-    if (n_tok == 2) return matmul_dt_nt<DT, 2>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
-    if (n_tok <= 4) return matmul_dt_nt<DT, 4>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
-    return matmul_dt_nt<DT, 8>(w, rb, row0, in_dim, out_dim, X, n_tok, Y, s);
+    w += (size_t)row0 * rb;
+    if (n_tok == 1) return matmul_dt_nt<DT, 1>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
+    if (n_tok == 2) return matmul_dt_nt<DT, 2>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
+    if (n_tok <= 4) return matmul_dt_nt<DT, 4>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
+    return matmul_dt_nt<DT, 8>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
 }
 
 }  // namespace
