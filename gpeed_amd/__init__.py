@@ -112,6 +112,9 @@ def lib():
             "gpeed_iq3xxs_moe_ws_bytes": ([i32, i32, i32, i32, i32], sz),
             "gpeed_iq3xxs_moe_experts": ([vp, vp, vp, i32, i32, i32, vp, i32, i32, vp, vp, vp, C.c_float, vp, vp,
                                           sz, vp], i32),
+            "gpeed_iq3xxs_moe_batch_ws_bytes": ([i32, i32, i32, i32, i32, i32], sz),
+            "gpeed_iq3xxs_moe_batch": ([vp, i32, i32, i32, i32, vp, C.c_float, i32, vp, vp, vp, vp, vp, vp, i32, i32,
+                                        vp, C.c_float, vp, vp, vp, vp, vp, sz, vp], i32),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -583,6 +586,44 @@ def moe_experts(w_gate, w_up, w_down, n_exp: int, hidden: int, inter: int, X, to
                                           top_k, _ptr(eptr), _ptr(tok), _ptr(wt), swiglu_limit, _ptr(out), _ptr(ws),
                                           ws.numel(), _stream(stream)), "moe_experts")
     return out
+
+
+def moe_batch_workspace(n_tok: int, n_exp: int, top_k: int, hidden: int, inter: int, shared: bool = True,
+                        device="cuda"):
+    return _zeros(lib().gpeed_iq3xxs_moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, int(shared)), device)
+
+
+def moe_batch(logits, X, w_gate, w_up, w_down, n_exp: int, hidden: int, inter: int, top_k: int, mode: int = 0,
+              bias=None, routed_scale: float = 1.0, norm_topk: bool = True, swiglu_limit: float = 10.0,
+              shared=None, out=None, ws=None, routing: bool = False, stream=None):
+    """The whole routed step of Model::moe_batch from the router logits
+    (model_batch.cpp:174-280) in five launches: router + buckets, routed
+    experts (T64 tensors), and the shared expert (shared = (gate, up, down)
+    T64 tensors, or None) added last. Returns Y [n_tok, hidden], or
+    (Y, eptr, tok, wt) with routing=True."""
+    torch = _torch()
+    _require_cuda(logits, X, w_gate, w_up, w_down)
+    T = X.shape[0]
+    dev_ = X.device
+    if out is None:
+        out = torch.empty(T, hidden, dtype=torch.float32, device=dev_)
+    if ws is None:
+        ws = moe_batch_workspace(T, n_exp, top_k, hidden, inter, shared is not None, dev_)
+    gs, us, ds = (C.c_void_p(0),) * 3 if shared is None else \
+        tuple(C.c_void_p(0) if t is None else _ptr(t) for t in shared)
+    eptr = tok = wt = None
+    if routing:
+        eptr = torch.empty(n_exp + 1, dtype=torch.int32, device=dev_)
+        tok = torch.empty(T * top_k, dtype=torch.int32, device=dev_)
+        wt = torch.empty(T * top_k, dtype=torch.float32, device=dev_)
+    nul = C.c_void_p(0)
+    b = nul if bias is None else _ptr(bias)
+    _check(lib().gpeed_iq3xxs_moe_batch(_ptr(logits), T, n_exp, top_k, mode, b, routed_scale, int(norm_topk),
+                                        _ptr(w_gate), _ptr(w_up), _ptr(w_down), gs, us, ds, hidden, inter, _ptr(X),
+                                        swiglu_limit, _ptr(out), _ptr(eptr) if routing else nul,
+                                        _ptr(tok) if routing else nul, _ptr(wt) if routing else nul, _ptr(ws),
+                                        ws.numel(), _stream(stream)), "moe_batch")
+    return (out, eptr, tok, wt) if routing else out
 
 
 def matmul_rows(dtype: int, w, n_rows: int, row0: int, in_dim: int, out_dim: int, X, out=None, stream=None):

@@ -813,6 +813,46 @@ int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "moe_experts launch");
 }
 
+size_t gpeed_iq3xxs_moe_batch_ws_bytes(int n_tok, int n_exp, int top_k, int hidden, int inter, int shared) {
+    if (n_tok < 1 || n_tok > 8192 || n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp) return 0;
+    if ((int64_t)n_tok * top_k > (1 << 24)) return 0;
+    if (!dims_ok(hidden) || !dims_ok(inter)) return 0;
+    return gpeed::moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, shared ? 1 : 0);
+}
+
+int gpeed_iq3xxs_moe_batch(const float* logits, int n_tok, int n_exp, int top_k, int mode, const float* bias,
+                           float routed_scale, int norm_topk, const void* w_gate, const void* w_up,
+                           const void* w_down, const void* w_gate_sh, const void* w_up_sh, const void* w_down_sh,
+                           int hidden, int inter, const float* X, float swiglu_limit, float* Y, int* eptr, int* tok,
+                           float* wt, void* ws, size_t ws_bytes, gpeed_stream_t stream) {
+    if (n_tok <= 0) return GPEED_OK;
+    if (hidden <= 0 || hidden % gpeed::kQK || inter <= 0 || inter % gpeed::kQK)
+        return fail(GPEED_ERR_UNALIGNED_ROW, "moe_batch: row not block aligned");
+    if (!dims_ok(hidden) || !dims_ok(inter)) return fail(GPEED_ERR_INVALID, "moe_batch: size too large");
+    if (n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp)
+        return fail(GPEED_ERR_UNIMPLEMENTED, "moe_batch: needs 1 <= top_k <= min(32, n_exp), n_exp <= 1024");
+    if (mode != 0 && mode != 1) return fail(GPEED_ERR_INVALID, "moe_batch: mode must be 0 (sigmoid) or 1 (softmax)");
+    if (n_tok > 8192) return fail(GPEED_ERR_INVALID, "moe_batch: at most 8192 tokens per call");
+    if (!logits || !w_gate || !w_up || !w_down || !X || !Y) return fail(GPEED_ERR_INVALID, "moe_batch: null pointer");
+    const bool sh = w_gate_sh || w_up_sh || w_down_sh;
+    if (sh && !(w_gate_sh && w_up_sh && w_down_sh))
+        return fail(GPEED_ERR_INVALID, "moe_batch: give all three shared-expert tensors or none");
+    for (const void* p : {w_gate, w_up, w_down, (const void*)X, (const void*)Y, w_gate_sh, w_up_sh, w_down_sh})
+        if (p && !aligned(p, 16)) return fail(GPEED_ERR_INVALID, "moe_batch: weights, X and Y must be 16-byte aligned");
+    if (!ws || !aligned(ws, 256) ||
+        ws_bytes < gpeed::moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, sh ? 1 : 0))
+        return fail(GPEED_ERR_WORKSPACE, "moe_batch: workspace missing, misaligned or too small");
+    const DeviceState* st = nullptr;
+    int rc = device_state(&st);
+    if (rc) return rc;
+    hipError_t e = gpeed::launch_moe_batch(
+        logits, n_tok, n_exp, top_k, mode, bias, routed_scale, norm_topk, static_cast<const uint8_t*>(w_gate),
+        static_cast<const uint8_t*>(w_up), static_cast<const uint8_t*>(w_down), static_cast<const uint8_t*>(w_gate_sh),
+        static_cast<const uint8_t*>(w_up_sh), static_cast<const uint8_t*>(w_down_sh), hidden, inter, X, swiglu_limit,
+        Y, eptr, tok, wt, static_cast<uint8_t*>(ws), st->num_cus, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "moe_batch launch");
+}
+
 size_t gpeed_iq3xxs_gemm_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_dim, int x_dtype) {
     if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(in_dim) || out_dim < 1 || out_dim > (1 << 24) ||
         (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16))

@@ -135,6 +135,17 @@ size_t moe_ws_bytes(int T, int E, int K, int H, int I);
 hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int E, int H,
                               int I, const float* X, int T, int K, const int* eptr, const int* tok,
                               const float* wt, float lim, float* Y, uint8_t* ws, int num_cus, hipStream_t s);
+// A whole routed step from the router logits (model_batch.cpp:174-280) in
+// five launches: router + bucket sort + work plan with the per-token X
+// images, grouped gate/up (the shared expert's segments included, w_gate_sh
+// non-null), SwiGLU images, grouped down, combine (+ shared expert).
+// eptr/tok/wt_out: optional device outputs of the routing.
+size_t moe_batch_ws_bytes(int T, int E, int K, int H, int I, int shared);
+hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, const float* bias,
+                            float routed_scale, int norm_topk, const uint8_t* w_gate, const uint8_t* w_up,
+                            const uint8_t* w_down, const uint8_t* w_gate_sh, const uint8_t* w_up_sh,
+                            const uint8_t* w_down_sh, int H, int I, const float* X, float lim, float* Y,
+                            int* eptr_out, int* tok_out, float* wt_out, uint8_t* ws, int num_cus, hipStream_t s);
 
 // Prefill GEMM: Y[m][j] = sum_k X[m][k] W[row0+j][k] for M tokens from the
 // T64 copy. X is fp32 (x_bf16 = 0) or bf16 (x_bf16 = 1), row-major [M][in_dim];

@@ -16,6 +16,7 @@
 //                whole row (no partial sums leave it).
 // k_moe_combine  Y[t] = sum over the token's slots, in expert order, of
 //                wt * down row (one fma per term, like axpy_f32).
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 
@@ -96,12 +97,11 @@ constexpr int kRouteLdsAsg = 2048;
 // J = register slots per lane: expert e lives in lane e % 64, slot e / 64.
 // kLds: T * K <= kRouteLdsAsg, the assignments stay in LDS.
 template <int J, bool kLds>
-__global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ logits, int T, int E, int K,
-                                                    int mode, const float* __restrict__ bias,
-                                                    float routed_scale, int norm_topk, int* __restrict__ eptr,
-                                                    int* __restrict__ tok, float* __restrict__ wt,
-                                                    int* __restrict__ sel, int* __restrict__ asg_e,
-                                                    float* __restrict__ asg_w) {
+__device__ __forceinline__ void route_body(const float* __restrict__ logits, int T, int E, int K, int mode,
+                                           const float* __restrict__ bias, float routed_scale, int norm_topk,
+                                           int* __restrict__ eptr, int* __restrict__ tok, float* __restrict__ wt,
+                                           int* __restrict__ sel, int* __restrict__ asg_e,
+                                           float* __restrict__ asg_w) {
     __shared__ int cnt[kMaxExperts];
     __shared__ int cursor[kMaxExperts];
     __shared__ __attribute__((aligned(16))) int chunk_e[1024];
@@ -263,24 +263,39 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ lo
     }
 }
 
+template <int J, bool kLds>
+__global__ __launch_bounds__(1024) void k_moe_route(const float* __restrict__ logits, int T, int E, int K,
+                                                    int mode, const float* __restrict__ bias,
+                                                    float routed_scale, int norm_topk, int* __restrict__ eptr,
+                                                    int* __restrict__ tok, float* __restrict__ wt,
+                                                    int* __restrict__ sel, int* __restrict__ asg_e,
+                                                    float* __restrict__ asg_w) {
+    route_body<J, kLds>(logits, T, E, K, mode, bias, routed_scale, norm_topk, eptr, tok, wt, sel, asg_e, asg_w);
+}
+
 // ---------------------------------------------------------------------------
 // Work plan of the grouped products
 
 struct MoePlan {
-    int* n_seg;      // [1]
+    int* n_seg;      // [1] segments, shared-expert ones first
+    int* n_sh_seg;   // [1] shared-expert segments (ceil(T_sh / kSegTok))
     int* n_valid;    // [1] bucket slots to multiply: eptr[E], or 0 for buckets that break the invariants
     int* seg_e;      // [S]
     int* seg_p0;     // [S]
     int* seg_n;      // [S]
-    int* seg_of;     // [N] segment of bucket slot p
-    int* idx_of;     // [N] token index of slot p inside its segment
+    int* seg_of;     // [N + T_sh] segment of slot p (routed bucket slots, then one per token for the shared expert)
+    int* idx_of;     // [N + T_sh] token index of slot p inside its segment
+    int* slot_tok;   // [N + T_sh] token of slot p (gather-mode activations)
     int* pos;        // [T][K] slots of token t, in expert order
     uint32_t* ctr;   // [2] work counters (gate/up, down)
     uint32_t* err;   // the workspace's error word (kWsBuckets)
 };
 
-__global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr, const int* __restrict__ tok,
-                                                   int T, int E, int K, MoePlan pl) {
+// T_sh: tokens of the shared expert (0 or T); its segments come first
+// (kSegTok tokens each, all full but the last: the heaviest work), slots
+// N .. N + T_sh - 1, token p - N.
+__device__ __forceinline__ void plan_body(const int* __restrict__ eptr, const int* __restrict__ tok, int T, int E,
+                                          int K, int T_sh, MoePlan pl) {
     __shared__ int ep[kMaxExperts + 1];
     __shared__ int fstart[kMaxExperts + 1];
     __shared__ int nfull[kMaxExperts];
@@ -320,6 +335,7 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
         for (int i = tid; i < T * K; i += 1024) pl.pos[i] = -1;
         if (tid == 0) {
             *pl.n_seg = 0;
+            *pl.n_sh_seg = 0;
             *pl.n_valid = 0;
             __hip_atomic_fetch_or(pl.err, kWsBuckets, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -336,8 +352,11 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
         if (g % kSegTok) atomicAdd(&ccount[g % kSegTok], 1);
     }
     __syncthreads();
-    const int n_full = block_exclusive_scan(nfull, fstart, tmp, E);
+    const int n_sh = (T_sh + kSegTok - 1) / kSegTok;
+    const int n_full = n_sh + block_exclusive_scan(nfull, fstart, tmp, E);
+    for (int e = tid; e < E; e += 1024) fstart[e] += n_sh;
     if (tid == 0) {
+        *pl.n_sh_seg = n_sh;
         int base = n_full;
         for (int c = kSegTok - 1; c >= 1; --c) {
             ccursor[c] = base;
@@ -365,8 +384,18 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
             pl.seg_n[pid[e]] = c;
         }
     }
-    __syncthreads();
     const int N = ep[E];
+    for (int j = tid; j < n_sh; j += 1024) {
+        pl.seg_e[j] = E;  // the shared expert
+        pl.seg_p0[j] = N + j * kSegTok;
+        pl.seg_n[j] = min(kSegTok, T_sh - j * kSegTok);
+    }
+    for (int t = tid; t < T_sh; t += 1024) {
+        pl.seg_of[N + t] = t / kSegTok;
+        pl.idx_of[N + t] = t % kSegTok;
+        pl.slot_tok[N + t] = t;
+    }
+    __syncthreads();
     for (int p = tid; p < N; p += 1024) {
         int lo = 0, hi = E;  // largest e with ep[e] <= p
         while (hi - lo > 1) {
@@ -377,6 +406,7 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
         const int r = p - ep[lo], j = r / kSegTok;
         pl.seg_of[p] = j < nfull[lo] ? fstart[lo] + j : pid[lo];
         pl.idx_of[p] = r % kSegTok;
+        pl.slot_tok[p] = tok[p];
     }
     // each token's slots in bucket order = expert order: every slot appends
     // itself to its token's list, then each list (at most K entries) is
@@ -407,6 +437,12 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr,
     }
 }
 
+__global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr, const int* __restrict__ tok,
+                                                   int T, int E, int K, MoePlan pl) {
+    plan_body(eptr, tok, T, E, K, 0, pl);
+}
+
+
 // ---------------------------------------------------------------------------
 // Activation gather / SwiGLU into per-segment prepared activations
 
@@ -420,16 +456,36 @@ __device__ __forceinline__ size_t act_off(int n_tok, int b, int t, int a, int be
     return base + (4 * beta + 2 * (t & 1) + hl) * 32 + a * 8;
 }
 
+// One 256-element block's activation images, built by one wavefront (lane
+// holds elements 4*lane .. 4*lane+3): the block's power-of-two scale from the
+// wavefront maximum, fp16 hi and lo parts.
+struct BlockImages {
+    _Float16 hi[4], lo[4];
+    int sc;
+};
+__device__ __forceinline__ BlockImages block_images(const float (&e)[4]) {
+    BlockImages r;
+    r.sc = pow2_scale_of_max(wave_max(fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])))));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float xs = ldexpf(e[c], r.sc);
+        r.hi[c] = (_Float16)xs;
+        r.lo[c] = (_Float16)(xs - (float)r.hi[c]);
+    }
+    return r;
+}
+
 // One wavefront per (slot p, block b). MODE 0: v = X[tok[p]]; MODE 1:
-// v = silu(min(G[p],lim)) * clamp(U[p],-lim,lim).
+// v = silu(min(G[p],lim)) * clamp(U[p],-lim,lim), over the bucket slots and
+// then the n_extra shared-expert slots.
 template <int MODE>
 __global__ __launch_bounds__(256) void k_prep_grouped(const float* __restrict__ X, const float* __restrict__ U,
                                                       const int* __restrict__ tok, const int* __restrict__ eptr,
                                                       int E, int nb, float lim, MoePlan pl,
-                                                      uint8_t* __restrict__ act, size_t seg_stride) {
+                                                      uint8_t* __restrict__ act, size_t seg_stride, int n_extra) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + wave;
-    const int N = *pl.n_valid;
+    const int N = *pl.n_valid + (*pl.n_seg > 0 ? n_extra : 0);
     if (item >= N * nb) return;
     const int p = item / nb, b = item - p * nb;
     const size_t row = MODE == 0 ? (size_t)tok[p] : (size_t)p;
@@ -446,21 +502,53 @@ __global__ __launch_bounds__(256) void k_prep_grouped(const float* __restrict__ 
             e[c] = (gi / (1.0f + expf(-gi))) * ui;
         }
     }
-    const int sc =
-        pow2_scale_of_max(wave_max(fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])))));
-    _Float16 hi[4], lo[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const float xs = ldexpf(e[c], sc);
-        hi[c] = (_Float16)xs;
-        lo[c] = (_Float16)(xs - (float)hi[c]);
-    }
+    const BlockImages im = block_images(e);
     const int s = pl.seg_of[p], t = pl.idx_of[p], n = pl.seg_n[s];
     uint8_t* base = act + (size_t)s * seg_stride;
     const int a = lane >> 4, beta = lane & 15;
-    *reinterpret_cast<u32x2_t*>(base + act_off(n, b, t, a, beta, 0)) = __builtin_bit_cast(u32x2_t, hi);
-    *reinterpret_cast<u32x2_t*>(base + act_off(n, b, t, a, beta, 1)) = __builtin_bit_cast(u32x2_t, lo);
-    if (lane == 0) reinterpret_cast<float*>(base + (size_t)nb * n * 1024)[(size_t)b * n + t] = ldexpf(1.0f, -sc);
+    *reinterpret_cast<u32x2_t*>(base + act_off(n, b, t, a, beta, 0)) = __builtin_bit_cast(u32x2_t, im.hi);
+    *reinterpret_cast<u32x2_t*>(base + act_off(n, b, t, a, beta, 1)) = __builtin_bit_cast(u32x2_t, im.lo);
+    if (lane == 0) reinterpret_cast<float*>(base + (size_t)nb * n * 1024)[(size_t)b * n + t] = ldexpf(1.0f, -im.sc);
+}
+
+// Per-token activation images of X (one 1 KiB image set per token and
+// block, in the layout of a one-token segment, plus the block unscale):
+// items (t, b) from `item0`, `n_waves` wavefronts in all.
+__device__ __forceinline__ void token_images(const float* __restrict__ X, int T, int nb, uint8_t* __restrict__ timg,
+                                             float* __restrict__ tus, int item0, int n_waves, uint32_t lane) {
+    for (int item = item0; item < T * nb; item += n_waves) {
+        const float4 v = *reinterpret_cast<const float4*>(X + (size_t)item * 256 + 4 * lane);
+        const float e[4] = {v.x, v.y, v.z, v.w};
+        const BlockImages im = block_images(e);
+        const int a = lane >> 4, beta = lane & 15;
+        uint8_t* base = timg + (size_t)item * 1024;
+        *reinterpret_cast<u32x2_t*>(base + act_off(1, 0, 0, a, beta, 0)) = __builtin_bit_cast(u32x2_t, im.hi);
+        *reinterpret_cast<u32x2_t*>(base + act_off(1, 0, 0, a, beta, 1)) = __builtin_bit_cast(u32x2_t, im.lo);
+        if (lane == 0) tus[item] = ldexpf(1.0f, -im.sc);
+    }
+}
+
+// The front of a whole routed step: workgroup 0 routes (route_body) and
+// plans (plan_body, with T_sh shared-expert tokens), the others build the
+// per-token X images, which do not depend on the routing.
+template <int J, bool kLds>
+__global__ __launch_bounds__(1024) void k_moe_front(const float* __restrict__ logits, int T, int E, int K, int mode,
+                                                    const float* __restrict__ bias, float routed_scale,
+                                                    int norm_topk, int* __restrict__ eptr, int* __restrict__ tok,
+                                                    float* __restrict__ wt, int* __restrict__ sel,
+                                                    int* __restrict__ asg_e, float* __restrict__ asg_w, int T_sh,
+                                                    MoePlan pl, const float* __restrict__ X, int nb,
+                                                    uint8_t* __restrict__ timg, float* __restrict__ tus) {
+    if (blockIdx.x == 0) {
+        route_body<J, kLds>(logits, T, E, K, mode, bias, routed_scale, norm_topk, eptr, tok, wt, sel, asg_e, asg_w);
+        // the plan reads eptr / tok as the router wrote them
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
+        __syncthreads();
+        plan_body(eptr, tok, T, E, K, T_sh, pl);
+    } else {
+        token_images(X, T, nb, timg, tus, (blockIdx.x - 1) * 16 + (int)(threadIdx.x >> 6), (gridDim.x - 1) * 16,
+                     threadIdx.x & 63);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -468,6 +556,7 @@ __global__ __launch_bounds__(256) void k_prep_grouped(const float* __restrict__ 
 
 struct GroupedArgs {
     const uint8_t* w[2];      // T64 tensors holding every expert's rows
+    const uint8_t* w_sh[2];   // the shared expert's T64 tensors (segments of expert n_exp), or null
     float* y[2];              // [N][rows_per_expert] per tensor, bucket order
     const uint8_t* act;       // per-segment prepared activations
     size_t seg_stride;
@@ -478,17 +567,49 @@ struct GroupedArgs {
     int rows;                 // rows per expert (= output width)
     MoePlan pl;
     int ctr_index;
+    int n_exp;                // expert id of the shared expert's segments
+    // gather mode: activations are per-token images (token_images), read
+    // through the slots' tokens, instead of per-segment images
+    const uint8_t* timg;
+    const float* tus;
 };
+
+// load_record with the activation gathered from per-token images: lane L of
+// pair p reads its 32 bytes from the image set of token 2p + ((L >> 1) & 1)
+// (token 2p for a last pair holding one token) at byte offset toff[p] of
+// timg_b, the images of block b.
+template <int NP>
+__device__ __forceinline__ void load_record_gather(Rec<NP>& r, const uint8_t* rec, const uint8_t* timg_b,
+                                                   const size_t (&toff)[NP], uint32_t lane) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+        r.u[i] = *reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u);
+    r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
+    const uint32_t slot_half = (lane >> 2) * 2 + (lane & 1);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const uint8_t* src = timg_b + toff[p] + slot_half * 32u;
+        const u32x4_t v0 = *reinterpret_cast<const u32x4_t*>(src);
+        const u32x4_t v1 = *reinterpret_cast<const u32x4_t*>(src + 16);
+        r.a[p][0] = u32x2_t{v0.x, v0.y};
+        r.a[p][1] = u32x2_t{v0.z, v0.w};
+        r.a[p][2] = u32x2_t{v1.x, v1.y};
+        r.a[p][3] = u32x2_t{v1.z, v1.w};
+    }
+}
 
 // One (segment, tensor, tile) item: the wavefront walks the tile's nb
 // records through a 2-deep ring and writes the 64 rows x n tokens result.
 // nt consecutive row tiles (records rec0 .. rec0 + nt*nb - 1, tile-major) of
 // one segment: the ring runs on across the tile boundaries; each tile's sums
 // go to y at its end.
-template <int NP>
+// kGather: the activations come from per-token images (timg, tus) through
+// slot_tok[p0 ..], not from the segment's own images at act.
+template <int NP, bool kGather>
 __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, uint32_t lane, const uint8_t* rec0,
                                              const uint8_t* act, int n, int nb, int nt, float* y, int rows,
-                                             int row0) {
+                                             int row0, const uint8_t* timg, const float* tus,
+                                             const int* slot_tok, int p0) {
     constexpr int PF = 2;
     const int nrec = nt * nb;
     const float* xsc = reinterpret_cast<const float*>(act + (size_t)nb * n * 1024);
@@ -497,11 +618,27 @@ __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, ui
     // latency.
     Rec<NP> ring[PF];
     const int tl = min((int)(lane & 7u), n - 1);
+    size_t toff[NP];
+    size_t us_row = 0;
+    if constexpr (kGather) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const bool half = (p == NP - 1) && (n & 1);
+            const int tt = min(2 * p + (half ? 0 : (int)((lane >> 1) & 1u)), n - 1);
+            toff[p] = (size_t)slot_tok[p0 + tt] * nb * 1024;
+        }
+        us_row = (size_t)slot_tok[p0 + tl] * nb;
+    }
     auto fill = [&](Rec<NP>& r, int k) {  // record k of the item (clamped to the last)
         k = min(k, nrec - 1);
         const int b = k % nb;
-        load_record<NP>(r, rec0 + (size_t)k * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
-        r.xs = __builtin_bit_cast(uint32_t, xsc[(size_t)b * n + tl]);
+        if constexpr (kGather) {
+            load_record_gather<NP>(r, rec0 + (size_t)k * kRecordBytes, timg + (size_t)b * 1024, toff, lane);
+            r.xs = __builtin_bit_cast(uint32_t, tus[us_row + b]);
+        } else {
+            load_record<NP>(r, rec0 + (size_t)k * kRecordBytes, act + (size_t)b * n * 1024, lane, n);
+            r.xs = __builtin_bit_cast(uint32_t, xsc[(size_t)b * n + tl]);
+        }
     };
 #pragma unroll
     for (int s = 0; s < PF; ++s) {
@@ -568,16 +705,23 @@ __global__ __launch_bounds__(kGroupedThreads, 2) void k_gemv_grouped(GroupedArgs
         const int rem = item - s * per_seg;
         const int ten = rem / groups, tile = (rem - ten * groups) * g.tiles_per_item;
         const int e = g.pl.seg_e[s], p0 = g.pl.seg_p0[s], n = g.pl.seg_n[s];
-        const uint8_t* rec0 = g.w[ten] + ((size_t)e * g.tiles + tile) * g.nb * kRecordBytes;
+        const uint8_t* rec0 = e == g.n_exp ? g.w_sh[ten] + (size_t)tile * g.nb * kRecordBytes
+                                           : g.w[ten] + ((size_t)e * g.tiles + tile) * g.nb * kRecordBytes;
         const uint8_t* act = g.act + (size_t)s * g.seg_stride;
         float* y = g.y[ten] + (size_t)p0 * g.rows;
         const int nt = g.tiles_per_item;
+#define GPEED_GROUPED_TILE(NP)                                                                                   \
+    (g.timg ? grouped_tile<NP, true>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows, g.timg, \
+                                     g.tus, g.pl.slot_tok, p0)                                                   \
+            : grouped_tile<NP, false>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows,       \
+                                      nullptr, nullptr, nullptr, 0))
         switch ((n + 1) >> 1) {
-            case 1: grouped_tile<1>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
-            case 2: grouped_tile<2>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
-            case 3: grouped_tile<3>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
-            default: grouped_tile<4>(tbl, lb, lane, rec0, act, n, g.nb, nt, y, g.rows, tile * kTileRows); break;
+            case 1: GPEED_GROUPED_TILE(1); break;
+            case 2: GPEED_GROUPED_TILE(2); break;
+            case 3: GPEED_GROUPED_TILE(3); break;
+            default: GPEED_GROUPED_TILE(4); break;
         }
+#undef GPEED_GROUPED_TILE
         uint32_t t = 0;
         if (lane == 0) t = __hip_atomic_fetch_add(g.pl.ctr + g.ctr_index, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         item = n_waves + __builtin_amdgcn_readfirstlane(__shfl(t, 0));
@@ -587,9 +731,13 @@ __global__ __launch_bounds__(kGroupedThreads, 2) void k_gemv_grouped(GroupedArgs
 // ---------------------------------------------------------------------------
 // Weighted combine (model_batch.cpp:257-261): Y[t] = sum_k wt * D[slot],
 // slots in expert order, one fma per term.
+// With the shared expert (sh: its down rows, one per token; model_batch.cpp:
+// 264-280), Y[t] = that sum + sh[t] (add_f32), unless the plan rejected
+// the buckets (n_seg 0).
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ D, const float* __restrict__ wt,
                                                      const int* __restrict__ pos, int T, int K, int H,
-                                                     float* __restrict__ Y) {
+                                                     float* __restrict__ Y, const float* __restrict__ sh,
+                                                     const int* __restrict__ n_seg) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     const size_t n4 = (size_t)T * H / 4;
     if (i >= n4) return;
@@ -606,36 +754,58 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ D
         y.z = fmaf(w, d.z, y.z);
         y.w = fmaf(w, d.w, y.w);
     }
+    if (sh && *n_seg > 0) {
+        const float4 d = *reinterpret_cast<const float4*>(sh + (size_t)t * H + h);
+        y.x = y.x + d.x;
+        y.y = y.y + d.y;
+        y.z = y.z + d.z;
+        y.w = y.w + d.w;
+    }
     *reinterpret_cast<float4*>(Y + (size_t)t * H + h) = y;
 }
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 struct MoeLayout {
-    size_t plan_off[8];
+    size_t plan_off[9];
     size_t act1, g, u, act2, d, total;
+    size_t eptr, tok, wt, sel, asg_e, asg_w, timg, tus;  // the whole-step path only
     size_t stride1, stride2;
     int seg_max;
 };
 
-MoeLayout moe_layout(int T, int E, int K, int H, int I) {
+// T_sh: shared-expert tokens (0 or T). fused: the whole step from the
+// logits (router outputs, router scratch and per-token X images in the
+// workspace, no per-segment X images).
+MoeLayout moe_layout(int T, int E, int K, int H, int I, int T_sh = 0, bool fused = false) {
     MoeLayout L{};
-    const size_t N = (size_t)T * K;
-    L.seg_max = (int)((N + (size_t)(kSegTok - 1) * E) / kSegTok + 1);
+    const size_t N = (size_t)T * K, NS = N + (size_t)T_sh;
+    L.seg_max = (int)((N + (size_t)(kSegTok - 1) * E) / kSegTok + 1) + (T_sh + kSegTok - 1) / kSegTok;
     size_t off = kWsHeader;
-    const size_t sizes[8] = {256, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max,
-                             4 * N, 4 * N, 4 * N, 256};
-    for (int i = 0; i < 8; ++i) {
+    const size_t sizes[9] = {256, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max,
+                             4 * NS, 4 * NS, 4 * N, 256, 4 * NS};
+    for (int i = 0; i < 9; ++i) {
         L.plan_off[i] = off;
         off += align256(sizes[i]);
     }
     L.stride1 = align256((size_t)(H / kQK) * kSegTok * (1024 + 4));
     L.stride2 = align256((size_t)(I / kQK) * kSegTok * (1024 + 4));
-    L.act1 = off; off += L.stride1 * L.seg_max;
-    L.g = off; off += align256(N * I * 4);
-    L.u = off; off += align256(N * I * 4);
+    if (fused) {
+        L.eptr = off; off += align256(4 * ((size_t)E + 1));
+        L.tok = off; off += align256(4 * N);
+        L.wt = off; off += align256(4 * N);
+        L.sel = off; off += align256(4 * N);
+        L.asg_e = off; off += align256(4 * N);
+        L.asg_w = off; off += align256(4 * N);
+        L.timg = off; off += (size_t)T * (H / kQK) * 1024;
+        L.tus = off; off += align256((size_t)T * (H / kQK) * 4);
+    } else {
+        L.act1 = off; off += L.stride1 * L.seg_max;
+    }
+    L.g = off; off += align256(NS * I * 4);
+    L.u = off; off += align256(NS * I * 4);
     L.act2 = off; off += L.stride2 * L.seg_max;
-    L.d = off; off += align256(N * H * 4);
+    L.d = off; off += align256(NS * H * 4);
     L.total = off;
     return L;
 }
@@ -644,6 +814,8 @@ MoePlan plan_ptrs(uint8_t* ws, const MoeLayout& L) {
     MoePlan p;
     p.n_seg = reinterpret_cast<int*>(ws + L.plan_off[0]);
     p.n_valid = p.n_seg + 1;
+    p.n_sh_seg = p.n_seg + 2;
+    p.slot_tok = reinterpret_cast<int*>(ws + L.plan_off[8]);
     p.err = reinterpret_cast<uint32_t*>(ws);
     p.ctr = reinterpret_cast<uint32_t*>(ws + L.plan_off[7]);
     p.seg_e = reinterpret_cast<int*>(ws + L.plan_off[1]);
@@ -692,7 +864,7 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_prep_grouped<0>, dim3((N * nbH + 3) / 4), dim3(256), 0, s, X, nullptr, tok, eptr, E,
-                       nbH, 0.0f, pl, ws + L.act1, L.stride1);
+                       nbH, 0.0f, pl, ws + L.act1, L.stride1, 0);
     const int grid = (num_cus > 0 ? num_cus : 256) * 2;
     GroupedArgs ga{};
     ga.w[0] = w_gate;
@@ -708,10 +880,11 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     ga.rows = I;
     ga.pl = pl;
     ga.ctr_index = 0;
+    ga.n_exp = E;
     e = launch_timed(kProfGrouped, k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, ga);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_prep_grouped<1>, dim3((N * nbI + 3) / 4), dim3(256), 0, s, G, U, tok, eptr, E, nbI,
-                       lim, pl, ws + L.act2, L.stride2);
+                       lim, pl, ws + L.act2, L.stride2, 0);
     GroupedArgs gd = ga;
     gd.w[0] = w_down;
     gd.w[1] = w_down;
@@ -733,7 +906,99 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     if (e != hipSuccess) return e;
     const size_t n4 = (size_t)T * H / 4;
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, D, wt, pl.pos, T, K, H,
-                       Y);
+                       Y, nullptr, pl.n_seg);
+    return hipGetLastError();
+}
+
+size_t moe_batch_ws_bytes(int T, int E, int K, int H, int I, int shared) {
+    return moe_layout(T, E, K, H, I, shared ? T : 0, true).total;
+}
+
+hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, const float* bias,
+                            float routed_scale, int norm_topk, const uint8_t* w_gate, const uint8_t* w_up,
+                            const uint8_t* w_down, const uint8_t* w_gate_sh, const uint8_t* w_up_sh,
+                            const uint8_t* w_down_sh, int H, int I, const float* X, float lim, float* Y,
+                            int* eptr_out, int* tok_out, float* wt_out, uint8_t* ws, int num_cus, hipStream_t s) {
+    const int T_sh = w_gate_sh ? T : 0;
+    const MoeLayout L = moe_layout(T, E, K, H, I, T_sh, true);
+    const MoePlan pl = plan_ptrs(ws, L);
+    const int N = T * K, NS = N + T_sh;
+    const int nbH = H / kQK, nbI = I / kQK;
+    int* eptr = eptr_out ? eptr_out : reinterpret_cast<int*>(ws + L.eptr);
+    int* tok = tok_out ? tok_out : reinterpret_cast<int*>(ws + L.tok);
+    float* wt = wt_out ? wt_out : reinterpret_cast<float*>(ws + L.wt);
+    float* G = reinterpret_cast<float*>(ws + L.g);
+    float* U = reinterpret_cast<float*>(ws + L.u);
+    float* D = reinterpret_cast<float*>(ws + L.d);
+    uint8_t* timg = ws + L.timg;
+    float* tus = reinterpret_cast<float*>(ws + L.tus);
+    // 1. router + bucket sort + work plan (workgroup 0) and the per-token X
+    // images (the other workgroups)
+    const int prep_groups = std::min((T * nbH + 15) / 16, 255);
+    auto front = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(1 + prep_groups), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale,
+                           norm_topk, eptr, tok, wt, reinterpret_cast<int*>(ws + L.sel),
+                           reinterpret_cast<int*>(ws + L.asg_e), reinterpret_cast<float*>(ws + L.asg_w), T_sh, pl, X,
+                           nbH, timg, tus);
+    };
+    const bool lds = (long long)T * K <= kRouteLdsAsg;
+    if (E <= 64) lds ? front(k_moe_front<1, true>) : front(k_moe_front<1, false>);
+    else if (E <= 128) lds ? front(k_moe_front<2, true>) : front(k_moe_front<2, false>);
+    else if (E <= 256) lds ? front(k_moe_front<4, true>) : front(k_moe_front<4, false>);
+    else lds ? front(k_moe_front<kMaxExperts / 64, true>) : front(k_moe_front<kMaxExperts / 64, false>);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // 2. gate / up of every segment (the shared expert's first)
+    const int grid = (num_cus > 0 ? num_cus : 256) * 2;
+    GroupedArgs ga{};
+    ga.w[0] = w_gate;
+    ga.w[1] = w_up;
+    ga.w_sh[0] = w_gate_sh;
+    ga.w_sh[1] = w_up_sh;
+    ga.y[0] = G;
+    ga.y[1] = U;
+    ga.act = nullptr;
+    ga.timg = timg;
+    ga.tus = tus;
+    ga.n_tensors = 2;
+    ga.nb = nbH;
+    ga.tiles = I / kTileRows;
+    ga.tiles_per_item = 1;
+    ga.rows = I;
+    ga.pl = pl;
+    ga.ctr_index = 0;
+    ga.n_exp = E;
+    e = launch_timed(kProfGrouped, k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, ga);
+    if (e != hipSuccess) return e;
+    // 3. SwiGLU images per slot
+    hipLaunchKernelGGL(k_prep_grouped<1>, dim3((NS * nbI + 3) / 4), dim3(256), 0, s, G, U, tok, eptr, E, nbI, lim,
+                       pl, ws + L.act2, L.stride2, T_sh);
+    // 4. down
+    GroupedArgs gd = ga;
+    gd.w[0] = w_down;
+    gd.w[1] = w_down;
+    gd.w_sh[0] = w_down_sh;
+    gd.w_sh[1] = w_down_sh;
+    gd.y[0] = D;
+    gd.y[1] = D;
+    gd.act = ws + L.act2;
+    gd.seg_stride = L.stride2;
+    gd.timg = nullptr;
+    gd.tus = nullptr;
+    gd.n_tensors = 1;
+    gd.nb = nbI;
+    gd.tiles = H / kTileRows;
+    gd.tiles_per_item = 1;
+    while (gd.tiles_per_item < 4 && gd.tiles % (2 * gd.tiles_per_item) == 0 && gd.nb * gd.tiles_per_item < 16)
+        gd.tiles_per_item *= 2;
+    gd.rows = H;
+    gd.ctr_index = 1;
+    e = launch_timed(kProfGrouped, k_gemv_grouped, dim3(grid), dim3(kGroupedThreads), 0, s, gd);
+    if (e != hipSuccess) return e;
+    // 5. weighted combine in expert order, then the shared expert's rows
+    const size_t n4 = (size_t)T * H / 4;
+    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, D, wt, pl.pos, T, K, H,
+                       Y, T_sh ? D + (size_t)N * H : nullptr, pl.n_seg);
     return hipGetLastError();
 }
 

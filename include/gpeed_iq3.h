@@ -368,6 +368,27 @@ int gpeed_iq3xxs_moe_experts(const void* w_gate, const void* w_up, const void* w
                              const float* wt, float swiglu_limit, float* Y, void* ws, size_t ws_bytes,
                              gpeed_stream_t stream);
 
+/* The whole routed-expert step of Model::moe_batch from the router logits
+ * (model_batch.cpp:174-280, steps 2-4; step 1's router product is a
+ * matvec / matmul of ffn_gate_inp): the router and bucket sort of
+ * gpeed_moe_route (mode, bias, routed_scale, norm_topk as there), the routed
+ * experts of gpeed_iq3xxs_moe_experts, and, when w_gate_sh / w_up_sh /
+ * w_down_sh are given (T64 copies of ffn_gate_shexp / ffn_up_shexp [inter,
+ * hidden] and ffn_down_shexp [hidden, inter]; all three NULL for none), the
+ * shared expert over every token, added last (add_f32,
+ * model_batch.cpp:264-280): Y[t] = (sum over the token's experts, in expert
+ * order, of wt * down) + shared[t]. Five launches. eptr / tok / wt
+ * (optional device outputs, may be NULL) receive the routing as
+ * gpeed_moe_route makes it. Limits as gpeed_moe_route and
+ * gpeed_iq3xxs_moe_experts. ws: gpeed_iq3xxs_moe_batch_ws_bytes(...,
+ * shared = 1 with a shared expert) bytes, initialised once for its header. */
+size_t gpeed_iq3xxs_moe_batch_ws_bytes(int n_tok, int n_exp, int top_k, int hidden, int inter, int shared);
+int gpeed_iq3xxs_moe_batch(const float* logits, int n_tok, int n_exp, int top_k, int mode, const float* bias,
+                           float routed_scale, int norm_topk, const void* w_gate, const void* w_up,
+                           const void* w_down, const void* w_gate_sh, const void* w_up_sh, const void* w_down_sh,
+                           int hidden, int inter, const float* X, float swiglu_limit, float* Y, int* eptr, int* tok,
+                           float* wt, void* ws, size_t ws_bytes, gpeed_stream_t stream);
+
 /* Checks expert buckets held in HOST memory against the invariants above
  * (what the reference's bucket sort, model_batch.cpp:205-219, produces):
  * GPEED_OK, or GPEED_ERR_INVALID with the first violation in

@@ -70,6 +70,12 @@ def lib():
                                       C.c_int, _i32p, _i32p, _f32p, C.c_float, _f32p]
         L.orc_dense_mlp.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, _f32p, C.c_int,
                                     C.c_float, _f32p]
+        L.orc_moe_forward.argtypes = [_f32p, C.c_int, C.c_int, C.c_void_p, C.c_float, C.c_int, C.c_void_p,
+                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                      _f32p, C.c_float, _f32p]
+        L.orc_moe_batch.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_float, C.c_int,
+                                    C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.c_int, C.c_int, _f32p, C.c_float, _f32p]
         _lib = L
     return _lib
 
@@ -163,6 +169,38 @@ def moe_experts(w_gate, w_up, w_down, hidden, inter, X, eptr, tok, wt, swiglu_li
     if rc != 0:
         raise RuntimeError(f"orc_moe_experts rc={rc}")
     return Y
+
+
+def moe_batch(logits, X, w_gate, w_up, w_down, hidden, inter, top_k, mode=0, bias=None, routed_scale=1.0,
+              norm_topk=True, swiglu_limit=10.0, shared=None):
+    """model_batch.cpp:165-281 from the logits; shared = (gate, up, down) GGUF payloads or None."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    X = np.ascontiguousarray(X, np.float32)
+    T, E = logits.shape
+    Y = np.empty((T, hidden), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    sh = (None, None, None) if shared is None else tuple(_ptr(np.ascontiguousarray(a)) for a in shared)
+    rc = lib().orc_moe_batch(logits, T, E, top_k, mode, None if b is None else _ptr(b), routed_scale,
+                             int(norm_topk), _ptr(w_gate), _ptr(w_up), _ptr(w_down), *sh, hidden, inter, X,
+                             swiglu_limit, Y)
+    if rc != 0:
+        raise RuntimeError(f"orc_moe_batch rc={rc}")
+    return Y
+
+
+def moe_forward(logits, x, w_gate, w_up, w_down, hidden, inter, top_k, bias=None, routed_scale=1.0,
+                norm_topk=True, swiglu_limit=10.0, shared=None):
+    """model.cpp:692-755 for one token (rank-order combine); shared = (gate, up, down) or None."""
+    logits = np.ascontiguousarray(logits, np.float32).reshape(-1)
+    y = np.empty(hidden, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    sh = (None, None, None) if shared is None else tuple(_ptr(np.ascontiguousarray(a)) for a in shared)
+    rc = lib().orc_moe_forward(logits, logits.size, top_k, None if b is None else _ptr(b), routed_scale,
+                               int(norm_topk), _ptr(w_gate), _ptr(w_up), _ptr(w_down), *sh, hidden, inter,
+                               np.ascontiguousarray(x, np.float32).reshape(-1), swiglu_limit, y)
+    if rc != 0:
+        raise RuntimeError(f"orc_moe_forward rc={rc}")
+    return y
 
 
 def dense_mlp(w_gate, w_up, w_down, hidden, inter, X, swiglu_limit=10.0):

@@ -342,3 +342,84 @@ int orc_dense_mlp(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_d
     free(U);
     return rc;
 }
+
+/* model_batch.cpp:165-281 (moe_batch) from the router logits: router and
+ * bucket sort (orc_moe_route), routed experts (orc_moe_experts), and, when
+ * the shared-expert tensors are given (non-NULL), the shared expert over
+ * every token (the dense FFN of orc_dense_mlp, model_batch.cpp:264-279)
+ * added last with add_f32 (simd.h:53-62: a[i] += b[i]). */
+int orc_moe_batch(const float* logits, int n_tok, int n_exp, int top_k, int mode, const float* bias,
+                  float routed_scale, int norm_topk, const uint8_t* w_gate, const uint8_t* w_up,
+                  const uint8_t* w_down, const uint8_t* w_gate_sh, const uint8_t* w_up_sh,
+                  const uint8_t* w_down_sh, int hidden, int inter, const float* X, float swiglu_limit, float* Y) {
+    const size_t N = (size_t)n_tok * top_k;
+    int* eptr = (int*)malloc(sizeof(int) * ((size_t)n_exp + 1));
+    int* tok = (int*)malloc(sizeof(int) * (N ? N : 1));
+    float* wt = (float*)malloc(sizeof(float) * (N ? N : 1));
+    int rc = orc_moe_route(logits, n_tok, n_exp, top_k, mode, bias, routed_scale, norm_topk, eptr, tok, wt, NULL);
+    if (rc == ORC_OK)
+        rc = orc_moe_experts(w_gate, w_up, w_down, hidden, inter, X, n_tok, n_exp, eptr, tok, wt, swiglu_limit, Y);
+    if (rc == ORC_OK && w_gate_sh) {
+        float* sd = (float*)malloc(sizeof(float) * (size_t)n_tok * hidden);
+        rc = orc_dense_mlp(w_gate_sh, w_up_sh, w_down_sh, hidden, inter, X, n_tok, swiglu_limit, sd);
+        for (size_t i = 0; i < (size_t)n_tok * hidden; ++i) Y[i] += sd[i];
+        free(sd);
+    }
+    free(eptr);
+    free(tok);
+    free(wt);
+    return rc;
+}
+
+/* model.cpp:692-755 (moe_forward, one token): sigmoid scores ranked by score
+ * + bias (the selection of orc_moe_route, mode 0), weights
+ * (score / denom) * routed_scale (each step rounded, :715-724; without
+ * norm_topk score * routed_scale), the experts in rank order, each
+ * axpy_f32 into the output, then the shared expert (shared tensors
+ * non-NULL) with add_f32. */
+int orc_moe_forward(const float* logits, int n_exp, int top_k, const float* bias, float routed_scale,
+                    int norm_topk, const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down,
+                    const uint8_t* w_gate_sh, const uint8_t* w_up_sh, const uint8_t* w_down_sh, int hidden,
+                    int inter, const float* x, float swiglu_limit, float* y) {
+    const int H = hidden, I = inter;
+    if (top_k <= 0 || top_k > n_exp || n_exp > 1024) return ORC_ERR_UNIMPLEMENTED;
+    int sel[32];
+    float score[1024];
+    if (top_k > 32) return ORC_ERR_UNIMPLEMENTED;
+    int eptr[1025], tok[32];
+    float wt[32];
+    int rc = orc_moe_route(logits, 1, n_exp, top_k, 0, bias, routed_scale, norm_topk, eptr, tok, wt, sel);
+    if (rc) return rc;
+    for (int e = 0; e < n_exp; ++e) score[e] = 1.0f / (1.0f + expf(-logits[e]));
+    float wsum[32], denom = 1e-20f;
+    for (int k = 0; k < top_k; ++k) {
+        wsum[k] = score[sel[k]];
+        denom += wsum[k];
+    }
+    if (norm_topk)
+        for (int k = 0; k < top_k; ++k) wsum[k] /= denom;
+    for (int k = 0; k < top_k; ++k) wsum[k] *= routed_scale;
+    float* g = (float*)malloc(sizeof(float) * (size_t)I);
+    float* u = (float*)malloc(sizeof(float) * (size_t)I);
+    float* d = (float*)malloc(sizeof(float) * (size_t)H);
+    memset(y, 0, sizeof(float) * (size_t)H);
+    for (int k = 0; k < top_k && rc == ORC_OK; ++k) {
+        const int e = sel[k];
+        rc |= orc_matvec_quant(w_gate, (uint64_t)e * I, H, I, x, g);
+        rc |= orc_matvec_quant(w_up, (uint64_t)e * I, H, I, x, u);
+        for (int i = 0; i < I; ++i) g[i] = swiglu1(g[i], u[i], swiglu_limit);
+        rc |= orc_matvec_quant(w_down, (uint64_t)e * H, I, H, g, d);
+        orc_axpy_f32(y, d, wsum[k], H);
+    }
+    if (rc == ORC_OK && w_gate_sh) {
+        rc |= orc_matvec_quant(w_gate_sh, 0, H, I, x, g);
+        rc |= orc_matvec_quant(w_up_sh, 0, H, I, x, u);
+        for (int i = 0; i < I; ++i) g[i] = swiglu1(g[i], u[i], swiglu_limit);
+        rc |= orc_matvec_quant(w_down_sh, 0, I, H, g, d);
+        for (int i = 0; i < H; ++i) y[i] += d[i];
+    }
+    free(g);
+    free(u);
+    free(d);
+    return rc;
+}

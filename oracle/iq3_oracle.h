@@ -22,6 +22,11 @@
  *   orc_moe_route        brute-force re-derivation of top-k + integer
  *                        invariants of the stable bucket sort
  *   orc_moe_experts      vs an fp64 dense restatement of each expert FFN
+ *   orc_moe_forward      one token, rank-order combine: vs an fp64
+ *                        restatement, and vs orc_moe_batch at one token
+ *   orc_moe_batch        route + experts + the shared expert: vs an fp64
+ *                        dense restatement of the whole step (every expert
+ *                        and the shared FFN)
  *   orc_dequant_block    (Q8_0, Q2_K, Q3_K, Q6_K, IQ2_S, IQ3_S, IQ4_XS)
  *                        bitwise vs oracle/_ref over random blocks and blocks
  *                        of special values, codebooks vs the reference
@@ -97,6 +102,14 @@ int orc_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w
 int orc_dense_mlp(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down,
                   int hidden, int inter, const float* X, int n_tok, float swiglu_limit,
                   float* Y);
+int orc_moe_forward(const float* logits, int n_exp, int top_k, const float* bias, float routed_scale,
+                    int norm_topk, const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down,
+                    const uint8_t* w_gate_sh, const uint8_t* w_up_sh, const uint8_t* w_down_sh, int hidden,
+                    int inter, const float* x, float swiglu_limit, float* y);
+int orc_moe_batch(const float* logits, int n_tok, int n_exp, int top_k, int mode, const float* bias,
+                  float routed_scale, int norm_topk, const uint8_t* w_gate, const uint8_t* w_up,
+                  const uint8_t* w_down, const uint8_t* w_gate_sh, const uint8_t* w_up_sh,
+                  const uint8_t* w_down_sh, int hidden, int inter, const float* X, float swiglu_limit, float* Y);
 
 #ifdef __cplusplus
 }

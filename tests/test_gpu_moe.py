@@ -30,16 +30,21 @@ def host(t):
 @pytest.mark.parametrize("T,E,K,mode", [
     (32, 64, 8, 1),      # the routed-expert decode batch: softmax top-8 of 64
     (32, 64, 8, 0),      # reference router: sigmoid + bias, routed_scale 2.5
+    (32, 64, 8, 2),      # the same without norm_topk (weights score * routed_scale)
     (300, 256, 8, 0),    # 2400 assignments: the scatter runs in three chunks
     (7, 100, 1, 1),      # experts not a multiple of 64, top-1
     (5, 1024, 32, 1),    # widest router
 ])
 def test_route_matches_oracle(gpu, T, E, K, mode):
+    # mode 2 here: the reference router (mode 0) with norm_topk off
+    norm = mode != 2
+    mode = 0 if mode == 2 else mode
     logits = synth.normal(70, T * 1000 + E, T * E).reshape(T, E)
     bias = synth.normal(71, E, E) * np.float32(0.05) if mode == 0 else None
     eptr, tok, wt, sel = G.moe_route(dev(logits, gpu), K, mode, None if bias is None else dev(bias, gpu),
-                                     routed_scale=2.5 if mode == 0 else 1.0)
-    r_eptr, r_tok, r_wt, r_sel = oracle.moe_route(logits, K, mode, bias=bias, routed_scale=2.5 if mode == 0 else 1.0)
+                                     routed_scale=2.5 if mode == 0 else 1.0, norm_topk=norm)
+    r_eptr, r_tok, r_wt, r_sel = oracle.moe_route(logits, K, mode, bias=bias, routed_scale=2.5 if mode == 0 else 1.0,
+                                                  norm_topk=norm)
     assert np.array_equal(host(eptr), r_eptr)
     assert np.array_equal(host(tok), r_tok)
     assert np.array_equal(host(sel), r_sel)
@@ -138,3 +143,89 @@ def test_moe_errors(gpu):
     with pytest.raises(G.GpeedError) as e:
         G.moe_route(logits, 2, 3)
     assert e.value.code == -1
+
+
+# ------------------------------------------------------------------ the whole step (moe_batch)
+
+def batch_case(gpu, seed, T, E, K, H, I, mode, shared, norm=True):
+    wg = synth.iq3xxs_matrix(seed, 0, E * I, H)
+    wu = synth.iq3xxs_matrix(seed, 1, E * I, H)
+    wd = synth.iq3xxs_matrix(seed, 2, E * H, I)
+    sh = tuple(synth.iq3xxs_matrix(seed, 5 + i, r, c) for i, (r, c) in enumerate(((I, H), (I, H), (H, I)))) \
+        if shared else None
+    X = synth.normal(seed, 3, T * H).reshape(T, H)
+    logits = synth.normal(seed, 4, T * E).reshape(T, E)
+    bias = synth.normal(seed, 8, E) * np.float32(0.05) if mode == 0 else None
+    scale = 2.5 if mode == 0 else 1.0
+    t = lambda a, r, c: G.tile(dev(a.reshape(-1), gpu), r, c)  # noqa: E731
+    tg, tu, td = t(wg, E * I, H), t(wu, E * I, H), t(wd, E * H, I)
+    tsh = (t(sh[0], I, H), t(sh[1], I, H), t(sh[2], H, I)) if shared else None
+    Y, eptr, tok, wt = G.moe_batch(dev(logits, gpu), dev(X, gpu), tg, tu, td, E, H, I, K, mode,
+                                   None if bias is None else dev(bias, gpu), scale, norm, 10.0, shared=tsh,
+                                   routing=True)
+    ref = oracle.moe_batch(logits, X, wg, wu, wd, H, I, K, mode, bias, scale, norm, 10.0, shared=sh)
+    r_eptr, r_tok, r_wt, _ = oracle.moe_route(logits, K, mode, bias=bias, routed_scale=scale, norm_topk=norm)
+    assert np.array_equal(host(eptr), r_eptr) and np.array_equal(host(tok), r_tok)
+    np.testing.assert_allclose(host(wt), r_wt, rtol=1e-6, atol=0)
+    return host(Y), ref, (tg, tu, td, X, eptr, tok, wt, logits, bias, sh, wg, wu, wd)
+
+
+@pytest.mark.parametrize("T,E,K,H,I,mode,shared,norm", [
+    (5, 8, 2, 512, 256, 0, True, True),
+    (32, 16, 4, 1024, 512, 0, True, False),   # reference router without norm_topk
+    (3, 4, 4, 768, 1280, 1, False, True),      # no shared expert
+    (17, 8, 3, 512, 512, 1, True, True),       # shared expert over 17 tokens: three segments, the last of one
+])
+def test_moe_batch_matches_oracle(gpu, T, E, K, H, I, mode, shared, norm):
+    Y, ref, _ = batch_case(gpu, 80, T, E, K, H, I, mode, shared, norm)
+    e = max(rel_err(Y[t], ref[t]) for t in range(T))
+    assert e < TIGHT, e
+
+
+def test_moe_batch_decode_batch_full_size(gpu):
+    """The routed-expert decode batch (64 experts of gate/up 2048x6144 and
+    down 6144x2048, 32 tokens, top-8 softmax routing) with a shared expert of
+    the same shape, from the logits in five launches."""
+    Y, ref, _ = batch_case(gpu, 81, 32, 64, 8, 6144, 2048, 1, True)
+    e = max(rel_err(Y[t], ref[t]) for t in range(32))
+    assert e < TIGHT, e
+
+
+def test_moe_batch_routed_part_equals_moe_experts(gpu):
+    """Without the shared expert, the whole step (activations gathered from
+    per-token images) gives bit for bit what moe_route + moe_experts give
+    (per-segment images)."""
+    T, E, K, H, I = 20, 8, 3, 512, 512
+    Y, _, (tg, tu, td, X, eptr, tok, wt, logits, bias, _, _, _, _) = batch_case(gpu, 82, T, E, K, H, I, 1, False)
+    Y2 = host(G.moe_experts(tg, tu, td, E, H, I, dev(X, gpu), K, eptr, tok, wt, 10.0))
+    assert np.array_equal(Y.view(np.uint32), Y2.view(np.uint32))
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_moe_batch_one_token_vs_moe_forward(gpu, norm):
+    """One token (model.cpp:692-755): the reference's rank-order combine with
+    (score / denom) * routed_scale, and the shared expert."""
+    H, I, E, K = 1024, 512, 64, 8
+    Y, _, (tg, tu, td, X, eptr, tok, wt, logits, bias, sh, wg, wu, wd) = batch_case(gpu, 83, 1, E, K, H, I, 0, True,
+                                                                                     norm)
+    ref = oracle.moe_forward(logits[0], X[0], wg, wu, wd, H, I, K, bias, 2.5, norm, 10.0, shared=sh)
+    assert rel_err(Y[0], ref) < TIGHT
+
+
+def test_moe_batch_errors(gpu):
+    import torch
+
+    T, E, K, H, I = 2, 4, 2, 256, 256
+    w = G.tile(dev(synth.iq3xxs_matrix(84, 0, E * I, H).reshape(-1), gpu), E * I, H)
+    X = torch.zeros(T, H, device=gpu)
+    lg = torch.zeros(T, E, device=gpu)
+    with pytest.raises(G.GpeedError) as e:  # only part of the shared expert
+        G.moe_batch(lg, X, w, w, w, E, H, I, K, shared=(w, w, None))
+    assert e.value.code == -1
+    with pytest.raises(G.GpeedError) as e:
+        G.moe_batch(lg, X, w, w, w, E, H, I, K, mode=3)
+    assert e.value.code == -1
+    ws = torch.zeros(256, dtype=torch.uint8, device=gpu)
+    with pytest.raises(G.GpeedError) as e:
+        G.moe_batch(lg, X, w, w, w, E, H, I, K, ws=ws)
+    assert e.value.code == -7

@@ -278,6 +278,80 @@ def test_route_ties_prefer_lower_expert():
     assert list(sel[1]) == [3, 9, 0, 1]
 
 
+def test_moe_batch_with_shared_expert_fp64():
+    """The whole moe_batch step (model_batch.cpp:165-281) with the reference
+    router (mode 0: sigmoid, bias, routed_scale, norm_topk) and the shared
+    expert added last, against an fp64 restatement of every piece: top-k of
+    sigmoid(logit) + bias, weights score * scale / (1e-20 + sum), each expert
+    FFN and the shared FFN over every token."""
+    H, I, E, T, K = 512, 256, 8, 6, 3
+    wg = synth.iq3xxs_matrix(32, 0, E * I, H)
+    wu = synth.iq3xxs_matrix(32, 1, E * I, H)
+    wd = synth.iq3xxs_matrix(32, 2, E * H, I)
+    sg = synth.iq3xxs_matrix(32, 3, I, H)
+    su = synth.iq3xxs_matrix(32, 4, I, H)
+    sd = synth.iq3xxs_matrix(32, 5, H, I)
+    X = synth.normal(32, 10, T * H).reshape(T, H)
+    logits = synth.normal(32, 11, T * E).reshape(T, E)
+    bias = synth.normal(32, 12, E) * 0.1
+    scale = 2.5
+    Y = oracle.moe_batch(logits, X, wg, wu, wd, H, I, K, 0, bias, scale, True, 10.0, shared=(sg, su, sd))
+    deq = lambda w, r, c: oracle.dequantize(w, r * c).reshape(r, c).astype(np.float64)  # noqa: E731
+    G, U, D = deq(wg, E * I, H).reshape(E, I, H), deq(wu, E * I, H).reshape(E, I, H), deq(wd, E * H, I).reshape(E, H, I)
+    SG, SU, SD = deq(sg, I, H), deq(su, I, H), deq(sd, H, I)
+
+    def ffn(g_m, u_m, d_m, x):
+        g = np.minimum(g_m @ x, 10.0)
+        u = np.clip(u_m @ x, -10.0, 10.0)
+        return d_m @ (g / (1.0 + np.exp(-g)) * u)
+
+    want = np.zeros((T, H))
+    for t in range(T):
+        s_e = 1.0 / (1.0 + np.exp(-logits[t].astype(np.float64)))
+        top = np.argsort(-(s_e + bias), kind="stable")[:K]
+        denom = 1e-20 + s_e[top].sum()
+        for e in sorted(top):
+            want[t] += s_e[e] * scale / denom * ffn(G[e], U[e], D[e], X[t])
+        want[t] += ffn(SG, SU, SD, X[t])
+    assert rel_err(Y, want) < 1e-5
+    # without the shared expert it is the routed part alone
+    Y0 = oracle.moe_batch(logits, X, wg, wu, wd, H, I, K, 0, bias, scale, True, 10.0)
+    shared = np.stack([ffn(SG, SU, SD, X[t]) for t in range(T)])
+    assert rel_err(Y0, want - shared) < 1e-5
+
+
+def test_moe_forward_one_token_fp64():
+    """moe_forward (model.cpp:692-755): the rank-order combine with
+    (score / denom) * routed_scale, against fp64, and against the batched
+    step at one token (same value, other rounding order)."""
+    H, I, E, K = 512, 256, 16, 4
+    wg = synth.iq3xxs_matrix(33, 0, E * I, H)
+    wu = synth.iq3xxs_matrix(33, 1, E * I, H)
+    wd = synth.iq3xxs_matrix(33, 2, E * H, I)
+    sh = tuple(synth.iq3xxs_matrix(33, 3 + i, r, c) for i, (r, c) in enumerate(((I, H), (I, H), (H, I))))
+    x = synth.normal(33, 10, H)
+    logits = synth.normal(33, 11, E)
+    bias = synth.normal(33, 12, E) * 0.1
+    for norm in (True, False):
+        y = oracle.moe_forward(logits, x, wg, wu, wd, H, I, K, bias, 2.5, norm, 10.0, shared=sh)
+        deq = lambda w, r, c: oracle.dequantize(w, r * c).reshape(r, c).astype(np.float64)  # noqa: E731
+        G, U, D = deq(wg, E * I, H).reshape(E, I, H), deq(wu, E * I, H).reshape(E, I, H), deq(wd, E * H, I).reshape(E, H, I)
+
+        def ffn(g_m, u_m, d_m):
+            g = np.minimum(g_m @ x, 10.0)
+            u = np.clip(u_m @ x, -10.0, 10.0)
+            return d_m @ (g / (1.0 + np.exp(-g)) * u)
+
+        s_e = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+        top = np.argsort(-(s_e + bias), kind="stable")[:K]
+        w = s_e[top] * 2.5 / ((1e-20 + s_e[top].sum()) if norm else 1.0)
+        want = sum(w[k] * ffn(G[e], U[e], D[e]) for k, e in enumerate(top)) + ffn(deq(sh[0], I, H), deq(sh[1], I, H),
+                                                                                 deq(sh[2], H, I))
+        assert rel_err(y, want) < 1e-5
+        yb = oracle.moe_batch(logits[None], x[None], wg, wu, wd, H, I, K, 0, bias, 2.5, norm, 10.0, shared=sh)[0]
+        assert rel_err(y, yb) < 1e-6
+
+
 def test_moe_experts_fp64():
     H, I, E, T, K = 512, 256, 6, 5, 2
     wg = synth.iq3xxs_matrix(31, 0, E * I, H)
