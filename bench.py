@@ -231,6 +231,51 @@ def moe_decode(torch, G, synth, dev, steps, warmup_s):
     gu_bytes = touched * 2 * blk_bytes + n_asg * (HM // 256) * 1028 + 2 * n_asg * IM * 4
     dn_bytes = touched * blk_bytes + n_asg * (IM // 256) * 1028 + n_asg * HM * 4
     k_ms = float(gu.mean() + dn.mean())
+
+    # the whole step from the logits with a shared expert of the same shape
+    # (gpeed_iq3xxs_moe_batch: five launches)
+    sh = []
+    for i, (r, c) in enumerate(((IM, HM), (IM, HM), (HM, IM))):
+        raw = torch.from_numpy(synth.iq3xxs_matrix(2025, 20 + i, r, c).reshape(-1)).to(dev)
+        sh.append(G.tile(raw, r, c))
+        del raw
+    ws_b = G.moe_batch_workspace(T, E, K, HM, IM, True, dev)
+    nul = ctypes.c_void_p(0)
+    batch_args = (vp(logits), T, E, K, 1, nul, ctypes.c_float(1.0), 1, vp(tens[0]), vp(tens[1]), vp(tens[2]),
+                  vp(sh[0]), vp(sh[1]), vp(sh[2]), HM, IM, vp(X), ctypes.c_float(SWIGLU_LIMIT), vp(Y), nul, nul,
+                  nul, vp(ws_b), ws_b.numel(), cur)
+
+    def step_batch():
+        if L.gpeed_iq3xxs_moe_batch(*batch_args) != 0:
+            raise RuntimeError(f"moe: {L.gpeed_last_error().decode(errors='replace')}")
+
+    t_end = time.perf_counter() + warmup_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            step_batch()
+        torch.cuda.synchronize()
+    for _ in range(steps):
+        step_batch()
+    t0.record()
+    for _ in range(steps):
+        step_batch()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_b = t0.elapsed_time(t1) / steps
+    G.prof_start(4 * steps + 8)
+    for _ in range(steps):
+        step_batch()
+    torch.cuda.synchronize()
+    d = G.prof_read(G.PROF_GROUPED).astype(np.float64)
+    b_bytes = moe_bytes + 3 * blk_bytes
+    whole = {"entry": "gpeed_iq3xxs_moe_batch", "launches": 5,
+             "workload": "the same batch from the logits with a shared expert (gate/up 2048x6144, down "
+                         "6144x2048) over every token, added last",
+             "packed_bytes_per_step": b_bytes, "ms_per_step": round(ms_b, 4),
+             "GBps": round(b_bytes / (ms_b * 1e-3) / 1e9, 1),
+             "frac_of_hbm_peak": round(b_bytes / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+             "grouped_gate_up_us": round(float(d[0::2].mean()) * 1e3, 2),
+             "grouped_down_us": round(float(d[1::2].mean()) * 1e3, 2)}
     return {
         "workload": "routed-expert decode batch: 64 experts x (gate/up 2048x6144 + down 6144x2048) IQ3_XXS, "
                     "32 tokens, softmax top-8, router + grouped GEMVs + combine on the GPU",
@@ -243,6 +288,7 @@ def moe_decode(torch, G, synth, dev, steps, warmup_s):
                          "algorithmic_bytes": gu_bytes + dn_bytes,
                          "GBps": round((gu_bytes + dn_bytes) / (k_ms * 1e-3) / 1e9, 1),
                          "frac": round((gu_bytes + dn_bytes) / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "whole_step": whole,
     }
 
 

@@ -72,19 +72,34 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 }
 
 // Exclusive scan of v[0..n) in LDS into out (n <= 1024, 1024 threads);
-// returns the total. tmp: 1024 ints of scratch.
+// returns the total. tmp: at least 17 ints of scratch. Each wavefront scans
+// its 64 values with lane shuffles, the 16 wavefront totals are scanned by
+// the first wavefront, and each value adds its wavefront's offset.
 __device__ __forceinline__ int block_exclusive_scan(const int* v, int* out, int* tmp, int n) {
-    const int tid = threadIdx.x;
-    tmp[tid] = tid < n ? v[tid] : 0;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int add = tid >= off ? tmp[tid - off] : 0;
-        __syncthreads();
-        tmp[tid] += add;
-        __syncthreads();
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int x = tid < n ? v[tid] : 0;
+    int inc = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off);
+        if (lane >= off) inc += y;
     }
-    const int total = tmp[1023];
-    if (tid < n) out[tid] = tmp[tid] - v[tid];
+    if (lane == 63) tmp[wave] = inc;
+    __syncthreads();
+    if (wave == 0) {
+        const int w = lane < 16 ? tmp[lane] : 0;
+        int wi = w;
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const int y = __shfl_up(wi, off);
+            if (lane >= off) wi += y;
+        }
+        if (lane < 16) tmp[lane] = wi - w;  // exclusive offset of wavefront `lane`
+        if (lane == 15) tmp[16] = wi;       // the total
+    }
+    __syncthreads();
+    if (tid < n) out[tid] = tmp[wave] + inc - x;
+    const int total = tmp[16];
     __syncthreads();
     return total;
 }
@@ -95,31 +110,15 @@ __device__ __forceinline__ int block_exclusive_scan(const int* v, int* out, int*
 constexpr int kRouteLdsAsg = 2048;
 
 // J = register slots per lane: expert e lives in lane e % 64, slot e / 64.
-// kLds: T * K <= kRouteLdsAsg, the assignments stay in LDS.
-template <int J, bool kLds>
-__device__ __forceinline__ void route_body(const float* __restrict__ logits, int T, int E, int K, int mode,
-                                           const float* __restrict__ bias, float routed_scale, int norm_topk,
-                                           int* __restrict__ eptr, int* __restrict__ tok, float* __restrict__ wt,
-                                           int* __restrict__ sel, int* __restrict__ asg_e,
-                                           float* __restrict__ asg_w) {
-    __shared__ int cnt[kMaxExperts];
-    __shared__ int cursor[kMaxExperts];
-    __shared__ __attribute__((aligned(16))) int chunk_e[1024];
-    __shared__ float rank_score[16][kMaxTopK];
-    __shared__ int lds_e[kLds ? kRouteLdsAsg : 1];
-    __shared__ float lds_w[kLds ? kRouteLdsAsg : 1];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    auto put_e = [&](size_t i, int v) {
-        if constexpr (kLds) lds_e[i] = v;
-        else asg_e[i] = v;
-    };
-    auto put_w = [&](size_t i, float v) {
-        if constexpr (kLds) lds_w[i] = v;
-        else asg_w[i] = v;
-    };
-    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
-    __syncthreads();
-
+// Top-k of tokens t_first, t_first + t_step, ... (one wavefront per token):
+// the ranked experts and their combine weights into out_e / out_w [T][K]
+// (LDS or global), sel (optional) and, with cnt non-null, the per-expert
+// counts (LDS atomics). rank_score: this wavefront's 32 floats of LDS.
+template <int J>
+__device__ __forceinline__ void topk_loop(const float* __restrict__ logits, int T, int E, int K, int mode,
+                                          const float* __restrict__ bias, float routed_scale, int norm_topk,
+                                          int* sel, int* out_e, float* out_w, int* cnt, float (*rank_score)[kMaxTopK],
+                                          int t_first, int t_step, int wave, int lane) {
     // 1. top-k per token (one wavefront per token); lane l holds experts
     // l + 64j. The next token's logits are loaded while this one is ranked.
     float nxt[J];
@@ -130,14 +129,14 @@ __device__ __forceinline__ void route_body(const float* __restrict__ logits, int
             nxt[j] = (t < T && e < E) ? logits[(size_t)t * E + e] : 0.0f;
         }
     };
-    load_logits(wave);
+    load_logits(t_first);
     float bias_j[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int e = lane + 64 * j;
         bias_j[j] = (mode == 0 && bias && e < E) ? bias[e] : 0.0f;
     }
-    for (int t = wave; t < T; t += 16) {
+    for (int t = t_first; t < T; t += t_step) {
         float key[J], sc[J];
         uint64_t rw[J];
 #pragma unroll
@@ -159,7 +158,7 @@ __device__ __forceinline__ void route_body(const float* __restrict__ logits, int
             }
             rw[j] = e < E ? rank_word(key[j], e) : 0;
         }
-        load_logits(t + 16);
+        load_logits(t + t_step);
         if constexpr (J == 1) {
             // rank of this lane's expert among all: one comparison per expert
             int rank = 0;
@@ -170,9 +169,9 @@ __device__ __forceinline__ void route_body(const float* __restrict__ logits, int
             }
             if (lane < E && rank < K) {
                 rank_score[wave][rank] = sc[0];
-                put_e((size_t)t * K + rank, lane);
-                if (!kLds && sel) sel[(size_t)t * K + rank] = lane;
-                atomicAdd(&cnt[lane], 1);
+                out_e[(size_t)t * K + rank] = lane;
+                if (sel) sel[(size_t)t * K + rank] = lane;
+                if (cnt) atomicAdd(&cnt[lane], 1);
             }
         } else {
             // K rounds: this lane's best remaining expert, then the wavefront's
@@ -193,9 +192,9 @@ __device__ __forceinline__ void route_body(const float* __restrict__ logits, int
                 if ((be & 63) == lane) taken |= 1u << (be >> 6);
                 if (lane == 0) {
                     rank_score[wave][k] = bs;
-                    put_e((size_t)t * K + k, be);
-                    if (!kLds && sel) sel[(size_t)t * K + k] = be;
-                    atomicAdd(&cnt[be], 1);
+                    out_e[(size_t)t * K + k] = be;
+                    if (sel) sel[(size_t)t * K + k] = be;
+                    if (cnt) atomicAdd(&cnt[be], 1);
                 }
             }
         }
@@ -216,20 +215,29 @@ __device__ __forceinline__ void route_body(const float* __restrict__ logits, int
             } else {
                 w = num / denom;
             }
-            put_w((size_t)t * K + lane, w);
+            out_w[(size_t)t * K + lane] = w;
         }
     }
-    __syncthreads();
-    if constexpr (kLds) {
-        if (sel)
-            for (int i = tid; i < T * K; i += 1024) sel[i] = lds_e[i];
-    }
+}
 
+// Exclusive scan of the expert counts into eptr and the stable scatter of
+// the assignments src_e / src_w (LDS or global) into tok / wt (and the LDS
+// copies l_eptr / l_tok when given). cnt, cursor, chunk_e: LDS.
+__device__ __forceinline__ void bucket_body(int T, int E, int K, int* __restrict__ eptr, int* __restrict__ tok,
+                                            float* __restrict__ wt, const int* src_e, const float* src_w, int* cnt,
+                                            int* cursor, int* chunk_e, int* l_eptr, int* l_tok) {
+    const int tid = threadIdx.x;
     // 2. exclusive scan of the expert counts (model_batch.cpp:205-209)
     {
         const int total = block_exclusive_scan(cnt, cursor, chunk_e, E);
-        for (int e = tid; e < E; e += 1024) eptr[e] = cursor[e];
-        if (tid == 0) eptr[E] = total;
+        for (int e = tid; e < E; e += 1024) {
+            eptr[e] = cursor[e];
+            if (l_eptr) l_eptr[e] = cursor[e];
+        }
+        if (tid == 0) {
+            eptr[E] = total;
+            if (l_eptr) l_eptr[E] = total;
+        }
     }
     __syncthreads();
 
@@ -239,7 +247,7 @@ __device__ __forceinline__ void route_body(const float* __restrict__ logits, int
     const int N = T * K;
     for (int c0 = 0; c0 < N; c0 += 1024) {
         const int a = c0 + tid;
-        const int ea = a < N ? (kLds ? lds_e[a] : asg_e[a]) : -1;
+        const int ea = a < N ? src_e[a] : -1;
         chunk_e[tid] = ea;
         __syncthreads();
         if (a < N) {
@@ -255,12 +263,43 @@ __device__ __forceinline__ void route_body(const float* __restrict__ logits, int
             for (int j = tid & ~3; j < tid; ++j) rank += chunk_e[j] == ea;
             const int p = cursor[ea] + rank;
             tok[p] = a / K;
-            wt[p] = kLds ? lds_w[a] : asg_w[a];
+            if (l_tok) l_tok[p] = a / K;
+            wt[p] = src_w[a];
         }
         __syncthreads();
         if (a < N) atomicAdd(&cursor[ea], 1);
         __syncthreads();
     }
+}
+
+
+// kLds: T * K <= kRouteLdsAsg, the assignments stay in LDS.
+template <int J, bool kLds>
+__device__ __forceinline__ void route_body(const float* __restrict__ logits, int T, int E, int K, int mode,
+                                           const float* __restrict__ bias, float routed_scale, int norm_topk,
+                                           int* __restrict__ eptr, int* __restrict__ tok, float* __restrict__ wt,
+                                           int* __restrict__ sel, int* __restrict__ asg_e,
+                                           float* __restrict__ asg_w, int* l_eptr = nullptr,
+                                           int* l_tok = nullptr) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int cursor[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) int chunk_e[1024];
+    __shared__ float rank_score[16][kMaxTopK];
+    __shared__ int lds_e[kLds ? kRouteLdsAsg : 1];
+    __shared__ float lds_w[kLds ? kRouteLdsAsg : 1];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+    __syncthreads();
+    int* out_e = kLds ? lds_e : asg_e;
+    float* out_w = kLds ? lds_w : asg_w;
+    topk_loop<J>(logits, T, E, K, mode, bias, routed_scale, norm_topk, kLds ? nullptr : sel, out_e, out_w, cnt,
+                 rank_score, wave, 16, wave, lane);
+    __syncthreads();
+    if constexpr (kLds) {
+        if (sel)
+            for (int i = tid; i < T * K; i += 1024) sel[i] = lds_e[i];
+    }
+    bucket_body(T, E, K, eptr, tok, wt, out_e, out_w, cnt, cursor, chunk_e, l_eptr, l_tok);
 }
 
 template <int J, bool kLds>
@@ -287,15 +326,18 @@ struct MoePlan {
     int* idx_of;     // [N + T_sh] token index of slot p inside its segment
     int* slot_tok;   // [N + T_sh] token of slot p (gather-mode activations)
     int* pos;        // [T][K] slots of token t, in expert order
-    uint32_t* ctr;   // [2] work counters (gate/up, down)
+    int* pos_tmp;    // [T][K] the same, unordered (global scratch of the stand-alone plan)
+    uint32_t* ctr;   // [3] work counters (gate/up, down) and the whole-step front kernel's ticket
     uint32_t* err;   // the workspace's error word (kWsBuckets)
 };
 
 // T_sh: tokens of the shared expert (0 or T); its segments come first
 // (kSegTok tokens each, all full but the last: the heaviest work), slots
 // N .. N + T_sh - 1, token p - N.
-__device__ __forceinline__ void plan_body(const int* __restrict__ eptr, const int* __restrict__ tok, int T, int E,
-                                          int K, int T_sh, MoePlan pl) {
+// eptr / tok may be LDS copies; pos_buf (LDS, or pl.pos itself) holds the
+// per-token slot lists while they are built and sorted.
+__device__ __forceinline__ void plan_body(const int* eptr, const int* tok, int T, int E, int K, int T_sh, MoePlan pl,
+                                          int* pos_buf) {
     __shared__ int ep[kMaxExperts + 1];
     __shared__ int fstart[kMaxExperts + 1];
     __shared__ int nfull[kMaxExperts];
@@ -409,37 +451,31 @@ __device__ __forceinline__ void plan_body(const int* __restrict__ eptr, const in
         pl.slot_tok[p] = tok[p];
     }
     // each token's slots in bucket order = expert order: every slot appends
-    // itself to its token's list, then each list (at most K entries) is
-    // sorted
+    // itself to its token's (unordered) list in pos_buf, then takes the place
+    // of its rank in that list
     for (int p = tid; p < N; p += 1024) {
         const int t = tok[p];
         if (t >= 0 && t < T) {
             const int c = atomicAdd(&tcnt[t], 1);
-            if (c < K) pl.pos[(size_t)t * K + c] = p;
+            if (c < K) pos_buf[(size_t)t * K + c] = p;
         }
     }
     __threadfence_block();
     __syncthreads();
-    for (int t = tid; t < T; t += 1024) {
-        int v[kMaxTopK];
-        const int n = min(tcnt[t], K);
-        for (int c = 0; c < n; ++c) v[c] = pl.pos[(size_t)t * K + c];
-        for (int i = 1; i < n; ++i) {
-            const int x = v[i];
-            int j = i - 1;
-            while (j >= 0 && v[j] > x) {
-                v[j + 1] = v[j];
-                --j;
-            }
-            v[j + 1] = x;
+    for (int p = tid; p < N; p += 1024) {
+        const int t = tok[p];
+        if (t >= 0 && t < T) {
+            const int n = min(tcnt[t], K);
+            int r = 0;
+            for (int c = 0; c < n; ++c) r += pos_buf[(size_t)t * K + c] < p;
+            pl.pos[(size_t)t * K + r] = p;
         }
-        for (int c = 0; c < n; ++c) pl.pos[(size_t)t * K + c] = v[c];
     }
 }
 
 __global__ __launch_bounds__(1024) void k_moe_plan(const int* __restrict__ eptr, const int* __restrict__ tok,
                                                    int T, int E, int K, MoePlan pl) {
-    plan_body(eptr, tok, T, E, K, 0, pl);
+    plan_body(eptr, tok, T, E, K, 0, pl, pl.pos_tmp);
 }
 
 
@@ -528,9 +564,13 @@ __device__ __forceinline__ void token_images(const float* __restrict__ X, int T,
     }
 }
 
-// The front of a whole routed step: workgroup 0 routes (route_body) and
-// plans (plan_body, with T_sh shared-expert tokens), the others build the
-// per-token X images, which do not depend on the routing.
+// The front of a whole routed step. The first n_rank workgroups rank the
+// tokens (token t on workgroup t % n_rank, wavefront (t / n_rank) % 16) into
+// asg_e / asg_w; the last of them to finish (a ticket in the plan's
+// counters, reset again at the end) counts the assignments per expert,
+// bucket-sorts them and makes the work plan (with T_sh shared-expert
+// tokens), its data in LDS when T * K <= kRouteLdsAsg. The other workgroups
+// build the per-token X images meanwhile.
 template <int J, bool kLds>
 __global__ __launch_bounds__(1024) void k_moe_front(const float* __restrict__ logits, int T, int E, int K, int mode,
                                                     const float* __restrict__ bias, float routed_scale,
@@ -538,17 +578,60 @@ __global__ __launch_bounds__(1024) void k_moe_front(const float* __restrict__ lo
                                                     float* __restrict__ wt, int* __restrict__ sel,
                                                     int* __restrict__ asg_e, float* __restrict__ asg_w, int T_sh,
                                                     MoePlan pl, const float* __restrict__ X, int nb,
-                                                    uint8_t* __restrict__ timg, float* __restrict__ tus) {
-    if (blockIdx.x == 0) {
-        route_body<J, kLds>(logits, T, E, K, mode, bias, routed_scale, norm_topk, eptr, tok, wt, sel, asg_e, asg_w);
-        // the plan reads eptr / tok as the router wrote them
+                                                    uint8_t* __restrict__ timg, float* __restrict__ tus,
+                                                    int n_rank) {
+    __shared__ float rank_score[16][kMaxTopK];
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int cursor[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) int chunk_e[1024];
+    __shared__ int lds_e[kLds ? kRouteLdsAsg : 1];
+    __shared__ float lds_w[kLds ? kRouteLdsAsg : 1];
+    __shared__ int l_eptr[kLds ? kMaxExperts + 1 : 1], l_tok[kLds ? kRouteLdsAsg : 1], l_pos[kLds ? kRouteLdsAsg : 1];
+    __shared__ uint32_t ticket_old;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int G = n_rank;
+    if ((int)blockIdx.x >= G) {
+        token_images(X, T, nb, timg, tus, ((int)blockIdx.x - G) * 16 + wave, ((int)gridDim.x - G) * 16, lane);
+        return;
+    }
+    topk_loop<J>(logits, T, E, K, mode, bias, routed_scale, norm_topk, sel, asg_e, asg_w, nullptr, rank_score,
+                 wave * G + blockIdx.x, G * 16, wave, lane);
+    // every wavefront's stores, then one ticket per workgroup
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    uint32_t* ticket = pl.ctr + 2;
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old >= (uint32_t)G) __hip_atomic_fetch_or(pl.err, kWsTicket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket_old = old;
+    }
+    __syncthreads();
+    if (ticket_old != (uint32_t)G - 1) return;  // uniform
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+    __syncthreads();
+    const int N = T * K;
+    for (int a = tid; a < N; a += 1024) {
+        const int e = asg_e[a];
+        if constexpr (kLds) {
+            lds_e[a] = e;
+            lds_w[a] = asg_w[a];
+        }
+        atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if constexpr (kLds) {
+        bucket_body(T, E, K, eptr, tok, wt, lds_e, lds_w, cnt, cursor, chunk_e, l_eptr, l_tok);
+        __syncthreads();
+        plan_body(l_eptr, l_tok, T, E, K, T_sh, pl, l_pos);
+    } else {
+        bucket_body(T, E, K, eptr, tok, wt, asg_e, asg_w, cnt, cursor, chunk_e, nullptr, nullptr);
+        // the plan reads eptr / tok as the bucket sort wrote them
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
         __syncthreads();
-        plan_body(eptr, tok, T, E, K, T_sh, pl);
-    } else {
-        token_images(X, T, nb, timg, tus, (blockIdx.x - 1) * 16 + (int)(threadIdx.x >> 6), (gridDim.x - 1) * 16,
-                     threadIdx.x & 63);
+        plan_body(eptr, tok, T, E, K, T_sh, pl, pl.pos_tmp);
     }
+    if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -767,7 +850,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ D
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 struct MoeLayout {
-    size_t plan_off[9];
+    size_t plan_off[10];
     size_t act1, g, u, act2, d, total;
     size_t eptr, tok, wt, sel, asg_e, asg_w, timg, tus;  // the whole-step path only
     size_t stride1, stride2;
@@ -782,9 +865,9 @@ MoeLayout moe_layout(int T, int E, int K, int H, int I, int T_sh = 0, bool fused
     const size_t N = (size_t)T * K, NS = N + (size_t)T_sh;
     L.seg_max = (int)((N + (size_t)(kSegTok - 1) * E) / kSegTok + 1) + (T_sh + kSegTok - 1) / kSegTok;
     size_t off = kWsHeader;
-    const size_t sizes[9] = {256, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max,
-                             4 * NS, 4 * NS, 4 * N, 256, 4 * NS};
-    for (int i = 0; i < 9; ++i) {
+    const size_t sizes[10] = {256, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max, 4 * (size_t)L.seg_max,
+                              4 * NS, 4 * NS, 4 * N, 256, 4 * NS, 4 * N};
+    for (int i = 0; i < 10; ++i) {
         L.plan_off[i] = off;
         off += align256(sizes[i]);
     }
@@ -816,6 +899,7 @@ MoePlan plan_ptrs(uint8_t* ws, const MoeLayout& L) {
     p.n_valid = p.n_seg + 1;
     p.n_sh_seg = p.n_seg + 2;
     p.slot_tok = reinterpret_cast<int*>(ws + L.plan_off[8]);
+    p.pos_tmp = reinterpret_cast<int*>(ws + L.plan_off[9]);
     p.err = reinterpret_cast<uint32_t*>(ws);
     p.ctr = reinterpret_cast<uint32_t*>(ws + L.plan_off[7]);
     p.seg_e = reinterpret_cast<int*>(ws + L.plan_off[1]);
@@ -932,14 +1016,16 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
     float* D = reinterpret_cast<float*>(ws + L.d);
     uint8_t* timg = ws + L.timg;
     float* tus = reinterpret_cast<float*>(ws + L.tus);
-    // 1. router + bucket sort + work plan (workgroup 0) and the per-token X
-    // images (the other workgroups)
-    const int prep_groups = std::min((T * nbH + 15) / 16, 255);
+    // 1. router, per-token X images, bucket sort and work plan
+    // ranking workgroups: one token per wavefront up to 64 of them; image
+    // workgroups: one (token, block) item per wavefront up to 192
+    const int n_rank = std::min((T + 15) / 16, 64);
+    const int groups = n_rank + std::min((T * nbH + 15) / 16, 192);
     auto front = [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3(1 + prep_groups), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale,
+        hipLaunchKernelGGL(kern, dim3(groups), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale,
                            norm_topk, eptr, tok, wt, reinterpret_cast<int*>(ws + L.sel),
                            reinterpret_cast<int*>(ws + L.asg_e), reinterpret_cast<float*>(ws + L.asg_w), T_sh, pl, X,
-                           nbH, timg, tus);
+                           nbH, timg, tus, n_rank);
     };
     const bool lds = (long long)T * K <= kRouteLdsAsg;
     if (E <= 64) lds ? front(k_moe_front<1, true>) : front(k_moe_front<1, false>);
