@@ -506,8 +506,10 @@ def main():
                     help="run 5 elementwise copies of 256 MiB (counter calibration), then 20 dense steps, and "
                          "exit; meant to run under rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE)")
     ap.add_argument("--gemm-probe", action="store_true",
-                    help="run the prefill GEMM (W 12288x6144, bf16 X [512, 6144]) 20 times and the dense "
+                    help="run the prefill GEMM (W 12288x6144, bf16 X [M, 6144]) 20 times and the dense "
                          "decode step 20 times, and exit; meant to run under rocprofv3 --pmc")
+    ap.add_argument("--gemm-m", type=int, default=512,
+                    help="tokens of the --gemm-probe GEMM (512 runs k_gemm3, 1024 and more k_gemm4)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the multi-GPU "
@@ -598,7 +600,7 @@ def main():
         return
 
     if args.gemm_probe:
-        N_, K_, M_ = 12288, 6144, 512
+        N_, K_, M_ = 12288, 6144, args.gemm_m
         t64 = G.tile(torch.from_numpy(synth.iq3xxs_matrix(2026, 0, N_, K_).reshape(-1)).to(dev), N_, K_)
         X = torch.from_numpy(synth.normal(2026, M_, M_ * K_).reshape(M_, K_)).to(dev).to(torch.bfloat16)
         Yg = torch.empty(M_, N_, device=dev)

@@ -122,7 +122,7 @@ void WeightStore::read_resident(const std::string& name, void* dst) const {
 WeightStore::~WeightStore() {
     for (auto& kv : tensors_) (void)gpeed_free(kv.second.data);
     for (auto& kv : ws_) (void)gpeed_free(kv.second.p);
-    for (Buffer* b : {&x_, &y_, &route_ws_, &moe_ws_, &logits_, &bias_, &eptr_, &tok_, &wt_})
+    for (Buffer* b : {&x_, &y_, &route_ws_, &moe_ws_, &batch_ws_, &logits_, &bias_, &eptr_, &tok_, &wt_})
         (void)gpeed_free(b->p);
 }
 
@@ -326,6 +326,39 @@ void WeightStore::moe_experts(const std::string& gate, const std::string& up, co
                                    moe_ws_.bytes, nullptr),
           "moe: experts");
     check_ws(mws, "moe: experts");
+    check(gpeed_memcpy(Y, yd, xb, kD2H), "moe: download y");
+}
+
+void WeightStore::moe_batch(const std::string& gate, const std::string& up, const std::string& down,
+                            const std::string& gate_sh, const std::string& up_sh, const std::string& down_sh,
+                            int n_exp, int hidden, int inter, const float* X, int n_tok, const float* logits,
+                            int top_k, int mode, const float* bias, float routed_scale, bool norm_topk,
+                            float swiglu_limit, float* Y) {
+    if (n_tok <= 0) return;
+    const Tensor& tg = get_iq3(gate, hidden);
+    const Tensor& tu = get_iq3(up, hidden);
+    const Tensor& td = get_iq3(down, inter);
+    const bool shared = !gate_sh.empty();
+    const void* sg = shared ? get_iq3(gate_sh, hidden).data : nullptr;
+    const void* su = shared ? get_iq3(up_sh, hidden).data : nullptr;
+    const void* sd = shared ? get_iq3(down_sh, inter).data : nullptr;
+    const size_t wsb = gpeed_iq3xxs_moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, shared ? 1 : 0);
+    if (wsb == 0) throw std::runtime_error("moe: unsupported shape");
+    void* ws = scratch(batch_ws_, wsb, true);
+    void* lg = scratch(logits_, (size_t)n_tok * n_exp * sizeof(float), false);
+    void* bd = bias ? scratch(bias_, (size_t)n_exp * sizeof(float), false) : nullptr;
+    const size_t xb = (size_t)n_tok * hidden * sizeof(float);
+    void* xd = scratch(x_, xb, false);
+    void* yd = scratch(y_, xb, false);
+    check(gpeed_memcpy(lg, logits, (size_t)n_tok * n_exp * sizeof(float), kH2D), "moe: upload logits");
+    if (bias) check(gpeed_memcpy(bd, bias, (size_t)n_exp * sizeof(float), kH2D), "moe: upload bias");
+    check(gpeed_memcpy(xd, X, xb, kH2D), "moe: upload x");
+    check(gpeed_iq3xxs_moe_batch(static_cast<const float*>(lg), n_tok, n_exp, top_k, mode,
+                                 static_cast<const float*>(bd), routed_scale, norm_topk ? 1 : 0, tg.data, tu.data,
+                                 td.data, sg, su, sd, hidden, inter, static_cast<const float*>(xd), swiglu_limit,
+                                 static_cast<float*>(yd), nullptr, nullptr, nullptr, ws, batch_ws_.bytes, nullptr),
+          "moe: batch");
+    check_ws(ws, "moe: batch");
     check(gpeed_memcpy(Y, yd, xb, kD2H), "moe: download y");
 }
 

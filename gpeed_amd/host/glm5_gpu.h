@@ -108,6 +108,15 @@ public:
     void moe_experts(const std::string& gate, const std::string& up, const std::string& down, int n_exp,
                      int hidden, int inter, const float* X, int n_tok, const float* logits, int top_k, int mode,
                      const float* bias, float routed_scale, bool norm_topk, float swiglu_limit, float* Y);
+    // The whole of Model::moe_batch after the router product
+    // (model_batch.cpp:174-280): moe_experts, plus, when gate_sh is not
+    // empty, the shared expert (gate_sh / up_sh [inter, hidden], down_sh
+    // [hidden, inter]) over every token added last, as add_f32 does. One
+    // call of gpeed_iq3xxs_moe_batch (five launches).
+    void moe_batch(const std::string& gate, const std::string& up, const std::string& down,
+                   const std::string& gate_sh, const std::string& up_sh, const std::string& down_sh, int n_exp,
+                   int hidden, int inter, const float* X, int n_tok, const float* logits, int top_k, int mode,
+                   const float* bias, float routed_scale, bool norm_topk, float swiglu_limit, float* Y);
 
 private:
     struct Tensor {
@@ -138,7 +147,7 @@ private:
     // it is made and grown when a call needs more; each launch leaves its
     // tickets at zero, and one sized for n_tok serves every smaller call.
     std::map<std::tuple<int, int>, Buffer> ws_;
-    Buffer x_, y_, route_ws_, moe_ws_, logits_, bias_, eptr_, tok_, wt_;
+    Buffer x_, y_, route_ws_, moe_ws_, batch_ws_, logits_, bias_, eptr_, tok_, wt_;
 };
 
 }  // namespace gpu

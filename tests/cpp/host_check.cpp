@@ -194,6 +194,28 @@ int main(int argc, char** argv) {
             spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
             return 0;
         }
+        if (mode == "moe-batch" && argc == 10) {  // the whole step, shared expert when sh == 1
+            const std::string dir = argv[2];
+            const int E = std::atoi(argv[3]), H = std::atoi(argv[4]), I = std::atoi(argv[5]);
+            const int T = std::atoi(argv[6]), K = std::atoi(argv[7]), md = std::atoi(argv[8]);
+            const bool sh = std::atoi(argv[9]) != 0;
+            glm5::gpu::WeightStore ws;
+            ws.add("gate", slurp(dir + "/gate.bin").data(), (uint64_t)E * I, H);
+            ws.add("up", slurp(dir + "/up.bin").data(), (uint64_t)E * I, H);
+            ws.add("down", slurp(dir + "/down.bin").data(), (uint64_t)E * H, I);
+            if (sh) {
+                ws.add("gate_sh", slurp(dir + "/gate_sh.bin").data(), (uint64_t)I, H);
+                ws.add("up_sh", slurp(dir + "/up_sh.bin").data(), (uint64_t)I, H);
+                ws.add("down_sh", slurp(dir + "/down_sh.bin").data(), (uint64_t)H, I);
+            }
+            const std::vector<char> x = slurp(dir + "/x.bin"), lg = slurp(dir + "/logits.bin");
+            std::vector<float> Y((size_t)T * H);
+            ws.moe_batch("gate", "up", "down", sh ? "gate_sh" : "", sh ? "up_sh" : "", sh ? "down_sh" : "", E, H, I,
+                         reinterpret_cast<const float*>(x.data()), T, reinterpret_cast<const float*>(lg.data()), K,
+                         md, nullptr, md == 0 ? 2.5f : 1.0f, true, 10.0f, Y.data());
+            spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
+            return 0;
+        }
         if (mode == "dequant" && argc == 6) {  // host-array dequantize (quant.h:18-22)
             const int dtype = std::atoi(argv[2]);
             const uint64_t n = std::strtoull(argv[4], nullptr, 10);

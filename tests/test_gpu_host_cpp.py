@@ -65,3 +65,27 @@ def test_moe_experts(gpu, tmp_path, mode):
     eptr, tok, wt, _ = oracle.moe_route(logits, K, mode, routed_scale=2.5 if mode == 0 else 1.0)
     ref = oracle.moe_experts(wg, wu, wd, H, I, X, eptr, tok, wt, 10.0)
     assert max(rel_err(Y[t], ref[t]) for t in range(T)) < TIGHT
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_moe_batch_whole_step(gpu, tmp_path, shared):
+    """WeightStore::moe_batch (model_batch.cpp:174-280 after the router
+    product) through the C++ layer, with and without the shared expert,
+    against the oracle's moe_batch."""
+    E, H, I, T, K, mode = 16, 1024, 512, 12, 4, 0
+    wg = synth.iq3xxs_matrix(82, 0, E * I, H)
+    wu = synth.iq3xxs_matrix(82, 1, E * I, H)
+    wd = synth.iq3xxs_matrix(82, 2, E * H, I)
+    sg = synth.iq3xxs_matrix(82, 5, I, H)
+    su = synth.iq3xxs_matrix(82, 6, I, H)
+    sd = synth.iq3xxs_matrix(82, 7, H, I)
+    X = synth.normal(82, 3, T * H).reshape(T, H)
+    logits = synth.normal(82, 4, T * E).reshape(T, E)
+    for name, a in (("gate", wg), ("up", wu), ("down", wd), ("gate_sh", sg), ("up_sh", su), ("down_sh", sd),
+                    ("x", X), ("logits", logits)):
+        a.tofile(tmp_path / f"{name}.bin")
+    run("moe-batch", tmp_path, E, H, I, T, K, mode, int(shared))
+    Y = np.fromfile(tmp_path / "Y.bin", np.float32).reshape(T, H)
+    ref = oracle.moe_batch(logits, X, wg, wu, wd, H, I, K, mode, None, 2.5, True, 10.0,
+                           shared=(sg, su, sd) if shared else None)
+    assert max(rel_err(Y[t], ref[t]) for t in range(T)) < TIGHT
