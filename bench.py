@@ -11,7 +11,9 @@ of gpeed_amd.synth), x ~ N(0,1) fp32, resident in HBM before timing. To
 measure HBM rather than the 256 MB Infinity Cache, `--copies` distinct
 copies of the three tensors (default 8, 694 MB) are rotated step by step.
 
-value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s.
+value = packed weight bytes per step (3 x 28,901,376) / step time, GB/s, over
+the --steps timed steps; before the --warmup steps the step runs untimed for
+about 0.25 s so that a freshly leased GPU's clocks and launch path settle.
 roofline = the GEMV kernel (k_gemv_t64: the gate+up launch and the down
 launch of a step): algorithmic bytes of the pair (packed W + fp32 x + the
 SwiGLU activation written and read + y) / the pair's duration, timed with
@@ -47,6 +49,12 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+# Kernel arguments in device memory (set before the HIP runtime starts): a
+# launch's first scalar loads of its arguments then come from HBM instead of
+# host memory, about 1.1 us less per launch on this stack (measured: dense
+# step 35.7 -> 33.2 us on one box). The library's callers get the same by
+# exporting the variable.
+os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
 
 METRIC = "IQ3_XXS GEMV weight GB/s (% of HBM peak) at batch 1; prefill GEMM TFLOP/s"
 HBM_PEAK_GBS = 8000.0
@@ -624,6 +632,18 @@ def main():
         log("traffic probe done")
         return
 
+    # Before the warm-up steps, the step runs untimed for about a quarter of
+    # a second through the C ABI: on a freshly leased GPU the clocks and the
+    # launch path take that long to settle (5 warm-up steps left a cold box's
+    # 20-step line ~11% below its steady state).
+    log("settle")
+    t_end = time.perf_counter() + 0.25
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(64):
+            step_fast(i % args.copies)
+            i += 1
+        torch.cuda.synchronize()
     log("warmup")
     for i in range(args.warmup):
         step(i % args.copies)
