@@ -187,13 +187,18 @@ __device__ __forceinline__ GemmArgs gemm_tensor(const GemmArgs& g, const GemmTil
 // all of this XCD's dirty L2 lines (other tiles' Y) that no reader needs. A
 // ticket past the split count (two launches sharing the workspace) sets
 // kWsTicket.
-// BN: the tile's W rows (48 per wavefront), NTHR: the workgroup's threads.
-template <int MT, int BN = kTileN, int NTHR = kGemmThreads>
-__device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t, const float4_t (&acc)[MT][3],
-                                           int m0, int n0, int wave, int lr, int lg, int tid, int* flag) {
+// BN: the tile's W rows, NTHR: the workgroup's threads. The wavefront's
+// rows are n0 + rbase + 16 j + lr (j < JT); a wavefront with active false
+// holds no rows of its own (its sums went to another wavefront) and only
+// joins the barriers and the last split's sum.
+template <int MT, int JT = 3, int BN = kTileN, int NTHR = kGemmThreads>
+__device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t, const float4_t (&acc)[MT][JT],
+                                           int m0, int n0, int rbase, int lr, int lg, int tid, int* flag,
+                                           bool active = true) {
     constexpr int BM = 16 * MT;
     constexpr int kTileN = BN;  // (shadows the 192-row default)
     if (g.ks == 1) {
+        if (!active) return;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -202,8 +207,8 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
                 if (m >= g.M) continue;
                 const float us = g.unscale[m];
 #pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const int n = n0 + wave * 48 + j * 16 + lr;
+                for (int j = 0; j < JT; ++j) {
+                    const int n = n0 + rbase + j * 16 + lr;
                     if (n < g.N) g.y[(size_t)m * g.N + n] = acc[mt][j][i] * us;
                 }
             }
@@ -217,10 +222,10 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int ml = mt * 16 + lg * 4 + i;
-            if (m0 + ml >= g.M) continue;
+            if (!active || m0 + ml >= g.M) continue;
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const int nl = wave * 48 + j * 16 + lr;
+            for (int j = 0; j < JT; ++j) {
+                const int nl = rbase + j * 16 + lr;
                 if (n0 + nl < g.N)
                     __hip_atomic_store(mine + ml * kTileN + nl, acc[mt][j][i], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -464,7 +469,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g_all) {
         });
     }
 
-    gemm_store<8>(g, tl, acc, m0, n0, wave, lr, lg, tid, &last_flag);
+    gemm_store<8>(g, tl, acc, m0, n0, wave * 48, lr, lg, tid, &last_flag);
 }
 
 
@@ -744,7 +749,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
         });
     }
 
-    gemm_store<MT>(g, tl, acc, m0, n0, wave, lr, (int)lg, tid, &sm.last_flag);
+    gemm_store<MT>(g, tl, acc, m0, n0, wave * 48, lr, (int)lg, tid, &sm.last_flag);
 }
 
 
@@ -791,13 +796,15 @@ struct GemmSmem4 {
     int last_flag;
 };
 
-// Entry (idx, s) = 4 fp16 values grid(idx)[0..3] * (2s+1), at (idx << 7) | (s << 3).
+// Entry (idx, s) = 4 fp16 values grid(idx)[0..3] * (2s+1), at (idx << 7) | (s << 3),
+// written by a workgroup of NTHR threads.
+template <int NTHR = 512>
 __device__ __forceinline__ void scaled_grid_table4(uint8_t* tbl, int tid) {
     const uint32_t s = tid & 15;
     const float m = (float)(2 * s + 1);
 #pragma unroll 2
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t idx = (tid >> 4) + 32 * i;
+    for (int i = 0; i < 4096 / NTHR; ++i) {
+        const uint32_t idx = (tid >> 4) + (NTHR / 16) * i;
         const uint32_t v = kIq3xxsGrid[idx];
         const uint32_t lo = f16_pair_of_floats((float)(v & 255u) * m, (float)((v >> 8) & 255u) * m);
         const uint32_t hi = f16_pair_of_floats((float)((v >> 16) & 255u) * m, (float)(v >> 24) * m);
@@ -996,7 +1003,315 @@ __global__ __launch_bounds__(kThreads4) void k_gemm4(GemmArgs g_all) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= f;
     }
-    gemm_store<MT, BN4, kThreads4>(g, tl, acc, m0, n0, wave, lr, (int)lg, tid, &sm.last_flag);
+    gemm_store<MT, 3, BN4, kThreads4>(g, tl, acc, m0, n0, wave * 48, lr, (int)lg, tid, &sm.last_flag);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM, K-halves form (one X image: bf16 input). k_gemm3's workgroup tile
+// (128 tokens x 192 W rows) on 512 threads: wavefront w owns rows
+// 48 (w & 3) .. +47 (3 column tiles of v_mfma_f32_16x16x32_f16, all 8 token
+// tiles) over the blocks of K half kh = w >> 2, so every SIMD runs two
+// wavefronts and every W value is still decoded once per workgroup. The 96
+// accumulators run in units of the row's running d, as in k_gemm4. Each K
+// half has its own double-buffered rings in LDS, filled by its own four
+// wavefronts: 64-column X stages (rows swizzled by 16-byte chunk,
+// register-staged one stage ahead) and W half blocks (units 0-2 or 3-5 of
+// the three row tiles, i.e. 4 sub-blocks, register-staged two stages
+// ahead) with the blocks' d. The B operands of a sub-block are decoded
+// while the MFMAs of the previous one run (W is in LDS two stages ahead, so
+// the next stage's operands are decoded before the barrier that ends this
+// one); rows whose block has d = 0 read a zero table entry. One workgroup
+// barrier per stage. At the end the K half 1 wavefronts leave their sums in
+// LDS and the K half 0 wavefronts add them (half 0 + half 1, fixed order)
+// and store the tile.
+
+constexpr int BM5 = 128, BN5 = 192, BK5 = 64;
+constexpr int kThreads5 = 512;
+constexpr int kXStage5 = BM5 * BK5 * 2;          // 16 KiB: 128 rows x 128 bytes
+constexpr int kWHalf5 = 3 * 3 * kUnitBytes;      // 9 KiB: 3 row tiles x 3 units
+constexpr uint32_t kZeroEntry5 = kTbl4;          // 8 zero bytes after the scaled grid
+
+struct GemmSmem5 {
+    uint8_t tbl[kTbl4 + 16];     // grid * (2s+1), k_gemm4's layout, then the zero entry
+    uint8_t xs[2][2][kXStage5];  // [K half][buffer]
+    uint8_t wb[2][2][kWHalf5];   // [K half][buffer]: [tile][unit][64 lanes x 16 B]
+    uint8_t wd[2][2][3 * 128];   // [K half][block parity]: [tile][64 fp16]
+    int last_flag;
+};
+// the K half 1 sums (128 x 192 fp32) overlay xs and wb
+static_assert(2 * 2 * kXStage5 + 2 * 2 * kWHalf5 >= 128 * 192 * 4, "reduction area");
+
+// B operand (group lg of a sub-block of one W row) from its grid-index word q
+// (bytes p0, p0+1) and sign/scale word w, as decode_group4; the table
+// offsets (idx << 7) | (s << 3) come from aligning the index byte with w
+// (whose top four bits are s), and a row with amask = 0, azero =
+// kZeroEntry5 reads the zero entry instead.
+__device__ __forceinline__ half8_t decode_group5(const uint8_t* tbl, uint32_t q, uint32_t w, uint32_t lg,
+                                                 uint32_t p0, uint32_t amask, uint32_t azero) {
+    const uint32_t sw = t64_signs(w);
+    const uint32_t wg = __builtin_amdgcn_alignbit(sw, sw, lg);
+    const uint64_t sw2 = ((uint64_t)(wg >> 4) << 32) | wg;
+    const uint64_t r01 = shl64<15>(sw2), r23 = shl64<7>(sw2);
+    const uint32_t i0 = __builtin_amdgcn_ubfe(q, 8 * p0, 8), i1 = __builtin_amdgcn_ubfe(q, 8 * p0 + 8, 8);
+    const uint32_t a0 = (__builtin_amdgcn_alignbit(i0, w, 25) & amask) | azero;
+    const uint32_t a1 = (__builtin_amdgcn_alignbit(i1, w, 25) & amask) | azero;
+    const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + a0);
+    const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(tbl + a1);
+    const u32x4_t r = {((uint32_t)r01 & 0x80008000u) | g0.x, ((uint32_t)(r01 >> 32) & 0x80008000u) | g0.y,
+                       ((uint32_t)r23 & 0x80008000u) | g1.x, ((uint32_t)(r23 >> 32) & 0x80008000u) | g1.y};
+    return __builtin_bit_cast(half8_t, r);
+}
+
+__global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
+    constexpr int MT = BM5 / 16;  // token tiles (8)
+    constexpr int JT = 3;         // column tiles per wavefront
+    constexpr int kSlots = 256;   // lanes staging one K half
+    constexpr int kXLoads = 4;    // 16-byte X pieces per lane and stage (1024 / 256)
+    constexpr int kWLoads = 3;    // W pieces per lane and half block (576 units + 24 d, of 768)
+    __shared__ __attribute__((aligned(16))) GemmSmem5 sm;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rq = wave & 3, kh = wave >> 2;
+    const uint32_t lane = tid & 63;
+    const int lr = lane & 15;
+    const uint32_t lg = lane >> 4;
+    const int ls = rq * 64 + (int)lane;  // lane slot among the K half's wavefronts
+
+    const GemmTile tl = gemm_tile(g_all);
+    if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
+    int tn;
+    const GemmArgs g = gemm_tensor(g_all, tl, tn);
+    const int m0 = tl.tm * BM5, n0 = tn * BN5;
+    const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
+    scaled_grid_table4<kThreads5>(sm.tbl, tid);
+    if (tid < 4) reinterpret_cast<uint32_t*>(sm.tbl + kZeroEntry5)[tid] = 0u;
+
+    // K halves: blocks [b0 + kh * nh, ...) of this split, nh per half (the
+    // second half of an odd count has one block fewer: its last block is
+    // loaded clamped and contributes zeros)
+    const int nblk = tl.b1 - tl.b0;
+    const int nh = (nblk + 1) >> 1;
+    const int kb0 = tl.b0 + kh * nh;
+    const int steps = nh * (kQK / BK5);
+    auto blk_of = [&](int c) { return min(kb0 + c, tl.b1 - 1); };
+
+    // X pieces of this lane: rows (ls >> 3) + 32 i, global chunk ls & 7,
+    // stored at LDS chunk (ls & 7) ^ (row & 7)
+    // (byte offsets from xh: the image is under 4 GiB, as the launch checks)
+    uint32_t xsrc[kXLoads];
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i)
+        xsrc[i] = ((uint32_t)min(m0 + (ls >> 3) + 32 * i, g.M - 1) * (uint32_t)g.K + (ls & 7) * 8) * 2u;
+    const uint32_t xdst = (uint32_t)(ls >> 3) * 128u + ((uint32_t)((ls & 7) ^ ((ls >> 3) & 7)) << 4);
+    u32x4_t xreg[kXLoads];
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(g.xh);
+    auto load_x = [&](int s) {
+        const uint32_t kc = (uint32_t)(blk_of(s >> 2) * kQK + (s & 3) * BK5) * 2u;
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) xreg[i] = *reinterpret_cast<const u32x4_t*>(xbase + (xsrc[i] + kc));
+    };
+    auto store_x = [&](int buf) {
+        uint8_t* dst = sm.xs[kh][buf] + xdst;
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) *reinterpret_cast<u32x4_t*>(dst + i * 32 * 128) = xreg[i];
+    };
+
+    // W pieces of this lane: item ls + 256 k. Items 0..575: unit ui =
+    // item / 64 of the half block (row tile ui / 3, unit ui % 3), lane slot
+    // `lane`; items 576..599: the three tiles' d, stored with a block's
+    // first half only; the rest load a W piece again and store nothing.
+    uint32_t w_goff[kWLoads], w_loff[kWLoads];
+    bool w_isd[kWLoads], w_idle[kWLoads];
+#pragma unroll
+    for (int k = 0; k < kWLoads; ++k) {
+        const int item = ls + kSlots * k;
+        w_isd[k] = false;
+        w_idle[k] = false;
+        if (item < 576) {
+            const int ui = item >> 6, jt = ui / 3, u = ui % 3;
+            const int tile = min(n0 / kTileRows + jt, last_tile);
+            w_goff[k] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + u * kUnitBytes + lane * 16u;
+            w_loff[k] = (uint32_t)ui * kUnitBytes + lane * 16u;
+        } else if (item < 600) {
+            const int e = item - 576, jt = e >> 3;
+            const int tile = min(n0 / kTileRows + jt, last_tile);
+            w_goff[k] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + kRecordDOffset + (e & 7) * 16u;
+            w_loff[k] = (uint32_t)jt * 128u + (e & 7) * 16u;
+            w_isd[k] = true;
+        } else {
+            w_goff[k] = w_goff[0];
+            w_loff[k] = 0;
+            w_idle[k] = true;
+        }
+    }
+    u32x4_t wreg[kWLoads];
+    // half block hb: block hb >> 1, units 3 (hb & 1) .. +2
+    auto load_w = [&](int hb) {
+        const uint32_t boff = (uint32_t)blk_of(hb >> 1) * kRecordBytes;
+        const uint32_t hoff = (uint32_t)(hb & 1) * 3 * kUnitBytes;
+#pragma unroll
+        for (int k = 0; k < kWLoads; ++k)
+            wreg[k] = *reinterpret_cast<const u32x4_t*>(g.w + (w_goff[k] + boff + (w_isd[k] ? 0u : hoff)));
+    };
+    auto store_w = [&](int hb) {
+#pragma unroll
+        for (int k = 0; k < kWLoads; ++k) {
+            if (w_idle[k]) continue;
+            if (w_isd[k]) {
+                if ((hb & 1) == 0) *reinterpret_cast<u32x4_t*>(sm.wd[kh][(hb >> 1) & 1] + w_loff[k]) = wreg[k];
+            } else {
+                *reinterpret_cast<u32x4_t*>(sm.wb[kh][hb & 1] + w_loff[k]) = wreg[k];
+            }
+        }
+    };
+
+    // this lane's rows j < JT: lane slot in the staged half block, and d
+    const uint8_t* wrow[JT];
+    uint32_t d_off[JT];
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+        const int r = rq * 48 + j * 16 + lr;
+        wrow[j] = &sm.wb[kh][0][0] + (r >> 6) * 3 * kUnitBytes + (r & 63) * 16;
+        d_off[j] = (uint32_t)(r >> 6) * 128u + (uint32_t)(r & 63) * 2u;
+    }
+    const uint32_t p0 = 2 * (lg & 1);
+    const bool hiq = lg >= 2;
+    const uint8_t* arow = &sm.xs[kh][0][0] + lr * 128;
+    // A operand chunk of sub-block t (of 2 per stage), swizzled
+    uint32_t a_off[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) a_off[t] = (uint32_t)((t * 4 + (int)lg) ^ (lr & 7)) << 4;
+
+    float4_t acc[MT][JT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < JT; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float dcur[JT], dnext[JT];
+    uint32_t amask[JT], azero[JT];
+
+    // block c's d per row (0 past this half's blocks): the table masks for
+    // its decode, and dnext
+    auto block_d = [&](int c) {
+        const bool live = kb0 + c < tl.b1;
+#pragma unroll
+        for (int j = 0; j < JT; ++j) {
+            const float dn =
+                live ? (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(&sm.wd[kh][c & 1][d_off[j]]))
+                     : 0.0f;
+            const bool z = dn == 0.0f;
+            amask[j] = z ? 0u : 0x7FF8u;
+            azero[j] = z ? kZeroEntry5 : 0u;
+            dnext[j] = dn;
+        }
+    };
+    // the accumulators move to the units of dnext where it is nonzero and differs
+    auto rescale = [&]() {
+#pragma unroll
+        for (int j = 0; j < JT; ++j) {
+            const bool change = dnext[j] != 0.0f && dnext[j] != dcur[j];
+            const float r = change ? dcur[j] * __builtin_amdgcn_rcpf(dnext[j]) : 1.0f;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= r;
+            dcur[j] = change ? dnext[j] : dcur[j];
+        }
+    };
+    // B operands of sub-block ib (0..7) of a block from W buffer `buf`
+    auto decode = [&](half8_t (&bop)[JT], int buf, int ib) {
+        const int lib = ib & 3;  // inside the half block
+        const int dq = 3 * lib + (hiq ? 1 : 0), dw = 3 * lib + 2;
+        const int oq = buf * kWHalf5 + (dq >> 2) * kUnitBytes + (dq & 3) * 4;
+        const int ow = buf * kWHalf5 + (dw >> 2) * kUnitBytes + (dw & 3) * 4;
+#pragma unroll
+        for (int j = 0; j < JT; ++j) {
+            const uint32_t q = *reinterpret_cast<const uint32_t*>(wrow[j] + oq);
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(wrow[j] + ow);
+            bop[j] = decode_group5(sm.tbl, q, w, lg, p0, amask[j], azero[j]);
+        }
+    };
+
+    // prologue: X stage 0 and W half block 0 (with block 0's d) in LDS, X
+    // stage 1 and W half block 1 in registers; block 0's d and the B
+    // operands of its first sub-block
+    load_x(0);
+    load_w(0);
+    store_x(0);
+    store_w(0);
+    load_x(min(1, steps - 1));
+    load_w(min(1, 2 * nh - 1));
+    __syncthreads();  // table, X stage 0, W half block 0
+    block_d(0);
+#pragma unroll
+    for (int j = 0; j < JT; ++j) dcur[j] = dnext[j];  // the accumulators are zero
+    half8_t bop[2][JT];
+    decode(bop[0], 0, 0);
+
+    for (int c = 0; c < nh; ++c) {
+        static_for<0, 4>([&](auto Uc) {
+            constexpr int U = decltype(Uc)::value;
+            const int s = 4 * c + U;
+            // X(s + 1) to LDS, X(s + 2) into the registers
+            if (s + 1 < steps) {
+                store_x((s + 1) & 1);
+                load_x(min(s + 2, steps - 1));
+            }
+            // at a half block's first stage: W(hb + 1) to LDS, W(hb + 2) into the registers
+            if constexpr ((U & 1) == 0) {
+                const int hb = s >> 1;
+                if (hb + 1 < 2 * nh) {
+                    store_w(hb + 1);
+                    load_w(min(hb + 2, 2 * nh - 1));
+                }
+            }
+            const uint8_t* xa = arow + (s & 1) * kXStage5;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                // the next sub-block's operands: this stage's second, or the
+                // next stage's first (its W half block is in LDS already;
+                // after a block's last stage, with the next block's d)
+                if (t == 0) {
+                    decode(bop[1], (s >> 1) & 1, 2 * U + 1);
+                } else if (s + 1 < steps) {
+                    if constexpr (U == 3) block_d(c + 1);
+                    decode(bop[0], ((s + 1) >> 1) & 1, (2 * U + 2) & 7);
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const half8_t a = *reinterpret_cast<const half8_t*>(xa + mt * 16 * 128 + a_off[t]);
+#pragma unroll
+                    for (int j = 0; j < JT; ++j)
+                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop[t][j], acc[mt][j], 0, 0, 0);
+                }
+            }
+            if constexpr (U == 3) {
+                if (c + 1 < nh) rescale();
+            }
+            __syncthreads();
+        });
+    }
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+        const float f = dcur[j] * 0.25f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= f;
+    }
+    // K half 1 -> LDS (over xs and wb, free after the last barrier); K half 0 adds
+    float4_t* red = reinterpret_cast<float4_t*>(&sm.xs[0][0][0]) + (size_t)rq * (MT * JT * 64) + lane;
+    if (kh == 1) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < JT; ++j) red[(mt * JT + j) * 64] = acc[mt][j];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < JT; ++j) acc[mt][j] += red[(mt * JT + j) * 64];
+    }
+    gemm_store<MT, JT, kTileN, kThreads5>(g, tl, acc, m0, n0, rq * 48, lr, (int)lg, tid, &sm.last_flag, kh == 0);
 }
 
 }  // namespace
@@ -1012,6 +1327,14 @@ int gemm_tile_m(int M) { return M <= 64 ? 64 : 128; }
 // where the K split its larger tiles need costs what the second wavefront
 // gains.
 static bool gemm_wide(int M, int x_bf16, bool two_tensors) { return x_bf16 && M >= 1024 && !two_tensors; }
+
+// k_gemm5 (K halves inside the workgroup, two wavefronts per SIMD) takes the
+// other bf16 X of more than 64 tokens: measured 113 us against k_gemm3's
+// 126-130 us at 512 tokens x 12288 x 6144 (k_gemm4 stays ahead at 2048
+// tokens: 371 against 405 us). Its X offsets are 32-bit.
+static bool gemm_halves(int M, int x_bf16, int K) {
+    return x_bf16 && M > 64 && (size_t)M * (size_t)K * 2 < (1ull << 32);
+}
 
 int gemm_splits(int M, int N, int K, int num_cus, int tile_n) {
     const int bm = gemm_tile_m(M);
@@ -1065,6 +1388,7 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
         (size_t)tiles_b * 3 * nb_sz * kRecordBytes >= (1ull << 32))
         return hipErrorInvalidValue;
     const bool wide = gemm_wide(M, x_bf16, out_b > 0);
+    const bool halves = gemm_halves(M, x_bf16, in_dim) && !wide;
     const int tile_n = wide ? BN4 : kTileN;
     const int tiles_a_w = wide ? (out_a + BN4 - 1) / BN4 : tiles_a;
     const int n_eq = wide ? out_a : (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
@@ -1106,6 +1430,7 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     a.part = reinterpret_cast<float*>(ws + L.part);
     a.err = err;
     const int grid = a.tiles_n * a.tiles_m * ks;
+    if (halves) return launch_timed(kProfGemm, k_gemm5, dim3(grid), dim3(kThreads5), 0, s, a);
     if (wide) return launch_timed(kProfGemm, k_gemm4, dim3(grid), dim3(kThreads4), 0, s, a);
     const dim3 gd(grid), bd(kGemmThreads);
     if (bm == 64)
