@@ -1035,7 +1035,7 @@ struct GemmSmem5 {
     uint8_t tbl[kTbl4 + 16];     // grid * (2s+1), k_gemm4's layout, then the zero entry
     uint8_t xs[2][2][kXStage5];  // [K half][buffer]
     uint8_t wb[2][2][kWHalf5];   // [K half][buffer]: [tile][unit][64 lanes x 16 B]
-    uint8_t wd[2][2][3 * 128];   // [K half][block parity]: [tile][64 fp16]
+    uint8_t wd[2][2][1024];      // [K half][block parity]: [tile][64 fp16] (a whole wavefront's copy)
     int last_flag;
 };
 // the K half 1 sums (128 x 192 fp32) overlay xs and wb
@@ -1065,9 +1065,6 @@ __device__ __forceinline__ half8_t decode_group5(const uint8_t* tbl, uint32_t q,
 __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     constexpr int MT = BM5 / 16;  // token tiles (8)
     constexpr int JT = 3;         // column tiles per wavefront
-    constexpr int kSlots = 256;   // lanes staging one K half
-    constexpr int kXLoads = 4;    // 16-byte X pieces per lane and stage (1024 / 256)
-    constexpr int kWLoads = 3;    // W pieces per lane and half block (576 units + 24 d, of 768)
     __shared__ __attribute__((aligned(16))) GemmSmem5 sm;
 
     const int tid = threadIdx.x;
@@ -1076,7 +1073,6 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     const uint32_t lane = tid & 63;
     const int lr = lane & 15;
     const uint32_t lg = lane >> 4;
-    const int ls = rq * 64 + (int)lane;  // lane slot among the K half's wavefronts
 
     const GemmTile tl = gemm_tile(g_all);
     if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
@@ -1096,74 +1092,55 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     const int steps = nh * (kQK / BK5);
     auto blk_of = [&](int c) { return min(kb0 + c, tl.b1 - 1); };
 
-    // X pieces of this lane: rows (ls >> 3) + 32 i, global chunk ls & 7,
-    // stored at LDS chunk (ls & 7) ^ (row & 7)
-    // (byte offsets from xh: the image is under 4 GiB, as the launch checks)
-    uint32_t xsrc[kXLoads];
+    // Loads go straight from global memory into LDS (global_load_lds_dwordx4:
+    // lane i of a wavefront writes the 16 bytes at the destination + 16 i),
+    // issued at a stage's start and complete at its closing barrier.
+    // X: the stage's 128 rows x 64 columns are 16 pieces of 8 rows; wavefront
+    // rq of the K half copies pieces rq + 4 i. Lane l of a piece fills LDS
+    // chunk l & 7 of row l >> 3 with global chunk (l & 7) ^ (row & 7), the
+    // swizzle the A reads undo. (Byte offsets from xh: the image is under
+    // 4 GiB, as the launch checks.)
+    uint32_t xsrc[4];
 #pragma unroll
-    for (int i = 0; i < kXLoads; ++i)
-        xsrc[i] = ((uint32_t)min(m0 + (ls >> 3) + 32 * i, g.M - 1) * (uint32_t)g.K + (ls & 7) * 8) * 2u;
-    const uint32_t xdst = (uint32_t)(ls >> 3) * 128u + ((uint32_t)((ls & 7) ^ ((ls >> 3) & 7)) << 4);
-    u32x4_t xreg[kXLoads];
-    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(g.xh);
-    auto load_x = [&](int s) {
-        const uint32_t kc = (uint32_t)(blk_of(s >> 2) * kQK + (s & 3) * BK5) * 2u;
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) xreg[i] = *reinterpret_cast<const u32x4_t*>(xbase + (xsrc[i] + kc));
-    };
-    auto store_x = [&](int buf) {
-        uint8_t* dst = sm.xs[kh][buf] + xdst;
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) *reinterpret_cast<u32x4_t*>(dst + i * 32 * 128) = xreg[i];
-    };
-
-    // W pieces of this lane: item ls + 256 k. Items 0..575: unit ui =
-    // item / 64 of the half block (row tile ui / 3, unit ui % 3), lane slot
-    // `lane`; items 576..599: the three tiles' d, stored with a block's
-    // first half only; the rest load a W piece again and store nothing.
-    uint32_t w_goff[kWLoads], w_loff[kWLoads];
-    bool w_isd[kWLoads], w_idle[kWLoads];
-#pragma unroll
-    for (int k = 0; k < kWLoads; ++k) {
-        const int item = ls + kSlots * k;
-        w_isd[k] = false;
-        w_idle[k] = false;
-        if (item < 576) {
-            const int ui = item >> 6, jt = ui / 3, u = ui % 3;
-            const int tile = min(n0 / kTileRows + jt, last_tile);
-            w_goff[k] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + u * kUnitBytes + lane * 16u;
-            w_loff[k] = (uint32_t)ui * kUnitBytes + lane * 16u;
-        } else if (item < 600) {
-            const int e = item - 576, jt = e >> 3;
-            const int tile = min(n0 / kTileRows + jt, last_tile);
-            w_goff[k] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + kRecordDOffset + (e & 7) * 16u;
-            w_loff[k] = (uint32_t)jt * 128u + (e & 7) * 16u;
-            w_isd[k] = true;
-        } else {
-            w_goff[k] = w_goff[0];
-            w_loff[k] = 0;
-            w_idle[k] = true;
-        }
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * (rq + 4 * i) + (int)(lane >> 3);
+        xsrc[i] = ((uint32_t)min(m0 + r, g.M - 1) * (uint32_t)g.K) * 2u + (((lane & 7u) ^ (lane >> 3)) << 4);
     }
-    u32x4_t wreg[kWLoads];
-    // half block hb: block hb >> 1, units 3 (hb & 1) .. +2
-    auto load_w = [&](int hb) {
-        const uint32_t boff = (uint32_t)blk_of(hb >> 1) * kRecordBytes;
-        const uint32_t hoff = (uint32_t)(hb & 1) * 3 * kUnitBytes;
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(g.xh);
+    // X stage s (past the last: the last one's columns again) into buffer s & 1
+    auto load_x = [&](int s) {
+        const int sc = min(s, steps - 1);
+        const uint32_t kc = (uint32_t)(blk_of(sc >> 2) * kQK + (sc & 3) * BK5) * 2u;
+        uint8_t* dst = sm.xs[kh][s & 1];
 #pragma unroll
-        for (int k = 0; k < kWLoads; ++k)
-            wreg[k] = *reinterpret_cast<const u32x4_t*>(g.w + (w_goff[k] + boff + (w_isd[k] ? 0u : hoff)));
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(xbase + (xsrc[i] + kc), dst + (rq + 4 * i) * 1024, 16, 0, 0);
     };
-    auto store_w = [&](int hb) {
+    // W half block hb (block hb >> 1, units 3 (hb & 1) .. +2 of the three row
+    // tiles: 9 units of 1 KiB): wavefront rq copies units rq + 4 k; at a
+    // block's first half, wavefront 3 also copies the tiles' d (lanes 0..23;
+    // the other lanes repeat lane 23's piece).
+    uint32_t wsrc[3];
 #pragma unroll
-        for (int k = 0; k < kWLoads; ++k) {
-            if (w_idle[k]) continue;
-            if (w_isd[k]) {
-                if ((hb & 1) == 0) *reinterpret_cast<u32x4_t*>(sm.wd[kh][(hb >> 1) & 1] + w_loff[k]) = wreg[k];
-            } else {
-                *reinterpret_cast<u32x4_t*>(sm.wb[kh][hb & 1] + w_loff[k]) = wreg[k];
-            }
-        }
+    for (int k = 0; k < 3; ++k) {
+        const int ui = min(rq + 4 * k, 8);
+        const int tile = min(n0 / kTileRows + ui / 3, last_tile);
+        wsrc[k] = (uint32_t)tile * (uint32_t)g.nb * kRecordBytes + (ui % 3) * kUnitBytes + lane * 16u;
+    }
+    const uint32_t dl = min(lane, 23u);
+    const uint32_t dsrc = (uint32_t)min(n0 / kTileRows + (int)(dl >> 3), last_tile) * (uint32_t)g.nb * kRecordBytes +
+                          kRecordDOffset + (dl & 7u) * 16u;
+    // (past the last half block: the last block's units again)
+    auto load_w = [&](int hb) {
+        const uint32_t boff = (uint32_t)blk_of(min(hb, 2 * nh - 1) >> 1) * kRecordBytes;
+        const uint32_t hoff = (uint32_t)(hb & 1) * 3 * kUnitBytes;
+        uint8_t* dst = sm.wb[kh][hb & 1];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            if (rq + 4 * k < 9) __builtin_amdgcn_global_load_lds(g.w + (wsrc[k] + boff + hoff), dst + (rq + 4 * k) * 1024, 16, 0, 0);
+        if ((hb & 1) == 0 && rq == 3)
+            __builtin_amdgcn_global_load_lds(g.w + (dsrc + boff), &sm.wd[0][0][0] + (kh * 2 + ((hb >> 1) & 1)) * 1024,
+                                             16, 0, 0);
     };
 
     // this lane's rows j < JT: lane slot in the staged half block, and d
@@ -1231,48 +1208,37 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
         }
     };
 
-    // prologue: X stage 0 and W half block 0 (with block 0's d) in LDS, X
-    // stage 1 and W half block 1 in registers; block 0's d and the B
-    // operands of its first sub-block
+    // prologue: X stage 0 and W half block 0 (with block 0's d) in LDS;
+    // block 0's d and the B operands of its first sub-block
     load_x(0);
     load_w(0);
-    store_x(0);
-    store_w(0);
-    load_x(min(1, steps - 1));
-    load_w(min(1, 2 * nh - 1));
-    __syncthreads();  // table, X stage 0, W half block 0
+    __syncthreads();  // table, X stage 0, W half block 0 with block 0's d
     block_d(0);
 #pragma unroll
     for (int j = 0; j < JT; ++j) dcur[j] = dnext[j];  // the accumulators are zero
     half8_t bop[2][JT];
     decode(bop[0], 0, 0);
 
+    // Stage s: the loads of X(s + 1) (and at a half block's first stage of
+    // W(hb + 1)) into the buffers last read in stage s - 1, before its
+    // barrier; the MFMAs of its two sub-blocks; under the first, the B
+    // operands of the second are decoded, under the second those of stage
+    // s + 1's first sub-block (its W half block is in LDS already; after a
+    // block's last stage, with the next block's d). Past the last stage the
+    // same steps run on clamped blocks and their results go unused, so a
+    // stage has no branch.
     for (int c = 0; c < nh; ++c) {
         static_for<0, 4>([&](auto Uc) {
             constexpr int U = decltype(Uc)::value;
             const int s = 4 * c + U;
-            // X(s + 1) to LDS, X(s + 2) into the registers
-            if (s + 1 < steps) {
-                store_x((s + 1) & 1);
-                load_x(min(s + 2, steps - 1));
-            }
-            // at a half block's first stage: W(hb + 1) to LDS, W(hb + 2) into the registers
-            if constexpr ((U & 1) == 0) {
-                const int hb = s >> 1;
-                if (hb + 1 < 2 * nh) {
-                    store_w(hb + 1);
-                    load_w(min(hb + 2, 2 * nh - 1));
-                }
-            }
+            load_x(s + 1);
+            if constexpr ((U & 1) == 0) load_w((s >> 1) + 1);
             const uint8_t* xa = arow + (s & 1) * kXStage5;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                // the next sub-block's operands: this stage's second, or the
-                // next stage's first (its W half block is in LDS already;
-                // after a block's last stage, with the next block's d)
                 if (t == 0) {
                     decode(bop[1], (s >> 1) & 1, 2 * U + 1);
-                } else if (s + 1 < steps) {
+                } else {
                     if constexpr (U == 3) block_d(c + 1);
                     decode(bop[0], ((s + 1) >> 1) & 1, (2 * U + 2) & 7);
                 }
