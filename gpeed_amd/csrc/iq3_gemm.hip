@@ -1029,10 +1029,10 @@ constexpr int BM5 = 128, BN5 = 192, BK5 = 64;
 constexpr int kThreads5 = 512;
 constexpr int kXStage5 = BM5 * BK5 * 2;          // 16 KiB: 128 rows x 128 bytes
 constexpr int kWHalf5 = 3 * 3 * kUnitBytes;      // 9 KiB: 3 row tiles x 3 units
-constexpr uint32_t kZeroEntry5 = kTbl4;          // 8 zero bytes after the scaled grid
+constexpr uint32_t kZeroEntry5 = kTbl4;          // 2 KiB of zeros after the scaled grid
 
 struct GemmSmem5 {
-    uint8_t tbl[kTbl4 + 16];     // grid * (2s+1), k_gemm4's layout, then the zero entry
+    uint8_t tbl[kTbl4 + 2048];   // grid * (2s+1) as [s][idx], then a zero "scale"
     uint8_t xs[2][2][kXStage5];  // [K half][buffer]
     uint8_t wb[2][2][kWHalf5];   // [K half][buffer]: [tile][unit][64 lanes x 16 B]
     uint8_t wd[2][2][1024];      // [K half][block parity]: [tile][64 fp16] (a whole wavefront's copy)
@@ -1041,20 +1041,38 @@ struct GemmSmem5 {
 // the K half 1 sums (128 x 192 fp32) overlay xs and wb
 static_assert(2 * 2 * kXStage5 + 2 * 2 * kWHalf5 >= 128 * 192 * 4, "reduction area");
 
+// Entry (idx, s) = 4 fp16 values grid(idx)[0..3] * (2s+1), at (s << 11) |
+// (idx << 3): the bank of a lookup follows the index's low five bits, so
+// the four lanes that decode one row (same s) spread like any others. A
+// workgroup of NTHR threads writes it.
+template <int NTHR>
+__device__ __forceinline__ void scaled_grid_table5(uint8_t* tbl, int tid) {
+#pragma unroll 2
+    for (int i = 0; i < 4096 / NTHR; ++i) {
+        const uint32_t e = (uint32_t)tid + NTHR * i, idx = e & 255u, s = e >> 8;
+        const float m = (float)(2 * s + 1);
+        const uint32_t v = kIq3xxsGrid[idx];
+        const uint32_t lo = f16_pair_of_floats((float)(v & 255u) * m, (float)((v >> 8) & 255u) * m);
+        const uint32_t hi = f16_pair_of_floats((float)((v >> 16) & 255u) * m, (float)(v >> 24) * m);
+        *reinterpret_cast<u32x2_t*>(tbl + (s << 11) + (idx << 3)) = u32x2_t{lo, hi};
+    }
+}
+
 // B operand (group lg of a sub-block of one W row) from its grid-index word q
-// (bytes p0, p0+1) and sign/scale word w, as decode_group4; the table
-// offsets (idx << 7) | (s << 3) come from aligning the index byte with w
-// (whose top four bits are s), and a row with amask = 0, azero =
-// kZeroEntry5 reads the zero entry instead.
+// (bytes p0, p0+1) and sign/scale word w, as decode_group4, from the
+// [s][idx] table: the scale's 2 KiB row at (s << 11) comes from rotating w
+// (whose top four bits are s) right by 17; a row with smask = 0, szero =
+// kZeroEntry5 reads the zero row instead.
 __device__ __forceinline__ half8_t decode_group5(const uint8_t* tbl, uint32_t q, uint32_t w, uint32_t lg,
-                                                 uint32_t p0, uint32_t amask, uint32_t azero) {
+                                                 uint32_t p0, uint32_t smask, uint32_t szero) {
     const uint32_t sw = t64_signs(w);
     const uint32_t wg = __builtin_amdgcn_alignbit(sw, sw, lg);
     const uint64_t sw2 = ((uint64_t)(wg >> 4) << 32) | wg;
     const uint64_t r01 = shl64<15>(sw2), r23 = shl64<7>(sw2);
+    const uint32_t srow = (__builtin_amdgcn_alignbit(w, w, 17) & smask) | szero;
     const uint32_t i0 = __builtin_amdgcn_ubfe(q, 8 * p0, 8), i1 = __builtin_amdgcn_ubfe(q, 8 * p0 + 8, 8);
-    const uint32_t a0 = (__builtin_amdgcn_alignbit(i0, w, 25) & amask) | azero;
-    const uint32_t a1 = (__builtin_amdgcn_alignbit(i1, w, 25) & amask) | azero;
+    const uint32_t a0 = (i0 << 3) | srow;
+    const uint32_t a1 = (i1 << 3) | srow;
     const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + a0);
     const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(tbl + a1);
     const u32x4_t r = {((uint32_t)r01 & 0x80008000u) | g0.x, ((uint32_t)(r01 >> 32) & 0x80008000u) | g0.y,
@@ -1080,8 +1098,6 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     const GemmArgs g = gemm_tensor(g_all, tl, tn);
     const int m0 = tl.tm * BM5, n0 = tn * BN5;
     const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
-    scaled_grid_table4<kThreads5>(sm.tbl, tid);
-    if (tid < 4) reinterpret_cast<uint32_t*>(sm.tbl + kZeroEntry5)[tid] = 0u;
 
     // K halves: blocks [b0 + kh * nh, ...) of this split, nh per half (the
     // second half of an odd count has one block fewer: its last block is
@@ -1178,7 +1194,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
                 live ? (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(&sm.wd[kh][c & 1][d_off[j]]))
                      : 0.0f;
             const bool z = dn == 0.0f;
-            amask[j] = z ? 0u : 0x7FF8u;
+            amask[j] = z ? 0u : 0x7800u;
             azero[j] = z ? kZeroEntry5 : 0u;
             dnext[j] = dn;
         }
@@ -1212,6 +1228,10 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     // block 0's d and the B operands of its first sub-block
     load_x(0);
     load_w(0);
+    // the table is built while the first copies are in flight
+    scaled_grid_table5<kThreads5>(sm.tbl, tid);
+    static_assert(kThreads5 * 4 == 2048, "one word of the zero row per thread");
+    reinterpret_cast<uint32_t*>(sm.tbl + kZeroEntry5)[tid] = 0u;
     __syncthreads();  // table, X stage 0, W half block 0 with block 0's d
     block_d(0);
 #pragma unroll
@@ -1277,7 +1297,43 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
 #pragma unroll
             for (int j = 0; j < JT; ++j) acc[mt][j] += red[(mt * JT + j) * 64];
     }
-    gemm_store<MT, JT, kTileN, kThreads5>(g, tl, acc, m0, n0, rq * 48, lr, (int)lg, tid, &sm.last_flag, kh == 0);
+    if (g.ks > 1) {
+        gemm_store<MT, JT, kTileN, kThreads5>(g, tl, acc, m0, n0, rq * 48, lr, (int)lg, tid, &sm.last_flag, kh == 0);
+        return;
+    }
+    // One K split: the K half 0 wavefronts leave the tile in LDS as rows of
+    // 192 floats (stride 196: the four token rows a store instruction touches
+    // fall on different banks), then every thread copies whole rows out,
+    // times the token's unscale, 16 bytes at a time.
+    constexpr int kTStride = BN5 + 4;
+    static_assert(BM5 * kTStride * 4 <= 2 * 2 * kXStage5 + 2 * 2 * kWHalf5, "output tile area");
+    float* tile = reinterpret_cast<float*>(&sm.xs[0][0][0]);
+    __syncthreads();  // the K half 1 sums are read
+    if (kh == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < JT; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    tile[(mt * 16 + (int)lg * 4 + i) * kTStride + rq * 48 + j * 16 + lr] = acc[mt][j][i];
+    }
+    __syncthreads();
+    const int rows = min(BM5, g.M - m0), cols = min(BN5, g.N - n0);
+    const bool vec = (g.N & 3) == 0 && (reinterpret_cast<uintptr_t>(g.y) & 15u) == 0;
+    for (int f = tid; f < rows * (BN5 / 4); f += kThreads5) {
+        const int m = f / (BN5 / 4), c4 = (f - m * (BN5 / 4)) * 4;
+        if (c4 >= cols) continue;
+        const float us = g.unscale[m0 + m];
+        const float4 v = *reinterpret_cast<const float4*>(&tile[m * kTStride + c4]);
+        float* yrow = g.y + (size_t)(m0 + m) * g.N + n0 + c4;
+        if (vec && c4 + 4 <= cols) {
+            *reinterpret_cast<float4*>(yrow) = float4{v.x * us, v.y * us, v.z * us, v.w * us};
+        } else {
+            const float o[4] = {v.x * us, v.y * us, v.z * us, v.w * us};
+            for (int e = 0; e < 4 && c4 + e < cols; ++e) yrow[e] = o[e];
+        }
+    }
 }
 
 }  // namespace
