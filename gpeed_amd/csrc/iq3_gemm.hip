@@ -10,13 +10,13 @@
 // image and an fp16 lo image, two MFMAs per step). Products are exact; sums
 // are fp32 in v_mfma_f32_16x16x32_f16.
 //
-// Tiling. A 256-thread workgroup computes 128 tokens x 192 W rows; wavefront
-// w owns rows 48w..48w+47 (3 column tiles) for all 8 token tiles, so every W
-// value is decoded exactly once per workgroup, straight into the MFMA B
-// operand registers. Workgroups are ordered so that the eight XCDs each
-// work on their own band of W rows (the band stays in that XCD's L2 while
-// all token tiles use it). k_gemm3 (bf16 X) and k_gemm2 (fp32 X) differ in
-// how W and X reach the wavefronts; see each kernel.
+// Tiling. A workgroup computes 128 (or 64) tokens x 192 W rows and decodes
+// every W value of its rows exactly once, straight into MFMA B operand
+// registers. Workgroups are ordered so that the eight XCDs each work on
+// their own band of W rows (the band stays in that XCD's L2 while all token
+// tiles use it). k_gemm5 (bf16 X, more than 64 tokens), k_gemm3 (64-token
+// tiles) and k_gemm2 (fp32 X) differ in how the wavefronts split the tile
+// and how W and X reach them; see each kernel.
 #include <type_traits>
 
 #include "iq3_common.h"
@@ -754,285 +754,42 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
 
 
 // ---------------------------------------------------------------------------
-// GEMM, two wavefronts per SIMD (one X image: bf16 input). A 512-thread
-// workgroup computes 128 tokens x 384 W rows; wavefront w owns rows
-// 48w..48w+47 (3 column tiles of v_mfma_f32_16x16x32_f16) and all 8 token
-// tiles, so every W value is still decoded once per workgroup, and the
-// eight wavefronts of the CU's one workgroup give each SIMD two to switch
-// between. What makes that fit:
-//   * one accumulator: the partial of a 256-wide block is not kept apart
-//     to be scaled by its d; instead the accumulator holds the sum in
-//     units of a running d (the last nonzero one of the row). When a block's
-//     d differs, the accumulator is rescaled by d_old / d_new before the
-//     block's MFMAs; a block with d = 0 contributes zeros (its B operands
-//     are cleared); the end multiplies by d/4. Products stay exact (B is
-//     +-grid*(2s+1) in fp16), the rescales add one rounding per change of d;
-//   * little register staging: a wavefront moves 2 KiB of each X stage and
-//     5 KiB of each W block through registers into LDS (16-byte loads and
-//     stores), X rows swizzled by 16-byte chunk (chunk c of row m at
-//     c ^ (m & 7)) so the A reads do not conflict;
-//   * the grid table with (2s+1) folded in (entry (idx, s) at
-//     (idx << 7) | (s << 3)) in one replica: 32 KiB.
-// X: a ring of three 64-column stages in LDS, each loaded into registers
-// two stages before it is stored (four before its use); W: whole
-// blocks of the six row tiles (36 KiB, 6 units each, with their d), loaded
-// at the start of the previous block and stored two stages later. One
-// workgroup barrier per stage.
-
-constexpr int BM4 = 128, BN4 = 384, BK4 = 64;
-constexpr int kThreads4 = 512;
-constexpr int kXStage4 = BM4 * BK4 * 2;                 // 16 KiB: 128 rows x 128 bytes
-constexpr int kWTiles4 = BN4 / kTileRows;               // 6 row tiles
-constexpr int kWBlk4 = kWTiles4 * 6 * kUnitBytes;       // 36 KiB
-constexpr int kTbl4 = 256 * 16 * 8;                     // 32 KiB
-constexpr int kXLoads4 = kXStage4 / 1024 / 8;           // X loads per wavefront and stage (2)
-constexpr int kWLoads4 = 5;                             // W loads per wavefront and block (36 units + d, of 40)
-
-struct GemmSmem4 {
-    uint8_t tbl[kTbl4];
-    uint8_t xs[3][kXStage4];
-    uint8_t wb[2][kWBlk4];
-    uint8_t wd[2][kWTiles4 * 128];
-    int last_flag;
-};
-
-// Entry (idx, s) = 4 fp16 values grid(idx)[0..3] * (2s+1), at (idx << 7) | (s << 3),
-// written by a workgroup of NTHR threads.
-template <int NTHR = 512>
-__device__ __forceinline__ void scaled_grid_table4(uint8_t* tbl, int tid) {
-    const uint32_t s = tid & 15;
-    const float m = (float)(2 * s + 1);
-#pragma unroll 2
-    for (int i = 0; i < 4096 / NTHR; ++i) {
-        const uint32_t idx = (tid >> 4) + (NTHR / 16) * i;
-        const uint32_t v = kIq3xxsGrid[idx];
-        const uint32_t lo = f16_pair_of_floats((float)(v & 255u) * m, (float)((v >> 8) & 255u) * m);
-        const uint32_t hi = f16_pair_of_floats((float)((v >> 16) & 255u) * m, (float)(v >> 24) * m);
-        *reinterpret_cast<u32x2_t*>(tbl + (idx << 7) + (s << 3)) = u32x2_t{lo, hi};
-    }
-}
-
-// B operand (group lg of a sub-block of one W row) from its grid-index word q
-// (bytes p0, p0+1) and sign/scale word w, as decode_group with the
-// one-replica table.
-__device__ __forceinline__ half8_t decode_group4(const uint8_t* tbl, uint32_t q, uint32_t w, uint32_t lg,
-                                                 uint32_t p0) {
-    const uint32_t sw = t64_signs(w);
-    const uint32_t wg = __builtin_amdgcn_alignbit(sw, sw, lg);
-    const uint64_t sw2 = ((uint64_t)(wg >> 4) << 32) | wg;
-    const uint64_t r01 = shl64<15>(sw2), r23 = shl64<7>(sw2);
-    const uint32_t s3 = (w >> 25) & 0x78u;  // s << 3
-    const uint32_t i0 = __builtin_amdgcn_ubfe(q, 8 * p0, 8), i1 = __builtin_amdgcn_ubfe(q, 8 * p0 + 8, 8);
-    const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + ((i0 << 7) | s3));
-    const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(tbl + ((i1 << 7) | s3));
-    const u32x4_t r = {((uint32_t)r01 & 0x80008000u) | g0.x, ((uint32_t)(r01 >> 32) & 0x80008000u) | g0.y,
-                       ((uint32_t)r23 & 0x80008000u) | g1.x, ((uint32_t)(r23 >> 32) & 0x80008000u) | g1.y};
-    return __builtin_bit_cast(half8_t, r);
-}
-
-__global__ __launch_bounds__(kThreads4) void k_gemm4(GemmArgs g_all) {
-    constexpr int MT = BM4 / 16;
-    __shared__ __attribute__((aligned(16))) GemmSmem4 sm;
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t lane = tid & 63;
-    const int lr = lane & 15;
-    const uint32_t lg = lane >> 4;
-
-    const GemmTile tl = gemm_tile(g_all);
-    if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
-    int tn;
-    const GemmArgs g = gemm_tensor(g_all, tl, tn);
-    const int m0 = tl.tm * BM4, n0 = tn * BN4;
-    const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
-    scaled_grid_table4(sm.tbl, tid);
-
-    // X pieces of this thread: rows 16 wave + 8 i + lane / 8, LDS chunk
-    // lane & 7 holding global chunk (lane & 7) ^ (row & 7)
-    const _Float16* xsrc[kXLoads4];
-#pragma unroll
-    for (int i = 0; i < kXLoads4; ++i) {
-        const int r = 16 * wave + 8 * i + (int)(lane >> 3);
-        const int c = (int)(lane & 7) ^ (r & 7);
-        xsrc[i] = g.xh + (size_t)min(m0 + r, g.M - 1) * g.K + tl.b0 * kQK + c * 8;
-    }
-    const uint32_t xdst = (uint32_t)(16 * wave) * 128u + lane * 16u;  // + i * 1024
-    u32x4_t xreg[2][kXLoads4];
-    auto load_x = [&](u32x4_t (&r)[kXLoads4], int s) {
-#pragma unroll
-        for (int i = 0; i < kXLoads4; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + s * BK4);
-    };
-    auto store_x = [&](const u32x4_t (&r)[kXLoads4], int buf) {
-#pragma unroll
-        for (int i = 0; i < kXLoads4; ++i) *reinterpret_cast<u32x4_t*>(sm.xs[buf] + xdst + i * 1024) = r[i];
-    };
-    // W loads: item wave + 8 k (k < 5) of 40: items 0..35 the six tiles' six
-    // units, 36..39 their d (lanes 0..47, 16 bytes each; 37..39 repeat 36)
-    const uint8_t* wsrc[kWLoads4];
-    uint32_t wdst[kWLoads4];  // LDS offset in wb[buf], or kWBlk4 + offset in wd[buf]
-#pragma unroll
-    for (int k = 0; k < kWLoads4; ++k) {
-        const int item = wave + 8 * k;
-        if (item < 36) {
-            const int jt = item / 6, u = item % 6;
-            const int tile = min(n0 / kTileRows + jt, last_tile);
-            wsrc[k] = g.w + ((size_t)tile * g.nb + tl.b0) * kRecordBytes + u * kUnitBytes + lane * 16;
-            wdst[k] = (uint32_t)(jt * 6 + u) * kUnitBytes + lane * 16u;
-        } else {
-            const uint32_t l = min(lane, 47u);  // lanes 48..63 repeat lane 47
-            const int tile = min(n0 / kTileRows + (int)(l >> 3), last_tile);
-            wsrc[k] = g.w + ((size_t)tile * g.nb + tl.b0) * kRecordBytes + kRecordDOffset + (l & 7) * 16;
-            wdst[k] = kWBlk4 + l * 16u;
-        }
-    }
-    u32x4_t wreg[kWLoads4];
-    auto load_w = [&](int b) {
-        const size_t boff = (size_t)b * kRecordBytes;
-#pragma unroll
-        for (int k = 0; k < kWLoads4; ++k) wreg[k] = *reinterpret_cast<const u32x4_t*>(wsrc[k] + boff);
-    };
-    auto store_w = [&](int buf) {
-#pragma unroll
-        for (int k = 0; k < kWLoads4; ++k) {
-            uint8_t* dst = wdst[k] < (uint32_t)kWBlk4 ? sm.wb[buf] + wdst[k] : sm.wd[buf] + (wdst[k] - kWBlk4);
-            *reinterpret_cast<u32x4_t*>(dst) = wreg[k];
-        }
-    };
-
-    // this lane's rows j = 0..2: their lane slot in the block copy and d
-    uint32_t w_rowoff[3], d_off[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int r = wave * 48 + j * 16 + lr;
-        w_rowoff[j] = (uint32_t)(r >> 6) * 6 * kUnitBytes + (uint32_t)(r & 63) * 16u;
-        d_off[j] = (uint32_t)(r >> 6) * 128u + (uint32_t)(r & 63) * 2u;
-    }
-    const uint32_t p0 = 2 * (lg & 1);
-    const bool hiq = lg >= 2;
-    // A operand reads: row mt*16 + lr, chunk t*4 + lg, swizzled
-    uint32_t a_off[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) a_off[t] = (uint32_t)lr * 128u + ((uint32_t)((t * 4 + (int)lg) ^ (lr & 7)) << 4);
-
-    float4_t acc[MT][3];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float dcur[3] = {0.0f, 0.0f, 0.0f};
-
-    const int nblk = tl.b1 - tl.b0;
-    const int steps = nblk * (kQK / BK4);
-    // prologue: X stages 0, 1 and W block 0 in LDS, X stages 2, 3 in registers
-    load_x(xreg[0], 0);
-    load_x(xreg[1], min(1, steps - 1));
-    load_w(0);
-    store_x(xreg[0], 0);
-    store_x(xreg[1], 1);
-    store_w(0);
-    load_x(xreg[0], min(2, steps - 1));
-    load_x(xreg[1], min(3, steps - 1));
-    __syncthreads();  // table, X stages 0 and 1, W block 0
-
-    int xb = 0;  // X buffer of stage s: s % 3
-    for (int c = 0; c < nblk; ++c) {
-        const uint8_t* wb = sm.wb[c & 1];
-        // the block's d: rescale the accumulators to it, or clear the B
-        // operands of rows whose block is zero
-        uint32_t zmask[3];
-        bool any_zero = false;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const float dn = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(&sm.wd[c & 1][d_off[j]]));
-            const bool z = dn == 0.0f;
-            zmask[j] = z ? 0u : 0xFFFFFFFFu;
-            any_zero |= z;
-            if (!z && dn != dcur[j]) {
-                const float r = dcur[j] == 0.0f ? 0.0f : dcur[j] / dn;
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= r;
-                dcur[j] = dn;
-            }
-        }
-        const bool zero_rows = __builtin_amdgcn_ballot_w64(any_zero) != 0;  // uniform
-        static_for<0, 4>([&](auto Uc) {
-            constexpr int U = decltype(Uc)::value;
-            const int s = 4 * c + U;
-            const int xb2 = xb == 0 ? 2 : xb - 1;  // (s + 2) % 3, the buffer of stage s - 1
-            // X(s + 2), loaded at stage s - 2, goes to LDS; X(s + 4) takes its
-            // registers
-            store_x(xreg[U & 1], xb2);
-            load_x(xreg[U & 1], min(s + 4, steps - 1));
-            if constexpr (U == 0) load_w(min(c + 1, nblk - 1));
-            const uint8_t* xs = sm.xs[xb];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int ib = 2 * U + t;
-                const int dq = 3 * ib + (hiq ? 1 : 0), dw = 3 * ib + 2;
-                const uint32_t oq = (uint32_t)(dq >> 2) * kUnitBytes + (dq & 3) * 4;
-                const uint32_t ow = (uint32_t)(dw >> 2) * kUnitBytes + (dw & 3) * 4;
-                half8_t bop[3];
-#pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const uint32_t q = *reinterpret_cast<const uint32_t*>(wb + w_rowoff[j] + oq);
-                    const uint32_t w = *reinterpret_cast<const uint32_t*>(wb + w_rowoff[j] + ow);
-                    bop[j] = decode_group4(sm.tbl, q, w, lg, p0);
-                    if (zero_rows) {
-                        u32x4_t v = __builtin_bit_cast(u32x4_t, bop[j]);
-                        v &= zmask[j];
-                        bop[j] = __builtin_bit_cast(half8_t, v);
-                    }
-                }
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const half8_t a = *reinterpret_cast<const half8_t*>(xs + mt * 16 * 128 + a_off[t]);
-#pragma unroll
-                    for (int j = 0; j < 3; ++j)
-                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop[j], acc[mt][j], 0, 0, 0);
-                }
-            }
-            if constexpr (U == 2) store_w((c + 1) & 1);
-            __syncthreads();
-            xb = xb == 2 ? 0 : xb + 1;
-        });
-    }
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const float f = dcur[j] * 0.25f;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= f;
-    }
-    gemm_store<MT, 3, BN4, kThreads4>(g, tl, acc, m0, n0, wave * 48, lr, (int)lg, tid, &sm.last_flag);
-}
-
-// ---------------------------------------------------------------------------
-// GEMM, K-halves form (one X image: bf16 input). k_gemm3's workgroup tile
-// (128 tokens x 192 W rows) on 512 threads: wavefront w owns rows
-// 48 (w & 3) .. +47 (3 column tiles of v_mfma_f32_16x16x32_f16, all 8 token
-// tiles) over the blocks of K half kh = w >> 2, so every SIMD runs two
-// wavefronts and every W value is still decoded once per workgroup. The 96
-// accumulators run in units of the row's running d, as in k_gemm4. Each K
-// half has its own double-buffered rings in LDS, filled by its own four
-// wavefronts: 64-column X stages (rows swizzled by 16-byte chunk,
-// register-staged one stage ahead) and W half blocks (units 0-2 or 3-5 of
-// the three row tiles, i.e. 4 sub-blocks, register-staged two stages
-// ahead) with the blocks' d. The B operands of a sub-block are decoded
-// while the MFMAs of the previous one run (W is in LDS two stages ahead, so
-// the next stage's operands are decoded before the barrier that ends this
-// one); rows whose block has d = 0 read a zero table entry. One workgroup
-// barrier per stage. At the end the K half 1 wavefronts leave their sums in
-// LDS and the K half 0 wavefronts add them (half 0 + half 1, fixed order)
-// and store the tile.
+// GEMM, K-halves form (one X image: bf16 input; every bf16 X of more than
+// 64 tokens). k_gemm3's workgroup tile (128 tokens x 192 W rows) on 512
+// threads: wavefront w owns rows 48 (w & 3) .. +47 (3 column tiles of
+// v_mfma_f32_16x16x32_f16, all 8 token tiles) over the blocks of K half
+// kh = w >> 2, so every SIMD runs two wavefronts and every W value is still
+// decoded once per workgroup.
+//   * One accumulator per output: the partial of a 256-wide block is not
+//     kept apart to be scaled by its d; the accumulator holds the sum in
+//     units of a running d (the row's last nonzero one). When a block's d
+//     differs, the accumulator is rescaled by d_old / d_new before the
+//     block's MFMAs; the end multiplies by d/4. Products stay exact (B is
+//     +-grid*(2s+1) in fp16); each change of d adds one rounding.
+//   * Each K half has its own double-buffered rings in LDS, filled by its
+//     own four wavefronts with copies straight from global memory
+//     (global_load_lds_dwordx4): 64-column X stages (rows swizzled by
+//     16-byte chunk) and W half blocks (units 0-2 or 3-5 of the three row
+//     tiles, i.e. 4 sub-blocks) with the blocks' d. One workgroup barrier
+//     per stage, which also waits for the copies.
+//   * The B operands of a sub-block are decoded while the MFMAs of the
+//     previous one run (W is in LDS a stage ahead, so the next stage's
+//     operands are decoded before the barrier that ends this one), from a
+//     grid table with 2s+1 folded in; rows whose block has d = 0 read a zero
+//     row of the table.
+//   * At the end the K half 1 wavefronts leave their sums in LDS, the K half
+//     0 wavefronts add them (half 0 + half 1, fixed order) and lay the tile
+//     out in LDS by rows, and all threads store it with 16-byte stores.
 
 constexpr int BM5 = 128, BN5 = 192, BK5 = 64;
 constexpr int kThreads5 = 512;
 constexpr int kXStage5 = BM5 * BK5 * 2;          // 16 KiB: 128 rows x 128 bytes
 constexpr int kWHalf5 = 3 * 3 * kUnitBytes;      // 9 KiB: 3 row tiles x 3 units
-constexpr uint32_t kZeroEntry5 = kTbl4;          // 2 KiB of zeros after the scaled grid
+constexpr int kTbl5 = 16 * 256 * 8;              // 32 KiB: the grid times every 2s+1
+constexpr uint32_t kZeroEntry5 = kTbl5;          // 2 KiB of zeros after the scaled grid
 
 struct GemmSmem5 {
-    uint8_t tbl[kTbl4 + 2048];   // grid * (2s+1) as [s][idx], then a zero "scale"
+    uint8_t tbl[kTbl5 + 2048];   // grid * (2s+1) as [s][idx], then a zero "scale"
     uint8_t xs[2][2][kXStage5];  // [K half][buffer]
     uint8_t wb[2][2][kWHalf5];   // [K half][buffer]: [tile][unit][64 lanes x 16 B]
     uint8_t wd[2][2][1024];      // [K half][block parity]: [tile][64 fp16] (a whole wavefront's copy)
@@ -1058,9 +815,10 @@ __device__ __forceinline__ void scaled_grid_table5(uint8_t* tbl, int tid) {
     }
 }
 
-// B operand (group lg of a sub-block of one W row) from its grid-index word q
-// (bytes p0, p0+1) and sign/scale word w, as decode_group4, from the
-// [s][idx] table: the scale's 2 KiB row at (s << 11) comes from rotating w
+// B operand of v_mfma_f32_16x16x32_f16 for one lane: the 8 weights of group
+// lg (columns 8lg..8lg+7 of a sub-block) of one W row, as fp16
+// +-grid*(2s+1), from its grid-index word q (bytes p0, p0+1) and sign/scale
+// word w, looked up in the [s][idx] table: the scale's 2 KiB row at (s << 11) comes from rotating w
 // (whose top four bits are s) right by 17; a row with smask = 0, szero =
 // kZeroEntry5 reads the zero row instead.
 __device__ __forceinline__ half8_t decode_group5(const uint8_t* tbl, uint32_t q, uint32_t w, uint32_t lg,
@@ -1343,17 +1101,11 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
 // Token rows per result tile: 64 for at most 64 tokens (no padding), else 128.
 int gemm_tile_m(int M) { return M <= 64 ? 64 : 128; }
 
-// k_gemm4 (384-row tiles, two wavefronts per SIMD) takes bf16 X of at least
-// 1024 tokens, one tensor: measured 377 us against k_gemm3's 470 us at 2048
-// tokens x 12288 x 6144, and no faster at 512 tokens (135 against 133 us),
-// where the K split its larger tiles need costs what the second wavefront
-// gains.
-static bool gemm_wide(int M, int x_bf16, bool two_tensors) { return x_bf16 && M >= 1024 && !two_tensors; }
-
-// k_gemm5 (K halves inside the workgroup, two wavefronts per SIMD) takes the
-// other bf16 X of more than 64 tokens: measured 113 us against k_gemm3's
-// 126-130 us at 512 tokens x 12288 x 6144 (k_gemm4 stays ahead at 2048
-// tokens: 371 against 405 us). Its X offsets are 32-bit.
+// k_gemm5 (K halves inside the workgroup, two wavefronts per SIMD) takes
+// bf16 X of more than 64 tokens: measured at 12288 x 6144, 97.6 us against
+// k_gemm3's 126-130 us at 512 tokens, and 344 us at 2048 tokens against 356 us
+// for a 384-row, 8-wavefront form with the full K per wavefront (removed).
+// Its X offsets are 32-bit.
 static bool gemm_halves(int M, int x_bf16, int K) {
     return x_bf16 && M > 64 && (size_t)M * (size_t)K * 2 < (1ull << 32);
 }
@@ -1389,12 +1141,7 @@ GemmWs gemm_ws(int M, int N, int K, int x_bf16, int ks, int tile_n = kTileN) {
 }  // namespace
 
 size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus) {
-    size_t b = gemm_ws(M, N, K, x_bf16, gemm_splits(M, N, K, num_cus)).total;
-    if (gemm_wide(M, x_bf16, false)) {
-        const size_t b4 = gemm_ws(M, N, K, x_bf16, gemm_splits(M, N, K, num_cus, BN4), BN4).total;
-        b = b4 > b ? b4 : b;
-    }
-    return b;
+    return gemm_ws(M, N, K, x_bf16, gemm_splits(M, N, K, num_cus)).total;
 }
 
 hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, const uint8_t* wb,
@@ -1409,19 +1156,16 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     if ((size_t)tiles_a * 3 * nb_sz * kRecordBytes >= (1ull << 32) ||
         (size_t)tiles_b * 3 * nb_sz * kRecordBytes >= (1ull << 32))
         return hipErrorInvalidValue;
-    const bool wide = gemm_wide(M, x_bf16, out_b > 0);
-    const bool halves = gemm_halves(M, x_bf16, in_dim) && !wide;
-    const int tile_n = wide ? BN4 : kTileN;
-    const int tiles_a_w = wide ? (out_a + BN4 - 1) / BN4 : tiles_a;
-    const int n_eq = wide ? out_a : (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
-    const int ks = gemm_splits(M, n_eq, in_dim, num_cus, tile_n);
-    const GemmWs L = gemm_ws(M, n_eq, in_dim, x_bf16, ks, tile_n);
+    const bool halves = gemm_halves(M, x_bf16, in_dim);
+    const int n_eq = (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
+    const int ks = gemm_splits(M, n_eq, in_dim, num_cus, kTileN);
+    const GemmWs L = gemm_ws(M, n_eq, in_dim, x_bf16, ks);
     _Float16* xh = reinterpret_cast<_Float16*>(ws + L.img);
     float* uns = reinterpret_cast<float*>(ws + L.uns);
     const int bm = gemm_tile_m(M);
     const int tiles_m = (M + bm - 1) / bm;
     uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
-    const int n_cnt = ks > 1 ? tiles_m * (wide ? tiles_a_w : tiles_a + tiles_b) : 0;
+    const int n_cnt = ks > 1 ? tiles_m * (tiles_a + tiles_b) : 0;
     if (x_bf16)
         hipLaunchKernelGGL(k_gemm_prep_x<1>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns, cnt,
                            n_cnt);
@@ -1442,8 +1186,8 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     a.N = out_a;
     a.K = in_dim;
     a.tiles_m = tiles_m;
-    a.tiles_n1 = wide ? tiles_a_w : tiles_a;
-    a.tiles_n = wide ? tiles_a_w : tiles_a + tiles_b;
+    a.tiles_n1 = tiles_a;
+    a.tiles_n = tiles_a + tiles_b;
     a.w2 = out_b > 0 ? wb + (size_t)(row0b / kTileRows) * a.nb * kRecordBytes : a.w;
     a.y2 = out_b > 0 ? Yb : Ya;
     a.N2 = out_b > 0 ? out_b : out_a;
@@ -1453,7 +1197,6 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     a.err = err;
     const int grid = a.tiles_n * a.tiles_m * ks;
     if (halves) return launch_timed(kProfGemm, k_gemm5, dim3(grid), dim3(kThreads5), 0, s, a);
-    if (wide) return launch_timed(kProfGemm, k_gemm4, dim3(grid), dim3(kThreads4), 0, s, a);
     const dim3 gd(grid), bd(kGemmThreads);
     if (bm == 64)
         return x_bf16 ? launch_timed(kProfGemm, k_gemm3<64, 1>, gd, bd, 0, s, a)
