@@ -14,9 +14,9 @@
 // every W value of its rows exactly once, straight into MFMA B operand
 // registers. Workgroups are ordered so that the eight XCDs each work on
 // their own band of W rows (the band stays in that XCD's L2 while all token
-// tiles use it). k_gemm5 (bf16 X, more than 64 tokens), k_gemm3 (64-token
-// tiles) and k_gemm2 (fp32 X) differ in how the wavefronts split the tile
-// and how W and X reach them; see each kernel.
+// tiles use it). k_gemm5 (bf16 X of more than 64 tokens, and fp32 X) and
+// k_gemm3 (bf16 X of at most 64 tokens) differ in how the wavefronts split
+// the tile and how W and X reach them; see each kernel.
 #include <type_traits>
 
 #include "iq3_common.h"
@@ -274,210 +274,11 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
 }
 
 // ---------------------------------------------------------------------------
-// GEMM, register-decode form. A 256-thread workgroup computes 128 tokens x
-// 192 rows; wavefront w owns rows [48w, 48w+48) as 3 column tiles of
-// v_mfma_f32_16x16x32_f16 and all 8 token tiles, so no W value is decoded
-// twice. A lane's B operand is 8 consecutive weights of one row (group g =
-// lane/16 of a 32-weight sub-block); it is decoded straight into registers
-// from two dwords of the T64 record (grid-index word, sign/scale word): two
-// lookups in the replicated unsigned grid table, the group's eighth sign
-// from the prefix-parity decode, four rotate-and-mask sign insertions and an exact fp16
-// multiply by 2s+1. X images are staged through LDS 64 columns at a time
-// (double buffered); W dwords are prefetched two stages ahead. Used for fp32
-// X (two images); bf16 X takes k_gemm3.
-
-constexpr int BM2 = 128, BN2 = 192, BK2 = 64;
-constexpr int kRow2 = BK2 + 8;                  // LDS row stride in halves
-constexpr int kTbl2Bytes = kGridTableBytes;  // replicated unsigned grid, as the GEMV
-
-struct WRing {
-    uint32_t q[2][3];  // [sub-block in stage][column tile]
-    uint32_t w[2][3];
-};
-
-// byte offset of dword idx (0..23) inside a lane slot of a T64 record
-constexpr uint32_t slot_dword_off(int idx) { return (uint32_t)((idx >> 2) * kUnitBytes + (idx & 3) * 4); }
-
-template <int V>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm2(GemmArgs g_all) {
-    __shared__ __attribute__((aligned(16))) uint8_t tbl[kTbl2Bytes];
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][V][BM2 * kRow2];
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t lane = tid & 63;
-    const int lr = lane & 15, lg = lane >> 4;
-
-    __shared__ int last_flag;
-    const GemmTile tl = gemm_tile(g_all);
-    if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
-    int tn;
-    const GemmArgs g = gemm_tensor(g_all, tl, tn);
-    const int tm = tl.tm;
-    const int m0 = tm * BM2, n0 = tn * BN2;
-    const uint32_t kboff = (uint32_t)tl.b0 * kRecordBytes;  // this split's first block
-
-    {
-        GridWords<kGemmThreads> gw;
-        grid_words<kGemmThreads>(gw, tid);
-        grid_table_store<kGemmThreads>(tbl, gw, tid);
-    }
-
-    // This lane's three W rows (clamped past N) as 32-bit byte offsets of
-    // their lane slot (and of their d) in block 0; block b adds b * 6272.
-    uint32_t rowoff[3], doff[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int r = min(n0 + wave * 48 + j * 16 + lr, g.N - 1);
-        const uint32_t base = (uint32_t)(r >> 6) * (uint32_t)g.nb * kRecordBytes + kboff;
-        rowoff[j] = base + (uint32_t)(r & 63) * 16u;
-        doff[j] = base + (uint32_t)kRecordDOffset + (uint32_t)(r & 63) * 2u;
-    }
-    const bool q1 = (lg >> 1) != 0;                                // q0 for groups 0,1; q1 for 2,3
-    const uint32_t p0 = 2 * (lg & 1), p1 = p0 + 1;                 // byte of each grid index
-    const uint32_t sel0 = 0x0C0C0000u | ((4u + p0) << 8);
-    const uint32_t sel1 = 0x0C0C0000u | ((4u + p1) << 8);
-    const uint32_t lb = (lane & 31u) << 3;  // this lane's replica of the grid table
-
-    // stage s = K columns [64s, 64s+64): sub-blocks 2P, 2P+1 (P = s % 4) of
-    // block s / 4. Loads are issued for a clamped stage so that no load sits
-    // under a branch.
-    auto load_w = [&](WRing& r, int s, auto Pc) {
-        constexpr int P = decltype(Pc)::value;
-        const uint32_t boff = (uint32_t)(s >> 2) * kRecordBytes;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int ib = 2 * P + t;
-            const uint32_t qo = q1 ? slot_dword_off(3 * ib + 1) : slot_dword_off(3 * ib);
-#pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const uint32_t o = rowoff[j] + boff;
-                r.q[t][j] = *reinterpret_cast<const uint32_t*>(g.w + (o + qo));
-                r.w[t][j] = *reinterpret_cast<const uint32_t*>(g.w + (o + slot_dword_off(3 * ib + 2)));
-            }
-        }
-    };
-    // X staging: the stage's 128 rows x 64 columns are 1024 16-byte pieces;
-    // piece tid + 256 i is row (tid >> 3) + 32 i, columns ((tid & 7) * 8)..+7,
-    // so 8 consecutive lanes read one row's 128 contiguous bytes.
-    const int xr = tid >> 3, xc = (tid & 7) * 8;
-    int xrow[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xrow[i] = min(m0 + xr + 32 * i, g.M - 1);
-    u32x4_t xreg[V][4];
-    auto load_x = [&](int s) {
-#pragma unroll
-        for (int v = 0; v < V; ++v)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                xreg[v][i] = *reinterpret_cast<const u32x4_t*>(g.xh + (size_t)v * g.M * g.K + (size_t)xrow[i] * g.K +
-                                                               tl.b0 * kQK + s * BK2 + xc);
-    };
-    auto store_x = [&](int buf) {
-#pragma unroll
-        for (int v = 0; v < V; ++v)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<u32x4_t*>(&xs[buf][v][(xr + 32 * i) * kRow2 + xc]) = xreg[v][i];
-    };
-    // B operand (8 weights of one row, group lg) from its grid word and sign
-    // word: unsigned grid values, signs on the fp16 sign bits, then an exact
-    // packed fp16 multiply by 2s+1 (|q (2s+1)| <= 1922)
-    auto decode_b = [&](uint32_t q, uint32_t w) -> half8_t {
-        const uint32_t sw = t64_signs(w);                              // all 32 signs
-        const uint32_t wg = __builtin_amdgcn_alignbit(sw, sw, (uint32_t)lg);  // group lg's at 4c, 4c+16
-        const _Float16 s2 = (_Float16)(float)((w >> 27) | 1u);
-        const half2v_t s22 = {s2, s2};
-        const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, lb, sel0));
-        const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(tbl + __builtin_amdgcn_perm(q, lb, sel1));
-        const half2v_t v0 = __builtin_bit_cast(half2v_t, g0.x | (__builtin_amdgcn_alignbit(wg, wg, 17) & 0x80008000u)) * s22;
-        const half2v_t v1 = __builtin_bit_cast(half2v_t, g0.y | (__builtin_amdgcn_alignbit(wg, wg, 21) & 0x80008000u)) * s22;
-        const half2v_t v2 = __builtin_bit_cast(half2v_t, g1.x | (__builtin_amdgcn_alignbit(wg, wg, 25) & 0x80008000u)) * s22;
-        const half2v_t v3 = __builtin_bit_cast(half2v_t, g1.y | (__builtin_amdgcn_alignbit(wg, wg, 29) & 0x80008000u)) * s22;
-        const u32x4_t r = {__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
-                           __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)};
-        return __builtin_bit_cast(half8_t, r);
-    };
-
-    float4_t acc[8][3], blk[8][3];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const float4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int steps = (tl.b1 - tl.b0) * (kQK / BK2);  // this split's stages, a multiple of 4
-    WRing ring[4];
-    uint32_t dreg[3];
-    load_w(ring[0], 0, std::integral_constant<int, 0>{});
-    load_w(ring[1], min(1, steps - 1), std::integral_constant<int, 1>{});
-    load_x(0);
-    store_x(0);
-    __syncthreads();  // table and first X stage ready
-
-    for (int s0 = 0; s0 < steps; s0 += 4) {
-        static_for<0, 4>([&](auto Uc) {
-            constexpr int U = decltype(Uc)::value;
-            const int s = s0 + U;
-            const int buf = U & 1;  // s0 is a multiple of 4
-            if constexpr (U == 0) {
-                // this block's d, used three stages later
-                const uint32_t boff = (uint32_t)(s >> 2) * kRecordBytes;
-#pragma unroll
-                for (int j = 0; j < 3; ++j) dreg[j] = *reinterpret_cast<const uint16_t*>(g.w + (doff[j] + boff));
-            }
-            // X for the next stage first: the wait for it before store_x then
-            // leaves the W loads of stage s+2 in flight
-            load_x(min(s + 1, steps - 1));
-            load_w(ring[(U + 2) & 3], min(s + 2, steps - 1), std::integral_constant<int, (U + 2) & 3>{});
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                half8_t bop[3];
-#pragma unroll
-                for (int j = 0; j < 3; ++j) bop[j] = decode_b(ring[U].q[t][j], ring[U].w[t][j]);
-#pragma unroll
-                for (int mt = 0; mt < 8; ++mt) {
-                    half8_t a[V];
-#pragma unroll
-                    for (int v = 0; v < V; ++v)
-                        a[v] = *reinterpret_cast<const half8_t*>(&xs[buf][v][(mt * 16 + lr) * kRow2 + t * 32 + lg * 8]);
-#pragma unroll
-                    for (int j = 0; j < 3; ++j)
-#pragma unroll
-                        for (int v = 0; v < V; ++v) {
-                            // a block's first MFMA starts from zero: no reset of blk
-                            const bool first = U == 0 && t == 0 && v == 0;
-                            blk[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[v], bop[j], first ? zero4 : blk[mt][j],
-                                                                                 0, 0, 0);
-                        }
-                }
-            }
-            if constexpr (U == 3) {
-                // block complete: acc += d/4 * partial (column = this lane's row)
-#pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)dreg[j]) * 0.25f;
-#pragma unroll
-                    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(d4, blk[mt][j][i], acc[mt][j][i]);
-                }
-            }
-            __syncthreads();  // everyone finished reading xs[buf ^ 1] (stage s - 1)
-            store_x(buf ^ 1);
-            __syncthreads();
-        });
-    }
-
-    gemm_store<8>(g, tl, acc, m0, n0, wave * 48, lr, lg, tid, &last_flag);
-}
-
-
-// ---------------------------------------------------------------------------
-// GEMM, pipelined form (one X image: bf16 input). Same tile and wavefront
-// split as k_gemm2 (128 tokens x 192 rows, wavefront w owns rows 48w..48w+47
-// and all 128 tokens), reorganised so that the matrix cores are fed every
-// cycle the wavefront can give them:
+// GEMM, one wavefront per SIMD (bf16 X of at most 64 tokens, as 64-token
+// tiles; the fallback for X images of 4 GiB or more). A 256-thread
+// workgroup computes BM tokens x 192 rows; wavefront w owns rows
+// 48w..48w+47 and all BM tokens, arranged so that the matrix cores are fed
+// every cycle the wavefront can give them:
 //   * W arrives as whole record units: per 256-wide block the workgroup
 //     copies the three row tiles' six 1 KiB units and their d values into
 //     LDS (coalesced 16-byte loads, one block ahead), and the decode reads
@@ -838,8 +639,13 @@ __device__ __forceinline__ half8_t decode_group5(const uint8_t* tbl, uint32_t q,
     return __builtin_bit_cast(half8_t, r);
 }
 
+// MT token tiles of V images each (MT * V = 8: bf16 X, 128 tokens, one
+// image; fp32 X, 64 tokens, hi and lo images): the X stage, the A reads per
+// sub-block and the MFMAs per decoded B operand are the same for both.
+template <int MT, int V>
 __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
-    constexpr int MT = BM5 / 16;  // token tiles (8)
+    static_assert(MT * V == 8, "one 16 KiB X stage");
+    constexpr int BM = 16 * MT;   // tokens per tile
     constexpr int JT = 3;         // column tiles per wavefront
     __shared__ __attribute__((aligned(16))) GemmSmem5 sm;
 
@@ -854,7 +660,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
     int tn;
     const GemmArgs g = gemm_tensor(g_all, tl, tn);
-    const int m0 = tl.tm * BM5, n0 = tn * BN5;
+    const int m0 = tl.tm * BM, n0 = tn * BN5;
     const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
 
     // K halves: blocks [b0 + kh * nh, ...) of this split, nh per half (the
@@ -869,16 +675,19 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     // Loads go straight from global memory into LDS (global_load_lds_dwordx4:
     // lane i of a wavefront writes the 16 bytes at the destination + 16 i),
     // issued at a stage's start and complete at its closing barrier.
-    // X: the stage's 128 rows x 64 columns are 16 pieces of 8 rows; wavefront
-    // rq of the K half copies pieces rq + 4 i. Lane l of a piece fills LDS
+    // X: the stage's V images of BM rows x 64 columns are 16 pieces of 8
+    // rows (piece p: image p / (2 MT), rows 8 (p % (2 MT)) ..); wavefront rq
+    // of the K half copies pieces rq + 4 i. Lane l of a piece fills LDS
     // chunk l & 7 of row l >> 3 with global chunk (l & 7) ^ (row & 7), the
-    // swizzle the A reads undo. (Byte offsets from xh: the image is under
+    // swizzle the A reads undo. (Byte offsets from xh: the images are under
     // 4 GiB, as the launch checks.)
     uint32_t xsrc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int r = 8 * (rq + 4 * i) + (int)(lane >> 3);
-        xsrc[i] = ((uint32_t)min(m0 + r, g.M - 1) * (uint32_t)g.K) * 2u + (((lane & 7u) ^ (lane >> 3)) << 4);
+        const int p = rq + 4 * i, v = p / (2 * MT);
+        const int r = 8 * (p % (2 * MT)) + (int)(lane >> 3);
+        xsrc[i] = ((uint32_t)v * (uint32_t)g.M * (uint32_t)g.K + (uint32_t)min(m0 + r, g.M - 1) * (uint32_t)g.K) * 2u +
+                  (((lane & 7u) ^ (lane >> 3)) << 4);
     }
     const uint8_t* xbase = reinterpret_cast<const uint8_t*>(g.xh);
     // X stage s (past the last: the last one's columns again) into buffer s & 1
@@ -1022,10 +831,15 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
                 }
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    const half8_t a = *reinterpret_cast<const half8_t*>(xa + mt * 16 * 128 + a_off[t]);
+                    half8_t a[V];
+#pragma unroll
+                    for (int v = 0; v < V; ++v)
+                        a[v] = *reinterpret_cast<const half8_t*>(xa + v * BM * 128 + mt * 16 * 128 + a_off[t]);
 #pragma unroll
                     for (int j = 0; j < JT; ++j)
-                        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop[t][j], acc[mt][j], 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < V; ++v)
+                            acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[v], bop[t][j], acc[mt][j], 0, 0, 0);
                 }
             }
             if constexpr (U == 3) {
@@ -1064,7 +878,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     // fall on different banks), then every thread copies whole rows out,
     // times the token's unscale, 16 bytes at a time.
     constexpr int kTStride = BN5 + 4;
-    static_assert(BM5 * kTStride * 4 <= 2 * 2 * kXStage5 + 2 * 2 * kWHalf5, "output tile area");
+    static_assert(BM * kTStride * 4 <= 2 * 2 * kXStage5 + 2 * 2 * kWHalf5, "output tile area");
     float* tile = reinterpret_cast<float*>(&sm.xs[0][0][0]);
     __syncthreads();  // the K half 1 sums are read
     if (kh == 0) {
@@ -1077,7 +891,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
                     tile[(mt * 16 + (int)lg * 4 + i) * kTStride + rq * 48 + j * 16 + lr] = acc[mt][j][i];
     }
     __syncthreads();
-    const int rows = min(BM5, g.M - m0), cols = min(BN5, g.N - n0);
+    const int rows = min(BM, g.M - m0), cols = min(BN5, g.N - n0);
     const bool vec = (g.N & 3) == 0 && (reinterpret_cast<uintptr_t>(g.y) & 15u) == 0;
     for (int f = tid; f < rows * (BN5 / 4); f += kThreads5) {
         const int m = f / (BN5 / 4), c4 = (f - m * (BN5 / 4)) * 4;
@@ -1098,20 +912,21 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
 
 // K splits per result tile: one when the tiles fill half the CUs, else
 // enough to fill them (at most 8, at least one block per split).
-// Token rows per result tile: 64 for at most 64 tokens (no padding), else 128.
-int gemm_tile_m(int M) { return M <= 64 ? 64 : 128; }
+// Token rows per result tile: 128 for bf16 X of more than 64 tokens, else 64
+// (fp32 X: two images per token; at most 64 tokens: no padding).
+int gemm_tile_m(int M, int x_bf16) { return x_bf16 && M > 64 ? 128 : 64; }
 
 // k_gemm5 (K halves inside the workgroup, two wavefronts per SIMD) takes
-// bf16 X of more than 64 tokens: measured at 12288 x 6144, 97.6 us against
-// k_gemm3's 126-130 us at 512 tokens, and 344 us at 2048 tokens against 356 us
-// for a 384-row, 8-wavefront form with the full K per wavefront (removed).
-// Its X offsets are 32-bit.
+// bf16 X of more than 64 tokens (measured at 12288 x 6144: 97.6 us against
+// k_gemm3's 126-130 us at 512 tokens, and 344 us at 2048 tokens against
+// 356 us for a 384-row, 8-wavefront form with the full K per wavefront,
+// removed) and fp32 X. Its X offsets are 32-bit.
 static bool gemm_halves(int M, int x_bf16, int K) {
-    return x_bf16 && M > 64 && (size_t)M * (size_t)K * 2 < (1ull << 32);
+    return (x_bf16 ? M > 64 : true) && (size_t)(x_bf16 ? 1 : 2) * M * (size_t)K * 2 < (1ull << 32);
 }
 
-int gemm_splits(int M, int N, int K, int num_cus, int tile_n) {
-    const int bm = gemm_tile_m(M);
+int gemm_splits(int M, int N, int K, int num_cus, int x_bf16, int tile_n) {
+    const int bm = gemm_tile_m(M, x_bf16);
     const int tiles = ((M + bm - 1) / bm) * ((N + tile_n - 1) / tile_n);
     const int cus = num_cus > 0 ? num_cus : 256;
     if (2 * tiles > cus) return 1;
@@ -1132,7 +947,7 @@ GemmWs gemm_ws(int M, int N, int K, int x_bf16, int ks, int tile_n = kTileN) {
     w.img = 0;
     w.uns = a256(v * (size_t)M * K * 2);
     w.cnt = w.uns + a256((size_t)M * 4);
-    const int bm = gemm_tile_m(M);
+    const int bm = gemm_tile_m(M, x_bf16);
     const size_t tiles = (size_t)((M + bm - 1) / bm) * ((N + tile_n - 1) / tile_n);
     w.part = w.cnt + (ks > 1 ? a256(tiles * 4) : 0);
     w.total = w.part + (ks > 1 ? tiles * ks * bm * tile_n * 4 : 0);
@@ -1141,7 +956,7 @@ GemmWs gemm_ws(int M, int N, int K, int x_bf16, int ks, int tile_n = kTileN) {
 }  // namespace
 
 size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus) {
-    return gemm_ws(M, N, K, x_bf16, gemm_splits(M, N, K, num_cus)).total;
+    return gemm_ws(M, N, K, x_bf16, gemm_splits(M, N, K, num_cus, x_bf16)).total;
 }
 
 hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, const uint8_t* wb,
@@ -1158,11 +973,11 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
         return hipErrorInvalidValue;
     const bool halves = gemm_halves(M, x_bf16, in_dim);
     const int n_eq = (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
-    const int ks = gemm_splits(M, n_eq, in_dim, num_cus, kTileN);
+    const int ks = gemm_splits(M, n_eq, in_dim, num_cus, x_bf16, kTileN);
     const GemmWs L = gemm_ws(M, n_eq, in_dim, x_bf16, ks);
     _Float16* xh = reinterpret_cast<_Float16*>(ws + L.img);
     float* uns = reinterpret_cast<float*>(ws + L.uns);
-    const int bm = gemm_tile_m(M);
+    const int bm = gemm_tile_m(M, x_bf16);
     const int tiles_m = (M + bm - 1) / bm;
     uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
     const int n_cnt = ks > 1 ? tiles_m * (tiles_a + tiles_b) : 0;
@@ -1196,13 +1011,14 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     a.part = reinterpret_cast<float*>(ws + L.part);
     a.err = err;
     const int grid = a.tiles_n * a.tiles_m * ks;
-    if (halves) return launch_timed(kProfGemm, k_gemm5, dim3(grid), dim3(kThreads5), 0, s, a);
+    if (halves)
+        return x_bf16 ? launch_timed(kProfGemm, k_gemm5<8, 1>, dim3(grid), dim3(kThreads5), 0, s, a)
+                      : launch_timed(kProfGemm, k_gemm5<4, 2>, dim3(grid), dim3(kThreads5), 0, s, a);
     const dim3 gd(grid), bd(kGemmThreads);
     if (bm == 64)
         return x_bf16 ? launch_timed(kProfGemm, k_gemm3<64, 1>, gd, bd, 0, s, a)
                       : launch_timed(kProfGemm, k_gemm3<64, 2>, gd, bd, 0, s, a);
-    return x_bf16 ? launch_timed(kProfGemm, k_gemm3<128, 1>, gd, bd, 0, s, a)
-                  : launch_timed(kProfGemm, k_gemm2<2>, gd, bd, 0, s, a);
+    return launch_timed(kProfGemm, k_gemm3<128, 1>, gd, bd, 0, s, a);
 }
 
 hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, int out_dim, const void* X, int x_bf16,
