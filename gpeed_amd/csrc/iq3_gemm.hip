@@ -908,6 +908,291 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// GEMM, 32x32 form (one K split; bf16 X, or fp32 X as two images). A
+// 512-thread workgroup computes 128 / V tokens x 256 W rows (four T64 row
+// tiles) with v_mfma_f32_32x32x16_f16: a single wavefront keeps that
+// instruction's pipe nearly full and leaves room for four VALU instructions
+// per MFMA, where v_mfma_f32_16x16x32_f16 needs two wavefronts and no VALU
+// to come close. Wavefront w owns row tile rg = w & 3 (two 32-row B tiles)
+// for all tokens over the blocks of K half kh = w >> 2; each decoded group of
+// 8 weights (one per lane and B tile) feeds 4 MFMAs of 32 x 32 x 16. The
+// rest follows k_gemm5: accumulators in units of the row's running d,
+// per-K-half LDS rings filled by global_load_lds_dwordx4 (X stages swizzled
+// by 16-byte chunk, W half blocks with the blocks' d), the next K step's B
+// operands decoded under the current MFMAs, one barrier per 64-column
+// stage, and at the end the K halves added in LDS and the tile stored as
+// whole rows.
+//
+// Operand layouts of v_mfma_f32_32x32x16_f16 (lane l): A holds token l & 31
+// of a 32-token tile at K elements 8 (l >> 5) .. +7; B holds W row l & 31 of
+// a 32-row tile at the same K elements; the 16 results of lane l are W row
+// l & 31, tokens 8 (i >> 2) + 4 (l >> 5) + (i & 3) for i < 16.
+
+constexpr int BN6 = 256, BK6 = 64;
+constexpr int kThreads6 = 512;
+constexpr int kXStage6 = 128 * BK6 * 2;          // 16 KiB: 128 rows (all images) x 128 bytes
+constexpr int kWHalf6 = 4 * 3 * kUnitBytes;      // 12 KiB: 4 row tiles x 3 units
+constexpr int kTStride6 = BN6 + 4;               // output tile row stride (floats)
+
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+struct GemmSmem6 {
+    // tbl, xs and wb are contiguous: after the main loop they hold the K
+    // half 1 sums, then the output tile
+    uint8_t tbl[kTbl5 + 2048];   // grid * (2s+1) as [s][idx], then a zero "scale"
+    uint8_t xs[2][2][kXStage6];  // [K half][buffer]
+    uint8_t wb[2][2][kWHalf6];   // [K half][buffer]: [tile][unit][64 lanes x 16 B]
+    uint8_t wd[2][2][1024];      // [K half][block parity]: [tile][64 fp16] (a whole wavefront's copy)
+};
+static_assert(kTbl5 + 2048 + 2 * 2 * kXStage6 + 2 * 2 * kWHalf6 >= 128 * kTStride6 * 4, "output tile area");
+static_assert(kTbl5 + 2048 + 2 * 2 * kXStage6 + 2 * 2 * kWHalf6 >= 4 * 128 * 64 * 4, "K half 1 sums");
+
+template <int V>
+__global__ __launch_bounds__(kThreads6) void k_gemm6(GemmArgs g_all) {
+    constexpr int BM = 128 / V;   // tokens per tile
+    constexpr int MT = BM / 32;   // 32-token A tiles per image
+    constexpr int JT = 2;         // 32-row B tiles per wavefront
+    __shared__ __attribute__((aligned(16))) GemmSmem6 sm;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rg = wave & 3, kh = wave >> 2;
+    const uint32_t lane = tid & 63;
+    const int l32 = lane & 31;
+    const uint32_t hk = lane >> 5;  // which 8 of a K step's 16 elements
+
+    const GemmTile tl = gemm_tile(g_all);
+    if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
+    int tn;
+    const GemmArgs g = gemm_tensor(g_all, tl, tn);
+    const int m0 = tl.tm * BM, n0 = tn * BN6;
+    const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
+
+    const int nblk = tl.b1 - tl.b0;
+    const int nh = (nblk + 1) >> 1;
+    const int kb0 = tl.b0 + kh * nh;
+    const int steps = nh * (kQK / BK6);
+    auto blk_of = [&](int c) { return min(kb0 + c, tl.b1 - 1); };
+
+    // X: the stage's V images of BM rows x 64 columns are 16 pieces of 8 rows
+    // (piece p: image p / (BM / 8), rows 8 (p % (BM / 8)) ..); wavefront rg of
+    // the K half copies pieces rg + 4 i, lane l into LDS chunk l & 7 of row
+    // l >> 3 from global chunk (l & 7) ^ (row & 7).
+    uint32_t xsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = rg + 4 * i, v = p / (BM / 8);
+        const int r = 8 * (p % (BM / 8)) + (int)(lane >> 3);
+        xsrc[i] = ((uint32_t)v * (uint32_t)g.M * (uint32_t)g.K + (uint32_t)min(m0 + r, g.M - 1) * (uint32_t)g.K) * 2u +
+                  (((lane & 7u) ^ (lane >> 3)) << 4);
+    }
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(g.xh);
+    auto load_x = [&](int s) {
+        const int sc = min(s, steps - 1);
+        const uint32_t kc = (uint32_t)(blk_of(sc >> 2) * kQK + (sc & 3) * BK6) * 2u;
+        uint8_t* dst = sm.xs[kh][s & 1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(xbase + (xsrc[i] + kc), dst + (rg + 4 * i) * 1024, 16, 0, 0);
+    };
+    // W half block hb: wavefront rg copies the three units of row tile rg; at
+    // a block's first half, wavefront 3 also copies the four tiles' d (lanes
+    // 0..31; the others repeat lane 31's piece).
+    const int wtile = min(n0 / kTileRows + rg, last_tile);
+    const uint32_t wsrc = (uint32_t)wtile * (uint32_t)g.nb * kRecordBytes + lane * 16u;
+    const uint32_t dl = min(lane, 31u);
+    const uint32_t dsrc = (uint32_t)min(n0 / kTileRows + (int)(dl >> 3), last_tile) * (uint32_t)g.nb * kRecordBytes +
+                          kRecordDOffset + (dl & 7u) * 16u;
+    auto load_w = [&](int hb) {
+        const uint32_t boff = (uint32_t)blk_of(min(hb, 2 * nh - 1) >> 1) * kRecordBytes;
+        const uint32_t hoff = (uint32_t)(hb & 1) * 3 * kUnitBytes;
+        uint8_t* dst = &sm.wb[0][0][0] + (kh * 2 + (hb & 1)) * kWHalf6 + rg * 3 * kUnitBytes;
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            __builtin_amdgcn_global_load_lds(g.w + (wsrc + boff + hoff + k * kUnitBytes), dst + k * kUnitBytes, 16, 0, 0);
+        if ((hb & 1) == 0 && rg == 3)
+            __builtin_amdgcn_global_load_lds(g.w + (dsrc + boff), &sm.wd[0][0][0] + (kh * 2 + ((hb >> 1) & 1)) * 1024,
+                                             16, 0, 0);
+    };
+
+    // this lane's rows j < JT (row l32 of B tile j of row tile rg): lane slot
+    // in the staged half block, and d
+    const uint8_t* wrow[JT];
+    uint32_t d_off[JT];
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+        const int r = j * 32 + l32;  // inside row tile rg
+        wrow[j] = &sm.wb[kh][0][0] + rg * 3 * kUnitBytes + r * 16;
+        d_off[j] = (uint32_t)rg * 128u + (uint32_t)r * 2u;
+    }
+    const uint32_t p0 = 2 * hk;  // the group's grid indices: bytes p0, p0 + 1 of its index word
+    const uint8_t* arow = &sm.xs[kh][0][0] + l32 * 128;
+
+    float16_t acc[MT][JT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < JT; ++j) acc[i][j] = float16_t{};
+    float dcur[JT], dnext[JT];
+    uint32_t smask[JT], szero[JT];
+
+    auto block_d = [&](int c) {
+        const bool live = kb0 + c < tl.b1;
+#pragma unroll
+        for (int j = 0; j < JT; ++j) {
+            const float dn =
+                live ? (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(&sm.wd[kh][c & 1][d_off[j]]))
+                     : 0.0f;
+            const bool z = dn == 0.0f;
+            smask[j] = z ? 0u : 0x7800u;
+            szero[j] = z ? kZeroEntry5 : 0u;
+            dnext[j] = dn;
+        }
+    };
+    auto rescale = [&]() {
+#pragma unroll
+        for (int j = 0; j < JT; ++j) {
+            const bool change = dnext[j] != 0.0f && dnext[j] != dcur[j];
+            const float r = change ? dcur[j] * __builtin_amdgcn_rcpf(dnext[j]) : 1.0f;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= r;
+            dcur[j] = change ? dnext[j] : dcur[j];
+        }
+    };
+    // B operands of K step ks (0..15) of a block (sub-block ks >> 1, group
+    // 2 (ks & 1) + hk) from W buffer `buf`
+    auto decode = [&](half8_t (&bop)[JT], int buf, int ks) {
+        const int lib = (ks >> 1) & 3;  // sub-block inside the half block
+        const int dq = 3 * lib + (ks & 1), dw = 3 * lib + 2;
+        const int oq = buf * kWHalf6 + (dq >> 2) * kUnitBytes + (dq & 3) * 4;
+        const int ow = buf * kWHalf6 + (dw >> 2) * kUnitBytes + (dw & 3) * 4;
+#pragma unroll
+        for (int j = 0; j < JT; ++j) {
+            const uint32_t q = *reinterpret_cast<const uint32_t*>(wrow[j] + oq);
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(wrow[j] + ow);
+            bop[j] = decode_group5(sm.tbl, q, w, 2 * (ks & 1) + hk, p0, smask[j], szero[j]);
+        }
+    };
+
+    load_x(0);
+    load_w(0);
+    scaled_grid_table5<kThreads6>(sm.tbl, tid);
+    static_assert(kThreads6 * 4 == 2048, "one word of the zero row per thread");
+    reinterpret_cast<uint32_t*>(sm.tbl + kZeroEntry5)[tid] = 0u;
+    __syncthreads();  // table, X stage 0, W half block 0 with block 0's d
+    block_d(0);
+#pragma unroll
+    for (int j = 0; j < JT; ++j) dcur[j] = dnext[j];
+    half8_t bop[2][JT];
+    decode(bop[0], 0, 0);
+
+    // Stage s (64 columns, K steps 4 (s & 3) .. +3 of its block): the copies
+    // of X(s + 1) and, at a half block's first stage, W(hb + 1); four K
+    // steps of MFMAs, each with the next K step's B operands decoded under it
+    // (after a block's last step, with the next block's d). Past the last
+    // stage the same steps run on clamped blocks and their results go unused.
+    for (int c = 0; c < nh; ++c) {
+        static_for<0, 4>([&](auto Uc) {
+            constexpr int U = decltype(Uc)::value;
+            const int s = 4 * c + U;
+            load_x(s + 1);
+            if constexpr ((U & 1) == 0) load_w((s >> 1) + 1);
+            const uint8_t* xa = arow + (s & 1) * kXStage6;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int ks = 4 * U + k;  // K step inside the block
+                const int cur = k & 1;
+                if (ks < 15) {
+                    decode(bop[cur ^ 1], ((ks + 1) >> 3) & 1, ks + 1);
+                } else {
+                    block_d(c + 1);
+                    decode(bop[cur ^ 1], 0, 0);  // next block, first half (buffer 0)
+                }
+                const uint32_t ac = (uint32_t)(((2 * k + (int)hk) ^ (l32 & 7)) << 4);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    half8_t a[V];
+#pragma unroll
+                    for (int v = 0; v < V; ++v)
+                        a[v] = *reinterpret_cast<const half8_t*>(xa + v * BM * 128 + mt * 32 * 128 + ac);
+#pragma unroll
+                    for (int j = 0; j < JT; ++j)
+#pragma unroll
+                        for (int v = 0; v < V; ++v)
+                            acc[mt][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[v], bop[cur][j], acc[mt][j], 0, 0, 0);
+                }
+            }
+            if constexpr (U == 3) {
+                if (c + 1 < nh) rescale();
+            }
+            __syncthreads();
+        });
+    }
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+        const float f = dcur[j] * 0.25f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= f;
+    }
+    // K half 1 -> LDS (over tbl, xs and wb, free after the last barrier); K half 0 adds
+    float4* red = reinterpret_cast<float4*>(&sm.tbl[0]) + (size_t)rg * (MT * JT * 4 * 64) + lane;
+    if (kh == 1) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < JT; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    red[((mt * JT + j) * 4 + q) * 64] =
+                        float4{acc[mt][j][4 * q], acc[mt][j][4 * q + 1], acc[mt][j][4 * q + 2], acc[mt][j][4 * q + 3]};
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < JT; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 o = red[((mt * JT + j) * 4 + q) * 64];
+                    acc[mt][j][4 * q] += o.x;
+                    acc[mt][j][4 * q + 1] += o.y;
+                    acc[mt][j][4 * q + 2] += o.z;
+                    acc[mt][j][4 * q + 3] += o.w;
+                }
+    }
+    __syncthreads();  // the K half 1 sums are read
+    // the tile as rows of 256 floats (stride 260), then whole rows out
+    float* tile = reinterpret_cast<float*>(&sm.tbl[0]);
+    if (kh == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < JT; ++j)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    tile[(mt * 32 + 8 * (i >> 2) + 4 * (int)hk + (i & 3)) * kTStride6 + rg * 64 + j * 32 + l32] =
+                        acc[mt][j][i];
+    }
+    __syncthreads();
+    const int rows = min(BM, g.M - m0), cols = min(BN6, g.N - n0);
+    const bool vec = (g.N & 3) == 0 && (reinterpret_cast<uintptr_t>(g.y) & 15u) == 0;
+    for (int f = tid; f < rows * (BN6 / 4); f += kThreads6) {
+        const int m = f / (BN6 / 4), c4 = (f - m * (BN6 / 4)) * 4;
+        if (c4 >= cols) continue;
+        const float us = g.unscale[m0 + m];
+        const float4 v = *reinterpret_cast<const float4*>(&tile[m * kTStride6 + c4]);
+        float* yrow = g.y + (size_t)(m0 + m) * g.N + n0 + c4;
+        if (vec && c4 + 4 <= cols) {
+            *reinterpret_cast<float4*>(yrow) = float4{v.x * us, v.y * us, v.z * us, v.w * us};
+        } else {
+            const float o[4] = {v.x * us, v.y * us, v.z * us, v.w * us};
+            for (int e = 0; e < 4 && c4 + e < cols; ++e) yrow[e] = o[e];
+        }
+    }
+}
+
 }  // namespace
 
 // K splits per result tile: one when the tiles fill half the CUs, else
@@ -916,11 +1201,14 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
 // (fp32 X: two images per token; at most 64 tokens: no padding).
 int gemm_tile_m(int M, int x_bf16) { return x_bf16 && M > 64 ? 128 : 64; }
 
-// k_gemm5 (K halves inside the workgroup, two wavefronts per SIMD) takes
-// bf16 X of more than 64 tokens (measured at 12288 x 6144: 97.6 us against
-// k_gemm3's 126-130 us at 512 tokens, and 344 us at 2048 tokens against
-// 356 us for a 384-row, 8-wavefront form with the full K per wavefront,
-// removed) and fp32 X. Its X offsets are 32-bit.
+// k_gemm5 / k_gemm6 (K halves inside the workgroup, two wavefronts per
+// SIMD) take bf16 X of more than 64 tokens and fp32 X; their X offsets are
+// 32-bit. k_gemm6 (v_mfma_f32_32x32x16_f16, 256-row tiles) runs where its
+// tiles cover every CU, k_gemm5 (16x16x32, 192-row tiles) elsewhere.
+// Measured at 12288 x 6144: 512 tokens, k_gemm5 97.6-103 us (k_gemm6, on
+// 192 of 256 CUs, 110 us; k_gemm3 126-130 us); 2048 tokens, k_gemm6 333 us,
+// k_gemm5 344 us, a 384-row 8-wavefront form with the full K per wavefront
+// (removed) 356 us.
 static bool gemm_halves(int M, int x_bf16, int K) {
     return (x_bf16 ? M > 64 : true) && (size_t)(x_bf16 ? 1 : 2) * M * (size_t)K * 2 < (1ull << 32);
 }
@@ -972,8 +1260,12 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
         (size_t)tiles_b * 3 * nb_sz * kRecordBytes >= (1ull << 32))
         return hipErrorInvalidValue;
     const bool halves = gemm_halves(M, x_bf16, in_dim);
+    // k_gemm6 (256-row tiles) where its tiles give every CU at least one
+    const int tiles6_a = (out_a + BN6 - 1) / BN6, tiles6_b = (out_b + BN6 - 1) / BN6;
+    const bool wide6 = halves && (long long)((M + gemm_tile_m(M, x_bf16) - 1) / gemm_tile_m(M, x_bf16)) *
+                                         (tiles6_a + tiles6_b) >= (num_cus > 0 ? num_cus : 256);
     const int n_eq = (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
-    const int ks = gemm_splits(M, n_eq, in_dim, num_cus, x_bf16, kTileN);
+    const int ks = wide6 ? 1 : gemm_splits(M, n_eq, in_dim, num_cus, x_bf16, kTileN);
     const GemmWs L = gemm_ws(M, n_eq, in_dim, x_bf16, ks);
     _Float16* xh = reinterpret_cast<_Float16*>(ws + L.img);
     float* uns = reinterpret_cast<float*>(ws + L.uns);
@@ -1001,8 +1293,8 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     a.N = out_a;
     a.K = in_dim;
     a.tiles_m = tiles_m;
-    a.tiles_n1 = tiles_a;
-    a.tiles_n = tiles_a + tiles_b;
+    a.tiles_n1 = wide6 ? tiles6_a : tiles_a;
+    a.tiles_n = wide6 ? tiles6_a + tiles6_b : tiles_a + tiles_b;
     a.w2 = out_b > 0 ? wb + (size_t)(row0b / kTileRows) * a.nb * kRecordBytes : a.w;
     a.y2 = out_b > 0 ? Yb : Ya;
     a.N2 = out_b > 0 ? out_b : out_a;
@@ -1011,6 +1303,9 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     a.part = reinterpret_cast<float*>(ws + L.part);
     a.err = err;
     const int grid = a.tiles_n * a.tiles_m * ks;
+    if (wide6)
+        return x_bf16 ? launch_timed(kProfGemm, k_gemm6<1>, dim3(grid), dim3(kThreads6), 0, s, a)
+                      : launch_timed(kProfGemm, k_gemm6<2>, dim3(grid), dim3(kThreads6), 0, s, a);
     if (halves)
         return x_bf16 ? launch_timed(kProfGemm, k_gemm5<8, 1>, dim3(grid), dim3(kThreads5), 0, s, a)
                       : launch_timed(kProfGemm, k_gemm5<4, 2>, dim3(grid), dim3(kThreads5), 0, s, a);
