@@ -517,7 +517,7 @@ def main():
                     help="run the prefill GEMM (W 12288x6144, bf16 X [M, 6144]) 20 times and the dense "
                          "decode step 20 times, and exit; meant to run under rocprofv3 --pmc")
     ap.add_argument("--gemm-m", type=int, default=512,
-                    help="tokens of the --gemm-probe GEMM (512 runs k_gemm3, 1024 and more k_gemm4)")
+                    help="tokens of the --gemm-probe GEMM (512 runs k_gemm5, 2048 k_gemm6)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the multi-GPU "
