@@ -42,9 +42,13 @@ __device__ __forceinline__ uint32_t f16_pair_of_floats(float lo, float hi) {
 // X -> fp16 images with a power-of-two scale per token row. One workgroup per
 // row. IN = 0: fp32 input (hi and lo images); IN = 1: bf16 input (one image);
 // IN = 2: X = SwiGLU(X, U) of fp32 gate and up rows (hi and lo images).
+// CPT > 0: the row is at most 256 * CPT chunks of 8 values, each thread holds
+// its CPT chunks in registers, so the row is read once and every load is in
+// flight before the first wait (a row of 12288 SwiGLU values: one memory
+// round trip instead of twelve); CPT = 0: any length, two passes.
 // The workgroups also clear the n_cnt split-K tickets of the GEMM launch
 // that follows on the same stream, so a workspace needs no initialisation.
-template <int IN>
+template <int IN, int CPT>
 __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X, const float* __restrict__ U,
                                                      float lim, int M, int K, _Float16* __restrict__ xh,
                                                      float* __restrict__ unscale, uint32_t* __restrict__ cnt,
@@ -53,45 +57,48 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
     const int tid = threadIdx.x;
     for (int i = m * 256 + tid; i < n_cnt; i += M * 256) cnt[i] = 0u;
     __shared__ float red[4];
-    // 8 consecutive values per access (16-byte loads; K is a multiple of 256)
-    auto ld8 = [&](int c, float (&v)[8]) {
+    // the 8 raw values of chunk c (16-byte loads; K is a multiple of 256)
+    struct Raw {
+        u32x4_t a, b, ua, ub;
+    };
+    auto load8 = [&](int c, Raw& r) {
         if constexpr (IN == 1) {
-            const u32x4_t u = reinterpret_cast<const u32x4_t*>(X)[((size_t)m * K >> 3) + c];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[2 * i] = __uint_as_float(u[i] << 16);
-                v[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
-            }
+            r.a = reinterpret_cast<const u32x4_t*>(X)[((size_t)m * K >> 3) + c];
         } else {
-            const float4* p = reinterpret_cast<const float4*>(X) + ((size_t)m * K >> 2) + 2 * c;
-            const float4 a = p[0], b = p[1];
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            const u32x4_t* p = reinterpret_cast<const u32x4_t*>(X) + ((size_t)m * K >> 2) + 2 * c;
+            r.a = p[0];
+            r.b = p[1];
             if constexpr (IN == 2) {
-                const float4* q = reinterpret_cast<const float4*>(U) + ((size_t)m * K >> 2) + 2 * c;
-                const float4 ua = q[0], ub = q[1];
-                const float u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = swiglu1(v[i], u[i], lim);
+                const u32x4_t* q = reinterpret_cast<const u32x4_t*>(U) + ((size_t)m * K >> 2) + 2 * c;
+                r.ua = q[0];
+                r.ub = q[1];
             }
         }
     };
-    const int n8 = K >> 3;
-    float mx = 0.0f;
-    for (int c = tid; c < n8; c += 256) {
-        float v[8];
-        ld8(c, v);
+    auto values8 = [&](const Raw& r, float (&v)[8]) {
+        if constexpr (IN == 1) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
-    }
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    const int sc = pow2_scale_of_max(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = __uint_as_float(r.a[i] << 16);
+                v[2 * i + 1] = __uint_as_float(r.a[i] & 0xFFFF0000u);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = __uint_as_float(r.a[i]);
+                v[4 + i] = __uint_as_float(r.b[i]);
+            }
+            if constexpr (IN == 2) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = swiglu1(v[i], __uint_as_float(r.ua[i]), lim);
+                    v[4 + i] = swiglu1(v[4 + i], __uint_as_float(r.ub[i]), lim);
+                }
+            }
+        }
+    };
     const size_t plane = (size_t)M * K;
-    for (int c = tid; c < n8; c += 256) {
-        float v[8];
-        ld8(c, v);
+    auto store8 = [&](int c, const float (&v)[8], int sc) {
         u32x4_t hi, lo;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -102,8 +109,76 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
         }
         reinterpret_cast<u32x4_t*>(xh + (size_t)m * K)[c] = hi;
         if constexpr (IN != 1) reinterpret_cast<u32x4_t*>(xh + plane + (size_t)m * K)[c] = lo;
+    };
+    auto row_scale = [&](float mx) {
+        mx = wave_max(mx);
+        if ((tid & 63) == 0) red[tid >> 6] = mx;
+        __syncthreads();
+        return pow2_scale_of_max(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    };
+    const int n8 = K >> 3;
+    float mx = 0.0f;
+    if constexpr (CPT > 0) {
+        // loads of chunks past the row are clamped to its last chunk (they
+        // leave the maximum unchanged) and their results are not stored
+        Raw r[CPT];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) load8(min(tid + 256 * j, n8 - 1), r[j]);
+        float v[CPT][8];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            values8(r[j], v[j]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[j][i]));
+        }
+        const int sc = row_scale(mx);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+            if (tid + 256 * j < n8) store8(tid + 256 * j, v[j], sc);
+        if (tid == 0) unscale[m] = ldexpf(1.0f, -sc);
+    } else {
+        for (int c = tid; c < n8; c += 256) {
+            Raw r;
+            float v[8];
+            load8(c, r);
+            values8(r, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+        }
+        const int sc = row_scale(mx);
+        for (int c = tid; c < n8; c += 256) {
+            Raw r;
+            float v[8];
+            load8(c, r);
+            values8(r, v);
+            store8(c, v, sc);
+        }
+        if (tid == 0) unscale[m] = ldexpf(1.0f, -sc);
     }
-    if (tid == 0) unscale[m] = ldexpf(1.0f, -sc);
+}
+
+// The preparation launch for rows of K values: chunks per thread in
+// registers where the row has at most 2048 chunks.
+template <int IN>
+hipError_t launch_prep_x(int M, int K, hipStream_t s, const void* X, const float* U, float lim, _Float16* xh,
+                         float* uns, uint32_t* cnt, int n_cnt) {
+    const int per = (K / 8 + 255) / 256;
+    const dim3 grid(M), block(256);
+    if (per <= 1)
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 1>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+    else if (per <= 2)
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 2>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+    else if (per <= 3)
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 3>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+    else if (per <= 4)
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 4>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+    else if (per <= 6)
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 6>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+    else if (per <= 8)
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 8>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+    else
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 0>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -240,35 +315,53 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
     }
     __syncthreads();
     if (!*flag) return;  // uniform
-    // four columns per thread and step; all splits' loads issued before the
-    // adds (buffer loads with sc1: past this XCD's L2, which may hold the
-    // workspace from an earlier call)
+    // four columns per item; a thread takes kR items per step and issues
+    // every split's loads of all of them before the first add, so a 64-token
+    // tile is one memory round trip (the loads miss in L2 by design: buffer
+    // loads with sc1, past this XCD's L2, which may hold the workspace from
+    // an earlier call)
+    constexpr int kR = 6;
     const int rows = min(BM, g.M - m0), cols = min(kTileN, g.N - n0);
+    const int n_items = rows * (kTileN / 4);
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(g.ks * BM * kTileN * 4), 0x00020000);
-    for (int q = tid; q < rows * (kTileN / 4); q += NTHR) {
-        const int ml = q / (kTileN / 4), nl = (q - ml * (kTileN / 4)) * 4;
-        if (nl >= cols) continue;
-        float4 v[8];
+    for (int q0 = tid; q0 < n_items; q0 += kR * NTHR) {
+        float4 v[kR][8];
 #pragma unroll
-        for (int z = 0; z < 8; ++z) {
-            const uint32_t off = z < g.ks ? (uint32_t)(((z * BM + ml) * kTileN + nl) * 4) : 0x80000000u;
-            v[z] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16));
-        }
-        float4 sum = v[0];
+        for (int u = 0; u < kR; ++u) {
+            const int q = q0 + u * NTHR;
+            const int ml = q / (kTileN / 4), nl = (q - ml * (kTileN / 4)) * 4;
+            const bool ok = q < n_items && nl < cols;
 #pragma unroll
-        for (int z = 1; z < 8; ++z)
-            if (z < g.ks) {
-                sum.x += v[z].x;
-                sum.y += v[z].y;
-                sum.z += v[z].z;
-                sum.w += v[z].w;
+            for (int z = 0; z < 8; ++z) {
+                const uint32_t off = ok && z < g.ks ? (uint32_t)(((z * BM + ml) * kTileN + nl) * 4) : 0x80000000u;
+                v[u][z] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16));
             }
-        const float us = g.unscale[m0 + ml];
-        float* yrow = g.y + (size_t)(m0 + ml) * g.N + n0 + nl;
-        const float o[4] = {sum.x * us, sum.y * us, sum.z * us, sum.w * us};
+        }
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (nl + c < cols) yrow[c] = o[c];
+        for (int u = 0; u < kR; ++u) {
+            const int q = q0 + u * NTHR;
+            const int ml = q / (kTileN / 4), nl = (q - ml * (kTileN / 4)) * 4;
+            if (q >= n_items || nl >= cols) continue;
+            float4 sum = v[u][0];
+#pragma unroll
+            for (int z = 1; z < 8; ++z)
+                if (z < g.ks) {
+                    sum.x += v[u][z].x;
+                    sum.y += v[u][z].y;
+                    sum.z += v[u][z].z;
+                    sum.w += v[u][z].w;
+                }
+            const float us = g.unscale[m0 + ml];
+            float* yrow = g.y + (size_t)(m0 + ml) * g.N + n0 + nl;
+            const float o[4] = {sum.x * us, sum.y * us, sum.z * us, sum.w * us};
+            if (nl + 4 <= cols && (reinterpret_cast<uintptr_t>(yrow) & 15u) == 0) {
+                *reinterpret_cast<float4*>(yrow) = float4{o[0], o[1], o[2], o[3]};
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (nl + c < cols) yrow[c] = o[c];
+            }
+        }
     }
     if (tid == 0) __hip_atomic_store(g.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -605,7 +698,8 @@ static_assert(2 * 2 * kXStage5 + 2 * 2 * kWHalf5 >= 128 * 192 * 4, "reduction ar
 // workgroup of NTHR threads writes it.
 template <int NTHR>
 __device__ __forceinline__ void scaled_grid_table5(uint8_t* tbl, int tid) {
-#pragma unroll 2
+    // unrolled: every grid word's load is in flight before the first use
+#pragma unroll
     for (int i = 0; i < 4096 / NTHR; ++i) {
         const uint32_t e = (uint32_t)tid + NTHR * i, idx = e & 255u, s = e >> 8;
         const float m = (float)(2 * s + 1);
@@ -1273,15 +1367,9 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
     const int tiles_m = (M + bm - 1) / bm;
     uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + L.cnt);
     const int n_cnt = ks > 1 ? tiles_m * (tiles_a + tiles_b) : 0;
-    if (x_bf16)
-        hipLaunchKernelGGL(k_gemm_prep_x<1>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns, cnt,
-                           n_cnt);
-    else if (U)
-        hipLaunchKernelGGL(k_gemm_prep_x<2>, dim3(M), dim3(256), 0, s, X, U, lim, M, in_dim, xh, uns, cnt, n_cnt);
-    else
-        hipLaunchKernelGGL(k_gemm_prep_x<0>, dim3(M), dim3(256), 0, s, X, nullptr, 0.0f, M, in_dim, xh, uns, cnt,
-                           n_cnt);
-    hipError_t e = hipGetLastError();
+    hipError_t e = x_bf16 ? launch_prep_x<1>(M, in_dim, s, X, nullptr, 0.0f, xh, uns, cnt, n_cnt)
+                          : (U ? launch_prep_x<2>(M, in_dim, s, X, U, lim, xh, uns, cnt, n_cnt)
+                               : launch_prep_x<0>(M, in_dim, s, X, nullptr, 0.0f, xh, uns, cnt, n_cnt));
     if (e != hipSuccess) return e;
     GemmArgs a{};
     a.nb = in_dim / kQK;
