@@ -63,7 +63,7 @@ inline size_t t64_bytes(unsigned long long n_rows, long long in_dim) {
 }
 
 // Exact fp16 encoding of a small non-negative integer (< 2048).
-inline uint16_t host_f16_of_small_uint(unsigned a) {
+constexpr uint16_t host_f16_of_small_uint(unsigned a) {
     if (a == 0) return 0;
     int e = 31 - __builtin_clz(a);  // a in [2^e, 2^(e+1))
     const unsigned man = (a << (10 - e)) & 0x3FFu;

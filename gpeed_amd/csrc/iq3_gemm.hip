@@ -694,19 +694,41 @@ static_assert(2 * 2 * kXStage5 + 2 * 2 * kWHalf5 >= 128 * 192 * 4, "reduction ar
 
 // Entry (idx, s) = 4 fp16 values grid(idx)[0..3] * (2s+1), at (s << 11) |
 // (idx << 3): the bank of a lookup follows the index's low five bits, so
-// the four lanes that decode one row (same s) spread like any others. A
-// workgroup of NTHR threads writes it.
+// the four lanes that decode one row (same s) spread like any others. Then
+// 2 KiB of zeros (the row that zero-d blocks read). The table is device data
+// built at compile time (every value is an integer below 2048, exact in
+// fp16) and copied into LDS at a launch's start.
+struct ScaledGrid5 {
+    uint32_t w[(kTbl5 + 2048) / 4];
+};
+constexpr ScaledGrid5 make_scaled_grid5() {
+    ScaledGrid5 t{};
+    for (uint32_t s = 0; s < 16; ++s)
+        for (uint32_t idx = 0; idx < 256; ++idx) {
+            const uint32_t v = kIq3xxsGrid[idx], m = 2 * s + 1;
+            const uint32_t o = ((s << 11) | (idx << 3)) / 4;
+            t.w[o] = host_f16_of_small_uint((v & 255u) * m) |
+                     ((uint32_t)host_f16_of_small_uint(((v >> 8) & 255u) * m) << 16);
+            t.w[o + 1] = host_f16_of_small_uint(((v >> 16) & 255u) * m) |
+                         ((uint32_t)host_f16_of_small_uint((v >> 24) * m) << 16);
+        }
+    return t;
+}
+__device__ __attribute__((aligned(16))) const ScaledGrid5 kScaledGrid5 = make_scaled_grid5();
+static_assert((kTbl5 + 2048) % 1024 == 0, "whole 1 KiB pieces");
+
+// A workgroup of NTHR threads copies the table into tbl with
+// global_load_lds_dwordx4 (1 KiB per wavefront instruction); the copies
+// complete at the caller's next barrier, like its other copies.
 template <int NTHR>
 __device__ __forceinline__ void scaled_grid_table5(uint8_t* tbl, int tid) {
-    // unrolled: every grid word's load is in flight before the first use
+    constexpr int kPieces = (kTbl5 + 2048) / 1024, kWaves = NTHR / 64;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(&kScaledGrid5) + (tid & 63) * 16;
 #pragma unroll
-    for (int i = 0; i < 4096 / NTHR; ++i) {
-        const uint32_t e = (uint32_t)tid + NTHR * i, idx = e & 255u, s = e >> 8;
-        const float m = (float)(2 * s + 1);
-        const uint32_t v = kIq3xxsGrid[idx];
-        const uint32_t lo = f16_pair_of_floats((float)(v & 255u) * m, (float)((v >> 8) & 255u) * m);
-        const uint32_t hi = f16_pair_of_floats((float)((v >> 16) & 255u) * m, (float)(v >> 24) * m);
-        *reinterpret_cast<u32x2_t*>(tbl + (s << 11) + (idx << 3)) = u32x2_t{lo, hi};
+    for (int i = 0; i < (kPieces + kWaves - 1) / kWaves; ++i) {
+        const int piece = wave + kWaves * i;
+        if (piece < kPieces) __builtin_amdgcn_global_load_lds(src + piece * 1024, tbl + piece * 1024, 16, 0, 0);
     }
 }
 
@@ -889,10 +911,8 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     // block 0's d and the B operands of its first sub-block
     load_x(0);
     load_w(0);
-    // the table is built while the first copies are in flight
+    // the table is copied with the first stages
     scaled_grid_table5<kThreads5>(sm.tbl, tid);
-    static_assert(kThreads5 * 4 == 2048, "one word of the zero row per thread");
-    reinterpret_cast<uint32_t*>(sm.tbl + kZeroEntry5)[tid] = 0u;
     __syncthreads();  // table, X stage 0, W half block 0 with block 0's d
     block_d(0);
 #pragma unroll
@@ -1172,8 +1192,6 @@ __global__ __launch_bounds__(kThreads6) void k_gemm6(GemmArgs g_all) {
     load_x(0);
     load_w(0);
     scaled_grid_table5<kThreads6>(sm.tbl, tid);
-    static_assert(kThreads6 * 4 == 2048, "one word of the zero row per thread");
-    reinterpret_cast<uint32_t*>(sm.tbl + kZeroEntry5)[tid] = 0u;
     __syncthreads();  // table, X stage 0, W half block 0 with block 0's d
     block_d(0);
 #pragma unroll
