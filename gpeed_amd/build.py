@@ -37,6 +37,12 @@ def _run(cmd):
     return out
 
 
+# Per-source extra flags. iq3_gemv.hip: the GEMV kernel's six leading scalar
+# arguments are preloaded into SGPRs at wave launch (the code object keeps a
+# fallback that loads them for firmware without kernel-argument preloading).
+EXTRA = {"iq3_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=6"]}
+
+
 def build(verbose: bool = False) -> str:
     """Compile every source to an object in csrc/_build and link the shared library."""
     bdir = os.path.join(CSRC, "_build")
@@ -44,7 +50,7 @@ def build(verbose: bool = False) -> str:
     objs = []
     for src in SOURCES:
         obj = os.path.join(bdir, src.replace(".hip", ".o"))
-        out = _run([HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        out = _run([HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj])
         if verbose and out.strip():
             print(out)
         objs.append(obj)

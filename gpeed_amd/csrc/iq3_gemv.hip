@@ -201,7 +201,11 @@ __device__ __forceinline__ void load_rec(Rec<(NT + 1) / 2>& r, const GemvArgs& g
     // buffer loads: a slot refilled past the wavefront's records gets an
     // out-of-range offset, so it costs no memory traffic (and no place in
     // the queue ahead of the epilogue's loads and stores)
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.w[ten]), 0, g.w_bytes, kBufferDword3);
+    // (the tensor's base by arithmetic on both fields, not an index into
+    // w: the kernel's copy of the arguments then stays in registers)
+    const uintptr_t w0 = reinterpret_cast<uintptr_t>(g.w[0]), w1 = reinterpret_cast<uintptr_t>(g.w[1]);
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<uint8_t*>(w0 + (ten ? w1 - w0 : 0)), 0,
+                                                      g.w_bytes, kBufferDword3);
     const uint32_t off = live ? (uint32_t)(rt * g.nb + b) * (uint32_t)kRecordBytes : kOutOfRange;
 #pragma unroll
     for (int i = 0; i < 6; ++i)
@@ -581,7 +585,7 @@ __device__ __forceinline__ void gemv_epilogue_y(GemvShared<NT, shared_layout<MOD
         const int row = (tile - ten * g.n_tiles) * kTileRows + lane;
         if (row < g.out_dim) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) g.y[ten][(size_t)t * g.out_dim + row] = sum[t];
+            for (int t = 0; t < NT; ++t) (ten ? g.y[1] : g.y[0])[(size_t)t * g.out_dim + row] = sum[t];
         }
     }
 }
@@ -653,8 +657,26 @@ __device__ __forceinline__ void gemv_epilogue_swiglu(GemvShared<1, 1>& sh, const
 // activation loads, a workgroup barrier with no memory wait, the first ring
 // slot, the grid table, the wavefront's own activation images, the other
 // slots), the record stream, the epilogue.
+// The fields the prologue needs first come as leading scalar arguments,
+// which the launch preloads into SGPRs (-amdgpu-kernarg-preload-count): the
+// first record loads then wait for no kernel-argument read (0.4 us earlier
+// on the 6144x12288 launch). The copy g takes them and reads the rest from
+// the kernel arguments; no field of it is indexed at run time, so it stays
+// in registers.
 template <int NT, int MODE, int EPI>
-__global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs g) {
+__global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(const uint8_t* w0, const uint8_t* w1,
+                                                                        const void* asrc, int chunk, int n_records,
+                                                                        int nb, GemvArgs g_in) {
+    GemvArgs g = g_in;
+    g.w[0] = w0;
+    g.w[1] = w1;
+    g.chunk = chunk;
+    g.n_records = n_records;
+    g.nb = nb;
+    if constexpr (MODE == 1 || MODE == 2)
+        g.x = static_cast<const float*>(asrc);
+    else
+        g.act = static_cast<const uint8_t*>(asrc);
     static_assert(MODE == 0 || NT == 1, "prepared-in-kernel and act64 activations take one vector");
     static_assert(EPI == 0 || (NT == 1 && MODE == 1), "the SwiGLU epilogue takes gate/up of one vector");
     constexpr int W = GemvCfg<NT>::kWaves;
@@ -686,10 +708,12 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(GemvArgs 
     for (int s = 1; s < PF; ++s) src.load(ring[s], s, lane);
     gemv_stream<NT, MODE, EPI>(sh, g, ring, src, ch, 0, ch.n_mine, wave, lane);
     lds_barrier();
+    // the epilogues read the kernel arguments themselves (g_in holds the
+    // same values as g)
     if constexpr (EPI == 0) {
-        gemv_epilogue_y<NT, MODE>(sh, g, ch, blockIdx.x, wave, lane);
+        gemv_epilogue_y<NT, MODE>(sh, g_in, ch, blockIdx.x, wave, lane);
     } else {
-        gemv_epilogue_swiglu(sh, g, ch, blockIdx.x, tid, wave, lane);
+        gemv_epilogue_swiglu(sh, g_in, ch, blockIdx.x, tid, wave, lane);
     }
 }
 
@@ -745,8 +769,9 @@ hipError_t launch_gemv_nt(const GemvPlan& plan, GemvArgs a, hipStream_t s) {
     if ((size_t)a.n_tiles * a.nb * kRecordBytes >= kOutOfRange) return hipErrorInvalidValue;
     a.chunk = plan.chunk;
     a.max_parts = plan.max_parts;
+    const void* asrc = (MODE == 1 || MODE == 2) ? static_cast<const void*>(a.x) : static_cast<const void*>(a.act);
     return launch_timed(kProfGemv, k_gemv_t64<NT, MODE, EPI>, dim3(plan.grid), dim3(GemvCfg<NT>::kWaves * 64), 0, s,
-                        a);
+                        a.w[0], a.w[1], asrc, a.chunk, a.n_records, a.nb, a);
 }
 
 // Largest chunk (records per workgroup) that touches at most S tiles.
