@@ -25,6 +25,10 @@ FLAGS = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # a kernel's first six scalar arguments are preloaded into SGPRs at wave
+    # launch, so its first loads wait for no kernel-argument read (the code
+    # object keeps a fallback that loads them on firmware without preloading)
+    "-mllvm", "-amdgpu-kernarg-preload-count=6",
 ]
 
 
@@ -37,10 +41,8 @@ def _run(cmd):
     return out
 
 
-# Per-source extra flags. iq3_gemv.hip: the GEMV kernel's six leading scalar
-# arguments are preloaded into SGPRs at wave launch (the code object keeps a
-# fallback that loads them for firmware without kernel-argument preloading).
-EXTRA = {"iq3_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=6"]}
+# Per-source extra flags: none at present.
+EXTRA: dict = {}
 
 
 def build(verbose: bool = False) -> str:
