@@ -333,7 +333,8 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
             const bool ok = q < n_items && nl < cols;
 #pragma unroll
             for (int z = 0; z < 8; ++z) {
-                const uint32_t off = ok && z < g.ks ? (uint32_t)(((z * BM + ml) * kTileN + nl) * 4) : 0x80000000u;
+                if (z >= g.ks) break;  // uniform: no load for splits that do not exist
+                const uint32_t off = ok ? (uint32_t)(((z * BM + ml) * kTileN + nl) * 4) : 0x80000000u;
                 v[u][z] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16));
             }
         }
