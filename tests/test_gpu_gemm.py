@@ -43,6 +43,13 @@ def as_bf16_tensor(xf, device):
     (37, 1536, 6144, 0, True),
     (1, 64, 256, 0, True),          # one token, one row tile, one block
     (65, 192, 512, 0, False),       # one token past the 64-token tile: 128-token tiles, fp32 input
+    # X preparation with 2, 4 and 8 register chunks per thread, and the
+    # two-pass form past 2048 chunks per row (K = 65 blocks: an odd block
+    # count under K halves keeps its split count)
+    (16, 64, 4096, 0, False),
+    (80, 64, 8192, 0, True),
+    (9, 64, 16384, 0, False),
+    (70, 64, 16640, 0, True),
 ])
 def test_gemm_small(gpu, M, N, K, row0, x_bf16):
     n_rows = row0 + N
@@ -107,7 +114,10 @@ def test_gemm_decode_mix_split_k(gpu, N, K, x_bf16):
     assert np.array_equal(Y, Y2)
 
 
-@pytest.mark.parametrize("M,H,I", [(64, 1024, 2048), (200, 512, 768), (64, 6144, 12288)])
+# (16, 256, 16640): the SwiGLU images of a row past 2048 register chunks
+# (two-pass preparation); (24, 512, 4096): two chunks per thread
+@pytest.mark.parametrize("M,H,I", [(64, 1024, 2048), (200, 512, 768), (64, 6144, 12288), (16, 256, 16640),
+                                   (24, 512, 4096)])
 def test_dense_mlp_batch_gemm(gpu, M, H, I):
     """dense_mlp_batch (model_batch.cpp:145-163) through the GEMM: gate and
     up GEMMs, then the down GEMM with SwiGLU formed while its images are
