@@ -266,6 +266,10 @@ __device__ __forceinline__ GemmArgs gemm_tensor(const GemmArgs& g, const GemmTil
 // rows are n0 + rbase + 16 j + lr (j < JT); a wavefront with active false
 // holds no rows of its own (its sums went to another wavefront) and only
 // joins the barriers and the last split's sum.
+template <int BM, int kTileN, int NTHR>
+__device__ __forceinline__ void gemm_split_finish(const GemmArgs& g, const GemmTile& t, int m0, int n0, int tid,
+                                                  int* flag);
+
 template <int MT, int JT = 3, int BN = kTileN, int NTHR = kGemmThreads>
 __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t, const float4_t (&acc)[MT][JT],
                                            int m0, int n0, int rbase, int lr, int lg, int tid, int* flag,
@@ -306,6 +310,17 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& g, const GemmTile& t,
                                        __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+    gemm_split_finish<BM, kTileN, NTHR>(g, t, m0, n0, tid, flag);
+}
+
+// After this split's partial went out (agent-scope write-through stores):
+// wait for their acknowledgement, take the tile's ticket; the last split adds
+// the partials in split order and writes Y, then clears the ticket.
+template <int BM, int kTileN, int NTHR>
+__device__ __forceinline__ void gemm_split_finish(const GemmArgs& g, const GemmTile& t, int m0, int n0, int tid,
+                                                  int* flag) {
+    const int tile = t.tm * g.tiles_n + t.tn;
+    float* base = g.part + (size_t)tile * g.ks * (BM * kTileN);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this split's partial is acknowledged
     __syncthreads();
     if (tid == 0) {
@@ -984,14 +999,12 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
 #pragma unroll
             for (int j = 0; j < JT; ++j) acc[mt][j] += red[(mt * JT + j) * 64];
     }
-    if (g.ks > 1) {
-        gemm_store<MT, JT, kTileN, kThreads5>(g, tl, acc, m0, n0, rq * 48, lr, (int)lg, tid, &sm.last_flag, kh == 0);
-        return;
-    }
-    // One K split: the K half 0 wavefronts leave the tile in LDS as rows of
-    // 192 floats (stride 196: the four token rows a store instruction touches
-    // fall on different banks), then every thread copies whole rows out,
-    // times the token's unscale, 16 bytes at a time.
+    // The K half 0 wavefronts leave the tile in LDS as rows of 192 floats
+    // (stride 196: the four token rows a store instruction touches fall on
+    // different banks), then every thread copies whole rows out 16 bytes at
+    // a time: one K split, Y times the token's unscale; several, this
+    // split's partial as write-through stores (cache policy sc1, agent
+    // scope) for the split-K sum.
     constexpr int kTStride = BN5 + 4;
     static_assert(BM * kTStride * 4 <= 2 * 2 * kXStage5 + 2 * 2 * kWHalf5, "output tile area");
     float* tile = reinterpret_cast<float*>(&sm.xs[0][0][0]);
@@ -1007,6 +1020,19 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     }
     __syncthreads();
     const int rows = min(BM, g.M - m0), cols = min(BN5, g.N - n0);
+    if (g.ks > 1) {
+        const int tile_id = tl.tm * g.tiles_n + tl.tn;
+        float* mine = g.part + ((size_t)tile_id * g.ks + tl.kz) * (BM * kTileN);
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(mine, 0, BM * kTileN * 4, 0x00020000);
+        for (int f = tid; f < rows * (BN5 / 4); f += kThreads5) {
+            const int m = f / (BN5 / 4), c4 = (f - m * (BN5 / 4)) * 4;
+            if (c4 >= cols) continue;
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&tile[m * kTStride + c4]);
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs, (uint32_t)((m * kTileN + c4) * 4), 0, 16);
+        }
+        gemm_split_finish<BM, kTileN, kThreads5>(g, tl, m0, n0, tid, &sm.last_flag);
+        return;
+    }
     const bool vec = (g.N & 3) == 0 && (reinterpret_cast<uintptr_t>(g.y) & 15u) == 0;
     for (int f = tid; f < rows * (BN5 / 4); f += kThreads5) {
         const int m = f / (BN5 / 4), c4 = (f - m * (BN5 / 4)) * 4;
