@@ -78,10 +78,13 @@ def lib():
             "gpeed_iq3xxs_untile": ([vp, u64, i64, vp, vp], i32),
             "gpeed_iq3xxs_matvec_ws_bytes": ([i64, i64], sz),
             "gpeed_iq3xxs_matmul_ws_bytes": ([i64, i64, i32], sz),
+            "gpeed_iq3xxs_matmul_ws_bytes_for": ([i64, i64, i32, i32], sz),
             "gpeed_iq3xxs_matvec": ([vp, u64, u64, i32, i32, vp, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_matmul": ([vp, u64, u64, i32, i32, vp, i32, vp, vp, sz, vp], i32),
             "gpeed_iq3xxs_matvec_raw": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
             "gpeed_iq3xxs_matvec_noalloc": ([vp, u64, u64, i32, i32, vp, vp, vp], i32),
+            "gpeed_iq3xxs_matvec_noalloc_status": ([vp], i32),
+            "gpeed_iq3xxs_matvec_noalloc_poke": ([sz, C.c_uint32], i32),
             "gpeed_iq3xxs_act_bytes": ([i64, i32], sz),
             "gpeed_iq3xxs_prep_act": ([vp, i64, i32, vp, sz, vp], i32),
             "gpeed_iq3xxs_prep_swiglu": ([vp, vp, i64, i32, C.c_float, vp, sz, vp], i32),
@@ -698,6 +701,12 @@ class WeightStore:
             ws = self._ws[key] = matmul_workspace(in_dim, out_dim, n_tok, self.device)
         return ws
 
+    @staticmethod
+    def _row0_shift(row0: int, out_dim: int, n_rows: int, name: str) -> int:
+        if row0 < 0 or row0 + out_dim > n_rows:
+            raise GpeedError(-1, f"weights: rows outside {name}")
+        return row0 % 64
+
     def matvec_quant(self, name: str, row0: int, in_dim: int, out_dim: int, x, dst=None):
         torch = _torch()
         t64, _, n_rows, dtype = self._get(name, in_dim)
@@ -709,8 +718,12 @@ class WeightStore:
             yd = matmul_rows(dtype, t64, n_rows, row0, in_dim, out_dim, xd.reshape(in_dim))
             ws = None
         else:
-            ws = self._workspace(in_dim, out_dim, 1)
-            yd = matvec(t64, n_rows, row0, in_dim, out_dim, xd, ws=ws)
+            # T64 products start on a 64-row tile; a row0 inside one runs from
+            # the tile's first row and keeps rows row0.. (weights.cpp:167-203
+            # takes any row0)
+            shift = self._row0_shift(row0, out_dim, n_rows, name)
+            ws = self._workspace(in_dim, out_dim + shift, 1)
+            yd = matvec(t64, n_rows, row0 - shift, in_dim, out_dim + shift, xd, ws=ws)[shift:]
         if host:
             if ws is not None:
                 ws_status(ws)  # synchronous, like the reference: report a flagged workspace here
@@ -736,8 +749,11 @@ class WeightStore:
             Yd = matmul_rows(dtype, t64, n_rows, row0, in_dim, out_dim, Xd)
             ws = None
         else:
-            ws = self._workspace(in_dim, out_dim, n_tok)
-            Yd = matmul(t64, n_rows, row0, in_dim, out_dim, Xd, ws=ws)
+            shift = self._row0_shift(row0, out_dim, n_rows, name)
+            ws = self._workspace(in_dim, out_dim + shift, n_tok)
+            Yd = matmul(t64, n_rows, row0 - shift, in_dim, out_dim + shift, Xd, ws=ws)
+            if shift:
+                Yd = Yd.reshape(n_tok, out_dim + shift)[:, shift:].contiguous()
         if host:
             if ws is not None:
                 ws_status(ws)

@@ -64,18 +64,35 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 std::mutex g_noalloc_mu;
 void* g_noalloc[kMaxDevices] = {};
 
+// Zero-fills this device's copy of `scratch` (at p) on `s` and waits for
+// the fill, so that a call from any stream afterwards sees it cleared.
+int noalloc_clear(void* p, hipStream_t s) {
+    hipError_t e = gpeed::launch_fill_zero(p, kNoAllocScratchBytes, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "clearing the no-allocation scratch");
+}
+
 // This device's copy of `scratch` (looked up once per device, with that
-// device current) and zero-filled on `s` the first time. No allocation.
+// device current), zero-filled on `s` the first time; the pointer is
+// published only once the fill has completed. The first use cannot be on a
+// stream under graph capture (its wait is not allowed there): gpeed_init
+// does it ahead of time. No allocation.
 int noalloc_scratch(int dev, hipStream_t s, void** out) {
     void* p = __atomic_load_n(&g_noalloc[dev], __ATOMIC_ACQUIRE);
     if (!p) {
         std::lock_guard<std::mutex> lk(g_noalloc_mu);
         p = g_noalloc[dev];
         if (!p) {
-            hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            hipError_t e = hipStreamIsCapturing(s, &cs);
+            if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+            if (cs != hipStreamCaptureStatusNone)
+                return fail(GPEED_ERR_INVALID,
+                            "matvec_noalloc: first use on this device under graph capture; call gpeed_init first");
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
             if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-            e = gpeed::launch_fill_zero(p, kNoAllocScratchBytes, s);
-            if (e != hipSuccess) return hip_fail(e, "clearing the no-allocation scratch");
+            const int rc = noalloc_clear(p, s);
+            if (rc) return rc;
             __atomic_store_n(&g_noalloc[dev], p, __ATOMIC_RELEASE);
         }
     }
@@ -356,6 +373,10 @@ int gpeed_matmul_rows(int dtype, const void* w, uint64_t n_rows, uint64_t row0, 
     const size_t rb = gpeed_dtype_row_bytes(dtype, (uint64_t)in_dim);
     hipError_t e = gpeed::launch_matmul_rows(dtype, static_cast<const uint8_t*>(w), rb, row0, in_dim, out_dim, X,
                                              n_tok, Y, static_cast<hipStream_t>(stream));
+    // (the type is known here, so the only invalid value left is a row
+    // length whose per-wavefront row group passes the 2 GiB offset range)
+    if (e == hipErrorInvalidValue)
+        return fail(GPEED_ERR_INVALID, "matmul_rows: rows too long (one wavefront's rows exceed 2 GiB)");
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "matmul_rows launch");
 }
 
@@ -453,19 +474,33 @@ static size_t matmul_tail(int64_t in_dim, int64_t out_dim, int n_tok, int num_cu
     if (n_tok < 2) return 0;
     size_t t = align256(gpeed::act_bytes((int)in_dim, n_tok < kMaxTok ? n_tok : kMaxTok));
     if (n_tok >= kMatmulGemmMinTok) {
-        // the GEMM's partials change only where the token tile count does
-        // (64-token tiles up to 64 tokens, 128-token tiles above), and its
-        // images grow with the tokens: the largest need up to n_tok is at
-        // one of those boundaries or at n_tok itself
+        // matmul hands the GEMM fp32 X, which it tiles by 64 tokens at every
+        // size. The split-K count (so the partials) depends only on the
+        // token tile count and is not monotonic in it, while the images grow
+        // with the tokens: the largest need of one tile count is at its last
+        // token count, so every count's need is covered by taking the maximum
+        // over the last count of each tile count below n_tok and n_tok
+        // itself. From the first tile count without split K on, no larger
+        // count splits either (more tiles), so only the images grow.
         auto g = [&](int m) {
             return align256(gpeed::gemm_ws_bytes(m, (int)out_dim, (int)in_dim, 0, num_cus));
         };
         size_t best = g(n_tok);
-        for (int m = 64; m < n_tok; m += (m < 128 ? 64 : 128))
-            if (m >= kMatmulGemmMinTok) best = std::max(best, g(m));
+        const int bm = gpeed::gemm_tile_m(n_tok, 0);
+        for (int m = bm; m < n_tok; m += bm) {
+            if (m < kMatmulGemmMinTok) continue;
+            best = std::max(best, g(m));
+            if (gpeed::gemm_splits(m, (int)out_dim, (int)in_dim, num_cus, 0) == 1) break;
+        }
         t = std::max(t, best);
     }
     return t;
+}
+
+static size_t matmul_ws_bytes_cus(int64_t in_dim, int64_t out_dim, int n_tok, int num_cus) {
+    if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(in_dim) || out_dim <= 0 || out_dim > (1 << 24)) return 0;
+    if (n_tok == 1) return matmul_front(in_dim, out_dim, 1);
+    return matmul_front(in_dim, out_dim, kMaxTok) + matmul_tail(in_dim, out_dim, n_tok, num_cus);
 }
 
 size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok) {
@@ -473,7 +508,12 @@ size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok) 
     if (n_tok == 1) return matmul_front(in_dim, out_dim, 1);
     const DeviceState* st = nullptr;
     if (device_state(&st)) return 0;
-    return matmul_front(in_dim, out_dim, kMaxTok) + matmul_tail(in_dim, out_dim, n_tok, st->num_cus);
+    return matmul_ws_bytes_cus(in_dim, out_dim, n_tok, st->num_cus);
+}
+
+size_t gpeed_iq3xxs_matmul_ws_bytes_for(int64_t in_dim, int64_t out_dim, int n_tok, int num_cus) {
+    if (num_cus < 1 || num_cus > (1 << 16)) return 0;
+    return matmul_ws_bytes_cus(in_dim, out_dim, n_tok, num_cus);
 }
 
 size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim, int64_t out_dim) {
@@ -756,6 +796,44 @@ int gpeed_iq3xxs_matvec_noalloc(const void* w_t64, uint64_t n_rows, uint64_t row
                              static_cast<uint8_t*>(sp) + gpeed::kWsHeader, static_cast<uint32_t*>(sp), st->num_cus,
                              s);
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec_noalloc launch");
+}
+
+int gpeed_iq3xxs_matvec_noalloc_status(gpeed_stream_t stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(GPEED_ERR_INVALID, "device index out of range");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    void* sp = nullptr;
+    int rc = noalloc_scratch(dev, s, &sp);
+    if (rc) return rc;
+    uint32_t flags = 0;
+    e = hipMemcpyAsync(&flags, sp, sizeof flags, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "matvec_noalloc_status");
+    if (flags == 0) return GPEED_OK;
+    // a flagged call may have left tickets and tagged partials behind: the
+    // whole array starts again from zero
+    rc = noalloc_clear(sp, s);
+    if (rc) return rc;
+    std::string msg = "matvec_noalloc_status: scratch flagged:";
+    if (flags & gpeed::kWsTicket) msg += " ticket count past the parts of a tile (calls overlapped)";
+    if (flags & gpeed::kWsTimeout) msg += " a wait for another workgroup's partial gave up";
+    return fail(GPEED_ERR_WS_STATE, msg + "; cleared");
+}
+
+int gpeed_iq3xxs_matvec_noalloc_poke(size_t offset, uint32_t value) {
+    if (offset % 4 || offset + 4 > kNoAllocScratchBytes)
+        return fail(GPEED_ERR_INVALID, "matvec_noalloc_poke: offset not a word inside the scratch");
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(GPEED_ERR_INVALID, "device index out of range");
+    void* sp = nullptr;
+    const int rc = noalloc_scratch(dev, nullptr, &sp);
+    if (rc) return rc;
+    e = hipMemcpy(static_cast<uint8_t*>(sp) + offset, &value, sizeof value, hipMemcpyHostToDevice);
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "matvec_noalloc_poke");
 }
 
 size_t gpeed_moe_route_ws_bytes(int n_tok, int n_exp, int top_k) {

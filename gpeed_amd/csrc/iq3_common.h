@@ -131,10 +131,13 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // SwiGLU with the reference's clamp (model_batch.cpp:245-253):
-// silu(min(g, lim)) * clamp(u, -lim, lim).
+// silu(min(g, lim)) * clamp(u, -lim, lim) as std::min and std::clamp
+// compute them: min(g, lim) = lim < g ? lim : g and clamp(u, lo, hi) =
+// u < lo ? lo : (hi < u ? hi : u), so a NaN g or u stays NaN (fminf and
+// fmaxf would turn it into a bound).
 __device__ __forceinline__ float swiglu1(float gv, float uv, float lim) {
-    const float gi = fminf(gv, lim);
-    const float ui = fminf(fmaxf(uv, -lim), lim);
+    const float gi = lim < gv ? lim : gv;
+    const float ui = uv < -lim ? -lim : (lim < uv ? lim : uv);
     return (gi / (1.0f + expf(-gi))) * ui;
 }
 

@@ -579,6 +579,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
     };
 
     float4_t acc[MT][3], blk[MT][3];
+    // per row: the sum of d - d over its blocks, 0 while every d is finite
+    // and NaN after an infinite or NaN one; added at the end, it makes such
+    // a row NaN, as the reference's sum of the block's +-inf products of
+    // both signs does (d/4 times the finite partial would give +-inf)
+    float pz[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -646,6 +651,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
                 for (int j = 0; j < 3; ++j) {
                     const uint16_t dh = *reinterpret_cast<const uint16_t*>(&sm.wd[c & 1][d_off[j]]);
                     const float d4 = (float)__builtin_bit_cast(_Float16, dh) * 0.25f;
+                    pz[j] += d4 - d4;
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -658,6 +664,10 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
             xb0 = xb1;
         });
     }
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][j] += pz[j];
 
     gemm_store<MT>(g, tl, acc, m0, n0, wave * 48, lr, (int)lg, tid, &sm.last_flag);
 }
@@ -881,6 +891,13 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
 #pragma unroll
         for (int j = 0; j < JT; ++j) acc[i][j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float dcur[JT], dnext[JT];
+    // per row: the sum of d - d over its blocks (0 while every d is finite,
+    // NaN after an infinite or NaN one), added at the end: such a row is
+    // NaN, as the reference's sum of the block's +-inf products of both
+    // signs is (the running-d rescale alone would give +-inf or 0)
+    float pz[JT];
+#pragma unroll
+    for (int j = 0; j < JT; ++j) pz[j] = 0.0f;
     uint32_t amask[JT], azero[JT];
 
     // block c's d per row (0 past this half's blocks): the table masks for
@@ -896,6 +913,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
             amask[j] = z ? 0u : 0x7800u;
             azero[j] = z ? kZeroEntry5 : 0u;
             dnext[j] = dn;
+            pz[j] += dn - dn;
         }
     };
     // the accumulators move to the units of dnext where it is nonzero and differs
@@ -982,7 +1000,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     for (int j = 0; j < JT; ++j) {
         const float f = dcur[j] * 0.25f;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= f;
+        for (int mt = 0; mt < MT; ++mt) acc[mt][j] = acc[mt][j] * f + pz[j];
     }
     // K half 1 -> LDS (over xs and wb, free after the last barrier); K half 0 adds
     float4_t* red = reinterpret_cast<float4_t*>(&sm.xs[0][0][0]) + (size_t)rq * (MT * JT * 64) + lane;
@@ -1176,6 +1194,13 @@ __global__ __launch_bounds__(kThreads6) void k_gemm6(GemmArgs g_all) {
 #pragma unroll
         for (int j = 0; j < JT; ++j) acc[i][j] = float16_t{};
     float dcur[JT], dnext[JT];
+    // per row: the sum of d - d over its blocks (0 while every d is finite,
+    // NaN after an infinite or NaN one), added at the end: such a row is
+    // NaN, as the reference's sum of the block's +-inf products of both
+    // signs is (the running-d rescale alone would give +-inf or 0)
+    float pz[JT];
+#pragma unroll
+    for (int j = 0; j < JT; ++j) pz[j] = 0.0f;
     uint32_t smask[JT], szero[JT];
 
     auto block_d = [&](int c) {
@@ -1189,6 +1214,7 @@ __global__ __launch_bounds__(kThreads6) void k_gemm6(GemmArgs g_all) {
             smask[j] = z ? 0u : 0x7800u;
             szero[j] = z ? kZeroEntry5 : 0u;
             dnext[j] = dn;
+            pz[j] += dn - dn;
         }
     };
     auto rescale = [&]() {
@@ -1272,7 +1298,7 @@ __global__ __launch_bounds__(kThreads6) void k_gemm6(GemmArgs g_all) {
     for (int j = 0; j < JT; ++j) {
         const float f = dcur[j] * 0.25f;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][j] *= f;
+        for (int mt = 0; mt < MT; ++mt) acc[mt][j] = acc[mt][j] * f + pz[j];
     }
     // K half 1 -> LDS (over tbl, xs and wb, free after the last barrier); K half 0 adds
     float4* red = reinterpret_cast<float4*>(&sm.tbl[0]) + (size_t)rg * (MT * JT * 4 * 64) + lane;

@@ -72,9 +72,7 @@ __global__ __launch_bounds__(256) void k_prep_act(const float* __restrict__ x,
         const float us[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const float gi = fminf(e[c], lim);
-            const float ui = fminf(fmaxf(us[c], -lim), lim);
-            e[c] = (gi / (1.0f + expf(-gi))) * ui;
+            e[c] = swiglu1(e[c], us[c], lim);
         }
     }
     const int sc =
@@ -421,6 +419,13 @@ __device__ __forceinline__ void gemv_stream(GemvShared<NT, shared_layout<MODE>()
             }
             if (valid) {
                 const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)ring[s].d) * 0.25f;
+                // 0 for a finite d, NaN for an infinite or NaN one: the
+                // reference sums a block of d = +-inf as +-inf products of
+                // both signs (NaN), where d * (finite partial) would give
+                // +-inf, so such a block makes the row NaN
+                const float dz = d4 - d4;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] += dz;
                 if constexpr (kPrep) {
                     const uint8_t* a_src = sh.xsl + (wave * KP + kk) * 1024 + ((lane >> 2) * 2 + (lane & 1)) * 8;
 #pragma unroll
@@ -739,6 +744,9 @@ __global__ __launch_bounds__(256) void k_matvec_raw(const uint8_t* __restrict__ 
         const float d = f16_bits_to_f32(h[0]);
         const uint32_t aux = (uint32_t)h[33 + 2 * ib] | ((uint32_t)h[34 + 2 * ib] << 16);
         const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+        // an infinite or NaN d makes the row NaN (the reference's +-inf
+        // products of both signs)
+        acc += d - d;
         const float4* xv = reinterpret_cast<const float4*>(x + (size_t)b * 256 + ib * 32);
         float part = 0.0f;
 #pragma unroll

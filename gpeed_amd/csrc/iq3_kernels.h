@@ -155,6 +155,8 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
 // every launch, and fp32 partials). Returns hipErrorInvalidValue when a
 // tensor's requested rows hold 4 GiB of records or more (32-bit offsets).
 int gemm_splits(int M, int N, int K, int num_cus, int x_bf16, int tile_n = 192);
+// Token rows of one result tile (64, or 128 for bf16 X of more than 64 tokens).
+int gemm_tile_m(int M, int x_bf16);
 size_t gemm_ws_bytes(int M, int N, int K, int x_bf16, int num_cus);
 // U (fp32, with x_bf16 = 0): X is SwiGLU(X, U) with clamp lim, formed while
 // the images are prepared.

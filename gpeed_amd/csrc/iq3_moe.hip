@@ -533,9 +533,7 @@ __global__ __launch_bounds__(256) void k_prep_grouped(const float* __restrict__ 
         const float us[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const float gi = fminf(e[c], lim);
-            const float ui = fminf(fmaxf(us[c], -lim), lim);
-            e[c] = (gi / (1.0f + expf(-gi))) * ui;
+            e[c] = swiglu1(e[c], us[c], lim);
         }
     }
     const BlockImages im = block_images(e);
@@ -743,9 +741,12 @@ __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, ui
                 for (int t = 0; t < 2 * NP; ++t) blk[t] = 0.0f;
                 record_dot<NP>(tbl, ring[s], lb, blk);
                 const float d4 = (float)__builtin_bit_cast(_Float16, (uint16_t)ring[s].d) * 0.25f;
+                // an infinite or NaN d makes the row NaN, as the reference's
+                // sum of that block's +-inf products of both signs does
+                const float dz = d4 - d4;
 #pragma unroll
                 for (int t = 0; t < 2 * NP; ++t)
-                    if (t < n) acc[t] = fmaf(d4 * rec_unscale(ring[s], t), blk[t], acc[t]);
+                    if (t < n) acc[t] = fmaf(d4 * rec_unscale(ring[s], t), blk[t], acc[t] + dz);
                 if (++kb == nb) {  // uniform
 #pragma unroll
                     for (int t = 0; t < 2 * NP; ++t) {

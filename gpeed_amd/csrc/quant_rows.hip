@@ -461,6 +461,8 @@ hipError_t matmul_dt_nt(const uint8_t* w, size_t rb, int in_dim, int out_dim, co
     // most 32768 token columns per launch
     constexpr int RW = RowsCfg<DT>::kRW;
     const long long max_rows = ((1ll << 31) - 64) / (long long)rb / (4 * RW) * (4 * RW);
+    // rows so long that one wavefront's rows pass 2 GiB cannot be sliced
+    if (max_rows < 1) return hipErrorInvalidValue;
     constexpr int kMaxTok = 32768 * NT;
     for (int j = 0; j < out_dim; j += (int)max_rows) {
         const int rows = out_dim - j < max_rows ? out_dim - j : (int)max_rows;

@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstring>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -221,19 +222,7 @@ void WeightStore::matvec_quant(const std::string& name, uint64_t row0, int in_di
         rows_product(t, name, row0, in_dim, out_dim, x, 1, dst);
         return;
     }
-    const size_t xb = (size_t)in_dim * sizeof(float), yb = (size_t)out_dim * sizeof(float);
-    void* xd = scratch(x_, xb, false);
-    void* yd = scratch(y_, yb, false);
-    const size_t wsb = gpeed_iq3xxs_matvec_ws_bytes(in_dim, out_dim);
-    if (wsb == 0) throw std::runtime_error("weights: unsupported shape for " + name);
-    Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
-    void* ws = scratch(wbuf, wsb, true);
-    check(gpeed_memcpy(xd, x, xb, kH2D), "weights: upload x");
-    check(gpeed_iq3xxs_matvec(t.data, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd),
-                              static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
-          ("weights: matvec_quant " + name).c_str());
-    check_ws(ws, "weights: matvec_quant " + name);
-    check(gpeed_memcpy(dst, yd, yb, kD2H), "weights: download y");
+    iq3_product(t, name, row0, in_dim, out_dim, x, 1, dst, "matvec_quant");
 }
 
 void WeightStore::matmul_quant(const std::string& name, uint64_t row0, int in_dim, int out_dim, const float* X,
@@ -244,19 +233,39 @@ void WeightStore::matmul_quant(const std::string& name, uint64_t row0, int in_di
         rows_product(t, name, row0, in_dim, out_dim, X, n_tok, Y);
         return;
     }
-    const size_t xb = (size_t)n_tok * in_dim * sizeof(float), yb = (size_t)n_tok * out_dim * sizeof(float);
+    iq3_product(t, name, row0, in_dim, out_dim, X, n_tok, Y, "matmul_quant");
+}
+
+// The T64 products start on a 64-row tile. The reference takes any row0
+// (weights.cpp:86-203), so a row0 inside a tile runs the product from the
+// tile's first row (at most 63 rows more) and keeps rows row0.. of the
+// result: the values of those rows are the same either way.
+void WeightStore::iq3_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,
+                              const float* X, int n_tok, float* Y, const char* who) {
+    const uint64_t shift = row0 % 64;
+    if (row0 > t.n_rows || (uint64_t)out_dim > t.n_rows - row0)
+        throw std::runtime_error(std::string("weights: ") + who + " rows outside " + name);
+    const int out_a = out_dim + (int)shift;
+    const size_t xb = (size_t)n_tok * in_dim * sizeof(float), yb = (size_t)n_tok * out_a * sizeof(float);
     void* xd = scratch(x_, xb, false);
     void* yd = scratch(y_, yb, false);
-    const size_t wsb = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_dim, n_tok);
+    const size_t wsb = gpeed_iq3xxs_matmul_ws_bytes(in_dim, out_a, n_tok);
     if (wsb == 0) throw std::runtime_error("weights: unsupported shape for " + name);
-    Buffer& wbuf = ws_[std::make_tuple(in_dim, out_dim)];
+    Buffer& wbuf = ws_[std::make_tuple(in_dim, out_a)];
     void* ws = scratch(wbuf, wsb, true);
     check(gpeed_memcpy(xd, X, xb, kH2D), "weights: upload x");
-    check(gpeed_iq3xxs_matmul(t.data, t.n_rows, row0, in_dim, out_dim, static_cast<const float*>(xd), n_tok,
+    check(gpeed_iq3xxs_matmul(t.data, t.n_rows, row0 - shift, in_dim, out_a, static_cast<const float*>(xd), n_tok,
                               static_cast<float*>(yd), ws, wbuf.bytes, nullptr),
-          ("weights: matmul_quant " + name).c_str());
-    check_ws(ws, "weights: matmul_quant " + name);
-    check(gpeed_memcpy(Y, yd, yb, kD2H), "weights: download y");
+          (std::string("weights: ") + who + " " + name).c_str());
+    check_ws(ws, std::string("weights: ") + who + " " + name);
+    if (shift == 0) {
+        check(gpeed_memcpy(Y, yd, yb, kD2H), "weights: download y");
+        return;
+    }
+    std::vector<float> full((size_t)n_tok * out_a);
+    check(gpeed_memcpy(full.data(), yd, yb, kD2H), "weights: download y");
+    for (int tk = 0; tk < n_tok; ++tk)
+        std::memcpy(Y + (size_t)tk * out_dim, full.data() + (size_t)tk * out_a + shift, (size_t)out_dim * sizeof(float));
 }
 
 void WeightStore::rows_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,

@@ -132,6 +132,8 @@ private:
     };
     const Tensor& get(const std::string& name, int in_dim);
     const Tensor& get_iq3(const std::string& name, int in_dim);
+    void iq3_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,
+                     const float* X, int n_tok, float* Y, const char* who);
     void rows_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,
                       const float* X, int n_tok, float* Y);
     void* scratch(Buffer& b, size_t bytes, bool init);

@@ -193,6 +193,10 @@ int gpeed_iq3xxs_untile(const void* t64, uint64_t n_rows, int64_t in_dim, void* 
  * workspace per stream: calls that run concurrently must not share one. */
 size_t gpeed_iq3xxs_matvec_ws_bytes(int64_t in_dim, int64_t out_dim);
 size_t gpeed_iq3xxs_matmul_ws_bytes(int64_t in_dim, int64_t out_dim, int n_tok);
+/* The same size for a device with num_cus compute units, computed on the
+ * host without touching a device (sizing ahead of time, or on a machine
+ * without the GPU). 0 for arguments the call would refuse. */
+size_t gpeed_iq3xxs_matmul_ws_bytes_for(int64_t in_dim, int64_t out_dim, int n_tok, int num_cus);
 /* Token count from which gpeed_iq3xxs_matmul runs the prefill GEMM (one pass
  * over W) instead of 8-token GEMV passes (one pass per 8 tokens). */
 int gpeed_iq3xxs_matmul_gemm_min_tok(void);
@@ -216,6 +220,21 @@ int gpeed_iq3xxs_matvec(const void* w_t64, uint64_t n_rows, uint64_t row0, int i
  * nothing and calls no allocating routine. */
 int gpeed_iq3xxs_matvec_noalloc(const void* w_t64, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                                 const float* x, float* dst, gpeed_stream_t stream);
+/* No counterpart in the reference (the status call of the entry point
+ * above, for the same callers that cannot allocate): waits for `stream`,
+ * then returns GPEED_OK if no kernel flagged this GPU's fixed scratch since
+ * the last check, else GPEED_ERR_WS_STATE (gpeed_last_error names the
+ * flags, as gpeed_ws_status) after zero-filling the whole array again, so
+ * the next call starts clean. Results of calls since the last check are
+ * unreliable when it reports a flag. Allocates nothing; not for use under
+ * graph capture (it waits). */
+int gpeed_iq3xxs_matvec_noalloc_status(gpeed_stream_t stream);
+/* Test aid for the status call (no reference counterpart): writes one
+ * 32-bit word at byte `offset` (a multiple of 4) of this GPU's fixed scratch,
+ * synchronously. The scratch starts with the workspace header (error word at
+ * 0), then at byte 256 one ticket word per 64-row tile of the last shape.
+ * Allocates nothing. */
+int gpeed_iq3xxs_matvec_noalloc_poke(size_t offset, uint32_t value);
 /* Y[t][j] = sum_i W[row0+j][i] * X[t][i] for t < n_tok (X [n_tok][in_dim],
  * Y [n_tok][out_dim], fp32, row-major). Row t of Y is the matvec of X[t]
  * (weights.cpp:86-165 makes the same promise) up to fp32 summation order.

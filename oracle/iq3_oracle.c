@@ -200,10 +200,12 @@ int orc_matmul_quant(const uint8_t* w, uint64_t row0, int in_dim, int out_dim, c
 }
 
 /* model_batch.cpp:245-253 / model.cpp:683-688: silu(min(g,lim)) * clamp(u,-lim,lim)
- * with silu(x) = x / (1 + exp(-x)) (ops.h:17). */
+ * with silu(x) = x / (1 + exp(-x)) (ops.h:17). std::min(g, lim) is
+ * `lim < g ? lim : g` and std::clamp(u, lo, hi) is `u < lo ? lo : (hi < u ?
+ * hi : u)`: a NaN g or u passes through both. */
 static float swiglu1(float g, float u, float lim) {
-    const float gi = g < lim ? g : lim;
-    const float ui = u < -lim ? -lim : (u > lim ? lim : u);
+    const float gi = lim < g ? lim : g;
+    const float ui = u < -lim ? -lim : (lim < u ? lim : u);
     return (gi / (1.0f + expf(-gi))) * ui;
 }
 

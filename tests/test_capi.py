@@ -222,3 +222,31 @@ def test_moe_check_buckets_host():
         with pytest.raises(gpeed_amd.GpeedError) as err:
             gpeed_amd.moe_check_buckets(e, t, E, T, K)
         assert err.value.code == -1 and what in str(err.value), (what, str(err.value))
+
+
+@pytest.mark.parametrize("in_dim,out_dim", [(6144, 12288), (12288, 6144), (6144, 3072), (6144, 576),
+                                            (6144, 1536), (2048, 6144), (6144, 2048)])
+@pytest.mark.parametrize("num_cus", [256, 304, 80])
+def test_matmul_workspace_covers_every_smaller_call(in_dim, out_dim, num_cus):
+    """A matmul workspace sized for n tokens serves every call with fewer
+    tokens (the header's promise): the size is non-decreasing in n_tok on the
+    GLM5 dense and latent shapes, for several CU counts (host arithmetic
+    only; the split-K count is not monotonic in the token tile count)."""
+    f = gpeed_amd.lib().gpeed_iq3xxs_matmul_ws_bytes_for
+    sizes = np.array([f(in_dim, out_dim, n, num_cus) for n in range(1, 1025)], np.int64)
+    assert (sizes > 0).all()
+    prefix_max = np.maximum.accumulate(sizes)
+    bad = np.nonzero(sizes < prefix_max)[0]
+    assert bad.size == 0, [(int(i) + 1, int(sizes[i]), int(prefix_max[i])) for i in bad[:5]]
+
+
+def test_matmul_rows_refuses_rows_past_the_offset_range():
+    """gpeed_matmul_rows refuses a row length whose per-wavefront row group
+    passes the kernels' 2 GiB buffer offsets (before any launch, so this
+    runs without a device: the pointers are never dereferenced)."""
+    L = gpeed_amd.lib()
+    fake = C.c_void_p(1 << 20)
+    for dt, in_dim in ((0, 1 << 28), (1, 1 << 28), (8, 1 << 28)):
+        rc = L.gpeed_matmul_rows(dt, fake, 8, 0, in_dim, 4, fake, 1, fake, None)
+        assert rc == -1, (dt, rc, L.gpeed_last_error())
+        assert b"rows too long" in L.gpeed_last_error()

@@ -36,7 +36,11 @@ def test_errors_match_reference(gpu):
 
 @pytest.mark.parametrize("n_rows,in_dim,row0,out_dim,n_tok", [(200, 1536, 64, 136, 3), (6144, 12288, 0, 6144, 1),
                                                              (300, 512, 0, 300, 11), (704, 1536, 64, 600, 9),
-                                                             (704, 1536, 64, 600, 64), (704, 1536, 64, 600, 512)])
+                                                             (704, 1536, 64, 600, 64), (704, 1536, 64, 600, 512),
+                                                             # row0 inside a 64-row tile (weights.cpp:86-203
+                                                             # takes any row0): GEMV and GEMM sides
+                                                             (200, 1536, 3, 136, 1), (200, 1536, 3, 136, 5),
+                                                             (704, 1536, 67, 600, 33), (300, 512, 299, 1, 2)])
 def test_matvec_matmul_quant(gpu, tmp_path, n_rows, in_dim, row0, out_dim, n_tok):
     w = synth.iq3xxs_matrix(80, n_tok, n_rows, in_dim)
     X = synth.normal(80, 1, n_tok * in_dim).reshape(n_tok, in_dim)

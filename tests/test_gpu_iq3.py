@@ -380,6 +380,16 @@ def test_weight_store_mirror(gpu):
     ref = oracle.matmul(w, 0, 512, 100, X)
     assert max(rel_err(Y[t], ref[t]) for t in range(5)) < TIGHT
     assert ws.matmul_quant("blk.0.ffn_up.weight", 0, 512, 100, X, 0) is None
+    # any row0, as weights.cpp:86-203: a row0 inside a 64-row tile
+    y = ws.matvec_quant("blk.0.ffn_up.weight", 3, 512, 70, x)
+    assert y.shape == (70,) and rel_err(y, oracle.matvec(w, 3, 512, 70, x)) < TIGHT
+    for n_tok in (5, 12):
+        Xn = np.stack([synth.normal(57, 20 + t, 512) for t in range(n_tok)])
+        Y = ws.matmul_quant("blk.0.ffn_up.weight", 3, 512, 125, Xn, n_tok)
+        ref = oracle.matmul(w, 3, 512, 125, Xn)
+        assert Y.shape == (n_tok, 125) and max(rel_err(Y[t], ref[t]) for t in range(n_tok)) < TIGHT
+    with pytest.raises(RuntimeError, match="rows outside"):
+        ws.matvec_quant("blk.0.ffn_up.weight", 100, 512, 29, x)
     with pytest.raises(RuntimeError, match="missing tensor"):
         ws.matvec_quant("nope", 0, 512, 16, x)
     with pytest.raises(RuntimeError, match="not block aligned"):

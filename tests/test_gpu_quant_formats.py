@@ -72,7 +72,7 @@ def test_rows_product_golden(gpu, dt):
 
 
 @pytest.mark.parametrize("dt", ALL_TYPES)
-@pytest.mark.parametrize("n_tok", [1, 3, 8, 13])
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 8, 13])
 def test_rows_product_vs_oracle(gpu, dt, n_tok):
     in_dim, rows, row0, out_dim = 2048, 200, 37, 150
     w = synth.quant_matrix(43, dt, dt, rows, in_dim)

@@ -230,6 +230,52 @@ def test_oracle_bitwise_vs_reference_build():
         assert np.array_equal(bits(p), bits(q))
 
 
+@pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref not built (needs the reference checkout)")
+@pytest.mark.parametrize("in_dim", [2048, 4096])
+def test_oracle_edge_blocks_bitwise_vs_reference_build(in_dim):
+    """The oracle's dequant, matvec and matmul on the edge-case matrices the
+    GPU edge tests use (d = +-0, subnormal, +-65504, 2^+-20 jumps, +-inf,
+    NaN): bit for bit the reference's own build, NaN positions included;
+    and every row holding an infinite or NaN d is NaN in the reference
+    (its +-inf products have both signs), the class the GPU must give."""
+    from edge_cases import edge_matrix
+
+    n_rows = 96
+    w = edge_matrix(70, 9, n_rows, in_dim, nonfinite=True)
+    R = oracle.ref()
+    deq = np.empty(n_rows * in_dim, np.float32)
+    assert R.ref_dequantize(18, w.ctypes.data, deq, deq.size) == 0
+    assert same_bits_or_nan(oracle.dequantize(w, deq.size), deq)
+    st = oracle.RefStore(w, n_rows, in_dim)
+    x = synth.normal(70, 1, in_dim)
+    yr = st.matvec(0, in_dim, n_rows, x)
+    assert same_bits_or_nan(oracle.matvec(w, 0, in_dim, n_rows, x), yr)
+    X = synth.normal(70, 2, 3 * in_dim).reshape(3, in_dim)
+    assert same_bits_or_nan(oracle.matmul(w, 0, in_dim, n_rows, X), st.matmul(0, in_dim, n_rows, X))
+    d = w.reshape(n_rows, -1, 98)[:, :, 0:2].copy().view(np.float16)[:, :, 0].astype(np.float32)
+    bad = ~np.isfinite(d).all(axis=1)
+    assert bad.any() and np.array_equal(np.isnan(yr), bad)
+
+
+def test_oracle_swiglu_keeps_nan():
+    """std::min(g, lim) and std::clamp(u, -lim, lim) (model.cpp:683-688,
+    model_batch.cpp:245-253) return a NaN argument: a gate row that is NaN
+    makes every down output NaN in the oracle's dense MLP, where fminf-style
+    clamps would give finite outputs."""
+    from edge_cases import edge_matrix
+
+    H, I = 256, 512
+    wg = edge_matrix(77, 0, I, H, nonfinite=True)
+    wu = synth.iq3xxs_matrix(77, 1, I, H)
+    wd = synth.iq3xxs_matrix(77, 2, H, I)
+    x = synth.normal(77, 3, H).reshape(1, H)
+    assert np.isnan(oracle.dense_mlp(wg, wu, wd, H, I, x, 10.0)).all()
+    # a NaN up value alone (gate finite) also passes the clamp
+    wu2 = edge_matrix(77, 4, I, H, nonfinite=True)
+    wg2 = synth.iq3xxs_matrix(77, 5, I, H)
+    assert np.isnan(oracle.dense_mlp(wg2, wu2, wd, H, I, x, 10.0)).all()
+
+
 # ------------------------------------------------------------------ routing
 
 def _brute_topk(key, k):

@@ -68,3 +68,33 @@ def test_matvec_noalloc_repeats_and_refuses_oversize(gpu):
     assert _noalloc(tbig, big_rows, 0, big_in, big_rows, xb, yb) == -1
     assert b"scratch" in G.lib().gpeed_last_error()
     torch.cuda.synchronize()
+
+
+def test_matvec_noalloc_status_reports_and_clears(gpu):
+    """A stale ticket in the fixed scratch (what overlapping calls leave) is
+    reported by gpeed_iq3xxs_matvec_noalloc_status, which then zero-fills the
+    scratch: the next call is bitwise equal to the workspace entry point.
+    The preset ticket only makes every part of tile 0 see a count past its
+    last, so no workgroup waits on it and every kernel exits normally."""
+    import torch
+
+    L = G.lib()
+    s = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    n_rows, in_dim = 6144, 12288  # tile 0's 48 records span three workgroups' chunks
+    w = synth.iq3xxs_matrix(97, 0, n_rows, in_dim)
+    t64 = G.tile(torch.from_numpy(w.reshape(-1)).to(gpu), n_rows, in_dim)
+    x = torch.from_numpy(synth.normal(97, 1, in_dim)).to(gpu)
+    assert L.gpeed_iq3xxs_matvec_noalloc_status(s) == 0, L.gpeed_last_error()
+    assert L.gpeed_iq3xxs_matvec_noalloc_poke(256, 1000) == 0, L.gpeed_last_error()  # tile 0's ticket
+    y = torch.empty(n_rows, device=gpu)
+    assert _noalloc(t64, n_rows, 0, in_dim, n_rows, x, y) == 0
+    assert L.gpeed_iq3xxs_matvec_noalloc_status(s) == -9
+    assert b"ticket" in L.gpeed_last_error() and b"cleared" in L.gpeed_last_error()
+    assert L.gpeed_iq3xxs_matvec_noalloc_status(s) == 0, L.gpeed_last_error()
+    y0 = torch.empty(n_rows, device=gpu)
+    G.matvec(t64, n_rows, 0, in_dim, n_rows, x, out=y0)
+    assert _noalloc(t64, n_rows, 0, in_dim, n_rows, x, y) == 0
+    assert L.gpeed_iq3xxs_matvec_noalloc_status(s) == 0, L.gpeed_last_error()
+    a, b = y0.cpu().numpy(), y.cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert L.gpeed_iq3xxs_matvec_noalloc_poke(3, 0) == -1  # not a word offset
