@@ -4,9 +4,10 @@
 Headline workload (value / metric): the dense-layer decode step at batch 1
 (dense_mlp, model.cpp:677-690) with IQ3_XXS weights gate/up 12288x6144
 (K=6144) and down 6144x12288 (K=12288) through gpeed_iq3xxs_dense_mlp: a
-gate+up launch (each wavefront prepares the activation blocks of its records;
-the workgroup that completes 64 rows writes SwiGLU(gate, up) as the down
-projection's prepared activation), then the down launch. Weights are synthetic (seeded, the block distribution
+gate+up launch (each wavefront prepares the activation blocks of its
+records; the workgroup that completes 64 rows writes SwiGLU(gate, up) as the
+down projection's prepared activation), then the down launch.
+Weights are synthetic (seeded, the block distribution
 of gpeed_amd.synth), x ~ N(0,1) fp32, resident in HBM before timing. To
 measure HBM rather than the 256 MB Infinity Cache, `--copies` distinct
 copies of the three tensors (default 8, 694 MB) are rotated step by step.
@@ -19,7 +20,9 @@ launch of a step): algorithmic bytes of the pair (packed W + fp32 x + the
 SwiGLU activation written and read + y) / the pair's duration, timed with
 HIP events on the launch stream around back-to-back steps of all copies in
 turn, as C-ABI calls or as replays of a HIP graph, whichever is faster (no
-host gaps either way; still HBM-bound).
+host gaps either way; still HBM-bound). roofline.down: the 6144x12288 shape
+alone (gpeed_iq3xxs_matvec on an fp32 vector, rotated copies), timed the
+same way, as its own field.
 cpu_baseline = the reference's own CPU path (oracle/_ref: WeightStore::
 matvec_quant compiled from the reference sources, single-threaded as the
 reference builds on Linux) on one full step of the same workload; the
@@ -724,10 +727,32 @@ def main():
     achieved = pair_bytes / (pair_ms * 1e-3) / 1e9
     kinds = {k: {"dispatch_event_us": round(float(v.mean()) * 1e3, 3), "algorithmic_bytes": launch_bytes[k]}
              for k, v in per_kind.items()}
-    # the down projection (6144x12288) alone: its bytes over its own
-    # dispatch-stamped launch time
     down_us = float(per_kind["down"].mean()) * 1e3
-    down_gbs = launch_bytes["down"] / (down_us * 1e-6) / 1e9
+
+    # the 6144x12288 shape alone: matvec_quant of the down weights on an
+    # fp32 vector (gpeed_iq3xxs_matvec, one launch), rotated copies
+    xdn = torch.from_numpy(synth.normal(2024, 101, I)).to(dev)
+    ws_mv = G.matvec_workspace(I, H, dev)
+    fn_mv = G.lib().gpeed_iq3xxs_matvec
+    mv_args = [(vp(c[2]), H, 0, I, H, vp(xdn), vp(y), vp(ws_mv), ws_mv.numel(), cur) for c in copies]
+    reps = max(8, args.steps // args.copies) * args.copies
+    for i in range(2 * args.copies):
+        fn_mv(*mv_args[i % args.copies])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        if fn_mv(*mv_args[i % args.copies]) != 0:
+            raise RuntimeError(G.lib().gpeed_last_error().decode(errors="replace"))
+    e1.record()
+    torch.cuda.synchronize()
+    mv_us = e0.elapsed_time(e1) / reps * 1e3
+    G.prof_start(64 + 8)
+    for i in range(64):
+        fn_mv(*mv_args[i % args.copies])
+    mv_stamped_us = float(G.prof_read(G.PROF_GEMV).astype(np.float64).mean()) * 1e3
+    mv_bytes = W_BYTES // 3 + I * 4 + H * 4
+    mv_gbs = mv_bytes / (mv_us * 1e-6) / 1e9
 
     rec = {
         "metric": METRIC,
@@ -755,8 +780,11 @@ def main():
                      "kernel": "k_gemv_t64", "avg_launch_us": round(pair_ms * 1e3 / 2, 3),
                      "pair_us": round(pair_ms * 1e3, 3), "timing": pair_timing,
                      "pair_algorithmic_bytes": pair_bytes, "launch_kinds": kinds,
-                     "down": {"shape": "6144x12288", "launch_us": round(down_us, 3),
-                              "achieved": round(down_gbs, 1), "frac": round(down_gbs / HBM_PEAK_GBS, 4)}},
+                     "down": {"shape": "6144x12288", "in_step_launch_us": round(down_us, 3),
+                              "entry": "gpeed_iq3xxs_matvec (fp32 x, one launch), rotated copies",
+                              "launch_us": round(mv_us, 3), "dispatch_event_us": round(mv_stamped_us, 3),
+                              "algorithmic_bytes": mv_bytes, "achieved": round(mv_gbs, 1),
+                              "frac": round(mv_gbs / HBM_PEAK_GBS, 4)}},
     }
     if not args.no_extra:
         del copies, base
