@@ -287,7 +287,8 @@ def moe_decode(torch, G, synth, dev, steps, warmup_s):
              "frac_of_hbm_peak": round(b_bytes / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
              "grouped_gate_up_us": round(float(d[0::2].mean()) * 1e3, 2),
              "grouped_down_us": round(float(d[1::2].mean()) * 1e3, 2)}
-    return {
+    prefill = moe_prefill(torch, G, synth, dev, tens, sh, 20)
+    return prefill, {
         "workload": "routed-expert decode batch: 64 experts x (gate/up 2048x6144 + down 6144x2048) IQ3_XXS, "
                     "32 tokens, softmax top-8, router + grouped GEMVs + combine on the GPU",
         "touched_experts": touched, "packed_bytes_per_step": moe_bytes,
@@ -301,6 +302,62 @@ def moe_decode(torch, G, synth, dev, steps, warmup_s):
                          "frac": round((gu_bytes + dn_bytes) / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "whole_step": whole,
     }
+
+
+def moe_prefill(torch, G, synth, dev, tens, sh, reps):
+    """Routed-expert prefill chunk: moe_batch over 512 tokens (64 experts,
+    top-8 softmax, shared expert), the experts as grouped MFMA GEMMs."""
+    import ctypes
+    E, T, K, HM, IM = 64, 512, 8, 6144, 2048
+    L = G.lib()
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    X = torch.from_numpy(synth.normal(2027, 10, T * HM).reshape(T, HM)).to(dev)
+    logits = torch.from_numpy(synth.normal(2027, 11, T * E).reshape(T, E)).to(dev)
+    Y = torch.empty(T, HM, device=dev)
+    eptr = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    ws = G.moe_batch_workspace(T, E, K, HM, IM, True, dev)
+    nul = ctypes.c_void_p(0)
+    args = (vp(logits), T, E, K, 1, nul, ctypes.c_float(1.0), 1, vp(tens[0]), vp(tens[1]), vp(tens[2]),
+            vp(sh[0]), vp(sh[1]), vp(sh[2]), HM, IM, vp(X), ctypes.c_float(SWIGLU_LIMIT), vp(Y), vp(eptr), nul,
+            nul, vp(ws), ws.numel(), cur)
+
+    def step():
+        if L.gpeed_iq3xxs_moe_batch(*args) != 0:
+            raise RuntimeError(f"moe prefill: {L.gpeed_last_error().decode(errors='replace')}")
+
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    counts = np.diff(eptr.cpu().numpy())
+    touched = int((counts > 0).sum())
+    blk_bytes = IM * HM // 256 * 98
+    # every touched expert's three tensors and the shared expert's, once
+    packed = (touched + 1) * 3 * blk_bytes
+    flops = 2.0 * (T * K + T) * 3 * HM * IM
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    G.prof_start(8 * reps + 8)
+    for _ in range(reps):
+        step()
+    torch.cuda.synchronize()
+    d = G.prof_read(G.PROF_GEMM).astype(np.float64) * 1e3  # per step: grouped gate/up, grouped down, shared x 2
+    names = ["grouped_gate_up_us", "grouped_down_us", "shared_gate_up_us", "shared_down_us"]
+    kern = {n: round(float(d[i::4].mean()), 2) for i, n in enumerate(names)}
+    return {"workload": "routed-expert prefill chunk: 512 tokens, 64 experts x (gate/up 2048x6144 + down "
+                        "6144x2048) IQ3_XXS, softmax top-8, shared expert of the same shape; fp32 X; the experts' "
+                        "buckets as grouped MFMA GEMMs (k_gemm5, 64-token tiles of hi + lo images)",
+            "entry": "gpeed_iq3xxs_moe_batch", "touched_experts": touched,
+            "packed_bytes_read_once": packed, "gflop_per_step": round(flops / 1e9, 2),
+            "ms_per_step": round(ms, 4), "GBps": round(packed / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(packed / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_of_fp16_peak": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4), "gemm_kernels": kern}
 
 
 def prefill_gemm(torch, G, synth, dev, reps):
@@ -789,7 +846,8 @@ def main():
     if not args.no_extra:
         del copies, base
         torch.cuda.empty_cache()
-        rec["extra"] = {"moe_decode": moe_decode(torch, G, synth, dev, max(30, args.steps // 5), 0.3)}
+        pre, dec = moe_decode(torch, G, synth, dev, max(30, args.steps // 5), 0.3)
+        rec["extra"] = {"moe_decode": dec, "moe_prefill": pre}
         torch.cuda.empty_cache()
         rec["extra"]["prefill_gemm"] = prefill_gemm(torch, G, synth, dev, 20)
         torch.cuda.empty_cache()

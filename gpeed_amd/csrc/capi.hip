@@ -895,7 +895,9 @@ size_t gpeed_iq3xxs_moe_batch_ws_bytes(int n_tok, int n_exp, int top_k, int hidd
     if (n_tok < 1 || n_tok > 8192 || n_exp < 1 || n_exp > 1024 || top_k < 1 || top_k > 32 || top_k > n_exp) return 0;
     if ((int64_t)n_tok * top_k > (1 << 24)) return 0;
     if (!dims_ok(hidden) || !dims_ok(inter)) return 0;
-    return gpeed::moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, shared ? 1 : 0);
+    const DeviceState* st = nullptr;
+    if (device_state(&st)) return 0;
+    return gpeed::moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, shared ? 1 : 0, st->num_cus);
 }
 
 int gpeed_iq3xxs_moe_batch(const float* logits, int n_tok, int n_exp, int top_k, int mode, const float* bias,
@@ -917,12 +919,12 @@ int gpeed_iq3xxs_moe_batch(const float* logits, int n_tok, int n_exp, int top_k,
         return fail(GPEED_ERR_INVALID, "moe_batch: give all three shared-expert tensors or none");
     for (const void* p : {w_gate, w_up, w_down, (const void*)X, (const void*)Y, w_gate_sh, w_up_sh, w_down_sh})
         if (p && !aligned(p, 16)) return fail(GPEED_ERR_INVALID, "moe_batch: weights, X and Y must be 16-byte aligned");
-    if (!ws || !aligned(ws, 256) ||
-        ws_bytes < gpeed::moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, sh ? 1 : 0))
-        return fail(GPEED_ERR_WORKSPACE, "moe_batch: workspace missing, misaligned or too small");
     const DeviceState* st = nullptr;
     int rc = device_state(&st);
     if (rc) return rc;
+    if (!ws || !aligned(ws, 256) ||
+        ws_bytes < gpeed::moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, sh ? 1 : 0, st->num_cus))
+        return fail(GPEED_ERR_WORKSPACE, "moe_batch: workspace missing, misaligned or too small");
     hipError_t e = gpeed::launch_moe_batch(
         logits, n_tok, n_exp, top_k, mode, bias, routed_scale, norm_topk, static_cast<const uint8_t*>(w_gate),
         static_cast<const uint8_t*>(w_up), static_cast<const uint8_t*>(w_down), static_cast<const uint8_t*>(w_gate_sh),

@@ -48,13 +48,16 @@ __device__ __forceinline__ uint32_t f16_pair_of_floats(float lo, float hi) {
 // round trip instead of twelve); CPT = 0: any length, two passes.
 // The workgroups also clear the n_cnt split-K tickets of the GEMM launch
 // that follows on the same stream, so a workspace needs no initialisation.
+// gather (may be null): image row m is X row gather[m] (bucket slots of
+// routed experts: the slot's token).
 template <int IN, int CPT>
 __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X, const float* __restrict__ U,
                                                      float lim, int M, int K, _Float16* __restrict__ xh,
                                                      float* __restrict__ unscale, uint32_t* __restrict__ cnt,
-                                                     int n_cnt) {
+                                                     int n_cnt, const int* __restrict__ gather) {
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
+    const int src = gather ? gather[m] : m;  // the X (and U) row of image row m
     for (int i = m * 256 + tid; i < n_cnt; i += M * 256) cnt[i] = 0u;
     __shared__ float red[4];
     // the 8 raw values of chunk c (16-byte loads; K is a multiple of 256)
@@ -63,13 +66,13 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
     };
     auto load8 = [&](int c, Raw& r) {
         if constexpr (IN == 1) {
-            r.a = reinterpret_cast<const u32x4_t*>(X)[((size_t)m * K >> 3) + c];
+            r.a = reinterpret_cast<const u32x4_t*>(X)[((size_t)src * K >> 3) + c];
         } else {
-            const u32x4_t* p = reinterpret_cast<const u32x4_t*>(X) + ((size_t)m * K >> 2) + 2 * c;
+            const u32x4_t* p = reinterpret_cast<const u32x4_t*>(X) + ((size_t)src * K >> 2) + 2 * c;
             r.a = p[0];
             r.b = p[1];
             if constexpr (IN == 2) {
-                const u32x4_t* q = reinterpret_cast<const u32x4_t*>(U) + ((size_t)m * K >> 2) + 2 * c;
+                const u32x4_t* q = reinterpret_cast<const u32x4_t*>(U) + ((size_t)src * K >> 2) + 2 * c;
                 r.ua = q[0];
                 r.ub = q[1];
             }
@@ -161,23 +164,23 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
 // registers where the row has at most 2048 chunks.
 template <int IN>
 hipError_t launch_prep_x(int M, int K, hipStream_t s, const void* X, const float* U, float lim, _Float16* xh,
-                         float* uns, uint32_t* cnt, int n_cnt) {
+                         float* uns, uint32_t* cnt, int n_cnt, const int* gather = nullptr) {
     const int per = (K / 8 + 255) / 256;
     const dim3 grid(M), block(256);
     if (per <= 1)
-        hipLaunchKernelGGL((k_gemm_prep_x<IN, 1>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 1>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt, gather);
     else if (per <= 2)
-        hipLaunchKernelGGL((k_gemm_prep_x<IN, 2>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 2>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt, gather);
     else if (per <= 3)
-        hipLaunchKernelGGL((k_gemm_prep_x<IN, 3>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 3>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt, gather);
     else if (per <= 4)
-        hipLaunchKernelGGL((k_gemm_prep_x<IN, 4>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 4>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt, gather);
     else if (per <= 6)
-        hipLaunchKernelGGL((k_gemm_prep_x<IN, 6>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 6>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt, gather);
     else if (per <= 8)
-        hipLaunchKernelGGL((k_gemm_prep_x<IN, 8>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 8>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt, gather);
     else
-        hipLaunchKernelGGL((k_gemm_prep_x<IN, 0>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt);
+        hipLaunchKernelGGL((k_gemm_prep_x<IN, 0>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt, gather);
     return hipGetLastError();
 }
 
@@ -200,6 +203,17 @@ struct GemmArgs {
     const uint8_t* w2;
     float* y2;
     int N2, tiles_n1;
+    // grouped (routed experts; k_gemm5 only): X rows are bucket slots,
+    // expert e's at grp_eptr[e] .. grp_eptr[e + 1] of [V][grp_rows][K]
+    // images; workgroup id / tiles_n picks entry grp_tile[.] = e << 16 | its
+    // token tile (grp_count[0] entries); the tensors' rows of expert e start
+    // grp_w_stride bytes of records after those of expert e - 1; Y rows are
+    // slots too. grp_eptr null: one GEMM over rows 0 .. M - 1.
+    const int* grp_eptr;
+    const int* grp_tile;
+    const int* grp_count;
+    int grp_rows;
+    unsigned long long grp_w_stride;
 };
 
 constexpr int kTileN = 192;  // result tile: 128 (or 64) tokens x 192 W rows
@@ -798,10 +812,36 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     const int lr = lane & 15;
     const uint32_t lg = lane >> 4;
 
-    const GemmTile tl = gemm_tile(g_all);
-    if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
+    GemmTile tl;
     int tn;
-    const GemmArgs g = gemm_tensor(g_all, tl, tn);
+    GemmArgs g;
+    // X rows [xrow0, xrow0 + g.M) of images of xplane rows each
+    int xrow0 = 0, xplane = g_all.M;
+    if (!g_all.grp_eptr) {
+        tl = gemm_tile(g_all);
+        if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
+        g = gemm_tensor(g_all, tl, tn);
+    } else {
+        // grouped: entry id / tiles_n of the expert tile table, result tile
+        // id % tiles_n of that expert's rows (one K split)
+        const int id = blockIdx.x / g_all.tiles_n;
+        tl.tn = blockIdx.x - id * g_all.tiles_n;
+        if (id >= *g_all.grp_count) return;  // uniform
+        const int ent = g_all.grp_tile[id];
+        const int e = ent >> 16;
+        tl.tm = ent & 0xFFFF;
+        tl.kz = 0;
+        tl.b0 = 0;
+        tl.b1 = g_all.nb;
+        g = gemm_tensor(g_all, tl, tn);
+        xrow0 = min(max(g_all.grp_eptr[e], 0), g_all.grp_rows);
+        xplane = g_all.grp_rows;
+        g.M = min(g_all.grp_eptr[e + 1], g_all.grp_rows) - xrow0;
+        if (g.M <= tl.tm * BM) return;  // uniform: no rows of this tile
+        g.w += (size_t)e * g_all.grp_w_stride;
+        g.y += (size_t)xrow0 * g.N;
+        g.unscale += xrow0;
+    }
     const int m0 = tl.tm * BM, n0 = tn * BN5;
     const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
 
@@ -828,7 +868,8 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     for (int i = 0; i < 4; ++i) {
         const int p = rq + 4 * i, v = p / (2 * MT);
         const int r = 8 * (p % (2 * MT)) + (int)(lane >> 3);
-        xsrc[i] = ((uint32_t)v * (uint32_t)g.M * (uint32_t)g.K + (uint32_t)min(m0 + r, g.M - 1) * (uint32_t)g.K) * 2u +
+        xsrc[i] = ((uint32_t)v * (uint32_t)xplane * (uint32_t)g.K +
+                   (uint32_t)(xrow0 + min(m0 + r, g.M - 1)) * (uint32_t)g.K) * 2u +
                   (((lane & 7u) ^ (lane >> 3)) << 4);
     }
     const uint8_t* xbase = reinterpret_cast<const uint8_t*>(g.xh);
@@ -1488,6 +1529,89 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
                        float lim) {
     return launch_gemm2(w, row0, out_dim, nullptr, 0, 0, in_dim, X, x_bf16, M, Y, nullptr, ws, err, num_cus, s, U,
                         lim);
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM over routed-expert buckets (the prefill-sized moe_batch,
+// model_batch.cpp:224-262: one matmul_quant per expert over its g tokens).
+
+namespace {
+// The expert tile table: for every expert e with tokens, one entry
+// e << 16 | mt per 64-token tile mt of its bucket eptr[e] .. eptr[e + 1];
+// count[0] = the number of entries (at most cap). One workgroup, one thread
+// per expert; bucket sizes are clamped to [0, S], so the table stays in
+// bounds whatever eptr holds.
+__global__ __launch_bounds__(1024) void k_grp_tiles(const int* __restrict__ eptr, int E, int S, int* __restrict__ tiles,
+                                                    int* __restrict__ count, int cap) {
+    __shared__ int sc[1024];
+    const int e = threadIdx.x;
+    int n = 0;
+    if (e < E) {
+        const int g = min(max(eptr[e + 1] - eptr[e], 0), S);
+        n = (g + 63) / 64;
+    }
+    sc[e] = n;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int v = e >= off ? sc[e - off] : 0;
+        __syncthreads();
+        sc[e] += v;
+        __syncthreads();
+    }
+    const int start = sc[e] - n;
+    for (int i = 0; i < n && start + i < cap; ++i) tiles[start + i] = (e << 16) | i;
+    if (e == 1023) count[0] = min(sc[1023], cap);
+}
+}  // namespace
+
+int grp_tiles_cap(int S, int E) { return S / 64 + E; }
+
+hipError_t launch_grp_tiles(const int* eptr, int E, int S, int* tiles, int* count, hipStream_t s) {
+    if (E < 1 || E > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_grp_tiles, dim3(1), dim3(1024), 0, s, eptr, E, S, tiles, count, grp_tiles_cap(S, E));
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, int in_dim, int E, const int* eptr,
+                               int S, const _Float16* xh, const float* uns, float* ya, float* yb, const int* tiles,
+                               const int* count, uint32_t* err, hipStream_t s) {
+    if (rows <= 0 || rows % kTileRows || S <= 0) return hipErrorInvalidValue;
+    // image offsets are 32-bit (two fp16 images of S rows)
+    if ((size_t)2 * S * in_dim * 2 >= (1ull << 32)) return hipErrorInvalidValue;
+    const size_t nb = (size_t)(in_dim / kQK);
+    const size_t stride = (size_t)(rows / kTileRows) * nb * kRecordBytes;
+    if (stride >= (1ull << 32)) return hipErrorInvalidValue;
+    GemmArgs a{};
+    a.nb = (int)nb;
+    a.w = wa;
+    a.xh = xh;
+    a.unscale = uns;
+    a.y = ya;
+    a.M = S;
+    a.N = rows;
+    a.K = in_dim;
+    const int tn1 = (rows + kTileN - 1) / kTileN;
+    a.tiles_n1 = tn1;
+    a.tiles_n = wb ? 2 * tn1 : tn1;
+    a.w2 = wb ? wb : wa;
+    a.y2 = wb ? yb : ya;
+    a.N2 = rows;
+    a.ks = 1;
+    a.err = err;
+    a.grp_eptr = eptr;
+    a.grp_tile = tiles;
+    a.grp_count = count;
+    a.grp_rows = S;
+    a.grp_w_stride = stride;
+    const int cap = grp_tiles_cap(S, E);
+    a.tiles_m = cap;
+    return launch_timed(kProfGemm, k_gemm5<4, 2>, dim3(cap * a.tiles_n), dim3(kThreads5), 0, s, a);
+}
+
+hipError_t launch_prep_x_rows(int M, int K, hipStream_t s, const float* X, const float* U, float lim, _Float16* xh,
+                              float* uns, const int* gather) {
+    return U ? launch_prep_x<2>(M, K, s, X, U, lim, xh, uns, nullptr, 0, gather)
+             : launch_prep_x<0>(M, K, s, X, nullptr, 0.0f, xh, uns, nullptr, 0, gather);
 }
 
 size_t gemm2_ws_bytes(int M, int out_a, int out_b, int K, int x_bf16, int num_cus) {

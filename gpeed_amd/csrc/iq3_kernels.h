@@ -140,7 +140,7 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
 // images, grouped gate/up (the shared expert's segments included, w_gate_sh
 // non-null), SwiGLU images, grouped down, combine (+ shared expert).
 // eptr/tok/wt_out: optional device outputs of the routing.
-size_t moe_batch_ws_bytes(int T, int E, int K, int H, int I, int shared);
+size_t moe_batch_ws_bytes(int T, int E, int K, int H, int I, int shared, int num_cus);
 hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, const float* bias,
                             float routed_scale, int norm_topk, const uint8_t* w_gate, const uint8_t* w_up,
                             const uint8_t* w_down, const uint8_t* w_gate_sh, const uint8_t* w_up_sh,
@@ -170,5 +170,22 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
                         unsigned long long row0b, int out_b, int in_dim, const void* X, int x_bf16, int M, float* Ya,
                         float* Yb, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s, const float* U = nullptr,
                         float lim = 0.0f);
+
+// Grouped GEMM over routed-expert buckets: for every expert e, rows
+// eptr[e] .. eptr[e + 1] of the [2][S][in_dim] fp16 images xh (fp32 X as hi
+// and lo, unscales uns[S]) times rows e * rows .. of wa (and wb, the second
+// tensor on the same X; null for one), into rows eptr[e] .. of ya / yb
+// ([S][rows]). tiles / count: the expert tile table launch_grp_tiles makes
+// from eptr (grp_tiles_cap(S, E) entries). rows a multiple of 64.
+int grp_tiles_cap(int S, int E);
+hipError_t launch_grp_tiles(const int* eptr, int E, int S, int* tiles, int* count, hipStream_t s);
+hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, int in_dim, int E, const int* eptr,
+                               int S, const _Float16* xh, const float* uns, float* ya, float* yb, const int* tiles,
+                               const int* count, uint32_t* err, hipStream_t s);
+// fp32 rows -> the GEMM's hi and lo images (unscale per row): X rows
+// gather[m] (gather null: row m), or SwiGLU(X, U) with clamp lim when U is
+// given.
+hipError_t launch_prep_x_rows(int M, int K, hipStream_t s, const float* X, const float* U, float lim, _Float16* xh,
+                              float* uns, const int* gather);
 
 }  // namespace gpeed

@@ -854,9 +854,18 @@ struct MoeLayout {
     size_t plan_off[10];
     size_t act1, g, u, act2, d, total;
     size_t eptr, tok, wt, sel, asg_e, asg_w, timg, tus;  // the whole-step path only
+    size_t xg, xg_uns, gtiles, gcount, hg, hg_uns, sh1, sh2;  // its grouped-GEMM form only
     size_t stride1, stride2;
     int seg_max;
 };
+
+// The whole step runs its experts as grouped GEMMs (each expert's weights
+// read once per 64 of its tokens) where the buckets average at least this
+// many tokens, and as grouped GEMVs over 8-token segments below (the GEMV
+// streams the weights once per segment). The same crossover as matmul_quant:
+// from 9 tokens one GEMM pass beats two GEMV passes.
+constexpr int kMoeGemmMinAvg = 9;
+bool moe_use_gemm(int T, int E, int K) { return (long long)T * K >= (long long)kMoeGemmMinAvg * E; }
 
 // T_sh: shared-expert tokens (0 or T). fused: the whole step from the
 // logits (router outputs, router scratch and per-token X images in the
@@ -890,6 +899,27 @@ MoeLayout moe_layout(int T, int E, int K, int H, int I, int T_sh = 0, bool fused
     L.u = off; off += align256(NS * I * 4);
     L.act2 = off; off += L.stride2 * L.seg_max;
     L.d = off; off += align256(NS * H * 4);
+    L.total = off;
+    return L;
+}
+
+// The grouped-GEMM form of the whole step: the layout above (its segment
+// images unused) and, after it, the slot-ordered X images, the expert tile
+// table, the SwiGLU images and the shared expert's GEMM workspaces.
+MoeLayout moe_gemm_layout(int T, int E, int K, int H, int I, int T_sh, int num_cus) {
+    MoeLayout L = moe_layout(T, E, K, H, I, T_sh, true);
+    const size_t S = (size_t)T * K;
+    size_t off = L.total;
+    L.xg = off; off += align256(2 * S * H * 2);
+    L.xg_uns = off; off += align256(S * 4);
+    L.gtiles = off; off += align256(4 * (size_t)grp_tiles_cap((int)S, E));
+    L.gcount = off; off += 256;
+    L.hg = off; off += align256(2 * S * I * 2);
+    L.hg_uns = off; off += align256(S * 4);
+    if (T_sh) {
+        L.sh1 = off; off += align256(gemm2_ws_bytes(T_sh, I, I, H, 0, num_cus));
+        L.sh2 = off; off += align256(gemm_ws_bytes(T_sh, H, I, 0, num_cus));
+    }
     L.total = off;
     return L;
 }
@@ -995,7 +1025,8 @@ hipError_t launch_moe_experts(const uint8_t* w_gate, const uint8_t* w_up, const 
     return hipGetLastError();
 }
 
-size_t moe_batch_ws_bytes(int T, int E, int K, int H, int I, int shared) {
+size_t moe_batch_ws_bytes(int T, int E, int K, int H, int I, int shared, int num_cus) {
+    if (moe_use_gemm(T, E, K)) return moe_gemm_layout(T, E, K, H, I, shared ? T : 0, num_cus).total;
     return moe_layout(T, E, K, H, I, shared ? T : 0, true).total;
 }
 
@@ -1005,7 +1036,8 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
                             const uint8_t* w_down_sh, int H, int I, const float* X, float lim, float* Y,
                             int* eptr_out, int* tok_out, float* wt_out, uint8_t* ws, int num_cus, hipStream_t s) {
     const int T_sh = w_gate_sh ? T : 0;
-    const MoeLayout L = moe_layout(T, E, K, H, I, T_sh, true);
+    const bool gemm = moe_use_gemm(T, E, K);
+    const MoeLayout L = gemm ? moe_gemm_layout(T, E, K, H, I, T_sh, num_cus) : moe_layout(T, E, K, H, I, T_sh, true);
     const MoePlan pl = plan_ptrs(ws, L);
     const int N = T * K, NS = N + T_sh;
     const int nbH = H / kQK, nbI = I / kQK;
@@ -1022,10 +1054,13 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
     // workgroups: one (token, block) item per wavefront up to 192
     const int n_rank = std::min((T + 15) / 16, 64);
     const int groups = n_rank + std::min((T * nbH + 15) / 16, 192);
+    // (the grouped-GEMM form runs the shared expert as GEMMs of its own, so
+    // its plan holds the routed segments only)
+    const int T_plan = gemm ? 0 : T_sh;
     auto front = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3(groups), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale,
                            norm_topk, eptr, tok, wt, reinterpret_cast<int*>(ws + L.sel),
-                           reinterpret_cast<int*>(ws + L.asg_e), reinterpret_cast<float*>(ws + L.asg_w), T_sh, pl, X,
+                           reinterpret_cast<int*>(ws + L.asg_e), reinterpret_cast<float*>(ws + L.asg_w), T_plan, pl, X,
                            nbH, timg, tus, n_rank);
     };
     const bool lds = (long long)T * K <= kRouteLdsAsg;
@@ -1035,6 +1070,40 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
     else lds ? front(k_moe_front<kMaxExperts / 64, true>) : front(k_moe_front<kMaxExperts / 64, false>);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (gemm) {
+        // prefill-sized batches (model_batch.cpp:224-280 at run_chunk's n,
+        // model_batch.cpp:391): X gathered into the slots' GEMM images, each
+        // expert's gate and up as grouped GEMMs over its bucket (row0 = e*I),
+        // SwiGLU images, the grouped down GEMM (row0 = e*H), the shared
+        // expert as the dense MLP's GEMMs over every token, then the combine
+        uint32_t* err = reinterpret_cast<uint32_t*>(ws);
+        _Float16* xg = reinterpret_cast<_Float16*>(ws + L.xg);
+        float* xg_uns = reinterpret_cast<float*>(ws + L.xg_uns);
+        int* gtiles = reinterpret_cast<int*>(ws + L.gtiles);
+        int* gcount = reinterpret_cast<int*>(ws + L.gcount);
+        _Float16* hg = reinterpret_cast<_Float16*>(ws + L.hg);
+        float* hg_uns = reinterpret_cast<float*>(ws + L.hg_uns);
+        e = launch_prep_x_rows(N, H, s, X, nullptr, 0.0f, xg, xg_uns, tok);
+        if (e == hipSuccess) e = launch_grp_tiles(eptr, E, N, gtiles, gcount, s);
+        if (e == hipSuccess)
+            e = launch_gemm_grouped(w_gate, w_up, I, H, E, eptr, N, xg, xg_uns, G, U, gtiles, gcount, err, s);
+        if (e == hipSuccess) e = launch_prep_x_rows(N, I, s, G, U, lim, hg, hg_uns, nullptr);
+        if (e == hipSuccess)
+            e = launch_gemm_grouped(w_down, nullptr, H, I, E, eptr, N, hg, hg_uns, D, nullptr, gtiles, gcount, err,
+                                    s);
+        if (e == hipSuccess && T_sh) {
+            float* Gs = G + (size_t)N * I;
+            float* Us = U + (size_t)N * I;
+            e = launch_gemm2(w_gate_sh, 0, I, w_up_sh, 0, I, H, X, 0, T, Gs, Us, ws + L.sh1, err, num_cus, s);
+            if (e == hipSuccess)
+                e = launch_gemm(w_down_sh, 0, I, H, Gs, 0, T, D + (size_t)N * H, ws + L.sh2, err, num_cus, s, Us, lim);
+        }
+        if (e != hipSuccess) return e;
+        const size_t n4 = (size_t)T * H / 4;
+        hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, D, wt, pl.pos, T, K,
+                           H, Y, T_sh ? D + (size_t)N * H : nullptr, pl.n_seg);
+        return hipGetLastError();
+    }
     // 2. gate / up of every segment (the shared expert's first)
     const int grid = (num_cus > 0 ? num_cus : 256) * 2;
     GroupedArgs ga{};
