@@ -691,7 +691,9 @@ __device__ __forceinline__ void grouped_tile(const uint8_t* tbl, uint32_t lb, ui
                                              const uint8_t* act, int n, int nb, int nt, float* y, int rows,
                                              int row0, const uint8_t* timg, const float* tus,
                                              const int* slot_tok, int p0) {
-    constexpr int PF = 2;
+    // records in flight: two, or one for four token pairs (a record and its
+    // activation images take 58 registers there; two of them spilled)
+    constexpr int PF = NP >= 4 ? 1 : 2;
     const int nrec = nt * nb;
     const float* xsc = reinterpret_cast<const float*>(act + (size_t)nb * n * 1024);
     // The block unscales travel with the record ring: one wait per record
