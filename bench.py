@@ -360,6 +360,36 @@ def moe_prefill(torch, G, synth, dev, tens, sh, reps):
             "frac_of_fp16_peak": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4), "gemm_kernels": kern}
 
 
+def router_product(torch, G, synth, dev, reps):
+    """moe_batch step 1 (model_batch.cpp:172): logits = X . ffn_gate_inp^T, an
+    F32 [64, 6144] tensor, for 32 and 512 tokens, through gpeed_matmul_rows
+    (dot_f32's own order: bitwise the reference's logits)."""
+    import ctypes
+    E, HM = 64, 6144
+    L = G.lib()
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    wr = torch.from_numpy((synth.normal(2028, 0, E * HM) * np.float32(0.05)).astype(np.float32)).to(dev)
+    out = {}
+    for T in (32, 512):
+        X = torch.from_numpy(synth.normal(2028, T, T * HM).reshape(T, HM)).to(dev)
+        lg = torch.empty(T, E, device=dev)
+        a = (0, vp(wr), E, 0, HM, E, vp(X), T, vp(lg), cur)
+        for _ in range(5):
+            L.gpeed_matmul_rows(*a)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            if L.gpeed_matmul_rows(*a) != 0:
+                raise RuntimeError(L.gpeed_last_error().decode(errors="replace"))
+        e1.record()
+        torch.cuda.synchronize()
+        out[f"T{T}_us"] = round(e0.elapsed_time(e1) / reps * 1e3, 2)
+    return {"workload": "router product of moe_batch: F32 ffn_gate_inp [64, 6144] times X [T, 6144] "
+                        "(k_dot_rows_f32, dot_f32's order), back-to-back launches", **out}
+
+
 def prefill_gemm(torch, G, synth, dev, reps):
     """Prefill GEMM: IQ3_XXS W 12288x6144, X bf16 [M, 6144], Y fp32 [M, 12288], M = 512 and 2048."""
     N, K = 12288, 6144
@@ -849,6 +879,7 @@ def main():
         pre, dec = moe_decode(torch, G, synth, dev, max(30, args.steps // 5), 0.3)
         rec["extra"] = {"moe_decode": dec, "moe_prefill": pre}
         torch.cuda.empty_cache()
+        rec["extra"]["router_product"] = router_product(torch, G, synth, dev, 50)
         rec["extra"]["prefill_gemm"] = prefill_gemm(torch, G, synth, dev, 20)
         torch.cuda.empty_cache()
         rec["extra"]["decode_mix"] = decode_mix(torch, G, synth, dev, 20)

@@ -361,8 +361,9 @@ int gpeed_matmul_rows(int dtype, const void* w, uint64_t n_rows, uint64_t row0, 
     if (n_tok <= 0 || out_dim <= 0) return GPEED_OK;  // weights.cpp:88
     const int be = gpeed::rows_block_elems(dtype);
     if (be == 0) return fail(GPEED_ERR_UNIMPLEMENTED, "matmul_rows: unimplemented type " + std::to_string(dtype));
-    // the kernels walk rows in 32-weight runs
-    if (in_dim <= 0 || in_dim % be || in_dim % 32)
+    // the block formats' kernels walk rows in 32-weight runs; F32 rows (in
+    // dot_f32's order) take any length, as the reference does (weights.cpp:92-94)
+    if (in_dim <= 0 || in_dim % be || (dtype != GPEED_DTYPE_F32 && in_dim % 32))
         return fail(GPEED_ERR_UNALIGNED_ROW, "matmul_rows: row not block aligned (and a multiple of 32)");
     if (in_dim > (1 << 28) || n_tok > (1 << 24)) return fail(GPEED_ERR_INVALID, "matmul_rows: size too large");
     if (!w || !X || !Y) return fail(GPEED_ERR_INVALID, "matmul_rows: null pointer");

@@ -484,10 +484,180 @@ hipError_t matmul_dt_nt(const uint8_t* w, size_t rb, int in_dim, int out_dim, co
     return hipSuccess;
 }
 
+// F32 rows (matmul_quant of an F32 tensor: the rows are copied, then
+// dot_f32, weights.cpp:86-203, simd.h:12-37) in dot_f32's own order, so the
+// products are bitwise the reference's: its two 8-lane AVX accumulators are
+// 16 independent fma chains (chain c takes the elements i = 16k + c of the
+// 16-wide steps, and chains 0..7 the one 8-wide step after them), then
+// s[l] = a0[l] + a1[l], lo[l] = s[l] + s[l + 4], (lo0 + lo1) + (lo2 + lo3),
+// and an fma per element of the tail. Here chain c is lane c of a 16-lane
+// group and the adds are lane exchanges in the same order. This is the
+// router product of moe_batch (ffn_gate_inp, model_batch.cpp:172): with its
+// logits bitwise the reference's, so are the routing integers.
+// Tiling: a workgroup takes RW = R NR rows x TW = TT NT tokens; lane c of
+// group (rs, ts) (tid >> 4 = rs + NR ts) runs chain c of the R x TT products
+// of rows rs R .. +R-1 and tokens ts TT .. +TT-1, its operands read from LDS
+// (R + TT floats per column, R TT fmas). Column chunks of CH go straight from
+// global memory into a ring of NB LDS buffers, NB - 1 chunks ahead of the
+// sums: each row's CH columns are CH / (64 V) wavefront copies
+// (global_load_lds of V dwords per lane). A buffer holds the RW rows then the
+// TW token rows, each padded by 16 / R floats, so the NR row groups of a
+// wavefront read four different bank quarters.
+template <int R, int TT, int NR, int NT, int CH, int NB, int V>
+struct DotTile {
+    static constexpr int kThreads = 16 * NR * NT, kWaves = kThreads / 64;
+    static constexpr int kRW = R * NR, kTW = TT * NT, kRows = kRW + kTW;
+    static constexpr int kStride = CH + 16 / R;
+    static constexpr int kPieces = CH / (64 * V);                  // copies per row and chunk
+    static constexpr int kPerWave = kRows * kPieces / kWaves;      // copies per wavefront and chunk
+    static constexpr size_t kLds = (size_t)NB * kRows * kStride * 4;  // bytes
+    static_assert(CH % (64 * V) == 0 && (kRows * kPieces) % kWaves == 0, "whole copies per wavefront");
+    static_assert((16 / R) % 4 == 0 || V == 1, "16-byte aligned LDS rows for 16-byte copies");
+    static_assert(NB >= 2 && (NB - 2) * kPerWave <= 63, "the copies in flight fit vmcnt");
+    static_assert(kLds <= 160 * 1024, "LDS");
+};
+
+// s_waitcnt vmcnt(N) (N < 64; expcnt and lgkmcnt not waited for)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int R, int TT, int NR, int NT, int CH, int NB, int V>
+__global__ __launch_bounds__(16 * NR * NT) void k_dot_rows_f32(const float* __restrict__ w, int in_dim, int out_dim,
+                                                               const float* __restrict__ X, int n_tok,
+                                                               float* __restrict__ Y, int ldy) {
+    using D = DotTile<R, TT, NR, NT, CH, NB, V>;
+    constexpr int RW = D::kRW, S = D::kStride;
+    __shared__ float dot_lds[NB * D::kRows * S];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = tid & 15, rs = (tid >> 4) % NR, ts = (tid >> 4) / NR;
+    const int j0 = blockIdx.x * RW, t0 = blockIdx.y * D::kTW;
+    const int cols = in_dim & ~15;  // the columns of the 16-wide steps
+    const int nchunk = (cols + CH - 1) / CH;
+
+    // copy q of a chunk: row q / kPieces of the buffer (rows past the matrix
+    // and tokens past the batch repeat the last one), columns (q % kPieces)
+    // 64 V + V lane .. + V - 1 (past the 16-wide steps: clamped; those words
+    // go unused)
+    auto copy = [&](int n) {
+        float* buf = dot_lds + (size_t)(n % NB) * D::kRows * S;
+        const int col0 = n * CH;
+#pragma unroll 8
+        for (int p = 0; p < D::kPerWave; ++p) {
+            const int q = wave + D::kWaves * p;
+            const int row = q / D::kPieces, piece = q % D::kPieces;
+            const float* base = row < RW ? w + (size_t)min(j0 + row, out_dim - 1) * in_dim
+                                         : X + (size_t)min(t0 + row - RW, n_tok - 1) * in_dim;
+            const int col = min(col0 + piece * 64 * V + V * lane, cols - V);
+            float* dst = buf + row * S + piece * 64 * V;
+            if constexpr (V == 4) __builtin_amdgcn_global_load_lds(base + col, dst, 16, 0, 0);
+            else __builtin_amdgcn_global_load_lds(base + col, dst, 4, 0, 0);
+        }
+    };
+
+    float acc[R][TT];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int u = 0; u < TT; ++u) acc[i][u] = 0.0f;
+    for (int n = 0; n < NB - 1 && n < nchunk; ++n) copy(n);
+    for (int n = 0; n < nchunk; ++n) {
+        // chunk n's copies are done when at most the later chunks' are in
+        // flight; the barrier then also says every wavefront is done with
+        // chunk n - 1, whose buffer the next copy takes
+        asm volatile("" ::: "memory");
+        if (n + NB - 2 < nchunk) wait_vmcnt<(NB - 2) * D::kPerWave>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (n + NB - 1 < nchunk) copy(n + NB - 1);
+        const float* buf = dot_lds + (size_t)(n % NB) * D::kRows * S;
+        const float* wl = buf + (rs * R) * S;
+        const float* xl = buf + (RW + ts * TT) * S;
+        const int len = min(CH, cols - n * CH);
+#pragma unroll 4
+        for (int k0 = 0; k0 < len; k0 += 16) {  // (len is a multiple of 16)
+            const int k = k0 + c;
+            float a[R], b[TT];
+#pragma unroll
+            for (int i = 0; i < R; ++i) a[i] = wl[i * S + k];
+#pragma unroll
+            for (int u = 0; u < TT; ++u) b[u] = xl[u * S + k];
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+#pragma unroll
+                for (int u = 0; u < TT; ++u) acc[i][u] = fmaf(a[i], b[u], acc[i][u]);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int j = j0 + rs * R + i;
+        const float* a = w + (size_t)min(j, out_dim - 1) * in_dim;
+#pragma unroll
+        for (int u = 0; u < TT; ++u) {
+            const int t = t0 + ts * TT + u;
+            const float* b = X + (size_t)min(t, n_tok - 1) * in_dim;
+            float v = acc[i][u];
+            int e = cols;
+            if (e + 8 <= in_dim) {  // the 8-wide step: accumulator a0 (chains 0..7)
+                if (c < 8) v = fmaf(a[e + c], b[e + c], v);
+                e += 8;
+            }
+            // s[l] = a0[l] + a1[l]; lo[l] = s[l] + s[l + 4]; h = lo[2m] + lo[2m + 1];
+            // sum = h0 + h1 (lane exchanges within the 16-lane group)
+            v = v + __shfl_xor(v, 8, 16);
+            v = v + __shfl_xor(v, 4, 16);
+            v = v + __shfl_xor(v, 1, 16);
+            v = v + __shfl_xor(v, 2, 16);
+            if (c == 0 && j < out_dim && t < n_tok) {
+                for (; e < in_dim; ++e) v = fmaf(a[e], b[e], v);
+                Y[(size_t)t * ldy + j] = v;
+            }
+        }
+    }
+}
+
+template <int R, int TT, int NR, int NT, int CH, int NB, int V>
+hipError_t launch_dot_rows_f32(const float* w, int in_dim, int out_dim, const float* X, int n_tok, float* Y,
+                               hipStream_t s) {
+    using D = DotTile<R, TT, NR, NT, CH, NB, V>;
+    const long long gy = (n_tok + D::kTW - 1) / D::kTW;
+    if (gy > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_dot_rows_f32<R, TT, NR, NT, CH, NB, V>),
+                       dim3((unsigned)((out_dim + D::kRW - 1) / D::kRW), (unsigned)gy), dim3(D::kThreads), 0, s, w,
+                       in_dim, out_dim, X, n_tok, Y, out_dim);
+    return hipGetLastError();
+}
+
+// 16-byte copies need 16-byte aligned rows (in_dim % 4 == 0) and bases; the
+// dword copies (four times as many) prefetch one chunk ahead
+template <int R, int TT, int NR, int NT, int CH, int NB>
+hipError_t launch_dot_rows_f32_any(const float* w, int in_dim, int out_dim, const float* X, int n_tok, float* Y,
+                                   hipStream_t s) {
+    if (in_dim % 4 == 0 && ((uintptr_t)w | (uintptr_t)X) % 16 == 0)
+        return launch_dot_rows_f32<R, TT, NR, NT, CH, NB, 4>(w, in_dim, out_dim, X, n_tok, Y, s);
+    return launch_dot_rows_f32<R, TT, NR, NT, CH, 2, 1>(w, in_dim, out_dim, X, n_tok, Y, s);
+}
+
 template <int DT>
 hipError_t matmul_dt(const uint8_t* w, size_t rb, unsigned long long row0, int in_dim, int out_dim, const float* X,
                      int n_tok, float* Y, hipStream_t s) {
     w += (size_t)row0 * rb;
+    if constexpr (DT == kDtF32) {
+        // 8 x 8 tiles where they make a workgroup per CU (256 CUs), else 4 x 4:
+        // each workgroup streams its rows and tokens through one CU's copies
+        // (about 25 GB/s each, measured), so the tile is as large as keeps
+        // every CU busy
+        const float* wf = reinterpret_cast<const float*>(w);
+        const long long tiles8 = (long long)((out_dim + 7) / 8) * ((n_tok + 7) / 8);
+        if (tiles8 >= 256) return launch_dot_rows_f32_any<2, 2, 4, 4, 256, 4>(wf, in_dim, out_dim, X, n_tok, Y, s);
+        return launch_dot_rows_f32_any<1, 1, 4, 4, 1024, 3>(wf, in_dim, out_dim, X, n_tok, Y, s);
+    }
     if (n_tok == 1) return matmul_dt_nt<DT, 1>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
     if (n_tok == 2) return matmul_dt_nt<DT, 2>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
     if (n_tok <= 4) return matmul_dt_nt<DT, 4>(w, rb, in_dim, out_dim, X, n_tok, Y, s);

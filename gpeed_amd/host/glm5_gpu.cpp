@@ -338,12 +338,46 @@ void WeightStore::moe_experts(const std::string& gate, const std::string& up, co
     check(gpeed_memcpy(Y, yd, xb, kD2H), "moe: download y");
 }
 
+void WeightStore::moe_batch(const std::string& router, const std::string& gate, const std::string& up,
+                            const std::string& down, const std::string& gate_sh, const std::string& up_sh,
+                            const std::string& down_sh, int n_exp, int hidden, int inter, const float* X, int n_tok,
+                            int top_k, int mode, const float* bias, float routed_scale, bool norm_topk,
+                            float swiglu_limit, float* Y) {
+    if (n_tok <= 0) return;
+    const Tensor& tr = get(router, hidden);
+    if (tr.dtype != GPEED_DTYPE_F32) throw std::runtime_error("moe: router " + router + " is not F32");
+    const size_t xb = (size_t)n_tok * hidden * sizeof(float);
+    void* xd = scratch(x_, xb, false);
+    void* lg = scratch(logits_, (size_t)n_tok * n_exp * sizeof(float), false);
+    check(gpeed_memcpy(xd, X, xb, kH2D), "moe: upload x");
+    check(gpeed_matmul_rows(tr.dtype, tr.data, tr.n_rows, 0, hidden, n_exp, static_cast<const float*>(xd), n_tok,
+                            static_cast<float*>(lg), nullptr),
+          ("moe: router product " + router).c_str());
+    moe_batch_dev(gate, up, down, gate_sh, up_sh, down_sh, n_exp, hidden, inter, n_tok, top_k, mode, bias,
+                  routed_scale, norm_topk, swiglu_limit, Y);
+}
+
 void WeightStore::moe_batch(const std::string& gate, const std::string& up, const std::string& down,
                             const std::string& gate_sh, const std::string& up_sh, const std::string& down_sh,
                             int n_exp, int hidden, int inter, const float* X, int n_tok, const float* logits,
                             int top_k, int mode, const float* bias, float routed_scale, bool norm_topk,
                             float swiglu_limit, float* Y) {
     if (n_tok <= 0) return;
+    const size_t xb = (size_t)n_tok * hidden * sizeof(float);
+    void* xd = scratch(x_, xb, false);
+    void* lg = scratch(logits_, (size_t)n_tok * n_exp * sizeof(float), false);
+    check(gpeed_memcpy(lg, logits, (size_t)n_tok * n_exp * sizeof(float), kH2D), "moe: upload logits");
+    check(gpeed_memcpy(xd, X, xb, kH2D), "moe: upload x");
+    moe_batch_dev(gate, up, down, gate_sh, up_sh, down_sh, n_exp, hidden, inter, n_tok, top_k, mode, bias,
+                  routed_scale, norm_topk, swiglu_limit, Y);
+}
+
+// The routed step from the logits and X already in the logits_ / x_
+// buffers; Y to the host.
+void WeightStore::moe_batch_dev(const std::string& gate, const std::string& up, const std::string& down,
+                                const std::string& gate_sh, const std::string& up_sh, const std::string& down_sh,
+                                int n_exp, int hidden, int inter, int n_tok, int top_k, int mode, const float* bias,
+                                float routed_scale, bool norm_topk, float swiglu_limit, float* Y) {
     const Tensor& tg = get_iq3(gate, hidden);
     const Tensor& tu = get_iq3(up, hidden);
     const Tensor& td = get_iq3(down, inter);
@@ -354,14 +388,12 @@ void WeightStore::moe_batch(const std::string& gate, const std::string& up, cons
     const size_t wsb = gpeed_iq3xxs_moe_batch_ws_bytes(n_tok, n_exp, top_k, hidden, inter, shared ? 1 : 0);
     if (wsb == 0) throw std::runtime_error("moe: unsupported shape");
     void* ws = scratch(batch_ws_, wsb, true);
-    void* lg = scratch(logits_, (size_t)n_tok * n_exp * sizeof(float), false);
+    void* lg = logits_.p;
     void* bd = bias ? scratch(bias_, (size_t)n_exp * sizeof(float), false) : nullptr;
     const size_t xb = (size_t)n_tok * hidden * sizeof(float);
-    void* xd = scratch(x_, xb, false);
+    void* xd = x_.p;
     void* yd = scratch(y_, xb, false);
-    check(gpeed_memcpy(lg, logits, (size_t)n_tok * n_exp * sizeof(float), kH2D), "moe: upload logits");
     if (bias) check(gpeed_memcpy(bd, bias, (size_t)n_exp * sizeof(float), kH2D), "moe: upload bias");
-    check(gpeed_memcpy(xd, X, xb, kH2D), "moe: upload x");
     check(gpeed_iq3xxs_moe_batch(static_cast<const float*>(lg), n_tok, n_exp, top_k, mode,
                                  static_cast<const float*>(bd), routed_scale, norm_topk ? 1 : 0, tg.data, tu.data,
                                  td.data, sg, su, sd, hidden, inter, static_cast<const float*>(xd), swiglu_limit,

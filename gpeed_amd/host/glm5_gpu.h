@@ -117,6 +117,16 @@ public:
                    const std::string& gate_sh, const std::string& up_sh, const std::string& down_sh, int n_exp,
                    int hidden, int inter, const float* X, int n_tok, const float* logits, int top_k, int mode,
                    const float* bias, float routed_scale, bool norm_topk, float swiglu_limit, float* Y);
+    // The whole of Model::moe_batch (model_batch.cpp:165-281) with step 1 on
+    // the device too: the router product matmul_quant(router) (ffn_gate_inp,
+    // model_batch.cpp:172; an F32 [n_exp, hidden] tensor of the store) of X,
+    // whose logits are bitwise the reference's (dot_f32's own order), then
+    // the routed step as the overload above. X goes up and Y comes down once.
+    void moe_batch(const std::string& router, const std::string& gate, const std::string& up,
+                   const std::string& down, const std::string& gate_sh, const std::string& up_sh,
+                   const std::string& down_sh, int n_exp, int hidden, int inter, const float* X, int n_tok,
+                   int top_k, int mode, const float* bias, float routed_scale, bool norm_topk, float swiglu_limit,
+                   float* Y);
 
 private:
     struct Tensor {
@@ -132,6 +142,10 @@ private:
     };
     const Tensor& get(const std::string& name, int in_dim);
     const Tensor& get_iq3(const std::string& name, int in_dim);
+    void moe_batch_dev(const std::string& gate, const std::string& up, const std::string& down,
+                       const std::string& gate_sh, const std::string& up_sh, const std::string& down_sh, int n_exp,
+                       int hidden, int inter, int n_tok, int top_k, int mode, const float* bias, float routed_scale,
+                       bool norm_topk, float swiglu_limit, float* Y);
     void iq3_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,
                      const float* X, int n_tok, float* Y, const char* who);
     void rows_product(const Tensor& t, const std::string& name, uint64_t row0, int in_dim, int out_dim,

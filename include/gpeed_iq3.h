@@ -156,8 +156,12 @@ size_t gpeed_dtype_row_bytes(int dtype, uint64_t n);
  * W[row0 + j][i] * X[t][i] for t < n_tok, j < out_dim, with the weights
  * dequantized bit-exactly and fp32 accumulation. X [n_tok][in_dim] fp32
  * (16-byte aligned), Y [n_tok][out_dim] fp32. in_dim must be a multiple of
- * the block size and of 32. No workspace. The IQ3_XXS entry points above
- * (T64 layout) are the fast path for IQ3_XXS; this one takes every type. */
+ * the block size and of 32, except for F32 rows, which take any length and
+ * are multiplied in dot_f32's own order (simd.h:12-37): bitwise the
+ * reference's products (the router's ffn_gate_inp, model_batch.cpp:172, so
+ * its logits and the routing they give). No workspace. The IQ3_XXS entry
+ * points above (T64 layout) are the fast path for IQ3_XXS; this one takes
+ * every type. */
 int gpeed_matmul_rows(int dtype, const void* w, uint64_t n_rows, uint64_t row0, int in_dim, int out_dim,
                       const float* X, int n_tok, float* Y, gpeed_stream_t stream);
 /* Host-only (no reference counterpart): the expanded codebook the kernels

@@ -216,6 +216,27 @@ int main(int argc, char** argv) {
             spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
             return 0;
         }
+        if (mode == "moe-router" && argc == 9) {  // the whole moe_batch from X: router product on the device too
+            const std::string dir = argv[2];
+            const int E = std::atoi(argv[3]), H = std::atoi(argv[4]), I = std::atoi(argv[5]);
+            const int T = std::atoi(argv[6]), K = std::atoi(argv[7]), md = std::atoi(argv[8]);
+            glm5::gpu::WeightStore ws;
+            ws.add("blk.0.ffn_gate_inp.weight", slurp(dir + "/router.bin").data(), (uint64_t)E, H,
+                   glm5::gpu::DType::F32);
+            ws.add("gate", slurp(dir + "/gate.bin").data(), (uint64_t)E * I, H);
+            ws.add("up", slurp(dir + "/up.bin").data(), (uint64_t)E * I, H);
+            ws.add("down", slurp(dir + "/down.bin").data(), (uint64_t)E * H, I);
+            ws.add("gate_sh", slurp(dir + "/gate_sh.bin").data(), (uint64_t)I, H);
+            ws.add("up_sh", slurp(dir + "/up_sh.bin").data(), (uint64_t)I, H);
+            ws.add("down_sh", slurp(dir + "/down_sh.bin").data(), (uint64_t)H, I);
+            const std::vector<char> x = slurp(dir + "/x.bin");
+            std::vector<float> Y((size_t)T * H);
+            ws.moe_batch("blk.0.ffn_gate_inp.weight", "gate", "up", "down", "gate_sh", "up_sh", "down_sh", E, H, I,
+                         reinterpret_cast<const float*>(x.data()), T, K, md, nullptr, md == 0 ? 2.5f : 1.0f, true,
+                         10.0f, Y.data());
+            spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
+            return 0;
+        }
         if (mode == "dequant" && argc == 6) {  // host-array dequantize (quant.h:18-22)
             const int dtype = std::atoi(argv[2]);
             const uint64_t n = std::strtoull(argv[4], nullptr, 10);

@@ -93,3 +93,28 @@ def test_moe_batch_whole_step(gpu, tmp_path, shared):
     ref = oracle.moe_batch(logits, X, wg, wu, wd, H, I, K, mode, None, 2.5, True, 10.0,
                            shared=(sg, su, sd) if shared else None)
     assert max(rel_err(Y[t], ref[t]) for t in range(T)) < TIGHT
+
+
+@pytest.mark.parametrize("T", [12, 96])
+def test_moe_batch_with_router_product(gpu, tmp_path, T):
+    """WeightStore::moe_batch from X with the router product on the device
+    (model_batch.cpp:172, ffn_gate_inp F32 [E, H]): its logits are bitwise
+    the reference's dot_f32, so the routing equals the oracle's from the
+    oracle's logits; 12 tokens run the grouped GEMVs, 96 the grouped GEMMs."""
+    E, H, I, K, mode = 16, 1024, 512, 4, 0
+    wr = (synth.normal(87, 9, E * H) * np.float32(0.05)).astype(np.float32).reshape(E, H)
+    wg = synth.iq3xxs_matrix(87, 0, E * I, H)
+    wu = synth.iq3xxs_matrix(87, 1, E * I, H)
+    wd = synth.iq3xxs_matrix(87, 2, E * H, I)
+    sg = synth.iq3xxs_matrix(87, 5, I, H)
+    su = synth.iq3xxs_matrix(87, 6, I, H)
+    sd = synth.iq3xxs_matrix(87, 7, H, I)
+    X = synth.normal(87, 3, T * H).reshape(T, H)
+    for name, a in (("router", wr), ("gate", wg), ("up", wu), ("down", wd), ("gate_sh", sg), ("up_sh", su),
+                    ("down_sh", sd), ("x", X)):
+        a.tofile(tmp_path / f"{name}.bin")
+    run("moe-router", tmp_path, E, H, I, T, K, mode)
+    Y = np.fromfile(tmp_path / "Y.bin", np.float32).reshape(T, H)
+    logits = oracle.matmul_rows(0, wr.view(np.uint8).reshape(E, -1), 0, H, E, X)
+    ref = oracle.moe_batch(logits, X, wg, wu, wd, H, I, K, mode, None, 2.5, True, 10.0, shared=(sg, su, sd))
+    assert max(rel_err(Y[t], ref[t]) for t in range(T)) < TIGHT

@@ -151,3 +151,21 @@ def test_host_dequantize_reference_signature(gpu, tmp_path):
     r = subprocess.run([exe, "dequant", "2", str(tmp_path / "raw.bin"), "32", str(tmp_path / "out.bin")],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode != 0 and "dequantize: unimplemented type Q4_0" in (r.stdout + r.stderr)
+
+
+@pytest.mark.parametrize("in_dim", [6144, 1000, 24, 7])
+@pytest.mark.parametrize("n_tok", [1, 5, 300])
+def test_f32_rows_bitwise_reference_order(gpu, in_dim, n_tok):
+    """F32 rows (matmul_quant of an F32 tensor: the router ffn_gate_inp,
+    model_batch.cpp:172) are multiplied in dot_f32's own order (simd.h:
+    12-37: 16 fma chains, their add tree, the fma tail), so the products are
+    bitwise the oracle's, which is bitwise the reference's build; lengths
+    with and without the 8-wide step and the tail (7 columns: the dword
+    copies of rows that are not a multiple of 4 long), 4 x 4 tiles (1 and 5 tokens)
+    and 8 x 8 tiles (300 tokens x 60 rows: 304 tiles)."""
+    rows = 64
+    w = (synth.normal(88, in_dim, rows * in_dim) * np.float32(0.05)).astype(np.float32).reshape(rows, in_dim)
+    X = synth.normal(88, 1, n_tok * in_dim).reshape(n_tok, in_dim)
+    Y = G.matmul_rows(0, dev(w.reshape(-1).view(np.uint8), gpu), rows, 3, in_dim, 60, dev(X, gpu)).cpu().numpy()
+    ref = oracle.matmul_rows(0, w.view(np.uint8), 3, in_dim, 60, X)
+    assert np.array_equal(Y.reshape(ref.shape).view(np.uint32), ref.view(np.uint32))
