@@ -35,9 +35,11 @@ the prefill GEMM (W 12288x6144, X bf16 [M,6144], M = 512 and 2048:
 TFLOP/s = 2*M*N*K / kernel time from dispatch-stamped events, against the
 2.5 PFLOP/s dense bf16/fp16 MFMA peak), and the continuous-batching decode
 mix (64 tokens through the latent projections and the shared-expert FFN:
-GB/s over the packed weights and TFLOP/s, both fractions), and the MLA
+GB/s over the packed weights and TFLOP/s, both fractions), the MLA
 per-head projections attn_k_b / attn_v_b (64 heads each, one launch per
-tensor, against 64 matvec launches).
+tensor, against 64 matvec launches), the router product of moe_batch (F32
+64x6144 in dot_f32's order, 32 and 512 tokens), and the other GGUF formats
+over raw rows (one token: GB/s; a 512-token chunk: fp32-MFMA TFLOP/s).
 """
 from __future__ import annotations
 
@@ -61,6 +63,7 @@ os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
 
 METRIC = "IQ3_XXS GEMV weight GB/s (% of HBM peak) at batch 1; prefill GEMM TFLOP/s"
 HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 H, I = 6144, 12288
 SWIGLU_LIMIT = 10.0
 # HBM traffic of the GEMV pair, measured with rocprofv3 --pmc (FETCH_SIZE and
@@ -472,7 +475,11 @@ def other_formats(torch, G, synth, dev, reps, min_bytes=600e6):
     format, rotated copies (at least `min_bytes` in all) so the reads come from HBM. Time per
     launch from events around `reps` back-to-back launches."""
     K = N = 6144
-    out = {"workload": "matvec over 6144x6144 GGUF rows, one token, fp32 x, per format"}
+    out = {"workload": "matvec over 6144x6144 GGUF rows, one token, fp32 x, per format; prefill512: the "
+                       "same weight times X [512, 6144] (k_gemm_rows: exact decode to fp32 tiles, fp32 MFMA)",
+           "prefill_peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS}
+    X512 = torch.from_numpy(synth.normal(2031, 1, 512 * K).reshape(512, K)).to(dev)
+    Y512 = torch.empty(512, N, device=dev)
     names = {8: "Q8_0", 10: "Q2_K", 11: "Q3_K", 14: "Q6_K", 21: "IQ3_S", 22: "IQ2_S", 23: "IQ4_XS", 1: "F16",
              30: "BF16", 18: "IQ3_XXS (raw rows)"}
     x = torch.from_numpy(synth.normal(2031, 0, K)).to(dev)
@@ -493,8 +500,19 @@ def other_formats(torch, G, synth, dev, reps, min_bytes=600e6):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
         gbs = nbytes / (us * 1e-6) / 1e9
+        G.matmul_rows(dt, w, N, 0, K, N, X512, out=Y512)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            G.matmul_rows(dt, w, N, 0, K, N, X512, out=Y512)
+        e1.record()
+        torch.cuda.synchronize()
+        pus = e0.elapsed_time(e1) * 1e3 / reps
+        tf = 2.0 * 512 * N * K / (pus * 1e-6) / 1e12
         out[name] = {"us": round(us, 2), "packed_bytes": nbytes, "GBs": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "prefill512": {"us": round(pus, 1), "TFLOPs": round(tf, 1),
+                                    "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}}
         del ws, w
         torch.cuda.empty_cache()
     return out

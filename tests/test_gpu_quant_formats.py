@@ -72,8 +72,11 @@ def test_rows_product_golden(gpu, dt):
 
 
 @pytest.mark.parametrize("dt", ALL_TYPES)
-@pytest.mark.parametrize("n_tok", [1, 2, 3, 8, 13])
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 8, 13, 16, 70])
 def test_rows_product_vs_oracle(gpu, dt, n_tok):
+    """Below 16 tokens the 8-token-slice kernel, from 16 the fp32-MFMA GEMM
+    (F32: dot_f32's order at every size); 150 rows and 70 tokens leave
+    partial 64-row and 64-token tiles."""
     in_dim, rows, row0, out_dim = 2048, 200, 37, 150
     w = synth.quant_matrix(43, dt, dt, rows, in_dim)
     X = synth.normal(43, 100 + n_tok, n_tok * in_dim).reshape(n_tok, in_dim)
@@ -93,6 +96,17 @@ def test_rows_product_model_width(gpu, dt):
         X = synth.normal(44, n_tok, n_tok * in_dim).reshape(n_tok, in_dim)
         Y = G.matmul_rows(dt, wd, rows, 0, in_dim, rows, dev(X, gpu))
         assert rel_err(Y.cpu().numpy(), oracle.matmul_rows(dt, w, 0, in_dim, rows, X)) < TIGHT
+
+
+@pytest.mark.parametrize("dt", [8, 14, 22, 30])
+def test_rows_product_prefill_chunk(gpu, dt):
+    """A 512-token prefill chunk (model_batch.cpp:30-95 call matmul_quant with
+    n = the chunk) through the fp32-MFMA GEMM over a 6144-wide slice."""
+    in_dim, rows, row0, out_dim = 6144, 200, 5, 190
+    w = synth.quant_matrix(45, dt, dt, rows, in_dim)
+    X = synth.normal(45, 512, 512 * in_dim).reshape(512, in_dim)
+    Y = G.matmul_rows(dt, dev(w.reshape(-1), gpu), rows, row0, in_dim, out_dim, dev(X, gpu))
+    assert rel_err(Y.cpu().numpy(), oracle.matmul_rows(dt, w, row0, in_dim, out_dim, X)) < TIGHT
 
 
 def test_rows_product_errors(gpu):
