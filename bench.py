@@ -393,40 +393,48 @@ def router_product(torch, G, synth, dev, reps):
                         "(k_dot_rows_f32, dot_f32's order), back-to-back launches", **out}
 
 
-def prefill_gemm(torch, G, synth, dev, reps):
-    """Prefill GEMM: IQ3_XXS W 12288x6144, X bf16 [M, 6144], Y fp32 [M, 12288], M = 512 and 2048."""
+def prefill_gemm(torch, G, synth, dev, reps, copies=12):
+    """Prefill GEMM: IQ3_XXS W 12288x6144, X bf16 [M, 6144], Y fp32 [M, 12288], M = 512 and 2048.
+    `copies` rotated weight copies (28.9 MB each, 347 MB in all: above the 256 MB Infinity Cache),
+    so each call reads its W from HBM as a prefill over a model's layers does. kernel_us comes
+    from dispatch-stamped launches in a loop of their own; stamp_overhead_us is that loop's time
+    per call less the unstamped loop's."""
     N, K = 12288, 6144
     w = synth.iq3xxs_matrix(2026, 0, N, K)
     t64 = G.tile(torch.from_numpy(w.reshape(-1)).to(dev), N, K)
+    ts = [t64] + [t64.clone() for _ in range(copies - 1)]
     out = {"workload": "prefill GEMM: IQ3_XXS W 12288x6144 (record units staged through LDS, decoded to exact "
                        "fp16 q*(2s+1) MFMA operands, d/4 per block in fp32), X bf16 [M,6144] ~ N(0,1), "
-                       "Y fp32 [M,12288]",
+                       f"Y fp32 [M,12288]; {copies} rotated weight copies",
            "peak_TFLOPs": 2500.0}
+
+    def loop(M, X, Y, ws, n):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for r in range(n):
+            G.gemm(ts[r % copies], N, 0, K, N, X, out=Y, ws=ws)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
     for M in (512, 2048):
         X = torch.from_numpy(synth.normal(2026, M, M * K).reshape(M, K)).to(dev).to(torch.bfloat16)
         Y = torch.empty(M, N, device=dev)
         ws = torch.zeros(G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, K, N, G.X_BF16), dtype=torch.uint8, device=dev)
-        for _ in range(3):
-            G.gemm(t64, N, 0, K, N, X, out=Y, ws=ws)
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(reps):
-            G.gemm(t64, N, 0, K, N, X, out=Y, ws=ws)
-        b.record()
-        torch.cuda.synchronize()
-        call_ms = a.elapsed_time(b) / reps
-        G.prof_start(reps + 8)  # kernel durations, dispatch-stamped, in a loop of their own
-        for _ in range(reps):
-            G.gemm(t64, N, 0, K, N, X, out=Y, ws=ws)
-        torch.cuda.synchronize()
+        n = max(reps, 2 * copies)
+        loop(M, X, Y, ws, copies)
+        call_ms = loop(M, X, Y, ws, n)
+        G.prof_start(n + 8)  # kernel durations, dispatch-stamped, in a loop of their own
+        stamped_ms = loop(M, X, Y, ws, n)
         k_ms = float(G.prof_read(G.PROF_GEMM).astype(np.float64).mean())
         fl = 2.0 * M * N * K
         out[f"M{M}"] = {"kernel_us": round(k_ms * 1e3, 2), "call_us": round(call_ms * 1e3, 2),
+                        "stamp_overhead_us": round((stamped_ms - call_ms) * 1e3, 2),
                         "TFLOPs_kernel": round(fl / (k_ms * 1e-3) / 1e12, 1),
                         "TFLOPs_call": round(fl / (call_ms * 1e-3) / 1e12, 1),
                         "frac_of_bf16_peak": round(fl / (k_ms * 1e-3) / 1e12 / 2500.0, 4)}
+    del ts
     return out
 
 
@@ -518,13 +526,76 @@ def other_formats(torch, G, synth, dev, reps, min_bytes=600e6):
     return out
 
 
-def decode_mix(torch, G, synth, dev, reps, copies=4):
+def moe_probe(torch, G, synth, dev, steps):
+    """The routed-expert decode step of the bench (gpeed_iq3xxs_moe_batch: 32 tokens, 64 experts,
+    softmax top-8, a shared expert over every token; five launches), `steps` times after three
+    warm-up steps, for counter runs. The experts (925 MB) exceed the Infinity Cache, so every
+    step streams them from HBM."""
+    import ctypes
+    E, T, K, HM, IM = 64, 32, 8, 6144, 2048
+    log("moe probe: generating 64 experts and a shared expert")
+    tens = []
+    for i, (r, c) in enumerate(((E * IM, HM), (E * IM, HM), (E * HM, IM))):
+        raw = torch.from_numpy(synth.iq3xxs_matrix(2025, i, r, c).reshape(-1)).to(dev)
+        tens.append(G.tile(raw, r, c))
+        del raw
+    sh = []
+    for i, (r, c) in enumerate(((IM, HM), (IM, HM), (HM, IM))):
+        raw = torch.from_numpy(synth.iq3xxs_matrix(2025, 20 + i, r, c).reshape(-1)).to(dev)
+        sh.append(G.tile(raw, r, c))
+        del raw
+    X = torch.from_numpy(synth.normal(2025, 10, T * HM).reshape(T, HM)).to(dev)
+    logits = torch.from_numpy(synth.normal(2025, 11, T * E).reshape(T, E)).to(dev)
+    Y = torch.empty(T, HM, device=dev)
+    L = G.lib()
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    nul = ctypes.c_void_p(0)
+    ws_b = G.moe_batch_workspace(T, E, K, HM, IM, True, dev)
+    args = (vp(logits), T, E, K, 1, nul, ctypes.c_float(1.0), 1, vp(tens[0]), vp(tens[1]), vp(tens[2]),
+            vp(sh[0]), vp(sh[1]), vp(sh[2]), HM, IM, vp(X), ctypes.c_float(SWIGLU_LIMIT), vp(Y), nul, nul,
+            nul, vp(ws_b), ws_b.numel(), cur)
+    for _ in range(3 + steps):
+        if L.gpeed_iq3xxs_moe_batch(*args) != 0:
+            raise RuntimeError(f"moe: {L.gpeed_last_error().decode(errors='replace')}")
+    torch.cuda.synchronize()
+    counts = np.diff(G.moe_route(logits, K, 1)[0].cpu().numpy())
+    log(f"moe probe done: {int((counts > 0).sum())} experts touched")
+
+
+def rows_probe(torch, G, synth, dev, reps, min_bytes=600e6):
+    """One-token products over raw GGUF rows (k_matmul_rows) of a Q8_0 and a Q6_K 6144x6144
+    weight, `reps` launches each over rotated copies (at least `min_bytes`, so the reads come from
+    HBM), then five 512-token products (k_gemm_rows) of each, for counter runs."""
+    K = N = 6144
+    x = torch.from_numpy(synth.normal(2031, 0, K)).to(dev)
+    X512 = torch.from_numpy(synth.normal(2031, 1, 512 * K).reshape(512, K)).to(dev)
+    y = torch.empty(N, device=dev)
+    Y512 = torch.empty(512, N, device=dev)
+    for dt in (8, 14):
+        w = torch.from_numpy(synth.quant_matrix(2031, dt, dt, N, K).reshape(-1)).to(dev)
+        copies = max(2, int(min_bytes // w.numel()) + 1)
+        ws = [w] + [w.clone() for _ in range(copies - 1)]
+        for r in range(reps):
+            G.matmul_rows(dt, ws[r % copies], N, 0, K, N, x, out=y)
+        for _ in range(5):
+            G.matmul_rows(dt, w, N, 0, K, N, X512, out=Y512)
+        torch.cuda.synchronize()
+        del ws, w
+        torch.cuda.empty_cache()
+    log("rows probe done")
+
+
+def decode_mix(torch, G, synth, dev, reps, copies=4, probe_steps=0):
     """Continuous-batching decode mix: 64 tokens (fp32 X [64, 6144]) through the MLA latent projections
-    kv_a 576x6144 and q_a 1536x6144 and the shared-expert FFN (gate, up 12288x6144; down 6144x12288 with
-    SwiGLU formed in its GEMM), all IQ3_XXS GEMMs. `copies` rotated weight sets keep it out of the
-    Infinity Cache."""
-    M, HM = 64, 6144
-    shapes = [("kv_a", 576, HM), ("q_a", 1536, HM), ("gate", 12288, HM), ("up", 12288, HM), ("down", HM, 12288)]
+    kv_a 576x6144 and q_a 1536x6144 and the shared-expert FFN (gate, up 12288x6144; down 6144x12288),
+    all IQ3_XXS GEMMs, as one gpeed_iq3xxs_mlp_gemm call: X images, the gate+up two-tensor GEMM, the
+    SwiGLU images, and one launch holding down and kv_a + q_a (K splits balanced over the CUs).
+    `copies` rotated weight sets keep it out of the Infinity Cache. The same products as three
+    calls (gemm2 kv_a+q_a, gemm2 gate+up, gemm_swiglu down) are timed beside it. With probe_steps,
+    runs that many steps (after three warm-up steps) and returns None (for counter runs)."""
+    M, HM, IM = 64, 6144, 12288
+    shapes = [("kv_a", 576, HM), ("q_a", 1536, HM), ("gate", IM, HM), ("up", IM, HM), ("down", HM, IM)]
     log("decode mix: generating weights")
     sets = []
     for c in range(copies):
@@ -536,41 +607,50 @@ def decode_mix(torch, G, synth, dev, reps, copies=4):
             sets.append({n: t.clone() for n, t in sets[0].items()})
     X = torch.from_numpy(synth.normal(2027, 10, M * HM).reshape(M, HM)).to(dev)
     out = {n: torch.empty(M, r, device=dev) for n, r, _ in shapes}
-    # kv_a + q_a and gate + up share X: one two-tensor GEMM each (X prepared
-    # once, both tensors' result tiles in one grid), then the down GEMM
-    ws = {"lat": G.lib().gpeed_iq3xxs_gemm2_ws_bytes(M, HM, 576, 1536, G.X_F32),
-          "ffn": G.lib().gpeed_iq3xxs_gemm2_ws_bytes(M, HM, 12288, 12288, G.X_F32),
-          "down": G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, 12288, HM, G.X_F32)}
-    ws = {n: torch.zeros(b, dtype=torch.uint8, device=dev) for n, b in ws.items()}
+    ws_m = G.mlp_gemm_workspace(M, HM, IM, G.X_F32, [576, 1536], dev)
 
     def step(c):
         W = sets[c % copies]
-        G.gemm2(W["kv_a"], 576, 0, 576, W["q_a"], 1536, 0, 1536, HM, X, out_a_t=out["kv_a"], out_b_t=out["q_a"],
-                ws=ws["lat"])
-        G.gemm2(W["gate"], 12288, 0, 12288, W["up"], 12288, 0, 12288, HM, X, out_a_t=out["gate"],
-                out_b_t=out["up"], ws=ws["ffn"])
-        G.gemm_swiglu(W["down"], HM, 0, 12288, HM, out["gate"], out["up"], SWIGLU_LIMIT, out=out["down"],
-                      ws=ws["down"])
+        G.mlp_gemm(W["gate"], W["up"], W["down"], HM, IM, X, SWIGLU_LIMIT,
+                   extra=((W["kv_a"], 576), (W["q_a"], 1536)), out=out["down"],
+                   extra_out=[out["kv_a"], out["q_a"]], ws=ws_m)
 
     # timed through the C ABI with prebuilt arguments (see the dense step)
     import ctypes
     L = G.lib()
     cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     vp = lambda t: ctypes.c_void_p(t.data_ptr())
-    calls = []
-    for c in range(copies):
-        W = sets[c]
-        cl = []
-        for (a, ra), (b, rb), w_name in ((("kv_a", 576), ("q_a", 1536), "lat"), (("gate", 12288), ("up", 12288), "ffn")):
-            cl.append((L.gpeed_iq3xxs_gemm2, (vp(W[a]), ra, 0, ra, vp(W[b]), rb, 0, rb, HM, vp(X), G.X_F32, M,
-                                              vp(out[a]), vp(out[b]), vp(ws[w_name]), ws[w_name].numel(), cur)))
-        cl.append((L.gpeed_iq3xxs_gemm_swiglu, (vp(W["down"]), HM, 0, 12288, HM, vp(out["gate"]), vp(out["up"]),
-                                                ctypes.c_float(SWIGLU_LIMIT), M, vp(out["down"]), vp(ws["down"]),
-                                                ws["down"].numel(), cur)))
-        calls.append(cl)
+    eo = (ctypes.c_int * 2)(576, 1536)
+    ey = (ctypes.c_void_p * 2)(out["kv_a"].data_ptr(), out["q_a"].data_ptr())
+    ew = [(ctypes.c_void_p * 2)(sets[c]["kv_a"].data_ptr(), sets[c]["q_a"].data_ptr()) for c in range(copies)]
+    args = [(vp(sets[c]["gate"]), vp(sets[c]["up"]), vp(sets[c]["down"]), HM, IM, vp(X), G.X_F32, M,
+             ctypes.c_float(SWIGLU_LIMIT), vp(out["down"]), 2, ew[c], eo, ey, vp(ws_m), ws_m.numel(), cur)
+            for c in range(copies)]
 
     def step_fast(c):
-        for f, a in calls[c % copies]:
+        if L.gpeed_iq3xxs_mlp_gemm(*args[c % copies]) != 0:
+            raise RuntimeError(f"decode mix: {L.gpeed_last_error().decode(errors='replace')}")
+
+    # the same products as three calls
+    ws3 = {"lat": G.lib().gpeed_iq3xxs_gemm2_ws_bytes(M, HM, 576, 1536, G.X_F32),
+           "ffn": G.lib().gpeed_iq3xxs_gemm2_ws_bytes(M, HM, IM, IM, G.X_F32),
+           "down": G.lib().gpeed_iq3xxs_gemm_ws_bytes(M, IM, HM, G.X_F32)}
+    ws3 = {n: torch.zeros(b, dtype=torch.uint8, device=dev) for n, b in ws3.items()}
+    g_u = (torch.empty(M, IM, device=dev), torch.empty(M, IM, device=dev))
+    calls3 = []
+    for c in range(copies):
+        W = sets[c]
+        calls3.append([
+            (L.gpeed_iq3xxs_gemm2, (vp(W["kv_a"]), 576, 0, 576, vp(W["q_a"]), 1536, 0, 1536, HM, vp(X), G.X_F32, M,
+                                    vp(out["kv_a"]), vp(out["q_a"]), vp(ws3["lat"]), ws3["lat"].numel(), cur)),
+            (L.gpeed_iq3xxs_gemm2, (vp(W["gate"]), IM, 0, IM, vp(W["up"]), IM, 0, IM, HM, vp(X), G.X_F32, M,
+                                    vp(g_u[0]), vp(g_u[1]), vp(ws3["ffn"]), ws3["ffn"].numel(), cur)),
+            (L.gpeed_iq3xxs_gemm_swiglu, (vp(W["down"]), HM, 0, IM, HM, vp(g_u[0]), vp(g_u[1]),
+                                          ctypes.c_float(SWIGLU_LIMIT), M, vp(out["down"]), vp(ws3["down"]),
+                                          ws3["down"].numel(), cur))])
+
+    def step_three(c):
+        for f, a in calls3[c % copies]:
             if f(*a) != 0:
                 raise RuntimeError(f"decode mix: {L.gpeed_last_error().decode(errors='replace')}")
 
@@ -578,29 +658,43 @@ def decode_mix(torch, G, synth, dev, reps, copies=4):
         step(c)
         step_fast(c)
     torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
-    for c in range(reps):
-        step_fast(c)
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
-    # GEMM kernel durations from dispatch-stamped launches, in a loop of their
-    # own (the stamps add to the step)
-    G.prof_start(3 * reps + 8)
-    for c in range(reps):
-        step_fast(c)
-    torch.cuda.synchronize()
-    k_ms = float(G.prof_read(G.PROF_GEMM).astype(np.float64).sum()) / reps
+    if probe_steps:
+        for c in range(probe_steps):
+            step_fast(c)
+        torch.cuda.synchronize()
+        return None
+
+    def timed(f):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        for c in range(copies):
+            f(c)
+        a.record()
+        for c in range(reps):
+            f(c)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    ms = timed(step_fast)
+    ms_three = timed(step_three)
+    # GEMM kernel durations (gate+up, down + kv_a/q_a) from dispatch-stamped
+    # launches, in a loop of their own (the stamps add to the step)
+    G.prof_start(2 * (reps + copies) + 8)
+    stamped_ms = timed(step_fast)
+    d = G.prof_read(G.PROF_GEMM).astype(np.float64)[-2 * reps:]
+    gu_ms, dl_ms = float(np.median(d[0::2])), float(np.median(d[1::2]))
     w_bytes = sum(r * k // 256 * 98 for _, r, k in shapes)
     flops = sum(2.0 * M * r * k for _, r, k in shapes)
     return {"workload": "continuous-batching decode mix: 64 tokens, fp32 X [64,6144], IQ3_XXS kv_a 576x6144, "
-                        "q_a 1536x6144, shared expert gate/up 12288x6144 and down 6144x12288 (SwiGLU in the "
-                        "down GEMM); kv_a+q_a and gate+up as two-tensor GEMMs on the shared X, K split over "
-                        "workgroups",
+                        "q_a 1536x6144, shared expert gate/up 12288x6144 and down 6144x12288, one "
+                        "gpeed_iq3xxs_mlp_gemm call: X images, gate+up GEMM (K split 2), SwiGLU images, one "
+                        "launch of down (6 K splits of 8 blocks) and kv_a+q_a (3 of 8), 225 workgroups",
             "packed_bytes_per_step": w_bytes, "gflop_per_step": round(flops / 1e9, 2),
-            "ms_per_step": round(ms, 4), "kernel_ms_per_step": round(k_ms, 4),
+            "ms_per_step": round(ms, 4),
+            "gemm_kernel_us": {"gate_up": round(gu_ms * 1e3, 2), "down_kv_a_q_a": round(dl_ms * 1e3, 2)},
+            "stamp_overhead_us_per_step": round((stamped_ms - ms) * 1e3, 2),
+            "three_calls_ms_per_step": round(ms_three, 4),
             "GBps": round(w_bytes / (ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(w_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
@@ -626,6 +720,10 @@ def main():
                          "decode step 20 times, and exit; meant to run under rocprofv3 --pmc")
     ap.add_argument("--gemm-m", type=int, default=512,
                     help="tokens of the --gemm-probe GEMM (512 runs k_gemm5, 2048 k_gemm6)")
+    ap.add_argument("--probe", choices=("moe", "mix", "rows"),
+                    help="run 5 elementwise copies of 256 MiB (counter calibration), then 20 steps of the "
+                         "routed-expert decode step (moe), the decode mix (mix) or the raw-row products "
+                         "(rows), and exit; meant to run under rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the multi-GPU "
@@ -727,6 +825,23 @@ def main():
             step(i % args.copies)
         torch.cuda.synchronize()
         log("gemm probe done")
+        return
+
+    if args.probe:
+        src = torch.ones(64 << 20, device=dev)  # 256 MiB fp32
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.add(src, 0.0, out=dst)  # reads 256 MiB, writes 256 MiB
+        torch.cuda.synchronize()
+        del src, dst, copies, base
+        torch.cuda.empty_cache()
+        if args.probe == "moe":
+            moe_probe(torch, G, synth, dev, 20)
+        elif args.probe == "mix":
+            decode_mix(torch, G, synth, dev, 20, probe_steps=20)
+        else:
+            rows_probe(torch, G, synth, dev, 20)
+        log(f"{args.probe} probe done")
         return
 
     if args.traffic_probe:

@@ -103,6 +103,9 @@ def lib():
             "gpeed_iq3xxs_gemm2_ws_bytes": ([i64, i64, i64, i64, i32], sz),
             "gpeed_iq3xxs_gemm2": ([vp, u64, u64, i32, vp, u64, u64, i32, i32, vp, i32, i32, vp, vp, vp, sz, vp],
                                    i32),
+            "gpeed_iq3xxs_mlp_gemm_ws_bytes": ([i64, i64, i64, i32, i32, vp], sz),
+            "gpeed_iq3xxs_mlp_gemm": ([vp, vp, vp, i32, i32, vp, i32, i32, C.c_float, vp, i32, vp, vp, vp, vp, sz,
+                                       vp], i32),
             "gpeed_stream_read": ([vp, sz, vp, sz, vp], i32),
             "gpeed_prof_start": ([i32], i32),
             "gpeed_prof_read": ([i32, vp, i32, vp], i32),
@@ -399,6 +402,46 @@ def gemm_swiglu(w_t64, n_rows: int, row0: int, in_dim: int, out_dim: int, G, U, 
     _check(lib().gpeed_iq3xxs_gemm_swiglu(_ptr(w_t64), n_rows, row0, in_dim, out_dim, _ptr(G), _ptr(U), limit, n_tok,
                                           _ptr(out), _ptr(ws), ws.numel(), _stream(stream)), "gemm_swiglu")
     return out
+
+
+def mlp_gemm_workspace(n_tok: int, hidden: int, inter: int, x_dtype: int = None, extra_out=(), device="cuda"):
+    """Workspace of mlp_gemm (zeroed: its header holds the error word)."""
+    xd = X_F32 if x_dtype is None else x_dtype
+    eo = (C.c_int * max(1, len(extra_out)))(*extra_out)
+    n = lib().gpeed_iq3xxs_mlp_gemm_ws_bytes(n_tok, hidden, inter, xd, len(extra_out), eo)
+    if n == 0:
+        raise ValueError("mlp_gemm: unsupported sizes")
+    return _zeros(n, device)
+
+
+def mlp_gemm(w_gate, w_up, w_down, hidden: int, inter: int, X, limit: float = 10.0, extra=(), out=None,
+             extra_out=None, ws=None, stream=None):
+    """dense_mlp_batch as GEMMs: Y [n_tok, hidden] = down(SwiGLU(gate X, up X)) for whole T64 tensors,
+    plus the products of up to two more whole T64 tensors of the same X, extra = ((w, out_dim), ...),
+    computed in the down launch. Returns (Y, [Y_extra ...])."""
+    torch = _torch()
+    _require_cuda(w_gate, w_up, w_down, X)
+    n_tok = X.shape[0]
+    xd = X_BF16 if X.dtype == torch.bfloat16 else X_F32
+    if xd == X_F32 and X.dtype != torch.float32:
+        raise ValueError("mlp_gemm: X must be float32 or bfloat16")
+    if len(extra) > 2:
+        raise ValueError("mlp_gemm: at most two extra tensors")
+    if out is None:
+        out = torch.empty(n_tok, hidden, dtype=torch.float32, device=X.device)
+    if extra_out is None:
+        extra_out = [torch.empty(n_tok, r, dtype=torch.float32, device=X.device) for _, r in extra]
+    dims = [r for _, r in extra]
+    if ws is None:
+        ws = mlp_gemm_workspace(n_tok, hidden, inter, xd, dims, X.device)
+    k = max(1, len(extra))
+    ew = (C.c_void_p * k)(*[_ptr(w) for w, _ in extra])
+    eo = (C.c_int * k)(*dims)
+    ey = (C.c_void_p * k)(*[_ptr(y) for y in extra_out])
+    _check(lib().gpeed_iq3xxs_mlp_gemm(_ptr(w_gate), _ptr(w_up), _ptr(w_down), hidden, inter, _ptr(X), xd, n_tok,
+                                       limit, _ptr(out), len(extra), ew, eo, ey, _ptr(ws), ws.numel(),
+                                       _stream(stream)), "mlp_gemm")
+    return out, extra_out
 
 
 def act_buffer(in_dim: int, n_tok: int = 1, device="cuda"):

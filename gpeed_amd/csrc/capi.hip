@@ -1037,6 +1037,63 @@ int gpeed_iq3xxs_gemm_swiglu(const void* w_t64, uint64_t n_rows, uint64_t row0, 
     return e == hipSuccess ? GPEED_OK : hip_fail(e, "gemm_swiglu launch");
 }
 
+size_t gpeed_iq3xxs_mlp_gemm_ws_bytes(int64_t n_tok, int64_t hidden, int64_t inter, int x_dtype, int n_extra,
+                                      const int* extra_out) {
+    if (n_tok < 1 || n_tok > (1 << 20) || !dims_ok(hidden) || !dims_ok(inter) || hidden > (1 << 24) ||
+        inter > (1 << 24) || (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16) || n_extra < 0 || n_extra > 2 ||
+        (n_extra > 0 && !extra_out))
+        return 0;
+    const int e1 = n_extra > 0 ? extra_out[0] : 0, e2 = n_extra > 1 ? extra_out[1] : 0;
+    if (e1 < 0 || e2 < 0 || e1 > (1 << 24) || e2 > (1 << 24)) return 0;
+    const DeviceState* st = nullptr;
+    if (device_state(&st)) return 0;
+    return gpeed::kWsHeader + gpeed::mlp_gemm_ws_bytes((int)hidden, (int)inter, (int)n_tok,
+                                                       x_dtype == GPEED_X_BF16, e1, e2, st->num_cus);
+}
+
+int gpeed_iq3xxs_mlp_gemm(const void* w_gate, const void* w_up, const void* w_down, int hidden, int inter,
+                          const void* X, int x_dtype, int n_tok, float swiglu_limit, float* Y, int n_extra,
+                          const void* const* extra_w, const int* extra_out, float* const* extra_Y, void* ws,
+                          size_t ws_bytes, gpeed_stream_t stream) {
+    if (n_tok <= 0) return GPEED_OK;  // weights.cpp:88
+    int rc = check_mv_args(w_gate, (uint64_t)inter, 0, hidden, inter, X, Y, "mlp_gemm");
+    if (!rc) rc = check_mv_args(w_up, (uint64_t)inter, 0, hidden, inter, X, Y, "mlp_gemm");
+    if (!rc) rc = check_mv_args(w_down, (uint64_t)hidden, 0, inter, hidden, X, Y, "mlp_gemm");
+    if (rc) return rc;
+    if (x_dtype != GPEED_X_F32 && x_dtype != GPEED_X_BF16) return fail(GPEED_ERR_INVALID, "mlp_gemm: x_dtype");
+    if (n_tok > (1 << 20)) return fail(GPEED_ERR_INVALID, "mlp_gemm: n_tok too large");
+    if (n_extra < 0 || n_extra > 2 || (n_extra > 0 && (!extra_w || !extra_out || !extra_Y)))
+        return fail(GPEED_ERR_INVALID, "mlp_gemm: extra tensors (0 to 2, with their outputs)");
+    const void* ew[2] = {nullptr, nullptr};
+    int eo[2] = {0, 0};
+    float* ey[2] = {nullptr, nullptr};
+    for (int i = 0; i < n_extra; ++i) {
+        if (extra_out[i] <= 0) continue;  // nothing to compute
+        rc = check_mv_args(extra_w[i], (uint64_t)extra_out[i], 0, hidden, extra_out[i], X, extra_Y[i], "mlp_gemm");
+        if (rc) return rc;
+        if (!aligned(extra_w[i], 16)) return fail(GPEED_ERR_INVALID, "mlp_gemm: misaligned operand");
+        ew[i] = extra_w[i];
+        eo[i] = extra_out[i];
+        ey[i] = extra_Y[i];
+    }
+    if (!aligned(w_gate, 16) || !aligned(w_up, 16) || !aligned(w_down, 16) || !aligned(X, 16))
+        return fail(GPEED_ERR_INVALID, "mlp_gemm: misaligned operand");
+    const DeviceState* st = nullptr;
+    rc = device_state(&st);
+    if (rc) return rc;
+    if (!ws || !aligned(ws, 256) ||
+        ws_bytes < gpeed::kWsHeader + gpeed::mlp_gemm_ws_bytes(hidden, inter, n_tok, x_dtype == GPEED_X_BF16,
+                                                                eo[0], eo[1], st->num_cus))
+        return fail(GPEED_ERR_WORKSPACE, "mlp_gemm: workspace missing, misaligned or too small");
+    hipError_t e = gpeed::launch_mlp_gemm(
+        static_cast<const uint8_t*>(w_gate), static_cast<const uint8_t*>(w_up), static_cast<const uint8_t*>(w_down),
+        hidden, inter, X, x_dtype == GPEED_X_BF16, n_tok, swiglu_limit, Y, static_cast<const uint8_t*>(ew[0]), eo[0],
+        ey[0], static_cast<const uint8_t*>(ew[1]), eo[1], ey[1], static_cast<uint8_t*>(ws) + gpeed::kWsHeader,
+        static_cast<uint32_t*>(ws), st->num_cus, static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue) return fail(GPEED_ERR_INVALID, "mlp_gemm: tensor of 4 GiB or more");
+    return e == hipSuccess ? GPEED_OK : hip_fail(e, "mlp_gemm launch");
+}
+
 int gpeed_iq3xxs_matvec_raw(const void* w_gguf, uint64_t n_rows, uint64_t row0, int in_dim,
                             int out_dim, const float* x, float* dst, gpeed_stream_t stream) {
     if (out_dim <= 0) return GPEED_OK;

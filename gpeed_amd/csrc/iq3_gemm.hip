@@ -17,6 +17,7 @@
 // tiles use it). k_gemm5 (bf16 X of more than 64 tokens, and fp32 X) and
 // k_gemm3 (bf16 X of at most 64 tokens) differ in how the wavefronts split
 // the tile and how W and X reach them; see each kernel.
+#include <algorithm>
 #include <type_traits>
 
 #include "iq3_common.h"
@@ -187,6 +188,24 @@ hipError_t launch_prep_x(int M, int K, hipStream_t s, const void* X, const float
 // ---------------------------------------------------------------------------
 // GEMM
 
+// A launch's second problem (k_gemm5, non-grouped; the same M): workgroups
+// wg0 .. grid - 1 compute it, from its own images (xh, unscale, K, nb), split
+// count, tickets and partials, one or two tensors like the first. wg0 0:
+// no second problem.
+struct GemmProb {
+    const uint8_t* w;
+    const _Float16* xh;
+    const float* unscale;
+    float* y;
+    int N, K, nb, tiles_n, ks;
+    uint32_t* cnt;
+    float* part;
+    const uint8_t* w2;
+    float* y2;
+    int N2, tiles_n1;
+    int wg0;
+};
+
 struct GemmArgs {
     const uint8_t* w;       // T64 records of the first requested tile
     const _Float16* xh;     // [V][M][K] fp16 images
@@ -214,6 +233,7 @@ struct GemmArgs {
     const int* grp_count;
     int grp_rows;
     unsigned long long grp_w_stride;
+    GemmProb p2;
 };
 
 constexpr int kTileN = 192;  // result tile: 128 (or 64) tokens x 192 W rows
@@ -225,10 +245,10 @@ constexpr int kTileN = 192;  // result tile: 128 (or 64) tokens x 192 W rows
 struct GemmTile {
     int tm, tn, kz, b0, b1;
 };
-__device__ __forceinline__ GemmTile gemm_tile(const GemmArgs& g) {
+__device__ __forceinline__ GemmTile gemm_tile(const GemmArgs& g, int bid) {
     GemmTile t;
-    t.kz = blockIdx.x % g.ks;
-    const int id = blockIdx.x / g.ks;
+    t.kz = bid % g.ks;
+    const int id = bid / g.ks;
     if (g.ks == 1 && g.tiles_n % 8 == 0) {
         const int per_band = g.tiles_n / 8;
         const int xcd = id & 7, local = id >> 3;
@@ -484,7 +504,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
     const int lr = lane & 15;
     const uint32_t lg = lane >> 4;
 
-    const GemmTile tl = gemm_tile(g_all);
+    const GemmTile tl = gemm_tile(g_all, blockIdx.x);
     if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
     int tn;
     const GemmArgs g = gemm_tensor(g_all, tl, tn);
@@ -818,9 +838,30 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     // X rows [xrow0, xrow0 + g.M) of images of xplane rows each
     int xrow0 = 0, xplane = g_all.M;
     if (!g_all.grp_eptr) {
-        tl = gemm_tile(g_all);
-        if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
-        g = gemm_tensor(g_all, tl, tn);
+        GemmArgs ga = g_all;
+        int bid = blockIdx.x;
+        if (g_all.p2.wg0 > 0 && bid >= g_all.p2.wg0) {  // uniform: the second problem
+            const GemmProb& q = g_all.p2;
+            ga.w = q.w;
+            ga.xh = q.xh;
+            ga.unscale = q.unscale;
+            ga.y = q.y;
+            ga.N = q.N;
+            ga.K = q.K;
+            ga.nb = q.nb;
+            ga.tiles_n = q.tiles_n;
+            ga.ks = q.ks;
+            ga.cnt = q.cnt;
+            ga.part = q.part;
+            ga.w2 = q.w2;
+            ga.y2 = q.y2;
+            ga.N2 = q.N2;
+            ga.tiles_n1 = q.tiles_n1;
+            bid -= q.wg0;
+        }
+        tl = gemm_tile(ga, bid);
+        if (tl.tm >= ga.tiles_m || tl.tn >= ga.tiles_n) return;  // uniform
+        g = gemm_tensor(ga, tl, tn);
     } else {
         // grouped: entry id / tiles_n of the expert tile table, result tile
         // id % tiles_n of that expert's rows (one K split)
@@ -1162,7 +1203,7 @@ __global__ __launch_bounds__(kThreads6) void k_gemm6(GemmArgs g_all) {
     const int l32 = lane & 31;
     const uint32_t hk = lane >> 5;  // which 8 of a K step's 16 elements
 
-    const GemmTile tl = gemm_tile(g_all);
+    const GemmTile tl = gemm_tile(g_all, blockIdx.x);
     if (tl.tm >= g_all.tiles_m || tl.tn >= g_all.tiles_n) return;  // uniform
     int tn;
     const GemmArgs g = gemm_tensor(g_all, tl, tn);
@@ -1529,6 +1570,151 @@ hipError_t launch_gemm(const uint8_t* w, unsigned long long row0, int in_dim, in
                        float lim) {
     return launch_gemm2(w, row0, out_dim, nullptr, 0, 0, in_dim, X, x_bf16, M, Y, nullptr, ws, err, num_cus, s, U,
                         lim);
+}
+
+// ---------------------------------------------------------------------------
+// Batched dense MLP as GEMMs (model_batch.cpp:62-72: matmul_quant of gate and
+// up over the same X, SwiGLU, matmul_quant of down): the gate+up two-tensor
+// GEMM, the SwiGLU images of its rows, and the down GEMM, with up to two
+// more tensors of the same X (extra) computed in the down launch. At up to
+// 64 tokens of fp32 X that launch holds two problems, down on the SwiGLU
+// images and the extra tensors on the X images the gate+up GEMM made, with
+// K splits chosen so that every workgroup streams the same number of blocks
+// and the grid fits the CUs (64 tokens, 6144 x 12288 down with kv_a 576 and
+// q_a 1536 over 6144: down in 6 splits of 8 blocks, the extra tensors in 3
+// of 8, 225 workgroups). Elsewhere the extra tensors are a two-tensor GEMM
+// launch of their own.
+
+namespace {
+struct MlpGemmPlan {
+    bool merged;
+    int ks_gu, ks_d, ks_e, tiles_m, tiles_d, tiles_e1, tiles_e2;
+    size_t yg, yu, a, b_img, b_uns, b_cnt, b_part, total;  // region offsets after the header
+};
+
+MlpGemmPlan mlp_gemm_plan(int H, int I, int M, int x_bf16, int out_e1, int out_e2, int num_cus) {
+    const auto a256 = [](size_t b) { return (b + 255) / 256 * 256; };
+    const auto tiles = [](int n) { return n > 0 ? (n + kTileN - 1) / kTileN : 0; };
+    const int cus = num_cus > 0 ? num_cus : 256;
+    MlpGemmPlan p{};
+    p.tiles_m = (M + gemm_tile_m(M, x_bf16) - 1) / gemm_tile_m(M, x_bf16);
+    p.tiles_d = tiles(H);
+    p.tiles_e1 = tiles(out_e1);
+    p.tiles_e2 = tiles(out_e2);
+    const int tiles_e = p.tiles_e1 + p.tiles_e2;
+    const int nb_h = H / kQK, nb_i = I / kQK;
+    p.ks_gu = gemm_splits(M, 2 * tiles(I) * kTileN, H, num_cus, x_bf16);
+    p.yg = 0;
+    p.yu = a256((size_t)M * I * 4);
+    p.a = p.yu + a256((size_t)M * I * 4);
+    // the smallest even number of blocks per split (at most 8 splits per
+    // tile) whose workgroups fit the CUs
+    if (tiles_e > 0 && !x_bf16 && M <= 64 && gemm_halves(M, 0, I) && gemm_halves(M, 0, H)) {
+        for (int blk = 2; blk <= nb_i || blk <= nb_h; blk += 2) {
+            const int kd = (nb_i + blk - 1) / blk, ke = (nb_h + blk - 1) / blk;
+            if (kd > 8 || ke > 8) continue;
+            if ((long long)p.tiles_m * (p.tiles_d * kd + tiles_e * ke) <= cus) {
+                p.merged = true;
+                p.ks_d = kd;
+                p.ks_e = ke;
+                break;
+            }
+        }
+    }
+    if (p.merged) {
+        const GemmWs la = gemm_ws(M, 2 * tiles(I) * kTileN, H, 0, p.ks_gu);
+        p.b_img = p.a + a256(la.total);
+        p.b_uns = p.b_img + a256((size_t)2 * M * I * 2);
+        p.b_cnt = p.b_uns + a256((size_t)M * 4);
+        p.b_part = p.b_cnt + a256((size_t)p.tiles_m * (p.tiles_d + tiles_e) * 4);
+        p.total = p.b_part + (size_t)p.tiles_m * (p.tiles_d * p.ks_d + tiles_e * p.ks_e) * 64 * kTileN * 4;
+    } else {
+        // gate+up, down and the extra tensors one after another through
+        // one scratch region
+        size_t sc = gemm2_ws_bytes(M, I, I, H, x_bf16, num_cus);
+        sc = std::max(sc, gemm_ws_bytes(M, H, I, 0, num_cus));
+        if (tiles_e > 0) sc = std::max(sc, gemm2_ws_bytes(M, std::max(out_e1, 1), out_e2, H, x_bf16, num_cus));
+        p.total = p.a + sc;
+    }
+    return p;
+}
+}  // namespace
+
+size_t mlp_gemm_ws_bytes(int H, int I, int M, int x_bf16, int out_e1, int out_e2, int num_cus) {
+    return mlp_gemm_plan(H, I, M, x_bf16, out_e1, out_e2, num_cus).total;
+}
+
+hipError_t launch_mlp_gemm(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int H, int I,
+                           const void* X, int x_bf16, int M, float lim, float* Y, const uint8_t* w_e1, int out_e1,
+                           float* y_e1, const uint8_t* w_e2, int out_e2, float* y_e2, uint8_t* ws, uint32_t* err,
+                           int num_cus, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    if (!w_e1) out_e1 = 0;
+    if (!w_e2) out_e2 = 0;
+    if (out_e1 <= 0 && out_e2 > 0) {  // the extra tensor in the first place
+        w_e1 = w_e2, out_e1 = out_e2, y_e1 = y_e2;
+        w_e2 = nullptr, out_e2 = 0;
+    }
+    const MlpGemmPlan p = mlp_gemm_plan(H, I, M, x_bf16, out_e1, out_e2, num_cus);
+    float* yg = reinterpret_cast<float*>(ws + p.yg);
+    float* yu = reinterpret_cast<float*>(ws + p.yu);
+    uint8_t* wa = ws + p.a;
+    hipError_t e = launch_gemm2(w_gate, 0, I, w_up, 0, I, H, X, x_bf16, M, yg, yu, wa, err, num_cus, s);
+    if (e != hipSuccess) return e;
+    if (!p.merged) {
+        e = launch_gemm(w_down, 0, I, H, yg, 0, M, Y, wa, err, num_cus, s, yu, lim);
+        if (e != hipSuccess || out_e1 <= 0) return e;
+        return launch_gemm2(w_e1, 0, out_e1, w_e2, 0, out_e2, H, X, x_bf16, M, y_e1, y_e2, wa, err, num_cus, s);
+    }
+    // the gate+up GEMM's X images (its workspace layout), and the SwiGLU
+    // images of its rows (tickets of both problems cleared on the way)
+    const GemmWs la = gemm_ws(M, 2 * ((I + kTileN - 1) / kTileN) * kTileN, H, 0, p.ks_gu);
+    _Float16* xa = reinterpret_cast<_Float16*>(wa + la.img);
+    float* ua = reinterpret_cast<float*>(wa + la.uns);
+    _Float16* xb = reinterpret_cast<_Float16*>(ws + p.b_img);
+    float* ub = reinterpret_cast<float*>(ws + p.b_uns);
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(ws + p.b_cnt);
+    float* part = reinterpret_cast<float*>(ws + p.b_part);
+    const int tiles_e = p.tiles_e1 + p.tiles_e2;
+    e = launch_prep_x<2>(M, I, s, yg, yu, lim, xb, ub, cnt, p.tiles_m * (p.tiles_d + tiles_e));
+    if (e != hipSuccess) return e;
+    GemmArgs a{};
+    a.w = w_down;
+    a.xh = xb;
+    a.unscale = ub;
+    a.y = Y;
+    a.M = M;
+    a.N = H;
+    a.K = I;
+    a.nb = I / kQK;
+    a.tiles_m = p.tiles_m;
+    a.tiles_n = a.tiles_n1 = p.tiles_d;
+    a.w2 = w_down;
+    a.y2 = Y;
+    a.N2 = H;
+    a.ks = p.ks_d;
+    a.cnt = cnt;
+    a.part = part;
+    a.err = err;
+    GemmProb& q = a.p2;
+    q.w = w_e1;
+    q.xh = xa;
+    q.unscale = ua;
+    q.y = y_e1;
+    q.N = out_e1;
+    q.K = H;
+    q.nb = H / kQK;
+    q.tiles_n = tiles_e;
+    q.tiles_n1 = p.tiles_e1;
+    q.w2 = out_e2 > 0 ? w_e2 : w_e1;
+    q.y2 = out_e2 > 0 ? y_e2 : y_e1;
+    q.N2 = out_e2 > 0 ? out_e2 : out_e1;
+    q.ks = p.ks_e;
+    q.cnt = cnt + p.tiles_m * p.tiles_d;
+    q.part = part + (size_t)p.tiles_m * p.tiles_d * p.ks_d * 64 * kTileN;
+    q.wg0 = p.tiles_m * p.tiles_d * p.ks_d;
+    const int grid = q.wg0 + p.tiles_m * tiles_e * p.ks_e;
+    return launch_timed(kProfGemm, k_gemm5<4, 2>, dim3(grid), dim3(kThreads5), 0, s, a);
 }
 
 // ---------------------------------------------------------------------------

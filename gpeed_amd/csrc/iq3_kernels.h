@@ -171,6 +171,17 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
                         float* Yb, uint8_t* ws, uint32_t* err, int num_cus, hipStream_t s, const float* U = nullptr,
                         float lim = 0.0f);
 
+// Batched dense MLP as GEMMs over M tokens: Y [M][H] = down(SwiGLU(gate X,
+// up X)) for whole T64 tensors gate/up [I][H] and down [H][I], plus up to two
+// more whole T64 tensors of the same X (w_e1 [out_e1][H] -> y_e1, w_e2 ->
+// y_e2; null for none) computed in the down launch where that balances;
+// ws: mlp_gemm_ws_bytes bytes.
+size_t mlp_gemm_ws_bytes(int H, int I, int M, int x_bf16, int out_e1, int out_e2, int num_cus);
+hipError_t launch_mlp_gemm(const uint8_t* w_gate, const uint8_t* w_up, const uint8_t* w_down, int H, int I,
+                           const void* X, int x_bf16, int M, float lim, float* Y, const uint8_t* w_e1, int out_e1,
+                           float* y_e1, const uint8_t* w_e2, int out_e2, float* y_e2, uint8_t* ws, uint32_t* err,
+                           int num_cus, hipStream_t s);
+
 // Grouped GEMM over routed-expert buckets: for every expert e, rows
 // eptr[e] .. eptr[e + 1] of the [2][S][in_dim] fp16 images xh (fp32 X as hi
 // and lo, unscales uns[S]) times rows e * rows .. of wa (and wb, the second

@@ -284,6 +284,26 @@ size_t gpeed_iq3xxs_gemm2_ws_bytes(int64_t n_tok, int64_t in_dim, int64_t out_a,
 int gpeed_iq3xxs_gemm2(const void* w_a, uint64_t n_rows_a, uint64_t row0_a, int out_a, const void* w_b,
                        uint64_t n_rows_b, uint64_t row0_b, int out_b, int in_dim, const void* X, int x_dtype,
                        int n_tok, float* Y_a, float* Y_b, void* ws, size_t ws_bytes, gpeed_stream_t stream);
+/* dense_mlp_batch (model_batch.cpp:145-163) over n_tok tokens as GEMMs:
+ * Y [n_tok][hidden] = down(SwiGLU(gate X, up X)) with the SwiGLU clamp of
+ * gpeed_iq3xxs_gemm_swiglu, for whole T64 tensors gate/up [inter][hidden] and
+ * down [hidden][inter]. Up to n_extra = 2 more whole T64 tensors of the same
+ * X (extra_w[i], extra_out[i] rows of hidden; extra_Y[i] [n_tok][extra_out[i]];
+ * e.g. the latent projections kv_a, q_a of model_batch.cpp:62, 72, which the
+ * reference runs as matmul_quant calls of their own) are computed in the
+ * down launch: at up to 64 tokens of fp32 X it holds both problems, with K
+ * splits that give every workgroup the same number of blocks, so those
+ * products fill the CUs the down product leaves idle (elsewhere they are a
+ * launch of their own). Four launches in all: X images, gate+up, SwiGLU
+ * images, down (+ extra). Each output is as the GEMM entry points above give
+ * it. ws: gpeed_iq3xxs_mlp_gemm_ws_bytes bytes (same rules as the GEMM's);
+ * the gate/up rows are kept in it. */
+size_t gpeed_iq3xxs_mlp_gemm_ws_bytes(int64_t n_tok, int64_t hidden, int64_t inter, int x_dtype, int n_extra,
+                                      const int* extra_out);
+int gpeed_iq3xxs_mlp_gemm(const void* w_gate, const void* w_up, const void* w_down, int hidden, int inter,
+                          const void* X, int x_dtype, int n_tok, float swiglu_limit, float* Y, int n_extra,
+                          const void* const* extra_w, const int* extra_out, float* const* extra_Y, void* ws,
+                          size_t ws_bytes, gpeed_stream_t stream);
 
 /* The two halves of the products, for callers that reuse one activation
  * across several tensors (gate and up of model.cpp:681-682) or fuse the

@@ -195,3 +195,64 @@ def test_gemm_errors(gpu):
     with pytest.raises(G.GpeedError) as e:
         G.gemm(t64, 128, 0, 500, 64, X)
     assert e.value.code == -3
+
+
+@pytest.mark.parametrize("M,H,I,extra,x_bf16", [
+    (64, 2048, 4096, (576, 1536), False),   # the down launch holds two problems (balanced K splits)
+    (37, 2048, 4096, (192,), False),        # partial token tile, one extra tensor
+    (1, 1024, 2048, (), False),             # no extra tensor: gate+up, SwiGLU images, down
+    (100, 1024, 2048, (320, 64), False),    # over 64 tokens: the extra tensors as a launch of their own
+    (40, 1024, 2048, (576,), True),         # bf16 X: likewise
+])
+def test_mlp_gemm(gpu, M, H, I, extra, x_bf16):
+    """dense_mlp_batch as GEMMs (gpeed_iq3xxs_mlp_gemm, model_batch.cpp:145-163)
+    with up to two extra tensors of the same X computed in the down launch:
+    every output against the oracle (dense_mlp, matmul_quant), and a second
+    call on the same workspace gives the same bits."""
+    import torch
+
+    wg = synth.iq3xxs_matrix(97, 0, I, H)
+    wu = synth.iq3xxs_matrix(97, 1, I, H)
+    wd = synth.iq3xxs_matrix(97, 2, H, I)
+    we = [synth.iq3xxs_matrix(97, 3 + i, r, H) for i, r in enumerate(extra)]
+    X = synth.normal(97, M, M * H).reshape(M, H)
+    if x_bf16:
+        X = bf16_round(X)
+    t = lambda a, r, c: G.tile(dev(a.reshape(-1), gpu), r, c)  # noqa: E731
+    tg, tu, td = t(wg, I, H), t(wu, I, H), t(wd, H, I)
+    te = [(t(w, r, H), r) for w, r in zip(we, extra)]
+    Xd = as_bf16_tensor(X, gpu) if x_bf16 else dev(X, gpu)
+    ws = G.mlp_gemm_workspace(M, H, I, G.X_BF16 if x_bf16 else G.X_F32, list(extra), gpu)
+    Y, Ye = G.mlp_gemm(tg, tu, td, H, I, Xd, 10.0, extra=te, ws=ws)
+    Y, Ye = Y.cpu().numpy(), [y.cpu().numpy() for y in Ye]
+    ref = oracle.dense_mlp(wg, wu, wd, H, I, X, 10.0)
+    assert max(rel_err(Y[i], ref[i]) for i in range(M)) < TIGHT
+    for y, w, r in zip(Ye, we, extra):
+        ref_e = oracle.matmul(w, 0, H, r, X)
+        assert max(rel_err(y[i], ref_e[i]) for i in range(M)) < TIGHT, r
+    Y2, Ye2 = G.mlp_gemm(tg, tu, td, H, I, Xd, 10.0, extra=te, ws=ws)
+    assert np.array_equal(Y, Y2.cpu().numpy())
+    assert all(np.array_equal(a, b.cpu().numpy()) for a, b in zip(Ye, Ye2))
+
+
+def test_mlp_gemm_decode_mix_full_size(gpu):
+    """The decode-mix shapes: 64 fp32 tokens through gate/up 12288x6144 and
+    down 6144x12288 with kv_a 576x6144 and q_a 1536x6144 in the down launch;
+    the five outputs against the oracle on 8 of the tokens."""
+    H, I, M = 6144, 12288, 64
+    wg = synth.iq3xxs_matrix(98, 0, I, H)
+    wu = synth.iq3xxs_matrix(98, 1, I, H)
+    wd = synth.iq3xxs_matrix(98, 2, H, I)
+    wk = synth.iq3xxs_matrix(98, 3, 576, H)
+    wq = synth.iq3xxs_matrix(98, 4, 1536, H)
+    X = synth.normal(98, 5, M * H).reshape(M, H)
+    t = lambda a, r, c: G.tile(dev(a.reshape(-1), gpu), r, c)  # noqa: E731
+    Y, (Yk, Yq) = G.mlp_gemm(t(wg, I, H), t(wu, I, H), t(wd, H, I), H, I, dev(X, gpu), 10.0,
+                             extra=((t(wk, 576, H), 576), (t(wq, 1536, H), 1536)))
+    sel = np.arange(0, M, 8)
+    ref = oracle.dense_mlp(wg, wu, wd, H, I, X[sel], 10.0)
+    Y, Yk, Yq = Y.cpu().numpy()[sel], Yk.cpu().numpy()[sel], Yq.cpu().numpy()[sel]
+    assert max(rel_err(Y[i], ref[i]) for i in range(len(sel))) < TIGHT
+    for y, w, r in ((Yk, wk, 576), (Yq, wq, 1536)):
+        ref_e = oracle.matmul(w, 0, H, r, X[sel])
+        assert max(rel_err(y[i], ref_e[i]) for i in range(len(sel))) < TIGHT, r
