@@ -393,30 +393,40 @@ __global__ __launch_bounds__(256) void k_matmul_rows(const uint8_t* base, int ba
                         xs[4 * k] = v.x; xs[4 * k + 1] = v.y; xs[4 * k + 2] = v.z; xs[4 * k + 3] = v.w;
                     }
                 }
-#pragma unroll
-                for (int r = 0; r < RW; ++r) {
-                    // the row's chunk starts (its byte address) mod 16 bytes into its
-                    // staged copy; row_bytes is even, so blocks stay 2-byte aligned
+                // the rows' chunks start (their byte addresses) mod 16 bytes into
+                // their staged copies; row_bytes is even, so blocks stay 2-byte
+                // aligned
+                auto decode_row = [&](int r, float (&y)[32]) {
                     const uint32_t o = (lead_c + (uint32_t)(j0 + r) * row_bytes) & 15u;
-                    const uint8_t* blk = &stage[wave][r][o + (uint32_t)((s - sb) / kSub) * kBB];
-                    float y[32];
-                    decode32<DT>(blk, s % kSub, tb, y);
-                    if constexpr (NT == 1) {
+                    decode32<DT>(&stage[wave][r][o + (uint32_t)((s - sb) / kSub) * kBB], s % kSub, tb, y);
+                };
+                if constexpr (NT == 1) {
+#pragma unroll
+                    for (int r = 0; r < RW; ++r) {
+                        float y[32];
+                        decode_row(r, y);
 #pragma unroll
                         for (int e = 0; e < 32; ++e) acc[r][0] = fmaf(y[e], xs[e], acc[r][0]);
-                    } else {
+                    }
+                } else {
+                    // every row decoded first, then each token's 32 activations
+                    // loaded once for all of them
+                    float y[RW][32];
 #pragma unroll
-                        for (int t = 0; t < NT; ++t) {
-                            if (t < nt) {
-                                const float4* xv =
-                                    reinterpret_cast<const float4*>(X + (size_t)(t0 + t) * in_dim + 32 * s);
+                    for (int r = 0; r < RW; ++r) decode_row(r, y[r]);
 #pragma unroll
-                                for (int k = 0; k < 8; ++k) {
-                                    const float4 v = xv[k];
-                                    acc[r][t] = fmaf(y[4 * k], v.x, acc[r][t]);
-                                    acc[r][t] = fmaf(y[4 * k + 1], v.y, acc[r][t]);
-                                    acc[r][t] = fmaf(y[4 * k + 2], v.z, acc[r][t]);
-                                    acc[r][t] = fmaf(y[4 * k + 3], v.w, acc[r][t]);
+                    for (int t = 0; t < NT; ++t) {
+                        if (t < nt) {
+                            const float4* xv = reinterpret_cast<const float4*>(X + (size_t)(t0 + t) * in_dim + 32 * s);
+#pragma unroll
+                            for (int k = 0; k < 8; ++k) {
+                                const float4 v = xv[k];
+#pragma unroll
+                                for (int r = 0; r < RW; ++r) {
+                                    acc[r][t] = fmaf(y[r][4 * k], v.x, acc[r][t]);
+                                    acc[r][t] = fmaf(y[r][4 * k + 1], v.y, acc[r][t]);
+                                    acc[r][t] = fmaf(y[r][4 * k + 2], v.z, acc[r][t]);
+                                    acc[r][t] = fmaf(y[r][4 * k + 3], v.w, acc[r][t]);
                                 }
                             }
                         }
@@ -760,11 +770,15 @@ hipError_t matmul_dt(const uint8_t* w, size_t rb, unsigned long long row0, int i
         if (tiles8 >= 256) return launch_dot_rows_f32_any<2, 2, 4, 4, 256, 4>(wf, in_dim, out_dim, X, n_tok, Y, s);
         return launch_dot_rows_f32_any<1, 1, 4, 4, 1024, 3>(wf, in_dim, out_dim, X, n_tok, Y, s);
     }
-    // from 16 tokens the MFMA GEMM (W decoded once per 64 tokens) is faster
-    // than the 8-token slices (measured on 6144 x 6144: 185 vs 265 us at 16
-    // tokens, 0.5-0.6 vs 8 ms at 512, every format)
+    // The MFMA GEMM (W decoded once per 64 tokens) from 40 tokens for the
+    // block formats and from 20 for F16/BF16; below, the 8-token slices
+    // (measured on 6144 x 6144, every format: 32 tokens 155-165 us against
+    // 190-213 us, 48 tokens 231-246 against 193-209; F16/BF16 16 tokens 142
+    // against 172, 24 tokens 207 against 182; 512 tokens 0.5-0.6 ms against
+    // 8 ms)
     if constexpr (DT != kDtF32)
-        if (n_tok >= 16) return gemm_rows_dt<DT>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
+        if (n_tok >= (DT == kDtF16 || DT == kDtBF16 ? 20 : 40))
+            return gemm_rows_dt<DT>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
     if (n_tok == 1) return matmul_dt_nt<DT, 1>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
     if (n_tok == 2) return matmul_dt_nt<DT, 2>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
     if (n_tok <= 4) return matmul_dt_nt<DT, 4>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
