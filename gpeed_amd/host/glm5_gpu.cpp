@@ -372,6 +372,39 @@ void WeightStore::moe_batch(const std::string& gate, const std::string& up, cons
                   routed_scale, norm_topk, swiglu_limit, Y);
 }
 
+void WeightStore::dense_mlp(const std::string& gate, const std::string& up, const std::string& down, int hidden,
+                            int inter, const float* X, int n_tok, float swiglu_limit, float* Y) {
+    if (n_tok <= 0) return;
+    const Tensor& tg = get_iq3(gate, hidden);
+    const Tensor& tu = get_iq3(up, hidden);
+    const Tensor& td = get_iq3(down, inter);
+    if (tg.n_rows < (uint64_t)inter || tu.n_rows < (uint64_t)inter || td.n_rows < (uint64_t)hidden)
+        throw std::runtime_error("dense_mlp: tensor rows fewer than the shape");
+    const size_t xb = (size_t)n_tok * hidden * sizeof(float);
+    void* xd = scratch(x_, xb, false);
+    void* yd = scratch(y_, xb, false);
+    check(gpeed_memcpy(xd, X, xb, kH2D), "dense_mlp: upload x");
+    void* ws = nullptr;
+    if (n_tok == 1) {
+        const size_t wsb = gpeed_iq3xxs_dense_mlp_ws_bytes(hidden, inter);
+        if (wsb == 0) throw std::runtime_error("dense_mlp: unsupported shape");
+        ws = scratch(mlp_ws_, wsb, true);
+        check(gpeed_iq3xxs_dense_mlp(tg.data, tu.data, td.data, hidden, inter, static_cast<const float*>(xd),
+                                     swiglu_limit, static_cast<float*>(yd), ws, mlp_ws_.bytes, nullptr),
+              "dense_mlp");
+    } else {
+        const size_t wsb = gpeed_iq3xxs_mlp_gemm_ws_bytes(n_tok, hidden, inter, GPEED_X_F32, 0, nullptr);
+        if (wsb == 0) throw std::runtime_error("dense_mlp: unsupported shape");
+        ws = scratch(mlp_ws_, wsb, true);
+        check(gpeed_iq3xxs_mlp_gemm(tg.data, tu.data, td.data, hidden, inter, xd, GPEED_X_F32, n_tok, swiglu_limit,
+                                    static_cast<float*>(yd), 0, nullptr, nullptr, nullptr, ws, mlp_ws_.bytes,
+                                    nullptr),
+              "dense_mlp");
+    }
+    check_ws(ws, "dense_mlp");
+    check(gpeed_memcpy(Y, yd, xb, kD2H), "dense_mlp: download y");
+}
+
 // The routed step from the logits and X already in the logits_ / x_
 // buffers; Y to the host.
 void WeightStore::moe_batch_dev(const std::string& gate, const std::string& up, const std::string& down,

@@ -100,6 +100,16 @@ public:
     void matvec_heads(const std::string& name, uint64_t row0, int in_dim, int rows_per_head, int n_heads,
                       const float* x, float* dst);
 
+    // Model::dense_mlp (model.cpp:677-690; one token) and dense_mlp_batch
+    // (model_batch.cpp:145-163; n_tok tokens) on the device: Y [n_tok][hidden]
+    // = down(SwiGLU(gate X, up X)) with the reference's clamp (min(g, lim),
+    // clamp(u, -lim, lim)), X [n_tok][hidden] and Y host arrays. gate / up
+    // [inter][hidden] and down [hidden][inter] are IQ3_XXS tensors of the
+    // store. One token: the two-launch dense GEMV (gpeed_iq3xxs_dense_mlp);
+    // more: gpeed_iq3xxs_mlp_gemm.
+    void dense_mlp(const std::string& gate, const std::string& up, const std::string& down, int hidden, int inter,
+                   const float* X, int n_tok, float swiglu_limit, float* Y);
+
     // Model::moe_batch steps 1-3: router top_k over logits [n_tok][n_exp]
     // (mode 0: sigmoid + bias with routed_scale / norm_topk as the reference;
     // mode 1: softmax over the top_k), expert buckets, per-expert gate/up
@@ -163,7 +173,7 @@ private:
     // it is made and grown when a call needs more; each launch leaves its
     // tickets at zero, and one sized for n_tok serves every smaller call.
     std::map<std::tuple<int, int>, Buffer> ws_;
-    Buffer x_, y_, route_ws_, moe_ws_, batch_ws_, logits_, bias_, eptr_, tok_, wt_;
+    Buffer x_, y_, route_ws_, moe_ws_, batch_ws_, logits_, bias_, eptr_, tok_, wt_, mlp_ws_;
 };
 
 }  // namespace gpu

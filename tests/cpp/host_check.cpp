@@ -237,6 +237,19 @@ int main(int argc, char** argv) {
             spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
             return 0;
         }
+        if (mode == "dense-mlp" && argc == 6) {  // Model::dense_mlp / dense_mlp_batch on the device
+            const std::string dir = argv[2];
+            const int H = std::atoi(argv[3]), I = std::atoi(argv[4]), T = std::atoi(argv[5]);
+            glm5::gpu::WeightStore ws;
+            ws.add("gate", slurp(dir + "/gate.bin").data(), (uint64_t)I, H);
+            ws.add("up", slurp(dir + "/up.bin").data(), (uint64_t)I, H);
+            ws.add("down", slurp(dir + "/down.bin").data(), (uint64_t)H, I);
+            const std::vector<char> x = slurp(dir + "/x.bin");
+            std::vector<float> Y((size_t)T * H);
+            ws.dense_mlp("gate", "up", "down", H, I, reinterpret_cast<const float*>(x.data()), T, 10.0f, Y.data());
+            spit(dir + "/Y.bin", Y.data(), Y.size() * 4);
+            return 0;
+        }
         if (mode == "dequant" && argc == 6) {  // host-array dequantize (quant.h:18-22)
             const int dtype = std::atoi(argv[2]);
             const uint64_t n = std::strtoull(argv[4], nullptr, 10);

@@ -118,3 +118,21 @@ def test_moe_batch_with_router_product(gpu, tmp_path, T):
     logits = oracle.matmul_rows(0, wr.view(np.uint8).reshape(E, -1), 0, H, E, X)
     ref = oracle.moe_batch(logits, X, wg, wu, wd, H, I, K, mode, None, 2.5, True, 10.0, shared=(sg, su, sd))
     assert max(rel_err(Y[t], ref[t]) for t in range(T)) < TIGHT
+
+
+@pytest.mark.parametrize("T", [1, 5, 70])
+def test_dense_mlp_host(gpu, tmp_path, T):
+    """WeightStore::dense_mlp: Model::dense_mlp (model.cpp:677-690) at one
+    token through the dense GEMV pair, dense_mlp_batch (model_batch.cpp:
+    145-163) at 5 and 70 through gpeed_iq3xxs_mlp_gemm, against the oracle."""
+    H, I = 1024, 2048
+    wg = synth.iq3xxs_matrix(89, 0, I, H)
+    wu = synth.iq3xxs_matrix(89, 1, I, H)
+    wd = synth.iq3xxs_matrix(89, 2, H, I)
+    X = synth.normal(89, T, T * H).reshape(T, H)
+    for name, a in (("gate", wg), ("up", wu), ("down", wd), ("x", X)):
+        a.tofile(tmp_path / f"{name}.bin")
+    run("dense-mlp", tmp_path, H, I, T)
+    Y = np.fromfile(tmp_path / "Y.bin", np.float32).reshape(T, H)
+    ref = oracle.dense_mlp(wg, wu, wd, H, I, X, 10.0)
+    assert max(rel_err(Y[t], ref[t]) for t in range(T)) < TIGHT
