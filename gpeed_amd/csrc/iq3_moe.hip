@@ -104,10 +104,11 @@ __device__ __forceinline__ int block_exclusive_scan(const int* v, int* out, int*
     return total;
 }
 
-// Assignments (token, k) kept in LDS when there are at most this many: the
-// top-k loop then issues no global store (on gfx9 a wavefront's next global
-// load would wait for its stores).
-constexpr int kRouteLdsAsg = 2048;
+// Assignments (token, k) kept in LDS when there are at most this many (a
+// 512-token prefill chunk at top-8): the top-k loop then issues no global
+// store (on gfx9 a wavefront's next global load would wait for its stores),
+// and the last workgroup's bucket sort and plan run on LDS copies.
+constexpr int kRouteLdsAsg = 4096;
 
 // J = register slots per lane: expert e lives in lane e % 64, slot e / 64.
 // Top-k of tokens t_first, t_first + t_step, ... (one wavefront per token):
@@ -1054,8 +1055,9 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
     // 1. router, per-token X images, bucket sort and work plan
     // ranking workgroups: one token per wavefront up to 64 of them; image
     // workgroups: one (token, block) item per wavefront up to 192
+    // (the grouped-GEMM form gathers its own images: no image workgroups)
     const int n_rank = std::min((T + 15) / 16, 64);
-    const int groups = n_rank + std::min((T * nbH + 15) / 16, 192);
+    const int groups = n_rank + (gemm ? 0 : std::min((T * nbH + 15) / 16, 192));
     // (the grouped-GEMM form runs the shared expert as GEMMs of its own, so
     // its plan holds the routed segments only)
     const int T_plan = gemm ? 0 : T_sh;
