@@ -451,41 +451,47 @@ __global__ __launch_bounds__(256) void k_matmul_rows(const uint8_t* base, int ba
 
 // Prefill-sized products over raw GGUF rows (every format but F32, whose
 // products keep dot_f32's order): Y[t][j] = sum_i W[j][i] X[t][i]. A
-// workgroup takes a 64-row x 64-token tile and walks K in chunks of 128
-// columns: lane l decodes sub-block l % 4 of the chunk of row l / 4
+// workgroup takes an RT-row x 64-token tile and walks K in chunks of 128
+// columns: lane l < 4 RT decodes sub-block l % 4 of the chunk of row l / 4
 // (decode32: the exact dequantization) into an fp32 LDS tile, X's chunk is
-// copied beside it, and the four wavefronts multiply 32 x 32 quarters with
-// fp32 MFMAs (v_mfma_f32_16x16x4f32: operands exact, fp32 accumulation in
-// another order than the reference's, as in every product here). W is
-// decoded once per 64 tokens instead of once per 8.
-constexpr int kRgRows = 64, kRgTok = 64, kRgK = 128, kRgStride = kRgK + 4;  // (+4: conflict-free reads)
+// copied beside it, and the four wavefronts multiply their share of the tile
+// with fp32 MFMAs (v_mfma_f32_16x16x4f32: operands exact, fp32 accumulation
+// in another order than the reference's, as in every product here). W is
+// decoded once per 64 tokens instead of once per 8. Every output's sum runs
+// over the same chunks and 4-column steps whatever RT is, so the tile shape
+// does not change a bit.
+constexpr int kRgTok = 64, kRgK = 128, kRgStride = kRgK + 4;  // (+4: conflict-free reads)
 
-template <int DT>
+template <int DT, int RT>
 __global__ __launch_bounds__(256, 2) void k_gemm_rows(const uint8_t* __restrict__ w, size_t rb, int in_dim,
                                                       int out_dim, const float* __restrict__ X, int n_tok,
                                                       float* __restrict__ Y, int ldy) {
     constexpr int kE = Fmt<DT>::kElems, kB = Fmt<DT>::kBytes;
+    // wavefront grid over the tile's 16 x 16 MFMA tiles: WR x WT wavefronts,
+    // each R2 row tiles x U2 token tiles
+    constexpr int RM = RT / 16, WR = RM < 2 ? RM : 2, WT = 4 / WR, R2 = RM / WR, U2 = (kRgTok / 16) / WT;
+    static_assert(RT == 16 || RT == 32 || RT == 64, "row tile");
     __shared__ Tables<DT> tb;
-    __shared__ __attribute__((aligned(16))) float wt[kRgRows][kRgStride];
+    __shared__ __attribute__((aligned(16))) float wt[RT][kRgStride];
     __shared__ __attribute__((aligned(16))) float xt[kRgTok][kRgStride];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     tb.load(tid, 256);
-    const int j0 = blockIdx.x * kRgRows, t0 = blockIdx.y * kRgTok;
+    const int j0 = blockIdx.x * RT, t0 = blockIdx.y * kRgTok;
     const int drow = tid >> 2, dsb = tid & 3;  // this lane's decode: row, sub-block of the chunk
     // (rows past out_dim decode the last row; tokens past n_tok copy the
     // last token: their outputs are not stored)
-    const uint8_t* wrow = w + (size_t)min(j0 + drow, out_dim - 1) * rb;
-    // this wavefront's quarter: rows qr .. qr + 31, tokens qt .. qt + 31
-    const int qr = (wave & 1) * 32, qt = (wave >> 1) * 32;
+    const uint8_t* wrow = w + (size_t)min(j0 + min(drow, RT - 1), out_dim - 1) * rb;
+    // this wavefront's share: rows qr .. qr + 16 R2 - 1, tokens qt .. qt + 16 U2 - 1
+    const int qr = (wave % WR) * 16 * R2, qt = (wave / WR) * 16 * U2;
     const int li = lane & 15, lk = lane >> 4;
-    float4_t acc[2][2];
+    float4_t acc[R2][U2];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < R2; ++r)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) acc[r][u] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int u = 0; u < U2; ++u) acc[r][u] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = 0; k0 < in_dim; k0 += kRgK) {
         __syncthreads();  // the MFMAs of the previous chunk have read their operands
-        {
+        if (drow < RT) {
             const int col = k0 + 32 * dsb;
             float y[32];
             if (col < in_dim) {
@@ -512,21 +518,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_rows(const uint8_t* __restrict_
         // tokens (token li, column lk); D[row 4 lk + i][token li]
 #pragma unroll 4
         for (int k = 0; k < kRgK; k += 4) {
-            float a[2], b[2];
+            float a[R2], b[U2];
 #pragma unroll
-            for (int r = 0; r < 2; ++r) a[r] = wt[qr + 16 * r + li][k + lk];
+            for (int r = 0; r < R2; ++r) a[r] = wt[qr + 16 * r + li][k + lk];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) b[u] = xt[qt + 16 * u + li][k + lk];
+            for (int u = 0; u < U2; ++u) b[u] = xt[qt + 16 * u + li][k + lk];
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
+            for (int r = 0; r < R2; ++r)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) acc[r][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], b[u], acc[r][u], 0, 0, 0);
+                for (int u = 0; u < U2; ++u) acc[r][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], b[u], acc[r][u], 0, 0, 0);
         }
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < R2; ++r)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < U2; ++u) {
             const int t = t0 + qt + 16 * u + li;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -536,19 +542,31 @@ __global__ __launch_bounds__(256, 2) void k_gemm_rows(const uint8_t* __restrict_
         }
 }
 
-template <int DT>
-hipError_t gemm_rows_dt(const uint8_t* w, size_t rb, int in_dim, int out_dim, const float* X, int n_tok, float* Y,
+template <int DT, int RT>
+hipError_t gemm_rows_rt(const uint8_t* w, size_t rb, int in_dim, int out_dim, const float* X, int n_tok, float* Y,
                         hipStream_t s) {
     constexpr int kMaxTok = 65535 * kRgTok;  // token tiles per launch (grid y)
-    const unsigned gx = (unsigned)((out_dim + kRgRows - 1) / kRgRows);
+    const unsigned gx = (unsigned)((out_dim + RT - 1) / RT);
     for (int t = 0; t < n_tok; t += kMaxTok) {
         const int nt = n_tok - t < kMaxTok ? n_tok - t : kMaxTok;
-        hipLaunchKernelGGL(k_gemm_rows<DT>, dim3(gx, (unsigned)((nt + kRgTok - 1) / kRgTok)), dim3(256), 0, s, w, rb,
-                           in_dim, out_dim, X + (size_t)t * in_dim, nt, Y + (size_t)t * out_dim, out_dim);
+        hipLaunchKernelGGL((k_gemm_rows<DT, RT>), dim3(gx, (unsigned)((nt + kRgTok - 1) / kRgTok)), dim3(256), 0, s,
+                           w, rb, in_dim, out_dim, X + (size_t)t * in_dim, nt, Y + (size_t)t * out_dim, out_dim);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// The row tile: 64 rows where the tiles make 256 workgroups (one per CU of a
+// 256-CU device), else 32 or 16 (more workgroups, each with fewer MFMAs:
+// 6144 rows at up to 64 tokens are 96 tiles of 64 rows, 384 of 16)
+template <int DT>
+hipError_t gemm_rows_dt(const uint8_t* w, size_t rb, int in_dim, int out_dim, const float* X, int n_tok, float* Y,
+                        hipStream_t s) {
+    const long long tt = (n_tok + kRgTok - 1) / kRgTok;
+    if ((long long)((out_dim + 63) / 64) * tt >= 256) return gemm_rows_rt<DT, 64>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
+    if ((long long)((out_dim + 31) / 32) * tt >= 256) return gemm_rows_rt<DT, 32>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
+    return gemm_rows_rt<DT, 16>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
 }
 
 template <int DT>
@@ -770,14 +788,14 @@ hipError_t matmul_dt(const uint8_t* w, size_t rb, unsigned long long row0, int i
         if (tiles8 >= 256) return launch_dot_rows_f32_any<2, 2, 4, 4, 256, 4>(wf, in_dim, out_dim, X, n_tok, Y, s);
         return launch_dot_rows_f32_any<1, 1, 4, 4, 1024, 3>(wf, in_dim, out_dim, X, n_tok, Y, s);
     }
-    // The MFMA GEMM (W decoded once per 64 tokens) from 40 tokens for the
-    // block formats and from 20 for F16/BF16; below, the 8-token slices
-    // (measured on 6144 x 6144, every format: 32 tokens 155-165 us against
-    // 190-213 us, 48 tokens 231-246 against 193-209; F16/BF16 16 tokens 142
-    // against 172, 24 tokens 207 against 182; 512 tokens 0.5-0.6 ms against
+    // The MFMA GEMM (W decoded once per 64 tokens) from 32 tokens for the
+    // block formats and from 16 for F16/BF16; below, the 8-token slices
+    // (measured on 6144 x 6144, every format: 24 tokens 129-173 us against
+    // 130-149 us, 32 tokens 151-209 against 133-152; F16/BF16 8 tokens 76
+    // against 122, 16 tokens 140 against 121; 512 tokens 0.5-0.6 ms against
     // 8 ms)
     if constexpr (DT != kDtF32)
-        if (n_tok >= (DT == kDtF16 || DT == kDtBF16 ? 20 : 40))
+        if (n_tok >= (DT == kDtF16 || DT == kDtBF16 ? 16 : 32))
             return gemm_rows_dt<DT>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
     if (n_tok == 1) return matmul_dt_nt<DT, 1>(w, rb, in_dim, out_dim, X, n_tok, Y, s);
     if (n_tok == 2) return matmul_dt_nt<DT, 2>(w, rb, in_dim, out_dim, X, n_tok, Y, s);

@@ -74,10 +74,10 @@ def test_rows_product_golden(gpu, dt):
 @pytest.mark.parametrize("dt", ALL_TYPES)
 @pytest.mark.parametrize("n_tok", [1, 2, 3, 8, 13, 24, 70])
 def test_rows_product_vs_oracle(gpu, dt, n_tok):
-    """The 8-token-slice kernel below 40 tokens (20 for F16/BF16), the
+    """The 8-token-slice kernel below 32 tokens (16 for F16/BF16), the
     fp32-MFMA GEMM from there (24 tokens: F16/BF16 only; F32: dot_f32's order
-    at every size); 150 rows and 70 tokens leave partial 64-row and 64-token
-    tiles."""
+    at every size); 150 rows and 70 tokens leave partial row tiles (16 rows
+    each at 70 tokens: 10 x 2 workgroups) and a partial 64-token tile."""
     in_dim, rows, row0, out_dim = 2048, 200, 37, 150
     w = synth.quant_matrix(43, dt, dt, rows, in_dim)
     X = synth.normal(43, 100 + n_tok, n_tok * in_dim).reshape(n_tok, in_dim)
@@ -108,6 +108,19 @@ def test_rows_product_prefill_chunk(gpu, dt):
     X = synth.normal(45, 512, 512 * in_dim).reshape(512, in_dim)
     Y = G.matmul_rows(dt, dev(w.reshape(-1), gpu), rows, row0, in_dim, out_dim, dev(X, gpu))
     assert rel_err(Y.cpu().numpy(), oracle.matmul_rows(dt, w, row0, in_dim, out_dim, X)) < TIGHT
+
+
+@pytest.mark.parametrize("dt", [8, 14])
+@pytest.mark.parametrize("rows", [4096, 2048])
+def test_rows_product_gemm_row_tiles(gpu, dt, rows):
+    """The fp32-MFMA GEMM's row tiles: 4096 rows x 256 tokens take 64-row
+    tiles (256 workgroups), 2048 rows 32-row tiles (and the suite's smaller
+    cases 16-row tiles)."""
+    in_dim, n_tok = 512, 256
+    w = synth.quant_matrix(46, dt, dt, rows, in_dim)
+    X = synth.normal(46, rows, n_tok * in_dim).reshape(n_tok, in_dim)
+    Y = G.matmul_rows(dt, dev(w.reshape(-1), gpu), rows, 0, in_dim, rows, dev(X, gpu))
+    assert rel_err(Y.cpu().numpy(), oracle.matmul_rows(dt, w, 0, in_dim, rows, X)) < TIGHT
 
 
 def test_rows_product_errors(gpu):
