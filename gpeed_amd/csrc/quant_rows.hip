@@ -309,8 +309,12 @@ __global__ __launch_bounds__(256) void k_dequant_scalar(const uint8_t* __restric
 }
 
 // Rows per wavefront and the bytes of one 64-sub-block chunk of a row.
-template <int DT> struct RowsCfg {
-    static constexpr int kRW = DT == kDtF32 ? 1 : (DT == kDtF16 || DT == kDtBF16) ? 2 : 4;
+template <int DT, int NT = 1> struct RowsCfg {
+    // rows per wavefront: two for one token (more wavefronts in flight; on
+    // 6144 x 6144, 12.3-16.3 us against 14.9-23.1 us with four and 21.7-24.9
+    // with one), four for 2-8 tokens (each token's activations loaded once
+    // serve four rows), two for F16/BF16
+    static constexpr int kRW = DT == kDtF32 ? 1 : (NT == 1 || DT == kDtF16 || DT == kDtBF16) ? 2 : 4;
     static constexpr int kChunkBytes = 64 * 32 / Fmt<DT>::kElems * Fmt<DT>::kBytes;  // 64 sub-blocks
     static constexpr int kSegs = (kChunkBytes + 15) / 16 + 1;  // 16-byte segments covering it, any alignment
     static constexpr int kLoads = (kSegs + 63) / 64;           // per lane
@@ -334,7 +338,7 @@ __global__ __launch_bounds__(256) void k_matmul_rows(const uint8_t* base, int ba
                                                      uint32_t row_bytes, int in_dim, int out_dim,
                                                      const float* __restrict__ X, int n_tok, float* __restrict__ Y,
                                                      int ldy) {
-    using C = RowsCfg<DT>;
+    using C = RowsCfg<DT, NT>;
     constexpr int RW = C::kRW, kSub = Fmt<DT>::kElems / 32, kBB = Fmt<DT>::kBytes;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, base_bytes, kBufferDword3);
     __shared__ Tables<DT> tb;
@@ -589,7 +593,7 @@ hipError_t matmul_dt_nt(const uint8_t* w, size_t rb, int in_dim, int out_dim, co
                         hipStream_t s) {
     // row slices whose bytes stay below 2 GiB (32-bit buffer offsets); at
     // most 32768 token columns per launch
-    constexpr int RW = RowsCfg<DT>::kRW;
+    constexpr int RW = RowsCfg<DT, NT>::kRW;
     const long long max_rows = ((1ll << 31) - 64) / (long long)rb / (4 * RW) * (4 * RW);
     // rows so long that one wavefront's rows pass 2 GiB cannot be sliced
     if (max_rows < 1) return hipErrorInvalidValue;
