@@ -33,6 +33,10 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v_t __attribute__((ext_vector_type(2)));
 
 constexpr int kGemmThreads = 256;
+// cache policy of k_gemm5's W loads: non-temporal (each W tile is read by
+// at most a few token tiles; k_gemm6's many token tiles re-read W from L2
+// and keep the default: 324.5 -> 328.4 us at M = 2048 with it)
+constexpr int kWNt = 2;
 
 __device__ __forceinline__ uint32_t f16_pair_of_floats(float lo, float hi) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
@@ -944,10 +948,11 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
         uint8_t* dst = sm.wb[kh][hb & 1];
 #pragma unroll
         for (int k = 0; k < 3; ++k)
-            if (rq + 4 * k < 9) __builtin_amdgcn_global_load_lds(g.w + (wsrc[k] + boff + hoff), dst + (rq + 4 * k) * 1024, 16, 0, 0);
+            if (rq + 4 * k < 9)
+                __builtin_amdgcn_global_load_lds(g.w + (wsrc[k] + boff + hoff), dst + (rq + 4 * k) * 1024, 16, 0, kWNt);
         if ((hb & 1) == 0 && rq == 3)
             __builtin_amdgcn_global_load_lds(g.w + (dsrc + boff), &sm.wd[0][0][0] + (kh * 2 + ((hb >> 1) & 1)) * 1024,
-                                             16, 0, 0);
+                                             16, 0, kWNt);
     };
 
     // this lane's rows j < JT: lane slot in the staged half block, and d

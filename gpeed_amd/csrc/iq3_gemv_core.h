@@ -132,10 +132,12 @@ __device__ __forceinline__ float rec_unscale(const Rec<NP>& r, int t) {
 template <int NP>
 __device__ __forceinline__ void load_record(Rec<NP>& r, const uint8_t* rec, const uint8_t* ab,
                                             uint32_t lane, int n_tok) {
+    // the record non-temporal (read once per item), so the weight stream
+    // leaves the activation images in L2
 #pragma unroll
     for (int i = 0; i < 6; ++i)
-        r.u[i] = *reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u);
-    r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
+        r.u[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u));
+    r.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u));
     const uint32_t slot_half = (lane >> 2) * 2 + (lane & 1);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {

@@ -663,10 +663,11 @@ struct GroupedArgs {
 template <int NP>
 __device__ __forceinline__ void load_record_gather(Rec<NP>& r, const uint8_t* rec, const uint8_t* timg_b,
                                                    const size_t (&toff)[NP], uint32_t lane) {
+    // the record non-temporal, as in load_record
 #pragma unroll
     for (int i = 0; i < 6; ++i)
-        r.u[i] = *reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u);
-    r.d = *reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u);
+        r.u[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(rec + i * kUnitBytes + lane * 16u));
+    r.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(rec + kRecordDOffset + lane * 2u));
     const uint32_t slot_half = (lane >> 2) * 2 + (lane & 1);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {

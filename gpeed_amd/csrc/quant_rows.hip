@@ -363,7 +363,8 @@ __global__ __launch_bounds__(256) void k_matmul_rows(const uint8_t* base, int ba
             for (int k = 0; k < C::kLoads; ++k) {
                 const uint32_t i = (uint32_t)(lane + 64 * k);
                 const uint32_t off = i < nseg ? b0 + 16 * i : 0x80000000u;  // past the range: zeros, no access
-                seg[r][k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+                // non-temporal: the rows are read once
+                seg[r][k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2));
             }
         }
     };
