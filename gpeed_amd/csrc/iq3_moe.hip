@@ -244,32 +244,53 @@ __device__ __forceinline__ void bucket_body(int T, int E, int K, int* __restrict
 
     // 3. stable scatter by expert (model_batch.cpp:211-219): assignment a
     // goes to its expert's cursor plus the number of earlier assignments of
-    // that expert, found per chunk of 1024 by comparison.
+    // that expert. Per chunk of 1024 (16 wavefronts of 64, in assignment
+    // order): the lanes of a wavefront with the same expert are found with
+    // one ballot per bit of the expert id, a lane's rank among them is the
+    // count below it; the wavefronts' counts per expert meet in a [16][64]
+    // table (chunk_e), 64 experts at a time, whose column scans in wavefront
+    // order give each wavefront's offset and advance the cursors.
     const int N = T * K;
+    const int wave = tid >> 6, lane = tid & 63;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int bits = 0;
+    while ((1 << bits) < E) ++bits;
     for (int c0 = 0; c0 < N; c0 += 1024) {
         const int a = c0 + tid;
         const int ea = a < N ? src_e[a] : -1;
-        chunk_e[tid] = ea;
-        __syncthreads();
-        if (a < N) {
-            // earlier assignments of the same expert in this chunk, four per
-            // LDS read
-            int rank = 0;
-            const int4* ce4 = reinterpret_cast<const int4*>(chunk_e);
-#pragma unroll 4
-            for (int j = 0; j < (tid >> 2); ++j) {
-                const int4 v = ce4[j];
-                rank += (v.x == ea) + (v.y == ea) + (v.z == ea) + (v.w == ea);
+        unsigned long long peers = __ballot(ea >= 0);
+        for (int b = 0; b < bits; ++b) {
+            const bool on = ea >= 0 && ((ea >> b) & 1);
+            const unsigned long long m = __ballot(on);
+            peers &= on ? m : ~m;
+        }
+        const int rank = __popcll(peers & below);
+        int base = 0;
+        for (int s0 = 0; s0 < E; s0 += 64) {
+            chunk_e[tid] = 0;
+            __syncthreads();
+            const bool here = ea >= s0 && ea < s0 + 64;
+            if (here && rank == 0) chunk_e[wave * 64 + (ea - s0)] = __popcll(peers);
+            __syncthreads();
+            if (tid < 64 && s0 + tid < E) {
+                int off = cursor[s0 + tid];
+                for (int w = 0; w < 16; ++w) {
+                    const int c = chunk_e[w * 64 + tid];
+                    chunk_e[w * 64 + tid] = off;
+                    off += c;
+                }
+                cursor[s0 + tid] = off;
             }
-            for (int j = tid & ~3; j < tid; ++j) rank += chunk_e[j] == ea;
-            const int p = cursor[ea] + rank;
+            __syncthreads();
+            if (here) base = chunk_e[wave * 64 + (ea - s0)];
+            __syncthreads();
+        }
+        if (a < N) {
+            const int p = base + rank;
             tok[p] = a / K;
             if (l_tok) l_tok[p] = a / K;
             wt[p] = src_w[a];
         }
-        __syncthreads();
-        if (a < N) atomicAdd(&cursor[ea], 1);
-        __syncthreads();
     }
 }
 
