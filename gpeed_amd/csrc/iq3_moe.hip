@@ -358,8 +358,10 @@ struct MoePlan {
 // N .. N + T_sh - 1, token p - N.
 // eptr / tok may be LDS copies; pos_buf (LDS, or pl.pos itself) holds the
 // per-token slot lists while they are built and sorted.
+// segs false (the grouped-GEMM form, which multiplies whole buckets): the
+// segment tables and the slots' segment entries are not written.
 __device__ __forceinline__ void plan_body(const int* eptr, const int* tok, int T, int E, int K, int T_sh, MoePlan pl,
-                                          int* pos_buf) {
+                                          int* pos_buf, bool segs = true) {
     __shared__ int ep[kMaxExperts + 1];
     __shared__ int fstart[kMaxExperts + 1];
     __shared__ int nfull[kMaxExperts];
@@ -432,7 +434,7 @@ __device__ __forceinline__ void plan_body(const int* eptr, const int* tok, int T
         __hip_atomic_store(pl.ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    for (int e = tid; e < E; e += 1024) {
+    for (int e = tid; e < E && segs; e += 1024) {
         const int g = ep[e + 1] - ep[e], c = g % kSegTok;
         // order among equal-size partial segments is free: no result depends on it
         pid[e] = c ? atomicAdd(&ccursor[c], 1) : -1;
@@ -449,18 +451,18 @@ __device__ __forceinline__ void plan_body(const int* eptr, const int* tok, int T
         }
     }
     const int N = ep[E];
-    for (int j = tid; j < n_sh; j += 1024) {
+    for (int j = tid; j < n_sh && segs; j += 1024) {
         pl.seg_e[j] = E;  // the shared expert
         pl.seg_p0[j] = N + j * kSegTok;
         pl.seg_n[j] = min(kSegTok, T_sh - j * kSegTok);
     }
-    for (int t = tid; t < T_sh; t += 1024) {
+    for (int t = tid; t < T_sh && segs; t += 1024) {
         pl.seg_of[N + t] = t / kSegTok;
         pl.idx_of[N + t] = t % kSegTok;
         pl.slot_tok[N + t] = t;
     }
     __syncthreads();
-    for (int p = tid; p < N; p += 1024) {
+    for (int p = tid; p < N && segs; p += 1024) {
         int lo = 0, hi = E;  // largest e with ep[e] <= p
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
@@ -599,7 +601,7 @@ __global__ __launch_bounds__(1024) void k_moe_front(const float* __restrict__ lo
                                                     int* __restrict__ asg_e, float* __restrict__ asg_w, int T_sh,
                                                     MoePlan pl, const float* __restrict__ X, int nb,
                                                     uint8_t* __restrict__ timg, float* __restrict__ tus,
-                                                    int n_rank) {
+                                                    int n_rank, int plan_segs) {
     __shared__ float rank_score[16][kMaxTopK];
     __shared__ int cnt[kMaxExperts];
     __shared__ int cursor[kMaxExperts];
@@ -643,13 +645,13 @@ __global__ __launch_bounds__(1024) void k_moe_front(const float* __restrict__ lo
     if constexpr (kLds) {
         bucket_body(T, E, K, eptr, tok, wt, lds_e, lds_w, cnt, cursor, chunk_e, l_eptr, l_tok);
         __syncthreads();
-        plan_body(l_eptr, l_tok, T, E, K, T_sh, pl, l_pos);
+        plan_body(l_eptr, l_tok, T, E, K, T_sh, pl, l_pos, plan_segs != 0);
     } else {
         bucket_body(T, E, K, eptr, tok, wt, asg_e, asg_w, cnt, cursor, chunk_e, nullptr, nullptr);
         // the plan reads eptr / tok as the bucket sort wrote them
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
         __syncthreads();
-        plan_body(eptr, tok, T, E, K, T_sh, pl, pl.pos_tmp);
+        plan_body(eptr, tok, T, E, K, T_sh, pl, pl.pos_tmp, plan_segs != 0);
     }
     if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1087,7 +1089,7 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
         hipLaunchKernelGGL(kern, dim3(groups), dim3(1024), 0, s, logits, T, E, K, mode, bias, routed_scale,
                            norm_topk, eptr, tok, wt, reinterpret_cast<int*>(ws + L.sel),
                            reinterpret_cast<int*>(ws + L.asg_e), reinterpret_cast<float*>(ws + L.asg_w), T_plan, pl, X,
-                           nbH, timg, tus, n_rank);
+                           nbH, timg, tus, n_rank, gemm ? 0 : 1);
     };
     const bool lds = (long long)T * K <= kRouteLdsAsg;
     if (E <= 64) lds ? front(k_moe_front<1, true>) : front(k_moe_front<1, false>);
