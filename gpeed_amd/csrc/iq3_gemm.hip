@@ -232,11 +232,16 @@ struct GemmArgs {
     // token tile (grp_count[0] entries); the tensors' rows of expert e start
     // grp_w_stride bytes of records after those of expert e - 1; Y rows are
     // slots too. grp_eptr null: one GEMM over rows 0 .. M - 1.
+    // grp_tok (may be null): slot p's image row (and unscale) is
+    // grp_tok[p] of images of grp_img_rows rows (per-token images of the
+    // batch, shared by every slot of a token) instead of row p.
     const int* grp_eptr;
     const int* grp_tile;
     const int* grp_count;
     int grp_rows;
     unsigned long long grp_w_stride;
+    const int* grp_tok;
+    int grp_img_rows;
     GemmProb p2;
 };
 
@@ -839,8 +844,10 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     GemmTile tl;
     int tn;
     GemmArgs g;
-    // X rows [xrow0, xrow0 + g.M) of images of xplane rows each
+    // X rows [xrow0, xrow0 + g.M) of images of xplane rows each (tokmap:
+    // row tokmap[m] for the tile's row m instead)
     int xrow0 = 0, xplane = g_all.M;
+    const int* tokmap = nullptr;
     if (!g_all.grp_eptr) {
         GemmArgs ga = g_all;
         int bid = blockIdx.x;
@@ -885,7 +892,12 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
         if (g.M <= tl.tm * BM) return;  // uniform: no rows of this tile
         g.w += (size_t)e * g_all.grp_w_stride;
         g.y += (size_t)xrow0 * g.N;
-        g.unscale += xrow0;
+        if (g_all.grp_tok) {
+            tokmap = g_all.grp_tok + xrow0;
+            xplane = g_all.grp_img_rows;
+        } else {
+            g.unscale += xrow0;
+        }
     }
     const int m0 = tl.tm * BM, n0 = tn * BN5;
     const int last_tile = (g.N + kTileRows - 1) / kTileRows - 1;
@@ -913,8 +925,9 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     for (int i = 0; i < 4; ++i) {
         const int p = rq + 4 * i, v = p / (2 * MT);
         const int r = 8 * (p % (2 * MT)) + (int)(lane >> 3);
-        xsrc[i] = ((uint32_t)v * (uint32_t)xplane * (uint32_t)g.K +
-                   (uint32_t)(xrow0 + min(m0 + r, g.M - 1)) * (uint32_t)g.K) * 2u +
+        const int mr = min(m0 + r, g.M - 1);
+        const int xr = tokmap ? min(max(tokmap[mr], 0), xplane - 1) : xrow0 + mr;
+        xsrc[i] = ((uint32_t)v * (uint32_t)xplane * (uint32_t)g.K + (uint32_t)xr * (uint32_t)g.K) * 2u +
                   (((lane & 7u) ^ (lane >> 3)) << 4);
     }
     const uint8_t* xbase = reinterpret_cast<const uint8_t*>(g.xh);
@@ -1142,7 +1155,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     for (int f = tid; f < rows * (BN5 / 4); f += kThreads5) {
         const int m = f / (BN5 / 4), c4 = (f - m * (BN5 / 4)) * 4;
         if (c4 >= cols) continue;
-        const float us = g.unscale[m0 + m];
+        const float us = tokmap ? g.unscale[min(max(tokmap[m0 + m], 0), xplane - 1)] : g.unscale[m0 + m];
         const float4 v = *reinterpret_cast<const float4*>(&tile[m * kTStride + c4]);
         float* yrow = g.y + (size_t)(m0 + m) * g.N + n0 + c4;
         if (vec && c4 + 4 <= cols) {
@@ -1765,10 +1778,10 @@ hipError_t launch_grp_tiles(const int* eptr, int E, int S, int* tiles, int* coun
 
 hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, int in_dim, int E, const int* eptr,
                                int S, const _Float16* xh, const float* uns, float* ya, float* yb, const int* tiles,
-                               const int* count, uint32_t* err, hipStream_t s) {
-    if (rows <= 0 || rows % kTileRows || S <= 0) return hipErrorInvalidValue;
-    // image offsets are 32-bit (two fp16 images of S rows)
-    if ((size_t)2 * S * in_dim * 2 >= (1ull << 32)) return hipErrorInvalidValue;
+                               const int* count, uint32_t* err, hipStream_t s, const int* tok, int img_rows) {
+    if (rows <= 0 || rows % kTileRows || S <= 0 || (tok && img_rows <= 0)) return hipErrorInvalidValue;
+    // image offsets are 32-bit (two fp16 images of S, or img_rows, rows)
+    if ((size_t)2 * (tok ? img_rows : S) * in_dim * 2 >= (1ull << 32)) return hipErrorInvalidValue;
     const size_t nb = (size_t)(in_dim / kQK);
     const size_t stride = (size_t)(rows / kTileRows) * nb * kRecordBytes;
     if (stride >= (1ull << 32)) return hipErrorInvalidValue;
@@ -1794,6 +1807,8 @@ hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, i
     a.grp_count = count;
     a.grp_rows = S;
     a.grp_w_stride = stride;
+    a.grp_tok = tok;
+    a.grp_img_rows = tok ? img_rows : S;
     const int cap = grp_tiles_cap(S, E);
     a.tiles_m = cap;
     return launch_timed(kProfGemm, k_gemm5<4, 2>, dim3(cap * a.tiles_n), dim3(kThreads5), 0, s, a);

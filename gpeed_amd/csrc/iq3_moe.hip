@@ -931,14 +931,15 @@ MoeLayout moe_layout(int T, int E, int K, int H, int I, int T_sh = 0, bool fused
 }
 
 // The grouped-GEMM form of the whole step: the layout above (its segment
-// images unused) and, after it, the slot-ordered X images, the expert tile
-// table, the SwiGLU images and the shared expert's GEMM workspaces.
+// images unused) and, after it, the per-token X images, the expert tile
+// table, the slot-ordered SwiGLU images and the shared expert's GEMM
+// workspaces.
 MoeLayout moe_gemm_layout(int T, int E, int K, int H, int I, int T_sh, int num_cus) {
     MoeLayout L = moe_layout(T, E, K, H, I, T_sh, true);
     const size_t S = (size_t)T * K;
     size_t off = L.total;
-    L.xg = off; off += align256(2 * S * H * 2);
-    L.xg_uns = off; off += align256(S * 4);
+    L.xg = off; off += align256(2 * (size_t)T * H * 2);
+    L.xg_uns = off; off += align256((size_t)T * 4);
     L.gtiles = off; off += align256(4 * (size_t)grp_tiles_cap((int)S, E));
     L.gcount = off; off += 256;
     L.hg = off; off += align256(2 * S * I * 2);
@@ -1111,10 +1112,12 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
         int* gcount = reinterpret_cast<int*>(ws + L.gcount);
         _Float16* hg = reinterpret_cast<_Float16*>(ws + L.hg);
         float* hg_uns = reinterpret_cast<float*>(ws + L.hg_uns);
-        e = launch_prep_x_rows(N, H, s, X, nullptr, 0.0f, xg, xg_uns, tok);
+        // X's images once per token; the gate/up GEMM reads a slot's row
+        // through its token
+        e = launch_prep_x_rows(T, H, s, X, nullptr, 0.0f, xg, xg_uns, nullptr);
         if (e == hipSuccess) e = launch_grp_tiles(eptr, E, N, gtiles, gcount, s);
         if (e == hipSuccess)
-            e = launch_gemm_grouped(w_gate, w_up, I, H, E, eptr, N, xg, xg_uns, G, U, gtiles, gcount, err, s);
+            e = launch_gemm_grouped(w_gate, w_up, I, H, E, eptr, N, xg, xg_uns, G, U, gtiles, gcount, err, s, tok, T);
         if (e == hipSuccess) e = launch_prep_x_rows(N, I, s, G, U, lim, hg, hg_uns, nullptr);
         if (e == hipSuccess)
             e = launch_gemm_grouped(w_down, nullptr, H, I, E, eptr, N, hg, hg_uns, D, nullptr, gtiles, gcount, err,
