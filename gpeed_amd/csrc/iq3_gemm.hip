@@ -18,6 +18,7 @@
 // k_gemm3 (bf16 X of at most 64 tokens) differ in how the wavefronts split
 // the tile and how W and X reach them; see each kernel.
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "iq3_common.h"
@@ -746,20 +747,21 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
 
 constexpr int BM5 = 128, BN5 = 192, BK5 = 64;
 constexpr int kThreads5 = 512;
-constexpr int kXStage5 = BM5 * BK5 * 2;          // 16 KiB: 128 rows x 128 bytes
 constexpr int kWHalf5 = 3 * 3 * kUnitBytes;      // 9 KiB: 3 row tiles x 3 units
 constexpr int kTbl5 = 16 * 256 * 8;              // 32 KiB: the grid times every 2s+1
 constexpr uint32_t kZeroEntry5 = kTbl5;          // 2 KiB of zeros after the scaled grid
 
+// XS: bytes of one X stage (16 KiB: 128 image rows; 20 KiB: 160, the
+// 80-token tiles of fp32 X)
+constexpr int kXStageMax5 = 160 * BK5 * 2;
+template <int XS>
 struct GemmSmem5 {
     uint8_t tbl[kTbl5 + 2048];   // grid * (2s+1) as [s][idx], then a zero "scale"
-    uint8_t xs[2][2][kXStage5];  // [K half][buffer]
+    uint8_t xs[2][2][XS];        // [K half][buffer]
     uint8_t wb[2][2][kWHalf5];   // [K half][buffer]: [tile][unit][64 lanes x 16 B]
     uint8_t wd[2][2][1024];      // [K half][block parity]: [tile][64 fp16] (a whole wavefront's copy)
     int last_flag;
 };
-// the K half 1 sums (128 x 192 fp32) overlay xs and wb
-static_assert(2 * 2 * kXStage5 + 2 * 2 * kWHalf5 >= 128 * 192 * 4, "reduction area");
 
 // Entry (idx, s) = 4 fp16 values grid(idx)[0..3] * (2s+1), at (s << 11) |
 // (idx << 3): the bank of a lookup follows the index's low five bits, so
@@ -829,10 +831,18 @@ __device__ __forceinline__ half8_t decode_group5(const uint8_t* tbl, uint32_t q,
 // sub-block and the MFMAs per decoded B operand are the same for both.
 template <int MT, int V>
 __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
-    static_assert(MT * V == 8, "one 16 KiB X stage");
+    static_assert(MT * V >= 4 && MT * V <= 10 && MT * V % 2 == 0, "an 8 to 20 KiB X stage");
     constexpr int BM = 16 * MT;   // tokens per tile
     constexpr int JT = 3;         // column tiles per wavefront
-    __shared__ __attribute__((aligned(16))) GemmSmem5 sm;
+    constexpr int XS = MT * V * 16 * BK5 * 2;  // one X stage: V images of BM rows x 64 columns
+    constexpr int XP = MT * V / 2;              // its 1 KiB pieces per wavefront of a K half
+    // (one layout, sized for the larger stage, for every instantiation: an
+    // array bound or a __shared__ variable's type that depends on MT and V
+    // here drops the kernel's host-side stub)
+    __shared__ __attribute__((aligned(16))) GemmSmem5<kXStageMax5> sm;
+    static_assert(XS <= kXStageMax5 && XP <= 5, "X stage");
+    // the K half 1 sums overlay xs and wb
+    static_assert(4 * MT * JT * 64 * 16 <= 2 * 2 * kXStageMax5 + 2 * 2 * kWHalf5, "reduction area");
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -914,15 +924,15 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     // Loads go straight from global memory into LDS (global_load_lds_dwordx4:
     // lane i of a wavefront writes the 16 bytes at the destination + 16 i),
     // issued at a stage's start and complete at its closing barrier.
-    // X: the stage's V images of BM rows x 64 columns are 16 pieces of 8
+    // X: the stage's V images of BM rows x 64 columns are 4 XP pieces of 8
     // rows (piece p: image p / (2 MT), rows 8 (p % (2 MT)) ..); wavefront rq
     // of the K half copies pieces rq + 4 i. Lane l of a piece fills LDS
     // chunk l & 7 of row l >> 3 with global chunk (l & 7) ^ (row & 7), the
     // swizzle the A reads undo. (Byte offsets from xh: the images are under
     // 4 GiB, as the launch checks.)
-    uint32_t xsrc[4];
+    uint32_t xsrc[5];  // XP of them
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XP; ++i) {
         const int p = rq + 4 * i, v = p / (2 * MT);
         const int r = 8 * (p % (2 * MT)) + (int)(lane >> 3);
         const int mr = min(m0 + r, g.M - 1);
@@ -937,7 +947,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
         const uint32_t kc = (uint32_t)(blk_of(sc >> 2) * kQK + (sc & 3) * BK5) * 2u;
         uint8_t* dst = sm.xs[kh][s & 1];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < XP; ++i)
             __builtin_amdgcn_global_load_lds(xbase + (xsrc[i] + kc), dst + (rq + 4 * i) * 1024, 16, 0, 0);
     };
     // W half block hb (block hb >> 1, units 3 (hb & 1) .. +2 of the three row
@@ -1068,7 +1078,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
             const int s = 4 * c + U;
             load_x(s + 1);
             if constexpr ((U & 1) == 0) load_w((s >> 1) + 1);
-            const uint8_t* xa = arow + (s & 1) * kXStage5;
+            const uint8_t* xa = arow + (s & 1) * kXStageMax5;  // the buffers' stride
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 if (t == 0) {
@@ -1124,7 +1134,7 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
     // split's partial as write-through stores (cache policy sc1, agent
     // scope) for the split-K sum.
     constexpr int kTStride = BN5 + 4;
-    static_assert(BM * kTStride * 4 <= 2 * 2 * kXStage5 + 2 * 2 * kWHalf5, "output tile area");
+    static_assert(BM * kTStride * 4 <= 2 * 2 * kXStageMax5 + 2 * 2 * kWHalf5, "output tile area");
     float* tile = reinterpret_cast<float*>(&sm.xs[0][0][0]);
     __syncthreads();  // the K half 1 sums are read
     if (kh == 0) {
@@ -1739,20 +1749,27 @@ hipError_t launch_mlp_gemm(const uint8_t* w_gate, const uint8_t* w_up, const uin
 // Grouped GEMM over routed-expert buckets (the prefill-sized moe_batch,
 // model_batch.cpp:224-262: one matmul_quant per expert over its g tokens).
 
+// Tokens per tile of the grouped GEMMs (fp32 X, two images): 16 * mt for
+// mt = 2..5, chosen from the mean bucket (grp_tile_mt). Every tile decodes
+// its W rows once, so the count of tiles sets the decode work and their
+// padding the MFMA work: a 512-token chunk at top-8 of 64 experts (buckets
+// of 48-82 slots) makes 95 tiles of 64 for 4096 slots, 65 of 80.
+constexpr int kGrpMinTile = 32;
+
 namespace {
 // The expert tile table: for every expert e with tokens, one entry
-// e << 16 | mt per 64-token tile mt of its bucket eptr[e] .. eptr[e + 1];
+// e << 16 | mt per bm-token tile mt of its bucket eptr[e] .. eptr[e + 1];
 // count[0] = the number of entries (at most cap). One workgroup, one thread
 // per expert; bucket sizes are clamped to [0, S], so the table stays in
 // bounds whatever eptr holds.
-__global__ __launch_bounds__(1024) void k_grp_tiles(const int* __restrict__ eptr, int E, int S, int* __restrict__ tiles,
-                                                    int* __restrict__ count, int cap) {
+__global__ __launch_bounds__(1024) void k_grp_tiles(const int* __restrict__ eptr, int E, int S, int bm,
+                                                    int* __restrict__ tiles, int* __restrict__ count, int cap) {
     __shared__ int sc[1024];
     const int e = threadIdx.x;
     int n = 0;
     if (e < E) {
         const int g = min(max(eptr[e + 1] - eptr[e], 0), S);
-        n = (g + 63) / 64;
+        n = (g + bm - 1) / bm;
     }
     sc[e] = n;
     __syncthreads();
@@ -1768,17 +1785,26 @@ __global__ __launch_bounds__(1024) void k_grp_tiles(const int* __restrict__ eptr
 }
 }  // namespace
 
-int grp_tiles_cap(int S, int E) { return S / 64 + E; }
+int grp_tiles_cap(int S, int E, int mt) { return S / (16 * (mt > 0 ? mt : kGrpMinTile / 16)) + E; }
 
-hipError_t launch_grp_tiles(const int* eptr, int E, int S, int* tiles, int* count, hipStream_t s) {
-    if (E < 1 || E > 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_grp_tiles, dim3(1), dim3(1024), 0, s, eptr, E, S, tiles, count, grp_tiles_cap(S, E));
+int grp_tile_mt(int S, int E) {
+    // the mean bucket plus two of its Poisson deviations, in 16-token tiles
+    const double avg = (double)S / (E > 0 ? E : 1);
+    const int mt = (int)std::ceil((avg + 2.0 * std::sqrt(avg)) / 16.0);
+    return std::min(std::max(mt, kGrpMinTile / 16), 5);
+}
+
+hipError_t launch_grp_tiles(const int* eptr, int E, int S, int mt, int* tiles, int* count, hipStream_t s) {
+    if (E < 1 || E > 1024 || mt < kGrpMinTile / 16 || mt > 5) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_grp_tiles, dim3(1), dim3(1024), 0, s, eptr, E, S, 16 * mt, tiles, count,
+                       grp_tiles_cap(S, E, mt));
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, int in_dim, int E, const int* eptr,
                                int S, const _Float16* xh, const float* uns, float* ya, float* yb, const int* tiles,
-                               const int* count, uint32_t* err, hipStream_t s, const int* tok, int img_rows) {
+                               const int* count, uint32_t* err, hipStream_t s, int mt, const int* tok,
+                               int img_rows) {
     if (rows <= 0 || rows % kTileRows || S <= 0 || (tok && img_rows <= 0)) return hipErrorInvalidValue;
     // image offsets are 32-bit (two fp16 images of S, or img_rows, rows)
     if ((size_t)2 * (tok ? img_rows : S) * in_dim * 2 >= (1ull << 32)) return hipErrorInvalidValue;
@@ -1809,9 +1835,16 @@ hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, i
     a.grp_w_stride = stride;
     a.grp_tok = tok;
     a.grp_img_rows = tok ? img_rows : S;
-    const int cap = grp_tiles_cap(S, E);
+    if (mt < kGrpMinTile / 16 || mt > 5) return hipErrorInvalidValue;
+    const int cap = grp_tiles_cap(S, E, mt);
     a.tiles_m = cap;
-    return launch_timed(kProfGemm, k_gemm5<4, 2>, dim3(cap * a.tiles_n), dim3(kThreads5), 0, s, a);
+    const dim3 grid(cap * a.tiles_n), block(kThreads5);
+    switch (mt) {
+        case 2: return launch_timed(kProfGemm, k_gemm5<2, 2>, grid, block, 0, s, a);
+        case 3: return launch_timed(kProfGemm, k_gemm5<3, 2>, grid, block, 0, s, a);
+        case 4: return launch_timed(kProfGemm, k_gemm5<4, 2>, grid, block, 0, s, a);
+        default: return launch_timed(kProfGemm, k_gemm5<5, 2>, grid, block, 0, s, a);
+    }
 }
 
 hipError_t launch_prep_x_rows(int M, int K, hipStream_t s, const float* X, const float* U, float lim, _Float16* xh,

@@ -187,14 +187,16 @@ hipError_t launch_mlp_gemm(const uint8_t* w_gate, const uint8_t* w_up, const uin
 // and lo, unscales uns[S]) times rows e * rows .. of wa (and wb, the second
 // tensor on the same X; null for one), into rows eptr[e] .. of ya / yb
 // ([S][rows]). tiles / count: the expert tile table launch_grp_tiles makes
-// from eptr (grp_tiles_cap(S, E) entries). rows a multiple of 64. tok (may
-// be null): the images hold img_rows rows (one per token) and slot p reads
-// row tok[p].
-int grp_tiles_cap(int S, int E);
-hipError_t launch_grp_tiles(const int* eptr, int E, int S, int* tiles, int* count, hipStream_t s);
+// from eptr (grp_tiles_cap(S, E, mt) entries) for tiles of 16 mt tokens
+// (mt = 2..5; grp_tile_mt picks it from the mean bucket; a cap for mt 0
+// holds any). rows a multiple of 64. tok (may be null): the images hold
+// img_rows rows (one per token) and slot p reads row tok[p].
+int grp_tiles_cap(int S, int E, int mt);
+int grp_tile_mt(int S, int E);
+hipError_t launch_grp_tiles(const int* eptr, int E, int S, int mt, int* tiles, int* count, hipStream_t s);
 hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, int in_dim, int E, const int* eptr,
                                int S, const _Float16* xh, const float* uns, float* ya, float* yb, const int* tiles,
-                               const int* count, uint32_t* err, hipStream_t s, const int* tok = nullptr,
+                               const int* count, uint32_t* err, hipStream_t s, int mt, const int* tok = nullptr,
                                int img_rows = 0);
 // fp32 rows -> the GEMM's hi and lo images (unscale per row): X rows
 // gather[m] (gather null: row m), or SwiGLU(X, U) with clamp lim when U is

@@ -940,7 +940,7 @@ MoeLayout moe_gemm_layout(int T, int E, int K, int H, int I, int T_sh, int num_c
     size_t off = L.total;
     L.xg = off; off += align256(2 * (size_t)T * H * 2);
     L.xg_uns = off; off += align256((size_t)T * 4);
-    L.gtiles = off; off += align256(4 * (size_t)grp_tiles_cap((int)S, E));
+    L.gtiles = off; off += align256(4 * (size_t)grp_tiles_cap((int)S, E, 0));
     L.gcount = off; off += 256;
     L.hg = off; off += align256(2 * S * I * 2);
     L.hg_uns = off; off += align256(S * 4);
@@ -1115,13 +1115,15 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
         // X's images once per token; the gate/up GEMM reads a slot's row
         // through its token
         e = launch_prep_x_rows(T, H, s, X, nullptr, 0.0f, xg, xg_uns, nullptr);
-        if (e == hipSuccess) e = launch_grp_tiles(eptr, E, N, gtiles, gcount, s);
+        const int mt = grp_tile_mt(N, E);
+        if (e == hipSuccess) e = launch_grp_tiles(eptr, E, N, mt, gtiles, gcount, s);
         if (e == hipSuccess)
-            e = launch_gemm_grouped(w_gate, w_up, I, H, E, eptr, N, xg, xg_uns, G, U, gtiles, gcount, err, s, tok, T);
+            e = launch_gemm_grouped(w_gate, w_up, I, H, E, eptr, N, xg, xg_uns, G, U, gtiles, gcount, err, s, mt, tok,
+                                    T);
         if (e == hipSuccess) e = launch_prep_x_rows(N, I, s, G, U, lim, hg, hg_uns, nullptr);
         if (e == hipSuccess)
             e = launch_gemm_grouped(w_down, nullptr, H, I, E, eptr, N, hg, hg_uns, D, nullptr, gtiles, gcount, err,
-                                    s);
+                                    s, mt);
         if (e == hipSuccess && T_sh) {
             float* Gs = G + (size_t)N * I;
             float* Us = U + (size_t)N * I;
