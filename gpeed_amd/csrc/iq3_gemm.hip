@@ -243,6 +243,12 @@ struct GemmArgs {
     unsigned long long grp_w_stride;
     const int* grp_tok;
     int grp_img_rows;
+    // grp_sh_e >= 0: table entries of that expert id are the shared expert
+    // (grp_sh_rows slots from grp_eptr[grp_sh_e], its tensors grp_w_sh /
+    // grp_w2_sh); with grp_tok its slot m reads image row m (token m)
+    int grp_sh_e, grp_sh_rows;
+    const uint8_t* grp_w_sh;
+    const uint8_t* grp_w2_sh;
     GemmProb p2;
 };
 
@@ -896,15 +902,25 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
         tl.b0 = 0;
         tl.b1 = g_all.nb;
         g = gemm_tensor(g_all, tl, tn);
+        const bool sh = e == g_all.grp_sh_e;
         xrow0 = min(max(g_all.grp_eptr[e], 0), g_all.grp_rows);
         xplane = g_all.grp_rows;
-        g.M = min(g_all.grp_eptr[e + 1], g_all.grp_rows) - xrow0;
+        g.M = (sh ? min(xrow0 + g_all.grp_sh_rows, g_all.grp_rows) : min(g_all.grp_eptr[e + 1], g_all.grp_rows)) -
+              xrow0;
         if (g.M <= tl.tm * BM) return;  // uniform: no rows of this tile
-        g.w += (size_t)e * g_all.grp_w_stride;
+        if (sh)
+            g.w = tl.tn >= g_all.tiles_n1 ? g_all.grp_w2_sh : g_all.grp_w_sh;
+        else
+            g.w += (size_t)e * g_all.grp_w_stride;
         g.y += (size_t)xrow0 * g.N;
         if (g_all.grp_tok) {
-            tokmap = g_all.grp_tok + xrow0;
             xplane = g_all.grp_img_rows;
+            if (sh) {
+                g.M = min(g.M, xplane);
+                xrow0 = 0;  // the shared expert's slot m is token m
+            } else {
+                tokmap = g_all.grp_tok + xrow0;
+            }
         } else {
             g.unscale += xrow0;
         }
@@ -1758,11 +1774,12 @@ constexpr int kGrpMinTile = 32;
 
 namespace {
 // The expert tile table: for every expert e with tokens, one entry
-// e << 16 | mt per bm-token tile mt of its bucket eptr[e] .. eptr[e + 1];
-// count[0] = the number of entries (at most cap). One workgroup, one thread
-// per expert; bucket sizes are clamped to [0, S], so the table stays in
-// bounds whatever eptr holds.
-__global__ __launch_bounds__(1024) void k_grp_tiles(const int* __restrict__ eptr, int E, int S, int bm,
+// e << 16 | mt per bm-token tile mt of its bucket eptr[e] .. eptr[e + 1],
+// then (sh_rows > 0) E << 16 | mt per tile of the shared expert's sh_rows
+// slots; count[0] = the number of entries (at most cap). One workgroup, one
+// thread per expert; bucket sizes are clamped to [0, S], so the table stays
+// in bounds whatever eptr holds.
+__global__ __launch_bounds__(1024) void k_grp_tiles(const int* __restrict__ eptr, int E, int S, int bm, int sh_rows,
                                                     int* __restrict__ tiles, int* __restrict__ count, int cap) {
     __shared__ int sc[1024];
     const int e = threadIdx.x;
@@ -1781,7 +1798,11 @@ __global__ __launch_bounds__(1024) void k_grp_tiles(const int* __restrict__ eptr
     }
     const int start = sc[e] - n;
     for (int i = 0; i < n && start + i < cap; ++i) tiles[start + i] = (e << 16) | i;
-    if (e == 1023) count[0] = min(sc[1023], cap);
+    // then the shared expert's tiles (id E) after the routed ones
+    const int total = sc[1023];
+    const int n_sh = sh_rows > 0 ? (min(sh_rows, S) + bm - 1) / bm : 0;
+    for (int i = e; i < n_sh && total + i < cap; i += 1024) tiles[total + i] = (E << 16) | i;
+    if (e == 1023) count[0] = min(total + n_sh, cap);
 }
 }  // namespace
 
@@ -1794,17 +1815,18 @@ int grp_tile_mt(int S, int E) {
     return std::min(std::max(mt, kGrpMinTile / 16), 5);
 }
 
-hipError_t launch_grp_tiles(const int* eptr, int E, int S, int mt, int* tiles, int* count, hipStream_t s) {
+hipError_t launch_grp_tiles(const int* eptr, int E, int S, int mt, int* tiles, int* count, hipStream_t s,
+                            int sh_rows) {
     if (E < 1 || E > 1024 || mt < kGrpMinTile / 16 || mt > 5) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_grp_tiles, dim3(1), dim3(1024), 0, s, eptr, E, S, 16 * mt, tiles, count,
-                       grp_tiles_cap(S, E, mt));
+    hipLaunchKernelGGL(k_grp_tiles, dim3(1), dim3(1024), 0, s, eptr, E, S + sh_rows, 16 * mt, sh_rows, tiles, count,
+                       grp_tiles_cap(S + sh_rows, E + (sh_rows > 0 ? 1 : 0), mt));
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, int in_dim, int E, const int* eptr,
                                int S, const _Float16* xh, const float* uns, float* ya, float* yb, const int* tiles,
                                const int* count, uint32_t* err, hipStream_t s, int mt, const int* tok,
-                               int img_rows) {
+                               int img_rows, const uint8_t* wa_sh, const uint8_t* wb_sh, int sh_rows) {
     if (rows <= 0 || rows % kTileRows || S <= 0 || (tok && img_rows <= 0)) return hipErrorInvalidValue;
     // image offsets are 32-bit (two fp16 images of S, or img_rows, rows)
     if ((size_t)2 * (tok ? img_rows : S) * in_dim * 2 >= (1ull << 32)) return hipErrorInvalidValue;
@@ -1835,8 +1857,14 @@ hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, i
     a.grp_w_stride = stride;
     a.grp_tok = tok;
     a.grp_img_rows = tok ? img_rows : S;
-    if (mt < kGrpMinTile / 16 || mt > 5) return hipErrorInvalidValue;
-    const int cap = grp_tiles_cap(S, E, mt);
+    // the shared expert's slots are the last sh_rows of the S
+    a.grp_sh_e = sh_rows > 0 ? E : -1;
+    a.grp_sh_rows = sh_rows;
+    a.grp_w_sh = wa_sh;
+    a.grp_w2_sh = wb_sh ? wb_sh : wa_sh;
+    if (mt < kGrpMinTile / 16 || mt > 5 || (sh_rows > 0 && (!wa_sh || (wb && !wb_sh) || sh_rows > S)))
+        return hipErrorInvalidValue;
+    const int cap = grp_tiles_cap(S, E + (sh_rows > 0 ? 1 : 0), mt);
     a.tiles_m = cap;
     const dim3 grid(cap * a.tiles_n), block(kThreads5);
     switch (mt) {

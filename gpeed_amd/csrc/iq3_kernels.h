@@ -190,14 +190,19 @@ hipError_t launch_mlp_gemm(const uint8_t* w_gate, const uint8_t* w_up, const uin
 // from eptr (grp_tiles_cap(S, E, mt) entries) for tiles of 16 mt tokens
 // (mt = 2..5; grp_tile_mt picks it from the mean bucket; a cap for mt 0
 // holds any). rows a multiple of 64. tok (may be null): the images hold
-// img_rows rows (one per token) and slot p reads row tok[p].
+// img_rows rows (one per token) and slot p reads row tok[p]. sh_rows > 0:
+// the last sh_rows of the S slots are the shared expert's (tensors wa_sh,
+// wb_sh; one table entry id E per tile of them, from launch_grp_tiles with
+// the same sh_rows and S less them); with tok its slot m reads row m.
 int grp_tiles_cap(int S, int E, int mt);
 int grp_tile_mt(int S, int E);
-hipError_t launch_grp_tiles(const int* eptr, int E, int S, int mt, int* tiles, int* count, hipStream_t s);
+hipError_t launch_grp_tiles(const int* eptr, int E, int S, int mt, int* tiles, int* count, hipStream_t s,
+                            int sh_rows = 0);
 hipError_t launch_gemm_grouped(const uint8_t* wa, const uint8_t* wb, int rows, int in_dim, int E, const int* eptr,
                                int S, const _Float16* xh, const float* uns, float* ya, float* yb, const int* tiles,
                                const int* count, uint32_t* err, hipStream_t s, int mt, const int* tok = nullptr,
-                               int img_rows = 0);
+                               int img_rows = 0, const uint8_t* wa_sh = nullptr, const uint8_t* wb_sh = nullptr,
+                               int sh_rows = 0);
 // fp32 rows -> the GEMM's hi and lo images (unscale per row): X rows
 // gather[m] (gather null: row m), or SwiGLU(X, U) with clamp lim when U is
 // given.

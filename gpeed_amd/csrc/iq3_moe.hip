@@ -930,6 +930,17 @@ MoeLayout moe_layout(int T, int E, int K, int H, int I, int T_sh = 0, bool fused
     return L;
 }
 
+// The grouped-GEMM form runs the shared expert's T_sh tokens as one more
+// bucket of its grouped launches where its gate/up GEMM alone (fp32 X,
+// 64-token tiles, 256-row tiles of gate and up) would not give every CU a
+// tile of the 32x32 form: merged, its tiles fill the grouped launches' last
+// round (256 tokens 717 -> 682 us, 128 tokens 569 -> 511 us on one box);
+// at 1024 tokens the separate 32x32 GEMMs win (1883 against 1971 us).
+bool moe_merge_shared(int T_sh, int I, int num_cus) {
+    const long long tiles = (long long)((T_sh + 63) / 64) * 2 * ((I + 255) / 256);
+    return T_sh > 0 && tiles < (num_cus > 0 ? num_cus : 256);
+}
+
 // The grouped-GEMM form of the whole step: the layout above (its segment
 // images unused) and, after it, the per-token X images, the expert tile
 // table, the slot-ordered SwiGLU images and the shared expert's GEMM
@@ -940,11 +951,13 @@ MoeLayout moe_gemm_layout(int T, int E, int K, int H, int I, int T_sh, int num_c
     size_t off = L.total;
     L.xg = off; off += align256(2 * (size_t)T * H * 2);
     L.xg_uns = off; off += align256((size_t)T * 4);
-    L.gtiles = off; off += align256(4 * (size_t)grp_tiles_cap((int)S, E, 0));
+    const bool merge = moe_merge_shared(T_sh, I, num_cus);
+    const size_t NS = S + (size_t)(merge ? T_sh : 0);
+    L.gtiles = off; off += align256(4 * (size_t)grp_tiles_cap((int)NS, E + 1, 0));
     L.gcount = off; off += 256;
-    L.hg = off; off += align256(2 * S * I * 2);
-    L.hg_uns = off; off += align256(S * 4);
-    if (T_sh) {
+    L.hg = off; off += align256(2 * NS * I * 2);
+    L.hg_uns = off; off += align256(NS * 4);
+    if (T_sh && !merge) {
         L.sh1 = off; off += align256(gemm2_ws_bytes(T_sh, I, I, H, 0, num_cus));
         L.sh2 = off; off += align256(gemm_ws_bytes(T_sh, H, I, 0, num_cus));
     }
@@ -1115,16 +1128,21 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
         // X's images once per token; the gate/up GEMM reads a slot's row
         // through its token
         e = launch_prep_x_rows(T, H, s, X, nullptr, 0.0f, xg, xg_uns, nullptr);
+        // the shared expert joins the grouped launches as one more bucket
+        // (expert id E, slots N .. N + T_sh - 1, its own tensors), unless
+        // its gate/up GEMM alone fills the CUs with 32x32 tiles
+        const int T_m = moe_merge_shared(T_sh, I, num_cus) ? T_sh : 0;
+        const int NM = N + T_m;
         const int mt = grp_tile_mt(N, E);
-        if (e == hipSuccess) e = launch_grp_tiles(eptr, E, N, mt, gtiles, gcount, s);
+        if (e == hipSuccess) e = launch_grp_tiles(eptr, E, N, mt, gtiles, gcount, s, T_m);
         if (e == hipSuccess)
-            e = launch_gemm_grouped(w_gate, w_up, I, H, E, eptr, N, xg, xg_uns, G, U, gtiles, gcount, err, s, mt, tok,
-                                    T);
-        if (e == hipSuccess) e = launch_prep_x_rows(N, I, s, G, U, lim, hg, hg_uns, nullptr);
+            e = launch_gemm_grouped(w_gate, w_up, I, H, E, eptr, NM, xg, xg_uns, G, U, gtiles, gcount, err, s, mt, tok,
+                                    T, w_gate_sh, w_up_sh, T_m);
+        if (e == hipSuccess) e = launch_prep_x_rows(NM, I, s, G, U, lim, hg, hg_uns, nullptr);
         if (e == hipSuccess)
-            e = launch_gemm_grouped(w_down, nullptr, H, I, E, eptr, N, hg, hg_uns, D, nullptr, gtiles, gcount, err,
-                                    s, mt);
-        if (e == hipSuccess && T_sh) {
+            e = launch_gemm_grouped(w_down, nullptr, H, I, E, eptr, NM, hg, hg_uns, D, nullptr, gtiles, gcount, err,
+                                    s, mt, nullptr, 0, w_down_sh, nullptr, T_m);
+        if (e == hipSuccess && T_sh && !T_m) {
             float* Gs = G + (size_t)N * I;
             float* Us = U + (size_t)N * I;
             e = launch_gemm2(w_gate_sh, 0, I, w_up_sh, 0, I, H, X, 0, T, Gs, Us, ws + L.sh1, err, num_cus, s);
