@@ -349,12 +349,15 @@ def moe_prefill(torch, G, synth, dev, tens, sh, reps):
     for _ in range(reps):
         step()
     torch.cuda.synchronize()
-    d = G.prof_read(G.PROF_GEMM).astype(np.float64) * 1e3  # per step: grouped gate/up, grouped down, shared x 2
-    names = ["grouped_gate_up_us", "grouped_down_us", "shared_gate_up_us", "shared_down_us"]
-    kern = {n: round(float(d[i::4].mean()), 2) for i, n in enumerate(names)}
+    # per step: the grouped gate/up and down GEMMs (the shared expert among
+    # their buckets), or those and the shared expert's two GEMMs
+    d = G.prof_read(G.PROF_GEMM).astype(np.float64) * 1e3
+    per = max(1, int(round(len(d) / reps)))
+    names = ["grouped_gate_up_us", "grouped_down_us", "shared_gate_up_us", "shared_down_us"][:per]
+    kern = {n: round(float(d[i::per].mean()), 2) for i, n in enumerate(names)}
     return {"workload": "routed-expert prefill chunk: 512 tokens, 64 experts x (gate/up 2048x6144 + down "
                         "6144x2048) IQ3_XXS, softmax top-8, shared expert of the same shape; fp32 X; the experts' "
-                        "buckets as grouped MFMA GEMMs (k_gemm5, 64-token tiles of hi + lo images)",
+                        "buckets as grouped MFMA GEMMs (k_gemm5, 32-80-token tiles of hi + lo images, the shared expert as one more bucket)",
             "entry": "gpeed_iq3xxs_moe_batch", "touched_experts": touched,
             "packed_bytes_read_once": packed, "gflop_per_step": round(flops / 1e9, 2),
             "ms_per_step": round(ms, 4), "GBps": round(packed / (ms * 1e-3) / 1e9, 1),
