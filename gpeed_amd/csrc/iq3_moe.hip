@@ -616,12 +616,26 @@ __global__ __launch_bounds__(1024) void k_moe_front(const float* __restrict__ lo
         token_images(X, T, nb, timg, tus, ((int)blockIdx.x - G) * 16 + wave, ((int)gridDim.x - G) * 16, lane);
         return;
     }
+    uint32_t* ticket = pl.ctr + 2;
+    const int N = T * K;
+    if (kLds && G == 1) {  // uniform
+        // one ranking workgroup: the assignments and their counts go
+        // straight to LDS, and no other workgroup has to see them
+        for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+        __syncthreads();
+        topk_loop<J>(logits, T, E, K, mode, bias, routed_scale, norm_topk, sel, lds_e, lds_w, cnt, rank_score, wave,
+                     16, wave, lane);
+        __syncthreads();
+        bucket_body(T, E, K, eptr, tok, wt, lds_e, lds_w, cnt, cursor, chunk_e, l_eptr, l_tok);
+        __syncthreads();
+        plan_body(l_eptr, l_tok, T, E, K, T_sh, pl, l_pos, plan_segs != 0);
+        return;
+    }
     topk_loop<J>(logits, T, E, K, mode, bias, routed_scale, norm_topk, sel, asg_e, asg_w, nullptr, rank_score,
                  wave * G + blockIdx.x, G * 16, wave, lane);
     // every wavefront's stores, then one ticket per workgroup
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
-    uint32_t* ticket = pl.ctr + 2;
     if (tid == 0) {
         const uint32_t old = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old >= (uint32_t)G) __hip_atomic_fetch_or(pl.err, kWsTicket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -632,7 +646,6 @@ __global__ __launch_bounds__(1024) void k_moe_front(const float* __restrict__ lo
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     for (int e = tid; e < E; e += 1024) cnt[e] = 0;
     __syncthreads();
-    const int N = T * K;
     for (int a = tid; a < N; a += 1024) {
         const int e = asg_e[a];
         if constexpr (kLds) {
@@ -1094,7 +1107,9 @@ hipError_t launch_moe_batch(const float* logits, int T, int E, int K, int mode, 
     // ranking workgroups: one token per wavefront up to 64 of them; image
     // workgroups: one (token, block) item per wavefront up to 192
     // (the grouped-GEMM form gathers its own images: no image workgroups)
-    const int n_rank = std::min((T + 15) / 16, 64);
+    // (up to 32 tokens: one ranking workgroup, two tokens per wavefront,
+    // whose assignments stay in its LDS)
+    const int n_rank = T <= 32 ? 1 : std::min((T + 15) / 16, 64);
     const int groups = n_rank + (gemm ? 0 : std::min((T * nbH + 15) / 16, 192));
     // (the grouped-GEMM form runs the shared expert as GEMMs of its own, so
     // its plan holds the routed segments only)
