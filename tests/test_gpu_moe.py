@@ -236,15 +236,20 @@ def test_moe_batch_errors(gpu):
 @pytest.mark.parametrize("T,E,K,H,I,mode,shared", [
     (128, 16, 4, 1024, 512, 0, True),    # 32 tokens per expert on average: grouped GEMMs
     (72, 64, 8, 512, 256, 1, True),      # 9 per expert: the crossover
-    (200, 8, 2, 768, 1280, 1, False),    # no shared expert; 50 per expert, partial 64-token tiles
+    (200, 8, 2, 768, 1280, 1, False),    # no shared expert; 50 per expert, partial 80-token tiles
     (300, 32, 6, 512, 512, 0, True),     # buckets of many tiles
+    # 40 per expert: 64-token tiles; the shared expert's gate/up (5 x 2 x 32
+    # tiles of the 32x32 form) fills the CUs, so it runs as GEMMs of its own
+    (320, 16, 2, 512, 8192, 1, True),
 ])
 def test_moe_batch_prefill_matches_oracle(gpu, T, E, K, H, I, mode, shared):
     """moe_batch at prefill chunk sizes (model_batch.cpp:165-281 called with
     n = the chunk, :391): from an average of 9 tokens per expert every
     expert's gate/up and down run as grouped MFMA GEMMs over its bucket
-    (row0 = e*I, e*H) and the shared expert as GEMMs over all tokens; the
-    router integers stay bit-exact and the outputs match the oracle."""
+    (row0 = e*I, e*H; tiles of 32 to 80 tokens from the mean bucket), the
+    shared expert as one more bucket of those launches or as GEMMs of its
+    own; the router integers stay bit-exact and the outputs match the
+    oracle."""
     assert G.lib().gpeed_iq3xxs_moe_batch_ws_bytes(T, E, K, H, I, int(shared)) > 0
     Y, ref, _ = batch_case(gpu, 85, T, E, K, H, I, mode, shared)
     e = max(rel_err(Y[t], ref[t]) for t in range(T))
