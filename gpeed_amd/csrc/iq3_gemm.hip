@@ -1560,9 +1560,17 @@ hipError_t launch_gemm2(const uint8_t* wa, unsigned long long row0a, int out_a, 
         return hipErrorInvalidValue;
     const bool halves = gemm_halves(M, x_bf16, in_dim);
     // k_gemm6 (256-row tiles) where its tiles give every CU at least one
+    // and its rounds of workgroups over the CUs take less time than
+    // k_gemm5's: a 256-row tile of the 32x32 form takes ~1.2x a 192-row one
+    // (M = 2048 bf16: 768 tiles in 3 rounds of ~110 us, against 90 us for
+    // k_gemm5's round at M = 512), so 512 fp32 tokens (384 tiles: two
+    // rounds, the second half empty) stay on k_gemm5 (512 tiles, two full
+    // rounds)
     const int tiles6_a = (out_a + BN6 - 1) / BN6, tiles6_b = (out_b + BN6 - 1) / BN6;
-    const bool wide6 = halves && (long long)((M + gemm_tile_m(M, x_bf16) - 1) / gemm_tile_m(M, x_bf16)) *
-                                         (tiles6_a + tiles6_b) >= (num_cus > 0 ? num_cus : 256);
+    const int cus = num_cus > 0 ? num_cus : 256;
+    const long long tm = (M + gemm_tile_m(M, x_bf16) - 1) / gemm_tile_m(M, x_bf16);
+    const long long t6 = tm * (tiles6_a + tiles6_b), t5 = tm * (tiles_a + tiles_b);
+    const bool wide6 = halves && t6 >= cus && 6 * ((t6 + cus - 1) / cus) < 5 * ((t5 + cus - 1) / cus);
     const int n_eq = (tiles_a + tiles_b) * kTileN;  // both tensors' result tiles, as one width
     const int ks = wide6 ? 1 : gemm_splits(M, n_eq, in_dim, num_cus, x_bf16, kTileN);
     const GemmWs L = gemm_ws(M, n_eq, in_dim, x_bf16, ks);
