@@ -481,8 +481,8 @@ static size_t matmul_tail(int64_t in_dim, int64_t out_dim, int n_tok, int num_cu
         // with the tokens: the largest need of one tile count is at its last
         // token count, so every count's need is covered by taking the maximum
         // over the last count of each tile count below n_tok and n_tok
-        // itself. From the first tile count without split K on, no larger
-        // count splits either (more tiles), so only the images grow.
+        // itself (the split count follows rounds of workgroups over the CUs,
+        // so a larger tile count may split again).
         auto g = [&](int m) {
             return align256(gpeed::gemm_ws_bytes(m, (int)out_dim, (int)in_dim, 0, num_cus));
         };
@@ -491,7 +491,6 @@ static size_t matmul_tail(int64_t in_dim, int64_t out_dim, int n_tok, int num_cu
         for (int m = bm; m < n_tok; m += bm) {
             if (m < kMatmulGemmMinTok) continue;
             best = std::max(best, g(m));
-            if (gpeed::gemm_splits(m, (int)out_dim, (int)in_dim, num_cus, 0) == 1) break;
         }
         t = std::max(t, best);
     }

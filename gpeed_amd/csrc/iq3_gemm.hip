@@ -1506,21 +1506,32 @@ static bool gemm_halves(int M, int x_bf16, int K) {
 
 int gemm_splits(int M, int N, int K, int num_cus, int x_bf16, int tile_n) {
     const int bm = gemm_tile_m(M, x_bf16);
-    const int tiles = ((M + bm - 1) / bm) * ((N + tile_n - 1) / tile_n);
+    const long long tiles = (long long)((M + bm - 1) / bm) * ((N + tile_n - 1) / tile_n);
     const int cus = num_cus > 0 ? num_cus : 256;
-    if (2 * tiles > cus) return 1;
-    int ks = (cus + tiles - 1) / tiles;
-    ks = ks > 8 ? 8 : ks;
     const int nb = K / kQK;
-    ks = ks > nb ? nb : ks;
-    // With K halves inside the workgroup, a split of an odd block count runs
-    // as long as one of the next even count (its second half streams a
-    // clamped block of zeros): take the largest split count that gives every
-    // split an even count, which does the same work in fewer workgroups
-    // with fewer partials (kv_a + q_a at 64 tokens: 8 -> 6 splits).
-    if (gemm_halves(M, x_bf16, K) && nb % 2 == 0)
-        while (ks > 1 && nb % (2 * ks) != 0) --ks;
-    return ks;
+    // The split count with the least modelled time: rounds of workgroups
+    // over the CUs (ceil(tiles * ks / CUs)) times the blocks one split
+    // streams (with K halves inside the workgroup an odd count runs as long
+    // as the next even one) at ~3.4 us per block, plus, split, ~2 us and the
+    // partials written and read back at ~1.8 TB/s. Fitted to 12288 x 6144 and
+    // 2048 / 4096 x 6144 at 64-512 fp32 tokens; rounds matter: 88 tiles in 3
+    // splits make 264 workgroups, a second round for 8 of them (71 us), in 2
+    // one round of 176 (52 us), while 176 tiles stay unsplit (81 us; 4
+    // splits, 99 us, most of it the partials).
+    const bool halves = gemm_halves(M, x_bf16, K);
+    int best = 1;
+    double best_t = 0.0;
+    for (int ks = 1; ks <= 8 && ks <= nb; ++ks) {
+        int per = (nb + ks - 1) / ks;
+        if (halves) per += per & 1;
+        double t = (double)((tiles * ks + cus - 1) / cus) * per * 3.4;
+        if (ks > 1) t += 2.0 + (double)tiles * ks * bm * tile_n * 4 * 2 / 1.8e6;
+        if (ks == 1 || t < best_t) {
+            best = ks;
+            best_t = t;
+        }
+    }
+    return best;
 }
 
 namespace {
