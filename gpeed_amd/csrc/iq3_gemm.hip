@@ -832,6 +832,26 @@ __device__ __forceinline__ half8_t decode_group5(const uint8_t* tbl, uint32_t q,
     return __builtin_bit_cast(half8_t, r);
 }
 
+// decode_group5 in two halves, so that a software pipeline can put an LDS
+// round trip between them: the table addresses of the group's two entries
+// (from the index word q and the sign/scale word w), then the B operand from
+// the two entries read there and w's signs.
+__device__ __forceinline__ void group5_addr(uint32_t q, uint32_t w, uint32_t p0, uint32_t smask, uint32_t szero,
+                                            uint32_t& a0, uint32_t& a1) {
+    const uint32_t srow = (__builtin_amdgcn_alignbit(w, w, 17) & smask) | szero;
+    a0 = (__builtin_amdgcn_ubfe(q, 8 * p0, 8) << 3) | srow;
+    a1 = (__builtin_amdgcn_ubfe(q, 8 * p0 + 8, 8) << 3) | srow;
+}
+__device__ __forceinline__ half8_t group5_signed(u32x2_t g0, u32x2_t g1, uint32_t w, uint32_t lg) {
+    const uint32_t sw = t64_signs(w);
+    const uint32_t wg = __builtin_amdgcn_alignbit(sw, sw, lg);
+    const uint64_t sw2 = ((uint64_t)(wg >> 4) << 32) | wg;
+    const uint64_t r01 = shl64<15>(sw2), r23 = shl64<7>(sw2);
+    const u32x4_t r = {((uint32_t)r01 & 0x80008000u) | g0.x, ((uint32_t)(r01 >> 32) & 0x80008000u) | g0.y,
+                       ((uint32_t)r23 & 0x80008000u) | g1.x, ((uint32_t)(r23 >> 32) & 0x80008000u) | g1.y};
+    return __builtin_bit_cast(half8_t, r);
+}
+
 // MT token tiles of V images each (MT * V = 8: bf16 X, 128 tokens, one
 // image; fp32 X, 64 tokens, hi and lo images): the X stage, the A reads per
 // sub-block and the MFMAs per decoded B operand are the same for both.
@@ -1053,22 +1073,40 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
             dcur[j] = change ? dnext[j] : dcur[j];
         }
     };
-    // B operands of sub-block ib (0..7) of a block from W buffer `buf`
-    auto decode = [&](half8_t (&bop)[JT], int buf, int ib) {
+    // The B operands go through a three-step software pipeline, one step per
+    // sub-block, so that neither of a decode's two LDS round trips stalls the
+    // MFMAs: while sub-block i's MFMAs run, the grid entries of sub-block
+    // i + 1 arrive (their addresses were made under sub-block i - 1) and
+    // become its B operands, and the index and sign/scale words of sub-block
+    // i + 2 arrive and become its table addresses. Each sub-block first
+    // issues all of its LDS reads (A operands, entries, words), then the
+    // MFMAs and the VALU work that consumes the reads.
+    uint32_t pq[JT], pw[JT];            // words of sub-block i + 2
+    uint32_t ad0[JT], ad1[JT], aw[JT];  // entry addresses and sign/scale words of sub-block i + 1
+    // the index and sign/scale words of sub-block ib (0..7) of a block from W buffer `buf`
+    auto read_words = [&](int buf, int ib) {
         const int lib = ib & 3;  // inside the half block
         const int dq = 3 * lib + (hiq ? 1 : 0), dw = 3 * lib + 2;
         const int oq = buf * kWHalf5 + (dq >> 2) * kUnitBytes + (dq & 3) * 4;
         const int ow = buf * kWHalf5 + (dw >> 2) * kUnitBytes + (dw & 3) * 4;
 #pragma unroll
         for (int j = 0; j < JT; ++j) {
-            const uint32_t q = *reinterpret_cast<const uint32_t*>(wrow[j] + oq);
-            const uint32_t w = *reinterpret_cast<const uint32_t*>(wrow[j] + ow);
-            bop[j] = decode_group5(sm.tbl, q, w, lg, p0, amask[j], azero[j]);
+            pq[j] = *reinterpret_cast<const uint32_t*>(wrow[j] + oq);
+            pw[j] = *reinterpret_cast<const uint32_t*>(wrow[j] + ow);
+        }
+    };
+    // the words just read -> table addresses (with the masks of their block)
+    auto addresses = [&]() {
+#pragma unroll
+        for (int j = 0; j < JT; ++j) {
+            group5_addr(pq[j], pw[j], p0, amask[j], azero[j], ad0[j], ad1[j]);
+            aw[j] = pw[j];
         }
     };
 
     // prologue: X stage 0 and W half block 0 (with block 0's d) in LDS;
-    // block 0's d and the B operands of its first sub-block
+    // block 0's d, the B operands of its first sub-block and the table
+    // addresses of its second
     load_x(0);
     load_w(0);
     // the table is copied with the first stages
@@ -1078,16 +1116,25 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
 #pragma unroll
     for (int j = 0; j < JT; ++j) dcur[j] = dnext[j];  // the accumulators are zero
     half8_t bop[2][JT];
-    decode(bop[0], 0, 0);
+    read_words(0, 0);
+    addresses();
+#pragma unroll
+    for (int j = 0; j < JT; ++j) {
+        const u32x2_t g0 = *reinterpret_cast<const u32x2_t*>(sm.tbl + ad0[j]);
+        const u32x2_t g1 = *reinterpret_cast<const u32x2_t*>(sm.tbl + ad1[j]);
+        bop[0][j] = group5_signed(g0, g1, aw[j], lg);
+    }
+    read_words(0, 1);
+    addresses();
 
     // Stage s: the loads of X(s + 1) (and at a half block's first stage of
     // W(hb + 1)) into the buffers last read in stage s - 1, before its
-    // barrier; the MFMAs of its two sub-blocks; under the first, the B
-    // operands of the second are decoded, under the second those of stage
-    // s + 1's first sub-block (its W half block is in LDS already; after a
-    // block's last stage, with the next block's d). Past the last stage the
-    // same steps run on clamped blocks and their results go unused, so a
-    // stage has no branch.
+    // barrier; then its two sub-blocks, each as above. Sub-block i + 2 lies
+    // in stage s + 1, whose W half block is in LDS already; the words of a
+    // block's first two sub-blocks take the masks of that block's d (read
+    // under the previous block's seventh sub-block). Past the last stage the
+    // same steps run on clamped blocks (zero-d masks) and their results go
+    // unused, so a stage has no branch.
     for (int c = 0; c < nh; ++c) {
         static_for<0, 4>([&](auto Uc) {
             constexpr int U = decltype(Uc)::value;
@@ -1095,27 +1142,34 @@ __global__ __launch_bounds__(kThreads5) void k_gemm5(GemmArgs g_all) {
             load_x(s + 1);
             if constexpr ((U & 1) == 0) load_w((s >> 1) + 1);
             const uint8_t* xa = arow + (s & 1) * kXStageMax5;  // the buffers' stride
+            static_for<0, 2>([&](auto tc) {
+                constexpr int t = decltype(tc)::value;
+                half8_t a[MT][V];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                if (t == 0) {
-                    decode(bop[1], (s >> 1) & 1, 2 * U + 1);
-                } else {
-                    if constexpr (U == 3) block_d(c + 1);
-                    decode(bop[0], ((s + 1) >> 1) & 1, (2 * U + 2) & 7);
-                }
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    half8_t a[V];
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                     for (int v = 0; v < V; ++v)
-                        a[v] = *reinterpret_cast<const half8_t*>(xa + v * BM * 128 + mt * 16 * 128 + a_off[t]);
+                        a[mt][v] = *reinterpret_cast<const half8_t*>(xa + v * BM * 128 + mt * 16 * 128 + a_off[t]);
+                u32x2_t g0[JT], g1[JT];
+#pragma unroll
+                for (int j = 0; j < JT; ++j) {
+                    g0[j] = *reinterpret_cast<const u32x2_t*>(sm.tbl + ad0[j]);
+                    g1[j] = *reinterpret_cast<const u32x2_t*>(sm.tbl + ad1[j]);
+                }
+                read_words(((s + 1) >> 1) & 1, (2 * U + 2 + t) & 7);
+                __builtin_amdgcn_sched_barrier(0);  // every LDS read above issues before the MFMAs
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                     for (int j = 0; j < JT; ++j)
 #pragma unroll
                         for (int v = 0; v < V; ++v)
-                            acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[v], bop[t][j], acc[mt][j], 0, 0, 0);
-                }
-            }
+                            acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][v], bop[t][j], acc[mt][j], 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < JT; ++j) bop[t ^ 1][j] = group5_signed(g0[j], g1[j], aw[j], lg);
+                if constexpr (U == 3 && t == 0) block_d(c + 1);
+                addresses();
+            });
             if constexpr (U == 3) {
                 if (c + 1 < nh) rescale();
             }
