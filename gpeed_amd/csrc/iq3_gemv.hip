@@ -166,6 +166,12 @@ struct GemvArgs {
     int tiles_per_head;
     uint32_t head_stride;
     uint32_t x_bytes;
+    // EPI 1: n_zero floats at y_zero set to zero (the next launch's output)
+    float* y_zero;
+    int n_zero;
+    // EPI 0: y is zero at the launch's start; shared row tiles are added into
+    // it with atomic adds
+    int y_atomic;
 };
 
 // buffer resource word 3 for raw (untyped) buffer loads on gfx9
@@ -569,6 +575,20 @@ __device__ __forceinline__ void gemv_epilogue_y(GemvShared<NT, shared_layout<MOD
 #pragma unroll
             for (int v = 0; v < W; ++v) sum[t] += sh.red[slot][v][t][lane];
         }
+        if (first != last && g.y_atomic) {
+            // y started at zero: each part adds its sums and leaves (the
+            // order of the two to four adds varies from run to run, so the
+            // result is repeatable to within their fp32 rounding)
+            const int ten = tile >= g.n_tiles ? 1 : 0;
+            const int row = (tile - ten * g.n_tiles) * kTileRows + lane;
+            if (row < g.out_dim) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    __hip_atomic_fetch_add((ten ? g.y[1] : g.y[0]) + (size_t)t * g.out_dim + row, sum[t],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            continue;
+        }
         if (first != last) {
             uint64_t* p = g.part + ((size_t)tile * g.max_parts * NT) * 64 + lane;
 #pragma unroll
@@ -705,6 +725,13 @@ __global__ __launch_bounds__(GemvCfg<NT>::kWaves * 64) void k_gemv_t64(const uin
     Rec<(NT + 1) / 2> ring[PF];
     src.load(ring[0], 0, lane);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (EPI == 1) {
+        // this workgroup's slice of the next launch's output, behind the
+        // first record loads
+        const int per = (g_in.n_zero + (int)gridDim.x - 1) / (int)gridDim.x;
+        const int z0 = (int)blockIdx.x * per;
+        for (int i = z0 + tid; i < min(z0 + per, g_in.n_zero); i += W * 64) g_in.y_zero[i] = 0.0f;
+    }
     // the LDS set-up runs while the first loads are in flight
     gemv_lds_init<NT, MODE>(sh, wave, lane, tid);
     lds_barrier();
@@ -941,7 +968,7 @@ size_t gate_up_ws_bytes(int in_dim, int out_dim) {
 
 hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int in_dim, int out_dim,
                                  const float* x, float lim, uint8_t* act_out, uint8_t* ws, uint32_t* err,
-                                 int num_cus, hipStream_t s) {
+                                 int num_cus, hipStream_t s, float* y_zero, int n_zero) {
     if (out_dim % kQK) return hipErrorInvalidValue;  // act64 blocks of the output
     const GemvPlan plan = plan_gemv(2, in_dim, out_dim, 1, num_cus, kPlanSwigluPairs);
     if (plan.grid == 0) return hipSuccess;
@@ -951,6 +978,8 @@ hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int
     a.x2 = x;
     a.lim = lim;
     a.act_out = act_out;
+    a.y_zero = y_zero;
+    a.n_zero = y_zero ? n_zero : 0;
     return launch_gemv_nt<1, 1, 1>(plan, a, s);
 }
 
@@ -969,14 +998,20 @@ hipError_t launch_dense_mlp(const uint8_t* w_gate, const uint8_t* w_up, const ui
     uint8_t* ws_a = ws + kWsHeader;
     uint8_t* ws_b = ws_a + a256(gate_up_ws_bytes(hidden, inter));
     uint8_t* act = ws_b + a256(gemv_ws_bytes(1, inter, hidden, 1));
-    hipError_t e = launch_gate_up_swiglu(w_gate, w_up, hidden, inter, x, lim, act, ws_a, err, num_cus, s);
+    // The gate/up launch zero-fills y and the down launch adds the parts of
+    // its shared row tiles into it, unless y overlaps x (which the gate/up
+    // launch reads): then the down launch sums them in chunk order.
+    const uintptr_t xb = reinterpret_cast<uintptr_t>(x), yb = reinterpret_cast<uintptr_t>(y);
+    const bool apart = yb + (size_t)hidden * 4 <= xb || xb + (size_t)hidden * 4 <= yb;
+    hipError_t e = launch_gate_up_swiglu(w_gate, w_up, hidden, inter, x, lim, act, ws_a, err, num_cus, s,
+                                         apart ? y : nullptr, hidden);
     if (e != hipSuccess) return e;
-    return launch_gemv_act64(w_down, inter, 0, hidden, act, y, ws_b, err, num_cus, s);
+    return launch_gemv_act64(w_down, inter, 0, hidden, act, y, ws_b, err, num_cus, s, apart);
 }
 
 hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
                              const uint8_t* act64, float* y, uint8_t* ws, uint32_t* err, int num_cus,
-                             hipStream_t s) {
+                             hipStream_t s, bool y_zeroed) {
     const GemvPlan plan = plan_gemv(1, in_dim, out_dim, 1, num_cus, kPlanPrep);
     if (plan.grid == 0) return hipSuccess;
     float* yy[1] = {y};
@@ -984,6 +1019,7 @@ hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long ro
     GemvArgs a = base_args(plan, ww, yy, 1, in_dim, row0, out_dim, ws, err);
     a.act = act64;
     a.xsc = reinterpret_cast<const float*>(act64 + (size_t)a.nb * 1024);
+    a.y_atomic = y_zeroed ? 1 : 0;
     return launch_gemv_nt<1, 3>(plan, a, s);
 }
 

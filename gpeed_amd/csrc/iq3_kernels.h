@@ -103,12 +103,17 @@ hipError_t launch_gemv_heads(const uint8_t* w, int in_dim, unsigned long long ro
 // (zero-filled once, left at zero by every launch).
 size_t act64_bytes(int in_dim);
 size_t gate_up_ws_bytes(int in_dim, int out_dim);
+// y_zero (n_zero floats, may be null): zero-filled by the gate/up launch
+// for a down launch that adds into it (launch_gemv_act64 with y_zeroed).
 hipError_t launch_gate_up_swiglu(const uint8_t* w_gate, const uint8_t* w_up, int in_dim, int out_dim,
                                  const float* x, float lim, uint8_t* act_out, uint8_t* ws, uint32_t* err,
-                                 int num_cus, hipStream_t s);
+                                 int num_cus, hipStream_t s, float* y_zero = nullptr, int n_zero = 0);
+// y_zeroed: y holds zeros when the launch starts; the parts of a row tile
+// shared by several workgroups are then added into y with atomic adds (no
+// ticket, no wait) instead of being summed in chunk order by the last part.
 hipError_t launch_gemv_act64(const uint8_t* w, int in_dim, unsigned long long row0, int out_dim,
                              const uint8_t* act64, float* y, uint8_t* ws, uint32_t* err, int num_cus,
-                             hipStream_t s);
+                             hipStream_t s, bool y_zeroed = false);
 // Both (the header, the act64 buffer, then each launch's tickets and
 // partials in one workspace of dense_mlp_ws_bytes, zero-filled once).
 size_t dense_mlp_ws_bytes(int hidden, int inter);

@@ -331,8 +331,10 @@ def test_dense_mlp_fused_launches(gpu):
 def test_dense_mlp(gpu, H, I):
     """dense_mlp (model.cpp:677-690) through gpeed_iq3xxs_dense_mlp: gate and
     up in one launch, the workgroup completing 64 rows writing their SwiGLU
-    as the down projection's activation; down in a second launch. Repeated
-    calls on one workspace give identical results."""
+    as the down projection's activation; down in a second launch, whose
+    shared row tiles are added into y (zero-filled by the first launch) with
+    atomic adds. Repeated calls on one workspace agree to within the fp32
+    rounding of those two to four adds, whose order varies."""
     wg = synth.iq3xxs_matrix(66, 0, I, H)
     wu = synth.iq3xxs_matrix(66, 1, I, H)
     wd = synth.iq3xxs_matrix(66, 2, H, I)
@@ -347,7 +349,7 @@ def test_dense_mlp(gpu, H, I):
     assert e < 1e-4, e  # silu via the device expf differs by ulps from glibc's
     for _ in range(3):
         y2 = host(G.dense_mlp(tg, tu, td, H, I, xd, 10.0, ws=ws))
-        assert np.array_equal(y, y2)
+        assert rel_err(y2, y) < 1e-6
     # a second input on the same workspace (the completion counters move on)
     x2 = synth.normal(66, 10, H)
     y3 = host(G.dense_mlp(tg, tu, td, H, I, dev(x2, gpu), 10.0, ws=ws))
