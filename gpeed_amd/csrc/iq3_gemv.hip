@@ -12,7 +12,8 @@
 // wavefronts' partials in LDS. A tile cut by a chunk boundary is finished by
 // whichever of its workgroups arrives last (atomic ticket in a caller-owned
 // workspace); it adds the workgroups' partials in chunk order, so results do
-// not depend on timing.
+// not depend on timing. (The dense step's down launch instead adds such
+// parts into an output the gate/up launch zero-filled, with atomic adds.)
 //
 // Decode and product. Lane n of a wavefront holds row n of the tile. Per
 // group of 4 weights it makes one LDS lookup in its own replica of the grid
@@ -558,8 +559,9 @@ __device__ __forceinline__ uint32_t take_ticket(uint32_t* cnt, uint32_t lane, in
 // EPI 0 epilogue: wavefront w finishes the chunk's tile slots w, w + W, ...:
 // the wavefront partials summed in wave order; a whole tile goes straight
 // to y, a shared tile's part is published, and the last ticket holder adds
-// the parts in chunk order — bitwise repeatable. Call after a barrier that
-// completes sh.red.
+// the parts in chunk order — bitwise repeatable; or, with g.y_atomic, the
+// part is added into the zero-filled y. Call after a barrier that completes
+// sh.red.
 template <int NT, int MODE>
 __device__ __forceinline__ void gemv_epilogue_y(GemvShared<NT, shared_layout<MODE>()>& sh, const GemvArgs& g,
                                                 const Chunk& ch, int blk, int wave, uint32_t lane) {

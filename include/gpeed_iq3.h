@@ -360,7 +360,12 @@ int gpeed_iq3xxs_matvec_heads(const void* w_t64, uint64_t n_rows, uint64_t row0,
  * with g = W_gate x, u = W_up x. gate and up run together; the workgroup
  * that completes 64 rows of g and u writes their SwiGLU straight into the
  * down projection's prepared activation (one power-of-two scale per 64
- * values); the second launch multiplies it. gate/up are T64 copies of inter x hidden, down
+ * values); the second launch multiplies it. The first launch also zero-fills
+ * y, and the second adds the parts of its row tiles that several workgroups
+ * share into y with atomic adds, so repeated calls agree to within the fp32
+ * rounding of those two to four adds (their order varies); where y overlaps
+ * x the parts are summed in a fixed order instead (bitwise repeatable).
+ * gate/up are T64 copies of inter x hidden, down
  * of hidden x inter (rows from 0); hidden and inter multiples of 256. ws:
  * gpeed_iq3xxs_dense_mlp_ws_bytes bytes, initialised once with
  * gpeed_ws_init (every call leaves it ready for the next); one workspace per

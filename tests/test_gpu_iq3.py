@@ -353,7 +353,15 @@ def test_dense_mlp(gpu, H, I):
     # a second input on the same workspace (the completion counters move on)
     x2 = synth.normal(66, 10, H)
     y3 = host(G.dense_mlp(tg, tu, td, H, I, dev(x2, gpu), 10.0, ws=ws))
-    assert rel_err(y3, oracle.dense_mlp(wg, wu, wd, H, I, x2[None, :], 10.0)[0]) < 1e-4
+    ref2 = oracle.dense_mlp(wg, wu, wd, H, I, x2[None, :], 10.0)[0]
+    assert rel_err(y3, ref2) < 1e-4
+    # in place (y over x: the down launch finishes shared row tiles by
+    # ticket), then the atomic path again on the same workspace
+    xin = dev(x2, gpu)
+    y4 = host(G.dense_mlp(tg, tu, td, H, I, xin, 10.0, out=xin, ws=ws))
+    assert rel_err(y4, ref2) < 1e-4
+    y5 = host(G.dense_mlp(tg, tu, td, H, I, xd, 10.0, ws=ws))
+    assert rel_err(y5, y) < 1e-6
 
 
 def test_dense_mlp_errors(gpu):
