@@ -439,6 +439,42 @@ def test_graph_replay_matches_eager(gpu):
         torch.cuda.synchronize()
 
 
+def test_dense_mlp_graph_replay(gpu):
+    """dense_mlp captured in a HIP graph: the gate/up launch's zero fill of y
+    and the down launch's atomic tile sums hold on every replay (y garbage
+    before each), with eager calls on the same workspace in between."""
+    import torch
+
+    H, I = 1024, 2048
+    wg = synth.iq3xxs_matrix(67, 0, I, H)
+    wu = synth.iq3xxs_matrix(67, 1, I, H)
+    wd = synth.iq3xxs_matrix(67, 2, H, I)
+    x = synth.normal(67, 9, H)
+    tg, tu, td = (G.tile(dev(a.reshape(-1), gpu), r, c) for a, r, c in ((wg, I, H), (wu, I, H), (wd, H, I)))
+    ws = G.dense_mlp_workspace(H, I, gpu)
+    xd = dev(x, gpu)
+    y = torch.empty(H, device=gpu)
+    G.dense_mlp(tg, tu, td, H, I, xd, 10.0, out=y, ws=ws)
+    torch.cuda.synchronize()
+    want = host(y).copy()
+    assert rel_err(want, oracle.dense_mlp(wg, wu, wd, H, I, x[None, :], 10.0)[0]) < 1e-4
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            G.dense_mlp(tg, tu, td, H, I, xd, 10.0, out=y, ws=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for r in range(4):
+        y.fill_(float(r + 1) * 1e6)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert rel_err(host(y), want) < 1e-6, r
+        G.dense_mlp(tg, tu, td, H, I, xd, 10.0, ws=ws)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("n_bytes,groups", [(16, 1), (4096 * 5 + 48, 3), (1 << 20, 256), (3 * (1 << 20) + 4080, 1024)])
 def test_stream_read_covers_every_byte(gpu, n_bytes, groups):
     """Workgroup i folds (XOR of 32-bit words) exactly its share: shares are
