@@ -56,16 +56,17 @@ __device__ __forceinline__ uint32_t f16_pair_of_floats(float lo, float hi) {
 // that follows on the same stream, so a workspace needs no initialisation.
 // gather (may be null): image row m is X row gather[m] (bucket slots of
 // routed experts: the slot's token).
-template <int IN, int CPT>
-__global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X, const float* __restrict__ U,
+template <int IN, int CPT, int NTHR = 256>
+__global__ __launch_bounds__(NTHR) void k_gemm_prep_x(const void* __restrict__ X, const float* __restrict__ U,
                                                      float lim, int M, int K, _Float16* __restrict__ xh,
                                                      float* __restrict__ unscale, uint32_t* __restrict__ cnt,
                                                      int n_cnt, const int* __restrict__ gather) {
     const int m = blockIdx.x;
     const int tid = threadIdx.x;
     const int src = gather ? gather[m] : m;  // the X (and U) row of image row m
-    for (int i = m * 256 + tid; i < n_cnt; i += M * 256) cnt[i] = 0u;
-    __shared__ float red[4];
+    for (int i = m * NTHR + tid; i < n_cnt; i += M * NTHR) cnt[i] = 0u;
+    constexpr int kW = NTHR / 64;
+    __shared__ float red[kW];
     // the 8 raw values of chunk c (16-byte loads; K is a multiple of 256)
     struct Raw {
         u32x4_t a, b, ua, ub;
@@ -123,7 +124,10 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
         mx = wave_max(mx);
         if ((tid & 63) == 0) red[tid >> 6] = mx;
         __syncthreads();
-        return pow2_scale_of_max(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+        float r = red[0];
+#pragma unroll
+        for (int w = 1; w < kW; ++w) r = fmaxf(r, red[w]);
+        return pow2_scale_of_max(r);
     };
     const int n8 = K >> 3;
     float mx = 0.0f;
@@ -132,7 +136,7 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
         // leave the maximum unchanged) and their results are not stored
         Raw r[CPT];
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) load8(min(tid + 256 * j, n8 - 1), r[j]);
+        for (int j = 0; j < CPT; ++j) load8(min(tid + NTHR * j, n8 - 1), r[j]);
         float v[CPT][8];
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
@@ -143,10 +147,10 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
         const int sc = row_scale(mx);
 #pragma unroll
         for (int j = 0; j < CPT; ++j)
-            if (tid + 256 * j < n8) store8(tid + 256 * j, v[j], sc);
+            if (tid + NTHR * j < n8) store8(tid + NTHR * j, v[j], sc);
         if (tid == 0) unscale[m] = ldexpf(1.0f, -sc);
     } else {
-        for (int c = tid; c < n8; c += 256) {
+        for (int c = tid; c < n8; c += NTHR) {
             Raw r;
             float v[8];
             load8(c, r);
@@ -155,7 +159,7 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
             for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
         }
         const int sc = row_scale(mx);
-        for (int c = tid; c < n8; c += 256) {
+        for (int c = tid; c < n8; c += NTHR) {
             Raw r;
             float v[8];
             load8(c, r);
@@ -167,10 +171,27 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ X,
 }
 
 // The preparation launch for rows of K values: chunks per thread in
-// registers where the row has at most 2048 chunks.
+// registers where the row has at most 2048 chunks. Fewer rows than CUs
+// take 1024 threads a row: four wavefronts per SIMD hide more of the
+// latency of each one's loads and SwiGLU chain (the decode mix's step,
+// whose two preparations have 64 rows, 93.4 -> 92.9 us, bitwise equal).
 template <int IN>
 hipError_t launch_prep_x(int M, int K, hipStream_t s, const void* X, const float* U, float lim, _Float16* xh,
                          float* uns, uint32_t* cnt, int n_cnt, const int* gather = nullptr) {
+    if (M < 256 && K >= 8 * 1024) {
+        const int per4 = (K / 8 + 1023) / 1024;
+        const dim3 grid(M), block(1024);
+        if (per4 <= 1)
+            hipLaunchKernelGGL((k_gemm_prep_x<IN, 1, 1024>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt,
+                               gather);
+        else if (per4 <= 2)
+            hipLaunchKernelGGL((k_gemm_prep_x<IN, 2, 1024>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt,
+                               gather);
+        else
+            hipLaunchKernelGGL((k_gemm_prep_x<IN, 0, 1024>), grid, block, 0, s, X, U, lim, M, K, xh, uns, cnt, n_cnt,
+                               gather);
+        return hipGetLastError();
+    }
     const int per = (K / 8 + 255) / 256;
     const dim3 grid(M), block(256);
     if (per <= 1)
@@ -751,7 +772,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm3(GemmArgs g_all) {
 //     0 wavefronts add them (half 0 + half 1, fixed order) and lay the tile
 //     out in LDS by rows, and all threads store it with 16-byte stores.
 
-constexpr int BM5 = 128, BN5 = 192, BK5 = 64;
+constexpr int BN5 = 192, BK5 = 64;
 constexpr int kThreads5 = 512;
 constexpr int kWHalf5 = 3 * 3 * kUnitBytes;      // 9 KiB: 3 row tiles x 3 units
 constexpr int kTbl5 = 16 * 256 * 8;              // 32 KiB: the grid times every 2s+1
